@@ -1,0 +1,258 @@
+/*
+ * sparsetriton_amd -- C ABI of the MI355X (gfx950) sparse-convolution hot path.
+ *
+ * One shared library, libsparsetriton_amd.so, built with hipcc for gfx950.
+ * Every entry point takes plain device pointers, 64-bit sizes, small enums
+ * and the hipStream_t to enqueue on; nothing here allocates device memory,
+ * synchronises the stream, or depends on torch types.  Callers own every
+ * buffer (inputs, outputs, workspaces).  Return value: ST_OK (0) on success,
+ * a negative ST_ERR_* code otherwise; device-side failures (full hash table,
+ * unpackable coordinate, duplicate coordinate) are counted into a caller-owned
+ * int32 status[ST_STATUS_WORDS] buffer instead of being dropped.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   HashTable.insert / build_hash_table_kernel ... sparsetriton/utils/hash.py:193-258, 516-544
+ *   HashTable.query / query_hash_table_kernel ..... sparsetriton/utils/hash.py:261-366, 546-580
+ *   compute_neighbor_indices ...................... sparsetriton/nn/functional/conv/conv.py:12-75
+ *   _build_out_coords_normal / _transposed ......... sparsetriton/nn/functional/conv/kmap.py:213-444
+ *   ConvPrecomputedNeighborGEMM fwd/dgrad/wgrad .... .../conv/funcs/implicit_precomputed_gemm.py:64-324
+ *   ConvHashOnTheFlyImplicitGEMM fwd/dgrad/wgrad ... .../conv/funcs/implicit_hashfly_gemm.py:45-452
+ */
+#ifndef SPARSETRITON_AMD_H
+#define SPARSETRITON_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; declared here so the header needs no HIP headers. */
+typedef struct ihipStream_t* st_stream_t;
+
+/* ------------------------------------------------------------------ enums */
+
+enum st_status_code {
+  ST_OK = 0,
+  ST_ERR_ARG = -1,         /* bad size, null pointer, unsupported shape      */
+  ST_ERR_HIP = -2,         /* a HIP launch or runtime call failed            */
+  ST_ERR_UNSUPPORTED = -3, /* dtype / kernel volume outside what is built    */
+};
+
+enum st_coord_dtype { ST_COORD_I16 = 0, ST_COORD_I32 = 1, ST_COORD_I64 = 2 };
+
+enum st_dtype { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2 };
+
+/* Device status words, accumulated by atomics (caller zeroes them). */
+enum st_status_word {
+  ST_STATUS_OVERFLOW = 0,  /* inserts that found the table full               */
+  ST_STATUS_BAD_COORD = 1, /* coordinates that do not pack into a 64-bit key  */
+  ST_STATUS_DUPLICATE = 2, /* inserts whose key was already present           */
+  ST_STATUS_WORDS = 4,
+};
+
+/* Weight re-layouts produced by st_weight_prep from W (K, C_in, C_out). */
+enum st_weight_mode {
+  ST_W_TRANSPOSE = 0, /* out[k][co][ci] = W[k][ci][co]        (forward B operand)   */
+  ST_W_REVERSE = 1,   /* out[k][ci][co] = W[K-1-k][ci][co]    (submanifold dgrad)   */
+  ST_W_COPY = 2,      /* out = W                              (general dgrad)       */
+};
+
+/* Kernel volume limit of the kernel-map row masks (mask words = ceil(K/32)). */
+#define ST_MAX_KVOL 512
+
+/* ------------------------------------------------------------- utilities */
+
+/* Library version string, e.g. "sparsetriton_amd 0.1 gfx950". */
+const char* st_version(void);
+
+/* Fill n 32-bit / 64-bit words with `value` (table clears, -1 map fills). */
+int st_fill_u32(uint32_t* dst, int64_t n, uint32_t value, st_stream_t stream);
+int st_fill_u64(uint64_t* dst, int64_t n, uint64_t value, st_stream_t stream);
+
+/* -------------------------------------------------------- coordinate hash */
+
+/*
+ * Replaces HashTable.insert -> build_hash_table_kernel (utils/hash.py:193-258, 516-544).
+ * Inserts the n rows of coords (n, 4) = (b, x, y, z), x/y/z multiplied by
+ * `scale` (1 normally; the stride for the transposed-conv table that
+ * sparse_conv3d builds from coords * s, conv.py:138-142), into an
+ * open-addressing table of `capacity` slots: keys (u64, packed coordinate,
+ * all-ones = empty) and vals (u32 row index, all-ones = none).  The caller
+ * clears both arrays to all-ones first (st_fill_u64 / st_fill_u32).  Linear
+ * probing from a 64-bit-mixed home slot; the key is claimed by a 64-bit CAS,
+ * the value by an atomic min, so duplicate coordinates resolve to the lowest
+ * row index on every run.
+ */
+int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale, uint64_t* keys, uint32_t* vals,
+                   int64_t capacity, int32_t* status, st_stream_t stream);
+
+/*
+ * Replaces HashTable.query -> query_hash_table_kernel (utils/hash.py:302-366, 546-580).
+ * out[i] = row index stored for coords[i], or -1 when absent.
+ */
+int st_hash_query(const void* coords, int coord_dtype, int64_t m, const uint64_t* keys, const uint32_t* vals,
+                  int64_t capacity, int32_t* out, st_stream_t stream);
+
+/* ------------------------------------------------------------ kernel maps */
+
+/*
+ * Replaces compute_neighbor_indices (nn/functional/conv/conv.py:12-75).
+ * For every output row o and offset k:
+ *   q = out_coords[o].xyz * stride - offsets[k]            (offsets: int32 (K, 3))
+ *   nbr[k * nbr_k_stride + o * nbr_r_stride] = row of q in the table if
+ *       0 <= q < shape (per axis) and present, else -1.
+ * row_masks (n_out, ceil(K/32)) u32, optional: bit k set iff nbr[o, k] >= 0.
+ * The default layout is offset-major (nbr_k_stride = n_out, nbr_r_stride = 1).
+ */
+int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
+                  int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
+                  const uint32_t* vals, int64_t capacity, int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride,
+                  uint32_t* row_masks, st_stream_t stream);
+
+/* Geometry of a strided or transposed convolution's output-coordinate build. */
+typedef struct st_outgeom {
+  int32_t K;            /* kernel volume (offsets rows)                              */
+  int32_t transposed;   /* 0: candidates (in + t_k) / stride; 1: in * stride + t_k   */
+  int64_t stride;       /* >= 1                                                      */
+  int64_t in_shape[3];  /* input spatial shape (bounds of the neighbour lookup)      */
+  int64_t out_shape[3]; /* output spatial shape (range filter of the candidates)     */
+} st_outgeom;
+
+/*
+ * Dedup-table capacity and per-block counter length the output-coordinate
+ * build needs for n input rows.  Fills *dedup_capacity and *num_blocks.
+ */
+int st_outcoords_sizes(int64_t n, const st_outgeom* g, int64_t kernel_size, int64_t dilation,
+                       int64_t* dedup_capacity, int64_t* num_blocks);
+
+/*
+ * Replaces the candidate expansion, stride / range filter and dedup of
+ * _build_out_coords_normal / _transposed (kmap.py:213-444, expand_coords_kernel
+ * :11-54, filter_unique_kernel :56-97, mask_spatial_range utils/spatial/tile.py).
+ * Pass 1 of 2.  Candidates are enumerated input-major, offset-minor (the
+ * reference's order); every valid candidate is inserted into the dedup table
+ * (dkeys/dvals, cleared to all-ones by the caller, capacity from
+ * st_outcoords_sizes) keeping the lowest candidate index per coordinate.
+ * block_counts (num_blocks + 1 int32) receives, after an exclusive scan, the
+ * output-row offset of each block; block_counts[num_blocks] = N_out.
+ */
+int st_outcoords_plan(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                      const st_outgeom* g, uint64_t* dkeys, uint32_t* dvals, int64_t dcap, int32_t* block_counts,
+                      int64_t num_blocks, int32_t* status, st_stream_t stream);
+
+/*
+ * Pass 2 of 2, after the caller read N_out = block_counts[num_blocks].
+ * Writes out_coords (N_out, 4) in the input's coordinate dtype, ordered by
+ * first occurrence in the candidate order; slot_out (dcap u32) maps dedup
+ * slots to output rows (so dkeys + slot_out form the output-coordinate
+ * table); and the kernel map in both directions, offset-major:
+ *   nbr    (K, N_out): input row feeding output o through offset k, or -1
+ *   invnbr (K, n)    : output row fed by input i through offset k, or -1
+ * plus row masks out_masks (N_out, W) and in_masks (n, W), W = ceil(K/32).
+ * nbr/invnbr must be pre-filled with -1 and the masks with 0 by the caller.
+ * With nbr == NULL only out_coords and slot_out are written (hash-fly mode).
+ * in_keys/in_vals/in_cap (optional) is the input-coordinate table the
+ * reference's neighbour query would use (coords * stride for transposed):
+ * when given, only the row that table resolves a coordinate to enters the
+ * map, so duplicate input coordinates behave as a lookup would.
+ */
+int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                      const st_outgeom* g, const uint64_t* dkeys, const uint32_t* dvals, uint32_t* slot_out,
+                      int64_t dcap, const int32_t* block_counts, int64_t num_blocks, const uint64_t* in_keys,
+                      const uint32_t* in_vals, int64_t in_cap, void* out_coords, int64_t n_out, int32_t* nbr,
+                      int32_t* invnbr, uint32_t* out_masks, uint32_t* in_masks, st_stream_t stream);
+
+/*
+ * Transposed kernel map of an arbitrary map nbr (k, o) -> i (strides as in
+ * st_kmap_query): invnbr[k * n_in + i] = o, in_masks (n_in, W) row masks of
+ * invnbr, and, if out_masks is non-null, out_masks (n_out, W) row masks of
+ * nbr.  invnbr must be pre-filled with -1 and in_masks with 0.  Used when a
+ * caller hands ConvPrecomputedNeighborGEMM a plain (N_out, K) map
+ * (implicit_precomputed_gemm.py:237-242) and for the submanifold map, whose
+ * transposed map feeds the atomic-free input gradient.
+ */
+int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride, int64_t n_out, int K,
+                   int64_t n_in, int32_t* invnbr, uint32_t* in_masks, uint32_t* out_masks, st_stream_t stream);
+
+/* ------------------------------------------------------------- gather-GEMM */
+
+/*
+ * Re-lays W (K, C_in, C_out) for the gather-GEMM's B operand (see
+ * st_weight_mode).  Replaces nothing in the reference, which reads W in
+ * place with 2-D strides inside each Triton kernel.
+ */
+int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mode, int dtype, st_stream_t stream);
+
+/*
+ * Output-stationary gather-GEMM, the forward of ConvPrecomputedNeighborGEMM
+ * (precomputed_fwd_kernel, implicit_precomputed_gemm.py:64-126) and, with the
+ * transposed map, its input-gradient (precomputed_bwd_feat_kernel :129-177,
+ * here a gather with no atomics):
+ *   out[r, :] = sum over k of A[map(k, r), :] @ Bt[k]^T  (map < 0 or >= n_src adds 0)
+ * A (n_src, Kd), Bt (K, Nd, Kd), out (n_dst, Nd), all of `dtype`, fp32
+ * accumulation on MFMA.  map(k, r) = map[k * map_k_stride + r * map_r_stride].
+ * row_masks (n_dst, mask_words) optional: offsets a whole workgroup tile lacks
+ * are skipped.  perm (n_dst) optional: the order rows are tiled in.
+ */
+int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
+                   const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, void* out,
+                   int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
+
+/*
+ * Weight gradient of ConvPrecomputedNeighborGEMM (precomputed_bwd_weight_kernel,
+ * implicit_precomputed_gemm.py:180-230):
+ *   dW[k] = sum over o with map(k, o) >= 0 of X[map(k, o)]^T @ dY[o]
+ * Each (k, split) workgroup compacts its slice of map column k in LDS and
+ * runs MFMA over the valid pairs only; partials (K * splits * C_in * C_out
+ * fp32 workspace) are reduced in a fixed order, so dW is bit-identical run
+ * to run.  X (n_in, C_in) and dY (n_out, C_out) are `dtype` (map entries
+ * outside [0, n_in) add nothing); dW (K, C_in, C_out) is written in `dw_dtype`
+ * (e.g. fp32 master weights under bf16 activations).
+ */
+int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,
+             int64_t map_r_stride, int64_t n_out, int K, int C_in, int C_out, int dtype, float* partials,
+             int64_t splits, void* dW, int dw_dtype, st_stream_t stream);
+
+/* ----------------------------------------------------- implicit hash-fly */
+
+/* Lookup rule of the hash-fly kernels: for row r with coordinate c and offset k
+ *   q = (c.xyz * mul + sign * offsets[k]) / div    (only when divisible)
+ * looked up in the table if 0 <= q < bounds per axis. */
+typedef struct st_lookup {
+  int32_t K;
+  int32_t sign;          /* -1 forward (q = c*s - t_k), +1 input-gradient direction   */
+  int64_t mul;
+  int64_t div;
+  int64_t bounds[3];     /* q must satisfy 0 <= q < bounds                            */
+  int64_t row_bounds[3]; /* if > 0: rows with c outside [0, row_bounds) get no pairs  */
+} st_lookup;
+
+/*
+ * Forward / input-gradient of ConvHashOnTheFlyImplicitGEMM
+ * (implicit_gemm_hash_on_fly_fwd_kernel, implicit_hashfly_gemm.py:45-148, and
+ * implicit_gemm_bwd_feat_kernel :151-237 recast as a gather): the same
+ * gather-GEMM as st_gather_gemm with map(k, r) found by probing the table
+ * inside the kernel, once per row tile rather than once per C_out tile.
+ */
+int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int coord_dtype, int64_t n_dst,
+                    const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,
+                    int64_t capacity, const void* Bt, void* out, int Kd, int Nd, int dtype, st_stream_t stream);
+
+/*
+ * Weight gradient of ConvHashOnTheFlyImplicitGEMM (implicit_gemm_bwd_weight_kernel,
+ * implicit_hashfly_gemm.py:239-328): st_wgrad with the pairs found by probing.
+ * out_coords are the rows of dY; the table holds the rows of X.
+ */
+int st_hashfly_wgrad(const void* X, int64_t n_in, const void* dY, const void* out_coords, int coord_dtype,
+                     int64_t n_out,
+                     const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,
+                     int64_t capacity, int C_in, int C_out, int dtype, float* partials, int64_t splits, void* dW,
+                     int dw_dtype, st_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSETRITON_AMD_H */

@@ -1,0 +1,277 @@
+"""CPU oracle of the sparse-convolution hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg may import this module, and only as the checker or the reported CPU
+baseline; the product package never does.
+
+Layers:
+  * ``liboracle.so`` (``st_oracle.c``, gcc + OpenMP): exact kernel map by
+    sort + binary search, first-occurrence output coordinates, float64 GEMMs,
+    and a port of the reference's own lossy hash + GEMM algorithm.
+  * pure-Python brute force for tiny inputs (dict lookups, explicit loops)
+    used to pin the C functions, and dense ``torch.nn.functional.conv3d`` /
+    ``conv_transpose3d`` on the CPU in float64 as the independent library
+    routine the reference's own tests use (tests/test_sparse_conv.py:37-44).
+
+Every function cites the reference code it restates.  Parity status of each
+function (what pins it) is listed in tests/test_oracle.py.
+"""
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+SRC = HERE / "st_oracle.c"
+LIB = HERE / "_build" / "liboracle.so"
+
+_P = ctypes.c_void_p
+_L = ctypes.c_int64
+_I = ctypes.c_int
+_SIG = {
+    "or_exact_kmap": ([_P, _L, _L, _P, _L, _P, _I, _L, _L, _L, _L, _P], _I),
+    "or_out_coords": ([_P, _L, _P, _I, _L, _I, _L, _L, _L, _P], _L),
+    "or_fwd_f64": ([_P, _I, _P, _I, _I, _P, _L, _P], None),
+    "or_dgrad_f64": ([_P, _I, _P, _I, _I, _P, _L, _L, _P], None),
+    "or_wgrad_f64": ([_P, _I, _P, _I, _P, _L, _I, _P], None),
+    "ref_hash_build": ([_P, _L, _P, _P, _L], _L),
+    "ref_hash_query": ([_P, _L, _P, _P, _L, _P], None),
+    "ref_kmap": ([_P, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, _P], None),
+    "ref_fwd_f32": ([_P, _I, _P, _I, _I, _P, _L, _P], None),
+    "ref_dgrad_f32": ([_P, _I, _P, _I, _I, _P, _L, _L, _P], None),
+    "ref_wgrad_f32": ([_P, _I, _P, _I, _P, _L, _I, _P], None),
+    "or_num_threads": ([], _I),
+    "or_set_threads": ([_I], None),
+}
+_lib = None
+
+
+def build() -> Path:
+    """Compile st_oracle.c (gcc, OpenMP) into oracle/_build/liboracle.so."""
+    LIB.parent.mkdir(exist_ok=True)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = ["gcc", "-O3", "-march=x86-64-v3", "-fopenmp", "-shared", "-fPIC", str(SRC), "-o", str(tmp)]
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        h = ctypes.CDLL(str(LIB))
+        for name, (args, res) in _SIG.items():
+            f = getattr(h, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = h
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a), dtype=np.int32)
+
+
+def _f64(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a), dtype=np.float64)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a), dtype=np.float32)
+
+
+# ------------------------------------------------------------ offsets / shapes
+
+def target_offsets(kernel_size: int, dilation: int, padding: int, transposed: bool) -> np.ndarray:
+    """(k^3, 3) int32 t_k; input = out*s - t_k (kmap.py:104-180, meshgrid 'ij', x-major)."""
+    k, d, p = kernel_size, dilation, padding
+    ax = np.arange(k) - k // 2
+    gx, gy, gz = np.meshgrid(ax, ax, ax, indexing="ij")
+    base = np.stack([gx, gy, gz], axis=-1).reshape(-1, 3) * d
+    if transposed:
+        t = base - p + (k - 1) * d // 2
+    else:
+        t = -base + p - (k - 1) * d // 2
+    return t.astype(np.int32)
+
+
+def out_shape(shape, k, s, d, p, transposed):
+    """kmap.py:254-258 (normal) and :373-377 (transposed)."""
+    if transposed:
+        return tuple((v - 1) * s + (k - 1) * d - 2 * p + 1 for v in shape)
+    return tuple((v - (k - 1) * d + 2 * p - 1) // s + 1 for v in shape)
+
+
+# ------------------------------------------------------------- exact (C)
+
+def exact_kmap(in_coords, out_coords, offsets, stride, shape, in_scale=1) -> np.ndarray:
+    """(n_out, K) int32 exact neighbour map (conv.py:12-75 with an exact lookup)."""
+    ic, oc, off = _i32(in_coords), _i32(out_coords), _i32(offsets)
+    n_out, K = oc.shape[0], off.shape[0]
+    nbr = np.empty((n_out, K), dtype=np.int32)
+    lib().or_exact_kmap(_p(ic), ic.shape[0], in_scale, _p(oc), n_out, _p(off), K, stride, *map(int, shape), _p(nbr))
+    return nbr
+
+
+def out_coords(in_coords, offsets, stride, transposed, new_shape) -> np.ndarray:
+    """Output coordinates in first-occurrence order (kmap.py:213-444)."""
+    ic, off = _i32(in_coords), _i32(offsets)
+    n, K = ic.shape[0], off.shape[0]
+    buf = np.empty((max(n * K, 1), 4), dtype=np.int32)
+    m = lib().or_out_coords(_p(ic), n, _p(off), K, stride, 1 if transposed else 0, new_shape[0] - 1,
+                            new_shape[1] - 1, new_shape[2] - 1, _p(buf))
+    return buf[:m].copy()
+
+
+def fwd_f64(X, W, nbr) -> np.ndarray:
+    X, W, nbr = _f64(X), _f64(W), _i32(nbr)
+    K, Cin, Cout = W.shape
+    out = np.empty((nbr.shape[0], Cout), dtype=np.float64)
+    lib().or_fwd_f64(_p(X), Cin, _p(W), K, Cout, _p(nbr), nbr.shape[0], _p(out))
+    return out
+
+
+def dgrad_f64(dY, W, nbr, n_in) -> np.ndarray:
+    dY, W, nbr = _f64(dY), _f64(W), _i32(nbr)
+    K, Cin, Cout = W.shape
+    dX = np.empty((n_in, Cin), dtype=np.float64)
+    lib().or_dgrad_f64(_p(dY), Cout, _p(W), K, Cin, _p(nbr), nbr.shape[0], n_in, _p(dX))
+    return dX
+
+
+def wgrad_f64(X, dY, nbr, K) -> np.ndarray:
+    X, dY, nbr = _f64(X), _f64(dY), _i32(nbr)
+    Cin, Cout = X.shape[1], dY.shape[1]
+    dW = np.empty((K, Cin, Cout), dtype=np.float64)
+    lib().or_wgrad_f64(_p(X), Cin, _p(dY), Cout, _p(nbr), nbr.shape[0], K, _p(dW))
+    return dW
+
+
+# ------------------------------------------------- reference-algorithm port
+
+class RefHash:
+    """Port of the reference HashTable (utils/hash.py:116-299): 31-bit keys, 128-probe cap, T = int(1.5 N)."""
+
+    def __init__(self, coords, factor: float = 1.5):
+        c = _i32(coords)
+        self.T = max(int(c.shape[0] * factor), 1)
+        self.keys = np.empty(self.T, dtype=np.int32)
+        self.vals = np.empty(self.T, dtype=np.int32)
+        self.dropped = int(lib().ref_hash_build(_p(c), c.shape[0], _p(self.keys), _p(self.vals), self.T))
+
+    def query(self, coords) -> np.ndarray:
+        c = _i32(coords)
+        out = np.empty(c.shape[0], dtype=np.int32)
+        lib().ref_hash_query(_p(c), c.shape[0], _p(self.keys), _p(self.vals), self.T, _p(out))
+        return out
+
+    def kmap(self, out_coords, offsets, stride, shape) -> np.ndarray:
+        oc, off = _i32(out_coords), _i32(offsets)
+        nbr = np.empty((oc.shape[0], off.shape[0]), dtype=np.int32)
+        lib().ref_kmap(_p(oc), oc.shape[0], _p(off), off.shape[0], stride, *map(int, shape), _p(self.keys),
+                       _p(self.vals), self.T, _p(nbr))
+        return nbr
+
+
+def ref_fwd_f32(X, W, nbr):
+    X, W, nbr = _f32(X), _f32(W), _i32(nbr)
+    K, Cin, Cout = W.shape
+    out = np.empty((nbr.shape[0], Cout), dtype=np.float32)
+    lib().ref_fwd_f32(_p(X), Cin, _p(W), K, Cout, _p(nbr), nbr.shape[0], _p(out))
+    return out
+
+
+def ref_dgrad_f32(dY, W, nbr, n_in):
+    dY, W, nbr = _f32(dY), _f32(W), _i32(nbr)
+    K, Cin, Cout = W.shape
+    dX = np.empty((n_in, Cin), dtype=np.float32)
+    lib().ref_dgrad_f32(_p(dY), Cout, _p(W), K, Cin, _p(nbr), nbr.shape[0], n_in, _p(dX))
+    return dX
+
+
+def ref_wgrad_f32(X, dY, nbr, K):
+    X, dY, nbr = _f32(X), _f32(dY), _i32(nbr)
+    Cin, Cout = X.shape[1], dY.shape[1]
+    dW = np.empty((K, Cin, Cout), dtype=np.float32)
+    lib().ref_wgrad_f32(_p(X), Cin, _p(dY), Cout, _p(nbr), nbr.shape[0], K, _p(dW))
+    return dW
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_threads(int(n))
+
+
+# --------------------------------------------------- brute force (tiny inputs)
+
+def bf_kmap(in_coords, out_coords, offsets, stride, shape, in_scale=1) -> np.ndarray:
+    """Dictionary lookup, one (o, k) at a time (conv.py:41-73 semantics)."""
+    idx = {}
+    for i, (b, x, y, z) in enumerate(np.asarray(in_coords).tolist()):
+        idx.setdefault((b, x * in_scale, y * in_scale, z * in_scale), i)
+    offs = np.asarray(offsets).tolist()
+    res = np.full((len(out_coords), len(offs)), -1, dtype=np.int32)
+    for o, (b, x, y, z) in enumerate(np.asarray(out_coords).tolist()):
+        for k, (tx, ty, tz) in enumerate(offs):
+            q = (x * stride - tx, y * stride - ty, z * stride - tz)
+            if all(0 <= q[a] < shape[a] for a in range(3)):
+                res[o, k] = idx.get((b,) + q, -1)
+    return res
+
+
+def bf_out_coords(in_coords, offsets, stride, transposed, new_shape) -> np.ndarray:
+    """Explicit candidate loop with a seen-set (kmap.py:278-330, 397-444 without chunking)."""
+    seen, out = set(), []
+    for b, x, y, z in np.asarray(in_coords).tolist():
+        for tx, ty, tz in np.asarray(offsets).tolist():
+            if transposed:
+                c = (x * stride + tx, y * stride + ty, z * stride + tz)
+            else:
+                c = (x + tx, y + ty, z + tz)
+                if any(v % stride for v in c):  # Python floor-mod, as torch's `%`
+                    continue
+                c = tuple(v // stride for v in c)
+            if not all(0 <= c[a] <= new_shape[a] - 1 for a in range(3)):
+                continue
+            key = (b,) + c
+            if key not in seen:
+                seen.add(key)
+                out.append(key)
+    return np.asarray(out, dtype=np.int32).reshape(-1, 4)
+
+
+def dense_conv_at(in_coords, feats, weight, kernel_size, stride, padding, dilation, transposed, out_coords,
+                  spatial_shape):
+    """Dense conv3d / conv_transpose3d (float64, CPU) read at out_coords -- tests/test_sparse_conv.py:37-44, 69-76."""
+    import torch
+    import torch.nn.functional as F
+
+    k = kernel_size
+    ic = torch.as_tensor(np.asarray(in_coords), dtype=torch.long)
+    f = torch.as_tensor(np.asarray(feats), dtype=torch.float64)
+    w = torch.as_tensor(np.asarray(weight), dtype=torch.float64)
+    Cin, Cout = w.shape[1], w.shape[2]
+    B = int(ic[:, 0].max().item()) + 1 if ic.shape[0] else 1
+    dense = torch.zeros((B, Cin) + tuple(int(v) for v in spatial_shape), dtype=torch.float64)
+    if ic.shape[0]:
+        dense[ic[:, 0], :, ic[:, 1], ic[:, 2], ic[:, 3]] = f
+    if transposed:
+        wt = w.view(k, k, k, Cin, Cout).permute(3, 4, 0, 1, 2).contiguous()
+        y = F.conv_transpose3d(dense, wt, stride=stride, padding=padding, dilation=dilation)
+    else:
+        wt = w.view(k, k, k, Cin, Cout).permute(4, 3, 0, 1, 2).contiguous()
+        y = F.conv3d(dense, wt, stride=stride, padding=padding, dilation=dilation)
+    oc = torch.as_tensor(np.asarray(out_coords), dtype=torch.long)
+    return y[oc[:, 0], :, oc[:, 1], oc[:, 2], oc[:, 3]].numpy()

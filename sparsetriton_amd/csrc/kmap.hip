@@ -1,0 +1,376 @@
+// Output coordinates and kernel maps of strided and transposed convolution.
+//
+// The reference materialises all N*K candidate coordinates, filters them with
+// boolean indexing and dedups them with a lossy 31-bit hash whose survivor is
+// whichever CAS wins (kmap.py:213-444).  Here candidates are never stored:
+// each pass recomputes them in registers from the input row (thread per input
+// row, offsets in LDS), and dedup uses exact 64-bit keys in an open-addressing
+// table keyed on the output coordinate.  The survivor of each coordinate is
+// its first candidate in input-major / offset-minor order (atomic min of the
+// candidate index), so the output order is deterministic; it is the order the
+// reference produces when its CAS winners happen to be first occurrences.
+//
+// Because each candidate (input i, offset k) that survives the filters is
+// exactly one kernel-map pair (i -> output of the candidate, offset k), the
+// map in both directions falls out of the same enumeration; no N_out x K
+// neighbour query is needed.
+#include "common.h"
+
+namespace st {
+
+struct Geom {
+  int K;
+  int transposed;
+  int64_t s;
+  int64_t in_shape[3];
+  int64_t out_shape[3];
+};
+
+// Candidate output coordinate of input (x, y, z) through offset t; false when
+// filtered out.  Normal conv: c = in + t must be >= 0 and divisible by the
+// stride on every axis, then c / s must be <= out_shape - 1 (kmap.py:286-309).
+// Transposed: c = in * s + t must lie in [0, out_shape - 1] (kmap.py:406-423).
+__device__ __forceinline__ bool candidate(const Geom& g, int64_t x, int64_t y, int64_t z, int32_t tx, int32_t ty,
+                                          int32_t tz, int64_t& ox, int64_t& oy, int64_t& oz) {
+  if (g.transposed) {
+    ox = x * g.s + tx;
+    oy = y * g.s + ty;
+    oz = z * g.s + tz;
+  } else {
+    const int64_t cx = x + tx, cy = y + ty, cz = z + tz;
+    if (cx < 0 || cy < 0 || cz < 0) return false;
+    if (cx % g.s || cy % g.s || cz % g.s) return false;
+    ox = cx / g.s;
+    oy = cy / g.s;
+    oz = cz / g.s;
+  }
+  return ox >= 0 && oy >= 0 && oz >= 0 && ox <= g.out_shape[0] - 1 && oy <= g.out_shape[1] - 1 &&
+         oz <= g.out_shape[2] - 1;
+}
+
+// The input side of the neighbour query: the reference looks the input up at
+// out * s - t (= in, or in * s for transposed) and keeps it only inside
+// [0, shape) (conv.py:54-59, 180-188).
+__device__ __forceinline__ bool input_in_bounds(const Geom& g, int64_t x, int64_t y, int64_t z) {
+  return x >= 0 && y >= 0 && z >= 0 && x < g.in_shape[0] && y < g.in_shape[1] && z < g.in_shape[2];
+}
+
+__device__ __forceinline__ void load_offsets(int32_t* off_s, const int32_t* __restrict__ offsets, int K) {
+  for (int t = threadIdx.x; t < K * 3; t += blockDim.x) off_s[t] = offsets[t];
+  __syncthreads();
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void cand_insert_kernel(const CT* __restrict__ coords, int64_t n,
+                                                          const int32_t* __restrict__ offsets, Geom g,
+                                                          uint64_t* __restrict__ dkeys, uint32_t* __restrict__ dvals,
+                                                          uint32_t dcap, int32_t* __restrict__ status) {
+  __shared__ int32_t off_s[ST_MAX_KVOL * 3];
+  load_offsets(off_s, offsets, g.K);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int64_t b, x, y, z;
+  load_coord(coords, i, b, x, y, z);
+  for (int k = 0; k < g.K; ++k) {
+    int64_t ox, oy, oz;
+    if (!candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz)) continue;
+    uint64_t key;
+    if (!pack_key(b, ox, oy, oz, key)) {
+      atomicAdd(&status[ST_STATUS_BAD_COORD], 1);
+      continue;
+    }
+    bool was_new;
+    uint32_t s = insert_slot(dkeys, dcap, key, was_new);
+    if (s == ST_NO_VAL) {
+      atomicAdd(&status[ST_STATUS_OVERFLOW], 1);
+      continue;
+    }
+    atomicMin(&dvals[s], (uint32_t)(i * g.K + k));
+  }
+}
+
+// Number of first-occurrence candidates of input row i, with the slot of each
+// one reported through the callback.
+template <typename CT, typename F>
+__device__ __forceinline__ int first_candidates(const CT* __restrict__ coords, int64_t i, const int32_t* off_s,
+                                                const Geom& g, const uint64_t* __restrict__ dkeys,
+                                                const uint32_t* __restrict__ dvals, uint32_t dcap, F&& on_first) {
+  int64_t b, x, y, z;
+  load_coord(coords, i, b, x, y, z);
+  int cnt = 0;
+  for (int k = 0; k < g.K; ++k) {
+    int64_t ox, oy, oz;
+    if (!candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz)) continue;
+    uint64_t key;
+    if (!pack_key(b, ox, oy, oz, key)) continue;
+    uint32_t s = find_slot(dkeys, dcap, key);
+    if (s == ST_NO_VAL || dvals[s] != (uint32_t)(i * g.K + k)) continue;
+    on_first(s, b, ox, oy, oz);
+    ++cnt;
+  }
+  return cnt;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void cand_count_kernel(const CT* __restrict__ coords, int64_t n,
+                                                         const int32_t* __restrict__ offsets, Geom g,
+                                                         const uint64_t* __restrict__ dkeys,
+                                                         const uint32_t* __restrict__ dvals, uint32_t dcap,
+                                                         int32_t* __restrict__ block_counts) {
+  __shared__ int32_t off_s[ST_MAX_KVOL * 3];
+  __shared__ int red[8];
+  load_offsets(off_s, offsets, g.K);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int cnt = 0;
+  if (i < n)
+    cnt = first_candidates(coords, i, off_s, g, dkeys, dvals, dcap,
+                           [](uint32_t, int64_t, int64_t, int64_t, int64_t) {});
+  cnt = wave_sum(cnt);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int t = 0;
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) t += red[w];
+    block_counts[blockIdx.x] = t;
+  }
+}
+
+// In-place exclusive scan of counts[0..n); counts[n] receives the total.
+// One workgroup of 1024 threads walks the array in 1024-element chunks.
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restrict__ counts, int64_t n) {
+  __shared__ int scratch[17];
+  int carry = 0;
+  for (int64_t base = 0; base < n; base += blockDim.x) {
+    const int64_t j = base + threadIdx.x;
+    const int v = j < n ? counts[j] : 0;
+    int tot;
+    const int ex = block_exclusive_scan(v, scratch, &tot);
+    if (j < n) counts[j] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) counts[n] = carry;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void cand_emit_kernel(const CT* __restrict__ coords, int64_t n,
+                                                        const int32_t* __restrict__ offsets, Geom g,
+                                                        const uint64_t* __restrict__ dkeys,
+                                                        const uint32_t* __restrict__ dvals,
+                                                        uint32_t* __restrict__ slot_out, uint32_t dcap,
+                                                        const int32_t* __restrict__ block_offsets,
+                                                        CT* __restrict__ out_coords) {
+  __shared__ int32_t off_s[ST_MAX_KVOL * 3];
+  __shared__ int scratch[5];
+  load_offsets(off_s, offsets, g.K);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int cnt = 0;
+  if (i < n)
+    cnt = first_candidates(coords, i, off_s, g, dkeys, dvals, dcap,
+                           [](uint32_t, int64_t, int64_t, int64_t, int64_t) {});
+  int tot;
+  int pos = block_offsets[blockIdx.x] + block_exclusive_scan(cnt, scratch, &tot);
+  if (i >= n || cnt == 0) return;
+  first_candidates(coords, i, off_s, g, dkeys, dvals, dcap,
+                   [&](uint32_t s, int64_t b, int64_t ox, int64_t oy, int64_t oz) {
+                     CT* r = out_coords + (int64_t)pos * 4;
+                     r[0] = (CT)b;
+                     r[1] = (CT)ox;
+                     r[2] = (CT)oy;
+                     r[3] = (CT)oz;
+                     slot_out[s] = (uint32_t)pos;
+                     ++pos;
+                   });
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void cand_map_kernel(const CT* __restrict__ coords, int64_t n,
+                                                       const int32_t* __restrict__ offsets, Geom g,
+                                                       const uint64_t* __restrict__ dkeys,
+                                                       const uint32_t* __restrict__ slot_out, uint32_t dcap,
+                                                       const uint64_t* __restrict__ in_keys,
+                                                       const uint32_t* __restrict__ in_vals, uint32_t in_cap,
+                                                       int64_t n_out, int32_t* __restrict__ nbr,
+                                                       int32_t* __restrict__ invnbr, uint32_t* __restrict__ out_masks,
+                                                       uint32_t* __restrict__ in_masks) {
+  __shared__ int32_t off_s[ST_MAX_KVOL * 3];
+  load_offsets(off_s, offsets, g.K);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int64_t b, x, y, z;
+  load_coord(coords, i, b, x, y, z);
+  if (!input_in_bounds(g, x, y, z)) return;
+  if (in_keys) {
+    // Only the row the input table resolves this coordinate to is a neighbour.
+    const int64_t sc = g.transposed ? g.s : 1;
+    uint64_t key;
+    if (!pack_key(b, x * sc, y * sc, z * sc, key)) return;
+    const uint32_t s = find_slot(in_keys, in_cap, key);
+    if (s == ST_NO_VAL || in_vals[s] != (uint32_t)i) return;
+  }
+  const int W = (g.K + 31) >> 5;
+  uint32_t mword = 0;
+  for (int k = 0; k < g.K; ++k) {
+    int64_t ox, oy, oz;
+    uint64_t key;
+    uint32_t o = ST_NO_VAL;
+    if (candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz) &&
+        pack_key(b, ox, oy, oz, key)) {
+      const uint32_t s = find_slot(dkeys, dcap, key);
+      if (s != ST_NO_VAL) o = slot_out[s];
+    }
+    if (o != ST_NO_VAL && (int64_t)o < n_out) {
+      invnbr[(int64_t)k * n + i] = (int32_t)o;
+      nbr[(int64_t)k * n_out + o] = (int32_t)i;
+      atomicOr(&out_masks[(int64_t)o * W + (k >> 5)], 1u << (k & 31));
+      mword |= 1u << (k & 31);
+    }
+    if ((k & 31) == 31 || k == g.K - 1) {
+      in_masks[i * W + (k >> 5)] = mword;
+      mword = 0;
+    }
+  }
+}
+
+static bool make_geom(const st_outgeom* in, Geom& g) {
+  if (!in || in->K <= 0 || in->K > ST_MAX_KVOL || in->stride < 1) return false;
+  g.K = in->K;
+  g.transposed = in->transposed ? 1 : 0;
+  g.s = in->stride;
+  for (int a = 0; a < 3; ++a) {
+    g.in_shape[a] = in->in_shape[a];
+    g.out_shape[a] = in->out_shape[a];
+  }
+  return true;
+}
+
+static int64_t gcd64(int64_t a, int64_t b) {
+  while (b) {
+    int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+}  // namespace st
+
+using namespace st;
+
+extern "C" {
+
+int st_outcoords_sizes(int64_t n, const st_outgeom* gin, int64_t kernel_size, int64_t dilation,
+                       int64_t* dedup_capacity, int64_t* num_blocks) {
+  Geom g;
+  if (n < 0 || !make_geom(gin, g) || kernel_size < 1 || dilation < 1 || !dedup_capacity || !num_blocks)
+    return ST_ERR_ARG;
+  // Candidates per input that can pass the stride filter: on each axis the
+  // offsets j*d hit one residue class mod s at most ceil(k / (s / gcd(d, s)))
+  // times.
+  int64_t per_axis = kernel_size;
+  if (!g.transposed && g.s > 1) {
+    const int64_t period = g.s / gcd64(dilation, g.s);
+    per_axis = (kernel_size + period - 1) / period;
+  }
+  int64_t kv = per_axis * per_axis * per_axis;
+  if (kv > g.K) kv = g.K;
+  int64_t cap = 2 * n * kv + 64;
+  if (cap >= (1ll << 31)) return ST_ERR_ARG;
+  *dedup_capacity = cap;
+  *num_blocks = (n + 255) / 256;
+  return ST_OK;
+}
+
+int st_outcoords_plan(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                      const st_outgeom* gin, uint64_t* dkeys, uint32_t* dvals, int64_t dcap, int32_t* block_counts,
+                      int64_t num_blocks, int32_t* status, st_stream_t stream) {
+  Geom g;
+  if (n < 0 || !make_geom(gin, g) || dcap <= 0 || dcap >= (1ll << 31) || !dkeys || !dvals || !block_counts ||
+      !status || !offsets)
+    return ST_ERR_ARG;
+  if (num_blocks != (n + 255) / 256 || n * (int64_t)g.K >= (1ll << 32) - 1) return ST_ERR_ARG;
+  if (n > 0 && !in_coords) return ST_ERR_ARG;
+  if (n > 0) {
+    ST_DISPATCH_COORD(coord_dtype, CT, {
+      cand_insert_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys,
+                                                                       dvals, (uint32_t)dcap, status);
+      cand_count_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys,
+                                                                      dvals, (uint32_t)dcap, block_counts);
+    });
+  }
+  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, num_blocks);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                      const st_outgeom* gin, const uint64_t* dkeys, const uint32_t* dvals, uint32_t* slot_out,
+                      int64_t dcap, const int32_t* block_counts, int64_t num_blocks, const uint64_t* in_keys,
+                      const uint32_t* in_vals, int64_t in_cap, void* out_coords, int64_t n_out, int32_t* nbr,
+                      int32_t* invnbr, uint32_t* out_masks, uint32_t* in_masks, st_stream_t stream) {
+  Geom g;
+  if (n < 0 || n_out < 0 || !make_geom(gin, g) || dcap <= 0 || dcap >= (1ll << 31) || !dkeys || !dvals ||
+      !slot_out || !block_counts || !offsets)
+    return ST_ERR_ARG;
+  if (num_blocks != (n + 255) / 256) return ST_ERR_ARG;
+  if (in_keys && (!in_vals || in_cap <= 0 || in_cap >= (1ll << 31))) return ST_ERR_ARG;
+  if (n == 0 || n_out == 0) return ST_OK;
+  if (!in_coords || !out_coords) return ST_ERR_ARG;
+  if (nbr && (!invnbr || !out_masks || !in_masks)) return ST_ERR_ARG;
+  ST_DISPATCH_COORD(coord_dtype, CT, {
+    cand_emit_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys, dvals,
+                                                                   slot_out, (uint32_t)dcap, block_counts,
+                                                                   (CT*)out_coords);
+    if (nbr)
+      cand_map_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>(
+        (const CT*)in_coords, n, offsets, g, dkeys, slot_out, (uint32_t)dcap, in_keys, in_vals, (uint32_t)in_cap,
+        n_out, nbr, invnbr, out_masks, in_masks);
+  });
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ map inversion
+
+namespace st {
+
+// One thread per output row o: every valid (k, o) -> i entry becomes
+// invnbr[k][i] = o.  For a convolution map each (i, k) has at most one o, so
+// the scatter has no write conflicts.
+__global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restrict__ nbr, int64_t ks, int64_t rs,
+                                                          int64_t n_out, int K, int64_t n_in,
+                                                          int32_t* __restrict__ invnbr, uint32_t* __restrict__ in_masks,
+                                                          uint32_t* __restrict__ out_masks) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n_out) return;
+  const int W = (K + 31) >> 5;
+  uint32_t mword = 0;
+  for (int k = 0; k < K; ++k) {
+    const int32_t i = nbr[(int64_t)k * ks + o * rs];
+    if (i >= 0 && (int64_t)i < n_in) {
+      invnbr[(int64_t)k * n_in + i] = (int32_t)o;
+      atomicOr(&in_masks[(int64_t)i * W + (k >> 5)], 1u << (k & 31));
+      mword |= 1u << (k & 31);
+    }
+    if ((k & 31) == 31 || k == K - 1) {
+      if (out_masks) out_masks[o * W + (k >> 5)] = mword;
+      mword = 0;
+    }
+  }
+}
+
+}  // namespace st
+
+extern "C" int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride, int64_t n_out, int K,
+                              int64_t n_in, int32_t* invnbr, uint32_t* in_masks, uint32_t* out_masks,
+                              st_stream_t stream) {
+  if (n_out < 0 || n_in < 0 || K <= 0 || K > ST_MAX_KVOL) return ST_ERR_ARG;
+  if (n_out >= (1ll << 31) || n_in >= (1ll << 31)) return ST_ERR_ARG;
+  if (n_out == 0) return ST_OK;
+  if (!nbr || (n_in > 0 && (!invnbr || !in_masks))) return ST_ERR_ARG;
+  st::kmap_invert_kernel<<<st_blocks(n_out, 256), 256, 0, stream>>>(nbr, nbr_k_stride, nbr_r_stride, n_out, K, n_in,
+                                                                    invnbr, in_masks, out_masks);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}

@@ -1,0 +1,86 @@
+// MFMA fragments for the 16x16 output tiles used by every GEMM kernel here.
+//
+// A wave computes D(16x16) += A(16 x KSTEP) * B(KSTEP x 16).  Lane l supplies
+// row (l & 15) of A and column (l & 15) of B, each as VEC consecutive
+// reduction elements starting at (l >> 4) * VEC:
+//   fp32  : VEC = 4, KSTEP = 16, four v_mfma_f32_16x16x4_f32 (one per vector element)
+//   f16/bf16: VEC = 8, KSTEP = 32, one v_mfma_f32_16x16x32_{f16,bf16}
+// The hardware's assignment of (lane group, element) to a reduction index is
+// the same for A and B, so any fixed assignment of reduction indices to
+// (l >> 4, element) gives the same sum; loading VEC consecutive elements per
+// lane keeps every fragment a single 16-byte load.
+// D layout: lane l holds D[(l >> 4) * 4 + r][l & 15] in accumulator element r.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace st {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+template <typename T>
+struct Frag;
+
+template <>
+struct Frag<float> {
+  using type = v4f;
+  static constexpr int VEC = 4;
+  static constexpr int KSTEP = 16;
+};
+template <>
+struct Frag<_Float16> {
+  using type = v8h;
+  static constexpr int VEC = 8;
+  static constexpr int KSTEP = 32;
+};
+template <>
+struct Frag<__bf16> {
+  using type = v8bf;
+  static constexpr int VEC = 8;
+  static constexpr int KSTEP = 32;
+};
+
+__device__ __forceinline__ v4f mfma(const v4f& a, const v4f& b, v4f acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], acc, 0, 0, 0);
+  return acc;
+}
+__device__ __forceinline__ v4f mfma(const v8h& a, const v8h& b, v4f acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma(const v8bf& a, const v8bf& b, v4f acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type zero_frag() {
+  typename Frag<T>::type f;
+#pragma unroll
+  for (int e = 0; e < Frag<T>::VEC; ++e) f[e] = (T)0.0f;
+  return f;
+}
+
+// Load VEC elements row[col .. col+VEC) with zero fill past `limit`.
+// `vec_ok` promises row + col is 16-byte aligned whenever col + VEC <= limit.
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type load_frag(const T* __restrict__ row, int col, int limit,
+                                                            bool vec_ok) {
+  using F = typename Frag<T>::type;
+  constexpr int VEC = Frag<T>::VEC;
+  if (vec_ok && col + VEC <= limit) return *reinterpret_cast<const F*>(row + col);
+  F f;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) f[e] = (col + e < limit) ? row[col + e] : (T)0.0f;
+  return f;
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) {
+  return (T)v;
+}
+
+}  // namespace st

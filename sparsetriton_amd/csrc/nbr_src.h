@@ -1,0 +1,72 @@
+// Neighbour sources for the GEMM kernels: where the row of A feeding row r
+// through kernel offset k comes from.
+//
+//   MapSrc  : a precomputed kernel map, map[k * ks + r * rs] (-1 = none).
+//   HashSrc : probe the coordinate table inside the GEMM (implicit hash-fly):
+//             q = (c.xyz * mul + sign * offsets[k]) / div, kept only when the
+//             division is exact and 0 <= q < bounds, then looked up.  Rows whose
+//             own c lies outside [0, row_bounds) (when given) have no pairs.
+//
+// A source is used as  rc = src.row(r)  (once per row)  then  src.get(rc, k).
+// k is uniform across the workgroup in every caller, so offsets[k] is a
+// scalar load.
+#pragma once
+
+#include "common.h"
+
+namespace st {
+
+struct MapSrc {
+  const int32_t* __restrict__ map;
+  int64_t ks, rs;
+  typedef int64_t RowCtx;
+  __device__ __forceinline__ RowCtx row(int64_t r) const { return r; }
+  __device__ __forceinline__ int32_t get(const RowCtx& r, int k) const { return map[(int64_t)k * ks + r * rs]; }
+};
+
+template <typename CT>
+struct HashSrc {
+  const CT* __restrict__ coords;
+  const int32_t* __restrict__ offsets;
+  const uint64_t* __restrict__ keys;
+  const uint32_t* __restrict__ vals;
+  uint32_t cap;
+  int32_t sign;
+  int64_t mul, div;
+  int64_t bx, by, bz;
+  int64_t rbx, rby, rbz;  // row bounds (checked when > 0)
+  struct RowCtx {
+    int64_t b, x, y, z;
+    bool ok;
+  };
+  __device__ __forceinline__ RowCtx row(int64_t r) const {
+    RowCtx c;
+    load_coord(coords, r, c.b, c.x, c.y, c.z);
+    c.ok = !((rbx > 0 && (c.x < 0 || c.x >= rbx)) || (rby > 0 && (c.y < 0 || c.y >= rby)) ||
+             (rbz > 0 && (c.z < 0 || c.z >= rbz)));
+    c.x *= mul;
+    c.y *= mul;
+    c.z *= mul;
+    return c;
+  }
+  __device__ __forceinline__ int32_t get(const RowCtx& c, int k) const {
+    if (!c.ok) return -1;
+    int64_t qx = c.x + sign * (int64_t)offsets[3 * k];
+    int64_t qy = c.y + sign * (int64_t)offsets[3 * k + 1];
+    int64_t qz = c.z + sign * (int64_t)offsets[3 * k + 2];
+    if (qx < 0 || qy < 0 || qz < 0) return -1;
+    if (div > 1) {
+      if (qx % div || qy % div || qz % div) return -1;
+      qx /= div;
+      qy /= div;
+      qz /= div;
+    }
+    if (qx >= bx || qy >= by || qz >= bz) return -1;
+    uint64_t key;
+    if (!pack_key(c.b, qx, qy, qz, key)) return -1;
+    const uint32_t s = find_slot(keys, cap, key);
+    return s == ST_NO_VAL ? -1 : (int32_t)vals[s];
+  }
+};
+
+}  // namespace st

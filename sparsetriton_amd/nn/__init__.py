@@ -1,0 +1,4 @@
+from . import functional
+from .modules import SparseConv3D, SparseConv3DBase, SparseConvTransposed3D, SubMConv3D
+
+__all__ = ["functional", "SparseConv3DBase", "SparseConv3D", "SubMConv3D", "SparseConvTransposed3D"]

@@ -1,0 +1,179 @@
+"""``sparse_conv3d``: the sparse-convolution entry point.
+
+Same signature, argument rules and results as the reference
+(``sparsetriton/nn/functional/conv/conv.py:77-239``):
+
+* cubic kernel, uniform stride / dilation / padding (``AssertionError`` otherwise);
+* submanifold forces padding ``(k-1)*d//2`` and excludes ``transposed``;
+* ``weight`` is (k^3, C_in, C_out); ``bias`` is added after the GEMM;
+* the coordinate hash table and, per geometry
+  ``(k, s, p, d, submanifold, transposed)``, the output coordinates and kernel
+  map are cached on the input's ``TensorCache``; a submanifold result shares
+  that cache, so a stack of submanifold layers builds its map once;
+* ``get_conv_algo()`` picks ``PrecomputedNeighborGEMM`` (kernel map + gather
+  GEMM) or ``ImplicitHashFlyGEMM`` (table probes inside the GEMM).
+
+Everything on the path runs as HIP kernels from ``libsparsetriton_amd.so``.
+"""
+
+from typing import Tuple, Union
+
+import torch
+
+from sparsetriton_amd import _lib
+from sparsetriton_amd.config import ConvAlgo, MIN_TABLE_FACTOR, get_conv_algo, get_h_table_f
+from sparsetriton_amd.tensor import SparseTensor
+from sparsetriton_amd.utils.hash import HashTable
+
+from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, InputGradLookup
+from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM
+from .kmap import KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map
+
+__all__ = ["sparse_conv3d", "compute_neighbor_indices", "table_capacity"]
+
+
+def table_capacity(n: int) -> int:
+    """Slots for a table of n keys: factor * n with the factor at least 2 (load <= 0.5)."""
+    return max(int(n * max(get_h_table_f(), MIN_TABLE_FACTOR)), 16)
+
+
+def compute_neighbor_indices(
+    in_hash_table: HashTable,
+    out_coords: torch.Tensor,
+    kernel_offsets: torch.Tensor,
+    spatial_shape: Tuple[int, int, int],
+    stride: int,
+    padding: int = 0,
+    dilation: int = 1,
+) -> torch.Tensor:
+    """(N_out, K) int32: row of ``out * stride - kernel_offsets[k]`` if in [0, shape) and present, else -1.
+
+    Same result as the reference (``conv.py:12-75``), computed by one HIP
+    kernel (``st_kmap_query``) without materialising the (N_out, K, 4)
+    candidate coordinates.  The returned tensor is a view of an offset-major
+    (K, N_out) buffer.
+    """
+    kmap = query_kernel_map(in_hash_table, out_coords, kernel_offsets, spatial_shape, stride, n_in=0)
+    return kmap.neighbor_indices
+
+
+def _input_table(tensor: SparseTensor, scale: int) -> HashTable:
+    """The coordinate table of ``tensor`` (coordinates * scale for transposed convs), cached."""
+    cache = tensor._cache
+    if scale == 1:
+        if cache.hashtable is None:
+            t = HashTable(table_capacity(tensor.C.shape[0]), device=tensor.F.device)
+            t.insert(tensor.C)
+            cache.hashtable = t
+        return cache.hashtable
+    key = ("scaled_table", scale)
+    if key not in cache.kmaps:
+        t = HashTable(table_capacity(tensor.C.shape[0]), device=tensor.F.device)
+        t.insert(tensor.C, scale=scale)
+        cache.kmaps[key] = t
+    return cache.kmaps[key]
+
+
+def _uniform(v, what: str) -> int:
+    if isinstance(v, (tuple, list)):
+        assert v[0] == v[1] == v[2], f"Only uniform {what} supported for now"
+        return int(v[0])
+    return int(v)
+
+
+def sparse_conv3d(
+    tensor: SparseTensor,
+    weight: torch.Tensor,
+    kernel_size: Union[int, Tuple[int, int, int]],
+    bias: torch.Tensor = None,
+    stride: Union[int, Tuple[int, int, int]] = 1,
+    dilation: Union[int, Tuple[int, int, int]] = 1,
+    padding: Union[int, Tuple[int, int, int]] = 0,
+    transposed: bool = False,
+    submanifold: bool = True,
+) -> SparseTensor:
+    """3-D sparse convolution of ``tensor`` with ``weight`` (k^3, C_in, C_out)."""
+    if isinstance(kernel_size, (tuple, list)):
+        assert kernel_size[0] == kernel_size[1] == kernel_size[2], "Only cubic kernels supported for now"
+    k = _uniform(kernel_size, "kernel")
+    s = _uniform(stride, "stride")
+    d = _uniform(dilation, "dilation")
+    if submanifold:
+        padding = ((k - 1) * d) // 2
+    p = _uniform(padding, "padding")
+    if submanifold:
+        assert not transposed, "Submanifold convolution does not support transposed=True"
+
+    device = tensor.F.device
+    K, C_in, C_out = weight.shape
+    assert C_in == tensor.F.shape[1], f"Input channels in weight({C_in}) and tensor({tensor.F.shape[1]}) must match"
+    assert K == k ** 3, f"Kernel size in weight({K}) and argument({k ** 3}) must match"
+    _lib.require_device(tensor.F, "SparseTensor features")
+
+    scale = s if (transposed and s > 1) else 1
+    in_table = _input_table(tensor, scale)
+    lookup_shape = tuple(int(v) * scale for v in tensor.spatial_shape)
+    subm_fast = submanifold and s == 1 and ((k - 1) * d) // 2 == p
+    cache_key = (k, s, p, d, submanifold, transposed)
+    algo = get_conv_algo()
+
+    if algo == ConvAlgo.PrecomputedNeighborGEMM:
+        hit = tensor._cache.neighbor_indices.get(cache_key)
+        if hit is not None:
+            out_coords, kmap, new_shape = hit
+        else:
+            if subm_fast:
+                out_coords, new_shape = tensor.C, tensor.spatial_shape
+                offsets = _target_offsets(k, d, p, False, device)
+                kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1, tensor.C.shape[0])
+            else:
+                out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
+                    tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
+            tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
+        if out_coords.shape[0] == 0:
+            return _empty(tensor, C_out, new_shape)
+        out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap)
+    elif algo == ConvAlgo.ImplicitHashFlyGEMM:
+        hkey = ("hashfly",) + cache_key
+        hit = tensor._cache.kmaps.get(hkey)
+        if hit is None:
+            if subm_fast:
+                out_coords, new_shape = tensor.C, tensor.spatial_shape
+                offsets = _target_offsets(k, d, p, False, device).to(tensor.C.dtype)
+                gl = InputGradLookup(in_table.table_keys, in_table.table_values, 1, 1, new_shape,
+                                     tensor.spatial_shape)
+            else:
+                out_coords, new_shape, offsets, _, out_table = build_out_coords_and_map(
+                    tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=False)
+                mul, div = (s, 1) if transposed else (1, s)
+                gl = InputGradLookup(out_table.table_keys, out_table.table_values, mul, div, new_shape,
+                                     tensor.spatial_shape)
+            hit = (out_coords, new_shape, offsets, gl)
+            tensor._cache.kmaps[hkey] = hit
+        out_coords, new_shape, offsets, gl = hit
+        if out_coords.shape[0] == 0:
+            return _empty(tensor, C_out, new_shape)
+        out_feats = ConvHashOnTheFlyImplicitGEMM.apply(
+            tensor.F, weight, out_coords, offsets, in_table.table_keys, in_table.table_values, lookup_shape,
+            1 if transposed else s, tensor.C, gl)
+    else:
+        raise ValueError(f"unknown convolution algorithm {algo}")
+
+    if bias is not None:
+        # in the features' dtype, as the reference's in-place `out_feats += bias` (conv.py:227-228)
+        out_feats = out_feats + bias.to(out_feats.dtype)
+
+    if submanifold and (out_coords is tensor.C or (out_coords.shape == tensor.C.shape
+                                                   and torch.equal(out_coords, tensor.C))):
+        return tensor.replace(out_feats)
+    return SparseTensor(feats=out_feats, coords=out_coords, spatial_shape=new_shape, batch_size=tensor.batch_size)
+
+
+def _empty(tensor: SparseTensor, C_out: int, new_shape) -> SparseTensor:
+    device = tensor.F.device
+    return SparseTensor(
+        feats=torch.empty((0, C_out), device=device, dtype=tensor.F.dtype),
+        coords=torch.empty((0, 4), device=device, dtype=tensor.C.dtype),
+        spatial_shape=new_shape,
+        batch_size=tensor.batch_size,
+    )

@@ -1,0 +1,143 @@
+"""Implicit GEMM that probes the coordinate hash table inside the kernel.
+
+``ConvHashOnTheFlyImplicitGEMM.apply(features, weights, coords, kernel_offsets,
+table_keys, table_vals, spatial_shape, lookup_stride)`` keeps the reference's
+signature and meaning (``.../conv/funcs/implicit_hashfly_gemm.py:330-452``):
+output row o with coordinate c sums, over offsets k, features at
+``q = c * lookup_stride - kernel_offsets[k]`` (when 0 <= q < spatial_shape
+and q is in the table) times ``weights[k]``.  ``table_keys`` /
+``table_vals`` are a ``HashTable``'s arrays (exact int64 keys here).
+
+No kernel map is stored.  The probe runs once per destination-row tile and
+offset (the reference repeats it for every C_out tile).  Two optional
+trailing arguments make the backward a gather like the forward:
+``in_coords`` (rows of ``features``) and ``grad_lookup`` (an
+``InputGradLookup``: a table of the output coordinates and the rule that
+finds them from an input row).  Given both, the input gradient probes that
+table; without them it builds the transposed map once from the forward
+lookups.  The weight gradient always probes the input table.
+"""
+
+import ctypes
+
+import torch
+
+from sparsetriton_amd import _lib
+from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
+    gather_gemm,
+    weight_prep,
+    wgrad_splits,
+)
+from sparsetriton_amd.nn.functional.conv.kmap import KernelMap
+
+__all__ = ["ConvHashOnTheFlyImplicitGEMM", "InputGradLookup"]
+
+
+def _lookup(K: int, sign: int, mul: int, div: int, bounds, row_bounds=(0, 0, 0)) -> _lib.Lookup:
+    lk = _lib.Lookup()
+    lk.K, lk.sign, lk.mul, lk.div = K, sign, int(mul), int(div)
+    for a in range(3):
+        lk.bounds[a] = int(bounds[a])
+        lk.row_bounds[a] = int(row_bounds[a])
+    return lk
+
+
+def _as_u64_keys(table_keys: torch.Tensor) -> torch.Tensor:
+    assert table_keys.dtype == torch.int64, "table_keys must be this package's int64 packed-coordinate keys"
+    return table_keys
+
+
+def hashfly_gemm(A, dst_coords, offsets_i32, lk, keys, vals, Bt, n_dst):
+    Kd, Nd = A.shape[1], Bt.shape[1]
+    out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
+    _lib.call("st_hashfly_gemm", _lib.ptr(A), A.shape[0], _lib.ptr(dst_coords), _lib.coord_code(dst_coords.dtype),
+              n_dst, _lib.ptr(offsets_i32), ctypes.byref(lk), _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
+              _lib.ptr(Bt), _lib.ptr(out), Kd, Nd, _lib.feat_code(A.dtype), _lib.stream_of(A.device))
+    return out
+
+
+def hashfly_wgrad(X, dY, out_coords, offsets_i32, lk, keys, vals, dw_dtype):
+    K, C_in, C_out = lk.K, X.shape[1], dY.shape[1]
+    n_out = out_coords.shape[0]
+    splits = wgrad_splits(n_out)
+    partials = torch.empty((K * splits * C_in * C_out,), dtype=torch.float32, device=X.device)
+    dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
+    _lib.call("st_hashfly_wgrad", _lib.ptr(X), X.shape[0], _lib.ptr(dY), _lib.ptr(out_coords),
+              _lib.coord_code(out_coords.dtype),
+              n_out, _lib.ptr(offsets_i32), ctypes.byref(lk), _lib.ptr(keys), _lib.ptr(vals), keys.shape[0], C_in,
+              C_out, _lib.feat_code(X.dtype), _lib.ptr(partials), splits, _lib.ptr(dW), _lib.feat_code(dw_dtype),
+              _lib.stream_of(X.device))
+    return dW
+
+
+class InputGradLookup:
+    """How the input gradient finds the output rows an input row feeds.
+
+    Forward pairs satisfy ``out * s - t_k = in_key``; solved for the output:
+    ``out = (in * mul + t_k) / div``, looked up in ``table_keys`` /
+    ``table_values`` (a table of the output coordinates) within ``out_shape``.
+    Input rows outside ``in_shape`` have no forward pairs.
+
+      submanifold / stride 1 : mul 1, div 1, table = input table
+      strided (s)            : mul 1, div s, table = output dedup table
+      transposed (s)         : mul s, div 1, table = output dedup table
+    """
+
+    def __init__(self, table_keys, table_values, mul: int, div: int, out_shape, in_shape):
+        self.table_keys, self.table_values = table_keys, table_values
+        self.mul, self.div = int(mul), int(div)
+        self.out_shape = tuple(int(v) for v in out_shape)
+        self.in_shape = tuple(int(v) for v in in_shape)
+
+
+class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, features, weights, coords, kernel_offsets, hash_table_keys, hash_table_vals, spatial_shape,
+                lookup_stride, in_coords=None, grad_lookup=None):
+        _lib.require_device(features, "features")
+        N_in, C_in = features.shape
+        K, C_in_w, C_out = weights.shape
+        assert C_in_w == C_in, f"weights C_in ({C_in_w}) != features C_in ({C_in})"
+        assert kernel_offsets.shape[0] == K, "kernel_offsets rows must equal the kernel volume"
+        features = features.contiguous()
+        coords = coords.contiguous()
+        offs = kernel_offsets.to(torch.int32).contiguous()
+        keys = _as_u64_keys(hash_table_keys)
+        vals = hash_table_vals.contiguous()
+        shape = tuple(int(v) for v in spatial_shape)
+        lk = _lookup(K, -1, int(lookup_stride), 1, shape)
+        wt = weight_prep(weights.to(features.dtype).contiguous(), _lib.W_TRANSPOSE)
+        out = hashfly_gemm(features, coords, offs, lk, keys, vals, wt, coords.shape[0])
+        ctx.save_for_backward(features, weights, coords, offs, keys, vals)
+        ctx.shape = shape
+        ctx.lookup_stride = int(lookup_stride)
+        ctx.in_coords = in_coords
+        ctx.grad_lookup = grad_lookup
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        features, weights, coords, offs, keys, vals = ctx.saved_tensors
+        K = weights.shape[0]
+        N_in = features.shape[0]
+        grad_output = grad_output.to(features.dtype).contiguous()
+        s = ctx.lookup_stride
+        grad_input = grad_weights = None
+        if ctx.needs_input_grad[0]:
+            w = weights.to(features.dtype).contiguous()
+            gl = ctx.grad_lookup
+            if ctx.in_coords is not None and gl is not None:
+                lk = _lookup(K, +1, gl.mul, gl.div, gl.out_shape, gl.in_shape)
+                grad_input = hashfly_gemm(grad_output, ctx.in_coords.contiguous(), offs, lk, gl.table_keys,
+                                          gl.table_values, w, N_in)
+            else:
+                nbr = torch.empty((K, coords.shape[0]), dtype=torch.int32, device=coords.device)
+                _lib.call("st_kmap_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0],
+                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
+                          _lib.ptr(nbr), coords.shape[0], 1, None, _lib.stream_of(coords.device))
+                kmap = KernelMap(nbr, N_in, coords.shape[0], K).ensure_inverse()
+                grad_input = gather_gemm(grad_output, kmap.invnbr, kmap.n_in, 1, kmap.in_masks, w, N_in, K)
+        if ctx.needs_input_grad[1]:
+            lk = _lookup(K, -1, s, 1, ctx.shape)
+            grad_weights = hashfly_wgrad(features, grad_output, coords, offs, lk, keys, vals, weights.dtype)
+        return grad_input, grad_weights, None, None, None, None, None, None, None, None

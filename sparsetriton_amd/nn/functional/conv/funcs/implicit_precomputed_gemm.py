@@ -1,0 +1,106 @@
+"""Gather-GEMM sparse convolution over a precomputed kernel map (HIP/MFMA).
+
+``ConvPrecomputedNeighborGEMM.apply(features, weights, neighbor_indices)`` has
+the reference's signature and meaning
+(``sparsetriton/nn/functional/conv/funcs/implicit_precomputed_gemm.py:233-324``):
+
+    out[o] = sum_k features[nbr[o, k]] @ weights[k]      (nbr = -1 contributes 0)
+
+with ``features`` (N_in, C_in), ``weights`` (K, C_in, C_out), output in the
+features' dtype, fp32 accumulation.  ``neighbor_indices`` is either the
+reference's (N_out, K) int32 tensor (any strides) or a ``KernelMap`` built by
+this package (which also carries row masks and the transposed map).
+
+Kernels (``libsparsetriton_amd.so``):
+  forward   st_gather_gemm over nbr with weights re-laid (K, C_out, C_in);
+  dgrad     st_gather_gemm over the transposed map with weights as stored
+            -- a gather, so no atomics and a deterministic result;
+  wgrad     st_wgrad, per-offset pair compaction + MFMA, fixed-order reduce.
+"""
+
+import torch
+
+from sparsetriton_amd import _lib
+from sparsetriton_amd.nn.functional.conv.kmap import KernelMap
+
+__all__ = ["ConvPrecomputedNeighborGEMM", "wgrad_splits"]
+
+
+def wgrad_splits(n_rows: int) -> int:
+    """Row splits per offset for the weight gradient: ~16k map rows per workgroup."""
+    return max(1, min(4096, (n_rows + 16383) // 16384))
+
+
+def _as_kmap(neighbor_indices, n_in: int) -> KernelMap:
+    if isinstance(neighbor_indices, KernelMap):
+        return neighbor_indices
+    return KernelMap.from_neighbor_indices(neighbor_indices, n_in)
+
+
+def gather_gemm(A: torch.Tensor, map_t: torch.Tensor, k_stride: int, r_stride: int, masks, Bt: torch.Tensor,
+                n_dst: int, K: int) -> torch.Tensor:
+    """out (n_dst, Nd) = sum_k A[map[k, r]] @ Bt[k]^T on the GPU."""
+    Kd = A.shape[1]
+    Nd = Bt.shape[1]
+    out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
+    W = (K + 31) // 32
+    _lib.call("st_gather_gemm", _lib.ptr(A), A.shape[0], _lib.ptr(map_t), k_stride, r_stride,
+              _lib.ptr(masks), W, None, _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd, _lib.feat_code(A.dtype),
+              _lib.stream_of(A.device))
+    return out
+
+
+def weight_prep(weights: torch.Tensor, mode: int) -> torch.Tensor:
+    K, C_in, C_out = weights.shape
+    shape = (K, C_out, C_in) if mode == _lib.W_TRANSPOSE else (K, C_in, C_out)
+    out = torch.empty(shape, dtype=weights.dtype, device=weights.device)
+    _lib.call("st_weight_prep", _lib.ptr(weights), _lib.ptr(out), K, C_in, C_out, mode,
+              _lib.feat_code(weights.dtype), _lib.stream_of(weights.device))
+    return out
+
+
+def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype) -> torch.Tensor:
+    K, C_in, C_out = kmap.K, X.shape[1], dY.shape[1]
+    splits = wgrad_splits(kmap.n_out)
+    partials = torch.empty((K * splits * C_in * C_out,), dtype=torch.float32, device=X.device)
+    dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
+    _lib.call("st_wgrad", _lib.ptr(X), X.shape[0], _lib.ptr(dY), _lib.ptr(kmap.nbr), kmap.k_stride, kmap.r_stride,
+              kmap.n_out,
+              K, C_in, C_out, _lib.feat_code(X.dtype), _lib.ptr(partials), splits, _lib.ptr(dW),
+              _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
+    return dW
+
+
+class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
+    """Sparse convolution with a precomputed neighbour map (gather-GEMM on MFMA)."""
+
+    @staticmethod
+    def forward(ctx, features, weights, neighbor_indices):
+        _lib.require_device(features, "features")
+        N_in, C_in = features.shape
+        K, C_in_w, C_out = weights.shape
+        assert C_in_w == C_in, f"weights C_in ({C_in_w}) != features C_in ({C_in})"
+        kmap = _as_kmap(neighbor_indices, N_in)
+        assert kmap.K == K, f"kernel map has {kmap.K} offsets, weights {K}"
+        features = features.contiguous()
+        w = weights.to(features.dtype).contiguous()
+        wt = weight_prep(w, _lib.W_TRANSPOSE)
+        out = gather_gemm(features, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, wt, kmap.n_out, K)
+        ctx.save_for_backward(features, weights)
+        ctx.kmap = kmap
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        features, weights = ctx.saved_tensors
+        kmap = ctx.kmap
+        grad_output = grad_output.to(features.dtype).contiguous()
+        grad_input = grad_weights = None
+        if ctx.needs_input_grad[0]:
+            kmap.ensure_inverse()
+            w = weights.to(features.dtype).contiguous()
+            # dX[i] = sum_k dY[invnbr[k, i]] @ W[k]^T: W[k] (C_in, C_out) is already the (Nd, Kd) operand.
+            grad_input = gather_gemm(grad_output, kmap.invnbr, kmap.n_in, 1, kmap.in_masks, w, kmap.n_in, kmap.K)
+        if ctx.needs_input_grad[1]:
+            grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
+        return grad_input, grad_weights, None

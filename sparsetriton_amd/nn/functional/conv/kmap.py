@@ -1,0 +1,290 @@
+"""Kernel offsets, output coordinates and kernel maps.
+
+Public functions keep the reference's names and meaning
+(``sparsetriton/nn/functional/conv/kmap.py:104-495``):
+
+* ``generate_base_offsets`` -- the k^3 offsets ``(i - k//2) * d`` per axis,
+  enumerated x-major / z-minor (``torch.meshgrid(indexing="ij")``), so offset
+  index ``k = (ix * ks + iy) * ks + iz``.
+* ``compute_target_offsets_normal`` / ``_transposed`` -- the per-offset shift
+  the neighbour lookup subtracts: input = output * stride - t_k.
+* ``build_out_coords`` -- (out_coords, new_spatial_shape, kernel_offsets).
+
+The output coordinates of a strided / transposed convolution and its kernel
+map come out of one HIP pipeline (``st_outcoords_plan`` / ``st_outcoords_emit``);
+the submanifold map comes from ``st_kmap_query``.  Maps are stored
+offset-major (K, N) int32 with per-row offset bitmasks, in both directions:
+``nbr[k, o]`` is the input row feeding output ``o`` through offset ``k`` and
+``invnbr[k, i]`` the output row input ``i`` feeds.
+"""
+
+from typing import Optional, Tuple
+
+import ctypes
+import torch
+
+from sparsetriton_amd import _lib
+from sparsetriton_amd.utils.hash import HashTable
+
+__all__ = [
+    "generate_base_offsets",
+    "compute_target_offsets_normal",
+    "compute_target_offsets_transposed",
+    "build_out_coords",
+    "KernelMap",
+    "out_spatial_shape",
+]
+
+
+# --------------------------------------------------------------- offsets/shape
+
+def generate_base_offsets(kernel_size, dilation, device) -> torch.Tensor:
+    """(k^3, 3) offsets ``(i - k//2) * d``, x-major (``kmap.py:104-132``)."""
+    ks = [int(v) for v in (kernel_size.tolist() if isinstance(kernel_size, torch.Tensor) else kernel_size)]
+    dil = dilation.to("cpu") if isinstance(dilation, torch.Tensor) else torch.as_tensor(dilation)
+    axes = [torch.arange(s) - (s // 2) for s in ks]
+    grid = torch.meshgrid(*axes, indexing="ij")
+    return (torch.stack(grid, dim=-1).reshape(-1, 3) * dil).to(device)
+
+
+def compute_target_offsets_normal(base_offsets, padding, dilation, kernel_size) -> torch.Tensor:
+    """t_k = -base + p - (k-1)*d//2: input = out*s - t_k (``kmap.py:135-155``)."""
+    return -base_offsets + padding - (kernel_size - 1) * dilation // 2
+
+
+def compute_target_offsets_transposed(base_offsets, padding, dilation, kernel_size, stride=None) -> torch.Tensor:
+    """t_k = base - p + (k-1)*d//2: output = in*s + t_k (``kmap.py:158-180``)."""
+    return base_offsets - padding + (kernel_size - 1) * dilation // 2
+
+
+def _target_offsets(kernel_size: int, dilation: int, padding: int, transposed: bool, device) -> torch.Tensor:
+    ks = torch.tensor([kernel_size] * 3)
+    dil = torch.tensor([dilation] * 3)
+    pad = torch.tensor([padding] * 3)
+    base = generate_base_offsets(ks, dil, "cpu")
+    if transposed:
+        t = compute_target_offsets_transposed(base, pad, dil, ks)
+    else:
+        t = compute_target_offsets_normal(base, pad, dil, ks)
+    return t.to(device)
+
+
+def out_spatial_shape(spatial_shape, kernel_size: int, stride: int, dilation: int, padding: int,
+                      transposed: bool) -> Tuple[int, int, int]:
+    """Output grid of a convolution (``kmap.py:254-258`` normal, ``:373-377`` transposed)."""
+    k, s, d, p = kernel_size, stride, dilation, padding
+    if transposed:
+        return tuple((int(v) - 1) * s + (k - 1) * d - 2 * p + 1 for v in spatial_shape)
+    return tuple((int(v) - (k - 1) * d + 2 * p - 1) // s + 1 for v in spatial_shape)
+
+
+def _mask_words(K: int) -> int:
+    return (K + 31) // 32
+
+
+# ------------------------------------------------------------------ KernelMap
+
+class KernelMap:
+    """Kernel map of one convolution geometry on one coordinate set.
+
+    ``nbr`` (K, N_out) int32, offset-major, -1 where no neighbour;
+    ``out_masks`` (N_out, W) row bitmasks of ``nbr`` (W = ceil(K/32));
+    ``invnbr`` (K, N_in) and ``in_masks`` (N_in, W) the transposed map, built
+    lazily by ``ensure_inverse`` for the input gradient.
+    ``nbr`` may be a strided view (``k_stride``/``r_stride``) of a caller's
+    (N_out, K) tensor.
+    """
+
+    def __init__(self, nbr: torch.Tensor, n_in: int, n_out: int, K: int, out_masks: Optional[torch.Tensor] = None,
+                 invnbr: Optional[torch.Tensor] = None, in_masks: Optional[torch.Tensor] = None,
+                 k_stride: Optional[int] = None, r_stride: Optional[int] = None):
+        self.nbr = nbr
+        self.n_in, self.n_out, self.K = int(n_in), int(n_out), int(K)
+        self.k_stride = n_out if k_stride is None else int(k_stride)
+        self.r_stride = 1 if r_stride is None else int(r_stride)
+        self.out_masks = out_masks
+        self.invnbr = invnbr
+        self.in_masks = in_masks
+
+    @classmethod
+    def from_neighbor_indices(cls, neighbor_indices: torch.Tensor, n_in: int) -> "KernelMap":
+        """Wrap a caller's (N_out, K) int32 map (any strides) without copying it."""
+        assert neighbor_indices.ndim == 2, "neighbor_indices must be (N_out, K)"
+        nbr = neighbor_indices
+        if nbr.dtype != torch.int32:
+            nbr = nbr.to(torch.int32)
+        n_out, K = nbr.shape
+        return cls(nbr, n_in, n_out, K, k_stride=nbr.stride(1), r_stride=nbr.stride(0))
+
+    @property
+    def mask_words(self) -> int:
+        return _mask_words(self.K)
+
+    @property
+    def neighbor_indices(self) -> torch.Tensor:
+        """(N_out, K) view, the reference's layout (``conv.py:12-75``)."""
+        return torch.as_strided(self.nbr, (self.n_out, self.K), (self.r_stride, self.k_stride))
+
+    def ensure_inverse(self) -> "KernelMap":
+        if self.invnbr is not None:
+            return self
+        dev = self.nbr.device
+        W = self.mask_words
+        self.invnbr = _lib.fill_(torch.empty((self.K, self.n_in), dtype=torch.int32, device=dev), -1)
+        self.in_masks = _lib.fill_(torch.empty((self.n_in, W), dtype=torch.int32, device=dev), 0)
+        need_out = self.out_masks is None
+        if need_out:
+            self.out_masks = torch.empty((self.n_out, W), dtype=torch.int32, device=dev)
+        _lib.call("st_kmap_invert", _lib.ptr(self.nbr), self.k_stride, self.r_stride, self.n_out, self.K, self.n_in,
+                  _lib.ptr(self.invnbr), _lib.ptr(self.in_masks), _lib.ptr(self.out_masks) if need_out else None,
+                  _lib.stream_of(dev))
+        return self
+
+    def ensure_out_masks(self) -> "KernelMap":
+        if self.out_masks is None:
+            self.ensure_inverse()
+        return self
+
+    def num_pairs(self) -> int:
+        """Number of valid (input, output, offset) triples (synchronises)."""
+        return int((self.neighbor_indices >= 0).sum().item())
+
+    def triples(self) -> torch.Tensor:
+        """(P, 3) int64 rows (in, out, k) sorted -- the canonical parity form."""
+        nb = self.neighbor_indices.long()
+        o, k = torch.nonzero(nb >= 0, as_tuple=True)
+        t = torch.stack([nb[o, k], o, k], dim=1)
+        key = (t[:, 0] * (self.n_out + 1) + t[:, 1]) * (self.K + 1) + t[:, 2]
+        return t[torch.argsort(key)]
+
+
+# ----------------------------------------------------------------- builders
+
+def _offsets_i32(kernel_offsets: torch.Tensor) -> torch.Tensor:
+    return kernel_offsets.to(torch.int32).contiguous()
+
+
+def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets: torch.Tensor, spatial_shape,
+                     stride: int, n_in: int) -> KernelMap:
+    """nbr[k, o] = row of out_o * stride - t_k (bounds [0, shape)), via ``st_kmap_query``."""
+    out_coords = out_coords.contiguous()
+    dev = out_coords.device
+    _lib.require_device(out_coords, "out_coords")
+    n_out = out_coords.shape[0]
+    K = kernel_offsets.shape[0]
+    if K > _lib.MAX_KVOL:
+        raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
+    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
+    masks = torch.empty((n_out, _mask_words(K)), dtype=torch.int32, device=dev)
+    sx, sy, sz = (int(v) for v in spatial_shape)
+    _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out,
+              _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, _lib.ptr(table.table_keys),
+              _lib.ptr(table.table_values), table.capacity, _lib.ptr(nbr), n_out, 1, _lib.ptr(masks),
+              _lib.stream_of(dev))
+    return KernelMap(nbr, n_in, n_out, K, out_masks=masks)
+
+
+class OutCoordTable:
+    """Dedup table of a strided / transposed build: output coordinate -> output row."""
+
+    def __init__(self, keys: torch.Tensor, slot_out: torch.Tensor):
+        self.table_keys = keys
+        self.table_values = slot_out
+
+    @property
+    def capacity(self) -> int:
+        return self.table_keys.shape[0]
+
+
+def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size: int, stride: int, dilation: int,
+                             padding: int, transposed: bool, in_table: Optional[HashTable] = None,
+                             with_map: bool = True):
+    """Strided / transposed output coordinates plus (optionally) their kernel map.
+
+    Returns (out_coords, new_spatial_shape, kernel_offsets, kmap_or_None, out_table).
+    One host synchronisation reads the output count.
+    """
+    dev = in_coords.device
+    _lib.require_device(in_coords, "coordinates")
+    in_coords = in_coords.contiguous()
+    n = in_coords.shape[0]
+    offsets = _target_offsets(kernel_size, dilation, padding, transposed, dev)
+    kernel_offsets = offsets.to(in_coords.dtype)
+    K = offsets.shape[0]
+    if K > _lib.MAX_KVOL:
+        raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
+    new_shape = out_spatial_shape(spatial_shape, kernel_size, stride, dilation, padding, transposed)
+    g = _lib.OutGeom()
+    g.K = K
+    g.transposed = 1 if transposed else 0
+    g.stride = int(stride)
+    for a in range(3):
+        g.in_shape[a] = int(spatial_shape[a])
+        g.out_shape[a] = int(new_shape[a])
+    dcap, nblocks = ctypes.c_int64(), ctypes.c_int64()
+    _lib.call("st_outcoords_sizes", n, ctypes.byref(g), int(kernel_size), int(dilation), ctypes.byref(dcap),
+              ctypes.byref(nblocks))
+    dcap, nblocks = dcap.value, nblocks.value
+    s = _lib.stream_of(dev)
+    dkeys = _lib.fill_(torch.empty((dcap,), dtype=torch.int64, device=dev), -1)
+    dvals = _lib.fill_(torch.empty((dcap,), dtype=torch.int32, device=dev), -1)
+    counts = torch.empty((nblocks + 1,), dtype=torch.int32, device=dev)
+    status = torch.zeros((_lib.STATUS_WORDS,), dtype=torch.int32, device=dev)
+    offs = _offsets_i32(offsets)
+    _lib.call("st_outcoords_plan", _lib.ptr(in_coords), _lib.coord_code(in_coords.dtype), n, _lib.ptr(offs),
+              ctypes.byref(g), _lib.ptr(dkeys), _lib.ptr(dvals), dcap, _lib.ptr(counts), nblocks, _lib.ptr(status), s)
+    tail = torch.stack([counts[nblocks], status[_lib.STATUS_OVERFLOW], status[_lib.STATUS_BAD_COORD]]).tolist()
+    n_out, overflow, bad = tail
+    if overflow:
+        raise RuntimeError(f"output-coordinate dedup table overflowed ({overflow} candidates dropped)")
+    if bad:
+        raise RuntimeError(f"{bad} output coordinates fall outside the packable range")
+    out_coords = torch.empty((n_out, 4), dtype=in_coords.dtype, device=dev)
+    slot_out = torch.empty((dcap,), dtype=torch.int32, device=dev)
+    kmap = None
+    nbr = invnbr = out_masks = in_masks = None
+    if with_map:
+        W = _mask_words(K)
+        nbr = _lib.fill_(torch.empty((K, n_out), dtype=torch.int32, device=dev), -1)
+        invnbr = _lib.fill_(torch.empty((K, n), dtype=torch.int32, device=dev), -1)
+        out_masks = _lib.fill_(torch.empty((n_out, W), dtype=torch.int32, device=dev), 0)
+        in_masks = _lib.fill_(torch.empty((n, W), dtype=torch.int32, device=dev), 0)
+    ik = iv = None
+    icap = 0
+    if in_table is not None:
+        ik, iv, icap = in_table.table_keys, in_table.table_values, in_table.capacity
+    _lib.call("st_outcoords_emit", _lib.ptr(in_coords), _lib.coord_code(in_coords.dtype), n, _lib.ptr(offs),
+              ctypes.byref(g), _lib.ptr(dkeys), _lib.ptr(dvals), _lib.ptr(slot_out), dcap, _lib.ptr(counts), nblocks,
+              _lib.ptr(ik), _lib.ptr(iv), icap, _lib.ptr(out_coords), n_out, _lib.ptr(nbr), _lib.ptr(invnbr),
+              _lib.ptr(out_masks), _lib.ptr(in_masks), s)
+    if with_map:
+        kmap = KernelMap(nbr, n, n_out, K, out_masks=out_masks, invnbr=invnbr, in_masks=in_masks)
+    return out_coords, torch.Size(new_shape), kernel_offsets, kmap, OutCoordTable(dkeys, slot_out)
+
+
+def build_out_coords(
+    in_coords: torch.Tensor,
+    spatial_shape,
+    kernel_size: int,
+    stride: int = 1,
+    dilation: int = 1,
+    padding: int = 1,
+    transposed: bool = False,
+    submanifold: bool = True,
+    chunk_size: int = None,
+):
+    """(out_coords, new_spatial_shape, kernel_offsets) of a sparse convolution (``kmap.py:447-495``).
+
+    Submanifold with stride 1 and centred padding returns the input
+    coordinates unchanged (``kmap.py:261-262``).  Otherwise candidates
+    ``in + t_k`` (or ``in * s + t_k`` transposed) pass the stride and range
+    filters and are deduplicated, in first-occurrence order of the
+    input-major / offset-minor candidate enumeration.  ``chunk_size`` is
+    accepted for compatibility; candidates are never materialised here.
+    """
+    offsets = _target_offsets(kernel_size, dilation, padding, transposed, in_coords.device).to(in_coords.dtype)
+    if submanifold and stride == 1 and ((kernel_size - 1) * dilation) // 2 == padding:
+        return in_coords, spatial_shape, offsets
+    out_coords, new_shape, kernel_offsets, _, _ = build_out_coords_and_map(
+        in_coords, spatial_shape, kernel_size, stride, dilation, padding, transposed, with_map=False)
+    return out_coords, new_shape, kernel_offsets

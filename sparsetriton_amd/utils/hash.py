@@ -1,0 +1,172 @@
+"""Coordinate hash table on the GPU, plus the coordinate packing helpers.
+
+Same public surface as the reference (``sparsetriton/utils/hash.py:22-580``):
+``HashTable(capacity=None, device="cpu", table_keys=None, table_values=None)``
+with ``insert``, ``query``, ``capacity``, ``device``, ``to``, ``cpu`` and the
+public ``table_keys`` / ``table_values`` arrays, and the ``flatten_coord`` /
+``unflatten_coord`` / ``hash_coords`` helpers.
+
+What differs, by design:
+
+* ``table_keys`` holds exact packed 64-bit coordinates (int64, the layout of
+  ``flatten_coord``), not a 31-bit hash of them.  The reference's stored key
+  (``hash_coords_kernel2``, ``hash.py:136-152``) aliases distinct coordinates,
+  so its table can return a wrong row; this one cannot.
+* Probing is bounded by the table size instead of 128 steps, so an insert
+  only fails when the table is full; failures are counted in ``status`` and
+  ``check()`` raises on them instead of dropping the coordinate.
+* Duplicate coordinates resolve to the lowest row index, on every run.
+
+Insert and query run as HIP kernels (``st_hash_insert`` / ``st_hash_query``);
+there is no CPU implementation of them.
+"""
+
+import torch
+
+from sparsetriton_amd import _lib
+from sparsetriton_amd.config import get_coords_dtype
+
+__all__ = ["HashTable", "flatten_coord", "hash_coords", "unflatten_coord"]
+
+
+def flatten_coord(coords: torch.Tensor) -> torch.Tensor:
+    """Pack (N, 4) rows (b, x, y, z) into int64 ``b<<48 | x<<32 | y<<16 | z`` (``hash.py:25-54``)."""
+    c = coords.to(torch.int64)
+    return (c[:, 0] << 48) | ((c[:, 1] & 0xFFFF) << 32) | ((c[:, 2] & 0xFFFF) << 16) | (c[:, 3] & 0xFFFF)
+
+
+def unflatten_coord(flat_coords: torch.Tensor) -> torch.Tensor:
+    """Inverse of ``flatten_coord``; returns (N, 4) in the configured coordinate dtype (``hash.py:57-83``)."""
+    f = flat_coords.to(torch.int64)
+    parts = [(f >> 48) & 0xFFFF, (f >> 32) & 0xFFFF, (f >> 16) & 0xFFFF, f & 0xFFFF]
+    return torch.stack(parts, dim=1).to(get_coords_dtype())
+
+
+def hash_coords(coords: torch.Tensor) -> torch.Tensor:
+    """Non-negative int32 spatial hash of (N, 4) coordinates.
+
+    The reference's host-side helper (``hash.py:86-113``): prime multipliers
+    per component, XOR-combined with int32 wrap-around, top bit cleared.  It
+    is not used by the table, which keys on exact coordinates.
+    """
+    c = coords.to(torch.int64)
+    h = (c[:, 1] * 73856093) ^ (c[:, 2] * 19349663) ^ (c[:, 3] * 83492791) ^ (c[:, 0] * 1000003)
+    return (h & 0x7FFFFFFF).to(torch.int32)
+
+
+class HashTable:
+    """Open-addressing table mapping packed coordinates to row indices.
+
+    ``table_keys`` (int64, -1 = empty) and ``table_values`` (int32, -1 =
+    none) have ``capacity`` slots each.  Build with ``insert`` (rows get their
+    index in the inserted tensor), look up with ``query`` (-1 when absent).
+    """
+
+    def __init__(self, capacity: int = None, device="cpu", table_keys: torch.Tensor = None,
+                 table_values: torch.Tensor = None):
+        assert capacity is not None or (table_keys is not None and table_values is not None), (
+            "Either capacity or both table_keys and table_values must be provided."
+        )
+        if table_keys is not None and table_values is not None:
+            assert table_keys.shape == table_values.shape, "table_keys and table_values must have the same shape."
+            self.table_keys, self.table_values = table_keys, table_values
+        else:
+            capacity = int(capacity)
+            assert capacity > 0, "capacity must be positive"
+            device = torch.device(device)
+            self.table_keys = torch.empty((capacity,), dtype=torch.int64, device=device)
+            self.table_values = torch.empty((capacity,), dtype=torch.int32, device=device)
+            self.clear()
+        self.status = None
+
+    # ------------------------------------------------------------ properties
+    @property
+    def device(self) -> torch.device:
+        return self.table_keys.device
+
+    @device.setter
+    def device(self, device) -> None:
+        self.table_keys = self.table_keys.to(device, non_blocking=True)
+        self.table_values = self.table_values.to(device, non_blocking=True)
+        if self.status is not None:
+            self.status = self.status.to(device, non_blocking=True)
+
+    def cpu(self) -> "HashTable":
+        self.device = torch.device("cpu")
+        return self
+
+    def to(self, device) -> "HashTable":
+        self.device = device
+        return self
+
+    @property
+    def capacity(self) -> int:
+        return self.table_keys.shape[0]
+
+    # ------------------------------------------------------------ operations
+    def clear(self) -> "HashTable":
+        """Mark every slot empty (keys and values all-ones, i.e. -1)."""
+        if self.table_keys.is_cuda:
+            _lib.fill_(self.table_keys, -1)
+            _lib.fill_(self.table_values, -1)
+        else:
+            self.table_keys.fill_(-1)
+            self.table_values.fill_(-1)
+        return self
+
+    def _status(self) -> torch.Tensor:
+        if self.status is None or self.status.device != self.device:
+            self.status = torch.zeros(_lib.STATUS_WORDS, dtype=torch.int32, device=self.device)
+        return self.status
+
+    def insert(self, keys: torch.Tensor, scale: int = 1) -> None:
+        """Insert (N, 4) coordinate rows; row i is stored with value i.
+
+        ``scale`` multiplies x, y, z before packing (the transposed-conv table
+        over ``coords * stride``).  Asynchronous: call ``check()`` to surface
+        a full table or unpackable coordinates.
+        """
+        keys = keys.contiguous()
+        n = keys.shape[0]
+        assert self.capacity >= n, (
+            "Hash table capacity should be at least twice the number of keys to ensure low collision rate."
+        )
+        assert keys.ndim == 2 and keys.shape[1] == 4, "keys must have shape (N, 4)"
+        _lib.require_device(self.table_keys, "HashTable")
+        if keys.device != self.device:
+            keys = keys.to(self.device)
+        assert self.table_keys.dtype == torch.int64 and self.table_values.dtype == torch.int32, (
+            "HashTable arrays must be int64 keys / int32 values"
+        )
+        _lib.call("st_hash_insert", _lib.ptr(keys), _lib.coord_code(keys.dtype), n, int(scale),
+                  _lib.ptr(self.table_keys), _lib.ptr(self.table_values), self.capacity,
+                  _lib.ptr(self._status()), _lib.stream_of(self.device))
+
+    def query(self, keys: torch.Tensor) -> torch.Tensor:
+        """Row index of each (N, 4) coordinate, or -1 when absent (int32, shape (N,))."""
+        keys = keys.contiguous()
+        n = keys.shape[0]
+        _lib.require_device(self.table_keys, "HashTable")
+        if keys.device != self.device:
+            keys = keys.to(self.device)
+        out = torch.empty((n,), dtype=torch.int32, device=self.device)
+        _lib.call("st_hash_query", _lib.ptr(keys), _lib.coord_code(keys.dtype), n, _lib.ptr(self.table_keys),
+                  _lib.ptr(self.table_values), self.capacity, _lib.ptr(out), _lib.stream_of(self.device))
+        return out
+
+    def counters(self) -> dict:
+        """Device failure counters (synchronises): overflow, bad_coord, duplicate."""
+        s = self._status().tolist()
+        return {"overflow": s[_lib.STATUS_OVERFLOW], "bad_coord": s[_lib.STATUS_BAD_COORD],
+                "duplicate": s[_lib.STATUS_DUPLICATE]}
+
+    def check(self) -> None:
+        """Raise if any insert found the table full or a coordinate unpackable."""
+        c = self.counters()
+        if c["overflow"]:
+            raise RuntimeError(f"HashTable: {c['overflow']} inserts found the table full (capacity {self.capacity})")
+        if c["bad_coord"]:
+            raise RuntimeError(
+                f"HashTable: {c['bad_coord']} coordinates outside the packable range "
+                "(batch in [0, 32767], x/y/z in [-32768, 32767])"
+            )

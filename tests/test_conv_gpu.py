@@ -1,0 +1,322 @@
+"""Sparse convolution forward / input gradient / weight gradient on the GPU.
+
+Tolerances (relative Frobenius error vs float64, per output tensor):
+fp32 2e-3, bf16 2e-2, fp16 1e-2 -- the north-star bounds; the fp32 MFMA path
+is IEEE fp32 and lands far inside.  The reference's own test tolerances
+(atol = rtol = 1e-3 forward, 5e-2 gradients, fp16; tests/test_sparse_conv.py)
+are applied on its parametrisations against dense convolution.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from sparsetriton_amd import SparseTensor, randn, workloads
+from sparsetriton_amd.config import ConvAlgo, set_conv_algo
+from sparsetriton_amd.nn import SparseConv3D, SparseConvTransposed3D, SubMConv3D
+from sparsetriton_amd.nn.functional import sparse_conv3d
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+TOL = {torch.float32: 2e-3, torch.bfloat16: 2e-2, torch.float16: 1e-2}
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _rand_coords(rng, n, S, B=2):
+    lin = np.sort(rng.choice(B * S ** 3, n, replace=False))
+    return np.stack([lin // S ** 3, (lin // S ** 2) % S, (lin // S) % S, lin % S], 1).astype(np.int32)
+
+
+def _run(device, c, shape, X, W, dY, k, s, p, d, tr, subm, dtype, algo):
+    set_conv_algo(algo)
+    feats = torch.as_tensor(X, device=device).to(dtype).requires_grad_(True)
+    w = torch.as_tensor(W, device=device).to(dtype).requires_grad_(True)
+    sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=shape)
+    out = sparse_conv3d(sp, w, k, stride=s, padding=p, dilation=d, transposed=tr, submanifold=subm)
+    out.F.backward(torch.as_tensor(dY, device=device).to(dtype))
+    return out, feats.grad, w.grad
+
+
+def _oracle(c, oc, shape, X, W, dY, k, s, p, d, tr):
+    off = O.target_offsets(k, d, p, tr)
+    if tr:
+        nbr = O.exact_kmap(c, oc, off, 1, tuple(v * s for v in shape), in_scale=s)
+    else:
+        nbr = O.exact_kmap(c, oc, off, s, shape)
+    return O.fwd_f64(X, W, nbr), O.dgrad_f64(dY, W, nbr, c.shape[0]), O.wgrad_f64(X, dY, nbr, k ** 3)
+
+
+# ------------------------------------------------------------- golden cases
+
+def _golden():
+    z = np.load(GOLD / "conv_cases.npz")
+    return z, sorted({k.split("/")[0] for k in z.files})
+
+
+@pytest.mark.parametrize("algo", list(ConvAlgo))
+@pytest.mark.parametrize("name", _golden()[1])
+def test_golden_dense_cases(device, name, algo):
+    z, _ = _golden()
+    g = lambda key: z[f"{name}/{key}"]
+    C_in, C_out, k, s, p, d, tr, subm = (int(v) for v in g("meta"))
+    c, X, W = g("coords"), g("feats"), g("weight")
+    shape = tuple(int(v) for v in g("spatial_shape"))
+    gold_rows = {tuple(r): i for i, r in enumerate(g("out_coords").tolist())}
+    # the GPU output order is its own (first occurrence); dY is given per golden row
+    set_conv_algo(algo)
+    feats = torch.as_tensor(X, device=device).requires_grad_(True)
+    w = torch.as_tensor(W, device=device).requires_grad_(True)
+    sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=shape)
+    out = sparse_conv3d(sp, w, k, stride=s, padding=p, dilation=d, transposed=bool(tr), submanifold=bool(subm))
+    oc = out.C.cpu().numpy()
+    assert oc.shape[0] == len(gold_rows)
+    perm = np.array([gold_rows[tuple(r)] for r in oc.tolist()])
+    assert rel(out.F.detach().cpu(), g("out")[perm]) < 1e-5
+    out.F.backward(torch.as_tensor(g("dY")[perm], device=device))
+    assert rel(feats.grad.cpu(), g("dX")) < 1e-5
+    assert rel(w.grad.cpu(), g("dW")) < 1e-5
+    if subm:
+        assert out.C is sp.C and out._cache is sp._cache
+
+
+# --------------------------------------------------- dtype / channel matrix
+
+CHANNELS = [(4, 8), (16, 32), (64, 64), (64, 128), (128, 64), (3, 5), (20, 36), (128, 128), (256, 32)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cin,cout", CHANNELS)
+def test_subm_dtypes_channels(device, dtype, cin, cout):
+    rng = np.random.default_rng(cin * 1000 + cout)
+    c = _rand_coords(rng, 4000, 20)
+    X = rng.standard_normal((4000, cin)).astype(np.float32)
+    W = (rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cin)).astype(np.float32)
+    dY = rng.standard_normal((4000, cout)).astype(np.float32)
+    # quantise inputs to the compute dtype so the oracle sees the same operands
+    Xq = torch.as_tensor(X).to(dtype).float().numpy()
+    Wq = torch.as_tensor(W).to(dtype).float().numpy()
+    dYq = torch.as_tensor(dY).to(dtype).float().numpy()
+    out, dX, dW = _run(device, c, (20, 20, 20), Xq, Wq, dYq, 3, 1, 1, 1, False, True, dtype,
+                       ConvAlgo.PrecomputedNeighborGEMM)
+    y, gx, gw = _oracle(c, c, (20, 20, 20), Xq, Wq, dYq, 3, 1, 1, 1, False)
+    tol = TOL[dtype]
+    assert out.F.dtype == dtype and dX.dtype == dtype and dW.dtype == dtype
+    assert rel(out.F.detach().float().cpu(), y) < tol
+    assert rel(dX.float().cpu(), gx) < tol
+    assert rel(dW.float().cpu(), gw) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("k,s,p,d,tr", [(3, 2, 1, 1, False), (3, 2, 1, 1, True), (5, 1, 2, 1, False),
+                                        (3, 1, 1, 1, True), (3, 2, 1, 2, False)])
+def test_general_geometries(device, dtype, k, s, p, d, tr):
+    rng = np.random.default_rng(k + 10 * s + 100 * p + tr)
+    shape = (16, 16, 16)
+    c = _rand_coords(rng, 2500, 16)
+    X = torch.as_tensor(rng.standard_normal((2500, 32)).astype(np.float32)).to(dtype).float().numpy()
+    W = torch.as_tensor((rng.standard_normal((k ** 3, 32, 48)) / np.sqrt(32 * k ** 3)).astype(np.float32)).to(
+        dtype).float().numpy()
+    for algo in ConvAlgo:
+        set_conv_algo(algo)
+        feats = torch.as_tensor(X, device=device).to(dtype).requires_grad_(True)
+        w = torch.as_tensor(W, device=device).to(dtype).requires_grad_(True)
+        sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=shape)
+        out = sparse_conv3d(sp, w, k, stride=s, padding=p, dilation=d, transposed=tr, submanifold=False)
+        oc = out.C.cpu().numpy()
+        dY = torch.as_tensor(rng.standard_normal((oc.shape[0], 48)).astype(np.float32)).to(dtype).float().numpy()
+        out.F.backward(torch.as_tensor(dY, device=device).to(dtype))
+        y, gx, gw = _oracle(c, oc, shape, X, W, dY, k, s, p, d, tr)
+        tol = TOL[dtype]
+        assert rel(out.F.detach().float().cpu(), y) < tol, algo
+        assert rel(feats.grad.float().cpu(), gx) < tol, algo
+        assert rel(w.grad.float().cpu(), gw) < tol, algo
+
+
+def test_mixed_precision_weight_grad_dtype(device):
+    # bf16 activations with fp32 master weights: dW comes back in fp32
+    rng = np.random.default_rng(2)
+    c = _rand_coords(rng, 1000, 12)
+    feats = torch.randn(1000, 16, device=device, dtype=torch.bfloat16, requires_grad=True)
+    conv = SubMConv3D(16, 16, 3).to(device)
+    out = conv(SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=(12, 12, 12)))
+    out.F.float().sum().backward()
+    assert out.F.dtype == torch.bfloat16 and conv.weight.grad.dtype == torch.float32
+    assert feats.grad.dtype == torch.bfloat16 and conv.bias.grad is not None
+
+
+# ---------------------------------------------- algorithms / determinism
+
+def test_hashfly_equals_precomputed_bitwise(device):
+    rng = np.random.default_rng(21)
+    c = _rand_coords(rng, 6000, 24)
+    X = rng.standard_normal((6000, 32)).astype(np.float32)
+    W = (rng.standard_normal((27, 32, 32)) / 30).astype(np.float32)
+    dY = rng.standard_normal((6000, 32)).astype(np.float32)
+    res = [_run(device, c, (24, 24, 24), X, W, dY, 3, 1, 1, 1, False, True, torch.float32, a) for a in ConvAlgo]
+    for a, b in zip(res[0], res[1]):
+        a = a.F if isinstance(a, SparseTensor) else a
+        b = b.F if isinstance(b, SparseTensor) else b
+        assert torch.equal(a, b)
+
+
+def test_deterministic(device):
+    rng = np.random.default_rng(22)
+    c = _rand_coords(rng, 8000, 24)
+    X = rng.standard_normal((8000, 64)).astype(np.float32)
+    W = (rng.standard_normal((27, 64, 64)) / 40).astype(np.float32)
+    dY = rng.standard_normal((8000, 64)).astype(np.float32)
+    r1 = _run(device, c, (24, 24, 24), X, W, dY, 3, 1, 1, 1, False, True, torch.bfloat16,
+              ConvAlgo.PrecomputedNeighborGEMM)
+    r2 = _run(device, c, (24, 24, 24), X, W, dY, 3, 1, 1, 1, False, True, torch.bfloat16,
+              ConvAlgo.PrecomputedNeighborGEMM)
+    assert torch.equal(r1[0].F, r2[0].F) and torch.equal(r1[1], r2[1]) and torch.equal(r1[2], r2[2])
+
+
+def test_plain_neighbor_indices_tensor(device):
+    # ConvPrecomputedNeighborGEMM.apply with the reference's (N_out, K) tensor form
+    from sparsetriton_amd.nn.functional.conv.funcs import ConvPrecomputedNeighborGEMM
+    rng = np.random.default_rng(23)
+    c = _rand_coords(rng, 3000, 20)
+    nbr = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, (20, 20, 20))
+    X = rng.standard_normal((3000, 16)).astype(np.float32)
+    W = (rng.standard_normal((27, 16, 24)) / 20).astype(np.float32)
+    dY = rng.standard_normal((3000, 24)).astype(np.float32)
+    feats = torch.as_tensor(X, device=device).requires_grad_(True)
+    w = torch.as_tensor(W, device=device).requires_grad_(True)
+    out = ConvPrecomputedNeighborGEMM.apply(feats, w, torch.as_tensor(nbr, device=device))
+    out.backward(torch.as_tensor(dY, device=device))
+    assert rel(out.detach().cpu(), O.fwd_f64(X, W, nbr)) < 1e-5
+    assert rel(feats.grad.cpu(), O.dgrad_f64(dY, W, nbr, 3000)) < 1e-5
+    assert rel(w.grad.cpu(), O.wgrad_f64(X, dY, nbr, 27)) < 1e-5
+
+
+# --------------------------------------------- reference test parametrisations
+
+@pytest.mark.parametrize("C_in,C_out,k,s,p,d", [(8, 16, 3, 1, 1, 1), (4, 8, 3, 2, 1, 1), (16, 16, 5, 2, 2, 1),
+                                                (16, 16, 5, 1, 2, 1)])
+def test_reference_forward_vs_dense(device, C_in, C_out, k, s, p, d):
+    torch.manual_seed(0)
+    sp = randn((10, 10, 10), batch_size=1, channels=C_in, nnz=27, device=device).half()
+    weight = torch.rand(k ** 3, C_in, C_out, device=device, dtype=torch.float16)
+    st_out = sparse_conv3d(sp, weight, kernel_size=k, stride=s, padding=p, dilation=d, submanifold=False).float()
+    w_t = weight.view(k, k, k, C_in, C_out).permute(4, 3, 0, 1, 2).contiguous().float().cpu()
+    dense_in = sp.dense().permute(0, 4, 1, 2, 3).contiguous().float().cpu()
+    dense_out = torch.nn.functional.conv3d(dense_in, w_t, stride=s, padding=p, dilation=d)
+    st_dense = st_out.dense().cpu()
+    torch.testing.assert_close(st_dense, dense_out.permute(0, 2, 3, 4, 1).contiguous(), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("C_in,C_out,k,s,p,d", [(16, 16, 3, 1, 1, 1), (32, 32, 3, 1, 1, 1), (32, 32, 5, 1, 2, 1),
+                                                (4, 8, 3, 2, 1, 1), (8, 16, 3, 2, 1, 1), (8, 16, 3, 4, 1, 1)])
+def test_reference_transposed_vs_dense(device, C_in, C_out, k, s, p, d):
+    torch.manual_seed(1)
+    sp = randn((10, 10, 10), batch_size=1, channels=C_in, nnz=27, device=device).half()
+    weight = torch.rand(k ** 3, C_in, C_out, device=device, dtype=torch.float16) / k ** 3
+    st_out = sparse_conv3d(sp, weight, kernel_size=k, stride=s, padding=p, dilation=d, submanifold=False,
+                           transposed=True).float()
+    w_t = weight.view(k, k, k, C_in, C_out).permute(3, 4, 0, 1, 2).contiguous().float().cpu()
+    dense_in = sp.dense().permute(0, 4, 1, 2, 3).contiguous().float().cpu()
+    dense_out = torch.nn.functional.conv_transpose3d(dense_in, w_t, stride=s, padding=p, dilation=d)
+    st_dense = st_out.dense().cpu()
+    torch.testing.assert_close(st_dense, dense_out.permute(0, 2, 3, 4, 1).contiguous(), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("C_in,C_out,k,s,p,d", [(16, 16, 3, 1, 2, 1), (32, 32, 3, 1, 0, 1), (32, 32, 5, 1, 2, 1),
+                                                (16, 16, 3, 2, 1, 1), (16, 16, 3, 2, 1, 2)])
+def test_reference_gradients_vs_dense(device, C_in, C_out, k, s, p, d):
+    torch.manual_seed(2)
+    sp_in = randn((64, 64, 64), batch_size=1, channels=C_in, nnz=32 ** 3, device=device)
+    feats = sp_in.F.half().detach().requires_grad_(True)
+    sp_in.F = feats
+    weight = (torch.randn(k ** 3, C_in, C_out, device=device, dtype=torch.float16) / k ** 3).requires_grad_(True)
+    st_out = sparse_conv3d(sp_in, weight, kernel_size=k, stride=s, padding=p, dilation=d, submanifold=False)
+    st_out.dense().float().abs().mean().backward()
+    w_t = weight.detach().float().view(k, k, k, C_in, C_out).permute(4, 3, 0, 1, 2).contiguous().requires_grad_(True)
+    dense_in = sp_in.dense().permute(0, 4, 1, 2, 3).contiguous().detach().float().requires_grad_(True)
+    dense_out = torch.nn.functional.conv3d(dense_in, w_t, stride=s, padding=p, dilation=d)
+    dense_out.permute(0, 2, 3, 4, 1).contiguous().abs().mean().backward()
+    coords = sp_in.coords.long()
+    g_in = dense_in.grad.permute(0, 2, 3, 4, 1)[coords[:, 0], coords[:, 1], coords[:, 2], coords[:, 3]]
+    g_w = w_t.grad.permute(2, 3, 4, 1, 0).reshape(k ** 3, C_in, C_out)
+    torch.testing.assert_close(weight.grad.float(), g_w, atol=5e-2, rtol=5e-2)
+    torch.testing.assert_close(feats.grad.float(), g_in, atol=5e-2, rtol=5e-2)
+
+
+def test_reference_submanifold_vs_dense(device):
+    torch.manual_seed(3)
+    for C_in, C_out, ks, pad, nnz in [(8, 16, 3, 1, 100), (8, 16, 5, 2, 120)]:
+        sp_in = randn((10, 10, 10), batch_size=1, channels=C_in, nnz=nnz, device=device).half()
+        weight = torch.rand(ks ** 3, C_in, C_out, device=device, dtype=torch.float16)
+        st_out = sparse_conv3d(sp_in, weight, kernel_size=ks, stride=1, padding=pad, dilation=1, submanifold=True)
+        assert torch.equal(st_out.coords, sp_in.coords) and st_out.F.shape == (nnz, C_out)
+        w_t = weight.view(ks, ks, ks, C_in, C_out).permute(4, 3, 0, 1, 2).contiguous().float().cpu()
+        dense = torch.nn.functional.conv3d(sp_in.dense().permute(0, 4, 1, 2, 3).float().cpu(), w_t, padding=pad)
+        c = st_out.coords.long().cpu()
+        ref = dense.permute(0, 2, 3, 4, 1)[c[:, 0], c[:, 1], c[:, 2], c[:, 3]]
+        torch.testing.assert_close(st_out.F.float().cpu(), ref, atol=1e-3, rtol=1e-3)
+    # non-centre padding is forced to centre for submanifold (conv.py:120-121)
+    out = sparse_conv3d(sp_in, torch.rand(27, 8, 16, device=device, dtype=torch.float16), 3, padding=0,
+                        submanifold=True)
+    assert torch.isfinite(out.F).all() and out.F.shape[1] == 16
+
+
+# ------------------------------------------------------------ modules / cache
+
+def test_module_stack_shares_kernel_map(device):
+    sp = randn((32, 32, 32), batch_size=2, nnz=5000, channels=16, device=device)
+    l1, l2 = SubMConv3D(16, 32, 3).to(device), SubMConv3D(32, 32, 3).to(device)
+    y1 = l1(sp)
+    y2 = l2(y1)
+    assert y1._cache is sp._cache and y2._cache is sp._cache
+    assert len(sp._cache.neighbor_indices) == 1 and sp._cache.hashtable is not None
+    down = SparseConv3D(32, 64, 3, stride=2, padding=1).to(device)(y2)
+    up = SparseConvTransposed3D(64, 32, 3, stride=2, padding=1).to(device)(down)
+    assert down.F.shape[1] == 64 and up.F.shape[1] == 32
+    (up.F.sum() + y2.F.sum()).backward()
+    assert torch.isfinite(l1.weight.grad).all() and l1.bias.grad.shape == (32,)
+
+
+def test_empty_tensor(device):
+    sp = SparseTensor(torch.empty((0, 8), device=device), torch.empty((0, 4), dtype=torch.int16, device=device),
+                      spatial_shape=(8, 8, 8), batch_size=1)
+    for conv in (SubMConv3D(8, 4, 3), SparseConv3D(8, 4, 3, stride=2, padding=1),
+                 SparseConvTransposed3D(8, 4, 3, stride=2)):
+        out = conv.to(device)(sp)
+        assert out.F.shape == (0, 4)
+
+
+# --------------------------------------------------- BASELINE-size properties
+
+def test_config2_full_size_properties(device):
+    """SubM 64->64 on the full config-2 set: exact rows on a sample, adjoint identities overall."""
+    c, shape = workloads.config2()
+    n = c.shape[0]
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal((n, 64)).astype(np.float32)
+    W = (rng.standard_normal((27, 64, 64)) / np.sqrt(27 * 64)).astype(np.float32)
+    dY = rng.standard_normal((n, 64)).astype(np.float32)
+    for dtype, tol in ((torch.float32, 2e-3), (torch.bfloat16, 2e-2)):
+        Xq = torch.as_tensor(X).to(dtype)
+        Wq = torch.as_tensor(W).to(dtype)
+        dYq = torch.as_tensor(dY).to(dtype)
+        out, dX, dW = _run(device, c, shape, Xq.float().numpy(), Wq.float().numpy(), dYq.float().numpy(), 3, 1, 1,
+                           1, False, True, dtype, ConvAlgo.PrecomputedNeighborGEMM)
+        y = out.F.detach().double().cpu()
+        # adjoint identities: <dY, Y> = <dX, X> = <dW, W> (linearity in X and in W)
+        s_y = float((dYq.double() * y).sum())
+        s_x = float((dX.double().cpu() * Xq.double()).sum())
+        s_w = float((dW.double().cpu() * Wq.double()).sum())
+        assert abs(s_x - s_y) <= tol * abs(s_y) and abs(s_w - s_y) <= tol * abs(s_y)
+        # exact rows on a random sample
+        rows = rng.choice(n, 3000, replace=False)
+        nbr = O.exact_kmap(c, c[rows], O.target_offsets(3, 1, 1, False), 1, shape)
+        y_ref = O.fwd_f64(Xq.float().numpy(), Wq.float().numpy(), nbr)
+        assert rel(y[rows].numpy(), y_ref) < tol

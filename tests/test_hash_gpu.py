@@ -1,0 +1,113 @@
+"""GPU coordinate hash table vs exact lookups (bit-exact), including the reference's KATs."""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from sparsetriton_amd.utils.hash import HashTable
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def test_reference_kats(device):
+    kats = json.loads((GOLD / "reference_kats.json").read_text())["hash_table"]["cases"]
+    for case in kats:
+        t = HashTable(capacity=case["capacity"], device=device)
+        assert t.capacity == case["capacity"]
+        assert torch.all(t.table_keys == -1) and torch.all(t.table_values == -1)
+        t.insert(torch.tensor(case["insert"], dtype=torch.int32, device=device))
+        assert torch.any(t.table_keys != -1)
+        assert t.query(torch.tensor(case["query"], dtype=torch.int32, device=device)).tolist() == case["expect"]
+        t.check()
+
+
+@pytest.mark.parametrize("dtype", [torch.int16, torch.int32, torch.int64])
+def test_random_insert_query_exact(device, dtype):
+    rng = np.random.default_rng(11)
+    n = 200_000
+    lin = rng.choice(4 * 512 * 512 * 64, n, replace=False)
+    c = np.stack([lin // (512 * 512 * 64), (lin // (512 * 64)) % 512, (lin // 64) % 512, lin % 64], 1)
+    miss = np.stack([rng.integers(0, 4, n), rng.integers(0, 512, n), rng.integers(0, 512, n),
+                     rng.integers(64, 128, n)], 1)  # z >= 64: never inserted
+    q = np.concatenate([c, miss])
+    perm = rng.permutation(q.shape[0])
+    q = q[perm]
+    expect = np.concatenate([np.arange(n), np.full(n, -1)])[perm]
+    t = HashTable(capacity=2 * n, device=device)
+    t.insert(torch.as_tensor(c, dtype=dtype, device=device))
+    t.check()
+    got = t.query(torch.as_tensor(q, dtype=dtype, device=device)).cpu().numpy()
+    assert (got == expect).all()
+    # exactly n occupied slots, each key the packed coordinate of its value's row
+    keys = t.table_keys.cpu().numpy()
+    vals = t.table_values.cpu().numpy()
+    occ = keys != -1
+    assert occ.sum() == n
+    packed = (c[:, 0].astype(np.int64) << 48) | (c[:, 1].astype(np.int64) << 32) | (c[:, 2] << 16) | c[:, 3]
+    assert (keys[occ] == packed[vals[occ]]).all()
+
+
+def test_full_table_and_overflow(device):
+    c = torch.tensor([[0, i, 0, 0] for i in range(15)], dtype=torch.int32, device=device)
+    t = HashTable(capacity=10, device=device)
+    t.insert(c[:10])  # exactly full: no overflow
+    assert t.counters()["overflow"] == 0
+    assert t.query(c[:10]).tolist() == list(range(10))
+    assert t.query(c[10:]).tolist() == [-1] * 5  # full sweep of a full table terminates
+    t.insert(c[10:])
+    assert t.counters()["overflow"] == 5
+    with pytest.raises(RuntimeError, match="full"):
+        t.check()
+
+
+def test_capacity_assert():
+    t = HashTable(capacity=10, device="cpu")
+    with pytest.raises(AssertionError, match="capacity should be at least"):
+        t.insert(torch.randint(0, 10, (20, 4), dtype=torch.int32))
+
+
+def test_duplicates_resolve_to_lowest_row(device):
+    c = torch.tensor([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1], [0, 1, 1, 1], [0, 2, 2, 2]], dtype=torch.int32,
+                     device=device)
+    for _ in range(3):
+        t = HashTable(capacity=64, device=device)
+        t.insert(c)
+        assert t.query(c).tolist() == [0, 1, 0, 0, 1]
+        assert t.counters()["duplicate"] == 3
+
+
+def test_unpackable_coordinates(device):
+    c = torch.tensor([[0, 40000, 0, 0], [-1, 0, 0, 0], [0, 5, 5, 5]], dtype=torch.int32, device=device)
+    t = HashTable(capacity=16, device=device)
+    t.insert(c)
+    assert t.counters()["bad_coord"] == 2
+    with pytest.raises(RuntimeError, match="packable"):
+        t.check()
+    assert t.query(c).tolist() == [-1, -1, 2]
+
+
+def test_reference_alias_pair_is_not_confused(device):
+    # key2 of these two coordinates collides in the reference's table (hash.py:136-152);
+    # exact keys keep them apart even when both probe chains start on the same slot.
+    kats = json.loads((GOLD / "reference_kats.json").read_text())["reference_hash_alias"]
+    t = HashTable(capacity=5, device=device)
+    t.insert(torch.tensor([kats["a"]], dtype=torch.int32, device=device))
+    assert t.query(torch.tensor([kats["a"], kats["b"]], dtype=torch.int32, device=device)).tolist() == [0, -1]
+
+
+def test_scaled_insert(device):
+    c = torch.tensor([[0, 1, 2, 3], [1, 4, 5, 6]], dtype=torch.int16, device=device)
+    t = HashTable(capacity=16, device=device)
+    t.insert(c, scale=2)
+    q = torch.tensor([[0, 2, 4, 6], [1, 8, 10, 12], [0, 1, 2, 3]], dtype=torch.int16, device=device)
+    assert t.query(q).tolist() == [0, 1, -1]
+
+
+def test_empty(device):
+    t = HashTable(capacity=4, device=device)
+    t.insert(torch.empty((0, 4), dtype=torch.int16, device=device))
+    assert t.query(torch.empty((0, 4), dtype=torch.int16, device=device)).shape == (0,)

@@ -1,0 +1,216 @@
+"""Kernel maps and output coordinates on the GPU vs the exact oracle (bit-exact).
+
+Submanifold maps are compared entry by entry; strided / transposed output
+coordinates are compared in order (first occurrence in the input-major /
+offset-minor candidate enumeration) and their maps entry by entry, which
+implies equality of the canonical sorted (in, out, k) triples.  The
+transposed map is checked for consistency with the forward map, and the row
+masks against the map.  Full-size BASELINE coordinate sets are included.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from sparsetriton_amd import SparseTensor, workloads
+from sparsetriton_amd.nn.functional.conv.conv import _input_table, compute_neighbor_indices
+from sparsetriton_amd.nn.functional.conv.kmap import (
+    _target_offsets,
+    build_out_coords,
+    build_out_coords_and_map,
+    query_kernel_map,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_coords(rng, n, S, B=2):
+    lin = np.sort(rng.choice(B * S ** 3, n, replace=False))
+    return np.stack([lin // S ** 3, (lin // S ** 2) % S, (lin // S) % S, lin % S], 1).astype(np.int32)
+
+
+def _check_masks(kmap):
+    nbr = kmap.nbr.cpu().numpy()
+    K = kmap.K
+    bits = (nbr >= 0).astype(np.uint64)
+    expect = np.zeros((kmap.n_out,), dtype=np.uint64)
+    for k in range(min(K, 32)):
+        expect |= bits[k] << np.uint64(k)
+    got = kmap.out_masks.cpu().numpy()[:, 0].astype(np.uint32).astype(np.uint64)
+    assert (got == expect).all()
+
+
+def _check_inverse(kmap):
+    kmap.ensure_inverse()
+    nbr = kmap.nbr.cpu().numpy()
+    inv = kmap.invnbr.cpu().numpy()
+    K = kmap.K
+    for k in range(K):
+        o = np.nonzero(nbr[k] >= 0)[0]
+        assert (inv[k, nbr[k, o]] == o).all()
+        assert (inv[k] >= 0).sum() == o.shape[0]
+    in_bits = (inv >= 0)
+    got = kmap.in_masks.cpu().numpy()[:, 0].astype(np.uint32)
+    expect = np.zeros(kmap.n_in, dtype=np.uint64)
+    for k in range(min(K, 32)):
+        expect |= in_bits[k].astype(np.uint64) << np.uint64(k)
+    assert (got.astype(np.uint64) == expect).all()
+
+
+def _subm(device, c, shape, k=3, d=1, dtype=torch.int16):
+    coords = torch.as_tensor(c, dtype=dtype, device=device)
+    sp = SparseTensor(torch.zeros((c.shape[0], 1), device=device), coords, spatial_shape=shape)
+    table = _input_table(sp, 1)
+    offs = _target_offsets(k, d, (k - 1) * d // 2, False, device)
+    return query_kernel_map(table, sp.C, offs, shape, 1, c.shape[0])
+
+
+@pytest.mark.parametrize("k,d", [(3, 1), (5, 1), (3, 2)])
+def test_subm_kmap_exact(device, k, d):
+    rng = np.random.default_rng(k + d)
+    c = _rand_coords(rng, 3000, 24)
+    kmap = _subm(device, c, (24, 24, 24), k, d)
+    off = O.target_offsets(k, d, (k - 1) * d // 2, False)
+    expect = O.exact_kmap(c, c, off, 1, (24, 24, 24))
+    assert (kmap.neighbor_indices.cpu().numpy() == expect).all()
+    if k ** 3 <= 32:
+        _check_masks(kmap)
+        _check_inverse(kmap)
+
+
+def test_subm_kmap_out_of_bounds_rows(device):
+    rng = np.random.default_rng(5)
+    c = _rand_coords(rng, 2000, 20)
+    shape = (15, 18, 20)  # some coordinates lie outside: their neighbours are dropped, as in conv.py:55-59
+    kmap = _subm(device, c, shape)
+    expect = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, shape)
+    assert (kmap.neighbor_indices.cpu().numpy() == expect).all()
+    _check_inverse(kmap)
+
+
+def test_compute_neighbor_indices_api(device):
+    rng = np.random.default_rng(6)
+    c = _rand_coords(rng, 1000, 16)
+    coords = torch.as_tensor(c, dtype=torch.int32, device=device)
+    sp = SparseTensor(torch.zeros((1000, 1), device=device), coords, spatial_shape=(16, 16, 16))
+    table = _input_table(sp, 1)
+    offs = _target_offsets(3, 1, 1, False, device).to(sp.C.dtype)
+    nbr = compute_neighbor_indices(table, sp.C, offs, (16, 16, 16), 1)
+    assert nbr.shape == (1000, 27) and nbr.dtype == torch.int32
+    assert (nbr.cpu().numpy() == O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, (16, 16, 16))).all()
+
+
+GEOMS = [
+    # k, s, p, d, transposed
+    (3, 2, 1, 1, False),
+    (5, 2, 2, 1, False),
+    (3, 2, 1, 2, False),
+    (3, 1, 0, 1, False),
+    (3, 3, 1, 1, False),
+    (3, 2, 1, 1, True),
+    (3, 1, 1, 1, True),
+    (3, 4, 1, 1, True),
+    (5, 1, 2, 1, True),
+]
+
+
+def _strided(device, c, shape, k, s, p, d, tr, dtype=torch.int16):
+    coords = torch.as_tensor(c, dtype=dtype, device=device)
+    sp = SparseTensor(torch.zeros((c.shape[0], 1), device=device), coords, spatial_shape=shape)
+    scale = s if (tr and s > 1) else 1
+    table = _input_table(sp, scale)
+    return build_out_coords_and_map(sp.C, shape, k, s, d, p, tr, in_table=table, with_map=True)
+
+
+def _oracle_strided(c, shape, k, s, p, d, tr):
+    off = O.target_offsets(k, d, p, tr)
+    ns = O.out_shape(shape, k, s, d, p, tr)
+    oc = O.out_coords(c, off, s, tr, ns)
+    if tr:
+        nbr = O.exact_kmap(c, oc, off, 1, tuple(v * s for v in shape), in_scale=s)
+    else:
+        nbr = O.exact_kmap(c, oc, off, s, shape)
+    return oc, ns, nbr
+
+
+@pytest.mark.parametrize("k,s,p,d,tr", GEOMS)
+def test_strided_transposed_exact(device, k, s, p, d, tr):
+    rng = np.random.default_rng(100 * k + 10 * s + p + d + tr)
+    shape = (20, 20, 20)
+    c = _rand_coords(rng, 1500, 20)
+    out_coords, ns, offsets, kmap, _ = _strided(device, c, shape, k, s, p, d, tr)
+    oc, ns_o, nbr = _oracle_strided(c, shape, k, s, p, d, tr)
+    assert tuple(ns) == ns_o
+    assert out_coords.dtype == torch.int16
+    assert (out_coords.cpu().numpy() == oc).all()
+    assert (kmap.neighbor_indices.cpu().numpy() == nbr).all()
+    assert (offsets.cpu().numpy() == O.target_offsets(k, d, p, tr)).all()
+    if k ** 3 <= 32:
+        _check_masks(kmap)
+        inv = kmap.invnbr.clone()
+        kmap.invnbr = None
+        _check_inverse(kmap)  # invert kernel == map emitted with the coordinates
+        assert torch.equal(kmap.invnbr, inv)
+
+
+def test_build_out_coords_api(device):
+    rng = np.random.default_rng(9)
+    c = torch.as_tensor(_rand_coords(rng, 500, 12), dtype=torch.int16, device=device)
+    oc, ns, offs = build_out_coords(c, (12, 12, 12), 3, stride=2, padding=1, submanifold=False)
+    expect = O.out_coords(c.cpu().numpy(), O.target_offsets(3, 1, 1, False), 2, False, (6, 6, 6))
+    assert tuple(ns) == (6, 6, 6) and (oc.cpu().numpy() == expect).all()
+    # submanifold short-circuit and the reference docstring KAT (kmap.py:477-484)
+    one = torch.tensor([[0, 1, 1, 1]], dtype=torch.int16, device=device)
+    oc1, ns1, _ = build_out_coords(one, (8, 8, 8), 3, stride=1, padding=1)
+    assert oc1 is one and oc1.shape[1] == 4
+
+
+def test_duplicate_inputs_use_table_row(device):
+    c = np.array([[0, 2, 2, 2], [0, 3, 2, 2], [0, 2, 2, 2], [0, 5, 5, 5]], dtype=np.int32)
+    out_coords, ns, _, kmap, _ = _strided(device, c, (8, 8, 8), 3, 2, 1, 1, False)
+    oc, _, nbr = _oracle_strided(c, (8, 8, 8), 3, 2, 1, 1, False)  # oracle keeps the lowest row per coordinate
+    assert (out_coords.cpu().numpy() == oc).all()
+    assert (kmap.neighbor_indices.cpu().numpy() == nbr).all()
+
+
+def test_empty_and_all_filtered(device):
+    e = np.zeros((0, 4), dtype=np.int32)
+    out_coords, ns, _, kmap, _ = _strided(device, e, (8, 8, 8), 3, 2, 1, 1, False)
+    assert out_coords.shape == (0, 4)
+    # stride 2, padding 0: a single voxel at an odd coordinate has no even-aligned output
+    out_coords, _, _, _, _ = _strided(device, np.array([[0, 1, 1, 1]], np.int32), (2, 2, 2), 1, 2, 0, 1, False)
+    assert out_coords.shape == (0, 4)
+
+
+# ------------------------------------------------------------ BASELINE sizes
+
+@pytest.fixture(scope="module")
+def cfg2():
+    return workloads.config2()
+
+
+def test_config2_subm_kmap_exact(device, cfg2):
+    c, shape = cfg2
+    kmap = _subm(device, c, shape)
+    expect = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, shape)
+    got = kmap.neighbor_indices.cpu().numpy()
+    assert (got == expect).all()
+    _check_masks(kmap)
+    p = int((expect >= 0).sum())
+    assert 3 * c.shape[0] <= p <= 8 * c.shape[0]
+
+
+def test_config3_config4_maps_exact(device, cfg2):
+    c, shape = cfg2
+    out3, ns3, _, kmap3, _ = _strided(device, c, shape, 3, 2, 1, 1, False)
+    oc3, ns3o, nbr3 = _oracle_strided(c, shape, 3, 2, 1, 1, False)
+    assert tuple(ns3) == ns3o == (720, 720, 21)
+    assert (out3.cpu().numpy() == oc3).all()
+    assert (kmap3.neighbor_indices.cpu().numpy() == nbr3).all()
+    # transposed k3 s2 p1 on the strided output (config 4)
+    out4, ns4, _, kmap4, _ = _strided(device, oc3, ns3o, 3, 2, 1, 1, True)
+    oc4, ns4o, nbr4 = _oracle_strided(oc3, ns3o, 3, 2, 1, 1, True)
+    assert tuple(ns4) == ns4o == (1439, 1439, 41)
+    assert (out4.cpu().numpy() == oc4).all()
+    assert (kmap4.neighbor_indices.cpu().numpy() == nbr4).all()

@@ -1,0 +1,178 @@
+"""Pins the CPU oracle (test infrastructure) before any GPU result is compared to it.
+
+What pins each oracle function:
+  exact_kmap      brute-force dictionary lookup (bf_kmap) on random sets, all geometries
+  out_coords      brute-force candidate loop (same order) and, as a set, the nonzero
+                  pattern of a dense convolution of the occupancy grid (golden fixtures)
+  fwd/dgrad/wgrad dense conv3d / conv_transpose3d values and autograd gradients
+                  (golden fixtures, torch float64)
+  RefHash         the reference tests' known answers (tests/test_utils_hash.py:95-123)
+                  and the closed-form key2 alias of (0,0,0,0) / (1,10,0,29)
+A mistake such as a sign flip in t_k, a transposed weight operand or a wrong
+stride rule breaks one of these.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def _rand_coords(rng, n, S=8, B=2):
+    lin = np.sort(rng.choice(B * S ** 3, n, replace=False))
+    return np.stack([lin // S ** 3, (lin // S ** 2) % S, (lin // S) % S, lin % S], 1).astype(np.int32)
+
+
+GEOMS = [(3, 1, 1, 1, False), (3, 2, 1, 1, False), (5, 2, 2, 1, False), (3, 2, 1, 2, False), (3, 1, 0, 1, False),
+         (3, 2, 1, 1, True), (3, 1, 1, 1, True), (3, 3, 0, 1, True), (2, 2, 0, 1, False)]
+
+
+@pytest.mark.parametrize("k,s,p,d,tr", GEOMS)
+def test_out_coords_and_kmap_vs_bruteforce(k, s, p, d, tr):
+    rng = np.random.default_rng(k * 100 + s * 10 + p + d + tr)
+    S = 8
+    c = _rand_coords(rng, 70, S)
+    off = O.target_offsets(k, d, p, tr)
+    ns = O.out_shape((S, S, S), k, s, d, p, tr)
+    oc = O.out_coords(c, off, s, tr, ns)
+    ob = O.bf_out_coords(c, off, s, tr, ns)
+    assert oc.shape == ob.shape and (oc == ob).all()
+    if tr:
+        a = O.exact_kmap(c, oc, off, 1, tuple(v * s for v in (S, S, S)), in_scale=s)
+        b = O.bf_kmap(c, oc, off, 1, tuple(v * s for v in (S, S, S)), in_scale=s)
+    else:
+        a = O.exact_kmap(c, oc, off, s, (S, S, S))
+        b = O.bf_kmap(c, oc, off, s, (S, S, S))
+    assert (a == b).all()
+    assert (a >= 0).sum() > 0
+
+
+def test_subm_kmap_vs_bruteforce_with_out_of_bounds():
+    rng = np.random.default_rng(7)
+    c = _rand_coords(rng, 90, 8)
+    off = O.target_offsets(3, 1, 1, False)
+    # a spatial shape smaller than the coordinates: the bounds check must drop neighbours
+    shape = (6, 7, 8)
+    assert (O.exact_kmap(c, c, off, 1, shape) == O.bf_kmap(c, c, off, 1, shape)).all()
+
+
+def _cases():
+    z = np.load(GOLD / "conv_cases.npz")
+    names = sorted({k.split("/")[0] for k in z.files})
+    return z, names
+
+
+@pytest.mark.parametrize("name", _cases()[1])
+def test_oracle_vs_dense_golden(name):
+    z, _ = _cases()
+    g = lambda key: z[f"{name}/{key}"]
+    C_in, C_out, k, s, p, d, tr, subm = (int(v) for v in g("meta"))
+    c, X, W = g("coords"), g("feats").astype(np.float64), g("weight").astype(np.float64)
+    S = tuple(int(v) for v in g("spatial_shape"))
+    off = O.target_offsets(k, d, p, bool(tr))
+    if subm:
+        oc = c
+    else:
+        ns = O.out_shape(S, k, s, d, p, bool(tr))
+        assert tuple(int(v) for v in g("out_shape")) == ns
+        oc = O.out_coords(c, off, s, bool(tr), ns)
+        # same set as the dense occupancy convolution
+        key = lambda a: set(map(tuple, np.asarray(a).tolist()))
+        assert key(oc) == key(g("out_coords"))
+    if tr:
+        nbr = O.exact_kmap(c, oc, off, 1, tuple(v * s for v in S), in_scale=s)
+    else:
+        nbr = O.exact_kmap(c, oc, off, s, S)
+    # reorder golden rows to the oracle's output order
+    gold_rows = {tuple(r): i for i, r in enumerate(g("out_coords").tolist())}
+    perm = np.array([gold_rows[tuple(r)] for r in oc.tolist()])
+    out = O.fwd_f64(X, W, nbr)
+    np.testing.assert_allclose(out, g("out")[perm], rtol=1e-5, atol=1e-5)
+    dY = g("dY").astype(np.float64)[perm]
+    np.testing.assert_allclose(O.dgrad_f64(dY, W, nbr, c.shape[0]), g("dX"), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(O.wgrad_f64(X, dY, nbr, k ** 3), g("dW"), rtol=1e-5, atol=1e-5)
+
+
+def test_ref_hash_port_reference_kats():
+    kats = json.loads((GOLD / "reference_kats.json").read_text())
+    for case in kats["hash_table"]["cases"]:
+        h = O.RefHash(case["insert"], factor=case["capacity"] / len(case["insert"]))
+        assert h.query(case["query"]).tolist() == case["expect"]
+
+
+def test_ref_hash_port_alias_defect():
+    kats = json.loads((GOLD / "reference_kats.json").read_text())["reference_hash_alias"]
+    # capacity 5 puts both coordinates' probe chains on slot 0; key2 aliases, so the
+    # reference's query returns row 0 for a coordinate that was never inserted.
+    h = O.RefHash([kats["a"]], factor=5.0)
+    assert h.T == 5
+    assert h.query([kats["b"]]).tolist() == [0]
+
+
+def test_ref_kmap_port_equals_exact_when_lossless():
+    rng = np.random.default_rng(3)
+    c = _rand_coords(rng, 200, 12)
+    off = O.target_offsets(3, 1, 1, False)
+    h = O.RefHash(c)
+    assert h.dropped == 0
+    ref = h.kmap(c, off, 1, (12, 12, 12))
+    exact = O.exact_kmap(c, c, off, 1, (12, 12, 12))
+    # the reference port may only differ by key2 aliasing; on this set it does not
+    assert (ref == exact).mean() > 0.999
+
+
+def test_ref_gemm_port_matches_f64():
+    rng = np.random.default_rng(4)
+    c = _rand_coords(rng, 150, 10)
+    off = O.target_offsets(3, 1, 1, False)
+    nbr = O.exact_kmap(c, c, off, 1, (10, 10, 10))
+    X = rng.standard_normal((150, 6)).astype(np.float32)
+    W = rng.standard_normal((27, 6, 10)).astype(np.float32)
+    dY = rng.standard_normal((150, 10)).astype(np.float32)
+    np.testing.assert_allclose(O.ref_fwd_f32(X, W, nbr), O.fwd_f64(X, W, nbr), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(O.ref_dgrad_f32(dY, W, nbr, 150), O.dgrad_f64(dY, W, nbr, 150), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(O.ref_wgrad_f32(X, dY, nbr, 27), O.wgrad_f64(X, dY, nbr, 27), rtol=1e-4, atol=1e-4)
+
+
+def test_offset_convention_kat():
+    kats = json.loads((GOLD / "reference_kats.json").read_text())["offset_convention"]
+    t = O.target_offsets(3, 1, 1, False)
+    assert list(t.shape) == kats["base_offsets_shape"]
+    # submanifold: neighbour = out - t_k = out + base_k
+    for key, k in kats["k_of"].items():
+        base = [int(v) for v in key.split(",")]
+        assert (-t[k]).tolist() == base
+
+
+def test_product_offsets_match_oracle():
+    from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets
+    for k, d, p, tr in [(3, 1, 1, False), (5, 2, 2, False), (3, 1, 1, True), (3, 1, 0, True), (2, 1, 0, False)]:
+        assert (_target_offsets(k, d, p, tr, "cpu").numpy() == O.target_offsets(k, d, p, tr)).all()
+
+
+def test_flatten_kats():
+    from sparsetriton_amd.utils.hash import flatten_coord, unflatten_coord
+    kats = json.loads((GOLD / "reference_kats.json").read_text())["flatten_coord"]
+    for case in kats["cases"]:
+        assert flatten_coord(torch.tensor(case["coords"])).tolist() == case["flat"]
+    rt = torch.tensor(kats["roundtrip"])
+    assert torch.equal(unflatten_coord(flatten_coord(rt)).long(), rt)
+
+
+def test_hash_coords_helper():
+    from sparsetriton_amd.utils.hash import hash_coords
+    h = hash_coords(torch.tensor([[0, 1, 2, 3], [0, 1, 2, 4]]))
+    assert h.dtype == torch.int32 and h.shape == (2,) and (h >= 0).all() and h[0] != h[1]
+    assert torch.unique(hash_coords(torch.randint(0, 100, (1000, 4)))).shape[0] > 500
+    # int32 wrap-around semantics, computed independently with numpy int32
+    c = np.array([[3, 40000, 50000, 60000]], dtype=np.int32)
+    with np.errstate(over="ignore"):
+        ref = ((c[:, 1] * np.int32(73856093)) ^ (c[:, 2] * np.int32(19349663)) ^ (c[:, 3] * np.int32(83492791))
+               ^ (c[:, 0] * np.int32(1000003))) & np.int32(0x7FFFFFFF)
+    assert hash_coords(torch.as_tensor(c)).tolist() == ref.tolist()
