@@ -10,8 +10,8 @@ A step = one forward + backward (input and weight gradient) of the layer
 through the public API (``sparse_conv3d`` + autograd), with the kernel map
 already cached on the tensor -- as in a stack of submanifold layers, where it
 is built once per coordinate set.  The kernel-map build (hash insert +
-neighbour query + transposed map) is timed separately and reported as
-``kmap_build_ms``.
+neighbour query + transposed map + mask-sorted tile plans + pair list) is
+timed separately and reported as ``kmap_build_ms``.
 
 value = effective TFLOP/s = 6 * P * C_in * C_out / step time, P = exact number
 of (input, output, offset) pairs.  ``roofline`` covers the dominant kernel,
@@ -111,7 +111,11 @@ def main():
     from sparsetriton_amd import _lib
     from sparsetriton_amd.nn.functional import sparse_conv3d
     from sparsetriton_amd.nn.functional.conv.conv import table_capacity
-    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import gather_gemm, weight_prep, wgrad
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
+        gather_gemm_plan,
+        weight_prep,
+        wgrad,
+    )
     from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets, query_kernel_map
     from sparsetriton_amd.utils.hash import HashTable
 
@@ -136,7 +140,7 @@ def main():
         t = HashTable(table_capacity(N), device=dev)
         t.insert(coords)
         km = query_kernel_map(t, coords, offsets, shape, 1, N)
-        km.ensure_inverse()
+        km.prepare()  # transposed map, mask-sorted tile plans, pair list
         return t, km
 
     for _ in range(3):
@@ -155,6 +159,7 @@ def main():
 
     ins_t = _events(torch, t_insert, 20)
     q_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N), 20)
+    prep_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N).prepare(), 20) - np.median(q_t)
 
     # --------------------------------------------------------- train step
     X = torch.as_tensor(X_np, device=dev).to(dtype)
@@ -190,9 +195,9 @@ def main():
     # ---------------------------------------------- per-kernel (events) timing
     wt = weight_prep(w.detach(), _lib.W_TRANSPOSE)
     wd = w.detach().contiguous()
-    fwd_t = _events(torch, lambda: gather_gemm(X, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, wt, N,
-                                               27), 30)
-    dgrad_t = _events(torch, lambda: gather_gemm(dY, kmap.invnbr, N, 1, kmap.in_masks, wd, N, 27), 30)
+    fplan, bplan = kmap.forward_plan(), kmap.backward_plan()
+    fwd_t = _events(torch, lambda: gather_gemm_plan(X, fplan, wt, N, 27), 30)
+    dgrad_t = _events(torch, lambda: gather_gemm_plan(dY, bplan, wd, N, 27), 30)
     wgrad_t = _events(torch, lambda: wgrad(X, dY, kmap, w.dtype), 30)
     kern = {"gather_gemm_fwd": float(np.mean(fwd_t)), "gather_gemm_dgrad": float(np.mean(dgrad_t)),
             "wgrad(+reduce)": float(np.mean(wgrad_t))}
@@ -215,6 +220,7 @@ def main():
         "kmap_build_ms": _stats(kmap_t),
         "hash_insert_ms": float(np.median(ins_t)), "hash_insert_GBps": ins_bytes / (np.median(ins_t) * 1e-3) / 1e9,
         "kmap_query_ms": float(np.median(q_t)), "kmap_query_GBps": q_bytes / (np.median(q_t) * 1e-3) / 1e9,
+        "plans_ms": float(np.median(prep_t)),
     }
     log(f"kernels (avg ms): {kern}; roofline {dom}: {achieved:.2f} TFLOP/s = {roofline['frac'] * 100:.1f}% of peak")
 

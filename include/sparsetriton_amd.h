@@ -176,6 +176,41 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
 int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride, int64_t n_out, int K,
                    int64_t n_in, int32_t* invnbr, uint32_t* in_masks, uint32_t* out_masks, st_stream_t stream);
 
+/*
+ * Destination-row order for the gather-GEMM (no reference counterpart; the
+ * reference tiles rows in storage order).  Rows are stably radix-sorted by
+ * their offset bitmask (masks (n, mask_words), folded to 32 bits when
+ * K > 32) so that 16/32-row MFMA slabs share their offsets.  perm (n) gets
+ * the sorted row ids.  keys_tmp holds 2n u32, rows_tmp n int32, workspace
+ * st_kmap_sort_workspace(n) bytes.
+ */
+int st_kmap_sort_workspace(int64_t n, size_t* bytes);
+int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp, int32_t* rows_tmp,
+                      int32_t* perm, void* workspace, size_t workspace_bytes, st_stream_t stream);
+
+/*
+ * The map in tile order: map_out[k * n + r] = map(k, perm[r]) and
+ * masks_out[r] = masks[perm[r]], so the gather-GEMM reads each offset's
+ * column with coalesced loads.
+ */
+int st_kmap_permute(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n, int K,
+                    const uint32_t* masks, int mask_words, const int32_t* perm, int32_t* map_out, uint32_t* masks_out,
+                    st_stream_t stream);
+
+/*
+ * Pair list of a kernel map for the weight gradient (replaces the per-tile
+ * map walk of precomputed_bwd_weight_kernel, implicit_precomputed_gemm.py:180-230):
+ * pairs (2P int32) = (in, out) for every map(k, out) in [0, n_in), sorted by
+ * (k, out); kstart (K + 1) = first pair of each offset (kstart[K] = P);
+ * cstart (K + 1) = first chunk of each offset when each offset's pairs are
+ * cut into chunks of `chunk` pairs.  block_counts holds K * num_blocks + 1
+ * int32 (num_blocks from st_kmap_pairs_sizes); pair_capacity >= K * n_out.
+ */
+int st_kmap_pairs_sizes(int64_t n_out, int K, int64_t* num_blocks);
+int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n_out, int K, int64_t n_in,
+                  int32_t* block_counts, int64_t num_blocks, int chunk, int32_t* kstart, int32_t* cstart,
+                  int32_t* pairs, int64_t pair_capacity, st_stream_t stream);
+
 /* ------------------------------------------------------------- gather-GEMM */
 
 /*
@@ -192,9 +227,13 @@ int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mod
  * here a gather with no atomics):
  *   out[r, :] = sum over k of A[map(k, r), :] @ Bt[k]^T  (map < 0 or >= n_src adds 0)
  * A (n_src, Kd), Bt (K, Nd, Kd), out (n_dst, Nd), all of `dtype`, fp32
- * accumulation on MFMA.  map(k, r) = map[k * map_k_stride + r * map_r_stride].
- * row_masks (n_dst, mask_words) optional: offsets a whole workgroup tile lacks
- * are skipped.  perm (n_dst) optional: the order rows are tiled in.
+ * accumulation on MFMA.  Rows are processed in tile order r = 0..n_dst-1:
+ * map(k, r) = map[k * map_k_stride + r * map_r_stride] and row_masks (n_dst,
+ * mask_words, optional) are indexed by r, and perm (optional) sends tile row r
+ * to output row perm[r] (identity when NULL) -- the mask-sorted order from
+ * st_kmap_sort_rows / st_kmap_permute.  Offsets no row of a 128-row tile has
+ * are skipped by the workgroup, offsets no row of a 32-row wave slab has by
+ * that wave.
  */
 int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
                    const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, void* out,
@@ -214,6 +253,18 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,
              int64_t map_r_stride, int64_t n_out, int K, int C_in, int C_out, int dtype, float* partials,
              int64_t splits, void* dW, int dw_dtype, st_stream_t stream);
+
+/*
+ * Weight gradient over a pair list from st_kmap_pairs: every chunk of
+ * `chunk` pairs is one equal-sized task (the centre offset of a submanifold
+ * map has N pairs, the others far fewer), its C_in x C_out partial goes to
+ * partials[chunk] (max_chunks * C_in * C_out fp32; max_chunks >= P / chunk + K)
+ * and each offset's chunks are summed in order.  Deterministic; fp32
+ * gathers feed MFMA operands straight from HBM, 16-bit ones go through LDS.
+ */
+int st_wgrad_pairs(const void* X, const void* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
+                   int K, int chunk, int64_t max_chunks, int C_in, int C_out, int dtype, float* partials, void* dW,
+                   int dw_dtype, st_stream_t stream);
 
 /* ----------------------------------------------------- implicit hash-fly */
 
@@ -235,6 +286,7 @@ typedef struct st_lookup {
  * implicit_gemm_bwd_feat_kernel :151-237 recast as a gather): the same
  * gather-GEMM as st_gather_gemm with map(k, r) found by probing the table
  * inside the kernel, once per row tile rather than once per C_out tile.
+ * dst_coords must be int16 or int32.
  */
 int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int coord_dtype, int64_t n_dst,
                     const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,

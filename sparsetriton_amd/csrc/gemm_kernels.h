@@ -1,0 +1,904 @@
+// Gather-GEMM (forward and input-gradient) and weight-gradient kernels.
+//
+// Forward, output-stationary (precomputed_fwd_kernel, implicit_precomputed_gemm.py:64-126):
+//   workgroup = 4 waves = 128 destination rows x BN columns.  Per kernel
+//   offset k present in the tile (row masks OR-ed in LDS), the B operand
+//   Bt[k] (BN x Kd slice) is staged in LDS once for all 4 waves; each wave
+//   gathers the A rows of its 32 destination rows straight from HBM into
+//   registers (one 16-byte load per lane per 16/32 reduction elements) and
+//   accumulates 2 x BN/16 MFMA tiles in registers.  Offsets no row of a wave
+//   has are skipped by that wave; offsets no row of the tile has are skipped
+//   by the workgroup.  Each destination row is written exactly once: no
+//   atomics, no zero-fill pass, deterministic.
+// Input gradient: the same kernel over the transposed kernel map (for a
+//   submanifold map, the same map with the weight offsets reversed), which
+//   replaces the reference's atomic scatter (precomputed_bwd_feat_kernel :129-177).
+// Weight gradient (precomputed_bwd_weight_kernel :180-230): workgroup (split,
+//   k) walks its slice of map column k, compacts the valid (in, out) pairs in
+//   LDS, stages 32 pairs at a time transposed (channel-major) in LDS and runs
+//   MFMA with the pairs as the reduction dimension.  Per-split fp32 partials
+//   are summed in a fixed order by a second kernel.
+#pragma once
+
+#include "common.h"
+#include "mfma.h"
+#include "nbr_src.h"
+
+namespace st {
+
+constexpr int kGemmBM = 128;
+
+template <typename T, int BN, typename Src>
+__global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ A, Src src,
+                                                          const uint32_t* __restrict__ masks, int W,
+                                                          const int32_t* __restrict__ perm, const T* __restrict__ Bt,
+                                                          T* __restrict__ out, int64_t n_src, int64_t n_dst, int K,
+                                                          int Kd, int Nd, int vec_a, int vec_b) {
+  using F = typename Frag<T>::type;
+  constexpr int VEC = Frag<T>::VEC;
+  constexpr int KSTEP = Frag<T>::KSTEP;
+  constexpr int KCH = sizeof(T) == 4 ? 64 : 128;  // reduction elements staged per pass
+  constexpr int PITCH = KCH + VEC;                // LDS row pitch (elements), 16-byte multiple
+  constexpr int NBLK = BN / 16;
+  constexpr int CV = KCH / VEC;
+  __shared__ __attribute__((aligned(16))) T bt_s[BN * PITCH];
+  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ int32_t drow_s[kGemmBM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
+  const int n0 = blockIdx.y * BN;
+
+  if (tid < kGemmBM) {
+    const int64_t r = row0 + tid;
+    drow_s[tid] = r < n_dst ? (perm ? perm[r] : (int32_t)r) : -1;
+  }
+  if (tid < W) tmask_s[tid] = 0;
+  __syncthreads();
+  if (masks) {
+    for (int w = 0; w < W; ++w) {
+      uint32_t v = 0;
+      if (tid < kGemmBM && row0 + tid < n_dst) v = masks[(row0 + tid) * W + w];
+      v = wave_or(v);
+      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+    }
+  } else if (tid < W) {
+    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+
+  // Lane (l & 31) resolves tile row wid*32 + (l & 31); MFMA row c of tile m
+  // is then fetched from lane m*16 + c with a shuffle.
+  const int64_t my_r = row0 + wid * 32 + (lane & 31);
+  const bool my_ok = my_r < n_dst;
+  const typename Src::RowCtx rc = src.row(my_ok ? my_r : 0);
+
+  v4f acc[2][NBLK];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int w = 0; w < W; ++w) {
+    uint32_t bits = tmask_s[w];
+    while (bits) {
+      const int k = w * 32 + __builtin_ctz(bits);
+      bits &= bits - 1;
+      int32_t s_own = my_ok ? src.get(rc, k) : -1;
+      if ((int64_t)s_own >= n_src) s_own = -1;  // a caller's map entry past A: no contribution
+      const int32_t s0 = __shfl(s_own, c, 64);
+      const int32_t s1 = __shfl(s_own, 16 + c, 64);
+      const bool wave_any = __ballot(s_own >= 0) != 0ull;
+      for (int kc0 = 0; kc0 < Kd; kc0 += KCH) {
+        __syncthreads();
+        for (int idx = tid; idx < BN * CV; idx += 256) {
+          const int nr = idx / CV, cv = idx - nr * CV;
+          F f = zero_frag<T>();
+          if (n0 + nr < Nd) f = load_frag<T>(Bt + ((int64_t)k * Nd + n0 + nr) * Kd, kc0 + cv * VEC, Kd, vec_b);
+          *reinterpret_cast<F*>(&bt_s[nr * PITCH + cv * VEC]) = f;
+        }
+        __syncthreads();
+        if (!wave_any) continue;
+        const int kend = min(KCH, Kd - kc0);
+        for (int kk = 0; kk < kend; kk += KSTEP) {
+          const int col = kc0 + kk + g * VEC;
+          const F a0 = s0 >= 0 ? load_frag<T>(A + (int64_t)s0 * Kd, col, Kd, vec_a) : zero_frag<T>();
+          const F a1 = s1 >= 0 ? load_frag<T>(A + (int64_t)s1 * Kd, col, Kd, vec_a) : zero_frag<T>();
+#pragma unroll
+          for (int nb = 0; nb < NBLK; ++nb) {
+            const F b = *reinterpret_cast<const F*>(&bt_s[(nb * 16 + c) * PITCH + kk + g * VEC]);
+            acc[0][nb] = mfma(a0, b, acc[0][nb]);
+            acc[1][nb] = mfma(a1, b, acc[1][nb]);
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+      if (drow < 0) continue;
+      T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) {
+        const int col = n0 + nb * 16 + c;
+        if (col < Nd) orow[col] = from_f32<T>(acc[m][nb][r]);
+      }
+    }
+}
+
+// Pipelined gather-GEMM for reduction depths known at compile time
+// (Kd <= KS * KSTEP).  Per workgroup: the list of offsets present in the tile
+// is built once; for offset i the B slice Bt[k_i] sits in LDS buffer i & 1
+// while Bt[k_{i+1}] and the next offset's A rows are already in flight into
+// registers, so global latency overlaps the MFMAs.  One barrier per offset.
+// The map and row masks are indexed in tile order r; rows[r] is the output
+// row (the mask-sorted permutation) or r itself when rows is null.
+template <typename T, int BN, int KS, typename Src>
+__global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
+    const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
+    const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
+    int vec_b) {
+  using F = typename Frag<T>::type;
+  constexpr int VEC = Frag<T>::VEC;
+  constexpr int KSTEP = Frag<T>::KSTEP;
+  constexpr int KDP = KS * KSTEP;
+  constexpr int PITCH = KDP + VEC;
+  constexpr int NBLK = BN / 16;
+  constexpr int CV = KDP / VEC;
+  constexpr int BREGS = (BN * CV + 255) / 256;
+  __shared__ __attribute__((aligned(16))) T bt_s[2][BN * PITCH];
+  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ int32_t drow_s[kGemmBM];
+  __shared__ int16_t klist_s[ST_MAX_KVOL];
+  __shared__ int nk_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
+  const int n0 = blockIdx.y * BN;
+
+  if (tid < kGemmBM) {
+    const int64_t r = row0 + tid;
+    drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
+  }
+  if (tid < W) tmask_s[tid] = 0;
+  __syncthreads();
+  if (masks) {
+    for (int w = 0; w < W; ++w) {
+      uint32_t v = 0;
+      if (tid < kGemmBM && row0 + tid < n_dst) v = masks[(row0 + tid) * W + w];
+      v = wave_or(v);
+      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+    }
+  } else if (tid < W) {
+    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int nk = 0;
+    for (int w = 0; w < W; ++w) {
+      uint32_t bits = tmask_s[w];
+      while (bits) {
+        klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+        bits &= bits - 1;
+      }
+    }
+    nk_s = nk;
+  }
+  __syncthreads();
+  const int nk = nk_s;
+
+  // Lane (l & 31) resolves tile row wid*32 + (l & 31); MFMA row c of slab m
+  // is fetched from lane m*16 + c.
+  const int64_t my_r = row0 + wid * 32 + (lane & 31);
+  const bool my_ok = my_r < n_dst;
+  const typename Src::RowCtx rc = src.row(my_ok ? my_r : 0);
+
+  auto sources = [&](int k, int32_t& s0, int32_t& s1) -> bool {
+    int32_t s = my_ok ? src.get(rc, k) : -1;
+    if ((int64_t)s >= n_src) s = -1;
+    s0 = __shfl(s, c, 64);
+    s1 = __shfl(s, 16 + c, 64);
+    return __ballot(s >= 0) != 0ull;
+  };
+  auto load_a = [&](int32_t s0, int32_t s1, F (&a)[2][KS]) {
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      const int col = j * KSTEP + g * VEC;
+      a[0][j] = s0 >= 0 ? load_frag<T>(A + (int64_t)s0 * Kd, col, Kd, vec_a) : zero_frag<T>();
+      a[1][j] = s1 >= 0 ? load_frag<T>(A + (int64_t)s1 * Kd, col, Kd, vec_a) : zero_frag<T>();
+    }
+  };
+  auto load_b = [&](int k, F (&b)[BREGS]) {
+#pragma unroll
+    for (int j = 0; j < BREGS; ++j) {
+      const int idx = tid + j * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      b[j] = zero_frag<T>();
+      if (idx < BN * CV && n0 + nr < Nd)
+        b[j] = load_frag<T>(Bt + ((int64_t)k * Nd + n0 + nr) * Kd, cv * VEC, Kd, vec_b);
+    }
+  };
+  auto store_b = [&](int buf, const F (&b)[BREGS]) {
+#pragma unroll
+    for (int j = 0; j < BREGS; ++j) {
+      const int idx = tid + j * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      if (idx < BN * CV) *reinterpret_cast<F*>(&bt_s[buf][nr * PITCH + cv * VEC]) = b[j];
+    }
+  };
+
+  v4f acc[2][NBLK];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    F a_cur[2][KS], a_nxt[2][KS];
+    F breg[BREGS];
+    int32_t s0, s1;
+    bool any_cur = sources(klist_s[0], s0, s1);
+    load_a(s0, s1, a_cur);
+    load_b(klist_s[0], breg);
+    store_b(0, breg);
+    __syncthreads();
+    for (int i = 0; i < nk; ++i) {
+      const bool has_next = i + 1 < nk;
+      bool any_nxt = false;
+      if (has_next) {
+        const int kn = klist_s[i + 1];
+        int32_t t0, t1;
+        any_nxt = sources(kn, t0, t1);
+        load_a(t0, t1, a_nxt);
+        load_b(kn, breg);
+      }
+      if (any_cur) {
+        const T* bs = bt_s[i & 1];
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+#pragma unroll
+          for (int nb = 0; nb < NBLK; ++nb) {
+            const F b = *reinterpret_cast<const F*>(&bs[(nb * 16 + c) * PITCH + j * KSTEP + g * VEC]);
+            acc[0][nb] = mfma(a_cur[0][j], b, acc[0][nb]);
+            acc[1][nb] = mfma(a_cur[1][j], b, acc[1][nb]);
+          }
+        }
+      }
+      if (has_next) store_b((i + 1) & 1, breg);
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int j = 0; j < KS; ++j) a_cur[m][j] = a_nxt[m][j];
+      any_cur = any_nxt;
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+      if (drow < 0) continue;
+      T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) {
+        const int col = n0 + nb * 16 + c;
+        if (col < Nd) orow[col] = from_f32<T>(acc[m][nb][r]);
+      }
+    }
+}
+
+// ------------------------------------------- weight gradient over pair lists
+//
+// pairs: (in, out) int32 pairs sorted by (offset k, out); kstart[k] = first
+// pair of offset k; the pair range of every offset is cut into chunks of
+// `chunk` pairs (cstart[k] = first chunk of offset k, cstart[K] = total), so
+// every workgroup task has the same size whatever the offset's density.
+// Workgroups walk chunks with a grid stride; chunk c's C_in x C_out partial
+// goes to partials[c] and the reduce kernel sums each offset's chunks in order.
+
+__device__ __forceinline__ int chunk_offset(const int32_t* cstart_s, int K, int c) {
+  int lo = 0, hi = K - 1;  // largest k with cstart[k] <= c
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cstart_s[mid] <= c) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// fp32: every lane gathers its own MFMA operands straight from HBM/L2
+// (16 lanes read 16 consecutive channels of one pair's row), no LDS staging.
+// A wave owns an MT x NT grid of 16x16 blocks; when the workgroup's channel
+// tile has fewer than 4 wave tiles, waves split the chunk's pairs and sum
+// through LDS at the end.
+template <int MT, int NT>
+__global__ __launch_bounds__(256) void wgrad_pairs_f32_kernel(const float* __restrict__ X, const float* __restrict__ dY,
+                                                              const int2* __restrict__ pairs,
+                                                              const int32_t* __restrict__ kstart,
+                                                              const int32_t* __restrict__ cstart, int K, int chunk,
+                                                              int Cin, int Cout, float* __restrict__ partials) {
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ float red_s[3][MT * NT * 4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  __syncthreads();
+  const int total = cstart_s[K];
+
+  const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
+  const int WM = (MB + MT - 1) / MT, WN = (NB + NT - 1) / NT;
+  const int wt0 = blockIdx.z * 4;
+  const int nt = min(4, WM * WN - wt0);
+  const int nphase = nt == 1 ? 4 : (nt == 2 ? 2 : 1);
+  const int my_t = wid % (nt == 3 ? 4 : nt);
+  const int phase = nt == 3 ? 0 : wid / nt;
+  const bool active = my_t < nt;
+  const int wt = wt0 + my_t;
+  const int cm0 = (wt / WN) * MT * 16, cn0 = (wt % WN) * NT * 16;
+
+  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+    const int k = chunk_offset(cstart_s, K, cidx);
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
+    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    v4f acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (active) {
+#pragma unroll 4
+      for (int q = p0 + phase * 4; q < p1; q += 4 * nphase) {
+        const int p = q + g;
+        int2 pr = make_int2(-1, -1);
+        if (p < p1) pr = pairs[p];
+        float a[MT], b[NT];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int ch = cm0 + i * 16 + c;
+          a[i] = (pr.x >= 0 && ch < Cin) ? X[(int64_t)pr.x * Cin + ch] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int ch = cn0 + j * 16 + c;
+          b[j] = (pr.y >= 0 && ch < Cout) ? dY[(int64_t)pr.y * Cout + ch] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (nphase > 1) {
+      if (active && phase > 0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red_s[(phase - 1) * nt + my_t][(i * NT + j) * 4 + r][lane] = acc[i][j][r];
+      }
+      __syncthreads();
+      if (active && phase == 0) {
+        for (int ph = 1; ph < nphase; ++ph)
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][r] += red_s[(ph - 1) * nt + my_t][(i * NT + j) * 4 + r][lane];
+      }
+    }
+    if (active && phase == 0) {
+      float* part = partials + (int64_t)cidx * Cin * Cout;
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = cn0 + j * 16 + c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = cm0 + i * 16 + g * 4 + r;
+            if (row < Cin && col < Cout) part[(int64_t)row * Cout + col] = acc[i][j][r];
+          }
+        }
+    }
+    __syncthreads();
+  }
+}
+
+// 16-bit: a batch of 64 pairs is staged in LDS channel-major (the MFMA
+// reduction runs over pairs, which are rows in HBM), then each wave runs its
+// share of the workgroup's 16x16 output blocks.
+constexpr int kWpQB = 64;
+template <typename T, int JB>  // JB: 16x16 output blocks per wave (4 waves x JB >= blocks of the tile)
+__global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restrict__ X, const T* __restrict__ dY,
+                                                              const int2* __restrict__ pairs,
+                                                              const int32_t* __restrict__ kstart,
+                                                              const int32_t* __restrict__ cstart, int K, int chunk,
+                                                              int Cin, int Cout, float* __restrict__ partials,
+                                                              int vec_x, int vec_y) {
+  using F = typename Frag<T>::type;
+  constexpr int VEC = Frag<T>::VEC;
+  constexpr int KSTEP = Frag<T>::KSTEP;
+  constexpr int PITCH = kWpQB + 8;
+  constexpr int TB = 8;  // 16x16 blocks per side of the workgroup tile (128 channels)
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ int2 pr_s[kWpQB];
+  __shared__ __attribute__((aligned(16))) T xt_s[TB * 16 * PITCH];
+  __shared__ __attribute__((aligned(16))) T yt_s[TB * 16 * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  __syncthreads();
+  const int total = cstart_s[K];
+
+  const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
+  const int nzn = (NB + TB - 1) / TB;
+  const int mz = blockIdx.z / nzn, nz = blockIdx.z % nzn;
+  const int mb0 = mz * TB, nb0 = nz * TB;
+  const int MT = min(TB, MB - mb0), NT = min(TB, NB - nb0);
+  const int nloc = MT * NT;
+  const int cm0 = mb0 * 16, cn0 = nb0 * 16;
+  const int CVX = (MT * 16) / VEC, CVY = (NT * 16) / VEC;
+
+  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+    const int k = chunk_offset(cstart_s, K, cidx);
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
+    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    v4f acc[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int q0 = p0; q0 < p1; q0 += kWpQB) {
+      const int nq = min(kWpQB, p1 - q0);
+      if (tid < kWpQB) pr_s[tid] = tid < nq ? pairs[q0 + tid] : make_int2(-1, -1);
+      __syncthreads();
+      for (int idx = tid; idx < kWpQB * CVX; idx += 256) {
+        const int p = idx / CVX, cv = idx - p * CVX;
+        F f = zero_frag<T>();
+        const int32_t i = pr_s[p].x;
+        if (i >= 0) f = load_frag<T>(X + (int64_t)i * Cin, cm0 + cv * VEC, Cin, vec_x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xt_s[(cv * VEC + e) * PITCH + p] = f[e];
+      }
+      for (int idx = tid; idx < kWpQB * CVY; idx += 256) {
+        const int p = idx / CVY, cv = idx - p * CVY;
+        F f = zero_frag<T>();
+        const int32_t o = pr_s[p].y;
+        if (o >= 0) f = load_frag<T>(dY + (int64_t)o * Cout, cn0 + cv * VEC, Cout, vec_y);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) yt_s[(cv * VEC + e) * PITCH + p] = f[e];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ps = 0; ps < kWpQB; ps += KSTEP) {
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+          const int j = wid + 4 * jj;
+          if (j < nloc) {
+            const int mb = j / NT, nb = j - mb * NT;
+            const F a = *reinterpret_cast<const F*>(&xt_s[(mb * 16 + c) * PITCH + ps + g * VEC]);
+            const F b = *reinterpret_cast<const F*>(&yt_s[(nb * 16 + c) * PITCH + ps + g * VEC]);
+            acc[jj] = mfma(a, b, acc[jj]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float* part = partials + (int64_t)cidx * Cin * Cout;
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj) {
+      const int j = wid + 4 * jj;
+      if (j < nloc) {
+        const int mb = j / NT, nb = j - mb * NT;
+        const int col = cn0 + nb * 16 + c;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = cm0 + mb * 16 + g * 4 + r;
+          if (row < Cin && col < Cout) part[(int64_t)row * Cout + col] = acc[jj][r];
+        }
+      }
+    }
+  }
+}
+
+template <typename TW>
+__global__ void wgrad_pairs_reduce_kernel(const float* __restrict__ partials, const int32_t* __restrict__ cstart,
+                                          int64_t per_k, int K, TW* __restrict__ dW) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= per_k * K) return;
+  const int64_t k = i / per_k, e = i - k * per_k;
+  float s = 0.f;
+  for (int cidx = cstart[k]; cidx < cstart[k + 1]; ++cidx) s += partials[(int64_t)cidx * per_k + e];
+  dW[i] = from_f32<TW>(s);
+}
+
+constexpr int kWgQB = 32;       // pairs per MFMA batch
+constexpr int kWgRows = 1024;   // map rows compacted per step (4 per thread)
+constexpr int kWgTileBlk = 8;   // 16x16 blocks per workgroup sub-tile side (128 channels)
+
+template <typename T, typename Src>
+__global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ X, const T* __restrict__ dY, Src src,
+                                                    int64_t n_in, int64_t n_out, int Cin, int Cout,
+                                                    int64_t rows_per_split,
+                                                    int splits, float* __restrict__ partials, int vec_x, int vec_y) {
+  using F = typename Frag<T>::type;
+  constexpr int VEC = Frag<T>::VEC;
+  constexpr int KSTEP = Frag<T>::KSTEP;
+  constexpr int PITCH = kWgQB + (sizeof(T) == 4 ? 4 : 8);
+  constexpr int CH = kWgTileBlk * 16;
+  __shared__ int32_t qin_s[kWgRows];
+  __shared__ int32_t qout_s[kWgRows];
+  __shared__ __attribute__((aligned(16))) T xt_s[CH * PITCH];
+  __shared__ __attribute__((aligned(16))) T yt_s[CH * PITCH];
+  __shared__ int scan_s[5];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int split = blockIdx.x, k = blockIdx.y;
+  const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
+  const int nzn = (NB + kWgTileBlk - 1) / kWgTileBlk;
+  const int mz = blockIdx.z / nzn, nz = blockIdx.z % nzn;
+  const int mb0 = mz * kWgTileBlk, nb0 = nz * kWgTileBlk;
+  const int MT = min(kWgTileBlk, MB - mb0), NT = min(kWgTileBlk, NB - nb0);
+  const int nloc = MT * NT;
+  const int cm0 = mb0 * 16, cn0 = nb0 * 16;
+
+  v4f acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t o_begin = (int64_t)split * rows_per_split;
+  const int64_t o_end = min(n_out, o_begin + rows_per_split);
+  const int CVX = (MT * 16) / VEC, CVY = (NT * 16) / VEC;
+
+  for (int64_t base = o_begin; base < o_end; base += kWgRows) {
+    int32_t ins[4];
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t o = base + tid * 4 + j;
+      ins[j] = -1;
+      if (o < o_end) ins[j] = src.get(src.row(o), k);
+      if ((int64_t)ins[j] >= n_in) ins[j] = -1;  // a caller's map entry past X: no contribution
+      cnt += ins[j] >= 0;
+    }
+    int total;
+    int pos = block_exclusive_scan(cnt, scan_s, &total);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (ins[j] >= 0) {
+        qin_s[pos] = ins[j];
+        qout_s[pos] = (int32_t)(base + tid * 4 + j);
+        ++pos;
+      }
+    __syncthreads();
+    for (int q0 = 0; q0 < total; q0 += kWgQB) {
+      const int nq = min(kWgQB, total - q0);
+      for (int idx = tid; idx < kWgQB * CVX; idx += 256) {
+        const int p = idx / CVX, cv = idx - p * CVX;
+        F f = zero_frag<T>();
+        if (p < nq) f = load_frag<T>(X + (int64_t)qin_s[q0 + p] * Cin, cm0 + cv * VEC, Cin, vec_x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xt_s[(cv * VEC + e) * PITCH + p] = f[e];
+      }
+      for (int idx = tid; idx < kWgQB * CVY; idx += 256) {
+        const int p = idx / CVY, cv = idx - p * CVY;
+        F f = zero_frag<T>();
+        if (p < nq) f = load_frag<T>(dY + (int64_t)qout_s[q0 + p] * Cout, cn0 + cv * VEC, Cout, vec_y);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) yt_s[(cv * VEC + e) * PITCH + p] = f[e];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ps = 0; ps < kWgQB; ps += KSTEP) {
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const int j = wid + 4 * jj;
+          if (j < nloc) {
+            const int mb = j / NT, nb = j - mb * NT;
+            const F a = *reinterpret_cast<const F*>(&xt_s[(mb * 16 + c) * PITCH + ps + g * VEC]);
+            const F b = *reinterpret_cast<const F*>(&yt_s[(nb * 16 + c) * PITCH + ps + g * VEC]);
+            acc[jj] = mfma(a, b, acc[jj]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  float* part = partials + ((int64_t)k * splits + split) * (int64_t)Cin * Cout;
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const int j = wid + 4 * jj;
+    if (j < nloc) {
+      const int mb = j / NT, nb = j - mb * NT;
+      const int col = cn0 + nb * 16 + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = cm0 + mb * 16 + g * 4 + r;
+        if (row < Cin && col < Cout) part[(int64_t)row * Cout + col] = acc[jj][r];
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ void wgrad_reduce_kernel(const float* __restrict__ partials, int64_t per_k, int splits, int K,
+                                    T* __restrict__ dW) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= per_k * K) return;
+  const int64_t k = i / per_k, e = i - k * per_k;
+  const float* p = partials + k * splits * per_k + e;
+  float s = 0.f;
+  for (int j = 0; j < splits; ++j) s += p[(int64_t)j * per_k];
+  dW[i] = from_f32<T>(s);
+}
+
+template <typename T>
+__global__ void weight_prep_kernel(const T* __restrict__ w, T* __restrict__ out, int K, int Cin, int Cout, int mode) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)K * Cin * Cout;
+  if (i >= total) return;
+  if (mode == ST_W_TRANSPOSE) {
+    // i indexes out[k][co][ci]
+    const int64_t k = i / ((int64_t)Cin * Cout);
+    const int64_t rem = i - k * Cin * Cout;
+    const int64_t co = rem / Cin, ci = rem - co * Cin;
+    out[i] = w[(k * Cin + ci) * Cout + co];
+  } else if (mode == ST_W_REVERSE) {
+    const int64_t k = i / ((int64_t)Cin * Cout);
+    const int64_t rem = i - k * Cin * Cout;
+    out[i] = w[(K - 1 - k) * Cin * Cout + rem];
+  } else {
+    out[i] = w[i];
+  }
+}
+
+// ---------------------------------------------------------------- dispatch
+//
+// Typed launchers, instantiated once per dtype in gemm_{f32,f16,bf16}.hip.
+
+template <typename T, int BN, int KS, typename Src>
+static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W, const int32_t* rows,
+                        const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
+                        hipStream_t stream) {
+  const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
+  gather_gemm_pipe_kernel<T, BN, KS, Src>
+      <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+}
+
+template <typename T, int KS, typename Src>
+static void launch_pipe_ks(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                           const int32_t* rows, const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
+                           int vec_b, hipStream_t stream) {
+  constexpr int LDS128 = 2 * 128 * (KS * Frag<T>::KSTEP + Frag<T>::VEC) * (int)sizeof(T);
+  if (Nd <= 16)
+    launch_pipe<T, 16, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else if (Nd <= 32)
+    launch_pipe<T, 32, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else if (Nd <= 64 || LDS128 > 65536)
+    launch_pipe<T, 64, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else if constexpr (LDS128 <= 65536)
+    launch_pipe<T, 128, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+}
+
+template <typename T, typename Src>
+static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                         const int32_t* rows, const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd,
+                         hipStream_t stream) {
+  constexpr int VEC = Frag<T>::VEC;
+  constexpr int KSTEP = Frag<T>::KSTEP;
+  const int vec_a = (Kd % VEC == 0) && ((uintptr_t)A % 16 == 0);
+  const int vec_b = (Kd % VEC == 0) && ((uintptr_t)Bt % 16 == 0);
+  const int ks = (Kd + KSTEP - 1) / KSTEP;
+  if (ks == 1) {
+    launch_pipe_ks<T, 1>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  } else if (ks == 2) {
+    launch_pipe_ks<T, 2>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  } else if (ks <= 4) {
+    launch_pipe_ks<T, 4>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  } else {
+    // Deep reductions: the single-buffered kernel stages Bt in chunks.
+    const unsigned gx = st_blocks(n_dst, kGemmBM);
+    if (Nd <= 16)
+      gather_gemm_kernel<T, 16, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
+                                                                       K, Kd, Nd, vec_a, vec_b);
+    else if (Nd <= 32)
+      gather_gemm_kernel<T, 32, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
+                                                                       K, Kd, Nd, vec_a, vec_b);
+    else if (Nd <= 64)
+      gather_gemm_kernel<T, 64, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
+                                                                       K, Kd, Nd, vec_a, vec_b);
+    else
+      gather_gemm_kernel<T, 128, Src><<<dim3(gx, st_blocks(Nd, 128)), 256, 0, stream>>>(
+          A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+  }
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+static int launch_wgrad_reduce(const float* partials, const int32_t* cstart_or_null, int64_t splits, int K,
+                               int Cin, int Cout, void* dW, int dw_dtype, hipStream_t stream) {
+  const int64_t per_k = (int64_t)Cin * Cout;
+  const unsigned gr = st_blocks(per_k * K, 256);
+#define ST_REDUCE(TW)                                                                                        \
+  if (cstart_or_null)                                                                                        \
+    wgrad_pairs_reduce_kernel<TW><<<gr, 256, 0, stream>>>(partials, cstart_or_null, per_k, K, (TW*)dW);      \
+  else                                                                                                       \
+    wgrad_reduce_kernel<TW><<<gr, 256, 0, stream>>>(partials, per_k, (int)splits, K, (TW*)dW);
+  switch (dw_dtype) {
+    case ST_F32:
+      ST_REDUCE(float);
+      break;
+    case ST_F16:
+      ST_REDUCE(_Float16);
+      break;
+    case ST_BF16:
+      ST_REDUCE(__bf16);
+      break;
+    default:
+      return ST_ERR_UNSUPPORTED;
+  }
+#undef ST_REDUCE
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+template <typename T, typename Src>
+static int launch_wgrad(const T* X, int64_t n_in, const T* dY, const Src& src, int64_t n_out, int K, int Cin,
+                        int Cout, float* partials, int64_t splits, void* dW, int dw_dtype, hipStream_t stream) {
+  constexpr int VEC = Frag<T>::VEC;
+  const int vec_x = (Cin % VEC == 0) && ((uintptr_t)X % 16 == 0);
+  const int vec_y = (Cout % VEC == 0) && ((uintptr_t)dY % 16 == 0);
+  const int64_t rows_per_split = (n_out + splits - 1) / splits;
+  const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
+  const unsigned gz = (unsigned)(((MB + kWgTileBlk - 1) / kWgTileBlk) * ((NB + kWgTileBlk - 1) / kWgTileBlk));
+  if (n_out > 0) {
+    wgrad_kernel<T, Src><<<dim3((unsigned)splits, (unsigned)K, gz), 256, 0, stream>>>(
+        X, dY, src, n_in, n_out, Cin, Cout, rows_per_split, (int)splits, partials, vec_x, vec_y);
+    ST_CHECK_LAUNCH();
+  } else {
+    const int rc = st_fill_u32((uint32_t*)partials, (int64_t)K * splits * Cin * Cout, 0u, stream);
+    if (rc != ST_OK) return rc;
+  }
+  return launch_wgrad_reduce(partials, nullptr, splits, K, Cin, Cout, dW, dw_dtype, stream);
+}
+
+template <int MT, int NT>
+static void launch_wgrad_pairs_f32(const float* X, const float* dY, const int2* pairs, const int32_t* kstart,
+                                   const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
+                                   float* partials, hipStream_t stream) {
+  const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
+  const int WT = ((MB + MT - 1) / MT) * ((NB + NT - 1) / NT);
+  const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
+  wgrad_pairs_f32_kernel<MT, NT><<<dim3(gx, 1, (unsigned)((WT + 3) / 4)), 256, 0, stream>>>(
+      X, dY, pairs, kstart, cstart, K, chunk, Cin, Cout, partials);
+}
+
+static int pow2_tile(int blocks) { return blocks >= 4 ? 4 : (blocks >= 2 ? 2 : 1); }
+
+template <typename T>
+int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
+                    int K, int chunk, int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
+                    hipStream_t stream) {
+  if (max_chunks > 0) {
+    if constexpr (sizeof(T) == 4) {
+      const int mt = pow2_tile((Cin + 15) / 16), nt = pow2_tile((Cout + 15) / 16);
+      const int2* pr = reinterpret_cast<const int2*>(pairs);
+#define ST_WP(A, B)                                                                                                 \
+  if (mt == A && nt == B)                                                                                           \
+    launch_wgrad_pairs_f32<A, B>((const float*)X, (const float*)dY, pr, kstart, cstart, K, chunk, max_chunks, Cin, \
+                                 Cout, partials, stream);
+      ST_WP(1, 1) ST_WP(1, 2) ST_WP(1, 4) ST_WP(2, 1) ST_WP(2, 2) ST_WP(2, 4) ST_WP(4, 1) ST_WP(4, 2) ST_WP(4, 4)
+#undef ST_WP
+    } else {
+      constexpr int VEC = Frag<T>::VEC;
+      const int vec_x = (Cin % VEC == 0) && ((uintptr_t)X % 16 == 0);
+      const int vec_y = (Cout % VEC == 0) && ((uintptr_t)dY % 16 == 0);
+      const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
+      const unsigned gz = (unsigned)(((MB + 7) / 8) * ((NB + 7) / 8));
+      const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
+      const int nloc = (MB < 8 ? MB : 8) * (NB < 8 ? NB : 8);
+      const int2* pr = reinterpret_cast<const int2*>(pairs);
+      if (nloc <= 4)
+        wgrad_pairs_lds_kernel<T, 1><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+                                                                          Cout, partials, vec_x, vec_y);
+      else if (nloc <= 16)
+        wgrad_pairs_lds_kernel<T, 4><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+                                                                          Cout, partials, vec_x, vec_y);
+      else
+        wgrad_pairs_lds_kernel<T, 16><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+                                                                           Cout, partials, vec_x, vec_y);
+    }
+    ST_CHECK_LAUNCH();
+  }
+  return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
+}
+
+template <typename T>
+int ops_gather_map(const T* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs, const uint32_t* masks, int W,
+                   const int32_t* rows, const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd,
+                   hipStream_t stream) {
+  MapSrc src{map, ks, rs};
+  return launch_gather<T>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, stream);
+}
+
+template <typename CT>
+static HashSrc<CT> make_hash_src(const void* coords, const int32_t* offsets, const st_lookup* lk, const uint64_t* keys,
+                                 const uint32_t* vals, int64_t cap) {
+  return HashSrc<CT>{(const CT*)coords, offsets,       keys,          vals,          (uint32_t)cap,
+                     lk->sign,          lk->mul,       lk->div,       lk->bounds[0], lk->bounds[1],
+                     lk->bounds[2],     lk->row_bounds[0], lk->row_bounds[1], lk->row_bounds[2]};
+}
+
+template <typename T>
+int ops_gather_hash(const T* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
+                    const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const T* Bt, T* out,
+                    int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
+  const int W = (lk->K + 31) / 32;
+  if (coord_dtype == ST_COORD_I16)
+    return launch_gather<T>(A, n_src, make_hash_src<int16_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
+                            nullptr, Bt, out, n_dst, lk->K, Kd, Nd, stream);
+  if (coord_dtype == ST_COORD_I32)
+    return launch_gather<T>(A, n_src, make_hash_src<int32_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
+                            nullptr, Bt, out, n_dst, lk->K, Kd, Nd, stream);
+  return ST_ERR_UNSUPPORTED;
+}
+
+template <typename T>
+int ops_wgrad_map(const T* X, int64_t n_in, const T* dY, const int32_t* map, int64_t ks, int64_t rs, int64_t n_out,
+                  int K, int Cin, int Cout, float* partials, int64_t splits, void* dW, int dw_dtype,
+                  hipStream_t stream) {
+  MapSrc src{map, ks, rs};
+  return launch_wgrad<T>(X, n_in, dY, src, n_out, K, Cin, Cout, partials, splits, dW, dw_dtype, stream);
+}
+
+template <typename T>
+int ops_wgrad_hash(const T* X, int64_t n_in, const T* dY, const void* coords, int coord_dtype, int64_t n_out,
+                   const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,
+                   int64_t cap, int Cin, int Cout, float* partials, int64_t splits, void* dW, int dw_dtype,
+                   hipStream_t stream) {
+  if (coord_dtype == ST_COORD_I16)
+    return launch_wgrad<T>(X, n_in, dY, make_hash_src<int16_t>(coords, offsets, lk, keys, vals, cap), n_out, lk->K,
+                           Cin, Cout, partials, splits, dW, dw_dtype, stream);
+  if (coord_dtype == ST_COORD_I32)
+    return launch_wgrad<T>(X, n_in, dY, make_hash_src<int32_t>(coords, offsets, lk, keys, vals, cap), n_out, lk->K,
+                           Cin, Cout, partials, splits, dW, dw_dtype, stream);
+  return ST_ERR_UNSUPPORTED;
+}
+
+template <typename T>
+int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipStream_t stream) {
+  const int64_t total = (int64_t)K * Cin * Cout;
+  weight_prep_kernel<T><<<st_blocks(total, 256), 256, 0, stream>>>(w, out, K, Cin, Cout, mode);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+}  // namespace st
+
+// Declares (X = extern) or instantiates (X empty) every typed launcher for T.
+#define ST_GEMM_OPS(X, T)                                                                                            \
+  namespace st {                                                                                                     \
+  X template int ops_gather_map<T>(const T*, int64_t, const int32_t*, int64_t, int64_t, const uint32_t*, int,        \
+                                   const int32_t*, const T*, T*, int64_t, int, int, int, hipStream_t);              \
+  X template int ops_gather_hash<T>(const T*, int64_t, const void*, int, const int32_t*, const st_lookup*,            \
+                                    const uint64_t*, const uint32_t*, int64_t, const T*, T*, int64_t, int, int,      \
+                                    hipStream_t);                                                                    \
+  X template int ops_wgrad_map<T>(const T*, int64_t, const T*, const int32_t*, int64_t, int64_t, int64_t, int, int,  \
+                                  int, float*, int64_t, void*, int, hipStream_t);                                    \
+  X template int ops_wgrad_hash<T>(const T*, int64_t, const T*, const void*, int, int64_t, const int32_t*,           \
+                                   const st_lookup*, const uint64_t*, const uint32_t*, int64_t, int, int, float*,    \
+                                   int64_t, void*, int, hipStream_t);                                                \
+  X template int ops_wgrad_pairs<T>(const T*, const T*, const int32_t*, const int32_t*, const int32_t*, int, int,    \
+                                    int64_t, int, int, float*, void*, int, hipStream_t);                             \
+  X template int ops_weight_prep<T>(const T*, T*, int, int, int, int, hipStream_t);                                  \
+  }

@@ -374,3 +374,126 @@ extern "C" int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t 
   ST_CHECK_LAUNCH();
   return ST_OK;
 }
+
+// ------------------------------------------------- tile-order map and pairs
+
+namespace st {
+
+// map_out[k][r] = map[k][perm[r]], masks_out[r] = masks[perm[r]]: the map in
+// the order the gather-GEMM tiles rows, so its per-offset reads are coalesced.
+__global__ __launch_bounds__(256) void kmap_permute_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
+                                                           int64_t n, int K, const uint32_t* __restrict__ masks, int W,
+                                                           const int32_t* __restrict__ perm,
+                                                           int32_t* __restrict__ map_out,
+                                                           uint32_t* __restrict__ masks_out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const int64_t src = perm[r];
+  for (int k = 0; k < K; ++k) map_out[(int64_t)k * n + r] = map[(int64_t)k * ks + src * rs];
+  for (int w = 0; w < W; ++w) masks_out[r * W + w] = masks[src * W + w];
+}
+
+constexpr int kPairRows = 1024;  // map rows per pair-compaction workgroup (4 per thread)
+
+__device__ __forceinline__ bool pair_valid(int32_t i, int64_t n_in) { return i >= 0 && (int64_t)i < n_in; }
+
+// counts[k * nb + b] = valid entries of map column k in rows [b*1024, b*1024+1024)
+__global__ __launch_bounds__(256) void pairs_count_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
+                                                          int64_t n_out, int64_t n_in, int64_t nb,
+                                                          int32_t* __restrict__ counts) {
+  __shared__ int red[4];
+  const int k = blockIdx.y;
+  const int64_t base = (int64_t)blockIdx.x * kPairRows + threadIdx.x * 4;
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t o = base + j;
+    if (o < n_out) cnt += pair_valid(map[(int64_t)k * ks + o * rs], n_in);
+  }
+  cnt = wave_sum(cnt);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[(int64_t)k * nb + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// kstart[k] = first pair of offset k (kstart[K] = P); cstart[k] = first chunk of
+// offset k, chunks of `chunk` pairs never straddling two offsets.
+__global__ void pairs_finalize_kernel(const int32_t* __restrict__ counts, int64_t nb, int K, int chunk,
+                                      int32_t* __restrict__ kstart, int32_t* __restrict__ cstart) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int32_t c = 0;
+  for (int k = 0; k < K; ++k) {
+    const int32_t s = counts[(int64_t)k * nb];
+    const int32_t e = (k + 1 < K) ? counts[(int64_t)(k + 1) * nb] : counts[(int64_t)K * nb];
+    kstart[k] = s;
+    cstart[k] = c;
+    c += (e - s + chunk - 1) / chunk;
+  }
+  kstart[K] = counts[(int64_t)K * nb];
+  cstart[K] = c;
+}
+
+__global__ __launch_bounds__(256) void pairs_emit_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
+                                                         int64_t n_out, int64_t n_in, int64_t nb,
+                                                         const int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ pairs) {
+  __shared__ int scratch[5];
+  const int k = blockIdx.y;
+  const int64_t base = (int64_t)blockIdx.x * kPairRows + threadIdx.x * 4;
+  int32_t v[4];
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t o = base + j;
+    v[j] = o < n_out ? map[(int64_t)k * ks + o * rs] : -1;
+    cnt += pair_valid(v[j], n_in);
+  }
+  int tot;
+  int pos = offsets[(int64_t)k * nb + blockIdx.x] + block_exclusive_scan(cnt, scratch, &tot);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (pair_valid(v[j], n_in)) {
+      pairs[2 * (int64_t)pos] = v[j];
+      pairs[2 * (int64_t)pos + 1] = (int32_t)(base + j);
+      ++pos;
+    }
+}
+
+}  // namespace st
+
+extern "C" int st_kmap_permute(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n, int K,
+                               const uint32_t* masks, int mask_words, const int32_t* perm, int32_t* map_out,
+                               uint32_t* masks_out, st_stream_t stream) {
+  if (n < 0 || n >= (1ll << 31) || K <= 0 || K > ST_MAX_KVOL || mask_words != (K + 31) / 32) return ST_ERR_ARG;
+  if (n == 0) return ST_OK;
+  if (!map || !masks || !perm || !map_out || !masks_out) return ST_ERR_ARG;
+  st::kmap_permute_kernel<<<st_blocks(n, 256), 256, 0, stream>>>(map, map_k_stride, map_r_stride, n, K, masks,
+                                                                 mask_words, perm, map_out, masks_out);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+extern "C" int st_kmap_pairs_sizes(int64_t n_out, int K, int64_t* num_blocks) {
+  if (n_out < 0 || K <= 0 || K > ST_MAX_KVOL || !num_blocks) return ST_ERR_ARG;
+  *num_blocks = (n_out + st::kPairRows - 1) / st::kPairRows;
+  return ST_OK;
+}
+
+extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n_out, int K,
+                             int64_t n_in, int32_t* block_counts, int64_t num_blocks, int chunk, int32_t* kstart,
+                             int32_t* cstart, int32_t* pairs, int64_t pair_capacity, st_stream_t stream) {
+  if (n_out < 0 || n_in < 0 || K <= 0 || K > ST_MAX_KVOL || chunk <= 0) return ST_ERR_ARG;
+  if (num_blocks != (n_out + st::kPairRows - 1) / st::kPairRows) return ST_ERR_ARG;
+  if ((int64_t)K * n_out >= (1ll << 31) || pair_capacity < (int64_t)K * n_out) return ST_ERR_ARG;
+  if (!block_counts || !kstart || !cstart || (n_out > 0 && (!map || !pairs))) return ST_ERR_ARG;
+  if (num_blocks > 0)
+    st::pairs_count_kernel<<<dim3((unsigned)num_blocks, (unsigned)K), 256, 0, stream>>>(
+        map, map_k_stride, map_r_stride, n_out, n_in, num_blocks, block_counts);
+  st::exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, (int64_t)K * num_blocks);
+  st::pairs_finalize_kernel<<<1, 64, 0, stream>>>(block_counts, num_blocks, K, chunk, kstart, cstart);
+  if (num_blocks > 0)
+    st::pairs_emit_kernel<<<dim3((unsigned)num_blocks, (unsigned)K), 256, 0, stream>>>(
+        map, map_k_stride, map_r_stride, n_out, n_in, num_blocks, block_counts, pairs);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}

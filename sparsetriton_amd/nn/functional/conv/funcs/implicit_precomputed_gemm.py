@@ -12,10 +12,12 @@ reference's (N_out, K) int32 tensor (any strides) or a ``KernelMap`` built by
 this package (which also carries row masks and the transposed map).
 
 Kernels (``libsparsetriton_amd.so``):
-  forward   st_gather_gemm over nbr with weights re-laid (K, C_out, C_in);
-  dgrad     st_gather_gemm over the transposed map with weights as stored
-            -- a gather, so no atomics and a deterministic result;
-  wgrad     st_wgrad, per-offset pair compaction + MFMA, fixed-order reduce.
+  forward   st_gather_gemm over the map in mask-sorted tile order, weights
+            re-laid (K, C_out, C_in);
+  dgrad     st_gather_gemm over the transposed map (also mask-sorted), weights
+            as stored -- a gather, so no atomics and a deterministic result;
+  wgrad     st_wgrad_pairs over the (offset, out)-sorted pair list in
+            equal-size chunks, fixed-order reduce.
 """
 
 import torch
@@ -38,16 +40,21 @@ def _as_kmap(neighbor_indices, n_in: int) -> KernelMap:
 
 
 def gather_gemm(A: torch.Tensor, map_t: torch.Tensor, k_stride: int, r_stride: int, masks, Bt: torch.Tensor,
-                n_dst: int, K: int) -> torch.Tensor:
-    """out (n_dst, Nd) = sum_k A[map[k, r]] @ Bt[k]^T on the GPU."""
+                n_dst: int, K: int, rows=None) -> torch.Tensor:
+    """out[rows[r]] = sum_k A[map[k, r]] @ Bt[k]^T on the GPU (rows = identity when None)."""
     Kd = A.shape[1]
     Nd = Bt.shape[1]
     out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
     W = (K + 31) // 32
     _lib.call("st_gather_gemm", _lib.ptr(A), A.shape[0], _lib.ptr(map_t), k_stride, r_stride,
-              _lib.ptr(masks), W, None, _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd, _lib.feat_code(A.dtype),
-              _lib.stream_of(A.device))
+              _lib.ptr(masks), W, _lib.ptr(rows), _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd,
+              _lib.feat_code(A.dtype), _lib.stream_of(A.device))
     return out
+
+
+def gather_gemm_plan(A: torch.Tensor, plan, Bt: torch.Tensor, n_dst: int, K: int) -> torch.Tensor:
+    """gather_gemm over a mask-sorted TilePlan."""
+    return gather_gemm(A, plan.map, n_dst, 1, plan.masks, Bt, n_dst, K, rows=plan.perm)
 
 
 def weight_prep(weights: torch.Tensor, mode: int) -> torch.Tensor:
@@ -60,6 +67,19 @@ def weight_prep(weights: torch.Tensor, mode: int) -> torch.Tensor:
 
 
 def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype) -> torch.Tensor:
+    """dW[k] = sum over pairs (i, o) of offset k of X[i]^T dY[o], over the map's pair list."""
+    K, C_in, C_out = kmap.K, X.shape[1], dY.shape[1]
+    pl = kmap.pair_list()
+    partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
+    dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
+    _lib.call("st_wgrad_pairs", _lib.ptr(X), _lib.ptr(dY), _lib.ptr(pl.pairs), _lib.ptr(pl.kstart),
+              _lib.ptr(pl.cstart), K, pl.chunk, pl.max_chunks, C_in, C_out, _lib.feat_code(X.dtype),
+              _lib.ptr(partials), _lib.ptr(dW), _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
+    return dW
+
+
+def wgrad_scan(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype) -> torch.Tensor:
+    """Weight gradient that compacts map columns on the fly (no pair list; st_wgrad)."""
     K, C_in, C_out = kmap.K, X.shape[1], dY.shape[1]
     splits = wgrad_splits(kmap.n_out)
     partials = torch.empty((K * splits * C_in * C_out,), dtype=torch.float32, device=X.device)
@@ -85,7 +105,7 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
         features = features.contiguous()
         w = weights.to(features.dtype).contiguous()
         wt = weight_prep(w, _lib.W_TRANSPOSE)
-        out = gather_gemm(features, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, wt, kmap.n_out, K)
+        out = gather_gemm_plan(features, kmap.forward_plan(), wt, kmap.n_out, K)
         ctx.save_for_backward(features, weights)
         ctx.kmap = kmap
         return out
@@ -97,10 +117,9 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
         grad_output = grad_output.to(features.dtype).contiguous()
         grad_input = grad_weights = None
         if ctx.needs_input_grad[0]:
-            kmap.ensure_inverse()
             w = weights.to(features.dtype).contiguous()
             # dX[i] = sum_k dY[invnbr[k, i]] @ W[k]^T: W[k] (C_in, C_out) is already the (Nd, Kd) operand.
-            grad_input = gather_gemm(grad_output, kmap.invnbr, kmap.n_in, 1, kmap.in_masks, w, kmap.n_in, kmap.K)
+            grad_input = gather_gemm_plan(grad_output, kmap.backward_plan(), w, kmap.n_in, kmap.K)
         if ctx.needs_input_grad[1]:
             grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
         return grad_input, grad_weights, None

@@ -32,6 +32,8 @@ __all__ = [
     "compute_target_offsets_transposed",
     "build_out_coords",
     "KernelMap",
+    "TilePlan",
+    "PairList",
     "out_spatial_shape",
 ]
 
@@ -105,6 +107,9 @@ class KernelMap:
         self.out_masks = out_masks
         self.invnbr = invnbr
         self.in_masks = in_masks
+        self._fwd = None
+        self._bwd = None
+        self._pairs = {}
 
     @classmethod
     def from_neighbor_indices(cls, neighbor_indices: torch.Tensor, n_in: int) -> "KernelMap":
@@ -145,6 +150,36 @@ class KernelMap:
             self.ensure_inverse()
         return self
 
+    # ------------------------------------------------------------ GEMM plans
+    def forward_plan(self) -> "TilePlan":
+        """Output rows in mask-sorted tile order, with the map and masks laid out in that order."""
+        if self._fwd is None:
+            self.ensure_out_masks()
+            self._fwd = TilePlan.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.out_masks)
+        return self._fwd
+
+    def backward_plan(self) -> "TilePlan":
+        """Input rows in mask-sorted tile order over the transposed map (for the input gradient)."""
+        if self._bwd is None:
+            self.ensure_inverse()
+            self._bwd = TilePlan.build(self.invnbr, self.n_in, 1, self.n_in, self.K, self.in_masks)
+        return self._bwd
+
+    def pair_list(self, chunk: int = 2048) -> "PairList":
+        """(in, out) pairs sorted by (offset, out) with equal-size chunks, for the weight gradient."""
+        pl = self._pairs.get(chunk)
+        if pl is None:
+            pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)
+            self._pairs[chunk] = pl
+        return pl
+
+    def prepare(self) -> "KernelMap":
+        """Build everything forward and backward need (idempotent)."""
+        self.forward_plan()
+        self.backward_plan()
+        self.pair_list()
+        return self
+
     def num_pairs(self) -> int:
         """Number of valid (input, output, offset) triples (synchronises)."""
         return int((self.neighbor_indices >= 0).sum().item())
@@ -156,6 +191,56 @@ class KernelMap:
         t = torch.stack([nb[o, k], o, k], dim=1)
         key = (t[:, 0] * (self.n_out + 1) + t[:, 1]) * (self.K + 1) + t[:, 2]
         return t[torch.argsort(key)]
+
+
+class TilePlan:
+    """A map in gather-GEMM tile order: ``map`` (K, n) and ``masks`` (n, W) indexed by tile row,
+    ``perm`` (n) the destination row of each tile row (rows sorted by offset bitmask)."""
+
+    def __init__(self, map_t: torch.Tensor, masks: torch.Tensor, perm: torch.Tensor):
+        self.map, self.masks, self.perm = map_t, masks, perm
+
+    @classmethod
+    def build(cls, map_t, k_stride, r_stride, n, K, masks) -> "TilePlan":
+        dev = map_t.device
+        W = _mask_words(K)
+        s = _lib.stream_of(dev)
+        nbytes = ctypes.c_size_t()
+        _lib.call("st_kmap_sort_workspace", n, ctypes.byref(nbytes))
+        ws = torch.empty((max(nbytes.value, 1),), dtype=torch.uint8, device=dev)
+        keys = torch.empty((2 * n,), dtype=torch.int32, device=dev)
+        rows = torch.empty((n,), dtype=torch.int32, device=dev)
+        perm = torch.empty((n,), dtype=torch.int32, device=dev)
+        _lib.call("st_kmap_sort_rows", _lib.ptr(masks), W, K, n, _lib.ptr(keys), _lib.ptr(rows), _lib.ptr(perm),
+                  _lib.ptr(ws), nbytes.value, s)
+        map_out = torch.empty((K, n), dtype=torch.int32, device=dev)
+        masks_out = torch.empty((n, W), dtype=torch.int32, device=dev)
+        _lib.call("st_kmap_permute", _lib.ptr(map_t), k_stride, r_stride, n, K, _lib.ptr(masks), W, _lib.ptr(perm),
+                  _lib.ptr(map_out), _lib.ptr(masks_out), s)
+        return cls(map_out, masks_out, perm)
+
+
+class PairList:
+    """(in, out) int32 pairs sorted by (offset, out); ``kstart`` / ``cstart`` (K + 1) the first pair /
+    chunk of each offset; ``max_chunks`` bounds the chunk count without reading it back."""
+
+    def __init__(self, pairs, kstart, cstart, chunk, max_chunks):
+        self.pairs, self.kstart, self.cstart = pairs, kstart, cstart
+        self.chunk, self.max_chunks = chunk, max_chunks
+
+    @classmethod
+    def build(cls, map_t, k_stride, r_stride, n_out, K, n_in, chunk) -> "PairList":
+        dev = map_t.device
+        nb = ctypes.c_int64()
+        _lib.call("st_kmap_pairs_sizes", n_out, K, ctypes.byref(nb))
+        cap = K * n_out
+        counts = torch.empty((K * nb.value + 1,), dtype=torch.int32, device=dev)
+        kstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
+        cstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
+        pairs = torch.empty((2 * max(cap, 1),), dtype=torch.int32, device=dev)
+        _lib.call("st_kmap_pairs", _lib.ptr(map_t), k_stride, r_stride, n_out, K, n_in, _lib.ptr(counts), nb.value,
+                  int(chunk), _lib.ptr(kstart), _lib.ptr(cstart), _lib.ptr(pairs), cap, _lib.stream_of(dev))
+        return cls(pairs, kstart, cstart, int(chunk), cap // int(chunk) + K)
 
 
 # ----------------------------------------------------------------- builders

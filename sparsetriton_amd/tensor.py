@@ -110,8 +110,19 @@ class SparseTensor:
         return to_dense(self.feats, self.coords, self.spatial_shape)
 
     def replace(self, feats: torch.Tensor) -> "SparseTensor":
-        """Same coordinates, shape, batch size and cache with new features."""
-        return SparseTensor(feats, self.coords, self.spatial_shape, self.batch_size, self._cache)
+        """Same coordinates, shape, batch size and cache with new features.
+
+        The coordinates were validated when this tensor was built, so no
+        device reduction (and no host synchronisation) happens here.
+        """
+        assert feats.ndim == 2 and feats.shape[0] == self.coords.shape[0], "The number of features and coordinates must match."
+        out = SparseTensor.__new__(SparseTensor)
+        out.feats = feats
+        out.coords = self.coords if self.coords.device == feats.device else self.coords.to(feats.device)
+        out.spatial_shape = self.spatial_shape
+        out.batch_size = self.batch_size
+        out._cache = self._cache
+        return out
 
     def __repr__(self) -> str:
         return (

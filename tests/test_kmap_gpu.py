@@ -214,3 +214,56 @@ def test_config3_config4_maps_exact(device, cfg2):
     assert tuple(ns4) == ns4o == (1439, 1439, 41)
     assert (out4.cpu().numpy() == oc4).all()
     assert (kmap4.neighbor_indices.cpu().numpy() == nbr4).all()
+
+
+# ------------------------------------------------- tile plans and pair lists
+
+def test_tile_plan_and_pair_list(device):
+    rng = np.random.default_rng(31)
+    c = _rand_coords(rng, 5000, 24)
+    kmap = _subm(device, c, (24, 24, 24))
+    nbr = kmap.nbr.cpu().numpy()  # (K, N)
+    K, N = nbr.shape
+    for plan, m, masks in ((kmap.forward_plan(), nbr, kmap.out_masks), (kmap.backward_plan(), None, None)):
+        if m is None:
+            m = kmap.invnbr.cpu().numpy()
+            masks = kmap.in_masks
+        perm = plan.perm.cpu().numpy()
+        assert np.array_equal(np.sort(perm), np.arange(N))
+        mk = masks.cpu().numpy()[:, 0].astype(np.uint32)
+        sorted_keys = mk[perm]
+        assert (np.diff(sorted_keys.astype(np.int64)) >= 0).all()  # stable radix order by mask
+        # stability: equal keys keep ascending row order
+        same = sorted_keys[1:] == sorted_keys[:-1]
+        assert (perm[1:][same] > perm[:-1][same]).all()
+        assert np.array_equal(plan.map.cpu().numpy(), m[:, perm])
+        assert np.array_equal(plan.masks.cpu().numpy()[:, 0].astype(np.uint32), mk[perm])
+    pl = kmap.pair_list(chunk=100)
+    ks = pl.kstart.cpu().numpy()
+    cs = pl.cstart.cpu().numpy()
+    P = int(ks[-1])
+    pairs = pl.pairs.cpu().numpy()[: 2 * P].reshape(-1, 2)
+    expect = []
+    for k in range(K):
+        o = np.nonzero(nbr[k] >= 0)[0]
+        expect.append(np.stack([nbr[k, o], o], 1))
+        assert ks[k + 1] - ks[k] == o.shape[0]
+        assert cs[k + 1] - cs[k] == (o.shape[0] + 99) // 100
+    assert np.array_equal(pairs, np.concatenate(expect))
+    assert cs[-1] <= pl.max_chunks
+
+
+def test_wgrad_scan_matches_pairs(device):
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import wgrad, wgrad_scan
+    rng = np.random.default_rng(32)
+    c = _rand_coords(rng, 6000, 24)
+    kmap = _subm(device, c, (24, 24, 24))
+    for dtype in (torch.float32, torch.bfloat16):
+        X = torch.randn(6000, 32, device=device, dtype=dtype)
+        dY = torch.randn(6000, 48, device=device, dtype=dtype)
+        a = wgrad(X, dY, kmap, torch.float32)
+        b = wgrad_scan(X, dY, kmap, torch.float32)
+        ref = O.wgrad_f64(X.float().cpu().numpy(), dY.float().cpu().numpy(), kmap.neighbor_indices.cpu().numpy(), 27)
+        for r in (a, b):
+            err = np.linalg.norm(r.cpu().numpy() - ref) / np.linalg.norm(ref)
+            assert err < (2e-3 if dtype == torch.float32 else 2e-2)
