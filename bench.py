@@ -112,7 +112,8 @@ def main():
     from sparsetriton_amd.nn.functional import sparse_conv3d
     from sparsetriton_amd.nn.functional.conv.conv import table_capacity
     from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
-        gather_gemm_plan,
+        gather_gemm_dgrad,
+        gather_gemm_fwd,
         weight_prep,
         wgrad,
     )
@@ -195,9 +196,8 @@ def main():
     # ---------------------------------------------- per-kernel (events) timing
     wt = weight_prep(w.detach(), _lib.W_TRANSPOSE)
     wd = w.detach().contiguous()
-    fplan, bplan = kmap.forward_plan(), kmap.backward_plan()
-    fwd_t = _events(torch, lambda: gather_gemm_plan(X, fplan, wt, N, 27), 30)
-    dgrad_t = _events(torch, lambda: gather_gemm_plan(dY, bplan, wd, N, 27), 30)
+    fwd_t = _events(torch, lambda: gather_gemm_fwd(X, kmap, wt), 30)
+    dgrad_t = _events(torch, lambda: gather_gemm_dgrad(dY, kmap, wd), 30)
     wgrad_t = _events(torch, lambda: wgrad(X, dY, kmap, w.dtype), 30)
     kern = {"gather_gemm_fwd": float(np.mean(fwd_t)), "gather_gemm_dgrad": float(np.mean(dgrad_t)),
             "wgrad(+reduce)": float(np.mean(wgrad_t))}

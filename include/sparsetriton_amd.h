@@ -104,7 +104,9 @@ int st_hash_query(const void* coords, int coord_dtype, int64_t m, const uint64_t
  *   nbr[k * nbr_k_stride + o * nbr_r_stride] = row of q in the table if
  *       0 <= q < shape (per axis) and present, else -1.
  * row_masks (n_out, ceil(K/32)) u32, optional: bit k set iff nbr[o, k] >= 0.
- * The default layout is offset-major (nbr_k_stride = n_out, nbr_r_stride = 1).
+ * The package uses the reference's row-major (n_out, K) layout
+ * (nbr_k_stride = 1, nbr_r_stride = K): a row's offsets share cache lines,
+ * which is what the mask-sorted gather-GEMM reads.
  */
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
@@ -147,9 +149,9 @@ int st_outcoords_plan(const void* in_coords, int coord_dtype, int64_t n, const i
  * Writes out_coords (N_out, 4) in the input's coordinate dtype, ordered by
  * first occurrence in the candidate order; slot_out (dcap u32) maps dedup
  * slots to output rows (so dkeys + slot_out form the output-coordinate
- * table); and the kernel map in both directions, offset-major:
- *   nbr    (K, N_out): input row feeding output o through offset k, or -1
- *   invnbr (K, n)    : output row fed by input i through offset k, or -1
+ * table); and the kernel map in both directions, row-major:
+ *   nbr    (N_out, K): input row feeding output o through offset k, or -1
+ *   invnbr (n, K)    : output row fed by input i through offset k, or -1
  * plus row masks out_masks (N_out, W) and in_masks (n, W), W = ceil(K/32).
  * nbr/invnbr must be pre-filled with -1 and the masks with 0 by the caller.
  * With nbr == NULL only out_coords and slot_out are written (hash-fly mode).
@@ -166,7 +168,7 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
 
 /*
  * Transposed kernel map of an arbitrary map nbr (k, o) -> i (strides as in
- * st_kmap_query): invnbr[k * n_in + i] = o, in_masks (n_in, W) row masks of
+ * st_kmap_query): invnbr[i * K + k] = o (row-major), in_masks (n_in, W) row masks of
  * invnbr, and, if out_masks is non-null, out_masks (n_out, W) row masks of
  * nbr.  invnbr must be pre-filled with -1 and in_masks with 0.  Used when a
  * caller hands ConvPrecomputedNeighborGEMM a plain (N_out, K) map
@@ -187,15 +189,6 @@ int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_strid
 int st_kmap_sort_workspace(int64_t n, size_t* bytes);
 int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp, int32_t* rows_tmp,
                       int32_t* perm, void* workspace, size_t workspace_bytes, st_stream_t stream);
-
-/*
- * The map in tile order: map_out[k * n + r] = map(k, perm[r]) and
- * masks_out[r] = masks[perm[r]], so the gather-GEMM reads each offset's
- * column with coalesced loads.
- */
-int st_kmap_permute(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n, int K,
-                    const uint32_t* masks, int mask_words, const int32_t* perm, int32_t* map_out, uint32_t* masks_out,
-                    st_stream_t stream);
 
 /*
  * Pair list of a kernel map for the weight gradient (replaces the per-tile
@@ -227,13 +220,13 @@ int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mod
  * here a gather with no atomics):
  *   out[r, :] = sum over k of A[map(k, r), :] @ Bt[k]^T  (map < 0 or >= n_src adds 0)
  * A (n_src, Kd), Bt (K, Nd, Kd), out (n_dst, Nd), all of `dtype`, fp32
- * accumulation on MFMA.  Rows are processed in tile order r = 0..n_dst-1:
- * map(k, r) = map[k * map_k_stride + r * map_r_stride] and row_masks (n_dst,
- * mask_words, optional) are indexed by r, and perm (optional) sends tile row r
- * to output row perm[r] (identity when NULL) -- the mask-sorted order from
- * st_kmap_sort_rows / st_kmap_permute.  Offsets no row of a 128-row tile has
- * are skipped by the workgroup, offsets no row of a 32-row wave slab has by
- * that wave.
+ * accumulation on MFMA.  map(k, r) = map[k * map_k_stride + r * map_r_stride]
+ * and row_masks (n_dst, mask_words, optional) are indexed by destination row.
+ * perm (optional) is the order destination rows are tiled in -- tile row t is
+ * row perm[t] -- normally the mask-sorted order from st_kmap_sort_rows, so
+ * rows sharing their offsets share MFMA slabs.  Offsets no row of a 128-row
+ * tile has are skipped by the workgroup, offsets no row of a 32-row slab has
+ * by that wave.
  */
 int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
                    const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, void* out,

@@ -67,7 +67,6 @@ _SIGNATURES = {
     "st_kmap_invert": [_P, _L, _L, _L, _I, _L, _P, _P, _P, _P],
     "st_kmap_sort_workspace": [_L, ctypes.POINTER(ctypes.c_size_t)],
     "st_kmap_sort_rows": [_P, _I, _I, _L, _P, _P, _P, _P, ctypes.c_size_t, _P],
-    "st_kmap_permute": [_P, _L, _L, _L, _I, _P, _I, _P, _P, _P, _P],
     "st_kmap_pairs_sizes": [_L, _I, ctypes.POINTER(_L)],
     "st_kmap_pairs": [_P, _L, _L, _L, _I, _L, _P, _L, _I, _P, _P, _P, _L, _P],
     "st_wgrad_pairs": [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _I, _P],

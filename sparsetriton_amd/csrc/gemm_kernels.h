@@ -27,6 +27,7 @@
 namespace st {
 
 constexpr int kGemmBM = 128;
+constexpr int kSrcGroup = 32;  // offsets whose source rows are resolved into LDS at once
 
 template <typename T, int BN, typename Src>
 __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ A, Src src,
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
   if (masks) {
     for (int w = 0; w < W; ++w) {
       uint32_t v = 0;
-      if (tid < kGemmBM && row0 + tid < n_dst) v = masks[(row0 + tid) * W + w];
+      if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
       v = wave_or(v);
       if (lane == 0 && v) atomicOr(&tmask_s[w], v);
     }
@@ -68,11 +69,11 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
   }
   __syncthreads();
 
-  // Lane (l & 31) resolves tile row wid*32 + (l & 31); MFMA row c of tile m
-  // is then fetched from lane m*16 + c with a shuffle.
-  const int64_t my_r = row0 + wid * 32 + (lane & 31);
-  const bool my_ok = my_r < n_dst;
-  const typename Src::RowCtx rc = src.row(my_ok ? my_r : 0);
+  // Lane (l & 31) resolves tile row wid*32 + (l & 31) (destination row
+  // drow_s[...]); MFMA row c of tile m is then fetched from lane m*16 + c.
+  const int32_t my_row = drow_s[wid * 32 + (lane & 31)];
+  const bool my_ok = my_row >= 0;
+  const typename Src::RowCtx rc = src.row(my_ok ? my_row : 0);
 
   v4f acc[2][NBLK];
 #pragma unroll
@@ -136,8 +137,9 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
 // is built once; for offset i the B slice Bt[k_i] sits in LDS buffer i & 1
 // while Bt[k_{i+1}] and the next offset's A rows are already in flight into
 // registers, so global latency overlaps the MFMAs.  One barrier per offset.
-// The map and row masks are indexed in tile order r; rows[r] is the output
-// row (the mask-sorted permutation) or r itself when rows is null.
+// Tile row r is destination row rows[r] (the mask-sorted permutation) or r
+// itself when rows is null; the map, the row masks and the hash-fly
+// coordinates are indexed by destination row.
 template <typename T, int BN, int KS, typename Src>
 __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
@@ -155,6 +157,7 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
   __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
   __shared__ int32_t drow_s[kGemmBM];
   __shared__ int16_t klist_s[ST_MAX_KVOL];
+  __shared__ int32_t src_s[kSrcGroup][kGemmBM];
   __shared__ int nk_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
   if (masks) {
     for (int w = 0; w < W; ++w) {
       uint32_t v = 0;
-      if (tid < kGemmBM && row0 + tid < n_dst) v = masks[(row0 + tid) * W + w];
+      if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
       v = wave_or(v);
       if (lane == 0 && v) atomicOr(&tmask_s[w], v);
     }
@@ -193,18 +196,24 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
   __syncthreads();
   const int nk = nk_s;
 
-  // Lane (l & 31) resolves tile row wid*32 + (l & 31); MFMA row c of slab m
-  // is fetched from lane m*16 + c.
-  const int64_t my_r = row0 + wid * 32 + (lane & 31);
-  const bool my_ok = my_r < n_dst;
-  const typename Src::RowCtx rc = src.row(my_ok ? my_r : 0);
-
-  auto sources = [&](int k, int32_t& s0, int32_t& s1) -> bool {
-    int32_t s = my_ok ? src.get(rc, k) : -1;
-    if ((int64_t)s >= n_src) s = -1;
-    s0 = __shfl(s, c, 64);
-    s1 = __shfl(s, 16 + c, 64);
-    return __ballot(s >= 0) != 0ull;
+  // Source rows of a group of up to kSrcGroup offsets, resolved for the whole
+  // tile at once (map loads / hash probes all in flight together) into LDS:
+  // thread t owns tile row t & 127 and offsets (t >> 7) + 2j of the group.
+  const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
+  const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
+  auto resolve_group = [&](int g0) {
+    const int ng = min(kSrcGroup, nk - g0);
+    for (int j = tid >> 7; j < ng; j += 2) {
+      int32_t v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+      if ((int64_t)v >= n_src) v = -1;
+      src_s[j][tid & (kGemmBM - 1)] = v;
+    }
+  };
+  auto sources = [&](int i, int32_t& s0, int32_t& s1) -> bool {
+    const int j = i % kSrcGroup;
+    s0 = src_s[j][wid * 32 + c];
+    s1 = src_s[j][wid * 32 + 16 + c];
+    return __ballot(s0 >= 0 || s1 >= 0) != 0ull;
   };
   auto load_a = [&](int32_t s0, int32_t s1, F (&a)[2][KS]) {
 #pragma unroll
@@ -243,18 +252,25 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     F a_cur[2][KS], a_nxt[2][KS];
     F breg[BREGS];
     int32_t s0, s1;
-    bool any_cur = sources(klist_s[0], s0, s1);
-    load_a(s0, s1, a_cur);
+    resolve_group(0);
     load_b(klist_s[0], breg);
     store_b(0, breg);
     __syncthreads();
+    bool any_cur = sources(0, s0, s1);
+    load_a(s0, s1, a_cur);
     for (int i = 0; i < nk; ++i) {
       const bool has_next = i + 1 < nk;
       bool any_nxt = false;
+      if (has_next && (i + 1) % kSrcGroup == 0) {
+        // every wave has read its sources of this group (they are in registers)
+        __syncthreads();
+        resolve_group(i + 1);
+        __syncthreads();
+      }
       if (has_next) {
         const int kn = klist_s[i + 1];
         int32_t t0, t1;
-        any_nxt = sources(kn, t0, t1);
+        any_nxt = sources(i + 1, t0, t1);
         load_a(t0, t1, a_nxt);
         load_b(kn, breg);
       }
@@ -509,15 +525,29 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
   }
 }
 
+// dW[k][e] = sum of partials[c][e] over offset k's chunks.  A 256-thread block
+// covers 32 consecutive elements of one offset; its 8 thread groups take the
+// chunks round-robin and are combined in a fixed order (deterministic).
 template <typename TW>
-__global__ void wgrad_pairs_reduce_kernel(const float* __restrict__ partials, const int32_t* __restrict__ cstart,
-                                          int64_t per_k, int K, TW* __restrict__ dW) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= per_k * K) return;
-  const int64_t k = i / per_k, e = i - k * per_k;
+__global__ __launch_bounds__(256) void wgrad_pairs_reduce_kernel(const float* __restrict__ partials,
+                                                                 const int32_t* __restrict__ cstart, int64_t per_k,
+                                                                 int K, TW* __restrict__ dW) {
+  __shared__ float red[8][32];
+  const int64_t blocks_per_k = (per_k + 31) / 32;
+  const int64_t k = blockIdx.x / blocks_per_k;
+  const int64_t e = (blockIdx.x - k * blocks_per_k) * 32 + (threadIdx.x & 31);
+  const int part = threadIdx.x >> 5;
   float s = 0.f;
-  for (int cidx = cstart[k]; cidx < cstart[k + 1]; ++cidx) s += partials[(int64_t)cidx * per_k + e];
-  dW[i] = from_f32<TW>(s);
+  if (e < per_k)
+    for (int cidx = cstart[k] + part; cidx < cstart[k + 1]; cidx += 8) s += partials[(int64_t)cidx * per_k + e];
+  red[part][threadIdx.x & 31] = s;
+  __syncthreads();
+  if (part == 0 && e < per_k) {
+    float t = red[0][threadIdx.x];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t += red[j][threadIdx.x];
+    dW[k * per_k + e] = from_f32<TW>(t);
+  }
 }
 
 constexpr int kWgQB = 32;       // pairs per MFMA batch
@@ -679,7 +709,7 @@ template <typename T, int KS, typename Src>
 static void launch_pipe_ks(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
                            const int32_t* rows, const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
                            int vec_b, hipStream_t stream) {
-  constexpr int LDS128 = 2 * 128 * (KS * Frag<T>::KSTEP + Frag<T>::VEC) * (int)sizeof(T);
+  constexpr int LDS128 = 2 * 128 * (KS * Frag<T>::KSTEP + Frag<T>::VEC) * (int)sizeof(T) + kSrcGroup * kGemmBM * 4;
   if (Nd <= 16)
     launch_pipe<T, 16, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if (Nd <= 32)
@@ -731,7 +761,8 @@ static int launch_wgrad_reduce(const float* partials, const int32_t* cstart_or_n
   const unsigned gr = st_blocks(per_k * K, 256);
 #define ST_REDUCE(TW)                                                                                        \
   if (cstart_or_null)                                                                                        \
-    wgrad_pairs_reduce_kernel<TW><<<gr, 256, 0, stream>>>(partials, cstart_or_null, per_k, K, (TW*)dW);      \
+    wgrad_pairs_reduce_kernel<TW><<<(unsigned)(K * ((per_k + 31) / 32)), 256, 0, stream>>>(                  \
+        partials, cstart_or_null, per_k, K, (TW*)dW);                                                        \
   else                                                                                                       \
     wgrad_reduce_kernel<TW><<<gr, 256, 0, stream>>>(partials, per_k, (int)splits, K, (TW*)dW);
   switch (dw_dtype) {

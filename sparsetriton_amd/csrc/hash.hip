@@ -59,9 +59,8 @@ __global__ __launch_bounds__(256) void hash_query_kernel(const CT* __restrict__ 
 }
 
 // Kernel map by query (conv.py:12-75).  One thread per output row walks all K
-// offsets; consecutive threads own consecutive rows, so each offset's column
-// of the offset-major map is written with coalesced stores.  Offsets live in
-// LDS (K <= ST_MAX_KVOL).
+// offsets and writes the row's K entries (strides given by the caller; the
+// package uses row-major (N, K)).  Offsets live in LDS (K <= ST_MAX_KVOL).
 template <typename CT>
 __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ out_coords, int64_t n_out,
                                                          const int32_t* __restrict__ offsets, int K, int64_t stride,

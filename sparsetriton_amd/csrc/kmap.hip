@@ -219,8 +219,8 @@ __global__ __launch_bounds__(256) void cand_map_kernel(const CT* __restrict__ co
       if (s != ST_NO_VAL) o = slot_out[s];
     }
     if (o != ST_NO_VAL && (int64_t)o < n_out) {
-      invnbr[(int64_t)k * n + i] = (int32_t)o;
-      nbr[(int64_t)k * n_out + o] = (int32_t)i;
+      invnbr[i * g.K + k] = (int32_t)o;
+      nbr[(int64_t)o * g.K + k] = (int32_t)i;
       atomicOr(&out_masks[(int64_t)o * W + (k >> 5)], 1u << (k & 31));
       mword |= 1u << (k & 31);
     }
@@ -336,8 +336,8 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
 namespace st {
 
 // One thread per output row o: every valid (k, o) -> i entry becomes
-// invnbr[k][i] = o.  For a convolution map each (i, k) has at most one o, so
-// the scatter has no write conflicts.
+// invnbr[i][k] = o (row-major, like the map).  For a convolution map each
+// (i, k) has at most one o, so the scatter has no write conflicts.
 __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restrict__ nbr, int64_t ks, int64_t rs,
                                                           int64_t n_out, int K, int64_t n_in,
                                                           int32_t* __restrict__ invnbr, uint32_t* __restrict__ in_masks,
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restr
   for (int k = 0; k < K; ++k) {
     const int32_t i = nbr[(int64_t)k * ks + o * rs];
     if (i >= 0 && (int64_t)i < n_in) {
-      invnbr[(int64_t)k * n_in + i] = (int32_t)o;
+      invnbr[(int64_t)i * K + k] = (int32_t)o;
       atomicOr(&in_masks[(int64_t)i * W + (k >> 5)], 1u << (k & 31));
       mword |= 1u << (k & 31);
     }
@@ -379,41 +379,29 @@ extern "C" int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t 
 
 namespace st {
 
-// map_out[k][r] = map[k][perm[r]], masks_out[r] = masks[perm[r]]: the map in
-// the order the gather-GEMM tiles rows, so its per-offset reads are coalesced.
-__global__ __launch_bounds__(256) void kmap_permute_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
-                                                           int64_t n, int K, const uint32_t* __restrict__ masks, int W,
-                                                           const int32_t* __restrict__ perm,
-                                                           int32_t* __restrict__ map_out,
-                                                           uint32_t* __restrict__ masks_out) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= n) return;
-  const int64_t src = perm[r];
-  for (int k = 0; k < K; ++k) map_out[(int64_t)k * n + r] = map[(int64_t)k * ks + src * rs];
-  for (int w = 0; w < W; ++w) masks_out[r * W + w] = masks[src * W + w];
-}
-
-constexpr int kPairRows = 1024;  // map rows per pair-compaction workgroup (4 per thread)
+constexpr int kPairRows = 1024;  // map rows per pair-compaction workgroup (4 passes of 256)
 
 __device__ __forceinline__ bool pair_valid(int32_t i, int64_t n_in) { return i >= 0 && (int64_t)i < n_in; }
 
-// counts[k * nb + b] = valid entries of map column k in rows [b*1024, b*1024+1024)
+// counts[k * nb + b] = valid entries of offset k among rows [b*1024, b*1024+1024).
+// Thread per row, all offsets of the row (row-major maps are read along rows).
 __global__ __launch_bounds__(256) void pairs_count_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
-                                                          int64_t n_out, int64_t n_in, int64_t nb,
+                                                          int64_t n_out, int64_t n_in, int K, int64_t nb,
                                                           int32_t* __restrict__ counts) {
-  __shared__ int red[4];
-  const int k = blockIdx.y;
-  const int64_t base = (int64_t)blockIdx.x * kPairRows + threadIdx.x * 4;
-  int cnt = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t o = base + j;
-    if (o < n_out) cnt += pair_valid(map[(int64_t)k * ks + o * rs], n_in);
-  }
-  cnt = wave_sum(cnt);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = cnt;
+  __shared__ int cnt_s[ST_MAX_KVOL];
+  for (int t = threadIdx.x; t < K; t += 256) cnt_s[t] = 0;
   __syncthreads();
-  if (threadIdx.x == 0) counts[(int64_t)k * nb + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  const int lane = threadIdx.x & 63;
+  for (int j = 0; j < kPairRows / 256; ++j) {
+    const int64_t o = (int64_t)blockIdx.x * kPairRows + j * 256 + threadIdx.x;
+    for (int k = 0; k < K; ++k) {
+      const bool v = o < n_out && pair_valid(map[(int64_t)k * ks + o * rs], n_in);
+      const uint64_t bal = __ballot(v);
+      if (lane == 0 && bal) atomicAdd(&cnt_s[k], (int)__popcll(bal));
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < K; t += 256) counts[(int64_t)t * nb + blockIdx.x] = cnt_s[t];
 }
 
 // kstart[k] = first pair of offset k (kstart[K] = P); cstart[k] = first chunk of
@@ -433,45 +421,44 @@ __global__ void pairs_finalize_kernel(const int32_t* __restrict__ counts, int64_
   cstart[K] = c;
 }
 
+// Writes (in, out) pairs at offsets[k * nb + b] + rank, rank = position of the
+// row among the block's valid rows of offset k (rows ascending), so each
+// offset's pairs come out sorted by output row.
 __global__ __launch_bounds__(256) void pairs_emit_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
-                                                         int64_t n_out, int64_t n_in, int64_t nb,
+                                                         int64_t n_out, int64_t n_in, int K, int64_t nb,
                                                          const int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ pairs) {
-  __shared__ int scratch[5];
-  const int k = blockIdx.y;
-  const int64_t base = (int64_t)blockIdx.x * kPairRows + threadIdx.x * 4;
-  int32_t v[4];
-  int cnt = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t o = base + j;
-    v[j] = o < n_out ? map[(int64_t)k * ks + o * rs] : -1;
-    cnt += pair_valid(v[j], n_in);
-  }
-  int tot;
-  int pos = offsets[(int64_t)k * nb + blockIdx.x] + block_exclusive_scan(cnt, scratch, &tot);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (pair_valid(v[j], n_in)) {
-      pairs[2 * (int64_t)pos] = v[j];
-      pairs[2 * (int64_t)pos + 1] = (int32_t)(base + j);
-      ++pos;
+  __shared__ int base_s[ST_MAX_KVOL];
+  __shared__ int wcnt_s[4][ST_MAX_KVOL];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int t = threadIdx.x; t < K; t += 256) base_s[t] = offsets[(int64_t)t * nb + blockIdx.x];
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int j = 0; j < kPairRows / 256; ++j) {
+    const int64_t o = (int64_t)blockIdx.x * kPairRows + j * 256 + threadIdx.x;
+    for (int k = 0; k < K; ++k) {
+      const bool v = o < n_out && pair_valid(map[(int64_t)k * ks + o * rs], n_in);
+      const uint64_t bal = __ballot(v);
+      if (lane == 0) wcnt_s[wid][k] = (int)__popcll(bal);
     }
+    __syncthreads();
+    for (int k = 0; k < K; ++k) {
+      const int32_t i = o < n_out ? map[(int64_t)k * ks + o * rs] : -1;
+      const bool v = pair_valid(i, n_in);
+      const uint64_t bal = __ballot(v);
+      if (v) {
+        int pos = base_s[k] + (int)__popcll(bal & below);
+        for (int w = 0; w < wid; ++w) pos += wcnt_s[w][k];
+        pairs[2 * (int64_t)pos] = i;
+        pairs[2 * (int64_t)pos + 1] = (int32_t)o;
+      }
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < K; t += 256) base_s[t] += wcnt_s[0][t] + wcnt_s[1][t] + wcnt_s[2][t] + wcnt_s[3][t];
+    __syncthreads();
+  }
 }
 
 }  // namespace st
-
-extern "C" int st_kmap_permute(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n, int K,
-                               const uint32_t* masks, int mask_words, const int32_t* perm, int32_t* map_out,
-                               uint32_t* masks_out, st_stream_t stream) {
-  if (n < 0 || n >= (1ll << 31) || K <= 0 || K > ST_MAX_KVOL || mask_words != (K + 31) / 32) return ST_ERR_ARG;
-  if (n == 0) return ST_OK;
-  if (!map || !masks || !perm || !map_out || !masks_out) return ST_ERR_ARG;
-  st::kmap_permute_kernel<<<st_blocks(n, 256), 256, 0, stream>>>(map, map_k_stride, map_r_stride, n, K, masks,
-                                                                 mask_words, perm, map_out, masks_out);
-  ST_CHECK_LAUNCH();
-  return ST_OK;
-}
 
 extern "C" int st_kmap_pairs_sizes(int64_t n_out, int K, int64_t* num_blocks) {
   if (n_out < 0 || K <= 0 || K > ST_MAX_KVOL || !num_blocks) return ST_ERR_ARG;
@@ -487,13 +474,13 @@ extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t m
   if ((int64_t)K * n_out >= (1ll << 31) || pair_capacity < (int64_t)K * n_out) return ST_ERR_ARG;
   if (!block_counts || !kstart || !cstart || (n_out > 0 && (!map || !pairs))) return ST_ERR_ARG;
   if (num_blocks > 0)
-    st::pairs_count_kernel<<<dim3((unsigned)num_blocks, (unsigned)K), 256, 0, stream>>>(
-        map, map_k_stride, map_r_stride, n_out, n_in, num_blocks, block_counts);
+    st::pairs_count_kernel<<<(unsigned)num_blocks, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, K,
+                                                                     num_blocks, block_counts);
   st::exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, (int64_t)K * num_blocks);
   st::pairs_finalize_kernel<<<1, 64, 0, stream>>>(block_counts, num_blocks, K, chunk, kstart, cstart);
   if (num_blocks > 0)
-    st::pairs_emit_kernel<<<dim3((unsigned)num_blocks, (unsigned)K), 256, 0, stream>>>(
-        map, map_k_stride, map_r_stride, n_out, n_in, num_blocks, block_counts, pairs);
+    st::pairs_emit_kernel<<<(unsigned)num_blocks, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, K,
+                                                                    num_blocks, block_counts, pairs);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

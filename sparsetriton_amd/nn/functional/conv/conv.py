@@ -50,8 +50,7 @@ def compute_neighbor_indices(
 
     Same result as the reference (``conv.py:12-75``), computed by one HIP
     kernel (``st_kmap_query``) without materialising the (N_out, K, 4)
-    candidate coordinates.  The returned tensor is a view of an offset-major
-    (K, N_out) buffer.
+    candidate coordinates.  The returned tensor is contiguous (N_out, K).
     """
     kmap = query_kernel_map(in_hash_table, out_coords, kernel_offsets, spatial_shape, stride, n_in=0)
     return kmap.neighbor_indices

@@ -12,7 +12,7 @@ reference's (N_out, K) int32 tensor (any strides) or a ``KernelMap`` built by
 this package (which also carries row masks and the transposed map).
 
 Kernels (``libsparsetriton_amd.so``):
-  forward   st_gather_gemm over the map in mask-sorted tile order, weights
+  forward   st_gather_gemm with rows tiled in mask-sorted order, weights
             re-laid (K, C_out, C_in);
   dgrad     st_gather_gemm over the transposed map (also mask-sorted), weights
             as stored -- a gather, so no atomics and a deterministic result;
@@ -52,9 +52,17 @@ def gather_gemm(A: torch.Tensor, map_t: torch.Tensor, k_stride: int, r_stride: i
     return out
 
 
-def gather_gemm_plan(A: torch.Tensor, plan, Bt: torch.Tensor, n_dst: int, K: int) -> torch.Tensor:
-    """gather_gemm over a mask-sorted TilePlan."""
-    return gather_gemm(A, plan.map, n_dst, 1, plan.masks, Bt, n_dst, K, rows=plan.perm)
+def gather_gemm_fwd(A: torch.Tensor, kmap: KernelMap, Bt: torch.Tensor) -> torch.Tensor:
+    """Forward: out rows in the mask-sorted order of the forward plan."""
+    plan = kmap.forward_plan()
+    return gather_gemm(A, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, Bt, kmap.n_out, kmap.K,
+                       rows=plan.perm)
+
+
+def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> torch.Tensor:
+    """Input gradient over the transposed map, in the mask-sorted order of the backward plan."""
+    plan = kmap.backward_plan()
+    return gather_gemm(dY, kmap.invnbr, 1, kmap.K, kmap.in_masks, W, kmap.n_in, kmap.K, rows=plan.perm)
 
 
 def weight_prep(weights: torch.Tensor, mode: int) -> torch.Tensor:
@@ -105,7 +113,7 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
         features = features.contiguous()
         w = weights.to(features.dtype).contiguous()
         wt = weight_prep(w, _lib.W_TRANSPOSE)
-        out = gather_gemm_plan(features, kmap.forward_plan(), wt, kmap.n_out, K)
+        out = gather_gemm_fwd(features, kmap, wt)
         ctx.save_for_backward(features, weights)
         ctx.kmap = kmap
         return out
@@ -119,7 +127,7 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             w = weights.to(features.dtype).contiguous()
             # dX[i] = sum_k dY[invnbr[k, i]] @ W[k]^T: W[k] (C_in, C_out) is already the (Nd, Kd) operand.
-            grad_input = gather_gemm_plan(grad_output, kmap.backward_plan(), w, kmap.n_in, kmap.K)
+            grad_input = gather_gemm_dgrad(grad_output, kmap, w)
         if ctx.needs_input_grad[1]:
             grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
         return grad_input, grad_weights, None

@@ -12,10 +12,10 @@ Public functions keep the reference's names and meaning
 
 The output coordinates of a strided / transposed convolution and its kernel
 map come out of one HIP pipeline (``st_outcoords_plan`` / ``st_outcoords_emit``);
-the submanifold map comes from ``st_kmap_query``.  Maps are stored
-offset-major (K, N) int32 with per-row offset bitmasks, in both directions:
-``nbr[k, o]`` is the input row feeding output ``o`` through offset ``k`` and
-``invnbr[k, i]`` the output row input ``i`` feeds.
+the submanifold map comes from ``st_kmap_query``.  Maps are stored row-major
+(N, K) int32 -- the reference's layout -- with per-row offset bitmasks, in both
+directions: ``nbr[o, k]`` is the input row feeding output ``o`` through offset
+``k`` and ``invnbr[i, k]`` the output row input ``i`` feeds.
 """
 
 from typing import Optional, Tuple
@@ -89,12 +89,11 @@ def _mask_words(K: int) -> int:
 class KernelMap:
     """Kernel map of one convolution geometry on one coordinate set.
 
-    ``nbr`` (K, N_out) int32, offset-major, -1 where no neighbour;
+    ``nbr`` (N_out, K) int32, row-major, -1 where no neighbour;
     ``out_masks`` (N_out, W) row bitmasks of ``nbr`` (W = ceil(K/32));
-    ``invnbr`` (K, N_in) and ``in_masks`` (N_in, W) the transposed map, built
+    ``invnbr`` (N_in, K) and ``in_masks`` (N_in, W) the transposed map, built
     lazily by ``ensure_inverse`` for the input gradient.
-    ``nbr`` may be a strided view (``k_stride``/``r_stride``) of a caller's
-    (N_out, K) tensor.
+    ``nbr`` may be any strided (N_out, K) view (``k_stride``/``r_stride``).
     """
 
     def __init__(self, nbr: torch.Tensor, n_in: int, n_out: int, K: int, out_masks: Optional[torch.Tensor] = None,
@@ -102,8 +101,8 @@ class KernelMap:
                  k_stride: Optional[int] = None, r_stride: Optional[int] = None):
         self.nbr = nbr
         self.n_in, self.n_out, self.K = int(n_in), int(n_out), int(K)
-        self.k_stride = n_out if k_stride is None else int(k_stride)
-        self.r_stride = 1 if r_stride is None else int(r_stride)
+        self.k_stride = 1 if k_stride is None else int(k_stride)
+        self.r_stride = int(K) if r_stride is None else int(r_stride)
         self.out_masks = out_masks
         self.invnbr = invnbr
         self.in_masks = in_masks
@@ -135,7 +134,7 @@ class KernelMap:
             return self
         dev = self.nbr.device
         W = self.mask_words
-        self.invnbr = _lib.fill_(torch.empty((self.K, self.n_in), dtype=torch.int32, device=dev), -1)
+        self.invnbr = _lib.fill_(torch.empty((self.n_in, self.K), dtype=torch.int32, device=dev), -1)
         self.in_masks = _lib.fill_(torch.empty((self.n_in, W), dtype=torch.int32, device=dev), 0)
         need_out = self.out_masks is None
         if need_out:
@@ -152,17 +151,17 @@ class KernelMap:
 
     # ------------------------------------------------------------ GEMM plans
     def forward_plan(self) -> "TilePlan":
-        """Output rows in mask-sorted tile order, with the map and masks laid out in that order."""
+        """Mask-sorted order of the output rows (forward)."""
         if self._fwd is None:
             self.ensure_out_masks()
-            self._fwd = TilePlan.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.out_masks)
+            self._fwd = TilePlan.build(self.n_out, self.K, self.out_masks)
         return self._fwd
 
     def backward_plan(self) -> "TilePlan":
-        """Input rows in mask-sorted tile order over the transposed map (for the input gradient)."""
+        """Mask-sorted order of the input rows over the transposed map (input gradient)."""
         if self._bwd is None:
             self.ensure_inverse()
-            self._bwd = TilePlan.build(self.invnbr, self.n_in, 1, self.n_in, self.K, self.in_masks)
+            self._bwd = TilePlan.build(self.n_in, self.K, self.in_masks)
         return self._bwd
 
     def pair_list(self, chunk: int = 2048) -> "PairList":
@@ -194,17 +193,16 @@ class KernelMap:
 
 
 class TilePlan:
-    """A map in gather-GEMM tile order: ``map`` (K, n) and ``masks`` (n, W) indexed by tile row,
-    ``perm`` (n) the destination row of each tile row (rows sorted by offset bitmask)."""
+    """Destination-row order of a gather-GEMM: ``perm`` (n) lists the rows sorted by their
+    offset bitmask, so 16/32-row MFMA slabs hold rows that need the same offsets."""
 
-    def __init__(self, map_t: torch.Tensor, masks: torch.Tensor, perm: torch.Tensor):
-        self.map, self.masks, self.perm = map_t, masks, perm
+    def __init__(self, perm: torch.Tensor):
+        self.perm = perm
 
     @classmethod
-    def build(cls, map_t, k_stride, r_stride, n, K, masks) -> "TilePlan":
-        dev = map_t.device
+    def build(cls, n, K, masks) -> "TilePlan":
+        dev = masks.device
         W = _mask_words(K)
-        s = _lib.stream_of(dev)
         nbytes = ctypes.c_size_t()
         _lib.call("st_kmap_sort_workspace", n, ctypes.byref(nbytes))
         ws = torch.empty((max(nbytes.value, 1),), dtype=torch.uint8, device=dev)
@@ -212,12 +210,8 @@ class TilePlan:
         rows = torch.empty((n,), dtype=torch.int32, device=dev)
         perm = torch.empty((n,), dtype=torch.int32, device=dev)
         _lib.call("st_kmap_sort_rows", _lib.ptr(masks), W, K, n, _lib.ptr(keys), _lib.ptr(rows), _lib.ptr(perm),
-                  _lib.ptr(ws), nbytes.value, s)
-        map_out = torch.empty((K, n), dtype=torch.int32, device=dev)
-        masks_out = torch.empty((n, W), dtype=torch.int32, device=dev)
-        _lib.call("st_kmap_permute", _lib.ptr(map_t), k_stride, r_stride, n, K, _lib.ptr(masks), W, _lib.ptr(perm),
-                  _lib.ptr(map_out), _lib.ptr(masks_out), s)
-        return cls(map_out, masks_out, perm)
+                  _lib.ptr(ws), nbytes.value, _lib.stream_of(dev))
+        return cls(perm)
 
 
 class PairList:
@@ -259,12 +253,12 @@ def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets:
     K = kernel_offsets.shape[0]
     if K > _lib.MAX_KVOL:
         raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
-    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
+    nbr = torch.empty((n_out, K), dtype=torch.int32, device=dev)
     masks = torch.empty((n_out, _mask_words(K)), dtype=torch.int32, device=dev)
     sx, sy, sz = (int(v) for v in spatial_shape)
     _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out,
               _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, _lib.ptr(table.table_keys),
-              _lib.ptr(table.table_values), table.capacity, _lib.ptr(nbr), n_out, 1, _lib.ptr(masks),
+              _lib.ptr(table.table_values), table.capacity, _lib.ptr(nbr), 1, K, _lib.ptr(masks),
               _lib.stream_of(dev))
     return KernelMap(nbr, n_in, n_out, K, out_masks=masks)
 
@@ -330,8 +324,8 @@ def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size
     nbr = invnbr = out_masks = in_masks = None
     if with_map:
         W = _mask_words(K)
-        nbr = _lib.fill_(torch.empty((K, n_out), dtype=torch.int32, device=dev), -1)
-        invnbr = _lib.fill_(torch.empty((K, n), dtype=torch.int32, device=dev), -1)
+        nbr = _lib.fill_(torch.empty((n_out, K), dtype=torch.int32, device=dev), -1)
+        invnbr = _lib.fill_(torch.empty((n, K), dtype=torch.int32, device=dev), -1)
         out_masks = _lib.fill_(torch.empty((n_out, W), dtype=torch.int32, device=dev), 0)
         in_masks = _lib.fill_(torch.empty((n, W), dtype=torch.int32, device=dev), 0)
     ik = iv = None
