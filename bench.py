@@ -140,7 +140,8 @@ def main():
     def build_kmap():
         t = HashTable(table_capacity(N), device=dev)
         t.insert(coords)
-        km = query_kernel_map(t, coords, offsets, shape, 1, N)
+        t.build_occupancy(coords, 4, shape)
+        km = query_kernel_map(t, coords, offsets, shape, 1, N, symmetric=True)
         km.prepare()  # transposed map, mask-sorted tile plans, pair list
         return t, km
 
@@ -157,10 +158,11 @@ def main():
     def t_insert():
         table.clear()
         table.insert(coords)
+        table.build_occupancy(coords, 4, shape)
 
     ins_t = _events(torch, t_insert, 20)
     q_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N), 20)
-    prep_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N).prepare(), 20) - np.median(q_t)
+    prep_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N, symmetric=True).prepare(), 20) - np.median(q_t)
 
     # --------------------------------------------------------- train step
     X = torch.as_tensor(X_np, device=dev).to(dtype)

@@ -95,6 +95,32 @@ int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale
 int st_hash_query(const void* coords, int coord_dtype, int64_t m, const uint64_t* keys, const uint32_t* vals,
                   int64_t capacity, int32_t* out, st_stream_t stream);
 
+/*
+ * Occupancy bitmap of a coordinate set (no reference counterpart; the
+ * reference probes its table for every neighbour).  One bit per voxel of the
+ * box [0, batches) x [0, shape[0]) x [0, shape[1]) x [0, shape[2]), stored in
+ * 4x4x4 bricks of one u64 word each: voxel (b, x, y, z) is bit
+ * (x%4)*16 + (y%4)*4 + z%4 of word ((b*BX + x/4)*BY + y/4)*BZ + z/4, where
+ * BX = ceil(shape[0]/4) and likewise BY, BZ.  A kernel-map query tests the
+ * bit before probing, so an absent neighbour -- most of the 27 on a surface
+ * -- costs one cached word load instead of a hash probe.  A query outside the
+ * box is probed as usual, so the bitmap never changes a result.
+ */
+typedef struct st_occupancy {
+  const uint64_t* words; /* st_occupancy_words() words written by st_occupancy_build */
+  int64_t batches;
+  int64_t shape[3];
+  int64_t scale;         /* table keys are coords * scale: a query off that lattice is absent */
+} st_occupancy;
+
+/* Number of u64 words of the bitmap of a (batches, sx, sy, sz) box. */
+int st_occupancy_words(int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* words);
+
+/* Clears `words` and sets the bit of every coordinate row inside the box
+ * (rows outside it are left to the table).  words: st_occupancy_words() u64s. */
+int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t* words, int64_t batches, int64_t sx,
+                       int64_t sy, int64_t sz, st_stream_t stream);
+
 /* ------------------------------------------------------------ kernel maps */
 
 /*
@@ -104,14 +130,15 @@ int st_hash_query(const void* coords, int coord_dtype, int64_t m, const uint64_t
  *   nbr[k * nbr_k_stride + o * nbr_r_stride] = row of q in the table if
  *       0 <= q < shape (per axis) and present, else -1.
  * row_masks (n_out, ceil(K/32)) u32, optional: bit k set iff nbr[o, k] >= 0.
- * The package uses the reference's row-major (n_out, K) layout
- * (nbr_k_stride = 1, nbr_r_stride = K): a row's offsets share cache lines,
- * which is what the mask-sorted gather-GEMM reads.
+ * occ, optional: the occupancy bitmap of the table's coordinates (a filter only).
+ * The package stores maps offset-major, (K, n_out) (nbr_k_stride = n_out,
+ * nbr_r_stride = 1): every kernel that walks rows then reads and writes each
+ * offset's column with coalesced accesses.
  */
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
-                  const uint32_t* vals, int64_t capacity, int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride,
-                  uint32_t* row_masks, st_stream_t stream);
+                  const uint32_t* vals, int64_t capacity, const st_occupancy* occ, int32_t* nbr,
+                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, st_stream_t stream);
 
 /* Geometry of a strided or transposed convolution's output-coordinate build. */
 typedef struct st_outgeom {
@@ -149,9 +176,9 @@ int st_outcoords_plan(const void* in_coords, int coord_dtype, int64_t n, const i
  * Writes out_coords (N_out, 4) in the input's coordinate dtype, ordered by
  * first occurrence in the candidate order; slot_out (dcap u32) maps dedup
  * slots to output rows (so dkeys + slot_out form the output-coordinate
- * table); and the kernel map in both directions, row-major:
- *   nbr    (N_out, K): input row feeding output o through offset k, or -1
- *   invnbr (n, K)    : output row fed by input i through offset k, or -1
+ * table); and the kernel map in both directions, offset-major:
+ *   nbr    (K, N_out): input row feeding output o through offset k, or -1
+ *   invnbr (K, n)    : output row fed by input i through offset k, or -1
  * plus row masks out_masks (N_out, W) and in_masks (n, W), W = ceil(K/32).
  * nbr/invnbr must be pre-filled with -1 and the masks with 0 by the caller.
  * With nbr == NULL only out_coords and slot_out are written (hash-fly mode).
@@ -168,7 +195,7 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
 
 /*
  * Transposed kernel map of an arbitrary map nbr (k, o) -> i (strides as in
- * st_kmap_query): invnbr[i * K + k] = o (row-major), in_masks (n_in, W) row masks of
+ * st_kmap_query): invnbr[k * n_in + i] = o (offset-major), in_masks (n_in, W) row masks of
  * invnbr, and, if out_masks is non-null, out_masks (n_out, W) row masks of
  * nbr.  invnbr must be pre-filled with -1 and in_masks with 0.  Used when a
  * caller hands ConvPrecomputedNeighborGEMM a plain (N_out, K) map

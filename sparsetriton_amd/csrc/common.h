@@ -66,6 +66,18 @@ __device__ __forceinline__ uint32_t find_slot(const uint64_t* __restrict__ keys,
   return ST_NO_VAL;
 }
 
+// find_slot continued from slot s whose key `k` the caller already loaded.
+__device__ __forceinline__ uint32_t find_slot_from(const uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
+                                                   uint32_t s, uint64_t k) {
+  for (uint32_t step = 0; step < cap; ++step) {
+    if (k == key) return s;
+    if (k == ST_EMPTY_KEY) return ST_NO_VAL;
+    s = next_slot(s, cap);
+    k = keys[s];
+  }
+  return ST_NO_VAL;
+}
+
 // Insert-or-find.  Returns the slot of `key` (claimed with a 64-bit CAS if new),
 // or ST_NO_VAL if the table is full.  `was_new` tells whether this call claimed it.
 __device__ __forceinline__ uint32_t insert_slot(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
@@ -92,6 +104,74 @@ __device__ __forceinline__ uint32_t insert_slot(uint64_t* __restrict__ keys, uin
     s = next_slot(s, cap);
   }
   return ST_NO_VAL;
+}
+
+// ------------------------------------------------------- occupancy bitmap
+
+// Device view of an st_occupancy (words == nullptr: no bitmap, always probe).
+struct Occ {
+  const uint64_t* words;
+  int nb, sx, sy, sz, bx, by, bz, scale;
+};
+
+__host__ __forceinline__ Occ make_occ(const st_occupancy* o) {
+  Occ d{};
+  if (!o || !o->words) return d;
+  d.words = o->words;
+  d.nb = (int)o->batches;
+  d.sx = (int)o->shape[0];
+  d.sy = (int)o->shape[1];
+  d.sz = (int)o->shape[2];
+  d.bx = (d.sx + 3) >> 2;
+  d.by = (d.sy + 3) >> 2;
+  d.bz = (d.sz + 3) >> 2;
+  d.scale = o->scale > 1 ? (int)o->scale : 1;
+  return d;
+}
+
+__host__ inline bool occ_valid(const st_occupancy* o) {
+  if (!o || !o->words) return true;
+  return o->batches > 0 && o->batches <= 32768 && o->scale >= 1 && o->scale <= 32768 && o->shape[0] > 0 &&
+         o->shape[0] <= 65536 && o->shape[1] > 0 && o->shape[1] <= 65536 && o->shape[2] > 0 &&
+         o->shape[2] <= 65536;
+}
+
+__device__ __forceinline__ int64_t occ_word(const Occ& o, int b, int x, int y, int z) {
+  return (((int64_t)b * o.bx + (x >> 2)) * o.by + (y >> 2)) * o.bz + (z >> 2);
+}
+
+__device__ __forceinline__ int occ_bit(int x, int y, int z) { return ((x & 3) << 4) | ((y & 3) << 2) | (z & 3); }
+
+// Occupancy test split in two so that many tests can have their word loads in
+// flight together: occ_locate() returns 0 when the coordinate (table-key
+// space, components packable) is certainly absent, 1 when bit `bit` of word
+// `word` decides, 2 when it must be probed (no bitmap, or outside the box).
+__device__ __forceinline__ int occ_locate(const Occ& o, int b, int x, int y, int z, int64_t& word, int& bit) {
+  if (!o.words) return 2;
+  if (o.scale > 1) {
+    if (x % o.scale || y % o.scale || z % o.scale) return 0;
+    x /= o.scale;
+    y /= o.scale;
+    z /= o.scale;
+  }
+  if (b < 0 || b >= o.nb || x < 0 || x >= o.sx || y < 0 || y >= o.sy || z < 0 || z >= o.sz) return 2;
+  word = occ_word(o, b, x, y, z);
+  bit = occ_bit(x, y, z);
+  return 1;
+}
+
+// False only when the coordinate (in table-key space, components packable)
+// is certainly absent; true means "probe the table".
+__device__ __forceinline__ bool occ_maybe(const Occ& o, int b, int x, int y, int z) {
+  if (!o.words) return true;
+  if (o.scale > 1) {
+    if (x % o.scale || y % o.scale || z % o.scale) return false;
+    x /= o.scale;
+    y /= o.scale;
+    z /= o.scale;
+  }
+  if (b < 0 || b >= o.nb || x < 0 || x >= o.sx || y < 0 || y >= o.sy || z < 0 || z >= o.sz) return true;
+  return (o.words[occ_word(o, b, x, y, z)] >> occ_bit(x, y, z)) & 1ull;
 }
 
 // ------------------------------------------------------------- coordinates
@@ -127,6 +207,17 @@ __device__ __forceinline__ int lanes_below(uint64_t ballot) {
   return __popcll(below);
 }
 
+// Inclusive prefix sum across the wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int t = __shfl_up(v, off, kWave);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
 // Workgroup-wide exclusive prefix of one int per thread (blockDim.x <= 1024,
 // multiple of 64).  `scratch` needs blockDim.x/64 + 1 ints of LDS.
 // Returns the exclusive prefix; *total receives the workgroup sum.
@@ -157,6 +248,10 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* to
   __syncthreads();
   return res;
 }
+
+// In-place exclusive scan of counts[0..n) on `stream`, counts[n] = total
+// (one workgroup; defined in kmap.hip).
+int launch_exclusive_scan(int32_t* counts, int64_t n, hipStream_t stream);
 
 }  // namespace st
 

@@ -58,15 +58,38 @@ __global__ __launch_bounds__(256) void hash_query_kernel(const CT* __restrict__ 
   out[i] = r;
 }
 
+// Sets the occupancy bit of every row inside the box.
+template <typename CT>
+__global__ __launch_bounds__(256) void occupancy_build_kernel(const CT* __restrict__ coords, int64_t n, Occ occ,
+                                                              uint64_t* __restrict__ words) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int64_t b, x, y, z;
+  load_coord(coords, i, b, x, y, z);
+  if (b < 0 || b >= occ.nb || x < 0 || x >= occ.sx || y < 0 || y >= occ.sy || z < 0 || z >= occ.sz) return;
+  atomicOr((unsigned long long*)&words[occ_word(occ, (int)b, (int)x, (int)y, (int)z)],
+           1ull << occ_bit((int)x, (int)y, (int)z));
+}
+
 // Kernel map by query (conv.py:12-75).  One thread per output row walks all K
-// offsets and writes the row's K entries (strides given by the caller; the
-// package uses row-major (N, K)).  Offsets live in LDS (K <= ST_MAX_KVOL).
+// offsets; consecutive threads own consecutive rows, so each offset's column
+// of the offset-major map is written with coalesced stores.  Offsets live in
+// LDS (K <= ST_MAX_KVOL).
+//
+// A row's queries are independent, so they are resolved kQGroup at a time in
+// three rounds whose loads are all in flight together: occupancy words, then
+// the home-slot keys of the candidates the bitmap lets through, then the
+// values of the hits.  Only a probe that meets another key at its home slot
+// continues its chain on its own.  This keeps the number of dependent memory
+// round trips per row near 3 * K / kQGroup instead of ~3 * K.
+constexpr int kQGroup = 9;
+
 template <typename CT>
 __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ out_coords, int64_t n_out,
                                                          const int32_t* __restrict__ offsets, int K, int64_t stride,
                                                          int64_t sx, int64_t sy, int64_t sz,
                                                          const uint64_t* __restrict__ keys,
-                                                         const uint32_t* __restrict__ vals, uint32_t cap,
+                                                         const uint32_t* __restrict__ vals, uint32_t cap, Occ occ,
                                                          int32_t* __restrict__ nbr, int64_t ks, int64_t rs,
                                                          uint32_t* __restrict__ row_masks) {
   __shared__ int32_t off_s[ST_MAX_KVOL * 3];
@@ -81,19 +104,55 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
   z *= stride;
   const int W = (K + 31) >> 5;
   uint32_t mword = 0;
-  for (int k = 0; k < K; ++k) {
-    const int64_t qx = x - off_s[3 * k], qy = y - off_s[3 * k + 1], qz = z - off_s[3 * k + 2];
-    int32_t r = -1;
-    uint64_t key;
-    if (qx >= 0 && qx < sx && qy >= 0 && qy < sy && qz >= 0 && qz < sz && pack_key(b, qx, qy, qz, key)) {
-      uint32_t s = find_slot(keys, cap, key);
-      if (s != ST_NO_VAL) r = (int32_t)vals[s];
+  for (int k0 = 0; k0 < K; k0 += kQGroup) {
+    uint64_t key[kQGroup];
+    int state[kQGroup];  // 0 absent, 1 bitmap decides, 2 probe
+    int64_t word[kQGroup];
+    int bit[kQGroup];
+#pragma unroll
+    for (int j = 0; j < kQGroup; ++j) {
+      const int k = k0 + j;
+      state[j] = 0;
+      word[j] = 0;
+      bit[j] = 0;
+      key[j] = 0;
+      if (k < K) {
+        const int64_t qx = x - off_s[3 * k], qy = y - off_s[3 * k + 1], qz = z - off_s[3 * k + 2];
+        if (qx >= 0 && qx < sx && qy >= 0 && qy < sy && qz >= 0 && qz < sz && pack_key(b, qx, qy, qz, key[j]))
+          state[j] = occ_locate(occ, (int)b, (int)qx, (int)qy, (int)qz, word[j], bit[j]);
+      }
     }
-    nbr[(int64_t)k * ks + o * rs] = r;
-    if (r >= 0) mword |= 1u << (k & 31);
-    if ((k & 31) == 31 || k == K - 1) {
-      if (row_masks) row_masks[o * W + (k >> 5)] = mword;
-      mword = 0;
+    // round 1: occupancy words
+    uint64_t w[kQGroup];
+#pragma unroll
+    for (int j = 0; j < kQGroup; ++j) w[j] = state[j] == 1 ? occ.words[word[j]] : 0ull;
+    // round 2: home-slot keys of the remaining candidates
+    uint32_t slot[kQGroup];
+    uint64_t hk[kQGroup];
+#pragma unroll
+    for (int j = 0; j < kQGroup; ++j) {
+      const bool probe = state[j] == 2 || (state[j] == 1 && ((w[j] >> bit[j]) & 1ull));
+      slot[j] = probe ? home_slot(key[j], cap) : ST_NO_VAL;
+      hk[j] = probe ? keys[slot[j]] : ST_EMPTY_KEY;
+    }
+    // finish the rare chains that met another key; round 3: values of the hits
+    int32_t r[kQGroup];
+#pragma unroll
+    for (int j = 0; j < kQGroup; ++j) {
+      if (slot[j] != ST_NO_VAL) slot[j] = find_slot_from(keys, cap, key[j], slot[j], hk[j]);
+      r[j] = slot[j] != ST_NO_VAL ? (int32_t)vals[slot[j]] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kQGroup; ++j) {
+      const int k = k0 + j;
+      if (k < K) {
+        nbr[(int64_t)k * ks + o * rs] = r[j];
+        if (r[j] >= 0) mword |= 1u << (k & 31);
+        if ((k & 31) == 31 || k == K - 1) {
+          if (row_masks) row_masks[o * W + (k >> 5)] = mword;
+          mword = 0;
+        }
+      }
     }
   }
 }
@@ -152,19 +211,48 @@ int st_hash_query(const void* coords, int coord_dtype, int64_t m, const uint64_t
   return ST_OK;
 }
 
+int st_occupancy_words(int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* words) {
+  if (!words || batches <= 0 || batches > 32768 || sx <= 0 || sy <= 0 || sz <= 0 || sx > 65536 || sy > 65536 ||
+      sz > 65536)
+    return ST_ERR_ARG;
+  *words = batches * ((sx + 3) / 4) * ((sy + 3) / 4) * ((sz + 3) / 4);
+  return ST_OK;
+}
+
+int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t* words, int64_t batches, int64_t sx,
+                       int64_t sy, int64_t sz, st_stream_t stream) {
+  int64_t nw = 0;
+  if (st_occupancy_words(batches, sx, sy, sz, &nw) != ST_OK || !words || n < 0 || n >= (1ll << 31))
+    return ST_ERR_ARG;
+  if (n > 0 && !coords) return ST_ERR_ARG;
+  st_occupancy o{words, batches, {sx, sy, sz}, 1};
+  const Occ occ = make_occ(&o);
+  unsigned g = st_blocks(nw, 256);
+  if (g > 65536) g = 65536;
+  fill_kernel<uint64_t><<<g, 256, 0, stream>>>(words, nw, 0ull);
+  if (n > 0) {
+    ST_DISPATCH_COORD(coord_dtype, CT,
+                      occupancy_build_kernel<CT><<<st_blocks(n, 256), 256, 0, stream>>>((const CT*)coords, n, occ,
+                                                                                         words));
+  }
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
-                  const uint32_t* vals, int64_t capacity, int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride,
-                  uint32_t* row_masks, st_stream_t stream) {
+                  const uint32_t* vals, int64_t capacity, const st_occupancy* occ, int32_t* nbr,
+                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, st_stream_t stream) {
   if (n_out < 0 || K <= 0 || K > ST_MAX_KVOL || stride < 1 || capacity <= 0 || capacity >= (1ll << 31))
     return ST_ERR_ARG;
+  if (!occ_valid(occ)) return ST_ERR_ARG;
   if (n_out >= (1ll << 31)) return ST_ERR_ARG;
   if (n_out == 0) return ST_OK;
   if (!out_coords || !offsets || !keys || !vals || !nbr) return ST_ERR_ARG;
   ST_DISPATCH_COORD(coord_dtype, CT,
                     kmap_query_kernel<CT><<<st_blocks(n_out, 256), 256, 0, stream>>>(
                         (const CT*)out_coords, n_out, offsets, K, stride, shape_x, shape_y, shape_z, keys, vals,
-                        (uint32_t)capacity, nbr, nbr_k_stride, nbr_r_stride, row_masks));
+                        (uint32_t)capacity, make_occ(occ), nbr, nbr_k_stride, nbr_r_stride, row_masks));
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

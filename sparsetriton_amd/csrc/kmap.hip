@@ -136,19 +136,54 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const CT* __restrict__ 
 }
 
 // In-place exclusive scan of counts[0..n); counts[n] receives the total.
-// One workgroup of 1024 threads walks the array in 1024-element chunks.
+// One workgroup of 1024 threads; each round covers 8192 elements, 8
+// consecutive ones per thread read and written as two 16-byte vectors (a
+// wave covers 2 KB contiguously), with one workgroup scan per round.
+constexpr int kScanPer = 8;
 __global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restrict__ counts, int64_t n) {
   __shared__ int scratch[17];
+  const bool vec = (reinterpret_cast<uintptr_t>(counts) & 15) == 0;
   int carry = 0;
-  for (int64_t base = 0; base < n; base += blockDim.x) {
-    const int64_t j = base + threadIdx.x;
-    const int v = j < n ? counts[j] : 0;
+  for (int64_t base = 0; base < n; base += (int64_t)kScanPer * 1024) {
+    const int64_t j0 = base + (int64_t)threadIdx.x * kScanPer;
+    const bool full = vec && j0 + kScanPer <= n;
+    int v[kScanPer];
+    if (full) {
+      const int4 lo = *reinterpret_cast<const int4*>(counts + j0);
+      const int4 hi = *reinterpret_cast<const int4*>(counts + j0 + 4);
+      v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w;
+      v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < kScanPer; ++e) v[e] = j0 + e < n ? counts[j0 + e] : 0;
+    }
+    int sum = 0;
+#pragma unroll
+    for (int e = 0; e < kScanPer; ++e) sum += v[e];
     int tot;
-    const int ex = block_exclusive_scan(v, scratch, &tot);
-    if (j < n) counts[j] = carry + ex;
+    int run = carry + block_exclusive_scan(sum, scratch, &tot);
+    int ex[kScanPer];
+#pragma unroll
+    for (int e = 0; e < kScanPer; ++e) {
+      ex[e] = run;
+      run += v[e];
+    }
+    if (full) {
+      *reinterpret_cast<int4*>(counts + j0) = make_int4(ex[0], ex[1], ex[2], ex[3]);
+      *reinterpret_cast<int4*>(counts + j0 + 4) = make_int4(ex[4], ex[5], ex[6], ex[7]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kScanPer; ++e)
+        if (j0 + e < n) counts[j0 + e] = ex[e];
+    }
     carry += tot;
   }
   if (threadIdx.x == 0) counts[n] = carry;
+}
+
+int launch_exclusive_scan(int32_t* counts, int64_t n, hipStream_t stream) {
+  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(counts, n);
+  return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
 }
 
 template <typename CT>
@@ -219,8 +254,8 @@ __global__ __launch_bounds__(256) void cand_map_kernel(const CT* __restrict__ co
       if (s != ST_NO_VAL) o = slot_out[s];
     }
     if (o != ST_NO_VAL && (int64_t)o < n_out) {
-      invnbr[i * g.K + k] = (int32_t)o;
-      nbr[(int64_t)o * g.K + k] = (int32_t)i;
+      invnbr[(int64_t)k * n + i] = (int32_t)o;
+      nbr[(int64_t)k * n_out + o] = (int32_t)i;
       atomicOr(&out_masks[(int64_t)o * W + (k >> 5)], 1u << (k & 31));
       mword |= 1u << (k & 31);
     }
@@ -336,7 +371,7 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
 namespace st {
 
 // One thread per output row o: every valid (k, o) -> i entry becomes
-// invnbr[i][k] = o (row-major, like the map).  For a convolution map each
+// invnbr[k][i] = o (offset-major, like the map).  For a convolution map each
 // (i, k) has at most one o, so the scatter has no write conflicts.
 __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restrict__ nbr, int64_t ks, int64_t rs,
                                                           int64_t n_out, int K, int64_t n_in,
@@ -349,7 +384,7 @@ __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restr
   for (int k = 0; k < K; ++k) {
     const int32_t i = nbr[(int64_t)k * ks + o * rs];
     if (i >= 0 && (int64_t)i < n_in) {
-      invnbr[(int64_t)i * K + k] = (int32_t)o;
+      invnbr[(int64_t)k * n_in + i] = (int32_t)o;
       atomicOr(&in_masks[(int64_t)i * W + (k >> 5)], 1u << (k & 31));
       mword |= 1u << (k & 31);
     }
@@ -379,29 +414,32 @@ extern "C" int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t 
 
 namespace st {
 
-constexpr int kPairRows = 1024;  // map rows per pair-compaction workgroup (4 passes of 256)
+constexpr int kPairRows = 4096;  // map rows per (block, offset) workgroup
+constexpr int kPairPer = kPairRows / 256;
 
 __device__ __forceinline__ bool pair_valid(int32_t i, int64_t n_in) { return i >= 0 && (int64_t)i < n_in; }
 
-// counts[k * nb + b] = valid entries of offset k among rows [b*1024, b*1024+1024).
-// Thread per row, all offsets of the row (row-major maps are read along rows).
+// counts[k * nb + b] = valid entries of offset k among rows [b*4096, b*4096+4096).
+// Grid (nb, K): one workgroup per (row block, offset) reads 4096 consecutive
+// entries of the offset's column, coalesced.
 __global__ __launch_bounds__(256) void pairs_count_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
-                                                          int64_t n_out, int64_t n_in, int K, int64_t nb,
+                                                          int64_t n_out, int64_t n_in, int64_t nb,
                                                           int32_t* __restrict__ counts) {
-  __shared__ int cnt_s[ST_MAX_KVOL];
-  for (int t = threadIdx.x; t < K; t += 256) cnt_s[t] = 0;
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  for (int j = 0; j < kPairRows / 256; ++j) {
-    const int64_t o = (int64_t)blockIdx.x * kPairRows + j * 256 + threadIdx.x;
-    for (int k = 0; k < K; ++k) {
-      const bool v = o < n_out && pair_valid(map[(int64_t)k * ks + o * rs], n_in);
-      const uint64_t bal = __ballot(v);
-      if (lane == 0 && bal) atomicAdd(&cnt_s[k], (int)__popcll(bal));
-    }
+  __shared__ int wsum_s[4];
+  const int k = blockIdx.y;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int32_t* col = map + (int64_t)k * ks;
+  const int64_t row0 = (int64_t)blockIdx.x * kPairRows + threadIdx.x;
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < kPairPer; ++j) {
+    const int64_t o = row0 + j * 256;
+    c += (o < n_out && pair_valid(col[o * rs], n_in)) ? 1 : 0;
   }
+  c = wave_sum(c);
+  if (lane == 0) wsum_s[wid] = c;
   __syncthreads();
-  for (int t = threadIdx.x; t < K; t += 256) counts[(int64_t)t * nb + blockIdx.x] = cnt_s[t];
+  if (threadIdx.x == 0) counts[(int64_t)k * nb + blockIdx.x] = wsum_s[0] + wsum_s[1] + wsum_s[2] + wsum_s[3];
 }
 
 // kstart[k] = first pair of offset k (kstart[K] = P); cstart[k] = first chunk of
@@ -421,40 +459,43 @@ __global__ void pairs_finalize_kernel(const int32_t* __restrict__ counts, int64_
   cstart[K] = c;
 }
 
-// Writes (in, out) pairs at offsets[k * nb + b] + rank, rank = position of the
-// row among the block's valid rows of offset k (rows ascending), so each
-// offset's pairs come out sorted by output row.
+// Writes the (in, out) pairs of one (row block, offset) at offsets[k * nb + b]
+// + rank, the rank counting the valid rows below in row order (j, wave, lane),
+// so each offset's pairs come out sorted by output row.
 __global__ __launch_bounds__(256) void pairs_emit_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
-                                                         int64_t n_out, int64_t n_in, int K, int64_t nb,
+                                                         int64_t n_out, int64_t n_in, int64_t nb,
                                                          const int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ pairs) {
-  __shared__ int base_s[ST_MAX_KVOL];
-  __shared__ int wcnt_s[4][ST_MAX_KVOL];
+  __shared__ int cnt_s[kPairPer * 4];
+  const int k = blockIdx.y;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  for (int t = threadIdx.x; t < K; t += 256) base_s[t] = offsets[(int64_t)t * nb + blockIdx.x];
+  const int32_t* col = map + (int64_t)k * ks;
+  const int64_t row0 = (int64_t)blockIdx.x * kPairRows + threadIdx.x;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  for (int j = 0; j < kPairRows / 256; ++j) {
-    const int64_t o = (int64_t)blockIdx.x * kPairRows + j * 256 + threadIdx.x;
-    for (int k = 0; k < K; ++k) {
-      const bool v = o < n_out && pair_valid(map[(int64_t)k * ks + o * rs], n_in);
-      const uint64_t bal = __ballot(v);
-      if (lane == 0) wcnt_s[wid][k] = (int)__popcll(bal);
+  int32_t iv[kPairPer];
+  uint64_t bal[kPairPer];
+#pragma unroll
+  for (int j = 0; j < kPairPer; ++j) {
+    const int64_t o = row0 + j * 256;
+    iv[j] = o < n_out ? col[o * rs] : -1;
+    bal[j] = __ballot(pair_valid(iv[j], n_in));
+    if (lane == 0) cnt_s[j * 4 + wid] = (int)__popcll(bal[j]);
+  }
+  __syncthreads();
+  static_assert(kPairPer * 4 == 64, "one wave scans the (step, wave) counts");
+  if (wid == 0) {
+    const int v = cnt_s[lane];
+    const int inc = wave_inclusive_scan(v);
+    cnt_s[lane] = inc - v;
+  }
+  __syncthreads();
+  const int base = offsets[(int64_t)k * nb + blockIdx.x];
+#pragma unroll
+  for (int j = 0; j < kPairPer; ++j) {
+    if (pair_valid(iv[j], n_in)) {
+      const int pos = base + cnt_s[j * 4 + wid] + (int)__popcll(bal[j] & below);
+      *reinterpret_cast<int2*>(pairs + 2 * (int64_t)pos) = make_int2(iv[j], (int32_t)(row0 + j * 256));
     }
-    __syncthreads();
-    for (int k = 0; k < K; ++k) {
-      const int32_t i = o < n_out ? map[(int64_t)k * ks + o * rs] : -1;
-      const bool v = pair_valid(i, n_in);
-      const uint64_t bal = __ballot(v);
-      if (v) {
-        int pos = base_s[k] + (int)__popcll(bal & below);
-        for (int w = 0; w < wid; ++w) pos += wcnt_s[w][k];
-        pairs[2 * (int64_t)pos] = i;
-        pairs[2 * (int64_t)pos + 1] = (int32_t)o;
-      }
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < K; t += 256) base_s[t] += wcnt_s[0][t] + wcnt_s[1][t] + wcnt_s[2][t] + wcnt_s[3][t];
-    __syncthreads();
   }
 }
 
@@ -473,14 +514,15 @@ extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t m
   if (num_blocks != (n_out + st::kPairRows - 1) / st::kPairRows) return ST_ERR_ARG;
   if ((int64_t)K * n_out >= (1ll << 31) || pair_capacity < (int64_t)K * n_out) return ST_ERR_ARG;
   if (!block_counts || !kstart || !cstart || (n_out > 0 && (!map || !pairs))) return ST_ERR_ARG;
+  const dim3 grid((unsigned)num_blocks, (unsigned)K);
   if (num_blocks > 0)
-    st::pairs_count_kernel<<<(unsigned)num_blocks, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, K,
-                                                                     num_blocks, block_counts);
+    st::pairs_count_kernel<<<grid, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, num_blocks,
+                                                     block_counts);
   st::exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, (int64_t)K * num_blocks);
   st::pairs_finalize_kernel<<<1, 64, 0, stream>>>(block_counts, num_blocks, K, chunk, kstart, cstart);
   if (num_blocks > 0)
-    st::pairs_emit_kernel<<<(unsigned)num_blocks, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, K,
-                                                                    num_blocks, block_counts, pairs);
+    st::pairs_emit_kernel<<<grid, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, num_blocks,
+                                                    block_counts, pairs);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

@@ -50,7 +50,8 @@ def compute_neighbor_indices(
 
     Same result as the reference (``conv.py:12-75``), computed by one HIP
     kernel (``st_kmap_query``) without materialising the (N_out, K, 4)
-    candidate coordinates.  The returned tensor is contiguous (N_out, K).
+    candidate coordinates.  The returned tensor is an (N_out, K) view of the
+    offset-major (K, N_out) map.
     """
     kmap = query_kernel_map(in_hash_table, out_coords, kernel_offsets, spatial_shape, stride, n_in=0)
     return kmap.neighbor_indices
@@ -63,12 +64,14 @@ def _input_table(tensor: SparseTensor, scale: int) -> HashTable:
         if cache.hashtable is None:
             t = HashTable(table_capacity(tensor.C.shape[0]), device=tensor.F.device)
             t.insert(tensor.C)
+            t.build_occupancy(tensor.C, tensor.batch_size, tensor.spatial_shape)
             cache.hashtable = t
         return cache.hashtable
     key = ("scaled_table", scale)
     if key not in cache.kmaps:
         t = HashTable(table_capacity(tensor.C.shape[0]), device=tensor.F.device)
         t.insert(tensor.C, scale=scale)
+        t.build_occupancy(tensor.C, tensor.batch_size, tensor.spatial_shape, scale=scale)
         cache.kmaps[key] = t
     return cache.kmaps[key]
 
@@ -124,7 +127,8 @@ def sparse_conv3d(
             if subm_fast:
                 out_coords, new_shape = tensor.C, tensor.spatial_shape
                 offsets = _target_offsets(k, d, p, False, device)
-                kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1, tensor.C.shape[0])
+                kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1, tensor.C.shape[0],
+                                        symmetric=(k % 2 == 1))
             else:
                 out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
                     tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)

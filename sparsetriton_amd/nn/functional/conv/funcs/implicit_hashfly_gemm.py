@@ -131,12 +131,12 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
                 grad_input = hashfly_gemm(grad_output, ctx.in_coords.contiguous(), offs, lk, gl.table_keys,
                                           gl.table_values, w, N_in)
             else:
-                nbr = torch.empty((coords.shape[0], K), dtype=torch.int32, device=coords.device)
+                nbr = torch.empty((K, coords.shape[0]), dtype=torch.int32, device=coords.device)
                 _lib.call("st_kmap_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0],
-                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
-                          _lib.ptr(nbr), 1, K, None, _lib.stream_of(coords.device))
+                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0], None,
+                          _lib.ptr(nbr), coords.shape[0], 1, None, _lib.stream_of(coords.device))
                 kmap = KernelMap(nbr, N_in, coords.shape[0], K).ensure_inverse()
-                grad_input = gather_gemm(grad_output, kmap.invnbr, 1, K, kmap.in_masks, w, N_in, K)
+                grad_input = gather_gemm(grad_output, kmap.invnbr, N_in, 1, kmap.in_masks, w, N_in, K)
         if ctx.needs_input_grad[1]:
             lk = _lookup(K, -1, s, 1, ctx.shape)
             grad_weights = hashfly_wgrad(features, grad_output, coords, offs, lk, keys, vals, weights.dtype)

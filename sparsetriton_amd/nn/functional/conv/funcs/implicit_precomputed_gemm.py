@@ -15,7 +15,10 @@ Kernels (``libsparsetriton_amd.so``):
   forward   st_gather_gemm with rows tiled in mask-sorted order, weights
             re-laid (K, C_out, C_in);
   dgrad     st_gather_gemm over the transposed map (also mask-sorted), weights
-            as stored -- a gather, so no atomics and a deterministic result;
+            as stored -- a gather, so no atomics and a deterministic result.
+            An odd-kernel submanifold map is its own transpose with offsets
+            reversed, so dgrad gathers through the forward map, masks and tile
+            order with the weights reversed along k (no inverse map is built);
   wgrad     st_wgrad_pairs over the (offset, out)-sorted pair list in
             equal-size chunks, fixed-order reduce.
 """
@@ -60,9 +63,16 @@ def gather_gemm_fwd(A: torch.Tensor, kmap: KernelMap, Bt: torch.Tensor) -> torch
 
 
 def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> torch.Tensor:
-    """Input gradient over the transposed map, in the mask-sorted order of the backward plan."""
+    """Input gradient over the transposed map, in the mask-sorted order of the backward plan.
+
+    For a symmetric (odd-kernel submanifold) map the transpose is the map read
+    with offsets reversed: dX[i] = sum_j dY[nbr[j, i]] @ W[K-1-j]^T."""
     plan = kmap.backward_plan()
-    return gather_gemm(dY, kmap.invnbr, 1, kmap.K, kmap.in_masks, W, kmap.n_in, kmap.K, rows=plan.perm)
+    if kmap.symmetric:
+        wr = weight_prep(W, _lib.W_REVERSE)
+        return gather_gemm(dY, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, wr, kmap.n_in, kmap.K,
+                           rows=plan.perm)
+    return gather_gemm(dY, kmap.invnbr, kmap.n_in, 1, kmap.in_masks, W, kmap.n_in, kmap.K, rows=plan.perm)
 
 
 def weight_prep(weights: torch.Tensor, mode: int) -> torch.Tensor:

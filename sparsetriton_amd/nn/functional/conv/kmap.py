@@ -12,10 +12,12 @@ Public functions keep the reference's names and meaning
 
 The output coordinates of a strided / transposed convolution and its kernel
 map come out of one HIP pipeline (``st_outcoords_plan`` / ``st_outcoords_emit``);
-the submanifold map comes from ``st_kmap_query``.  Maps are stored row-major
-(N, K) int32 -- the reference's layout -- with per-row offset bitmasks, in both
-directions: ``nbr[o, k]`` is the input row feeding output ``o`` through offset
-``k`` and ``invnbr[i, k]`` the output row input ``i`` feeds.
+the submanifold map comes from ``st_kmap_query``.  Maps are stored
+offset-major (K, N) int32 with per-row offset bitmasks, in both directions:
+``nbr[k, o]`` is the input row feeding output ``o`` through offset ``k`` and
+``invnbr[k, i]`` the output row input ``i`` feeds.  Every kernel that walks rows
+then touches each offset's column with coalesced accesses; the reference's
+(N, K) layout is exposed as a transposed view.
 """
 
 from typing import Optional, Tuple
@@ -89,20 +91,25 @@ def _mask_words(K: int) -> int:
 class KernelMap:
     """Kernel map of one convolution geometry on one coordinate set.
 
-    ``nbr`` (N_out, K) int32, row-major, -1 where no neighbour;
+    ``nbr`` (K, N_out) int32, offset-major, -1 where no neighbour;
     ``out_masks`` (N_out, W) row bitmasks of ``nbr`` (W = ceil(K/32));
-    ``invnbr`` (N_in, K) and ``in_masks`` (N_in, W) the transposed map, built
+    ``invnbr`` (K, N_in) and ``in_masks`` (N_in, W) the transposed map, built
     lazily by ``ensure_inverse`` for the input gradient.
-    ``nbr`` may be any strided (N_out, K) view (``k_stride``/``r_stride``).
+    ``nbr`` may also be a caller's (N_out, K) tensor (``k_stride``/``r_stride``).
     """
 
     def __init__(self, nbr: torch.Tensor, n_in: int, n_out: int, K: int, out_masks: Optional[torch.Tensor] = None,
                  invnbr: Optional[torch.Tensor] = None, in_masks: Optional[torch.Tensor] = None,
-                 k_stride: Optional[int] = None, r_stride: Optional[int] = None):
+                 k_stride: Optional[int] = None, r_stride: Optional[int] = None, symmetric: bool = False):
         self.nbr = nbr
+        # A submanifold map of an odd kernel is its own transpose with the offsets
+        # reversed: base_{K-1-k} = -base_k, so nbr[k, o] = i <=> nbr[K-1-k, i] = o
+        # (coordinates unique).  The input gradient then gathers through ``nbr``
+        # itself, with the forward's masks and tile order and reversed weights.
+        self.symmetric = bool(symmetric) and int(n_in) == int(n_out)
         self.n_in, self.n_out, self.K = int(n_in), int(n_out), int(K)
-        self.k_stride = 1 if k_stride is None else int(k_stride)
-        self.r_stride = int(K) if r_stride is None else int(r_stride)
+        self.k_stride = int(n_out) if k_stride is None else int(k_stride)
+        self.r_stride = 1 if r_stride is None else int(r_stride)
         self.out_masks = out_masks
         self.invnbr = invnbr
         self.in_masks = in_masks
@@ -134,7 +141,7 @@ class KernelMap:
             return self
         dev = self.nbr.device
         W = self.mask_words
-        self.invnbr = _lib.fill_(torch.empty((self.n_in, self.K), dtype=torch.int32, device=dev), -1)
+        self.invnbr = _lib.fill_(torch.empty((self.K, self.n_in), dtype=torch.int32, device=dev), -1)
         self.in_masks = _lib.fill_(torch.empty((self.n_in, W), dtype=torch.int32, device=dev), 0)
         need_out = self.out_masks is None
         if need_out:
@@ -159,6 +166,8 @@ class KernelMap:
 
     def backward_plan(self) -> "TilePlan":
         """Mask-sorted order of the input rows over the transposed map (input gradient)."""
+        if self.symmetric:
+            return self.forward_plan()
         if self._bwd is None:
             self.ensure_inverse()
             self._bwd = TilePlan.build(self.n_in, self.K, self.in_masks)
@@ -243,9 +252,17 @@ def _offsets_i32(kernel_offsets: torch.Tensor) -> torch.Tensor:
     return kernel_offsets.to(torch.int32).contiguous()
 
 
+def _occupancy_ref(table):
+    ref = getattr(table, "occupancy_ref", None)
+    return ref() if ref is not None else None
+
+
 def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets: torch.Tensor, spatial_shape,
-                     stride: int, n_in: int) -> KernelMap:
-    """nbr[k, o] = row of out_o * stride - t_k (bounds [0, shape)), via ``st_kmap_query``."""
+                     stride: int, n_in: int, symmetric: bool = False) -> KernelMap:
+    """nbr[k, o] = row of out_o * stride - t_k (bounds [0, shape)), via ``st_kmap_query``.
+
+    ``symmetric`` declares a submanifold map of an odd kernel (offsets ``t`` and
+    ``-t`` at k and K-1-k), whose transpose is the map itself read backwards."""
     out_coords = out_coords.contiguous()
     dev = out_coords.device
     _lib.require_device(out_coords, "out_coords")
@@ -253,14 +270,15 @@ def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets:
     K = kernel_offsets.shape[0]
     if K > _lib.MAX_KVOL:
         raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
-    nbr = torch.empty((n_out, K), dtype=torch.int32, device=dev)
+    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
     masks = torch.empty((n_out, _mask_words(K)), dtype=torch.int32, device=dev)
     sx, sy, sz = (int(v) for v in spatial_shape)
     _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out,
               _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, _lib.ptr(table.table_keys),
-              _lib.ptr(table.table_values), table.capacity, _lib.ptr(nbr), 1, K, _lib.ptr(masks),
+              _lib.ptr(table.table_values), table.capacity, _occupancy_ref(table), _lib.ptr(nbr), n_out, 1,
+              _lib.ptr(masks),
               _lib.stream_of(dev))
-    return KernelMap(nbr, n_in, n_out, K, out_masks=masks)
+    return KernelMap(nbr, n_in, n_out, K, out_masks=masks, symmetric=symmetric)
 
 
 class OutCoordTable:
@@ -324,8 +342,8 @@ def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size
     nbr = invnbr = out_masks = in_masks = None
     if with_map:
         W = _mask_words(K)
-        nbr = _lib.fill_(torch.empty((n_out, K), dtype=torch.int32, device=dev), -1)
-        invnbr = _lib.fill_(torch.empty((n, K), dtype=torch.int32, device=dev), -1)
+        nbr = _lib.fill_(torch.empty((K, n_out), dtype=torch.int32, device=dev), -1)
+        invnbr = _lib.fill_(torch.empty((K, n), dtype=torch.int32, device=dev), -1)
         out_masks = _lib.fill_(torch.empty((n_out, W), dtype=torch.int32, device=dev), 0)
         in_masks = _lib.fill_(torch.empty((n, W), dtype=torch.int32, device=dev), 0)
     ik = iv = None

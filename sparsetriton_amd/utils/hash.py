@@ -78,6 +78,7 @@ class HashTable:
             self.table_values = torch.empty((capacity,), dtype=torch.int32, device=device)
             self.clear()
         self.status = None
+        self.occupancy = None  # (words tensor, ctypes st_occupancy) once build_occupancy() ran
 
     # ------------------------------------------------------------ properties
     @property
@@ -106,6 +107,7 @@ class HashTable:
     # ------------------------------------------------------------ operations
     def clear(self) -> "HashTable":
         """Mark every slot empty (keys and values all-ones, i.e. -1)."""
+        self.occupancy = None
         if self.table_keys.is_cuda:
             _lib.fill_(self.table_keys, -1)
             _lib.fill_(self.table_values, -1)
@@ -141,6 +143,37 @@ class HashTable:
         _lib.call("st_hash_insert", _lib.ptr(keys), _lib.coord_code(keys.dtype), n, int(scale),
                   _lib.ptr(self.table_keys), _lib.ptr(self.table_values), self.capacity,
                   _lib.ptr(self._status()), _lib.stream_of(self.device))
+
+    def build_occupancy(self, coords: torch.Tensor, batch_size: int, spatial_shape, scale: int = 1) -> bool:
+        """Occupancy bitmap of the inserted ``coords`` over (batch_size, *spatial_shape).
+
+        Kernel-map queries test a voxel's bit before probing, so absent
+        neighbours cost one cached word load.  The bitmap (1 bit per voxel of
+        the box) is built only when it is no larger than one 8-byte read per
+        query of a 27-offset map (216 bytes per row) and at most 1 GiB;
+        returns whether it was built.  ``scale`` is the insert's scale.
+        """
+        n = coords.shape[0]
+        sx, sy, sz = (int(v) for v in spatial_shape)
+        if n == 0 or batch_size <= 0 or min(sx, sy, sz) <= 0 or max(sx, sy, sz) > 65536 or batch_size > 32768:
+            self.occupancy = None
+            return False
+        nw = _lib.ctypes.c_int64()
+        _lib.call("st_occupancy_words", int(batch_size), sx, sy, sz, _lib.ctypes.byref(nw))
+        if nw.value * 8 > min(216 * n, 1 << 30):
+            self.occupancy = None
+            return False
+        coords = coords.contiguous()
+        words = torch.empty((nw.value,), dtype=torch.int64, device=self.device)
+        _lib.call("st_occupancy_build", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(words),
+                  int(batch_size), sx, sy, sz, _lib.stream_of(self.device))
+        occ = _lib.Occupancy(words.data_ptr(), int(batch_size), (_lib.ctypes.c_int64 * 3)(sx, sy, sz), int(scale))
+        self.occupancy = (words, occ)
+        return True
+
+    def occupancy_ref(self):
+        """ctypes pointer to the bitmap descriptor, or None."""
+        return None if self.occupancy is None else _lib.ctypes.byref(self.occupancy[1])
 
     def query(self, keys: torch.Tensor) -> torch.Tensor:
         """Row index of each (N, 4) coordinate, or -1 when absent (int32, shape (N,))."""

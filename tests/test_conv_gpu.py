@@ -155,9 +155,10 @@ def test_mixed_precision_weight_grad_dtype(device):
 # ---------------------------------------------- algorithms / determinism
 
 def test_hashfly_equals_precomputed(device):
-    # Forward and input gradient accumulate each row's offsets in the same order in both
-    # algorithms, so they agree bitwise; the weight gradients sum pairs in different
-    # (fixed) orders and agree to fp32 rounding.
+    # The forward accumulates each row's offsets in the same order in both algorithms, so
+    # it agrees bitwise.  The submanifold input gradient of the precomputed path walks the
+    # offsets in reverse (it reads the map's symmetric transpose) and the weight gradients
+    # sum pairs in different fixed orders: both agree to fp32 rounding.
     rng = np.random.default_rng(21)
     c = _rand_coords(rng, 6000, 24)
     X = rng.standard_normal((6000, 32)).astype(np.float32)
@@ -165,7 +166,7 @@ def test_hashfly_equals_precomputed(device):
     dY = rng.standard_normal((6000, 32)).astype(np.float32)
     res = [_run(device, c, (24, 24, 24), X, W, dY, 3, 1, 1, 1, False, True, torch.float32, a) for a in ConvAlgo]
     assert torch.equal(res[0][0].F, res[1][0].F)
-    assert torch.equal(res[0][1], res[1][1])
+    assert rel(res[0][1].cpu(), res[1][1].cpu()) < 1e-6
     assert rel(res[0][2].cpu(), res[1][2].cpu()) < 1e-6
 
 

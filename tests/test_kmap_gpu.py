@@ -44,7 +44,7 @@ def _check_masks(kmap):
 def _check_inverse(kmap):
     kmap.ensure_inverse()
     nbr = kmap.neighbor_indices.cpu().numpy().T  # (K, N_out)
-    inv = kmap.invnbr.cpu().numpy().T  # (K, N_in)
+    inv = kmap.invnbr.cpu().numpy()  # (K, N_in)
     K = kmap.K
     for k in range(K):
         o = np.nonzero(nbr[k] >= 0)[0]
@@ -224,7 +224,7 @@ def test_tile_plan_and_pair_list(device):
     kmap = _subm(device, c, (24, 24, 24))
     nbr = kmap.neighbor_indices.cpu().numpy().T  # (K, N)
     K, N = nbr.shape
-    assert kmap.nbr.is_contiguous() and kmap.nbr.shape == (N, K)
+    assert kmap.nbr.is_contiguous() and kmap.nbr.shape == (K, N)
     for plan, masks in ((kmap.forward_plan(), kmap.out_masks), (kmap.backward_plan(), None)):
         if masks is None:
             masks = kmap.in_masks
@@ -251,6 +251,65 @@ def test_tile_plan_and_pair_list(device):
     assert cs[-1] <= pl.max_chunks
 
 
+@pytest.mark.parametrize("k,d", [(3, 1), (5, 1), (3, 2)])
+def test_subm_map_is_its_own_transpose(device, k, d):
+    """An odd-kernel submanifold map read with offsets reversed equals the explicit
+    transposed map (st_kmap_invert), which the symmetric input gradient relies on."""
+    rng = np.random.default_rng(40 + k + d)
+    c = _rand_coords(rng, 7000, 20)
+    kmap = _subm(device, c, (20, 20, 20), k=k, d=d)
+    kmap.ensure_inverse()
+    assert torch.equal(kmap.invnbr, kmap.nbr.flip(0))
+    K = k ** 3
+    bits = np.unpackbits(kmap.out_masks.cpu().numpy().view(np.uint8), axis=1, bitorder="little")[:, :K]
+    ibits = np.unpackbits(kmap.in_masks.cpu().numpy().view(np.uint8), axis=1, bitorder="little")[:, :K]
+    assert np.array_equal(ibits, bits[:, ::-1])
+    # input gradient through the symmetric map == through the explicit transpose
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import gather_gemm_dgrad
+    from sparsetriton_amd.nn.functional.conv.kmap import KernelMap
+    explicit = KernelMap(kmap.nbr, kmap.n_in, kmap.n_out, K, out_masks=kmap.out_masks, invnbr=kmap.invnbr,
+                         in_masks=kmap.in_masks)
+    sym = KernelMap(kmap.nbr, kmap.n_in, kmap.n_out, K, out_masks=kmap.out_masks, symmetric=True)
+    for dtype, tol in ((torch.float32, 1e-5), (torch.bfloat16, 1e-2)):
+        dY = torch.randn(kmap.n_out, 48, device=device, dtype=dtype)
+        W = torch.randn(K, 40, 48, device=device, dtype=dtype)
+        a = gather_gemm_dgrad(dY, sym, W).float()
+        b = gather_gemm_dgrad(dY, explicit, W).float()
+        assert (torch.linalg.norm(a - b) / torch.linalg.norm(b)).item() < tol
+
+
+def _fold_keys(masks):
+    """32-bit sort key of a (n, W) mask array: word w rotated left by 7w, xor-folded."""
+    m = masks.astype(np.uint64)
+    key = m[:, 0].copy()
+    for w in range(1, m.shape[1]):
+        r = (7 * w) & 31
+        key ^= ((m[:, w] << np.uint64(r)) | (m[:, w] >> np.uint64(32 - r))) & np.uint64(0xFFFFFFFF) if r else m[:, w]
+    return key.astype(np.uint32)
+
+
+@pytest.mark.parametrize("n,K", [(0, 27), (1, 27), (4095, 8), (4097, 1), (300_001, 27), (123_457, 125), (70_000, 343)])
+def test_sort_rows_stable(device, n, K):
+    """st_kmap_sort_rows is a stable sort of rows by their (folded) offset mask:
+    equal to numpy's stable argsort across many 4096-row tiles and all digits."""
+    from sparsetriton_amd.nn.functional.conv.kmap import TilePlan
+    rng = np.random.default_rng(n + K)
+    W = (K + 31) // 32
+    # few distinct masks (long equal runs test stability) mixed with random ones
+    pool = rng.integers(0, 2**32, size=(64, W), dtype=np.uint64).astype(np.uint32)
+    if K % 32:
+        pool[:, -1] &= np.uint32((1 << (K % 32)) - 1)
+    masks = pool[rng.integers(0, 64, size=n)]
+    rnd = rng.random(n) < 0.3
+    masks[rnd] = rng.integers(0, 2**32, size=(int(rnd.sum()), W), dtype=np.uint64).astype(np.uint32)
+    if K % 32 and n:
+        masks[:, -1] &= np.uint32((1 << (K % 32)) - 1)
+    m_t = torch.from_numpy(masks.view(np.int32).copy()).to(device)
+    perm = TilePlan.build(n, K, m_t).perm.cpu().numpy()
+    expect = np.argsort(_fold_keys(masks), kind="stable")
+    assert np.array_equal(perm, expect)
+
+
 def test_wgrad_scan_matches_pairs(device):
     from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import wgrad, wgrad_scan
     rng = np.random.default_rng(32)
@@ -265,3 +324,34 @@ def test_wgrad_scan_matches_pairs(device):
         for r in (a, b):
             err = np.linalg.norm(r.cpu().numpy() - ref) / np.linalg.norm(ref)
             assert err < (2e-3 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("case", ["subm", "transposed"])
+def test_occupancy_filter_changes_nothing(device, case):
+    """Kernel maps with and without the occupancy bitmap are identical (the bitmap only skips
+    probes that would miss), for the plain table and for a scaled (transposed) table."""
+    rng = np.random.default_rng(77)
+    c = _rand_coords(rng, 9000, 24, B=3)
+    coords = torch.as_tensor(c, dtype=torch.int16, device=device)
+    sp = SparseTensor(torch.zeros((c.shape[0], 1), device=device), coords, spatial_shape=(24, 24, 24))
+    if case == "subm":
+        table = _input_table(sp, 1)
+        assert table.occupancy is not None
+        offs = _target_offsets(3, 1, 1, False, device)
+        q, shape, stride = sp.C, (24, 24, 24), 1
+    else:
+        s = 2
+        table = _input_table(sp, s)
+        assert table.occupancy is not None and table.occupancy[1].scale == s
+        offs = _target_offsets(3, 1, 1, True, device)
+        q, shape, stride = build_out_coords(sp.C, (24, 24, 24), 3, stride=s, padding=1, transposed=True,
+                                            submanifold=False)[0], (48, 48, 48), 1
+    with_bm = query_kernel_map(table, q, offs, shape, stride, c.shape[0]).neighbor_indices.clone()
+    occ = table.occupancy
+    table.occupancy = None
+    try:
+        without = query_kernel_map(table, q, offs, shape, stride, c.shape[0]).neighbor_indices
+    finally:
+        table.occupancy = occ
+    assert torch.equal(with_bm, without)
+    assert int((with_bm >= 0).sum()) > c.shape[0]
