@@ -42,7 +42,12 @@ enum st_status_code {
 
 enum st_coord_dtype { ST_COORD_I16 = 0, ST_COORD_I32 = 1, ST_COORD_I64 = 2 };
 
-enum st_dtype { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2 };
+/* Feature dtypes.  ST_F32_BF16X3: fp32 tensors whose products are computed
+ * as three bf16 MFMAs over hi/lo splits of each operand (hi*hi + hi*lo +
+ * lo*hi, relative error per product <= ~2^-15, fp32 accumulation) -- the
+ * matrix-core path for fp32, as TF32 is for the reference's tl.dot.  Entry
+ * points without a split kernel compute ST_F32_BF16X3 in plain fp32. */
+enum st_dtype { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2, ST_F32_BF16X3 = 3 };
 
 /* Device status words, accumulated by atomics (caller zeroes them). */
 enum st_status_word {

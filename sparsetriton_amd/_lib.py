@@ -165,6 +165,20 @@ def feat_code(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported feature dtype {dtype}; use float32, float16 or bfloat16") from None
 
 
+F32_BF16X3 = 3
+
+
+def compute_code(dtype: torch.dtype) -> int:
+    """dtype code for a GEMM entry point: fp32 follows ``config.get_fp32_precision()``."""
+    code = feat_code(dtype)
+    if code == 0:
+        from sparsetriton_amd.config import get_fp32_precision
+
+        if get_fp32_precision() == "bf16x3":
+            return F32_BF16X3
+    return code
+
+
 def fill_(t: torch.Tensor, value: int) -> torch.Tensor:
     """Fill a 4- or 8-byte-element device tensor with a raw bit pattern via the library."""
     s = stream_of(t.device)

@@ -18,6 +18,13 @@ Differences in meaning, both deliberate:
   never reads it either (its kernels hard-code 128 probes, ``utils/hash.py:211``);
   this package's probes are bounded by the table size, so an insert can only
   fail when the table is full, and that failure is reported, not dropped.
+
+One addition: ``set_fp32_precision`` picks how fp32 convolutions use the
+matrix cores.  The reference's fp32 ``tl.dot`` runs in TF32 on NVIDIA GPUs
+(10-bit mantissa products).  Here the default ``"bf16x3"`` splits each fp32
+operand into two bf16 parts and sums three bf16 MFMA products (relative error
+per product about 2^-15, fp32 accumulation); ``"ieee"`` uses the fp32 MFMA
+instructions (one-sixteenth of the bf16 rate on gfx950).
 """
 
 from enum import Enum
@@ -34,8 +41,13 @@ __all__ = [
     "get_h_table_f",
     "set_h_table_max_p",
     "get_h_table_max_p",
+    "set_fp32_precision",
+    "get_fp32_precision",
+    "FP32_PRECISIONS",
     "MIN_TABLE_FACTOR",
 ]
+
+FP32_PRECISIONS = ("bf16x3", "ieee")
 
 # Lowest slots-per-key ratio the hash table is built with (load factor 0.5).
 MIN_TABLE_FACTOR = 2.0
@@ -59,6 +71,7 @@ _STATE: dict = {
     "algo": ConvAlgo.PrecomputedNeighborGEMM,
     "h_tbl_factor": 1.5,
     "h_tbl_max_probe_n": 16,
+    "fp32_precision": "bf16x3",
 }
 
 
@@ -114,3 +127,15 @@ def set_h_table_max_p(probe_n) -> None:
 def get_h_table_max_p() -> int:
     """Return the (compatibility-only) maximum probe count."""
     return _STATE["h_tbl_max_probe_n"]
+
+
+def set_fp32_precision(precision: str) -> None:
+    """Matrix-core arithmetic of fp32 convolutions: ``"bf16x3"`` (default) or ``"ieee"``."""
+    if precision not in FP32_PRECISIONS:
+        raise ValueError(f"fp32 precision must be one of {FP32_PRECISIONS}, got {precision!r}")
+    _STATE["fp32_precision"] = precision
+
+
+def get_fp32_precision() -> str:
+    """Current fp32 matrix-core arithmetic (``"bf16x3"`` or ``"ieee"``)."""
+    return _STATE["fp32_precision"]

@@ -6,11 +6,26 @@ ST_GEMM_OPS(extern, float)
 ST_GEMM_OPS(extern, _Float16)
 ST_GEMM_OPS(extern, __bf16)
 
+namespace st {
+int ops_gather_map_x3(const float* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs,
+                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, int64_t n_dst,
+                      int K, int Kd, int Nd, hipStream_t stream);
+int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
+                       const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const float* Bt,
+                       float* out, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
+int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
+                       const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
+                       float* partials, void* dW, int dw_dtype, hipStream_t stream);
+}  // namespace st
+
 using namespace st;
 
+// ST_F32_BF16X3 dispatches like ST_F32 except where a call site names its
+// split-operand kernel first.
 #define ST_DISPATCH_DTYPE(dt, T, ...) \
   switch (dt) {                       \
-    case ST_F32: {                    \
+    case ST_F32:                      \
+    case ST_F32_BF16X3: {             \
       using T = float;                \
       return __VA_ARGS__;             \
     }                                 \
@@ -46,6 +61,9 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
   if (n_dst == 0) return ST_OK;
   if (!map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
   const int W = (K + 31) / 32;
+  if (dtype == ST_F32_BF16X3)
+    return ops_gather_map_x3((const float*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
+                             (const float*)Bt, (float*)out, n_dst, K, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_map<T>((const T*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
                                       (const T*)Bt, (T*)out, n_dst, K, Kd, Nd, stream));
@@ -70,6 +88,9 @@ int st_wgrad_pairs(const void* X, const void* dY, const int32_t* pairs, const in
       C_out <= 0)
     return ST_ERR_ARG;
   if (!kstart || !cstart || !partials || !dW || (max_chunks > 0 && (!pairs || !X || !dY))) return ST_ERR_ARG;
+  if (dtype == ST_F32_BF16X3)
+    return ops_wgrad_pairs_x3((const float*)X, (const float*)dY, pairs, kstart, cstart, K, chunk, max_chunks, C_in,
+                              C_out, partials, dW, dw_dtype, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_wgrad_pairs<T>((const T*)X, (const T*)dY, pairs, kstart, cstart, K, chunk, max_chunks, C_in,
                                        C_out, partials, dW, dw_dtype, stream));
@@ -82,6 +103,9 @@ int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int co
   if (capacity <= 0 || capacity >= (1ll << 31) || n_dst >= (1ll << 31)) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!dst_coords || !offsets || !keys || !vals || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
+  if (dtype == ST_F32_BF16X3)
+    return ops_gather_hash_x3((const float*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
+                              (const float*)Bt, (float*)out, n_dst, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_hash<T>((const T*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
                                        (const T*)Bt, (T*)out, n_dst, Kd, Nd, stream));

@@ -525,6 +525,122 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
   }
 }
 
+// 16-bit, one MFMA k-step (32 pairs) per wave at a time, no workgroup barrier
+// inside a chunk: the four waves take the chunk's 32-pair steps round-robin.
+// Each wave stages its step's X and dY rows in its own LDS area row-major
+// (pair-major, 16-byte stores straight from the gathered rows) and reads the
+// MFMA fragments -- 8 pairs of one channel per lane -- with 16-bit LDS reads.
+// Pair p of a step lives in LDS row p, and lane group g takes pairs 4e + g
+// (e = 0..7) for both operands (any common assignment gives the same sum), so
+// with an 80-element row pitch the four groups hit disjoint LDS banks.
+// The wave tile is the workgroup's whole 64 x 64 channel tile (16 blocks);
+// the waves' accumulators are summed through LDS once per chunk.  Requires
+// C_in and C_out multiples of 64 and 16-byte aligned rows.
+constexpr int kWvPitch = 80;
+template <typename T>
+__global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
+                                                               const int2* __restrict__ pairs,
+                                                               const int32_t* __restrict__ kstart,
+                                                               const int32_t* __restrict__ cstart, int K, int chunk,
+                                                               int Cin, int Cout, float* __restrict__ partials) {
+  using F = typename Frag<T>::type;
+  static_assert(Frag<T>::KSTEP == 32 && Frag<T>::VEC == 8, "16-bit MFMA fragments");
+  constexpr int STAGE = 32 * kWvPitch;  // elements per operand per wave
+  constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(T);
+  constexpr int RP = 68;                // row pitch (floats) of the per-wave tiles summed at the end
+  constexpr int RED_BYTES = 4 * 64 * RP * (int)sizeof(float);
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  __syncthreads();
+  const int total = cstart_s[K];
+
+  const int ntn = Cout / 64;
+  const int cm0 = (blockIdx.z / ntn) * 64, cn0 = (blockIdx.z % ntn) * 64;
+  T* xs = reinterpret_cast<T*>(lds) + wid * 2 * STAGE;
+  T* ys = xs + STAGE;
+  float* red = reinterpret_cast<float*>(lds);
+  // loader lanes: pair lp of the step, channel half lh (32 channels = 4 x 8)
+  const int lp = lane >> 1, lh = lane & 1;
+
+  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+    const int k = chunk_offset(cstart_s, K, cidx);
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
+    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    F xr[4], yr[4];
+    auto load_step = [&](int q) {
+      const int p = q + lp;
+      int2 pr = make_int2(-1, -1);
+      if (p < p1) pr = pairs[p];
+      const F* xrow = reinterpret_cast<const F*>(X + (int64_t)(pr.x >= 0 ? pr.x : 0) * Cin + cm0 + lh * 32);
+      const F* yrow = reinterpret_cast<const F*>(dY + (int64_t)(pr.y >= 0 ? pr.y : 0) * Cout + cn0 + lh * 32);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        xr[v] = pr.x >= 0 ? xrow[v] : zero_frag<T>();
+        yr[v] = pr.y >= 0 ? yrow[v] : zero_frag<T>();
+      }
+    };
+    int q = p0 + wid * 32;
+    if (q < p1) load_step(q);
+    for (; q < p1; q += 128) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        *reinterpret_cast<F*>(&xs[lp * kWvPitch + lh * 32 + v * 8]) = xr[v];
+        *reinterpret_cast<F*>(&ys[lp * kWvPitch + lh * 32 + v * 8]) = yr[v];
+      }
+      // LDS operations of one wave complete in order: the reads below see the
+      // stores above; the fence keeps the compiler from moving them across.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (q + 128 < p1) load_step(q + 128);
+      F a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[i][e] = xs[(e * 4 + g) * kWvPitch + i * 16 + c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[i][e] = ys[(e * 4 + g) * kWvPitch + i * 16 + c];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // sum the four waves' tiles through LDS; every thread then adds and stores
+    // 16 elements of the 64 x 64 partial, row-contiguous
+    __syncthreads();
+    float* mine = red + wid * 64 * RP;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * RP + j * 16 + c] = acc[i][j][r];
+    __syncthreads();
+    float* part = partials + (int64_t)cidx * Cin * Cout;
+#pragma unroll 4
+    for (int m = 0; m < 16; ++m) {
+      const int e = tid + m * 256;
+      const int row = e >> 6, col = e & 63;
+      const float s = red[row * RP + col] + red[64 * RP + row * RP + col] + red[128 * RP + row * RP + col] +
+                      red[192 * RP + row * RP + col];
+      part[(int64_t)(cm0 + row) * Cout + cn0 + col] = s;
+    }
+    __syncthreads();
+  }
+}
+
 // dW[k][e] = sum of partials[c][e] over offset k's chunks.  A 256-thread block
 // covers 32 consecutive elements of one offset; its 8 thread groups take the
 // chunks round-robin and are combined in a fixed order (deterministic).
@@ -767,6 +883,7 @@ static int launch_wgrad_reduce(const float* partials, const int32_t* cstart_or_n
     wgrad_reduce_kernel<TW><<<gr, 256, 0, stream>>>(partials, per_k, (int)splits, K, (TW*)dW);
   switch (dw_dtype) {
     case ST_F32:
+    case ST_F32_BF16X3:
       ST_REDUCE(float);
       break;
     case ST_F16:
@@ -816,6 +933,17 @@ static void launch_wgrad_pairs_f32(const float* X, const float* dY, const int2* 
 
 static int pow2_tile(int blocks) { return blocks >= 4 ? 4 : (blocks >= 2 ? 2 : 1); }
 
+// 16-bit weight-gradient kernel: 0 = per-wave steps (default), 1 = workgroup
+// LDS transpose (ST_WGRAD16=lds selects it, for comparison runs).
+static int wgrad16_mode() {
+  static int mode = -1;
+  if (mode < 0) {
+    const char* e = getenv("ST_WGRAD16");
+    mode = (e && e[0] == 'l') ? 1 : 0;
+  }
+  return mode;
+}
+
 template <typename T>
 int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
                     int K, int chunk, int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
@@ -835,10 +963,18 @@ int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t
       const int vec_x = (Cin % VEC == 0) && ((uintptr_t)X % 16 == 0);
       const int vec_y = (Cout % VEC == 0) && ((uintptr_t)dY % 16 == 0);
       const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
-      const unsigned gz = (unsigned)(((MB + 7) / 8) * ((NB + 7) / 8));
       const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
-      const int nloc = (MB < 8 ? MB : 8) * (NB < 8 ? NB : 8);
       const int2* pr = reinterpret_cast<const int2*>(pairs);
+      const int mode = wgrad16_mode();
+      if (mode == 0 && Cin % 64 == 0 && Cout % 64 == 0 && vec_x && vec_y) {
+        const unsigned gz64 = (unsigned)((Cin / 64) * (Cout / 64));
+        wgrad_pairs_wave_kernel<T><<<dim3(gx, 1, gz64), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+                                                                          Cout, partials);
+        ST_CHECK_LAUNCH();
+        return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
+      }
+      const unsigned gz = (unsigned)(((MB + 7) / 8) * ((NB + 7) / 8));
+      const int nloc = (MB < 8 ? MB : 8) * (NB < 8 ? NB : 8);
       if (nloc <= 4)
         wgrad_pairs_lds_kernel<T, 1><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
                                                                           Cout, partials, vec_x, vec_y);

@@ -1,0 +1,395 @@
+// fp32 gather-GEMM and weight gradient on bf16 MFMA with split operands.
+//
+// gfx950's matrix cores run bf16 at 16x the fp32 rate.  Each fp32 operand x
+// is split into bf16 parts hi = bf16(x) and lo = bf16(x - hi), so
+// x = hi + lo + d with |d| <= 2^-18 |x|, and a product is taken as
+//     a*b ~= ah*bh + ah*bl + al*bh           (three bf16 MFMAs)
+// leaving out al*bl (<= 2^-16 |ab|).  Products are exact in the fp32
+// accumulator, so every product carries a relative error of at most ~2^-15
+// (3e-5) -- about 16x tighter than a TF32 product (10-bit mantissa) --
+// and sums accumulate in fp32 as in the plain fp32 kernels.  Inputs,
+// outputs and weights stay fp32 in HBM; the split happens in registers as
+// tiles are loaded.
+//
+// The kernels mirror the 16-bit ones (gemm_kernels.h): the forward / input
+// gradient gather-GEMM with a double-buffered B tile in LDS (hi and lo
+// planes) and A rows prefetched one offset ahead; the weight gradient with
+// per-wave 32-pair steps staged row-major in LDS.
+#pragma once
+
+#include "gemm_kernels.h"
+
+namespace st {
+
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+
+// hi/lo bf16 split of 8 consecutive fp32 values.
+__device__ __forceinline__ void split8(const v4f& x0, const v4f& x1, v8bf& hi, v8bf& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const __bf16 h0 = (__bf16)x0[e];
+    const __bf16 h1 = (__bf16)x1[e];
+    hi[e] = h0;
+    hi[e + 4] = h1;
+    lo[e] = (__bf16)(x0[e] - (float)h0);
+    lo[e + 4] = (__bf16)(x1[e] - (float)h1);
+  }
+}
+
+__device__ __forceinline__ v4f mfma_x3(const v8bf& ah, const v8bf& al, const v8bf& bh, const v8bf& bl, v4f acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+// ------------------------------------------------------ forward / dgrad
+//
+// Same structure as gather_gemm_pipe_kernel: 128 destination rows per
+// workgroup (a wave owns 32), BN output columns, the tile's active offsets
+// in klist order, sources of up to kSrcGroup offsets resolved into LDS at
+// once.  Reduction steps are 32 wide (KS steps cover Kd).
+template <int BN, int KS, typename Src>
+__global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
+    const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
+    const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd,
+    int vec_a, int vec_b) {
+  constexpr int KDP = KS * 32;
+  constexpr int PITCH = KDP + 8;  // bf16 elements per LDS row of the B tile
+  constexpr int NBLK = BN / 16;
+  constexpr int CV = KDP / 4;  // 4-float chunks per B row
+  constexpr int BREGS = (BN * CV + 255) / 256;
+  __shared__ __attribute__((aligned(16))) __bf16 bt_s[2][2][BN * PITCH];  // [buffer][hi, lo]
+  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ int32_t drow_s[kGemmBM];
+  __shared__ int16_t klist_s[ST_MAX_KVOL];
+  __shared__ int32_t src_s[kSrcGroup][kGemmBM];
+  __shared__ int nk_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
+  const int n0 = blockIdx.y * BN;
+
+  if (tid < kGemmBM) {
+    const int64_t r = row0 + tid;
+    drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
+  }
+  if (tid < W) tmask_s[tid] = 0;
+  __syncthreads();
+  if (masks) {
+    for (int w = 0; w < W; ++w) {
+      uint32_t v = 0;
+      if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
+      v = wave_or(v);
+      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+    }
+  } else if (tid < W) {
+    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int nk = 0;
+    for (int w = 0; w < W; ++w) {
+      uint32_t bits = tmask_s[w];
+      while (bits) {
+        klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+        bits &= bits - 1;
+      }
+    }
+    nk_s = nk;
+  }
+  __syncthreads();
+  const int nk = nk_s;
+
+  const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
+  const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
+  auto resolve_group = [&](int g0) {
+    const int ng = min(kSrcGroup, nk - g0);
+    for (int j = tid >> 7; j < ng; j += 2) {
+      int32_t v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+      if ((int64_t)v >= n_src) v = -1;
+      src_s[j][tid & (kGemmBM - 1)] = v;
+    }
+  };
+  auto sources = [&](int i, int32_t& s0, int32_t& s1) -> bool {
+    const int j = i % kSrcGroup;
+    s0 = src_s[j][wid * 32 + c];
+    s1 = src_s[j][wid * 32 + 16 + c];
+    return __ballot(s0 >= 0 || s1 >= 0) != 0ull;
+  };
+  // raw fp32 A fragments: [m][step][half] = 4 consecutive reduction elements
+  auto load_a = [&](int32_t s0, int32_t s1, v4f (&a)[2][KS][2]) {
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int col = j * 32 + g * 8 + h * 4;
+        a[0][j][h] = s0 >= 0 ? load_frag<float>(A + (int64_t)s0 * Kd, col, Kd, vec_a) : zero_frag<float>();
+        a[1][j][h] = s1 >= 0 ? load_frag<float>(A + (int64_t)s1 * Kd, col, Kd, vec_a) : zero_frag<float>();
+      }
+    }
+  };
+  auto load_b = [&](int k, v4f (&b)[BREGS]) {
+#pragma unroll
+    for (int j = 0; j < BREGS; ++j) {
+      const int idx = tid + j * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      b[j] = zero_frag<float>();
+      if (idx < BN * CV && n0 + nr < Nd)
+        b[j] = load_frag<float>(Bt + ((int64_t)k * Nd + n0 + nr) * Kd, cv * 4, Kd, vec_b);
+    }
+  };
+  auto store_b = [&](int buf, const v4f (&b)[BREGS]) {
+#pragma unroll
+    for (int j = 0; j < BREGS; ++j) {
+      const int idx = tid + j * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      if (idx < BN * CV) {
+        v4bf hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hi[e] = (__bf16)b[j][e];
+          lo[e] = (__bf16)(b[j][e] - (float)hi[e]);
+        }
+        *reinterpret_cast<v4bf*>(&bt_s[buf][0][nr * PITCH + cv * 4]) = hi;
+        *reinterpret_cast<v4bf*>(&bt_s[buf][1][nr * PITCH + cv * 4]) = lo;
+      }
+    }
+  };
+
+  v4f acc[2][NBLK];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    v4f a_cur[2][KS][2], a_nxt[2][KS][2];
+    v4f breg[BREGS];
+    int32_t s0, s1;
+    resolve_group(0);
+    load_b(klist_s[0], breg);
+    store_b(0, breg);
+    __syncthreads();
+    bool any_cur = sources(0, s0, s1);
+    load_a(s0, s1, a_cur);
+    for (int i = 0; i < nk; ++i) {
+      const bool has_next = i + 1 < nk;
+      bool any_nxt = false;
+      if (has_next && (i + 1) % kSrcGroup == 0) {
+        __syncthreads();
+        resolve_group(i + 1);
+        __syncthreads();
+      }
+      if (has_next) {
+        const int kn = klist_s[i + 1];
+        int32_t t0, t1;
+        any_nxt = sources(i + 1, t0, t1);
+        load_a(t0, t1, a_nxt);
+        load_b(kn, breg);
+      }
+      if (any_cur) {
+        const __bf16* bh_s = bt_s[i & 1][0];
+        const __bf16* bl_s = bt_s[i & 1][1];
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+          v8bf ah[2], al[2];
+          split8(a_cur[0][j][0], a_cur[0][j][1], ah[0], al[0]);
+          split8(a_cur[1][j][0], a_cur[1][j][1], ah[1], al[1]);
+#pragma unroll
+          for (int nb = 0; nb < NBLK; ++nb) {
+            const int off = (nb * 16 + c) * PITCH + j * 32 + g * 8;
+            const v8bf bh = *reinterpret_cast<const v8bf*>(&bh_s[off]);
+            const v8bf bl = *reinterpret_cast<const v8bf*>(&bl_s[off]);
+            acc[0][nb] = mfma_x3(ah[0], al[0], bh, bl, acc[0][nb]);
+            acc[1][nb] = mfma_x3(ah[1], al[1], bh, bl, acc[1][nb]);
+          }
+        }
+      }
+      if (has_next) store_b((i + 1) & 1, breg);
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+          a_cur[m][j][0] = a_nxt[m][j][0];
+          a_cur[m][j][1] = a_nxt[m][j][1];
+        }
+      any_cur = any_nxt;
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+      if (drow < 0) continue;
+      float* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) {
+        const int col = n0 + nb * 16 + c;
+        if (col < Nd) orow[col] = acc[m][nb][r];
+      }
+    }
+}
+
+// ------------------------------------------------------ weight gradient
+//
+// As wgrad_pairs_wave_kernel with fp32 rows: a wave stages its 32-pair step
+// (X and dY rows, 64 channels each) in LDS as fp32 and splits the fragments
+// as it reads them.  Requires C_in, C_out multiples of 64, 16-byte aligned.
+constexpr int kWvPitchF = 72;
+__global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __restrict__ X,
+                                                                const float* __restrict__ dY,
+                                                                const int2* __restrict__ pairs,
+                                                                const int32_t* __restrict__ kstart,
+                                                                const int32_t* __restrict__ cstart, int K, int chunk,
+                                                                int Cin, int Cout, float* __restrict__ partials) {
+  constexpr int STAGE = 32 * kWvPitchF;  // floats per operand per wave
+  constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(float);
+  constexpr int RP = 68;
+  constexpr int RED_BYTES = 4 * 64 * RP * (int)sizeof(float);
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  __syncthreads();
+  const int total = cstart_s[K];
+
+  const int ntn = Cout / 64;
+  const int cm0 = (blockIdx.z / ntn) * 64, cn0 = (blockIdx.z % ntn) * 64;
+  float* xs = reinterpret_cast<float*>(lds) + wid * 2 * STAGE;
+  float* ys = xs + STAGE;
+  float* red = reinterpret_cast<float*>(lds);
+  const int lp = lane >> 1, lh = lane & 1;
+
+  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+    const int k = chunk_offset(cstart_s, K, cidx);
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
+    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f xr[8], yr[8];
+    auto load_step = [&](int q) {
+      const int p = q + lp;
+      int2 pr = make_int2(-1, -1);
+      if (p < p1) pr = pairs[p];
+      const v4f* xrow = reinterpret_cast<const v4f*>(X + (int64_t)(pr.x >= 0 ? pr.x : 0) * Cin + cm0 + lh * 32);
+      const v4f* yrow = reinterpret_cast<const v4f*>(dY + (int64_t)(pr.y >= 0 ? pr.y : 0) * Cout + cn0 + lh * 32);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        xr[v] = pr.x >= 0 ? xrow[v] : zero_frag<float>();
+        yr[v] = pr.y >= 0 ? yrow[v] : zero_frag<float>();
+      }
+    };
+    int q = p0 + wid * 32;
+    if (q < p1) load_step(q);
+    for (; q < p1; q += 128) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        *reinterpret_cast<v4f*>(&xs[lp * kWvPitchF + lh * 32 + v * 4]) = xr[v];
+        *reinterpret_cast<v4f*>(&ys[lp * kWvPitchF + lh * 32 + v * 4]) = yr[v];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (q + 128 < p1) load_step(q + 128);
+      v8bf bh[4], bl[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v4f y0, y1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y0[e] = ys[(e * 4 + g) * kWvPitchF + j * 16 + c];
+          y1[e] = ys[((e + 4) * 4 + g) * kWvPitchF + j * 16 + c];
+        }
+        split8(y0, y1, bh[j], bl[j]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4f x0, x1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x0[e] = xs[(e * 4 + g) * kWvPitchF + i * 16 + c];
+          x1[e] = xs[((e + 4) * 4 + g) * kWvPitchF + i * 16 + c];
+        }
+        v8bf ah, al;
+        split8(x0, x1, ah, al);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_x3(ah, al, bh[j], bl[j], acc[i][j]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();
+    float* mine = red + wid * 64 * RP;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * RP + j * 16 + c] = acc[i][j][r];
+    __syncthreads();
+    float* part = partials + (int64_t)cidx * Cin * Cout;
+#pragma unroll 4
+    for (int m = 0; m < 16; ++m) {
+      const int e = tid + m * 256;
+      const int row = e >> 6, col = e & 63;
+      const float s = red[row * RP + col] + red[64 * RP + row * RP + col] + red[128 * RP + row * RP + col] +
+                      red[192 * RP + row * RP + col];
+      part[(int64_t)(cm0 + row) * Cout + cn0 + col] = s;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------ launchers
+
+template <int BN, int KS, typename Src>
+static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                      const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
+                      int vec_a, int vec_b, hipStream_t stream) {
+  const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
+  gather_gemm_x3_kernel<BN, KS, Src>
+      <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+}
+
+template <int KS, typename Src>
+static void launch_x3_ks(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                         const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
+                         int vec_a, int vec_b, hipStream_t stream) {
+  if (Nd <= 16)
+    launch_x3<16, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else if (Nd <= 32)
+    launch_x3<32, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else
+    launch_x3<64, KS>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+}
+
+// Split-operand gather-GEMM for reductions up to 128 wide; deeper ones use
+// the plain fp32 kernels.
+template <typename Src>
+static int launch_gather_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                            const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
+                            hipStream_t stream) {
+  const int ks = (Kd + 31) / 32;
+  if (ks > 4) return launch_gather<float>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, stream);
+  const int vec_a = (Kd % 4 == 0) && ((uintptr_t)A % 16 == 0);
+  const int vec_b = (Kd % 4 == 0) && ((uintptr_t)Bt % 16 == 0);
+  if (ks == 1)
+    launch_x3_ks<1>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else if (ks == 2)
+    launch_x3_ks<2>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  else
+    launch_x3_ks<4>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+}  // namespace st

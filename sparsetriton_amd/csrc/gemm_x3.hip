@@ -1,0 +1,43 @@
+// Split-operand (3 x bf16 MFMA) fp32 gather-GEMM and weight-gradient launchers.
+#include "gemm_x3.h"
+
+namespace st {
+
+int ops_gather_map_x3(const float* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs,
+                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, int64_t n_dst,
+                      int K, int Kd, int Nd, hipStream_t stream) {
+  MapSrc src{map, ks, rs};
+  return launch_gather_x3(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, stream);
+}
+
+int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
+                       const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const float* Bt,
+                       float* out, int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
+  const int W = (lk->K + 31) / 32;
+  if (coord_dtype == ST_COORD_I16)
+    return launch_gather_x3(A, n_src, make_hash_src<int16_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
+                            nullptr, Bt, out, n_dst, lk->K, Kd, Nd, stream);
+  if (coord_dtype == ST_COORD_I32)
+    return launch_gather_x3(A, n_src, make_hash_src<int32_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
+                            nullptr, Bt, out, n_dst, lk->K, Kd, Nd, stream);
+  return ST_ERR_UNSUPPORTED;
+}
+
+int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
+                       const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
+                       float* partials, void* dW, int dw_dtype, hipStream_t stream) {
+  const bool fits = Cin % 64 == 0 && Cout % 64 == 0 && (uintptr_t)X % 16 == 0 && (uintptr_t)dY % 16 == 0;
+  if (!fits)
+    return ops_wgrad_pairs<float>(X, dY, pairs, kstart, cstart, K, chunk, max_chunks, Cin, Cout, partials, dW,
+                                  dw_dtype, stream);
+  if (max_chunks > 0) {
+    const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
+    const unsigned gz = (unsigned)((Cin / 64) * (Cout / 64));
+    wgrad_pairs_x3_kernel<<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, reinterpret_cast<const int2*>(pairs), kstart,
+                                                                cstart, K, chunk, Cin, Cout, partials);
+    ST_CHECK_LAUNCH();
+  }
+  return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
+}
+
+}  // namespace st

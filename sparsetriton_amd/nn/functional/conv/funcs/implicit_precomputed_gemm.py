@@ -51,7 +51,7 @@ def gather_gemm(A: torch.Tensor, map_t: torch.Tensor, k_stride: int, r_stride: i
     W = (K + 31) // 32
     _lib.call("st_gather_gemm", _lib.ptr(A), A.shape[0], _lib.ptr(map_t), k_stride, r_stride,
               _lib.ptr(masks), W, _lib.ptr(rows), _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd,
-              _lib.feat_code(A.dtype), _lib.stream_of(A.device))
+              _lib.compute_code(A.dtype), _lib.stream_of(A.device))
     return out
 
 
@@ -91,7 +91,7 @@ def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dt
     partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
     dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
     _lib.call("st_wgrad_pairs", _lib.ptr(X), _lib.ptr(dY), _lib.ptr(pl.pairs), _lib.ptr(pl.kstart),
-              _lib.ptr(pl.cstart), K, pl.chunk, pl.max_chunks, C_in, C_out, _lib.feat_code(X.dtype),
+              _lib.ptr(pl.cstart), K, pl.chunk, pl.max_chunks, C_in, C_out, _lib.compute_code(X.dtype),
               _lib.ptr(partials), _lib.ptr(dW), _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
     return dW
 

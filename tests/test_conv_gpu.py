@@ -1,8 +1,10 @@
 """Sparse convolution forward / input gradient / weight gradient on the GPU.
 
 Tolerances (relative Frobenius error vs float64, per output tensor):
-fp32 2e-3, bf16 2e-2, fp16 1e-2 -- the north-star bounds; the fp32 MFMA path
-is IEEE fp32 and lands far inside.  The reference's own test tolerances
+fp32 2e-3, bf16 2e-2, fp16 1e-2 -- the north-star bounds.  fp32 runs in the
+default split-bf16 mode (three bf16 MFMAs per product) unless a test selects
+IEEE fp32; both land far inside, and test_fp32_precision_modes pins each
+mode's own accuracy.  The reference's own test tolerances
 (atol = rtol = 1e-3 forward, 5e-2 gradients, fp16; tests/test_sparse_conv.py)
 are applied on its parametrisations against dense convolution.
 """
@@ -153,6 +155,29 @@ def test_mixed_precision_weight_grad_dtype(device):
 
 
 # ---------------------------------------------- algorithms / determinism
+
+@pytest.mark.parametrize("algo", list(ConvAlgo))
+@pytest.mark.parametrize("precision,bound", [("bf16x3", 1e-4), ("ieee", 2e-5)])
+@pytest.mark.parametrize("cin,cout", [(64, 64), (32, 48), (64, 128)])
+def test_fp32_precision_modes(device, algo, precision, bound, cin, cout):
+    # Split-bf16 products carry <= ~2^-15 relative error (TF32: 2^-11); the sums
+    # of a few hundred products land near 1e-5 relative.  IEEE fp32 lands near 1e-6.
+    from sparsetriton_amd.config import set_fp32_precision
+    set_fp32_precision(precision)
+    rng = np.random.default_rng(cin + cout)
+    c = _rand_coords(rng, 5000, 20)
+    X = rng.standard_normal((5000, cin)).astype(np.float32)
+    W = (rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cin)).astype(np.float32)
+    dY = rng.standard_normal((5000, cout)).astype(np.float32)
+    out, gx, gw = _run(device, c, (20, 20, 20), X, W, dY, 3, 1, 1, 1, False, True, torch.float32, algo)
+    f, dx, dw = _oracle(c, c, (20, 20, 20), X, W, dY, 3, 1, 1, 1, False)
+    errs = (rel(out.F.detach().cpu(), f), rel(gx.cpu(), dx), rel(gw.cpu(), dw))
+    assert max(errs) < bound, errs
+    if precision == "bf16x3":  # the split kernels really ran: IEEE fp32 rounds differently
+        set_fp32_precision("ieee")
+        out2, _, _ = _run(device, c, (20, 20, 20), X, W, dY, 3, 1, 1, 1, False, True, torch.float32, algo)
+        assert not torch.equal(out.F, out2.F)
+
 
 def test_hashfly_equals_precomputed(device):
     # The forward accumulates each row's offsets in the same order in both algorithms, so
