@@ -99,6 +99,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="short run for counter collection: few repetitions, plus a 256 MiB device copy whose "
+                         "HBM counters calibrate the per-kernel traffic figures")
     ap.add_argument("--fp32-precision", choices=["bf16x3", "ieee"], default="bf16x3",
                     help="fp32 matrix-core arithmetic (split-bf16 MFMA, the default, or IEEE fp32 MFMA)")
     args = ap.parse_args()
@@ -153,7 +156,8 @@ def main():
     for _ in range(3):
         build_kmap()
     torch.cuda.synchronize()
-    kmap_t = _events(torch, build_kmap, 20)
+    R = 3 if args.profile else 20
+    kmap_t = _events(torch, build_kmap, R)
     table, kmap = build_kmap()
     table.check()
     P = kmap.num_pairs()
@@ -165,9 +169,9 @@ def main():
         table.insert(coords)
         table.build_occupancy(coords, 4, shape)
 
-    ins_t = _events(torch, t_insert, 20)
-    q_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N), 20)
-    prep_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N, symmetric=True).prepare(), 20) - np.median(q_t)
+    ins_t = _events(torch, t_insert, R)
+    q_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N), R)
+    prep_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N, symmetric=True).prepare(), R) - np.median(q_t)
 
     # --------------------------------------------------------- train step
     X = torch.as_tensor(X_np, device=dev).to(dtype)
@@ -203,9 +207,10 @@ def main():
     # ---------------------------------------------- per-kernel (events) timing
     wt = weight_prep(w.detach(), _lib.W_TRANSPOSE)
     wd = w.detach().contiguous()
-    fwd_t = _events(torch, lambda: gather_gemm_fwd(X, kmap, wt), 30)
-    dgrad_t = _events(torch, lambda: gather_gemm_dgrad(dY, kmap, wd), 30)
-    wgrad_t = _events(torch, lambda: wgrad(X, dY, kmap, w.dtype), 30)
+    KR = 5 if args.profile else 30
+    fwd_t = _events(torch, lambda: gather_gemm_fwd(X, kmap, wt), KR)
+    dgrad_t = _events(torch, lambda: gather_gemm_dgrad(dY, kmap, wd), KR)
+    wgrad_t = _events(torch, lambda: wgrad(X, dY, kmap, w.dtype), KR)
     kern = {"gather_gemm_fwd": float(np.mean(fwd_t)), "gather_gemm_dgrad": float(np.mean(dgrad_t)),
             "wgrad(+reduce)": float(np.mean(wgrad_t))}
     dom = max(kern, key=kern.get)
@@ -236,6 +241,15 @@ def main():
         "plans_ms": float(np.median(prep_t)),
     }
     log(f"kernels (avg ms): {kern}; roofline {dom}: {achieved:.2f} TFLOP/s = {roofline['frac'] * 100:.1f}% of peak")
+
+    if args.profile:
+        # calibration for HBM counters: a plain device copy of 256 MiB (reads and writes 262144 KiB)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if not args.no_cpu:

@@ -222,6 +222,26 @@ int st_kmap_sort_workspace(int64_t n, size_t* bytes);
 int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp, int32_t* rows_tmp,
                       int32_t* perm, void* workspace, size_t workspace_bytes, st_stream_t stream);
 
+/* Destination rows per gather-GEMM tile (the workgroup tile of st_gather_gemm). */
+#define ST_TILE_ROWS 128
+
+/*
+ * Tile plan of a gather-GEMM (no reference counterpart; built once per kernel
+ * map and reused by every layer and by forward and input gradient): for each
+ * tile t of ST_TILE_ROWS destination rows, taken in perm order,
+ *   tile_nk[t]                      number of offsets any row of the tile has,
+ *   tile_klist[t * K + j]           those offsets, ascending (int16),
+ *   tile_map[(t * K + j) * 128 + r] source row of tile row r through offset
+ *                                   tile_klist[t * K + j] (-1 = none, also for
+ *                                   map entries >= n_src).
+ * ntiles = ceil(n_dst / 128); tile_klist holds ntiles * K entries and
+ * tile_map ntiles * K * 128 (only the first tile_nk[t] offsets of a tile are
+ * written).  map / row_masks as in st_gather_gemm (masks optional: all K).
+ */
+int st_tile_plan(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks,
+                 int mask_words, int K, const int32_t* perm, int64_t n_dst, int64_t n_src, int32_t* tile_nk,
+                 int16_t* tile_klist, int32_t* tile_map, st_stream_t stream);
+
 /*
  * Pair list of a kernel map for the weight gradient (replaces the per-tile
  * map walk of precomputed_bwd_weight_kernel, implicit_precomputed_gemm.py:180-230):
@@ -263,6 +283,17 @@ int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mod
 int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
                    const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, void* out,
                    int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
+
+/*
+ * st_gather_gemm over a tile plan (st_tile_plan built with the same perm):
+ * the workgroup reads its tile's offsets and source rows contiguously
+ * instead of gathering map entries and masks row by row.  Same result as
+ * st_gather_gemm with that map.  Reductions wider than 128 (16-bit and
+ * ST_F32_BF16X3) or 64 (ST_F32) return ST_ERR_UNSUPPORTED.
+ */
+int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
+                         const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, void* out, int64_t n_dst,
+                         int K, int Kd, int Nd, int dtype, st_stream_t stream);
 
 /*
  * Weight gradient of ConvPrecomputedNeighborGEMM (precomputed_bwd_weight_kernel,

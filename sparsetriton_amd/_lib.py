@@ -25,6 +25,7 @@ STATUS_OVERFLOW, STATUS_BAD_COORD, STATUS_DUPLICATE = 0, 1, 2
 
 W_TRANSPOSE, W_REVERSE, W_COPY = 0, 1, 2
 MAX_KVOL = 512
+TILE_ROWS = 128
 
 
 class OutGeom(ctypes.Structure):
@@ -83,6 +84,8 @@ _SIGNATURES = {
     "st_kmap_pairs": [_P, _L, _L, _L, _I, _L, _P, _L, _I, _P, _P, _P, _L, _P],
     "st_wgrad_pairs": [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _I, _P],
     "st_weight_prep": [_P, _P, _I, _I, _I, _I, _I, _P],
+    "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],
+    "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
     "st_gather_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _P, _P, _L, _I, _I, _I, _I, _P],
     "st_wgrad": [_P, _L, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P, _L, _P, _I, _P],
     "st_hashfly_gemm": [_P, _L, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _P, _P, _I, _I, _I, _P],

@@ -13,6 +13,9 @@ int ops_gather_map_x3(const float* A, int64_t n_src, const int32_t* map, int64_t
 int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
                        const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const float* Bt,
                        float* out, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
+int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
+                        const int32_t* tmap, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
+                        hipStream_t stream);
 int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
                        const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
                        float* partials, void* dW, int dw_dtype, hipStream_t stream);
@@ -67,6 +70,21 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_map<T>((const T*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
                                       (const T*)Bt, (T*)out, n_dst, K, Kd, Nd, stream));
+}
+
+int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
+                         const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, void* out, int64_t n_dst,
+                         int K, int Kd, int Nd, int dtype, st_stream_t stream) {
+  if (n_src < 0 || n_dst < 0 || K <= 0 || K > ST_MAX_KVOL || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
+  if (n_dst >= (1ll << 31) || n_src >= (1ll << 31)) return ST_ERR_ARG;
+  if (n_dst == 0) return ST_OK;
+  if (!perm || !tile_nk || !tile_klist || !tile_map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
+  if (dtype == ST_F32_BF16X3)
+    return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
+                               (float*)out, n_dst, K, Kd, Nd, stream);
+  ST_DISPATCH_DTYPE(dtype, T,
+                    ops_gather_tiled<T>((const T*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const T*)Bt,
+                                        (T*)out, n_dst, K, Kd, Nd, stream));
 }
 
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,

@@ -169,29 +169,36 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     const int64_t r = row0 + tid;
     drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
   }
-  if (tid < W) tmask_s[tid] = 0;
-  __syncthreads();
-  if (masks) {
-    for (int w = 0; w < W; ++w) {
-      uint32_t v = 0;
-      if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
-      v = wave_or(v);
-      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
-    }
-  } else if (tid < W) {
-    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int nk = 0;
-    for (int w = 0; w < W; ++w) {
-      uint32_t bits = tmask_s[w];
-      while (bits) {
-        klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
-        bits &= bits - 1;
+  if constexpr (Src::kTiled) {
+    // the tile plan lists this tile's active offsets
+    const int nkt = src.nk[blockIdx.x];
+    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[(int64_t)blockIdx.x * src.K + j];
+    if (tid == 0) nk_s = nkt;
+  } else {
+    if (tid < W) tmask_s[tid] = 0;
+    __syncthreads();
+    if (masks) {
+      for (int w = 0; w < W; ++w) {
+        uint32_t v = 0;
+        if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
+        v = wave_or(v);
+        if (lane == 0 && v) atomicOr(&tmask_s[w], v);
       }
+    } else if (tid < W) {
+      tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
     }
-    nk_s = nk;
+    __syncthreads();
+    if (tid == 0) {
+      int nk = 0;
+      for (int w = 0; w < W; ++w) {
+        uint32_t bits = tmask_s[w];
+        while (bits) {
+          klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+          bits &= bits - 1;
+        }
+      }
+      nk_s = nk;
+    }
   }
   __syncthreads();
   const int nk = nk_s;
@@ -204,7 +211,11 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
   auto resolve_group = [&](int g0) {
     const int ng = min(kSrcGroup, nk - g0);
     for (int j = tid >> 7; j < ng; j += 2) {
-      int32_t v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+      int32_t v;
+      if constexpr (Src::kTiled)
+        v = src.get_tile(blockIdx.x, g0 + j, tid & (kGemmBM - 1));
+      else
+        v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
       if ((int64_t)v >= n_src) v = -1;
       src_s[j][tid & (kGemmBM - 1)] = v;
     }
@@ -851,6 +862,8 @@ static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32
     launch_pipe_ks<T, 2>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   } else if (ks <= 4) {
     launch_pipe_ks<T, 4>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+  } else if constexpr (Src::kTiled) {
+    return ST_ERR_UNSUPPORTED;  // deep reductions take the untiled kernels
   } else {
     // Deep reductions: the single-buffered kernel stages Bt in chunks.
     const unsigned gx = st_blocks(n_dst, kGemmBM);
@@ -998,6 +1011,14 @@ int ops_gather_map(const T* A, int64_t n_src, const int32_t* map, int64_t ks, in
   return launch_gather<T>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, stream);
 }
 
+template <typename T>
+int ops_gather_tiled(const T* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
+                     const int32_t* tmap, const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd,
+                     hipStream_t stream) {
+  TiledSrc src{nk, klist, tmap, K};
+  return launch_gather<T>(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, n_dst, K, Kd, Nd, stream);
+}
+
 template <typename CT>
 static HashSrc<CT> make_hash_src(const void* coords, const int32_t* offsets, const st_lookup* lk, const uint64_t* keys,
                                  const uint32_t* vals, int64_t cap) {
@@ -1068,4 +1089,6 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
   X template int ops_wgrad_pairs<T>(const T*, const T*, const int32_t*, const int32_t*, const int32_t*, int, int,    \
                                     int64_t, int, int, float*, void*, int, hipStream_t);                             \
   X template int ops_weight_prep<T>(const T*, T*, int, int, int, int, hipStream_t);                                  \
+  X template int ops_gather_tiled<T>(const T*, int64_t, const int32_t*, const int32_t*, const int16_t*,              \
+                                     const int32_t*, const T*, T*, int64_t, int, int, int, hipStream_t);             \
   }

@@ -74,29 +74,36 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
     const int64_t r = row0 + tid;
     drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
   }
-  if (tid < W) tmask_s[tid] = 0;
-  __syncthreads();
-  if (masks) {
-    for (int w = 0; w < W; ++w) {
-      uint32_t v = 0;
-      if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
-      v = wave_or(v);
-      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
-    }
-  } else if (tid < W) {
-    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int nk = 0;
-    for (int w = 0; w < W; ++w) {
-      uint32_t bits = tmask_s[w];
-      while (bits) {
-        klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
-        bits &= bits - 1;
+  if constexpr (Src::kTiled) {
+    // the tile plan lists this tile's active offsets
+    const int nkt = src.nk[blockIdx.x];
+    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[(int64_t)blockIdx.x * src.K + j];
+    if (tid == 0) nk_s = nkt;
+  } else {
+    if (tid < W) tmask_s[tid] = 0;
+    __syncthreads();
+    if (masks) {
+      for (int w = 0; w < W; ++w) {
+        uint32_t v = 0;
+        if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
+        v = wave_or(v);
+        if (lane == 0 && v) atomicOr(&tmask_s[w], v);
       }
+    } else if (tid < W) {
+      tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
     }
-    nk_s = nk;
+    __syncthreads();
+    if (tid == 0) {
+      int nk = 0;
+      for (int w = 0; w < W; ++w) {
+        uint32_t bits = tmask_s[w];
+        while (bits) {
+          klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+          bits &= bits - 1;
+        }
+      }
+      nk_s = nk;
+    }
   }
   __syncthreads();
   const int nk = nk_s;
@@ -106,7 +113,11 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
   auto resolve_group = [&](int g0) {
     const int ng = min(kSrcGroup, nk - g0);
     for (int j = tid >> 7; j < ng; j += 2) {
-      int32_t v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+      int32_t v;
+      if constexpr (Src::kTiled)
+        v = src.get_tile(blockIdx.x, g0 + j, tid & (kGemmBM - 1));
+      else
+        v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
       if ((int64_t)v >= n_src) v = -1;
       src_s[j][tid & (kGemmBM - 1)] = v;
     }
@@ -379,7 +390,12 @@ static int launch_gather_x3(const float* A, int64_t n_src, const Src& src, const
                             const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
                             hipStream_t stream) {
   const int ks = (Kd + 31) / 32;
-  if (ks > 4) return launch_gather<float>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, stream);
+  if (ks > 4) {
+    if constexpr (Src::kTiled)
+      return ST_ERR_UNSUPPORTED;
+    else
+      return launch_gather<float>(A, n_src, src, masks, W, rows, Bt, out, n_dst, K, Kd, Nd, stream);
+  }
   const int vec_a = (Kd % 4 == 0) && ((uintptr_t)A % 16 == 0);
   const int vec_b = (Kd % 4 == 0) && ((uintptr_t)Bt % 16 == 0);
   if (ks == 1)

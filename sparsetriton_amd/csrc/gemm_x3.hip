@@ -23,6 +23,13 @@ int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int co
   return ST_ERR_UNSUPPORTED;
 }
 
+int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
+                        const int32_t* tmap, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
+                        hipStream_t stream) {
+  TiledSrc src{nk, klist, tmap, K};
+  return launch_gather_x3(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, n_dst, K, Kd, Nd, stream);
+}
+
 int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
                        const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
                        float* partials, void* dW, int dw_dtype, hipStream_t stream) {

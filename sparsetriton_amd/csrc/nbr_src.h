@@ -2,6 +2,10 @@
 // through kernel offset k comes from.
 //
 //   MapSrc  : a precomputed kernel map, map[k * ks + r * rs] (-1 = none).
+//   TiledSrc: a tile plan (st_tile_plan): per 128-row destination tile its
+//             active offsets and, per active offset, the 128 source rows
+//             stored contiguously -- the gather-GEMM's map reads become
+//             coalesced 512-byte loads instead of one cache line per entry.
 //   HashSrc : probe the coordinate table inside the GEMM (implicit hash-fly):
 //             q = (c.xyz * mul + sign * offsets[k]) / div, kept only when the
 //             division is exact and 0 <= q < bounds, then looked up.  Rows whose
@@ -17,6 +21,7 @@
 namespace st {
 
 struct MapSrc {
+  static constexpr bool kTiled = false;
   const int32_t* __restrict__ map;
   int64_t ks, rs;
   typedef int64_t RowCtx;
@@ -24,8 +29,27 @@ struct MapSrc {
   __device__ __forceinline__ int32_t get(const RowCtx& r, int k) const { return map[(int64_t)k * ks + r * rs]; }
 };
 
+// Tile plan of a gather-GEMM (kTileRows destination rows per tile):
+// nk[t] active offsets of tile t, listed in klist[t * K + j] (ascending), and
+// tmap[((int64_t)t * K + j) * kTileRows + r] = source row of the tile's row r
+// through its j-th active offset (-1 = none).
+constexpr int kTileRows = 128;
+struct TiledSrc {
+  static constexpr bool kTiled = true;
+  const int32_t* __restrict__ nk;
+  const int16_t* __restrict__ klist;
+  const int32_t* __restrict__ tmap;
+  int K;
+  typedef int64_t RowCtx;
+  __device__ __forceinline__ RowCtx row(int64_t r) const { return r; }
+  __device__ __forceinline__ int32_t get_tile(int64_t tile, int j, int r) const {
+    return tmap[((int64_t)tile * K + j) * kTileRows + r];
+  }
+};
+
 template <typename CT>
 struct HashSrc {
+  static constexpr bool kTiled = false;
   const CT* __restrict__ coords;
   const int32_t* __restrict__ offsets;
   const uint64_t* __restrict__ keys;

@@ -20,6 +20,7 @@
 //                        running per-digit counters in LDS plus, inside a
 //                        wave, the lanes below with the same digit (9 ballots).
 #include "common.h"
+#include "nbr_src.h"
 
 namespace st {
 
@@ -107,6 +108,63 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint32_t* __re
   }
 }
 
+// Tile plan: one workgroup per 128-row destination tile (rows in perm order).
+// The union of the rows' masks gives the tile's active offsets (ascending);
+// for each of them the 128 source rows are gathered from the map once and
+// stored contiguously.  Source rows >= n_src are stored as -1.
+__global__ __launch_bounds__(256) void tile_plan_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
+                                                        const uint32_t* __restrict__ masks, int W, int K,
+                                                        const int32_t* __restrict__ perm, int64_t n_dst,
+                                                        int64_t n_src, int32_t* __restrict__ tile_nk,
+                                                        int16_t* __restrict__ tile_klist,
+                                                        int32_t* __restrict__ tile_map) {
+  __shared__ int32_t row_s[kTileRows];
+  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ int16_t klist_s[ST_MAX_KVOL];
+  __shared__ int nk_s;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t tile = blockIdx.x;
+  if (tid < kTileRows) {
+    const int64_t r = tile * kTileRows + tid;
+    row_s[tid] = r < n_dst ? perm[r] : -1;
+  }
+  if (tid < W) tmask_s[tid] = 0;
+  __syncthreads();
+  if (masks) {
+    for (int w = 0; w < W; ++w) {
+      uint32_t v = 0;
+      if (tid < kTileRows && row_s[tid] >= 0) v = masks[(int64_t)row_s[tid] * W + w];
+      v = wave_or(v);
+      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+    }
+  } else if (tid < W) {
+    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int nk = 0;
+    for (int w = 0; w < W; ++w) {
+      uint32_t bits = tmask_s[w];
+      while (bits) {
+        klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+        bits &= bits - 1;
+      }
+    }
+    nk_s = nk;
+    tile_nk[tile] = nk;
+  }
+  __syncthreads();
+  const int nk = nk_s;
+  for (int j = tid; j < nk; j += 256) tile_klist[tile * K + j] = klist_s[j];
+  for (int e = tid; e < nk * kTileRows; e += 256) {
+    const int j = e / kTileRows, r = e - j * kTileRows;
+    const int32_t row = row_s[r];
+    int32_t v = row >= 0 ? map[(int64_t)klist_s[j] * ks + (int64_t)row * rs] : -1;
+    if ((int64_t)v >= n_src) v = -1;
+    tile_map[(tile * K + j) * kTileRows + r] = v;
+  }
+}
+
 static int radix_passes(int K) {
   const int bits = K < 32 ? K : 32;
   return (bits + kRadixBits - 1) / kRadixBits;
@@ -143,6 +201,21 @@ extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, i
     st::radix_scatter_kernel<<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], vbuf[in], n, shift, ntiles, hist,
                                                                    p + 1 < passes ? kbuf[out] : nullptr, vbuf[out]);
   }
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+extern "C" int st_tile_plan(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks,
+                            int mask_words, int K, const int32_t* perm, int64_t n_dst, int64_t n_src,
+                            int32_t* tile_nk, int16_t* tile_klist, int32_t* tile_map, st_stream_t stream) {
+  if (K <= 0 || K > ST_MAX_KVOL || n_dst < 0 || n_dst >= (1ll << 31) || n_src < 0) return ST_ERR_ARG;
+  if (row_masks && mask_words != (K + 31) / 32) return ST_ERR_ARG;
+  if (n_dst == 0) return ST_OK;
+  if (!map || !perm || !tile_nk || !tile_klist || !tile_map) return ST_ERR_ARG;
+  const int64_t ntiles = (n_dst + st::kTileRows - 1) / st::kTileRows;
+  st::tile_plan_kernel<<<(unsigned)ntiles, 256, 0, stream>>>(map, map_k_stride, map_r_stride, row_masks,
+                                                             (K + 31) / 32, K, perm, n_dst, n_src, tile_nk,
+                                                             tile_klist, tile_map);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

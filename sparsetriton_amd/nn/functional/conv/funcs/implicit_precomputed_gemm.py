@@ -55,8 +55,26 @@ def gather_gemm(A: torch.Tensor, map_t: torch.Tensor, k_stride: int, r_stride: i
     return out
 
 
+def tiled_ok(dtype: torch.dtype, Kd: int) -> bool:
+    """Whether st_gather_gemm_tiled covers this reduction width (it covers every common one)."""
+    return Kd <= (64 if _lib.compute_code(dtype) == 0 else 128)
+
+
+def gather_gemm_tiled(A: torch.Tensor, tiles, Bt: torch.Tensor, n_dst: int, K: int) -> torch.Tensor:
+    """out[perm[t]] = sum over the tile's offsets of A[source] @ Bt[k]^T, over a tile plan."""
+    Kd = A.shape[1]
+    Nd = Bt.shape[1]
+    out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
+    _lib.call("st_gather_gemm_tiled", _lib.ptr(A), A.shape[0], _lib.ptr(tiles.perm), _lib.ptr(tiles.nk),
+              _lib.ptr(tiles.klist), _lib.ptr(tiles.tmap), _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd,
+              _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+    return out
+
+
 def gather_gemm_fwd(A: torch.Tensor, kmap: KernelMap, Bt: torch.Tensor) -> torch.Tensor:
-    """Forward: out rows in the mask-sorted order of the forward plan."""
+    """Forward: out rows in the mask-sorted order of the forward plan, over its tile plan."""
+    if tiled_ok(A.dtype, A.shape[1]):
+        return gather_gemm_tiled(A, kmap.forward_tiles(), Bt, kmap.n_out, kmap.K)
     plan = kmap.forward_plan()
     return gather_gemm(A, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, Bt, kmap.n_out, kmap.K,
                        rows=plan.perm)
@@ -67,10 +85,13 @@ def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> tor
 
     For a symmetric (odd-kernel submanifold) map the transpose is the map read
     with offsets reversed: dX[i] = sum_j dY[nbr[j, i]] @ W[K-1-j]^T."""
+    if kmap.symmetric:
+        W = weight_prep(W, _lib.W_REVERSE)
+    if tiled_ok(dY.dtype, dY.shape[1]):
+        return gather_gemm_tiled(dY, kmap.backward_tiles(), W, kmap.n_in, kmap.K)
     plan = kmap.backward_plan()
     if kmap.symmetric:
-        wr = weight_prep(W, _lib.W_REVERSE)
-        return gather_gemm(dY, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, wr, kmap.n_in, kmap.K,
+        return gather_gemm(dY, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, W, kmap.n_in, kmap.K,
                            rows=plan.perm)
     return gather_gemm(dY, kmap.invnbr, kmap.n_in, 1, kmap.in_masks, W, kmap.n_in, kmap.K, rows=plan.perm)
 

@@ -115,6 +115,8 @@ class KernelMap:
         self.in_masks = in_masks
         self._fwd = None
         self._bwd = None
+        self._fwd_tiles = None
+        self._bwd_tiles = None
         self._pairs = {}
 
     @classmethod
@@ -164,6 +166,24 @@ class KernelMap:
             self._fwd = TilePlan.build(self.n_out, self.K, self.out_masks)
         return self._fwd
 
+    def forward_tiles(self) -> "TileMap":
+        """Tile plan of the forward gather-GEMM (offsets and source rows per 128-row tile)."""
+        if self._fwd_tiles is None:
+            plan = self.forward_plan()
+            self._fwd_tiles = TileMap.build(self.nbr, self.k_stride, self.r_stride, self.out_masks, self.K,
+                                            plan.perm, self.n_out, self.n_in)
+        return self._fwd_tiles
+
+    def backward_tiles(self) -> "TileMap":
+        """Tile plan of the input-gradient gather-GEMM (the forward's for a symmetric map)."""
+        if self.symmetric:
+            return self.forward_tiles()
+        if self._bwd_tiles is None:
+            plan = self.backward_plan()
+            self._bwd_tiles = TileMap.build(self.invnbr, self.n_in, 1, self.in_masks, self.K, plan.perm, self.n_in,
+                                            self.n_out)
+        return self._bwd_tiles
+
     def backward_plan(self) -> "TilePlan":
         """Mask-sorted order of the input rows over the transposed map (input gradient)."""
         if self.symmetric:
@@ -183,8 +203,8 @@ class KernelMap:
 
     def prepare(self) -> "KernelMap":
         """Build everything forward and backward need (idempotent)."""
-        self.forward_plan()
-        self.backward_plan()
+        self.forward_tiles()
+        self.backward_tiles()
         self.pair_list()
         return self
 
@@ -199,6 +219,25 @@ class KernelMap:
         t = torch.stack([nb[o, k], o, k], dim=1)
         key = (t[:, 0] * (self.n_out + 1) + t[:, 1]) * (self.K + 1) + t[:, 2]
         return t[torch.argsort(key)]
+
+
+class TileMap:
+    """Per-tile offsets and source rows of a gather-GEMM (``st_tile_plan``), in the tile order of
+    a ``TilePlan``: ``nk`` (ntiles), ``klist`` (ntiles, K) int16, ``tmap`` (ntiles, K, 128) int32."""
+
+    def __init__(self, perm, nk, klist, tmap):
+        self.perm, self.nk, self.klist, self.tmap = perm, nk, klist, tmap
+
+    @classmethod
+    def build(cls, map_t, k_stride, r_stride, masks, K, perm, n_dst, n_src) -> "TileMap":
+        dev = map_t.device
+        ntiles = (n_dst + _lib.TILE_ROWS - 1) // _lib.TILE_ROWS
+        nk = torch.empty((max(ntiles, 1),), dtype=torch.int32, device=dev)
+        klist = torch.empty((max(ntiles, 1) * K,), dtype=torch.int16, device=dev)
+        tmap = torch.empty((max(ntiles, 1) * K * _lib.TILE_ROWS,), dtype=torch.int32, device=dev)
+        _lib.call("st_tile_plan", _lib.ptr(map_t), k_stride, r_stride, _lib.ptr(masks), _mask_words(K), K,
+                  _lib.ptr(perm), n_dst, n_src, _lib.ptr(nk), _lib.ptr(klist), _lib.ptr(tmap), _lib.stream_of(dev))
+        return cls(perm, nk, klist, tmap)
 
 
 class TilePlan:

@@ -236,6 +236,21 @@ def test_tile_plan_and_pair_list(device):
         # stability: equal keys keep ascending row order
         same = sorted_keys[1:] == sorted_keys[:-1]
         assert (perm[1:][same] > perm[:-1][same]).all()
+    # tile plan: each 128-row tile (perm order) lists the union of its rows' offsets and,
+    # per listed offset, the map entries of its rows contiguously
+    tiles = kmap.forward_tiles()
+    perm = kmap.forward_plan().perm.cpu().numpy()
+    nk = tiles.nk.cpu().numpy()
+    kl = tiles.klist.cpu().numpy().reshape(-1, K)
+    tm = tiles.tmap.cpu().numpy().reshape(-1, K, 128)
+    ntiles = (N + 127) // 128
+    for t in range(ntiles):
+        rows = perm[t * 128:(t + 1) * 128]
+        active = np.nonzero((nbr[:, rows] >= 0).any(axis=1))[0]
+        assert nk[t] == len(active) and np.array_equal(kl[t, :nk[t]], active)
+        expect = np.full((len(active), 128), -1, dtype=np.int32)
+        expect[:, :len(rows)] = nbr[active][:, rows]
+        assert np.array_equal(tm[t, :nk[t]], expect)
     pl = kmap.pair_list(chunk=100)
     ks = pl.kstart.cpu().numpy()
     cs = pl.cstart.cpu().numpy()
