@@ -20,6 +20,8 @@
 //   are summed in a fixed order by a second kernel.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "mfma.h"
 #include "nbr_src.h"
@@ -304,6 +306,192 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
 #pragma unroll
         for (int j = 0; j < KS; ++j) a_cur[m][j] = a_nxt[m][j];
       any_cur = any_nxt;
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+      if (drow < 0) continue;
+      T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) {
+        const int col = n0 + nb * 16 + c;
+        if (col < Nd) orow[col] = from_f32<T>(acc[m][nb][r]);
+      }
+    }
+}
+
+// ------------------------------------------ gather-GEMM, D-deep load ring
+//
+// As gather_gemm_pipe_kernel, but the A rows and the B tile of an offset are
+// loaded D-1 offsets before they are used, into a ring of D register slots.
+// Vector-memory loads complete in issue order, so the wait for offset i's
+// loads at step i leaves the D-1 younger offsets' gathers in flight; with a
+// single slot of look-ahead every step would wait out a full gather latency.
+// Per step i: issue offset i+D-1's loads, store offset i's B tile into LDS
+// (double-buffered), barrier, MFMAs on offset i.  Requires Kd a multiple of
+// KS * KSTEP and 16-byte aligned A and Bt (every full-vector case).
+template <typename T, int BN, int KS, int D, typename Src>
+__global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
+    const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
+    const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
+    int vec_b) {
+  using F = typename Frag<T>::type;
+  constexpr int VEC = Frag<T>::VEC;
+  constexpr int KSTEP = Frag<T>::KSTEP;
+  constexpr int KDP = KS * KSTEP;
+  constexpr int PITCH = KDP + VEC;
+  constexpr int NBLK = BN / 16;
+  constexpr int CV = KDP / VEC;
+  constexpr int BREGS = (BN * CV + 255) / 256;
+  __shared__ __attribute__((aligned(16))) T bt_s[2][BN * PITCH];
+  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ int32_t drow_s[kGemmBM];
+  __shared__ int16_t klist_s[ST_MAX_KVOL];
+  __shared__ int32_t src_s[kSrcGroup][kGemmBM];
+  __shared__ int nk_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
+  const int n0 = blockIdx.y * BN;
+
+  if (tid < kGemmBM) {
+    const int64_t r = row0 + tid;
+    drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
+  }
+  if constexpr (Src::kTiled) {
+    const int nkt = src.nk[blockIdx.x];
+    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[(int64_t)blockIdx.x * src.K + j];
+    if (tid == 0) nk_s = nkt;
+  } else {
+    if (tid < W) tmask_s[tid] = 0;
+    __syncthreads();
+    if (masks) {
+      for (int w = 0; w < W; ++w) {
+        uint32_t v = 0;
+        if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
+        v = wave_or(v);
+        if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+      }
+    } else if (tid < W) {
+      tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int nk = 0;
+      for (int w = 0; w < W; ++w) {
+        uint32_t bits = tmask_s[w];
+        while (bits) {
+          klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+          bits &= bits - 1;
+        }
+      }
+      nk_s = nk;
+    }
+  }
+  __syncthreads();
+  const int nk = nk_s;
+
+  const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
+  const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
+  auto resolve_group = [&](int g0) {
+    const int ng = min(kSrcGroup, nk - g0);
+    for (int j = tid >> 7; j < ng; j += 2) {
+      int32_t v;
+      if constexpr (Src::kTiled)
+        v = src.get_tile(blockIdx.x, g0 + j, tid & (kGemmBM - 1));
+      else
+        v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+      if ((int64_t)v >= n_src) v = -1;
+      src_s[j][tid & (kGemmBM - 1)] = v;
+    }
+  };
+
+  F a_ring[D][2][KS];
+  F b_ring[D][BREGS];
+  bool any_ring[D];
+  v4f acc[2][NBLK];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // loads of offset i (its sources must be resolved) into ring slot SL
+  auto issue = [&](int i, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    const int j = i % kSrcGroup;
+    const int32_t s0 = src_s[j][wid * 32 + c];
+    const int32_t s1 = src_s[j][wid * 32 + 16 + c];
+    any_ring[SL] = __ballot(s0 >= 0 || s1 >= 0) != 0ull;
+    // Branch-free loads (invalid rows read row 0 and are zeroed): loads under
+    // divergent branches would make the compiler drain the load queue.
+    const F* ar0 = reinterpret_cast<const F*>(A + (int64_t)(s0 >= 0 ? s0 : 0) * Kd + g * VEC);
+    const F* ar1 = reinterpret_cast<const F*>(A + (int64_t)(s1 >= 0 ? s1 : 0) * Kd + g * VEC);
+#pragma unroll
+    for (int jj = 0; jj < KS; ++jj) {
+      a_ring[SL][0][jj] = ar0[jj * (KSTEP / VEC)];
+      a_ring[SL][1][jj] = ar1[jj * (KSTEP / VEC)];
+      if (s0 < 0) a_ring[SL][0][jj] = zero_frag<T>();
+      if (s1 < 0) a_ring[SL][1][jj] = zero_frag<T>();
+    }
+    const int k = klist_s[i];
+#pragma unroll
+    for (int jb = 0; jb < BREGS; ++jb) {
+      const int idx = tid + jb * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      const bool ok = idx < BN * CV && n0 + nr < Nd;
+      b_ring[SL][jb] = *reinterpret_cast<const F*>(Bt + ((int64_t)k * Nd + (ok ? n0 + nr : 0)) * Kd + cv * VEC);
+      if (!ok) b_ring[SL][jb] = zero_frag<T>();
+    }
+  };
+  // Step i of a group of gn offsets starting at g0 (ring slot SL = i % D):
+  // issue offset i + D - 1 (clamped to the group's last offset, so every step
+  // issues the same loads and the compiler's load-queue accounting stays
+  // exact), store offset i's B tile, barrier, MFMAs if offset i exists.
+  auto step = [&](int g0, int gn, int i, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    constexpr int NSL = (SL + D - 1) % D;
+    issue(g0 + min(i + D - 1, gn - 1), std::integral_constant<int, NSL>());
+    const int buf = i & 1;
+#pragma unroll
+    for (int jb = 0; jb < BREGS; ++jb) {
+      const int idx = tid + jb * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      if (idx < BN * CV) *reinterpret_cast<F*>(&bt_s[buf][nr * PITCH + cv * VEC]) = b_ring[SL][jb];
+    }
+    __syncthreads();
+    if (i < gn && any_ring[SL]) {
+      const T* bs = bt_s[buf];
+#pragma unroll
+      for (int jj = 0; jj < KS; ++jj) {
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const F b = *reinterpret_cast<const F*>(&bs[(nb * 16 + c) * PITCH + jj * KSTEP + g * VEC]);
+          acc[0][nb] = mfma(a_ring[SL][0][jj], b, acc[0][nb]);
+          acc[1][nb] = mfma(a_ring[SL][1][jj], b, acc[1][nb]);
+        }
+      }
+    }
+  };
+
+  static_assert(D >= 2 && D <= 4, "ring depth 2..4");  // 2 is the one launched
+  for (int g0 = 0; g0 < nk; g0 += kSrcGroup) {
+    const int gn = min(kSrcGroup, nk - g0);
+    if (g0 > 0) __syncthreads();  // the previous group's sources are all issued
+    resolve_group(g0);
+    __syncthreads();
+    issue(g0, std::integral_constant<int, 0>());
+    if constexpr (D > 2) issue(g0 + min(1, gn - 1), std::integral_constant<int, 1>());
+    if constexpr (D > 3) issue(g0 + min(2, gn - 1), std::integral_constant<int, 2>());
+    for (int i0 = 0; i0 < gn; i0 += D) {
+      step(g0, gn, i0, std::integral_constant<int, 0>());
+      step(g0, gn, i0 + 1, std::integral_constant<int, 1 % D>());
+      if constexpr (D > 2) step(g0, gn, i0 + 2, std::integral_constant<int, 2 % D>());
+      if constexpr (D > 3) step(g0, gn, i0 + 3, std::integral_constant<int, 3 % D>());
     }
   }
 
@@ -823,13 +1011,30 @@ __global__ void weight_prep_kernel(const T* __restrict__ w, T* __restrict__ out,
 //
 // Typed launchers, instantiated once per dtype in gemm_{f32,f16,bf16}.hip.
 
+// Gather-GEMM look-ahead: ST_GEMM_RING=1 selects the one-offset pipelined
+// kernel instead of the two-slot ring kernel (comparison runs only).  Depth 2
+// measured fastest on MI355X (config 2, bf16: 90 us vs 107 us at depth 1,
+// 101 us at 3, 116 us at 4 -- deeper rings cost occupancy).
+static int gemm_ring_depth() {
+  static int d = -1;
+  if (d < 0) {
+    const char* e = getenv("ST_GEMM_RING");
+    d = (e && e[0] == '1') ? 1 : 2;
+  }
+  return d;
+}
+
 template <typename T, int BN, int KS, typename Src>
 static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W, const int32_t* rows,
                         const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  gather_gemm_pipe_kernel<T, BN, KS, Src>
-      <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+  if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)
+    gather_gemm_ring_kernel<T, BN, KS, 2, Src>
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+  else
+    gather_gemm_pipe_kernel<T, BN, KS, Src>
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
 }
 
 template <typename T, int KS, typename Src>

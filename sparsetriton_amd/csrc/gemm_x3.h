@@ -245,6 +245,190 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
     }
 }
 
+// ------------------------------------------------ forward / dgrad, ring
+//
+// gather_gemm_ring_kernel with split operands: offset i's fp32 A rows and B
+// tile are loaded D-1 offsets ahead into a register ring; B is split into
+// hi / lo planes when stored to LDS, A when it is used.  Requires Kd =
+// KS * 32 and 16-byte aligned A and Bt.
+template <int BN, int KS, int D, typename Src>
+__global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
+    const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
+    const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd) {
+  constexpr int KDP = KS * 32;
+  constexpr int PITCH = KDP + 8;
+  constexpr int NBLK = BN / 16;
+  constexpr int CV = KDP / 4;
+  constexpr int BREGS = (BN * CV + 255) / 256;
+  __shared__ __attribute__((aligned(16))) __bf16 bt_s[2][2][BN * PITCH];
+  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ int32_t drow_s[kGemmBM];
+  __shared__ int16_t klist_s[ST_MAX_KVOL];
+  __shared__ int32_t src_s[kSrcGroup][kGemmBM];
+  __shared__ int nk_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
+  const int n0 = blockIdx.y * BN;
+
+  if (tid < kGemmBM) {
+    const int64_t r = row0 + tid;
+    drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
+  }
+  if constexpr (Src::kTiled) {
+    const int nkt = src.nk[blockIdx.x];
+    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[(int64_t)blockIdx.x * src.K + j];
+    if (tid == 0) nk_s = nkt;
+  } else {
+    if (tid < W) tmask_s[tid] = 0;
+    __syncthreads();
+    if (masks) {
+      for (int w = 0; w < W; ++w) {
+        uint32_t v = 0;
+        if (tid < kGemmBM && drow_s[tid] >= 0) v = masks[(int64_t)drow_s[tid] * W + w];
+        v = wave_or(v);
+        if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+      }
+    } else if (tid < W) {
+      tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int nk = 0;
+      for (int w = 0; w < W; ++w) {
+        uint32_t bits = tmask_s[w];
+        while (bits) {
+          klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
+          bits &= bits - 1;
+        }
+      }
+      nk_s = nk;
+    }
+  }
+  __syncthreads();
+  const int nk = nk_s;
+
+  const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
+  const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
+  auto resolve_group = [&](int g0) {
+    const int ng = min(kSrcGroup, nk - g0);
+    for (int j = tid >> 7; j < ng; j += 2) {
+      int32_t v;
+      if constexpr (Src::kTiled)
+        v = src.get_tile(blockIdx.x, g0 + j, tid & (kGemmBM - 1));
+      else
+        v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+      if ((int64_t)v >= n_src) v = -1;
+      src_s[j][tid & (kGemmBM - 1)] = v;
+    }
+  };
+
+  v4f a_ring[D][2][KS][2];
+  v4f b_ring[D][BREGS];
+  bool any_ring[D];
+  v4f acc[2][NBLK];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](int i, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    const int j = i % kSrcGroup;
+    const int32_t s0 = src_s[j][wid * 32 + c];
+    const int32_t s1 = src_s[j][wid * 32 + 16 + c];
+    any_ring[SL] = __ballot(s0 >= 0 || s1 >= 0) != 0ull;
+    const v4f* ar0 = reinterpret_cast<const v4f*>(A + (int64_t)(s0 >= 0 ? s0 : 0) * Kd + g * 8);
+    const v4f* ar1 = reinterpret_cast<const v4f*>(A + (int64_t)(s1 >= 0 ? s1 : 0) * Kd + g * 8);
+#pragma unroll
+    for (int jj = 0; jj < KS; ++jj)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        a_ring[SL][0][jj][h] = ar0[jj * 8 + h];
+        a_ring[SL][1][jj][h] = ar1[jj * 8 + h];
+        if (s0 < 0) a_ring[SL][0][jj][h] = zero_frag<float>();
+        if (s1 < 0) a_ring[SL][1][jj][h] = zero_frag<float>();
+      }
+    const int k = klist_s[i];
+#pragma unroll
+    for (int jb = 0; jb < BREGS; ++jb) {
+      const int idx = tid + jb * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      const bool ok = idx < BN * CV && n0 + nr < Nd;
+      b_ring[SL][jb] = *reinterpret_cast<const v4f*>(Bt + ((int64_t)k * Nd + (ok ? n0 + nr : 0)) * Kd + cv * 4);
+      if (!ok) b_ring[SL][jb] = zero_frag<float>();
+    }
+  };
+  auto step = [&](int g0, int gn, int i, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    constexpr int NSL = (SL + D - 1) % D;
+    issue(g0 + min(i + D - 1, gn - 1), std::integral_constant<int, NSL>());
+    const int buf = i & 1;
+#pragma unroll
+    for (int jb = 0; jb < BREGS; ++jb) {
+      const int idx = tid + jb * 256;
+      const int nr = idx / CV, cv = idx - nr * CV;
+      if (idx < BN * CV) {
+        v4bf hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hi[e] = (__bf16)b_ring[SL][jb][e];
+          lo[e] = (__bf16)(b_ring[SL][jb][e] - (float)hi[e]);
+        }
+        *reinterpret_cast<v4bf*>(&bt_s[buf][0][nr * PITCH + cv * 4]) = hi;
+        *reinterpret_cast<v4bf*>(&bt_s[buf][1][nr * PITCH + cv * 4]) = lo;
+      }
+    }
+    __syncthreads();
+    if (i < gn && any_ring[SL]) {
+#pragma unroll
+      for (int jj = 0; jj < KS; ++jj) {
+        v8bf ah[2], al[2];
+        split8(a_ring[SL][0][jj][0], a_ring[SL][0][jj][1], ah[0], al[0]);
+        split8(a_ring[SL][1][jj][0], a_ring[SL][1][jj][1], ah[1], al[1]);
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int off = (nb * 16 + c) * PITCH + jj * 32 + g * 8;
+          const v8bf bh = *reinterpret_cast<const v8bf*>(&bt_s[buf][0][off]);
+          const v8bf bl = *reinterpret_cast<const v8bf*>(&bt_s[buf][1][off]);
+          acc[0][nb] = mfma_x3(ah[0], al[0], bh, bl, acc[0][nb]);
+          acc[1][nb] = mfma_x3(ah[1], al[1], bh, bl, acc[1][nb]);
+        }
+      }
+    }
+  };
+
+  static_assert(D >= 2 && D <= 3, "ring depth 2..3");
+  for (int g0 = 0; g0 < nk; g0 += kSrcGroup) {
+    const int gn = min(kSrcGroup, nk - g0);
+    if (g0 > 0) __syncthreads();
+    resolve_group(g0);
+    __syncthreads();
+    issue(g0, std::integral_constant<int, 0>());
+    if constexpr (D > 2) issue(g0 + min(1, gn - 1), std::integral_constant<int, 1>());
+    for (int i0 = 0; i0 < gn; i0 += D) {
+      step(g0, gn, i0, std::integral_constant<int, 0>());
+      step(g0, gn, i0 + 1, std::integral_constant<int, 1 % D>());
+      if constexpr (D > 2) step(g0, gn, i0 + 2, std::integral_constant<int, 2 % D>());
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+      if (drow < 0) continue;
+      float* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) {
+        const int col = n0 + nb * 16 + c;
+        if (col < Nd) orow[col] = acc[m][nb][r];
+      }
+    }
+}
+
 // ------------------------------------------------------ weight gradient
 //
 // As wgrad_pairs_wave_kernel with fp32 rows: a wave stages its 32-pair step
@@ -367,8 +551,12 @@ static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint3
                       const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  gather_gemm_x3_kernel<BN, KS, Src>
-      <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+  if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)
+    gather_gemm_ring_x3_kernel<BN, KS, 2, Src>
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd);
+  else
+    gather_gemm_x3_kernel<BN, KS, Src>
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
 }
 
 template <int KS, typename Src>
