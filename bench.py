@@ -56,6 +56,38 @@ def _events(torch, fn, reps):
     return np.array(times)
 
 
+def _events_batch(torch, fn, reps):
+    """Average device time (ms) of fn() over reps back-to-back calls, bracketed by HIP events
+    on the current stream (the stream every kernel here is launched on); the host's launch
+    work overlaps the previous call's kernels, so this is the kernels' time, not the host's."""
+    fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config2_subm64.md")
+
+
+def _measured_traffic(dtype, role):
+    """HBM bytes per launch of a GEMM role, from the committed rocprofv3 counter summary
+    (lines `traffic <dtype> <role> <bytes>`), or None when it has no entry."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            f = line.split()
+            if len(f) == 4 and f[0] == "traffic" and f[1] == dtype and f[2] == role:
+                return float(f[3])
+    except OSError:
+        pass
+    return None
+
+
 def _stats(t):
     return {"median": float(np.median(t)), "p10": float(np.percentile(t, 10)), "p90": float(np.percentile(t, 90))}
 
@@ -208,11 +240,9 @@ def main():
     wt = weight_prep(w.detach(), _lib.W_TRANSPOSE)
     wd = w.detach().contiguous()
     KR = 5 if args.profile else 30
-    fwd_t = _events(torch, lambda: gather_gemm_fwd(X, kmap, wt), KR)
-    dgrad_t = _events(torch, lambda: gather_gemm_dgrad(dY, kmap, wd), KR)
-    wgrad_t = _events(torch, lambda: wgrad(X, dY, kmap, w.dtype), KR)
-    kern = {"gather_gemm_fwd": float(np.mean(fwd_t)), "gather_gemm_dgrad": float(np.mean(dgrad_t)),
-            "wgrad(+reduce)": float(np.mean(wgrad_t))}
+    kern = {"gather_gemm_fwd": _events_batch(torch, lambda: gather_gemm_fwd(X, kmap, wt), KR),
+            "gather_gemm_dgrad": _events_batch(torch, lambda: gather_gemm_dgrad(dY, kmap, wd), KR),
+            "wgrad(+reduce)": _events_batch(torch, lambda: wgrad(X, dY, kmap, w.dtype), KR)}
     dom = max(kern, key=kern.get)
     gemm_flops = 2.0 * P * Cin * Cout
     peak_key = {"f32": "f32_TFLOPs", "bf16": "bf16_TFLOPs"}[args.dtype]
@@ -226,8 +256,10 @@ def main():
     esz = 4 if args.dtype == "f32" else 2
     # compulsory bytes of one gather-GEMM pass: A rows + output rows + weights + 8 B per pair
     gemm_bytes = esz * (N * Cin + N * Cout + 27 * Cin * Cout) + 8 * P
+    dkey = args.dtype if args.dtype != "f32" else f"f32-{args.fp32_precision}"
     roofline = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                "frac": achieved / peak, "traffic": None, "kernel": dom, "peak_note": peak_note,
+                "frac": achieved / peak, "traffic": _measured_traffic(dkey, dom), "traffic_unit": "bytes/launch",
+                "kernel": dom, "peak_note": peak_note,
                 "kernel_avg_ms": kern[dom], "algorithmic_flops_per_launch": gemm_flops,
                 "hbm_bound_ms": gemm_bytes / (PEAK["hbm_GBps"] * 1e9) * 1e3}
     T = table.capacity

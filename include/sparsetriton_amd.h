@@ -256,6 +256,16 @@ int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride
                   int32_t* block_counts, int64_t num_blocks, int chunk, int32_t* kstart, int32_t* cstart,
                   int32_t* pairs, int64_t pair_capacity, st_stream_t stream);
 
+/*
+ * keys[c] (max_chunks u32) = output row of the first pair of chunk c of a pair
+ * list from st_kmap_pairs, all-ones for c >= the chunk count.  Sorting chunk
+ * ids by these keys (st_kmap_sort_rows with K = 32, one key word per row)
+ * gives the chunk order st_wgrad_pairs walks: chunks of every offset that
+ * touch the same output rows -- and hence nearby input rows -- run together.
+ */
+int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
+                             int64_t max_chunks, uint32_t* keys, st_stream_t stream);
+
 /* ------------------------------------------------------------- gather-GEMM */
 
 /*
@@ -317,10 +327,14 @@ int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, in
  * partials[chunk] (max_chunks * C_in * C_out fp32; max_chunks >= P / chunk + K)
  * and each offset's chunks are summed in order.  Deterministic; fp32
  * gathers feed MFMA operands straight from HBM, 16-bit ones go through LDS.
+ * chunk_order (optional, max_chunks int32): the order chunks are taken in
+ * (st_kmap_pairs_chunk_keys); each workgroup takes a contiguous run of it and
+ * the workgroups one XCD runs (launched round-robin over the 8 XCDs) take
+ * adjacent runs, so chunks sharing input and output rows meet in one L2.
  */
 int st_wgrad_pairs(const void* X, const void* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
-                   int K, int chunk, int64_t max_chunks, int C_in, int C_out, int dtype, float* partials, void* dW,
-                   int dw_dtype, st_stream_t stream);
+                   int K, int chunk, int64_t max_chunks, const int32_t* chunk_order, int C_in, int C_out, int dtype,
+                   float* partials, void* dW, int dw_dtype, st_stream_t stream);
 
 /* ----------------------------------------------------- implicit hash-fly */
 

@@ -519,6 +519,18 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 // Workgroups walk chunks with a grid stride; chunk c's C_in x C_out partial
 // goes to partials[c] and the reduce kernel sums each offset's chunks in order.
 
+// A workgroup's share of the (ordered) chunk list: a contiguous run, with the
+// workgroups of one XCD -- the hardware deals workgroups to the 8 XCDs
+// round-robin by id -- taking adjacent runs when the grid is a multiple of 8.
+struct ChunkRange {
+  int q0, q1;
+};
+__device__ __forceinline__ ChunkRange chunk_range(int total) {
+  const int G = gridDim.x;
+  const int L = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  return ChunkRange{(int)((int64_t)L * total / G), (int)((int64_t)(L + 1) * total / G)};
+}
+
 __device__ __forceinline__ int chunk_offset(const int32_t* cstart_s, int K, int c) {
   int lo = 0, hi = K - 1;  // largest k with cstart[k] <= c
   while (lo < hi) {
@@ -538,7 +550,8 @@ template <int MT, int NT>
 __global__ __launch_bounds__(256) void wgrad_pairs_f32_kernel(const float* __restrict__ X, const float* __restrict__ dY,
                                                               const int2* __restrict__ pairs,
                                                               const int32_t* __restrict__ kstart,
-                                                              const int32_t* __restrict__ cstart, int K, int chunk,
+                                                              const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
+    int K, int chunk,
                                                               int Cin, int Cout, float* __restrict__ partials) {
   __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
   __shared__ float red_s[3][MT * NT * 4][64];
@@ -559,7 +572,9 @@ __global__ __launch_bounds__(256) void wgrad_pairs_f32_kernel(const float* __res
   const int wt = wt0 + my_t;
   const int cm0 = (wt / WN) * MT * 16, cn0 = (wt % WN) * NT * 16;
 
-  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+  const ChunkRange cr = chunk_range(total);
+  for (int cq = cr.q0; cq < cr.q1; ++cq) {
+    const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
     const int p1 = min(p0 + chunk, kstart[k + 1]);
@@ -637,7 +652,8 @@ template <typename T, int JB>  // JB: 16x16 output blocks per wave (4 waves x JB
 __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                               const int2* __restrict__ pairs,
                                                               const int32_t* __restrict__ kstart,
-                                                              const int32_t* __restrict__ cstart, int K, int chunk,
+                                                              const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
+    int K, int chunk,
                                                               int Cin, int Cout, float* __restrict__ partials,
                                                               int vec_x, int vec_y) {
   using F = typename Frag<T>::type;
@@ -664,7 +680,9 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
   const int cm0 = mb0 * 16, cn0 = nb0 * 16;
   const int CVX = (MT * 16) / VEC, CVY = (NT * 16) / VEC;
 
-  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+  const ChunkRange cr = chunk_range(total);
+  for (int cq = cr.q0; cq < cr.q1; ++cq) {
+    const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
     const int p1 = min(p0 + chunk, kstart[k + 1]);
@@ -740,7 +758,8 @@ template <typename T>
 __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
                                                                const int32_t* __restrict__ kstart,
-                                                               const int32_t* __restrict__ cstart, int K, int chunk,
+                                                               const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
+    int K, int chunk,
                                                                int Cin, int Cout, float* __restrict__ partials) {
   using F = typename Frag<T>::type;
   static_assert(Frag<T>::KSTEP == 32 && Frag<T>::VEC == 8, "16-bit MFMA fragments");
@@ -764,7 +783,9 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
   // loader lanes: pair lp of the step, channel half lh (32 channels = 4 x 8)
   const int lp = lane >> 1, lh = lane & 1;
 
-  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+  const ChunkRange cr = chunk_range(total);
+  for (int cq = cr.q0; cq < cr.q1; ++cq) {
+    const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
     const int p1 = min(p0 + chunk, kstart[k + 1]);
@@ -1138,18 +1159,27 @@ static int launch_wgrad(const T* X, int64_t n_in, const T* dY, const Src& src, i
   return launch_wgrad_reduce(partials, nullptr, splits, K, Cin, Cout, dW, dw_dtype, stream);
 }
 
+// Weight-gradient grid: up to 1024 workgroups, a multiple of 8 (one run of
+// chunks per workgroup, adjacent runs per XCD; see chunk_range).
+static unsigned wgrad_grid(int64_t max_chunks) {
+  int64_t g = max_chunks < 1024 ? max_chunks : 1024;
+  if (g >= 8) g -= g % 8;
+  return (unsigned)(g > 0 ? g : 1);
+}
+
 template <int MT, int NT>
 static void launch_wgrad_pairs_f32(const float* X, const float* dY, const int2* pairs, const int32_t* kstart,
-                                   const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
-                                   float* partials, hipStream_t stream) {
+                                   const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
+                                   int64_t max_chunks, int Cin, int Cout, float* partials, hipStream_t stream) {
   const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
   const int WT = ((MB + MT - 1) / MT) * ((NB + NT - 1) / NT);
-  const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
+  const unsigned gx = wgrad_grid(max_chunks);
   wgrad_pairs_f32_kernel<MT, NT><<<dim3(gx, 1, (unsigned)((WT + 3) / 4)), 256, 0, stream>>>(
-      X, dY, pairs, kstart, cstart, K, chunk, Cin, Cout, partials);
+      X, dY, pairs, kstart, cstart, chunk_order, K, chunk, Cin, Cout, partials);
 }
 
 static int pow2_tile(int blocks) { return blocks >= 4 ? 4 : (blocks >= 2 ? 2 : 1); }
+
 
 // 16-bit weight-gradient kernel: 0 = per-wave steps (default), 1 = workgroup
 // LDS transpose (ST_WGRAD16=lds selects it, for comparison runs).
@@ -1164,16 +1194,16 @@ static int wgrad16_mode() {
 
 template <typename T>
 int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
-                    int K, int chunk, int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
-                    hipStream_t stream) {
+                    const int32_t* chunk_order, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
+                    float* partials, void* dW, int dw_dtype, hipStream_t stream) {
   if (max_chunks > 0) {
     if constexpr (sizeof(T) == 4) {
       const int mt = pow2_tile((Cin + 15) / 16), nt = pow2_tile((Cout + 15) / 16);
       const int2* pr = reinterpret_cast<const int2*>(pairs);
 #define ST_WP(A, B)                                                                                                 \
   if (mt == A && nt == B)                                                                                           \
-    launch_wgrad_pairs_f32<A, B>((const float*)X, (const float*)dY, pr, kstart, cstart, K, chunk, max_chunks, Cin, \
-                                 Cout, partials, stream);
+    launch_wgrad_pairs_f32<A, B>((const float*)X, (const float*)dY, pr, kstart, cstart, chunk_order, K, chunk,     \
+                                 max_chunks, Cin, Cout, partials, stream);
       ST_WP(1, 1) ST_WP(1, 2) ST_WP(1, 4) ST_WP(2, 1) ST_WP(2, 2) ST_WP(2, 4) ST_WP(4, 1) ST_WP(4, 2) ST_WP(4, 4)
 #undef ST_WP
     } else {
@@ -1181,12 +1211,12 @@ int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t
       const int vec_x = (Cin % VEC == 0) && ((uintptr_t)X % 16 == 0);
       const int vec_y = (Cout % VEC == 0) && ((uintptr_t)dY % 16 == 0);
       const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
-      const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
+      const unsigned gx = wgrad_grid(max_chunks);
       const int2* pr = reinterpret_cast<const int2*>(pairs);
       const int mode = wgrad16_mode();
       if (mode == 0 && Cin % 64 == 0 && Cout % 64 == 0 && vec_x && vec_y) {
         const unsigned gz64 = (unsigned)((Cin / 64) * (Cout / 64));
-        wgrad_pairs_wave_kernel<T><<<dim3(gx, 1, gz64), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+        wgrad_pairs_wave_kernel<T><<<dim3(gx, 1, gz64), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
                                                                           Cout, partials);
         ST_CHECK_LAUNCH();
         return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
@@ -1194,13 +1224,13 @@ int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t
       const unsigned gz = (unsigned)(((MB + 7) / 8) * ((NB + 7) / 8));
       const int nloc = (MB < 8 ? MB : 8) * (NB < 8 ? NB : 8);
       if (nloc <= 4)
-        wgrad_pairs_lds_kernel<T, 1><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+        wgrad_pairs_lds_kernel<T, 1><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
                                                                           Cout, partials, vec_x, vec_y);
       else if (nloc <= 16)
-        wgrad_pairs_lds_kernel<T, 4><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+        wgrad_pairs_lds_kernel<T, 4><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
                                                                           Cout, partials, vec_x, vec_y);
       else
-        wgrad_pairs_lds_kernel<T, 16><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, K, chunk, Cin,
+        wgrad_pairs_lds_kernel<T, 16><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
                                                                            Cout, partials, vec_x, vec_y);
     }
     ST_CHECK_LAUNCH();
@@ -1291,8 +1321,8 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
   X template int ops_wgrad_hash<T>(const T*, int64_t, const T*, const void*, int, int64_t, const int32_t*,           \
                                    const st_lookup*, const uint64_t*, const uint32_t*, int64_t, int, int, float*,    \
                                    int64_t, void*, int, hipStream_t);                                                \
-  X template int ops_wgrad_pairs<T>(const T*, const T*, const int32_t*, const int32_t*, const int32_t*, int, int,    \
-                                    int64_t, int, int, float*, void*, int, hipStream_t);                             \
+  X template int ops_wgrad_pairs<T>(const T*, const T*, const int32_t*, const int32_t*, const int32_t*,              \
+                                    const int32_t*, int, int, int64_t, int, int, float*, void*, int, hipStream_t);   \
   X template int ops_weight_prep<T>(const T*, T*, int, int, int, int, hipStream_t);                                  \
   X template int ops_gather_tiled<T>(const T*, int64_t, const int32_t*, const int32_t*, const int16_t*,              \
                                      const int32_t*, const T*, T*, int64_t, int, int, int, hipStream_t);             \

@@ -434,12 +434,25 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 // As wgrad_pairs_wave_kernel with fp32 rows: a wave stages its 32-pair step
 // (X and dY rows, 64 channels each) in LDS as fp32 and splits the fragments
 // as it reads them.  Requires C_in, C_out multiples of 64, 16-byte aligned.
-constexpr int kWvPitchF = 72;
+//
+// LDS layout: pair p's row of 64 floats is 16 chunks of 16 bytes; chunk ch is
+// stored at position ch ^ swz(p & 7), swz(r) = (r & 1) << 2 | (r >> 1) & 3.
+// The row stores (lanes 0-31 take pairs 0-31, lanes 32-63 the second half of
+// the same rows) then put any 8 consecutive lanes on 8 different bank groups,
+// and the fragment reads (lane group g takes pairs 4e + g) put the two lane
+// groups read together on disjoint bank halves: no bank conflicts either way.
+constexpr int kWvPitchF = 64;
+__device__ __forceinline__ int wv_swz(int r) { return ((r & 1) << 2) | ((r >> 1) & 3); }
+// LDS float index of (pair p, channel col) in the swizzled layout
+__device__ __forceinline__ int wv_at(int p, int col) {
+  return p * kWvPitchF + ((((col >> 2) ^ wv_swz(p & 7)) << 2) | (col & 3));
+}
 __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __restrict__ X,
                                                                 const float* __restrict__ dY,
                                                                 const int2* __restrict__ pairs,
                                                                 const int32_t* __restrict__ kstart,
-                                                                const int32_t* __restrict__ cstart, int K, int chunk,
+                                                                const int32_t* __restrict__ cstart,
+                                                                const int32_t* __restrict__ chunk_order, int K, int chunk,
                                                                 int Cin, int Cout, float* __restrict__ partials) {
   constexpr int STAGE = 32 * kWvPitchF;  // floats per operand per wave
   constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(float);
@@ -458,9 +471,11 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   float* xs = reinterpret_cast<float*>(lds) + wid * 2 * STAGE;
   float* ys = xs + STAGE;
   float* red = reinterpret_cast<float*>(lds);
-  const int lp = lane >> 1, lh = lane & 1;
+  const int lp = lane & 31, lh = lane >> 5;
 
-  for (int cidx = blockIdx.x; cidx < total; cidx += gridDim.x) {
+  const ChunkRange cr = chunk_range(total);
+  for (int cq = cr.q0; cq < cr.q1; ++cq) {
+    const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
     const int p1 = min(p0 + chunk, kstart[k + 1]);
@@ -487,8 +502,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
     for (; q < p1; q += 128) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        *reinterpret_cast<v4f*>(&xs[lp * kWvPitchF + lh * 32 + v * 4]) = xr[v];
-        *reinterpret_cast<v4f*>(&ys[lp * kWvPitchF + lh * 32 + v * 4]) = yr[v];
+        *reinterpret_cast<v4f*>(&xs[wv_at(lp, lh * 32 + v * 4)]) = xr[v];
+        *reinterpret_cast<v4f*>(&ys[wv_at(lp, lh * 32 + v * 4)]) = yr[v];
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -500,8 +515,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
         v4f y0, y1;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          y0[e] = ys[(e * 4 + g) * kWvPitchF + j * 16 + c];
-          y1[e] = ys[((e + 4) * 4 + g) * kWvPitchF + j * 16 + c];
+          y0[e] = ys[wv_at(e * 4 + g, j * 16 + c)];
+          y1[e] = ys[wv_at((e + 4) * 4 + g, j * 16 + c)];
         }
         split8(y0, y1, bh[j], bl[j]);
       }
@@ -510,8 +525,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
         v4f x0, x1;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          x0[e] = xs[(e * 4 + g) * kWvPitchF + i * 16 + c];
-          x1[e] = xs[((e + 4) * 4 + g) * kWvPitchF + i * 16 + c];
+          x0[e] = xs[wv_at(e * 4 + g, i * 16 + c)];
+          x1[e] = xs[wv_at((e + 4) * 4 + g, i * 16 + c)];
         }
         v8bf ah, al;
         split8(x0, x1, ah, al);

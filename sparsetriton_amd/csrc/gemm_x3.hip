@@ -31,17 +31,17 @@ int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, cons
 }
 
 int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
-                       const int32_t* cstart, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
-                       float* partials, void* dW, int dw_dtype, hipStream_t stream) {
+                       const int32_t* cstart, const int32_t* chunk_order, int K, int chunk, int64_t max_chunks,
+                       int Cin, int Cout, float* partials, void* dW, int dw_dtype, hipStream_t stream) {
   const bool fits = Cin % 64 == 0 && Cout % 64 == 0 && (uintptr_t)X % 16 == 0 && (uintptr_t)dY % 16 == 0;
   if (!fits)
-    return ops_wgrad_pairs<float>(X, dY, pairs, kstart, cstart, K, chunk, max_chunks, Cin, Cout, partials, dW,
-                                  dw_dtype, stream);
+    return ops_wgrad_pairs<float>(X, dY, pairs, kstart, cstart, chunk_order, K, chunk, max_chunks, Cin, Cout,
+                                  partials, dW, dw_dtype, stream);
   if (max_chunks > 0) {
-    const unsigned gx = (unsigned)(max_chunks < 1024 ? max_chunks : 1024);
+    const unsigned gx = wgrad_grid(max_chunks);
     const unsigned gz = (unsigned)((Cin / 64) * (Cout / 64));
     wgrad_pairs_x3_kernel<<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, reinterpret_cast<const int2*>(pairs), kstart,
-                                                                cstart, K, chunk, Cin, Cout, partials);
+                                                                cstart, chunk_order, K, chunk, Cin, Cout, partials);
     ST_CHECK_LAUNCH();
   }
   return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);

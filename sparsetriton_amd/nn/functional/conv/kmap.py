@@ -266,9 +266,10 @@ class PairList:
     """(in, out) int32 pairs sorted by (offset, out); ``kstart`` / ``cstart`` (K + 1) the first pair /
     chunk of each offset; ``max_chunks`` bounds the chunk count without reading it back."""
 
-    def __init__(self, pairs, kstart, cstart, chunk, max_chunks):
+    def __init__(self, pairs, kstart, cstart, chunk, max_chunks, corder=None):
         self.pairs, self.kstart, self.cstart = pairs, kstart, cstart
         self.chunk, self.max_chunks = chunk, max_chunks
+        self.corder = corder  # chunk ids sorted by their first output row (weight-gradient order)
 
     @classmethod
     def build(cls, map_t, k_stride, r_stride, n_out, K, n_in, chunk) -> "PairList":
@@ -282,7 +283,12 @@ class PairList:
         pairs = torch.empty((2 * max(cap, 1),), dtype=torch.int32, device=dev)
         _lib.call("st_kmap_pairs", _lib.ptr(map_t), k_stride, r_stride, n_out, K, n_in, _lib.ptr(counts), nb.value,
                   int(chunk), _lib.ptr(kstart), _lib.ptr(cstart), _lib.ptr(pairs), cap, _lib.stream_of(dev))
-        return cls(pairs, kstart, cstart, int(chunk), cap // int(chunk) + K)
+        max_chunks = cap // int(chunk) + K
+        keys = torch.empty((max_chunks, 1), dtype=torch.int32, device=dev)
+        _lib.call("st_kmap_pairs_chunk_keys", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
+                  max_chunks, _lib.ptr(keys), _lib.stream_of(dev))
+        corder = TilePlan.build(max_chunks, 32, keys).perm
+        return cls(pairs, kstart, cstart, int(chunk), max_chunks, corder)
 
 
 # ----------------------------------------------------------------- builders
