@@ -116,6 +116,8 @@ typedef struct st_occupancy {
   int64_t batches;
   int64_t shape[3];
   int64_t scale;         /* table keys are coords * scale: a query off that lattice is absent */
+  const int32_t* prefix; /* optional rank index (st_occupancy_rank): set bits before word w */
+  const int32_t* rowmap; /* optional: row of the voxel of each rank                          */
 } st_occupancy;
 
 /* Number of u64 words of the bitmap of a (batches, sx, sy, sz) box. */
@@ -126,6 +128,20 @@ int st_occupancy_words(int64_t batches, int64_t sx, int64_t sy, int64_t sz, int6
 int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t* words, int64_t batches, int64_t sx,
                        int64_t sy, int64_t sz, st_stream_t stream);
 
+/*
+ * Rank index of a built bitmap (no reference counterpart): the voxels of the
+ * box are ranked in word / bit order; prefix[w] (nw + 1 int32) = set bits in
+ * words[0..w), rowmap[rank] (n int32) = row of that voxel (the lowest row for
+ * duplicate coordinates).  With occ->prefix / occ->rowmap set, st_kmap_query
+ * resolves every in-box neighbour as
+ *   rank = prefix[w] + popcount(words[w] & bits below b);  row = rowmap[rank]
+ * -- reads that follow the spatial order of the bitmap -- instead of probing
+ * the hash table.  occ->words must be built; workspace: (nw + 4095) / 4096 + 1
+ * int32.  Rows outside the box are not indexed (no in-bounds query reaches them).
+ */
+int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_occupancy* occ, int32_t* prefix,
+                      int32_t* rowmap, int32_t* workspace, st_stream_t stream);
+
 /* ------------------------------------------------------------ kernel maps */
 
 /*
@@ -135,7 +151,10 @@ int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t*
  *   nbr[k * nbr_k_stride + o * nbr_r_stride] = row of q in the table if
  *       0 <= q < shape (per axis) and present, else -1.
  * row_masks (n_out, ceil(K/32)) u32, optional: bit k set iff nbr[o, k] >= 0.
- * occ, optional: the occupancy bitmap of the table's coordinates (a filter only).
+ * occ, optional: the occupancy bitmap of the table's coordinates (a filter
+ * only), with its rank index the source of every in-box hit.  keys / vals may
+ * be NULL when occ carries a rank index: queries outside the bitmap's box are
+ * then absent (a submanifold query of in-range coordinates never leaves it).
  * The package stores maps offset-major, (K, n_out) (nbr_k_stride = n_out,
  * nbr_r_stride = 1): every kernel that walks rows then reads and writes each
  * offset's column with coalesced accesses.
@@ -257,14 +276,15 @@ int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride
                   int32_t* pairs, int64_t pair_capacity, st_stream_t stream);
 
 /*
- * keys[c] (max_chunks u32) = output row of the first pair of chunk c of a pair
- * list from st_kmap_pairs, all-ones for c >= the chunk count.  Sorting chunk
- * ids by these keys (st_kmap_sort_rows with K = 32, one key word per row)
- * gives the chunk order st_wgrad_pairs walks: chunks of every offset that
- * touch the same output rows -- and hence nearby input rows -- run together.
+ * keys[c] (max_chunks u32) = row * 512 / n_out for the output row of the first
+ * pair of chunk c of a pair list from st_kmap_pairs (a 9-bit bucket), 511 for
+ * c >= the chunk count.  Stably sorting chunk ids by these keys
+ * (st_kmap_sort_rows with K = 9, one key word per row: one radix pass) gives
+ * the chunk order st_wgrad_pairs walks: chunks of every offset that touch the
+ * same output rows -- and hence nearby input rows -- run together.
  */
 int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
-                             int64_t max_chunks, uint32_t* keys, st_stream_t stream);
+                             int64_t max_chunks, int64_t n_out, uint32_t* keys, st_stream_t stream);
 
 /* ------------------------------------------------------------- gather-GEMM */
 

@@ -55,6 +55,8 @@ class Occupancy(ctypes.Structure):
         ("batches", ctypes.c_int64),
         ("shape", ctypes.c_int64 * 3),
         ("scale", ctypes.c_int64),
+        ("prefix", ctypes.c_void_p),
+        ("rowmap", ctypes.c_void_p),
     ]
 
 
@@ -71,6 +73,7 @@ _SIGNATURES = {
     "st_hash_query": [_P, _I, _L, _P, _P, _L, _P, _P],
     "st_occupancy_words": [_L, _L, _L, _L, ctypes.POINTER(_L)],
     "st_occupancy_build": [_P, _I, _L, _P, _L, _L, _L, _L, _P],
+    "st_occupancy_rank": [_P, _I, _L, ctypes.POINTER(Occupancy), _P, _P, _P, _P],
     "st_kmap_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, ctypes.POINTER(Occupancy), _P, _L, _L, _P,
                       _P],
     "st_outcoords_sizes": [_L, ctypes.POINTER(OutGeom), _L, _L, ctypes.POINTER(_L), ctypes.POINTER(_L)],
@@ -82,7 +85,7 @@ _SIGNATURES = {
     "st_kmap_sort_rows": [_P, _I, _I, _L, _P, _P, _P, _P, ctypes.c_size_t, _P],
     "st_kmap_pairs_sizes": [_L, _I, ctypes.POINTER(_L)],
     "st_kmap_pairs": [_P, _L, _L, _L, _I, _L, _P, _L, _I, _P, _P, _P, _L, _P],
-    "st_kmap_pairs_chunk_keys": [_P, _P, _P, _I, _I, _L, _P, _P],
+    "st_kmap_pairs_chunk_keys": [_P, _P, _P, _I, _I, _L, _L, _P, _P],
     "st_wgrad_pairs": [_P, _P, _P, _P, _P, _I, _I, _L, _P, _I, _I, _I, _P, _P, _I, _P],
     "st_weight_prep": [_P, _P, _I, _I, _I, _I, _I, _P],
     "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],

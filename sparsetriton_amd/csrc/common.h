@@ -80,6 +80,7 @@ __device__ __forceinline__ uint32_t find_slot_from(const uint64_t* __restrict__ 
 
 // Insert-or-find.  Returns the slot of `key` (claimed with a 64-bit CAS if new),
 // or ST_NO_VAL if the table is full.  `was_new` tells whether this call claimed it.
+// A plain load precedes each CAS: probing with CAS alone measured slower.
 __device__ __forceinline__ uint32_t insert_slot(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
                                                 bool& was_new) {
   uint32_t s = home_slot(key, cap);
@@ -111,6 +112,8 @@ __device__ __forceinline__ uint32_t insert_slot(uint64_t* __restrict__ keys, uin
 // Device view of an st_occupancy (words == nullptr: no bitmap, always probe).
 struct Occ {
   const uint64_t* words;
+  const int32_t* prefix;  // rank index (optional)
+  const int32_t* rowmap;
   int nb, sx, sy, sz, bx, by, bz, scale;
 };
 
@@ -118,6 +121,8 @@ __host__ __forceinline__ Occ make_occ(const st_occupancy* o) {
   Occ d{};
   if (!o || !o->words) return d;
   d.words = o->words;
+  d.prefix = o->prefix;
+  d.rowmap = o->rowmap;
   d.nb = (int)o->batches;
   d.sx = (int)o->shape[0];
   d.sy = (int)o->shape[1];

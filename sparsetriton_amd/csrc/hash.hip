@@ -71,6 +71,80 @@ __global__ __launch_bounds__(256) void occupancy_build_kernel(const CT* __restri
            1ull << occ_bit((int)x, (int)y, (int)z));
 }
 
+// Rank index: popcount sums per 4096-word block, then per word the exclusive
+// prefix within its block plus the block's offset.  Words are read and the
+// prefixes written with coalesced accesses (word base + e * 256 + thread); the
+// scan itself runs over 16 consecutive words per thread, staged in LDS with a
+// padded layout (index i + i / 16) so the strided reads are conflict-free.
+constexpr int kRankBlock = 4096;  // 256 threads x 16 words
+__global__ __launch_bounds__(256) void rank_block_sums_kernel(const uint64_t* __restrict__ words, int64_t nw,
+                                                              int32_t* __restrict__ sums) {
+  __shared__ int part_s[4];
+  const int64_t base = (int64_t)blockIdx.x * kRankBlock + threadIdx.x;
+  int c = 0;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t w = base + e * 256;
+    c += w < nw ? __popcll(words[w]) : 0;
+  }
+  c = wave_sum(c);
+  if ((threadIdx.x & 63) == 0) part_s[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) sums[blockIdx.x] = part_s[0] + part_s[1] + part_s[2] + part_s[3];
+}
+
+__global__ __launch_bounds__(256) void rank_prefix_kernel(const uint64_t* __restrict__ words, int64_t nw,
+                                                          const int32_t* __restrict__ sums,
+                                                          int32_t* __restrict__ prefix) {
+  __shared__ int pc_s[kRankBlock + kRankBlock / 16];
+  __shared__ int scratch[5];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kRankBlock;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int i = e * 256 + tid;
+    const int64_t w = base + i;
+    pc_s[i + (i >> 4)] = w < nw ? (int)__popcll(words[w]) : 0;
+  }
+  __syncthreads();
+  int v[16];
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    v[j] = pc_s[tid * 17 + j];
+    c += v[j];
+  }
+  int tot;
+  int run = sums[blockIdx.x] + block_exclusive_scan(c, scratch, &tot);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    pc_s[tid * 17 + j] = run;
+    run += v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int i = e * 256 + tid;
+    const int64_t w = base + i;
+    if (w < nw) prefix[w] = pc_s[i + (i >> 4)];
+  }
+  if (blockIdx.x == gridDim.x - 1 && tid == 0) prefix[nw] = sums[blockIdx.x] + tot;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void rank_rowmap_kernel(const CT* __restrict__ coords, int64_t n, Occ occ,
+                                                          int32_t* __restrict__ rowmap) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int64_t b, x, y, z;
+  load_coord(coords, i, b, x, y, z);
+  if (b < 0 || b >= occ.nb || x < 0 || x >= occ.sx || y < 0 || y >= occ.sy || z < 0 || z >= occ.sz) return;
+  const int64_t w = occ_word(occ, (int)b, (int)x, (int)y, (int)z);
+  const int bit = occ_bit((int)x, (int)y, (int)z);
+  const int rank = occ.prefix[w] + (int)__popcll(occ.words[w] & ((1ull << bit) - 1ull));
+  atomicMin(&rowmap[rank], (int32_t)i);
+}
+
 // Kernel map by query (conv.py:12-75).  One thread per output row walks all K
 // offsets; consecutive threads own consecutive rows, so each offset's column
 // of the offset-major map is written with coalesced stores.  Offsets live in
@@ -122,25 +196,34 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
           state[j] = occ_locate(occ, (int)b, (int)qx, (int)qy, (int)qz, word[j], bit[j]);
       }
     }
-    // round 1: occupancy words
+    // round 1: occupancy words (and, with a rank index, the words' rank prefixes)
     uint64_t w[kQGroup];
-#pragma unroll
-    for (int j = 0; j < kQGroup; ++j) w[j] = state[j] == 1 ? occ.words[word[j]] : 0ull;
-    // round 2: home-slot keys of the remaining candidates
-    uint32_t slot[kQGroup];
-    uint64_t hk[kQGroup];
+    int32_t pre[kQGroup];
+    const bool ranked = occ.rowmap != nullptr;
 #pragma unroll
     for (int j = 0; j < kQGroup; ++j) {
-      const bool probe = state[j] == 2 || (state[j] == 1 && ((w[j] >> bit[j]) & 1ull));
-      slot[j] = probe ? home_slot(key[j], cap) : ST_NO_VAL;
-      hk[j] = probe ? keys[slot[j]] : ST_EMPTY_KEY;
+      w[j] = state[j] == 1 ? occ.words[word[j]] : 0ull;
+      pre[j] = (ranked && state[j] == 1) ? occ.prefix[word[j]] : 0;
     }
-    // finish the rare chains that met another key; round 3: values of the hits
+    // round 2: rows by rank for in-box hits, home-slot keys for what must be probed
+    // (with no table -- keys == nullptr, rank index only -- nothing is probed)
+    uint32_t slot[kQGroup];
+    uint64_t hk[kQGroup];
     int32_t r[kQGroup];
 #pragma unroll
     for (int j = 0; j < kQGroup; ++j) {
+      const bool set = state[j] == 1 && ((w[j] >> bit[j]) & 1ull);
+      const bool by_rank = ranked && set;
+      r[j] = by_rank ? occ.rowmap[pre[j] + (int)__popcll(w[j] & ((1ull << bit[j]) - 1ull))] : -1;
+      const bool probe = keys != nullptr && !by_rank && (state[j] == 2 || set);
+      slot[j] = probe ? home_slot(key[j], cap) : ST_NO_VAL;
+      hk[j] = probe ? keys[slot[j]] : ST_EMPTY_KEY;
+    }
+    // finish the rare chains that met another key; round 3: values of the probed hits
+#pragma unroll
+    for (int j = 0; j < kQGroup; ++j) {
       if (slot[j] != ST_NO_VAL) slot[j] = find_slot_from(keys, cap, key[j], slot[j], hk[j]);
-      r[j] = slot[j] != ST_NO_VAL ? (int32_t)vals[slot[j]] : -1;
+      if (slot[j] != ST_NO_VAL) r[j] = (int32_t)vals[slot[j]];
     }
 #pragma unroll
     for (int j = 0; j < kQGroup; ++j) {
@@ -239,16 +322,40 @@ int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t*
   return ST_OK;
 }
 
+int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_occupancy* occ, int32_t* prefix,
+                      int32_t* rowmap, int32_t* workspace, st_stream_t stream) {
+  if (!occ || !occ->words || !occ_valid(occ) || occ->scale != 1 || n < 0 || n >= (1ll << 31)) return ST_ERR_ARG;
+  if (!prefix || !rowmap || !workspace || (n > 0 && !coords)) return ST_ERR_ARG;
+  int64_t nw = 0;
+  if (st_occupancy_words(occ->batches, occ->shape[0], occ->shape[1], occ->shape[2], &nw) != ST_OK) return ST_ERR_ARG;
+  const int64_t nblk = (nw + kRankBlock - 1) / kRankBlock;
+  rank_block_sums_kernel<<<(unsigned)nblk, 256, 0, stream>>>(occ->words, nw, workspace);
+  if (launch_exclusive_scan(workspace, nblk, stream) != ST_OK) return ST_ERR_HIP;
+  rank_prefix_kernel<<<(unsigned)nblk, 256, 0, stream>>>(occ->words, nw, workspace, prefix);
+  if (n > 0) {
+    unsigned g = st_blocks(n, 256);
+    fill_kernel<uint32_t><<<g < 65536 ? g : 65536, 256, 0, stream>>>((uint32_t*)rowmap, n, 0x7FFFFFFFu);
+    st_occupancy o = *occ;
+    o.prefix = prefix;
+    const Occ d = make_occ(&o);
+    ST_DISPATCH_COORD(coord_dtype, CT,
+                      rank_rowmap_kernel<CT><<<st_blocks(n, 256), 256, 0, stream>>>((const CT*)coords, n, d, rowmap));
+  }
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
                   const uint32_t* vals, int64_t capacity, const st_occupancy* occ, int32_t* nbr,
                   int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, st_stream_t stream) {
-  if (n_out < 0 || K <= 0 || K > ST_MAX_KVOL || stride < 1 || capacity <= 0 || capacity >= (1ll << 31))
-    return ST_ERR_ARG;
+  const bool rank_only = !keys && occ && occ->words && occ->prefix && occ->rowmap;
+  if (n_out < 0 || K <= 0 || K > ST_MAX_KVOL || stride < 1 || capacity >= (1ll << 31)) return ST_ERR_ARG;
+  if (!rank_only && capacity <= 0) return ST_ERR_ARG;
   if (!occ_valid(occ)) return ST_ERR_ARG;
   if (n_out >= (1ll << 31)) return ST_ERR_ARG;
   if (n_out == 0) return ST_OK;
-  if (!out_coords || !offsets || !keys || !vals || !nbr) return ST_ERR_ARG;
+  if (!out_coords || !offsets || !nbr || (!rank_only && (!keys || !vals))) return ST_ERR_ARG;
   ST_DISPATCH_COORD(coord_dtype, CT,
                     kmap_query_kernel<CT><<<st_blocks(n_out, 256), 256, 0, stream>>>(
                         (const CT*)out_coords, n_out, offsets, K, stride, shape_x, shape_y, shape_z, keys, vals,

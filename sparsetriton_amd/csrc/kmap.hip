@@ -528,16 +528,19 @@ extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t m
 }
 
 namespace st {
-// keys[c] = output row of chunk c's first pair (chunks of `chunk` pairs per
-// offset, in (offset, out) pair order), all-ones past the last chunk.
+// keys[c] = 9-bit bucket (row * 512 / n_out) of the output row of chunk c's
+// first pair (chunks of `chunk` pairs per offset, in (offset, out) pair
+// order); 511 past the last chunk, which a stable sort keeps behind the
+// real chunks of that bucket.
 __global__ __launch_bounds__(256) void chunk_keys_kernel(const int32_t* __restrict__ pairs,
                                                          const int32_t* __restrict__ kstart,
                                                          const int32_t* __restrict__ cstart, int K, int chunk,
-                                                         int64_t max_chunks, uint32_t* __restrict__ keys) {
+                                                         int64_t max_chunks, int64_t n_out,
+                                                         uint32_t* __restrict__ keys) {
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= max_chunks) return;
   const int total = cstart[K];
-  uint32_t key = 0xFFFFFFFFu;
+  uint32_t key = 511u;
   if (c < total) {
     int lo = 0, hi = K - 1;  // offset of chunk c: largest k with cstart[k] <= c
     while (lo < hi) {
@@ -546,19 +549,22 @@ __global__ __launch_bounds__(256) void chunk_keys_kernel(const int32_t* __restri
       else hi = mid - 1;
     }
     const int64_t p0 = kstart[lo] + (c - cstart[lo]) * (int64_t)chunk;
-    key = (uint32_t)pairs[2 * p0 + 1];
+    const int64_t row = pairs[2 * p0 + 1];
+    key = (uint32_t)(row * 512 / (n_out > 0 ? n_out : 1));
+    if (key > 511u) key = 511u;
   }
   keys[c] = key;
 }
 }  // namespace st
 
 extern "C" int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K,
-                                        int chunk, int64_t max_chunks, uint32_t* keys, st_stream_t stream) {
+                                        int chunk, int64_t max_chunks, int64_t n_out, uint32_t* keys,
+                                        st_stream_t stream) {
   if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0 || max_chunks >= (1ll << 31)) return ST_ERR_ARG;
   if (max_chunks == 0) return ST_OK;
   if (!pairs || !kstart || !cstart || !keys) return ST_ERR_ARG;
   st::chunk_keys_kernel<<<st_blocks(max_chunks, 256), 256, 0, stream>>>(pairs, kstart, cstart, K, chunk, max_chunks,
-                                                                        keys);
+                                                                        n_out, keys);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

@@ -286,8 +286,8 @@ class PairList:
         max_chunks = cap // int(chunk) + K
         keys = torch.empty((max_chunks, 1), dtype=torch.int32, device=dev)
         _lib.call("st_kmap_pairs_chunk_keys", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
-                  max_chunks, _lib.ptr(keys), _lib.stream_of(dev))
-        corder = TilePlan.build(max_chunks, 32, keys).perm
+                  max_chunks, n_out, _lib.ptr(keys), _lib.stream_of(dev))
+        corder = TilePlan.build(max_chunks, 9, keys).perm
         return cls(pairs, kstart, cstart, int(chunk), max_chunks, corder)
 
 
@@ -318,11 +318,20 @@ def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets:
     nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
     masks = torch.empty((n_out, _mask_words(K)), dtype=torch.int32, device=dev)
     sx, sy, sz = (int(v) for v in spatial_shape)
+    occ = _occupancy_ref(table)
+    # With a rank index of these very coordinates over the query box no hash probe is
+    # needed: a submanifold query stays in the box (its bounds are the query bounds)
+    # and in the batches of the rows it comes from.
+    rank_only = (getattr(table, "has_rank_index", lambda c=None: False)(out_coords) and int(stride) == 1
+                 and tuple(int(v) for v in table.occupancy[1].shape) == (sx, sy, sz))
+    if rank_only:
+        keys = vals = None
+        cap = 0
+    else:
+        keys, vals, cap = _lib.ptr(table.table_keys), _lib.ptr(table.table_values), table.capacity
     _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out,
-              _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, _lib.ptr(table.table_keys),
-              _lib.ptr(table.table_values), table.capacity, _occupancy_ref(table), _lib.ptr(nbr), n_out, 1,
-              _lib.ptr(masks),
-              _lib.stream_of(dev))
+              _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, keys, vals, cap, occ,
+              _lib.ptr(nbr), n_out, 1, _lib.ptr(masks), _lib.stream_of(dev))
     return KernelMap(nbr, n_in, n_out, K, out_masks=masks, symmetric=symmetric)
 
 

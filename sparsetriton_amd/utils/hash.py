@@ -16,6 +16,11 @@ What differs, by design:
   only fails when the table is full; failures are counted in ``status`` and
   ``check()`` raises on them instead of dropping the coordinate.
 * Duplicate coordinates resolve to the lowest row index, on every run.
+* ``insert`` records the rows; the insert kernel runs when the table arrays
+  are first needed (``table_keys`` / ``table_values``, ``query``,
+  ``counters``, moving devices).  A submanifold kernel map over the
+  occupancy bitmap's rank index never needs them, so it never pays for the
+  hash build.
 
 Insert and query run as HIP kernels (``st_hash_insert`` / ``st_hash_query``);
 there is no CPU implementation of them.
@@ -67,28 +72,51 @@ class HashTable:
         assert capacity is not None or (table_keys is not None and table_values is not None), (
             "Either capacity or both table_keys and table_values must be provided."
         )
+        self._pending = None  # (coords, scale) recorded by insert(), applied by _materialize()
+        self._needs_clear = False
+        self.status = None
+        self.occupancy = None  # (words, ctypes st_occupancy, tensors kept alive) once build_occupancy() ran
         if table_keys is not None and table_values is not None:
             assert table_keys.shape == table_values.shape, "table_keys and table_values must have the same shape."
-            self.table_keys, self.table_values = table_keys, table_values
+            self._keys, self._vals = table_keys, table_values
         else:
             capacity = int(capacity)
             assert capacity > 0, "capacity must be positive"
             device = torch.device(device)
-            self.table_keys = torch.empty((capacity,), dtype=torch.int64, device=device)
-            self.table_values = torch.empty((capacity,), dtype=torch.int32, device=device)
+            self._keys = torch.empty((capacity,), dtype=torch.int64, device=device)
+            self._vals = torch.empty((capacity,), dtype=torch.int32, device=device)
             self.clear()
-        self.status = None
-        self.occupancy = None  # (words tensor, ctypes st_occupancy) once build_occupancy() ran
 
     # ------------------------------------------------------------ properties
     @property
+    def table_keys(self) -> torch.Tensor:
+        self._materialize()
+        return self._keys
+
+    @table_keys.setter
+    def table_keys(self, value: torch.Tensor) -> None:
+        self._materialize()
+        self._keys = value
+
+    @property
+    def table_values(self) -> torch.Tensor:
+        self._materialize()
+        return self._vals
+
+    @table_values.setter
+    def table_values(self, value: torch.Tensor) -> None:
+        self._materialize()
+        self._vals = value
+
+    @property
     def device(self) -> torch.device:
-        return self.table_keys.device
+        return self._keys.device
 
     @device.setter
     def device(self, device) -> None:
-        self.table_keys = self.table_keys.to(device, non_blocking=True)
-        self.table_values = self.table_values.to(device, non_blocking=True)
+        self._materialize()
+        self._keys = self._keys.to(device, non_blocking=True)
+        self._vals = self._vals.to(device, non_blocking=True)
         if self.status is not None:
             self.status = self.status.to(device, non_blocking=True)
 
@@ -102,19 +130,39 @@ class HashTable:
 
     @property
     def capacity(self) -> int:
-        return self.table_keys.shape[0]
+        return self._keys.shape[0]
+
+    def has_rank_index(self, coords: torch.Tensor = None) -> bool:
+        """Whether the occupancy bitmap carries a rank index (so queries need no hash probe),
+        and, if ``coords`` is given, was built from that very tensor."""
+        if self.occupancy is None or not self.occupancy[1].rowmap:
+            return False
+        return coords is None or coords is self.occupancy[3]
 
     # ------------------------------------------------------------ operations
     def clear(self) -> "HashTable":
         """Mark every slot empty (keys and values all-ones, i.e. -1)."""
         self.occupancy = None
-        if self.table_keys.is_cuda:
-            _lib.fill_(self.table_keys, -1)
-            _lib.fill_(self.table_values, -1)
+        self._pending = None
+        if self._keys.is_cuda:
+            self._needs_clear = True  # filled when the table is next needed
         else:
-            self.table_keys.fill_(-1)
-            self.table_values.fill_(-1)
+            self._keys.fill_(-1)
+            self._vals.fill_(-1)
         return self
+
+    def _materialize(self) -> None:
+        """Apply the deferred clear and insert."""
+        if self._needs_clear:
+            self._needs_clear = False
+            _lib.fill_(self._keys, -1)
+            _lib.fill_(self._vals, -1)
+        if self._pending is not None:
+            keys, scale = self._pending
+            self._pending = None
+            _lib.call("st_hash_insert", _lib.ptr(keys), _lib.coord_code(keys.dtype), keys.shape[0], int(scale),
+                      _lib.ptr(self._keys), _lib.ptr(self._vals), self.capacity,
+                      _lib.ptr(self._status()), _lib.stream_of(self.device))
 
     def _status(self) -> torch.Tensor:
         if self.status is None or self.status.device != self.device:
@@ -134,15 +182,15 @@ class HashTable:
             "Hash table capacity should be at least twice the number of keys to ensure low collision rate."
         )
         assert keys.ndim == 2 and keys.shape[1] == 4, "keys must have shape (N, 4)"
-        _lib.require_device(self.table_keys, "HashTable")
+        _lib.require_device(self._keys, "HashTable")
         if keys.device != self.device:
             keys = keys.to(self.device)
-        assert self.table_keys.dtype == torch.int64 and self.table_values.dtype == torch.int32, (
+        assert self._keys.dtype == torch.int64 and self._vals.dtype == torch.int32, (
             "HashTable arrays must be int64 keys / int32 values"
         )
-        _lib.call("st_hash_insert", _lib.ptr(keys), _lib.coord_code(keys.dtype), n, int(scale),
-                  _lib.ptr(self.table_keys), _lib.ptr(self.table_values), self.capacity,
-                  _lib.ptr(self._status()), _lib.stream_of(self.device))
+        _lib.coord_code(keys.dtype)  # rejects unsupported coordinate dtypes now
+        self._materialize()  # an earlier pending insert goes first
+        self._pending = (keys, int(scale))
 
     def build_occupancy(self, coords: torch.Tensor, batch_size: int, spatial_shape, scale: int = 1) -> bool:
         """Occupancy bitmap of the inserted ``coords`` over (batch_size, *spatial_shape).
@@ -165,10 +213,22 @@ class HashTable:
             return False
         coords = coords.contiguous()
         words = torch.empty((nw.value,), dtype=torch.int64, device=self.device)
+        stream = _lib.stream_of(self.device)
         _lib.call("st_occupancy_build", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(words),
-                  int(batch_size), sx, sy, sz, _lib.stream_of(self.device))
-        occ = _lib.Occupancy(words.data_ptr(), int(batch_size), (_lib.ctypes.c_int64 * 3)(sx, sy, sz), int(scale))
-        self.occupancy = (words, occ)
+                  int(batch_size), sx, sy, sz, stream)
+        occ = _lib.Occupancy(words.data_ptr(), int(batch_size), (_lib.ctypes.c_int64 * 3)(sx, sy, sz), int(scale),
+                             None, None)
+        keep = [words]
+        if scale == 1:
+            # rank index: in-box neighbours resolve by rank, with no hash probe
+            prefix = torch.empty((nw.value + 1,), dtype=torch.int32, device=self.device)
+            rowmap = torch.empty((n,), dtype=torch.int32, device=self.device)
+            work = torch.empty(((nw.value + 4095) // 4096 + 1,), dtype=torch.int32, device=self.device)
+            _lib.call("st_occupancy_rank", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ctypes.byref(occ),
+                      _lib.ptr(prefix), _lib.ptr(rowmap), _lib.ptr(work), stream)
+            occ.prefix, occ.rowmap = prefix.data_ptr(), rowmap.data_ptr()
+            keep += [prefix, rowmap]
+        self.occupancy = (words, occ, keep, coords)
         return True
 
     def occupancy_ref(self):
@@ -189,6 +249,7 @@ class HashTable:
 
     def counters(self) -> dict:
         """Device failure counters (synchronises): overflow, bad_coord, duplicate."""
+        self._materialize()
         s = self._status().tolist()
         return {"overflow": s[_lib.STATUS_OVERFLOW], "bad_coord": s[_lib.STATUS_BAD_COORD],
                 "duplicate": s[_lib.STATUS_DUPLICATE]}

@@ -140,6 +140,19 @@ def test_occupancy_bitmap_layout(device, shape):
     assert t.build_occupancy(ct, B, shape)
     got = t.occupancy[0].cpu().numpy().view(np.uint64)
     assert np.array_equal(got, _occupancy_np(c, B, shape))
+    # rank index: prefix = exclusive popcount prefix of the words; rowmap[rank] = lowest row
+    # of the rank-th set voxel in word / bit order
+    prefix, rowmap = (x.cpu().numpy() for x in t.occupancy[2][1:3])
+    pcs = np.array([bin(int(v)).count("1") for v in got], dtype=np.int64)
+    assert np.array_equal(prefix, np.concatenate([[0], np.cumsum(pcs)]))
+    BX, BY, BZ = ((s + 3) // 4 for s in shape)
+    inside = (c[:, 0] < B) & (c[:, 1] < shape[0])
+    ci = c[inside].astype(np.int64)
+    rows = np.nonzero(inside)[0]
+    lin = (((ci[:, 0] * BX + ci[:, 1] // 4) * BY + ci[:, 2] // 4) * BZ + ci[:, 3] // 4) * 64 + \
+        (ci[:, 1] % 4) * 16 + (ci[:, 2] % 4) * 4 + ci[:, 3] % 4
+    uniq, first = np.unique(lin, return_index=True)  # sorted = rank order; first = lowest row (rows ascend)
+    assert np.array_equal(rowmap[:len(uniq)], rows[first])
     # rebuilding over other coordinates clears the previous bits
     half = c.shape[0] // 2
     assert t.build_occupancy(ct[:half], B, shape)

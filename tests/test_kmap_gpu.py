@@ -264,6 +264,16 @@ def test_tile_plan_and_pair_list(device):
         assert cs[k + 1] - cs[k] == (o.shape[0] + 99) // 100
     assert np.array_equal(pairs, np.concatenate(expect))
     assert cs[-1] <= pl.max_chunks
+    # chunk order: the real chunks first, stably sorted by the 9-bit bucket of their first output row
+    corder = pl.corder.cpu().numpy()
+    total = int(cs[-1])
+    assert np.array_equal(np.sort(corder), np.arange(pl.max_chunks))
+    bucket = []
+    for cidx in range(total):
+        k = int(np.searchsorted(cs, cidx, side="right") - 1)
+        p0 = ks[k] + (cidx - cs[k]) * 100
+        bucket.append(pairs[p0, 1] * 512 // N)
+    assert np.array_equal(corder[:total], np.argsort(np.array(bucket), kind="stable"))
 
 
 @pytest.mark.parametrize("k,d", [(3, 1), (5, 1), (3, 2)])
