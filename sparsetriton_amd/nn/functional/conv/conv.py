@@ -133,6 +133,8 @@ def sparse_conv3d(
                 out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
                     tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
+            if torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
+                kmap.start_pair_list()  # the weight gradient's pair list, overlapping the forward
         if out_coords.shape[0] == 0:
             return _empty(tensor, C_out, new_shape)
         out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap)

@@ -118,6 +118,7 @@ class KernelMap:
         self._fwd_tiles = None
         self._bwd_tiles = None
         self._pairs = {}
+        self._pairs_ready = {}  # chunk -> event of a pair list being built on the side stream
 
     @classmethod
     def from_neighbor_indices(cls, neighbor_indices: torch.Tensor, n_in: int) -> "KernelMap":
@@ -199,10 +200,34 @@ class KernelMap:
         if pl is None:
             pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)
             self._pairs[chunk] = pl
+        ev = self._pairs_ready.pop(chunk, None)
+        if ev is not None:
+            torch.cuda.current_stream(self.nbr.device).wait_event(ev)
         return pl
 
+    def start_pair_list(self, chunk: int = 2048) -> None:
+        """Begin building the pair list on a side stream, so it overlaps the tile plans and the
+        forward GEMM; ``pair_list()`` makes the calling stream wait for it."""
+        if chunk in self._pairs:
+            return
+        dev = self.nbr.device
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        side.wait_stream(main)
+        self.nbr.record_stream(side)  # read on the side stream
+        with torch.cuda.stream(side):
+            pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)
+            ev = torch.cuda.Event()
+            ev.record(side)
+        for t in (pl.pairs, pl.kstart, pl.cstart, pl.corder):
+            t.record_stream(main)  # the main stream reads them; keep the allocator from recycling early
+        self._pairs[chunk] = pl
+        self._pairs_ready[chunk] = ev
+
     def prepare(self) -> "KernelMap":
-        """Build everything forward and backward need (idempotent)."""
+        """Build everything forward and backward need (idempotent); the pair list is built on a
+        side stream alongside the tile plans."""
+        self.start_pair_list()
         self.forward_tiles()
         self.backward_tiles()
         self.pair_list()
@@ -219,6 +244,19 @@ class KernelMap:
         t = torch.stack([nb[o, k], o, k], dim=1)
         key = (t[:, 0] * (self.n_out + 1) + t[:, 1]) * (self.K + 1) + t[:, 2]
         return t[torch.argsort(key)]
+
+
+_SIDE_STREAMS = {}
+
+
+def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
+    """One extra stream per device (default priority) for map-building work that can overlap."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(key)
+    if s is None:
+        s = torch.cuda.Stream(device=dev)
+        _SIDE_STREAMS[key] = s
+    return s
 
 
 class TileMap:
