@@ -21,6 +21,11 @@ cap, output-major map, output-stationary forward, scatter input gradient,
 per-offset weight gradient; fp32, OpenMP) on the same voxel set.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--dtype f32|bf16] [--no-cpu]
+                       [--fp32-precision bf16x3|ieee] [--profile] [--workload config2|config3|...]
+
+``--workload`` other than config2 measures another BASELINE configuration (strided conv,
+transposed conv, the 1M-voxel submanifold layer with either algorithm): one JSON line with the
+same fields, the step timed the same way, plus the first-call time (map build + forward).
 """
 
 import argparse
@@ -124,6 +129,114 @@ def cpu_baseline(coords, shape, X, W, dY):
     }
 
 
+EXTRA = {
+    # name: (description, C_in, C_out, k, stride, padding, transposed, submanifold, dtype, algorithm)
+    "config3": ("SparseConv3D 64->128 k3 s2 p1 on the config-2 voxel set", 64, 128, 3, 2, 1, False, False, "f32",
+                "precomputed"),
+    "config4": ("SparseConvTransposed3D 128->64 k3 s2 p1 on config 3's output coordinates", 128, 64, 3, 2, 1, True,
+                False, "bf16", "precomputed"),
+    "config5": ("SubMConv3D 128->128 k3, 1M voxels of 2-voxel walls in 256^3 (PrecomputedNeighborGEMM)", 128, 128,
+                3, 1, 1, False, True, "bf16", "precomputed"),
+    "config5-hashfly": ("SubMConv3D 128->128 k3, same set (ImplicitHashFlyGEMM)", 128, 128, 3, 1, 1, False, True,
+                        "bf16", "hashfly"),
+}
+
+
+def run_extra(args):
+    """One JSON line for a BASELINE configuration other than the headline one: the layer's
+    fwd+bwd step (map cached) and its kernel-map build, timed like the headline."""
+    import torch
+
+    from sparsetriton_amd import SparseTensor, workloads
+    from sparsetriton_amd.config import ConvAlgo, set_conv_algo, set_fp32_precision
+    from sparsetriton_amd.nn.functional import sparse_conv3d
+
+    desc, Cin, Cout, k, s, p, tr, subm, dts, algo = EXTRA[args.workload]
+    set_fp32_precision(args.fp32_precision)
+    set_conv_algo(ConvAlgo.ImplicitHashFlyGEMM if algo == "hashfly" else ConvAlgo.PrecomputedNeighborGEMM)
+    dev = torch.device("cuda:0")
+    dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[dts]
+    seed = 0
+    if args.workload.startswith("config5"):
+        coords_np, shape = workloads.config5(seed=seed)
+        batch = 1
+    else:
+        coords_np, shape = workloads.config2(seed=seed)
+        batch = 4
+    coords = torch.as_tensor(coords_np, device=dev).to(torch.int16)
+    if args.workload == "config4":
+        # input = the output coordinates of config 3's strided convolution
+        from sparsetriton_amd.nn.functional.conv.kmap import build_out_coords
+        coords, shape, _ = build_out_coords(coords, shape, 3, stride=2, padding=1, submanifold=False)
+        shape = tuple(int(v) for v in shape)
+    N = coords.shape[0]
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    X = torch.randn(N, Cin, generator=g).to(dev, dtype)
+    bound = 1.0 / np.sqrt(Cin * k ** 3)
+    W = ((torch.rand(k ** 3, Cin, Cout, generator=g) * 2 - 1) * bound).to(dev, dtype).requires_grad_(True)
+
+    def fresh():
+        feats = X.clone().requires_grad_(True)
+        return feats, SparseTensor(feats, coords, spatial_shape=shape, batch_size=batch)
+
+    def build():
+        # a new coordinate set: table, kernel map (or hash-fly lookups) and all plans
+        feats, sp = fresh()
+        out = sparse_conv3d(sp, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)
+        return sp, out
+
+    # map build = first call's extra time over a cached call, both fwd only
+    sp, out = build()
+    torch.cuda.synchronize()
+    n_out = out.F.shape[0]
+    if algo == "hashfly":
+        P = None
+    else:
+        km = next(iter(sp._cache.neighbor_indices.values()))[1]
+        km.prepare()
+        P = km.num_pairs()
+    dY = torch.randn(n_out, Cout, generator=g).to(dev, dtype)
+    R = 3 if args.profile else 10
+    build_t = _events(torch, build, R)
+
+    feats = sp.F
+
+    def step():
+        feats.grad = None
+        W.grad = None
+        o = sparse_conv3d(sp, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)
+        o.F.backward(dY)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    if P is None:  # hash-fly: count pairs from an exact map of the same geometry
+        set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)
+        _, sp2 = fresh()
+        sparse_conv3d(sp2, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)
+        P = next(iter(sp2._cache.neighbor_indices.values()))[1].num_pairs()
+    value = 6.0 * P * Cin * Cout / (ms * 1e-3) / 1e12
+    log(f"{args.workload}: N_in={N} N_out={n_out} P={P}; step {ms:.3f} ms -> {value:.2f} TFLOP/s; "
+        f"first-call (map build + fwd) median {np.median(build_t):.3f} ms")
+    line = {
+        "metric": METRIC, "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dts, "fp32_precision": args.fp32_precision if dts == "f32" else None,
+        "data": "synthetic (seeded voxel set, N(0,1) features)",
+        "config": {"workload": f"{args.workload}: {desc}", "voxels_in": N, "voxels_out": n_out, "pairs": P,
+                   "C_in": Cin, "C_out": Cout, "seed": seed, "algorithm": algo},
+        "first_call_build_plus_fwd_ms": _stats(build_t),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,9 +247,16 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="short run for counter collection: few repetitions, plus a 256 MiB device copy whose "
                          "HBM counters calibrate the per-kernel traffic figures")
+    ap.add_argument("--workload", choices=["config2"] + sorted(EXTRA), default="config2",
+                    help="config2 is the headline; the others measure BASELINE's other configurations")
     ap.add_argument("--fp32-precision", choices=["bf16x3", "ieee"], default="bf16x3",
                     help="fp32 matrix-core arithmetic (split-bf16 MFMA, the default, or IEEE fp32 MFMA)")
     args = ap.parse_args()
+    if args.workload != "config2":
+        if args.gpus != 1:
+            print("bench.py: one GPU only", file=sys.stderr)
+            sys.exit(2)
+        return run_extra(args)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
               "the sparse-convolution path is not sharded across GPUs here", file=sys.stderr)
