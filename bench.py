@@ -372,26 +372,38 @@ def main():
     dom = max(kern, key=kern.get)
     gemm_flops = 2.0 * P * Cin * Cout
     peak_key = {"f32": "f32_TFLOPs", "bf16": "bf16_TFLOPs"}[args.dtype]
-    peak = PEAK[peak_key]
-    peak_note = f"dense {args.dtype} MFMA peak"
+    mfma_peak = PEAK[peak_key]
+    mfma_note = f"dense {args.dtype} MFMA peak"
     if args.dtype == "f32" and args.fp32_precision == "bf16x3":
         # every fp32 product is three bf16 MFMA products: the ceiling is a third of the bf16 peak
-        peak = PEAK["bf16_TFLOPs"] / 3.0
-        peak_note = "dense bf16 MFMA peak / 3 (three bf16 products per fp32 product)"
-    achieved = gemm_flops / (kern[dom] * 1e-3) / 1e12
+        mfma_peak = PEAK["bf16_TFLOPs"] / 3.0
+        mfma_note = "dense bf16 MFMA peak / 3 (three bf16 products per fp32 product)"
+    tflops = gemm_flops / (kern[dom] * 1e-3) / 1e12
     esz = 4 if args.dtype == "f32" else 2
-    # compulsory bytes of one gather-GEMM pass: A rows + output rows + weights + 8 B per pair
+    # algorithmic bytes of one pass (any of the three kernels): the two feature arrays
+    # (A rows read, output rows written / X and dY read), the weights (dW: fp32 partial-free
+    # result), and one (input, output) int32 index pair per map pair
     gemm_bytes = esz * (N * Cin + N * Cout + 27 * Cin * Cout) + 8 * P
+    intensity = gemm_flops / gemm_bytes
+    ridge = mfma_peak * 1e12 / (PEAK["hbm_GBps"] * 1e9)
     dkey = args.dtype if args.dtype != "f32" else f"f32-{args.fp32_precision}"
-    roofline = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                "frac": achieved / peak, "traffic": _measured_traffic(dkey, dom), "traffic_unit": "bytes/launch",
-                "kernel": dom, "peak_note": peak_note,
-                "kernel_avg_ms": kern[dom], "algorithmic_flops_per_launch": gemm_flops,
-                "hbm_bound_ms": gemm_bytes / (PEAK["hbm_GBps"] * 1e9) * 1e3}
+    common = {"traffic": _measured_traffic(dkey, dom), "traffic_unit": "bytes/launch", "kernel": dom,
+              "kernel_avg_ms": kern[dom], "algorithmic_bytes_per_launch": gemm_bytes,
+              "algorithmic_flops_per_launch": gemm_flops, "flops_per_byte": intensity,
+              "ridge_flops_per_byte": ridge, "mfma_TFLOPs": tflops, "mfma_peak_TFLOPs": mfma_peak,
+              "mfma_frac": tflops / mfma_peak, "mfma_peak_note": mfma_note}
+    if intensity < ridge:  # below the ridge point: HBM is the bounding roof
+        gbps = gemm_bytes / (kern[dom] * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": gbps, "peak": PEAK["hbm_GBps"], "unit": "GB/s",
+                    "frac": gbps / PEAK["hbm_GBps"], **common}
+    else:
+        roofline = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",
+                    "frac": tflops / mfma_peak, **common}
     T = table.capacity
-    ins_bytes = 16 * N + 12 * T + 12 * N  # coords read + table clear + one slot written per insert
-    # query: coords read + one slot (8 B key + 4 B value) per in-bound query + the (K, N) map write
-    q_bytes = 16 * N + 12 * 27 * N + 4 * 27 * N
+    ins_bytes = 8 * N + 12 * T + 12 * N  # int16 coords read + table clear + one slot written per insert
+    # query through the rank index: int16 coords read, the (K, N) map and (N, 1) row masks written,
+    # and per found neighbour its rank prefix and row id read
+    q_bytes = 8 * N + 4 * 27 * N + 4 * N + 8 * P
     kmap_info = {
         "kmap_build_ms": _stats(kmap_t),
         "hash_insert_ms": float(np.median(ins_t)), "hash_insert_GBps": ins_bytes / (np.median(ins_t) * 1e-3) / 1e9,
@@ -399,7 +411,8 @@ def main():
         "kmap_query_ms": float(np.median(q_t)), "kmap_query_GBps": q_bytes / (np.median(q_t) * 1e-3) / 1e9,
         "plans_ms": float(np.median(prep_t)),
     }
-    log(f"kernels (avg ms): {kern}; roofline {dom}: {achieved:.2f} TFLOP/s = {roofline['frac'] * 100:.1f}% of peak")
+    log(f"kernels (avg ms): {kern}; roofline {dom}: {roofline['achieved']:.1f} {roofline['unit']} = "
+        f"{roofline['frac'] * 100:.1f}% of the {roofline['bound']} peak; MFMA {tflops:.1f} TFLOP/s")
 
     if args.profile:
         # calibration for HBM counters: a plain device copy of 256 MiB (reads and writes 262144 KiB)

@@ -233,8 +233,10 @@ int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_strid
  * Destination-row order for the gather-GEMM (no reference counterpart; the
  * reference tiles rows in storage order).  Rows are stably radix-sorted by
  * their offset bitmask (masks (n, mask_words), folded to 32 bits when
- * K > 32) so that 16/32-row MFMA slabs share their offsets.  perm (n) gets
- * the sorted row ids.  keys_tmp holds 2n u32, rows_tmp n int32, workspace
+ * K > 32) so that 128-row gather-GEMM tiles share their offsets.  For
+ * K = 27 (3x3x3, x-major offsets) the key's bits are the mask's bits ordered
+ * by how many axes the offset leaves the centre on (centre lowest, corners
+ * highest), then by index.  perm (n) gets the sorted row ids.  keys_tmp holds 2n u32, rows_tmp n int32, workspace
  * st_kmap_sort_workspace(n) bytes.
  */
 int st_kmap_sort_workspace(int64_t n, size_t* bytes);

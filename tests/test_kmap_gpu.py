@@ -230,9 +230,8 @@ def test_tile_plan_and_pair_list(device):
             masks = kmap.in_masks
         perm = plan.perm.cpu().numpy()
         assert np.array_equal(np.sort(perm), np.arange(N))
-        mk = masks.cpu().numpy()[:, 0].astype(np.uint32)
-        sorted_keys = mk[perm]
-        assert (np.diff(sorted_keys.astype(np.int64)) >= 0).all()  # stable radix order by mask
+        sorted_keys = _fold_keys(masks.cpu().numpy().view(np.uint32), K)[perm]
+        assert (np.diff(sorted_keys.astype(np.int64)) >= 0).all()  # stable radix order by mask key
         # stability: equal keys keep ascending row order
         same = sorted_keys[1:] == sorted_keys[:-1]
         assert (perm[1:][same] > perm[:-1][same]).all()
@@ -303,13 +302,24 @@ def test_subm_map_is_its_own_transpose(device, k, d):
         assert (torch.linalg.norm(a - b) / torch.linalg.norm(b)).item() < tol
 
 
-def _fold_keys(masks):
-    """32-bit sort key of a (n, W) mask array: word w rotated left by 7w, xor-folded."""
+def _fold_keys(masks, K):
+    """32-bit sort key of a (n, W) mask array: word w rotated left by 7w, xor-folded; for K = 27
+    the bits then reordered: offsets ranked by the number of axes (0..3) on which
+    (k // 9, k // 3 % 3, k % 3) differs from the centre (1, 1, 1), ties by index."""
     m = masks.astype(np.uint64)
     key = m[:, 0].copy()
     for w in range(1, m.shape[1]):
         r = (7 * w) & 31
         key ^= ((m[:, w] << np.uint64(r)) | (m[:, w] >> np.uint64(32 - r))) & np.uint64(0xFFFFFFFF) if r else m[:, w]
+    if K == 27:
+        axes = [sum(int(v != 1) for v in (k // 9, k // 3 % 3, k % 3)) for k in range(27)]
+        rank = sorted(range(27), key=lambda k: (axes[k], k))
+        pos = {k: p for p, k in enumerate(rank)}
+        assert [pos[k] for k in (13, 4, 0, 26)] == [0, 1, 19, 26]  # centre, first face, first/last corner
+        out = np.zeros_like(key)
+        for k in range(27):
+            out |= ((key >> np.uint64(k)) & np.uint64(1)) << np.uint64(pos[k])
+        key = out
     return key.astype(np.uint32)
 
 
@@ -331,7 +341,7 @@ def test_sort_rows_stable(device, n, K):
         masks[:, -1] &= np.uint32((1 << (K % 32)) - 1)
     m_t = torch.from_numpy(masks.view(np.int32).copy()).to(device)
     perm = TilePlan.build(n, K, m_t).perm.cpu().numpy()
-    expect = np.argsort(_fold_keys(masks), kind="stable")
+    expect = np.argsort(_fold_keys(masks, K), kind="stable")
     assert np.array_equal(perm, expect)
 
 
