@@ -780,8 +780,12 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
   T* xs = reinterpret_cast<T*>(lds) + wid * 2 * STAGE;
   T* ys = xs + STAGE;
   float* red = reinterpret_cast<float*>(lds);
-  // loader lanes: pair lp of the step, channel half lh (32 channels = 4 x 8)
-  const int lp = lane >> 1, lh = lane & 1;
+  // loader lanes: a step's 32 rows of 64 elements (128 bytes, one cache line)
+  // are read as 4 instructions of 8 whole rows -- 8 consecutive lanes take one
+  // row's 8 chunks of 16 bytes -- so no instruction splits a line with another.
+  // Each lane keeps pair (lane mod 32) and takes instruction v's row index
+  // from lane 8v + lane / 8.
+  const int lr = lane >> 3, lc = lane & 7;
 
   const ChunkRange cr = chunk_range(total);
   for (int cq = cr.q0; cq < cr.q1; ++cq) {
@@ -796,15 +800,14 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
       for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
     F xr[4], yr[4];
     auto load_step = [&](int q) {
-      const int p = q + lp;
+      const int p = q + (lane & 31);
       int2 pr = make_int2(-1, -1);
       if (p < p1) pr = pairs[p];
-      const F* xrow = reinterpret_cast<const F*>(X + (int64_t)(pr.x >= 0 ? pr.x : 0) * Cin + cm0 + lh * 32);
-      const F* yrow = reinterpret_cast<const F*>(dY + (int64_t)(pr.y >= 0 ? pr.y : 0) * Cout + cn0 + lh * 32);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        xr[v] = pr.x >= 0 ? xrow[v] : zero_frag<T>();
-        yr[v] = pr.y >= 0 ? yrow[v] : zero_frag<T>();
+        const int ix = __shfl(pr.x, v * 8 + lr, 64), iy = __shfl(pr.y, v * 8 + lr, 64);
+        xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lc * 8) : zero_frag<T>();
+        yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lc * 8) : zero_frag<T>();
       }
     };
     int q = p0 + wid * 32;
@@ -812,8 +815,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
     for (; q < p1; q += 128) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        *reinterpret_cast<F*>(&xs[lp * kWvPitch + lh * 32 + v * 8]) = xr[v];
-        *reinterpret_cast<F*>(&ys[lp * kWvPitch + lh * 32 + v * 8]) = yr[v];
+        *reinterpret_cast<F*>(&xs[(v * 8 + lr) * kWvPitch + lc * 8]) = xr[v];
+        *reinterpret_cast<F*>(&ys[(v * 8 + lr) * kWvPitch + lc * 8]) = yr[v];
       }
       // LDS operations of one wave complete in order: the reads below see the
       // stores above; the fence keeps the compiler from moving them across.

@@ -435,12 +435,19 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 // (X and dY rows, 64 channels each) in LDS as fp32 and splits the fragments
 // as it reads them.  Requires C_in, C_out multiples of 64, 16-byte aligned.
 //
+// Row loads: a step's 32 rows of 64 floats (256 bytes, two cache lines) are
+// read as 8 instructions of 4 whole rows each -- 16 consecutive lanes take one
+// row's 16 chunks of 16 bytes -- so every load instruction touches 8 cache
+// lines and uses all of each.  (Lane-per-row loads touch 64 lines for 16
+// bytes each and re-reference every line 8 times, which the 32 KB L1 cannot
+// hold across 8 resident waves.)  Each lane keeps its own pair index (lane
+// mod 32) and takes the row index of instruction v from lane 4v + lane / 16.
+//
 // LDS layout: pair p's row of 64 floats is 16 chunks of 16 bytes; chunk ch is
-// stored at position ch ^ swz(p & 7), swz(r) = (r & 1) << 2 | (r >> 1) & 3.
-// The row stores (lanes 0-31 take pairs 0-31, lanes 32-63 the second half of
-// the same rows) then put any 8 consecutive lanes on 8 different bank groups,
-// and the fragment reads (lane group g takes pairs 4e + g) put the two lane
-// groups read together on disjoint bank halves: no bank conflicts either way.
+// stored at position ch ^ swz(p & 7), swz(r) = (r & 1) << 2 | (r >> 1) & 3: a
+// row store is one contiguous 256-byte span, and the fragment reads (lane
+// group g takes pairs 4e + g) put the two lane groups read together on
+// disjoint bank halves.
 constexpr int kWvPitchF = 64;
 __device__ __forceinline__ int wv_swz(int r) { return ((r & 1) << 2) | ((r >> 1) & 3); }
 // LDS float index of (pair p, channel col) in the swizzled layout
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   float* xs = reinterpret_cast<float*>(lds) + wid * 2 * STAGE;
   float* ys = xs + STAGE;
   float* red = reinterpret_cast<float*>(lds);
-  const int lp = lane & 31, lh = lane >> 5;
+  const int lr = lane >> 4, lc = lane & 15;  // loader lanes: row lr of each 4-row group, 16-byte chunk lc
 
   const ChunkRange cr = chunk_range(total);
   for (int cq = cr.q0; cq < cr.q1; ++cq) {
@@ -486,15 +493,14 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
       for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
     v4f xr[8], yr[8];
     auto load_step = [&](int q) {
-      const int p = q + lp;
+      const int p = q + (lane & 31);
       int2 pr = make_int2(-1, -1);
       if (p < p1) pr = pairs[p];
-      const v4f* xrow = reinterpret_cast<const v4f*>(X + (int64_t)(pr.x >= 0 ? pr.x : 0) * Cin + cm0 + lh * 32);
-      const v4f* yrow = reinterpret_cast<const v4f*>(dY + (int64_t)(pr.y >= 0 ? pr.y : 0) * Cout + cn0 + lh * 32);
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        xr[v] = pr.x >= 0 ? xrow[v] : zero_frag<float>();
-        yr[v] = pr.y >= 0 ? yrow[v] : zero_frag<float>();
+        const int ix = __shfl(pr.x, v * 4 + lr, 64), iy = __shfl(pr.y, v * 4 + lr, 64);
+        xr[v] = ix >= 0 ? *reinterpret_cast<const v4f*>(X + (int64_t)ix * Cin + cm0 + lc * 4) : zero_frag<float>();
+        yr[v] = iy >= 0 ? *reinterpret_cast<const v4f*>(dY + (int64_t)iy * Cout + cn0 + lc * 4) : zero_frag<float>();
       }
     };
     int q = p0 + wid * 32;
@@ -502,8 +508,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
     for (; q < p1; q += 128) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        *reinterpret_cast<v4f*>(&xs[wv_at(lp, lh * 32 + v * 4)]) = xr[v];
-        *reinterpret_cast<v4f*>(&ys[wv_at(lp, lh * 32 + v * 4)]) = yr[v];
+        *reinterpret_cast<v4f*>(&xs[wv_at(v * 4 + lr, lc * 4)]) = xr[v];
+        *reinterpret_cast<v4f*>(&ys[wv_at(v * 4 + lr, lc * 4)]) = yr[v];
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
