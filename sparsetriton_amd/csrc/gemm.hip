@@ -44,6 +44,24 @@ using namespace st;
       return ST_ERR_UNSUPPORTED;      \
   }
 
+namespace st {
+// out[0 .. n) (16-bit units) = 0.
+__global__ __launch_bounds__(256) void zero_u16_kernel(uint16_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+}  // namespace st
+
+// A gather-GEMM with no source rows writes zero rows.  The kernels read a
+// clamped row 0 for every missing source, so they are not launched then (an
+// empty A may have no storage at all).
+static int zero_output(void* out, int64_t n_dst, int Nd, int dtype, hipStream_t stream) {
+  const int64_t n = n_dst * Nd * ((dtype == ST_F16 || dtype == ST_BF16) ? 1 : 2);
+  const int64_t blocks = (n + 255) / 256;
+  st::zero_u16_kernel<<<(unsigned)(blocks < 65536 ? blocks : 65536), 256, 0, stream>>>((uint16_t*)out, n);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
 static bool lookup_ok(const st_lookup* lk) {
   return lk && lk->K > 0 && lk->K <= ST_MAX_KVOL && lk->mul >= 1 && lk->div >= 1 && (lk->sign == 1 || lk->sign == -1);
 }
@@ -63,6 +81,7 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
   if (row_masks && mask_words != (K + 31) / 32) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
+  if (n_src == 0) return zero_output(out, n_dst, Nd, dtype, stream);
   const int W = (K + 31) / 32;
   if (dtype == ST_F32_BF16X3)
     return ops_gather_map_x3((const float*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
@@ -79,6 +98,7 @@ int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, cons
   if (n_dst >= (1ll << 31) || n_src >= (1ll << 31)) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!perm || !tile_nk || !tile_klist || !tile_map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
+  if (n_src == 0) return zero_output(out, n_dst, Nd, dtype, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
                                (float*)out, n_dst, K, Kd, Nd, stream);
@@ -121,6 +141,7 @@ int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int co
   if (capacity <= 0 || capacity >= (1ll << 31) || n_dst >= (1ll << 31)) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!dst_coords || !offsets || !keys || !vals || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
+  if (n_src == 0) return zero_output(out, n_dst, Nd, dtype, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_hash_x3((const float*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
                               (const float*)Bt, (float*)out, n_dst, Kd, Nd, stream);

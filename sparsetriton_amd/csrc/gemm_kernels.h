@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
 // Per step i: issue offset i+D-1's loads, store offset i's B tile into LDS
 // (double-buffered), barrier, MFMAs on offset i.  Requires Kd a multiple of
 // KS * KSTEP and 16-byte aligned A and Bt (every full-vector case).
-template <typename T, int BN, int KS, int D, typename Src>
+template <typename T, int BN, int KS, int D, typename Src, bool LINES>
 __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
@@ -347,11 +347,24 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   constexpr int NBLK = BN / 16;
   constexpr int CV = KDP / VEC;
   constexpr int BREGS = (BN * CV + 255) / 256;
+  // Whole-line A gathers (LINES): a row is CPR 16-byte chunks, an instruction
+  // loads RPI whole rows (CPR lanes per row) and the 2 * KS instructions of a
+  // step cover the wave's 32 rows; the rows pass through a per-wave LDS stage
+  // (chunk ch of row r at position ch ^ (r mod CPR): conflict-free stores and
+  // fragment reads) into the MFMA layout.  Fragment-shaped gathers instead
+  // touch 16 cache lines per instruction for a part of each, and every line
+  // twice, which backs up the L1 tag path when the rows hit in L2.
+  constexpr int CPR = KDP / VEC;
+  constexpr int RPI = 64 / CPR;
+  static_assert(!LINES || (CPR >= 4 && CPR <= 16 && 2 * KS * RPI == 32), "whole-line gather shape");
+  // offsets whose sources are resolved at once (fewer with the A stage, to keep 4 workgroups per CU)
+  constexpr int SG = LINES ? 8 : kSrcGroup;
   __shared__ __attribute__((aligned(16))) T bt_s[2][BN * PITCH];
+  __shared__ __attribute__((aligned(16))) T a_s[LINES ? 4 : 1][LINES ? 32 * KDP : VEC];
   __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
   __shared__ int32_t drow_s[kGemmBM];
   __shared__ int16_t klist_s[ST_MAX_KVOL];
-  __shared__ int32_t src_s[kSrcGroup][kGemmBM];
+  __shared__ int32_t src_s[SG][kGemmBM];
   __shared__ int nk_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -399,7 +412,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
   const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
   auto resolve_group = [&](int g0) {
-    const int ng = min(kSrcGroup, nk - g0);
+    const int ng = min(SG, nk - g0);
     for (int j = tid >> 7; j < ng; j += 2) {
       int32_t v;
       if constexpr (Src::kTiled)
@@ -411,7 +424,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     }
   };
 
-  F a_ring[D][2][KS];
+  F a_ring[D][2][KS];  // LINES: a_ring[SL][v / KS][v % KS] holds instruction v's chunk
   F b_ring[D][BREGS];
   bool any_ring[D];
   v4f acc[2][NBLK];
@@ -419,24 +432,38 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int lr = lane / CPR, lc = lane % CPR;  // whole-line loader lanes: row in the instruction, chunk
+  T* const a_w = a_s[LINES ? wid : 0];
 
   // loads of offset i (its sources must be resolved) into ring slot SL
   auto issue = [&](int i, auto slot) {
     constexpr int SL = decltype(slot)::value;
-    const int j = i % kSrcGroup;
-    const int32_t s0 = src_s[j][wid * 32 + c];
-    const int32_t s1 = src_s[j][wid * 32 + 16 + c];
-    any_ring[SL] = __ballot(s0 >= 0 || s1 >= 0) != 0ull;
-    // Branch-free loads (invalid rows read row 0 and are zeroed): loads under
-    // divergent branches would make the compiler drain the load queue.
-    const F* ar0 = reinterpret_cast<const F*>(A + (int64_t)(s0 >= 0 ? s0 : 0) * Kd + g * VEC);
-    const F* ar1 = reinterpret_cast<const F*>(A + (int64_t)(s1 >= 0 ? s1 : 0) * Kd + g * VEC);
+    const int j = i % SG;
+    if constexpr (LINES) {
+      bool any = false;
 #pragma unroll
-    for (int jj = 0; jj < KS; ++jj) {
-      a_ring[SL][0][jj] = ar0[jj * (KSTEP / VEC)];
-      a_ring[SL][1][jj] = ar1[jj * (KSTEP / VEC)];
-      if (s0 < 0) a_ring[SL][0][jj] = zero_frag<T>();
-      if (s1 < 0) a_ring[SL][1][jj] = zero_frag<T>();
+      for (int v = 0; v < 2 * KS; ++v) {
+        const int32_t sv = src_s[j][wid * 32 + v * RPI + lr];
+        any |= sv >= 0;
+        a_ring[SL][v / KS][v % KS] = *reinterpret_cast<const F*>(A + (int64_t)(sv >= 0 ? sv : 0) * Kd + lc * VEC);
+        if (sv < 0) a_ring[SL][v / KS][v % KS] = zero_frag<T>();
+      }
+      any_ring[SL] = __ballot(any) != 0ull;
+    } else {
+      const int32_t s0 = src_s[j][wid * 32 + c];
+      const int32_t s1 = src_s[j][wid * 32 + 16 + c];
+      any_ring[SL] = __ballot(s0 >= 0 || s1 >= 0) != 0ull;
+      // Branch-free loads (invalid rows read row 0 and are zeroed): loads under
+      // divergent branches would make the compiler drain the load queue.
+      const F* ar0 = reinterpret_cast<const F*>(A + (int64_t)(s0 >= 0 ? s0 : 0) * Kd + g * VEC);
+      const F* ar1 = reinterpret_cast<const F*>(A + (int64_t)(s1 >= 0 ? s1 : 0) * Kd + g * VEC);
+#pragma unroll
+      for (int jj = 0; jj < KS; ++jj) {
+        a_ring[SL][0][jj] = ar0[jj * (KSTEP / VEC)];
+        a_ring[SL][1][jj] = ar1[jj * (KSTEP / VEC)];
+        if (s0 < 0) a_ring[SL][0][jj] = zero_frag<T>();
+        if (s1 < 0) a_ring[SL][1][jj] = zero_frag<T>();
+      }
     }
     const int k = klist_s[i];
 #pragma unroll
@@ -466,21 +493,42 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     __syncthreads();
     if (i < gn && any_ring[SL]) {
       const T* bs = bt_s[buf];
+      if constexpr (LINES) {
+#pragma unroll
+        for (int v = 0; v < 2 * KS; ++v) {
+          const int r = v * RPI + lr;
+          *reinterpret_cast<F*>(&a_w[r * KDP + (lc ^ (r & (CPR - 1))) * VEC]) = a_ring[SL][v / KS][v % KS];
+        }
+        // LDS operations of one wave complete in order; the fences keep the
+        // compiler from moving the fragment reads above the stores.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
 #pragma unroll
       for (int jj = 0; jj < KS; ++jj) {
+        F a0, a1;
+        if constexpr (LINES) {
+          const int q = jj * (KSTEP / VEC) + g;
+          a0 = *reinterpret_cast<const F*>(&a_w[c * KDP + (q ^ (c & (CPR - 1))) * VEC]);
+          a1 = *reinterpret_cast<const F*>(&a_w[(16 + c) * KDP + (q ^ ((16 + c) & (CPR - 1))) * VEC]);
+        } else {
+          a0 = a_ring[SL][0][jj];
+          a1 = a_ring[SL][1][jj];
+        }
 #pragma unroll
         for (int nb = 0; nb < NBLK; ++nb) {
           const F b = *reinterpret_cast<const F*>(&bs[(nb * 16 + c) * PITCH + jj * KSTEP + g * VEC]);
-          acc[0][nb] = mfma(a_ring[SL][0][jj], b, acc[0][nb]);
-          acc[1][nb] = mfma(a_ring[SL][1][jj], b, acc[1][nb]);
+          acc[0][nb] = mfma(a0, b, acc[0][nb]);
+          acc[1][nb] = mfma(a1, b, acc[1][nb]);
         }
       }
     }
   };
 
   static_assert(D >= 2 && D <= 4, "ring depth 2..4");  // 2 is the one launched
-  for (int g0 = 0; g0 < nk; g0 += kSrcGroup) {
-    const int gn = min(kSrcGroup, nk - g0);
+  for (int g0 = 0; g0 < nk; g0 += SG) {
+    const int gn = min(SG, nk - g0);
     if (g0 > 0) __syncthreads();  // the previous group's sources are all issued
     resolve_group(g0);
     __syncthreads();
@@ -1048,13 +1096,28 @@ static int gemm_ring_depth() {
   return d;
 }
 
+// Whole-line A gathers staged through LDS (default); ST_GATHER_LINES=0
+// selects fragment-shaped gathers straight into registers (comparison runs).
+static bool gather_lines() {
+  static int on = -1;
+  if (on < 0) {
+    const char* e = getenv("ST_GATHER_LINES");
+    on = (e && e[0] == '0') ? 0 : 1;
+  }
+  return on == 1;
+}
+
 template <typename T, int BN, int KS, typename Src>
 static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W, const int32_t* rows,
                         const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)
-    gather_gemm_ring_kernel<T, BN, KS, 2, Src>
+  // (IEEE fp32 keeps the register path: its MFMAs dominate and the A stage only costs occupancy there)
+  if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2)
+    gather_gemm_ring_kernel<T, BN, KS, 2, Src, true>
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
+  else if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)
+    gather_gemm_ring_kernel<T, BN, KS, 2, Src, false>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
   else
     gather_gemm_pipe_kernel<T, BN, KS, Src>

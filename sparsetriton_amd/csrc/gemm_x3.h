@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
 // tile are loaded D-1 offsets ahead into a register ring; B is split into
 // hi / lo planes when stored to LDS, A when it is used.  Requires Kd =
 // KS * 32 and 16-byte aligned A and Bt.
-template <int BN, int KS, int D, typename Src>
+template <int BN, int KS, int D, typename Src, bool LINES>
 __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
     const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd) {
@@ -260,11 +260,19 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
   constexpr int NBLK = BN / 16;
   constexpr int CV = KDP / 4;
   constexpr int BREGS = (BN * CV + 255) / 256;
+  // Whole-line A gathers (LINES), as in gather_gemm_ring_kernel: CPR 16-byte
+  // chunks per fp32 row, RPI rows per instruction, 4 * KS instructions per
+  // step, rows staged per wave in LDS (chunk ch of row r at ch ^ (r mod CPR)).
+  constexpr int CPR = KDP / 4;
+  constexpr int RPI = 64 / CPR;
+  static_assert(!LINES || (CPR >= 8 && CPR <= 32 && 4 * KS * RPI == 32), "whole-line gather shape");
+  constexpr int SG = LINES ? 8 : kSrcGroup;
   __shared__ __attribute__((aligned(16))) __bf16 bt_s[2][2][BN * PITCH];
+  __shared__ __attribute__((aligned(16))) float a_s[LINES ? 4 : 1][LINES ? 32 * KDP : 4];
   __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
   __shared__ int32_t drow_s[kGemmBM];
   __shared__ int16_t klist_s[ST_MAX_KVOL];
-  __shared__ int32_t src_s[kSrcGroup][kGemmBM];
+  __shared__ int32_t src_s[SG][kGemmBM];
   __shared__ int nk_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -312,7 +320,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
   const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
   const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
   auto resolve_group = [&](int g0) {
-    const int ng = min(kSrcGroup, nk - g0);
+    const int ng = min(SG, nk - g0);
     for (int j = tid >> 7; j < ng; j += 2) {
       int32_t v;
       if constexpr (Src::kTiled)
@@ -333,23 +341,38 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 #pragma unroll
     for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  const int lr = lane / CPR, lc = lane % CPR;  // whole-line loader lanes
+  float* const a_w = a_s[LINES ? wid : 0];
   auto issue = [&](int i, auto slot) {
     constexpr int SL = decltype(slot)::value;
-    const int j = i % kSrcGroup;
-    const int32_t s0 = src_s[j][wid * 32 + c];
-    const int32_t s1 = src_s[j][wid * 32 + 16 + c];
-    any_ring[SL] = __ballot(s0 >= 0 || s1 >= 0) != 0ull;
-    const v4f* ar0 = reinterpret_cast<const v4f*>(A + (int64_t)(s0 >= 0 ? s0 : 0) * Kd + g * 8);
-    const v4f* ar1 = reinterpret_cast<const v4f*>(A + (int64_t)(s1 >= 0 ? s1 : 0) * Kd + g * 8);
+    const int j = i % SG;
+    if constexpr (LINES) {
+      bool any = false;
 #pragma unroll
-    for (int jj = 0; jj < KS; ++jj)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        a_ring[SL][0][jj][h] = ar0[jj * 8 + h];
-        a_ring[SL][1][jj][h] = ar1[jj * 8 + h];
-        if (s0 < 0) a_ring[SL][0][jj][h] = zero_frag<float>();
-        if (s1 < 0) a_ring[SL][1][jj][h] = zero_frag<float>();
+      for (int v = 0; v < 4 * KS; ++v) {
+        const int32_t sv = src_s[j][wid * 32 + v * RPI + lr];
+        any |= sv >= 0;
+        v4f& dst = a_ring[SL][v / (2 * KS)][(v / 2) % KS][v % 2];
+        dst = *reinterpret_cast<const v4f*>(A + (int64_t)(sv >= 0 ? sv : 0) * Kd + lc * 4);
+        if (sv < 0) dst = zero_frag<float>();
       }
+      any_ring[SL] = __ballot(any) != 0ull;
+    } else {
+      const int32_t s0 = src_s[j][wid * 32 + c];
+      const int32_t s1 = src_s[j][wid * 32 + 16 + c];
+      any_ring[SL] = __ballot(s0 >= 0 || s1 >= 0) != 0ull;
+      const v4f* ar0 = reinterpret_cast<const v4f*>(A + (int64_t)(s0 >= 0 ? s0 : 0) * Kd + g * 8);
+      const v4f* ar1 = reinterpret_cast<const v4f*>(A + (int64_t)(s1 >= 0 ? s1 : 0) * Kd + g * 8);
+#pragma unroll
+      for (int jj = 0; jj < KS; ++jj)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          a_ring[SL][0][jj][h] = ar0[jj * 8 + h];
+          a_ring[SL][1][jj][h] = ar1[jj * 8 + h];
+          if (s0 < 0) a_ring[SL][0][jj][h] = zero_frag<float>();
+          if (s1 < 0) a_ring[SL][1][jj][h] = zero_frag<float>();
+        }
+    }
     const int k = klist_s[i];
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
@@ -382,11 +405,35 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
     }
     __syncthreads();
     if (i < gn && any_ring[SL]) {
+      if constexpr (LINES) {
+#pragma unroll
+        for (int v = 0; v < 4 * KS; ++v) {
+          const int r = v * RPI + lr;
+          *reinterpret_cast<v4f*>(&a_w[r * KDP + (lc ^ (r & (CPR - 1))) * 4]) =
+              a_ring[SL][v / (2 * KS)][(v / 2) % KS][v % 2];
+        }
+        // LDS operations of one wave complete in order; the fences keep the
+        // compiler from moving the fragment reads above the stores.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
 #pragma unroll
       for (int jj = 0; jj < KS; ++jj) {
         v8bf ah[2], al[2];
-        split8(a_ring[SL][0][jj][0], a_ring[SL][0][jj][1], ah[0], al[0]);
-        split8(a_ring[SL][1][jj][0], a_ring[SL][1][jj][1], ah[1], al[1]);
+        if constexpr (LINES) {
+          const int q = jj * 8 + g * 2;
+          const float* r0 = a_w + c * KDP;
+          const float* r1 = a_w + (16 + c) * KDP;
+          const int z0 = c & (CPR - 1), z1 = (16 + c) & (CPR - 1);
+          split8(*reinterpret_cast<const v4f*>(&r0[(q ^ z0) * 4]), *reinterpret_cast<const v4f*>(&r0[((q + 1) ^ z0) * 4]),
+                 ah[0], al[0]);
+          split8(*reinterpret_cast<const v4f*>(&r1[(q ^ z1) * 4]), *reinterpret_cast<const v4f*>(&r1[((q + 1) ^ z1) * 4]),
+                 ah[1], al[1]);
+        } else {
+          split8(a_ring[SL][0][jj][0], a_ring[SL][0][jj][1], ah[0], al[0]);
+          split8(a_ring[SL][1][jj][0], a_ring[SL][1][jj][1], ah[1], al[1]);
+        }
 #pragma unroll
         for (int nb = 0; nb < NBLK; ++nb) {
           const int off = (nb * 16 + c) * PITCH + jj * 32 + g * 8;
@@ -400,8 +447,8 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
   };
 
   static_assert(D >= 2 && D <= 3, "ring depth 2..3");
-  for (int g0 = 0; g0 < nk; g0 += kSrcGroup) {
-    const int gn = min(kSrcGroup, nk - g0);
+  for (int g0 = 0; g0 < nk; g0 += SG) {
+    const int gn = min(SG, nk - g0);
     if (g0 > 0) __syncthreads();
     resolve_group(g0);
     __syncthreads();
@@ -572,8 +619,11 @@ static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint3
                       const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)
-    gather_gemm_ring_x3_kernel<BN, KS, 2, Src>
+  if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines())
+    gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true>
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd);
+  else if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)
+    gather_gemm_ring_x3_kernel<BN, KS, 2, Src, false>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd);
   else
     gather_gemm_x3_kernel<BN, KS, Src>

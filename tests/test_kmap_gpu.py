@@ -390,3 +390,21 @@ def test_occupancy_filter_changes_nothing(device, case):
         table.occupancy = occ
     assert torch.equal(with_bm, without)
     assert int((with_bm >= 0).sum()) > c.shape[0]
+
+
+def test_gather_without_sources_writes_zeros(device):
+    """A gather-GEMM over zero source rows (e.g. the input gradient of a layer whose output is
+    empty) writes zero rows without touching the (storage-less) source array."""
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import gather_gemm, gather_gemm_tiled
+    from sparsetriton_amd.nn.functional.conv.kmap import TileMap, TilePlan
+    K, n_dst = 27, 300
+    nbr = torch.full((K, n_dst), -1, dtype=torch.int32, device=device)
+    masks = torch.zeros((n_dst, 1), dtype=torch.int32, device=device)
+    perm = TilePlan.build(n_dst, K, masks).perm
+    tiles = TileMap.build(nbr, n_dst, 1, masks, K, perm, n_dst, 0)
+    assert int(tiles.nk.sum()) == 0
+    for dt in (torch.float32, torch.bfloat16):
+        A = torch.empty((0, 64), dtype=dt, device=device)
+        Bt = torch.randn((K, 64, 64), device=device).to(dt)
+        for out in (gather_gemm_tiled(A, tiles, Bt, n_dst, K), gather_gemm(A, nbr, n_dst, 1, masks, Bt, n_dst, K)):
+            assert out.shape == (n_dst, 64) and int(torch.count_nonzero(out)) == 0
