@@ -434,6 +434,9 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
   const int lr = lane / CPR, lc = lane % CPR;  // whole-line loader lanes: row in the instruction, chunk
   T* const a_w = a_s[LINES ? wid : 0];
+  // LINES: buffer loads (the host keeps both arrays under 2 GB); missing rows read zeros
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(A, LINES ? n_src * Kd * (int64_t)sizeof(T) : 0);
+  const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(Bt, LINES ? (int64_t)K * Nd * Kd * (int64_t)sizeof(T) : 0);
 
   // loads of offset i (its sources must be resolved) into ring slot SL
   auto issue = [&](int i, auto slot) {
@@ -445,8 +448,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
       for (int v = 0; v < 2 * KS; ++v) {
         const int32_t sv = src_s[j][wid * 32 + v * RPI + lr];
         any |= sv >= 0;
-        a_ring[SL][v / KS][v % KS] = *reinterpret_cast<const F*>(A + (int64_t)(sv >= 0 ? sv : 0) * Kd + lc * VEC);
-        if (sv < 0) a_ring[SL][v / KS][v % KS] = zero_frag<T>();
+        a_ring[SL][v / KS][v % KS] = load16<F>(a_rsrc, sv >= 0 ? sv * (Kd * (int)sizeof(T)) + lc * 16 : kOobOffset);
       }
       any_ring[SL] = __ballot(any) != 0ull;
     } else {
@@ -471,8 +473,12 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
       const int idx = tid + jb * 256;
       const int nr = idx / CV, cv = idx - nr * CV;
       const bool ok = idx < BN * CV && n0 + nr < Nd;
-      b_ring[SL][jb] = *reinterpret_cast<const F*>(Bt + ((int64_t)k * Nd + (ok ? n0 + nr : 0)) * Kd + cv * VEC);
-      if (!ok) b_ring[SL][jb] = zero_frag<T>();
+      if constexpr (LINES) {
+        b_ring[SL][jb] = load16<F>(b_rsrc, ok ? ((k * Nd + n0 + nr) * Kd + cv * VEC) * (int)sizeof(T) : kOobOffset);
+      } else {
+        b_ring[SL][jb] = *reinterpret_cast<const F*>(Bt + ((int64_t)k * Nd + (ok ? n0 + nr : 0)) * Kd + cv * VEC);
+        if (!ok) b_ring[SL][jb] = zero_frag<T>();
+      }
     }
   };
   // Step i of a group of gn offsets starting at g0 (ring slot SL = i % D):
@@ -1107,13 +1113,19 @@ static bool gather_lines() {
   return on == 1;
 }
 
+// Whole-line kernels address A and Bt through 32-bit buffer offsets.
+static bool buffer_ok(int64_t n_src, int K, int Kd, int Nd, size_t esz) {
+  return n_src * Kd * (int64_t)esz < (1ll << 31) - 64 && (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
+}
+
 template <typename T, int BN, int KS, typename Src>
 static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W, const int32_t* rows,
                         const T* Bt, T* out, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
   // (IEEE fp32 keeps the register path: its MFMAs dominate and the A stage only costs occupancy there)
-  if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2)
+  if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2 &&
+      buffer_ok(n_src, K, Kd, Nd, sizeof(T)))
     gather_gemm_ring_kernel<T, BN, KS, 2, Src, true>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b);
   else if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)

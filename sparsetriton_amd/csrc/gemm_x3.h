@@ -343,6 +343,9 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 
   const int lr = lane / CPR, lc = lane % CPR;  // whole-line loader lanes
   float* const a_w = a_s[LINES ? wid : 0];
+  // LINES: buffer loads (the host keeps both arrays under 2 GB); missing rows read zeros
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(A, LINES ? n_src * Kd * 4 : 0);
+  const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(Bt, LINES ? (int64_t)K * Nd * Kd * 4 : 0);
   auto issue = [&](int i, auto slot) {
     constexpr int SL = decltype(slot)::value;
     const int j = i % SG;
@@ -352,9 +355,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
       for (int v = 0; v < 4 * KS; ++v) {
         const int32_t sv = src_s[j][wid * 32 + v * RPI + lr];
         any |= sv >= 0;
-        v4f& dst = a_ring[SL][v / (2 * KS)][(v / 2) % KS][v % 2];
-        dst = *reinterpret_cast<const v4f*>(A + (int64_t)(sv >= 0 ? sv : 0) * Kd + lc * 4);
-        if (sv < 0) dst = zero_frag<float>();
+        a_ring[SL][v / (2 * KS)][(v / 2) % KS][v % 2] = load16<v4f>(a_rsrc, sv >= 0 ? sv * (Kd * 4) + lc * 16 : kOobOffset);
       }
       any_ring[SL] = __ballot(any) != 0ull;
     } else {
@@ -379,8 +380,12 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
       const int idx = tid + jb * 256;
       const int nr = idx / CV, cv = idx - nr * CV;
       const bool ok = idx < BN * CV && n0 + nr < Nd;
-      b_ring[SL][jb] = *reinterpret_cast<const v4f*>(Bt + ((int64_t)k * Nd + (ok ? n0 + nr : 0)) * Kd + cv * 4);
-      if (!ok) b_ring[SL][jb] = zero_frag<float>();
+      if constexpr (LINES) {
+        b_ring[SL][jb] = load16<v4f>(b_rsrc, ok ? ((k * Nd + n0 + nr) * Kd + cv * 4) * 4 : kOobOffset);
+      } else {
+        b_ring[SL][jb] = *reinterpret_cast<const v4f*>(Bt + ((int64_t)k * Nd + (ok ? n0 + nr : 0)) * Kd + cv * 4);
+        if (!ok) b_ring[SL][jb] = zero_frag<float>();
+      }
     }
   };
   auto step = [&](int g0, int gn, int i, auto slot) {
@@ -619,7 +624,7 @@ static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint3
                       const int32_t* rows, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines())
+  if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines() && buffer_ok(n_src, K, Kd, Nd, 4))
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd);
   else if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)

@@ -78,6 +78,20 @@ __device__ __forceinline__ typename Frag<T>::type load_frag(const T* __restrict_
   return f;
 }
 
+// Raw buffer resource over [base, base + bytes), bytes < 2^31 (gfx9-family
+// descriptor, word 3 = 32-bit data format).  A 16-byte load at a byte offset
+// past the end returns zeros and touches no memory: kOobOffset marks a
+// missing row without a clamp or a select.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+constexpr int kOobOffset = 0x7FFFFFF0;
+template <typename V>
+__device__ __forceinline__ V load16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  static_assert(sizeof(V) == 16, "16-byte fragment");
+  return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
+}
+
 template <typename T>
 __device__ __forceinline__ T from_f32(float v) {
   return (T)v;

@@ -323,10 +323,12 @@ def _fold_keys(masks, K):
     return key.astype(np.uint32)
 
 
-@pytest.mark.parametrize("n,K", [(0, 27), (1, 27), (4095, 8), (4097, 1), (300_001, 27), (123_457, 125), (70_000, 343)])
+@pytest.mark.parametrize("n,K", [(0, 27), (1, 27), (4095, 8), (4097, 1), (300_001, 27), (123_457, 125), (70_000, 343),
+                                 (1_100_000, 27)])
 def test_sort_rows_stable(device, n, K):
     """st_kmap_sort_rows is a stable sort of rows by their (folded) offset mask:
-    equal to numpy's stable argsort across many 4096-row tiles and all digits."""
+    equal to numpy's stable argsort across many 4096-row tiles and all digits (up to 256 tiles
+    the scatter sums its offsets from the count table itself; 1.1M rows take the scan launch)."""
     from sparsetriton_amd.nn.functional.conv.kmap import TilePlan
     rng = np.random.default_rng(n + K)
     W = (K + 31) // 32
