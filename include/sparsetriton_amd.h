@@ -353,10 +353,12 @@ int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, in
  * (st_kmap_pairs_chunk_keys); each workgroup takes a contiguous run of it and
  * the workgroups one XCD runs (launched round-robin over the 8 XCDs) take
  * adjacent runs, so chunks sharing input and output rows meet in one L2.
+ * n_in / n_out: rows of X / dY (every pair indexes inside them).
  */
-int st_wgrad_pairs(const void* X, const void* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
-                   int K, int chunk, int64_t max_chunks, const int32_t* chunk_order, int C_in, int C_out, int dtype,
-                   float* partials, void* dW, int dw_dtype, st_stream_t stream);
+int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, const int32_t* pairs,
+                   const int32_t* kstart, const int32_t* cstart, int K, int chunk, int64_t max_chunks,
+                   const int32_t* chunk_order, int C_in, int C_out, int dtype, float* partials, void* dW, int dw_dtype,
+                   st_stream_t stream);
 
 /* ----------------------------------------------------- implicit hash-fly */
 

@@ -16,9 +16,10 @@ int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int co
 int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
                         const int32_t* tmap, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
                         hipStream_t stream);
-int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
-                       const int32_t* cstart, const int32_t* chunk_order, int K, int chunk, int64_t max_chunks,
-                       int Cin, int Cout, float* partials, void* dW, int dw_dtype, hipStream_t stream);
+int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,
+                       const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
+                       int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
+                       hipStream_t stream);
 }  // namespace st
 
 using namespace st;
@@ -119,19 +120,20 @@ int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, in
                                      C_out, partials, splits, dW, dw_dtype, stream));
 }
 
-int st_wgrad_pairs(const void* X, const void* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
-                   int K, int chunk, int64_t max_chunks, const int32_t* chunk_order, int C_in, int C_out, int dtype,
-                   float* partials, void* dW, int dw_dtype, st_stream_t stream) {
+int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, const int32_t* pairs,
+                   const int32_t* kstart, const int32_t* cstart, int K, int chunk, int64_t max_chunks,
+                   const int32_t* chunk_order, int C_in, int C_out, int dtype, float* partials, void* dW, int dw_dtype,
+                   st_stream_t stream) {
   if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0 || max_chunks >= (1ll << 31) || C_in <= 0 ||
-      C_out <= 0)
+      C_out <= 0 || n_in < 0 || n_out < 0)
     return ST_ERR_ARG;
   if (!kstart || !cstart || !partials || !dW || (max_chunks > 0 && (!pairs || !X || !dY))) return ST_ERR_ARG;
   if (dtype == ST_F32_BF16X3)
-    return ops_wgrad_pairs_x3((const float*)X, (const float*)dY, pairs, kstart, cstart, chunk_order, K, chunk,
-                              max_chunks, C_in, C_out, partials, dW, dw_dtype, stream);
+    return ops_wgrad_pairs_x3((const float*)X, n_in, (const float*)dY, n_out, pairs, kstart, cstart, chunk_order, K,
+                              chunk, max_chunks, C_in, C_out, partials, dW, dw_dtype, stream);
   ST_DISPATCH_DTYPE(dtype, T,
-                    ops_wgrad_pairs<T>((const T*)X, (const T*)dY, pairs, kstart, cstart, chunk_order, K, chunk,
-                                       max_chunks, C_in, C_out, partials, dW, dw_dtype, stream));
+                    ops_wgrad_pairs<T>((const T*)X, n_in, (const T*)dY, n_out, pairs, kstart, cstart, chunk_order, K,
+                                       chunk, max_chunks, C_in, C_out, partials, dW, dw_dtype, stream));
 }
 
 int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int coord_dtype, int64_t n_dst,

@@ -808,13 +808,13 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
 // the waves' accumulators are summed through LDS once per chunk.  Requires
 // C_in and C_out multiples of 64 and 16-byte aligned rows.
 constexpr int kWvPitch = 80;
-template <typename T>
+template <typename T, bool BUF>  // BUF: row loads through buffer resources (X and dY under 2 GB)
 __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
                                                                const int32_t* __restrict__ kstart,
                                                                const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
     int K, int chunk,
-                                                               int Cin, int Cout, float* __restrict__ partials) {
+                                                               int Cin, int Cout, int64_t n_in, int64_t n_out, float* __restrict__ partials) {
   using F = typename Frag<T>::type;
   static_assert(Frag<T>::KSTEP == 32 && Frag<T>::VEC == 8, "16-bit MFMA fragments");
   constexpr int STAGE = 32 * kWvPitch;  // elements per operand per wave
@@ -840,6 +840,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
   // Each lane keeps pair (lane mod 32) and takes instruction v's row index
   // from lane 8v + lane / 8.
   const int lr = lane >> 3, lc = lane & 7;
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * (int64_t)sizeof(T) : 0);
+  const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, BUF ? n_out * Cout * (int64_t)sizeof(T) : 0);
 
   const ChunkRange cr = chunk_range(total);
   for (int cq = cr.q0; cq < cr.q1; ++cq) {
@@ -860,8 +862,13 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int ix = __shfl(pr.x, v * 8 + lr, 64), iy = __shfl(pr.y, v * 8 + lr, 64);
-        xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lc * 8) : zero_frag<T>();
-        yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lc * 8) : zero_frag<T>();
+        if constexpr (BUF) {
+          xr[v] = load16<F>(x_rsrc, ix >= 0 ? (ix * Cin + cm0 + lc * 8) * (int)sizeof(T) : kOobOffset);
+          yr[v] = load16<F>(y_rsrc, iy >= 0 ? (iy * Cout + cn0 + lc * 8) * (int)sizeof(T) : kOobOffset);
+        } else {
+          xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lc * 8) : zero_frag<T>();
+          yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lc * 8) : zero_frag<T>();
+        }
       }
     };
     int q = p0 + wid * 32;
@@ -1259,6 +1266,11 @@ static void launch_wgrad_pairs_f32(const float* X, const float* dY, const int2* 
 static int pow2_tile(int blocks) { return blocks >= 4 ? 4 : (blocks >= 2 ? 2 : 1); }
 
 
+// Row arrays addressable by 32-bit buffer offsets.
+static bool rows_fit_buffer(int64_t n_in, int Cin, int64_t n_out, int Cout, size_t esz) {
+  return n_in * Cin * (int64_t)esz < (1ll << 31) - 64 && n_out * Cout * (int64_t)esz < (1ll << 31) - 64;
+}
+
 // 16-bit weight-gradient kernel: 0 = per-wave steps (default), 1 = workgroup
 // LDS transpose (ST_WGRAD16=lds selects it, for comparison runs).
 static int wgrad16_mode() {
@@ -1271,9 +1283,9 @@ static int wgrad16_mode() {
 }
 
 template <typename T>
-int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t* kstart, const int32_t* cstart,
-                    const int32_t* chunk_order, int K, int chunk, int64_t max_chunks, int Cin, int Cout,
-                    float* partials, void* dW, int dw_dtype, hipStream_t stream) {
+int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const int32_t* pairs, const int32_t* kstart,
+                    const int32_t* cstart, const int32_t* chunk_order, int K, int chunk, int64_t max_chunks, int Cin,
+                    int Cout, float* partials, void* dW, int dw_dtype, hipStream_t stream) {
   if (max_chunks > 0) {
     if constexpr (sizeof(T) == 4) {
       const int mt = pow2_tile((Cin + 15) / 16), nt = pow2_tile((Cout + 15) / 16);
@@ -1294,8 +1306,12 @@ int ops_wgrad_pairs(const T* X, const T* dY, const int32_t* pairs, const int32_t
       const int mode = wgrad16_mode();
       if (mode == 0 && Cin % 64 == 0 && Cout % 64 == 0 && vec_x && vec_y) {
         const unsigned gz64 = (unsigned)((Cin / 64) * (Cout / 64));
-        wgrad_pairs_wave_kernel<T><<<dim3(gx, 1, gz64), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
-                                                                          Cout, partials);
+        if (rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T)))
+          wgrad_pairs_wave_kernel<T, true><<<dim3(gx, 1, gz64), 256, 0, stream>>>(
+              X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
+        else
+          wgrad_pairs_wave_kernel<T, false><<<dim3(gx, 1, gz64), 256, 0, stream>>>(
+              X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
         ST_CHECK_LAUNCH();
         return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
       }
@@ -1399,8 +1415,9 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
   X template int ops_wgrad_hash<T>(const T*, int64_t, const T*, const void*, int, int64_t, const int32_t*,           \
                                    const st_lookup*, const uint64_t*, const uint32_t*, int64_t, int, int, float*,    \
                                    int64_t, void*, int, hipStream_t);                                                \
-  X template int ops_wgrad_pairs<T>(const T*, const T*, const int32_t*, const int32_t*, const int32_t*,              \
-                                    const int32_t*, int, int, int64_t, int, int, float*, void*, int, hipStream_t);   \
+  X template int ops_wgrad_pairs<T>(const T*, int64_t, const T*, int64_t, const int32_t*, const int32_t*,          \
+                                    const int32_t*, const int32_t*, int, int, int64_t, int, int, float*, void*, int, \
+                                    hipStream_t);                                                                    \
   X template int ops_weight_prep<T>(const T*, T*, int, int, int, int, hipStream_t);                                  \
   X template int ops_gather_tiled<T>(const T*, int64_t, const int32_t*, const int32_t*, const int16_t*,              \
                                      const int32_t*, const T*, T*, int64_t, int, int, int, hipStream_t);             \

@@ -506,13 +506,15 @@ __device__ __forceinline__ int wv_swz(int r) { return ((r & 1) << 2) | ((r >> 1)
 __device__ __forceinline__ int wv_at(int p, int col) {
   return p * kWvPitchF + ((((col >> 2) ^ wv_swz(p & 7)) << 2) | (col & 3));
 }
+template <bool BUF>  // BUF: row loads through buffer resources (X and dY under 2 GB)
 __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __restrict__ X,
                                                                 const float* __restrict__ dY,
                                                                 const int2* __restrict__ pairs,
                                                                 const int32_t* __restrict__ kstart,
                                                                 const int32_t* __restrict__ cstart,
                                                                 const int32_t* __restrict__ chunk_order, int K, int chunk,
-                                                                int Cin, int Cout, float* __restrict__ partials) {
+                                                                int Cin, int Cout, int64_t n_in, int64_t n_out,
+                                                                float* __restrict__ partials) {
   constexpr int STAGE = 32 * kWvPitchF;  // floats per operand per wave
   constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(float);
   constexpr int RP = 68;
@@ -531,6 +533,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   float* ys = xs + STAGE;
   float* red = reinterpret_cast<float*>(lds);
   const int lr = lane >> 4, lc = lane & 15;  // loader lanes: row lr of each 4-row group, 16-byte chunk lc
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * 4 : 0);
+  const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, BUF ? n_out * Cout * 4 : 0);
 
   const ChunkRange cr = chunk_range(total);
   for (int cq = cr.q0; cq < cr.q1; ++cq) {
@@ -551,8 +555,13 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         const int ix = __shfl(pr.x, v * 4 + lr, 64), iy = __shfl(pr.y, v * 4 + lr, 64);
-        xr[v] = ix >= 0 ? *reinterpret_cast<const v4f*>(X + (int64_t)ix * Cin + cm0 + lc * 4) : zero_frag<float>();
-        yr[v] = iy >= 0 ? *reinterpret_cast<const v4f*>(dY + (int64_t)iy * Cout + cn0 + lc * 4) : zero_frag<float>();
+        if constexpr (BUF) {
+          xr[v] = load16<v4f>(x_rsrc, ix >= 0 ? (ix * Cin + cm0 + lc * 4) * 4 : kOobOffset);
+          yr[v] = load16<v4f>(y_rsrc, iy >= 0 ? (iy * Cout + cn0 + lc * 4) * 4 : kOobOffset);
+        } else {
+          xr[v] = ix >= 0 ? *reinterpret_cast<const v4f*>(X + (int64_t)ix * Cin + cm0 + lc * 4) : zero_frag<float>();
+          yr[v] = iy >= 0 ? *reinterpret_cast<const v4f*>(dY + (int64_t)iy * Cout + cn0 + lc * 4) : zero_frag<float>();
+        }
       }
     };
     int q = p0 + wid * 32;

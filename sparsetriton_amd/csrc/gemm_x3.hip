@@ -30,18 +30,24 @@ int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, cons
   return launch_gather_x3(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, n_dst, K, Kd, Nd, stream);
 }
 
-int ops_wgrad_pairs_x3(const float* X, const float* dY, const int32_t* pairs, const int32_t* kstart,
-                       const int32_t* cstart, const int32_t* chunk_order, int K, int chunk, int64_t max_chunks,
-                       int Cin, int Cout, float* partials, void* dW, int dw_dtype, hipStream_t stream) {
+int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,
+                       const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
+                       int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
+                       hipStream_t stream) {
   const bool fits = Cin % 64 == 0 && Cout % 64 == 0 && (uintptr_t)X % 16 == 0 && (uintptr_t)dY % 16 == 0;
   if (!fits)
-    return ops_wgrad_pairs<float>(X, dY, pairs, kstart, cstart, chunk_order, K, chunk, max_chunks, Cin, Cout,
-                                  partials, dW, dw_dtype, stream);
+    return ops_wgrad_pairs<float>(X, n_in, dY, n_out, pairs, kstart, cstart, chunk_order, K, chunk, max_chunks, Cin,
+                                  Cout, partials, dW, dw_dtype, stream);
   if (max_chunks > 0) {
     const unsigned gx = wgrad_grid(max_chunks);
     const unsigned gz = (unsigned)((Cin / 64) * (Cout / 64));
-    wgrad_pairs_x3_kernel<<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, reinterpret_cast<const int2*>(pairs), kstart,
-                                                                cstart, chunk_order, K, chunk, Cin, Cout, partials);
+    const int2* pr = reinterpret_cast<const int2*>(pairs);
+    if (rows_fit_buffer(n_in, Cin, n_out, Cout, 4))
+      wgrad_pairs_x3_kernel<true><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk,
+                                                                       Cin, Cout, n_in, n_out, partials);
+    else
+      wgrad_pairs_x3_kernel<false><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K,
+                                                                        chunk, Cin, Cout, n_in, n_out, partials);
     ST_CHECK_LAUNCH();
   }
   return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);

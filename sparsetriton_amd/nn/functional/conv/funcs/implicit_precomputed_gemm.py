@@ -111,8 +111,8 @@ def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dt
     pl = kmap.pair_list()
     partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
     dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
-    _lib.call("st_wgrad_pairs", _lib.ptr(X), _lib.ptr(dY), _lib.ptr(pl.pairs), _lib.ptr(pl.kstart),
-              _lib.ptr(pl.cstart), K, pl.chunk, pl.max_chunks, _lib.ptr(pl.corder), C_in, C_out,
+    _lib.call("st_wgrad_pairs", _lib.ptr(X), X.shape[0], _lib.ptr(dY), dY.shape[0], _lib.ptr(pl.pairs),
+              _lib.ptr(pl.kstart), _lib.ptr(pl.cstart), K, pl.chunk, pl.max_chunks, _lib.ptr(pl.corder), C_in, C_out,
               _lib.compute_code(X.dtype),
               _lib.ptr(partials), _lib.ptr(dW), _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
     return dW
