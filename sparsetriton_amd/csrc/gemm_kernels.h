@@ -359,7 +359,11 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   static_assert(!LINES || (CPR >= 4 && CPR <= 16 && 2 * KS * RPI == 32), "whole-line gather shape");
   // offsets whose sources are resolved at once (fewer with the A stage, to keep 4 workgroups per CU)
   constexpr int SG = LINES ? 8 : kSrcGroup;
-  __shared__ __attribute__((aligned(16))) T bt_s[2][BN * PITCH];
+  // LINES: the B tile unpadded, chunk ch of row n at ch ^ bswz(n) -- the 16
+  // rows one fragment read touches land on 16 distinct 4-bank groups
+  constexpr int BPITCH = LINES ? KDP : PITCH;
+  constexpr int BRPB = 16 / CV > 0 ? 16 / CV : 1;  // B rows per 256 bytes
+  __shared__ __attribute__((aligned(16))) T bt_s[2][BN * BPITCH];
   __shared__ __attribute__((aligned(16))) T a_s[LINES ? 4 : 1][LINES ? 32 * KDP : VEC];
   __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
   __shared__ int32_t drow_s[kGemmBM];
@@ -432,6 +436,13 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  // element offset of 16-byte chunk ch of B row n
+  auto bpos = [](int n, int ch) -> int {
+    if constexpr (LINES)
+      return n * BPITCH + (ch ^ ((n / BRPB) % CV)) * VEC;
+    else
+      return n * BPITCH + ch * VEC;
+  };
   const int lr = lane / CPR, lc = lane % CPR;  // whole-line loader lanes: row in the instruction, chunk
   T* const a_w = a_s[LINES ? wid : 0];
   // LINES: buffer loads (the host keeps both arrays under 2 GB); missing rows read zeros
@@ -494,7 +505,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     for (int jb = 0; jb < BREGS; ++jb) {
       const int idx = tid + jb * 256;
       const int nr = idx / CV, cv = idx - nr * CV;
-      if (idx < BN * CV) *reinterpret_cast<F*>(&bt_s[buf][nr * PITCH + cv * VEC]) = b_ring[SL][jb];
+      if (idx < BN * CV) *reinterpret_cast<F*>(&bt_s[buf][bpos(nr, cv)]) = b_ring[SL][jb];
     }
     __syncthreads();
     if (i < gn && any_ring[SL]) {
@@ -524,7 +535,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
         }
 #pragma unroll
         for (int nb = 0; nb < NBLK; ++nb) {
-          const F b = *reinterpret_cast<const F*>(&bs[(nb * 16 + c) * PITCH + jj * KSTEP + g * VEC]);
+          const F b = *reinterpret_cast<const F*>(&bs[bpos(nb * 16 + c, jj * (KSTEP / VEC) + g)]);
           acc[0][nb] = mfma(a0, b, acc[0][nb]);
           acc[1][nb] = mfma(a1, b, acc[1][nb]);
         }

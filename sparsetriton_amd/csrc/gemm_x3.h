@@ -267,7 +267,11 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
   constexpr int RPI = 64 / CPR;
   static_assert(!LINES || (CPR >= 8 && CPR <= 32 && 4 * KS * RPI == 32), "whole-line gather shape");
   constexpr int SG = LINES ? 8 : kSrcGroup;
-  __shared__ __attribute__((aligned(16))) __bf16 bt_s[2][2][BN * PITCH];
+  // LINES: hi / lo B planes unpadded, 8-element chunk ch of row n at ch ^ bswz(n)
+  constexpr int BCH = KDP / 8;  // chunks per B row
+  constexpr int BPITCH = LINES ? KDP : PITCH;
+  constexpr int BRPB = 16 / BCH > 0 ? 16 / BCH : 1;
+  __shared__ __attribute__((aligned(16))) __bf16 bt_s[2][2][BN * BPITCH];
   __shared__ __attribute__((aligned(16))) float a_s[LINES ? 4 : 1][LINES ? 32 * KDP : 4];
   __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
   __shared__ int32_t drow_s[kGemmBM];
@@ -341,6 +345,13 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 #pragma unroll
     for (int nb = 0; nb < NBLK; ++nb) acc[m][nb] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  // element offset of 8-element chunk ch of B row n (either plane)
+  auto bpos = [](int n, int ch) -> int {
+    if constexpr (LINES)
+      return n * BPITCH + (ch ^ ((n / BRPB) % BCH)) * 8;
+    else
+      return n * BPITCH + ch * 8;
+  };
   const int lr = lane / CPR, lc = lane % CPR;  // whole-line loader lanes
   float* const a_w = a_s[LINES ? wid : 0];
   // LINES: buffer loads (the host keeps both arrays under 2 GB); missing rows read zeros
@@ -404,8 +415,9 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
           hi[e] = (__bf16)b_ring[SL][jb][e];
           lo[e] = (__bf16)(b_ring[SL][jb][e] - (float)hi[e]);
         }
-        *reinterpret_cast<v4bf*>(&bt_s[buf][0][nr * PITCH + cv * 4]) = hi;
-        *reinterpret_cast<v4bf*>(&bt_s[buf][1][nr * PITCH + cv * 4]) = lo;
+        const int o = bpos(nr, cv >> 1) + (cv & 1) * 4;
+        *reinterpret_cast<v4bf*>(&bt_s[buf][0][o]) = hi;
+        *reinterpret_cast<v4bf*>(&bt_s[buf][1][o]) = lo;
       }
     }
     __syncthreads();
@@ -441,7 +453,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
         }
 #pragma unroll
         for (int nb = 0; nb < NBLK; ++nb) {
-          const int off = (nb * 16 + c) * PITCH + jj * 32 + g * 8;
+          const int off = bpos(nb * 16 + c, jj * 4 + g);
           const v8bf bh = *reinterpret_cast<const v8bf*>(&bt_s[buf][0][off]);
           const v8bf bl = *reinterpret_cast<const v8bf*>(&bt_s[buf][1][off]);
           acc[0][nb] = mfma_x3(ah[0], al[0], bh, bl, acc[0][nb]);
