@@ -134,8 +134,16 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"sparsetriton_amd: {what} failed: {ERRORS.get(rc, rc)} ({rc})")
 
 
+_FNS = {}
+
+
 def call(name: str, *args) -> None:
-    check(getattr(lib(), name)(*args), name)
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(lib(), name)
+    rc = fn(*args)
+    if rc != ST_OK:
+        check(rc, name)
 
 
 def ptr(t) -> int:
@@ -145,8 +153,15 @@ def ptr(t) -> int:
     return t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device):
-    """Raw hipStream_t of torch's current stream on `device`."""
+    """Raw hipStream_t of torch's current stream on `device` (the kernel launches are cheap
+    enough that this lookup shows up in map builds, hence the direct binding)."""
+    if _raw_stream is not None:
+        idx = device.index
+        return _raw_stream(idx if idx is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

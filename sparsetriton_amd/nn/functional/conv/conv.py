@@ -133,11 +133,13 @@ def sparse_conv3d(
                 out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
                     tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
-            if torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
-                kmap.start_pair_list()  # the weight gradient's pair list, overlapping the forward
         if out_coords.shape[0] == 0:
             return _empty(tensor, C_out, new_shape)
         out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap)
+        if hit is None and torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
+            # the weight gradient's pair list on a side stream, queued after the forward (which
+            # needs the tile plan first) and running alongside it
+            kmap.start_pair_list()
     elif algo == ConvAlgo.ImplicitHashFlyGEMM:
         hkey = ("hashfly",) + cache_key
         hit = tensor._cache.kmaps.get(hkey)

@@ -119,6 +119,12 @@ class KernelMap:
         self._bwd_tiles = None
         self._pairs = {}
         self._pairs_ready = {}  # chunk -> event of a pair list being built on the side stream
+        # the map is complete on the creating stream once this event has passed, so side-stream
+        # work can start before whatever the creating stream queues after it
+        self._built = None
+        if nbr.is_cuda:
+            self._built = torch.cuda.Event()
+            self._built.record(torch.cuda.current_stream(nbr.device))
 
     @classmethod
     def from_neighbor_indices(cls, neighbor_indices: torch.Tensor, n_in: int) -> "KernelMap":
@@ -207,13 +213,17 @@ class KernelMap:
 
     def start_pair_list(self, chunk: int = 2048) -> None:
         """Begin building the pair list on a side stream, so it overlaps the tile plans and the
-        forward GEMM; ``pair_list()`` makes the calling stream wait for it."""
+        forward GEMM; ``pair_list()`` makes the calling stream wait for it.  The side stream
+        waits only for the map itself, so this may be called after the forward is queued."""
         if chunk in self._pairs:
             return
         dev = self.nbr.device
         main = torch.cuda.current_stream(dev)
         side = _side_stream(dev)
-        side.wait_stream(main)
+        if self._built is not None:
+            side.wait_event(self._built)
+        else:
+            side.wait_stream(main)
         self.nbr.record_stream(side)  # read on the side stream
         with torch.cuda.stream(side):
             pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)
@@ -226,10 +236,11 @@ class KernelMap:
 
     def prepare(self) -> "KernelMap":
         """Build everything forward and backward need (idempotent); the pair list is built on a
-        side stream alongside the tile plans."""
-        self.start_pair_list()
+        side stream alongside the tile plans (queued after them: host launch time is the scarcer
+        resource, and the forward needs the plans first)."""
         self.forward_tiles()
         self.backward_tiles()
+        self.start_pair_list()
         self.pair_list()
         return self
 
