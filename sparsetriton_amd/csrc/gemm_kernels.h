@@ -819,6 +819,24 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
 // the waves' accumulators are summed through LDS once per chunk.  Requires
 // C_in and C_out multiples of 64 and 16-byte aligned rows.
 constexpr int kWvPitch = 80;
+// MFMA operand fragment of a 32-pair step staged row-major (pitch kWvPitch
+// 16-bit elements): lane (c, g) gets channel col0 + c of pairs 8g .. 8g+7,
+// with two gfx950 transpose reads (ds_read_b64_tr_b16).  Within a 16-lane
+// group such a read hands lane l the element l mod 4 of the 4 elements lane
+// 4e + l/4 addresses, for e = 0..3; so lane c addresses pair 8g + 4h + c/4 at
+// channel col0 + 4 (c mod 4) and receives channel col0 + c of pairs 8g + 4h + e.
+template <typename F, typename T>
+__device__ __forceinline__ F tr_frag(const T* st, int g, int c, int col0) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef short v8s __attribute__((ext_vector_type(8)));
+  using lds_v4s = __attribute__((address_space(3))) v4s;
+  const T* p0 = st + (g * 8 + (c >> 2)) * kWvPitch + col0 + (c & 3) * 4;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 4 * kWvPitch));
+  const v8s both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(F, both);
+}
+
 template <typename T, bool BUF>  // BUF: row loads through buffer resources (X and dY under 2 GB)
 __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
@@ -899,10 +917,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
       F a[4], b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[i][e] = xs[(e * 4 + g) * kWvPitch + i * 16 + c];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) b[i][e] = ys[(e * 4 + g) * kWvPitch + i * 16 + c];
+        a[i] = tr_frag<F>(xs, g, c, i * 16);
+        b[i] = tr_frag<F>(ys, g, c, i * 16);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
