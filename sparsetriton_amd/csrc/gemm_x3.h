@@ -518,6 +518,31 @@ __device__ __forceinline__ int wv_swz(int r) { return ((r & 1) << 2) | ((r >> 1)
 __device__ __forceinline__ int wv_at(int p, int col) {
   return p * kWvPitchF + ((((col >> 2) ^ wv_swz(p & 7)) << 2) | (col & 3));
 }
+
+// bf16 plane of a 32-pair step (32 rows x 64 channels): 4-element granule q of
+// row r at position q ^ f(r), f(r) = 4 * (((r >> 1) & 1) | ((r >> 2) & 2)).
+// The transpose reads below touch rows 8g + 4h + {0..3}; f puts the even (and
+// the odd) rows of two lane groups read together on four different granule
+// groups, so each half-wave covers 64 distinct banks.
+__device__ __forceinline__ int pl_at(int r, int col) {
+  const int f = (((r >> 1) & 1) | ((r >> 2) & 2)) << 2;
+  return r * 64 + ((((col >> 2) ^ f)) << 2) + (col & 3);
+}
+
+// MFMA operand fragment from a bf16 plane: lane (c, g) gets channel col0 + c
+// of pairs 8g .. 8g+7 by two gfx950 transpose reads (ds_read_b64_tr_b16: in a
+// 16-lane group, lane l receives element l mod 4 of the 4 elements lane
+// 4e + l/4 addresses, e = 0..3), lane c addressing pair 8g + 4h + c/4 at
+// channel col0 + 4 (c mod 4).
+__device__ __forceinline__ v8bf tr_plane(const __bf16* plane, int g, int c, int col0) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef short v8s __attribute__((ext_vector_type(8)));
+  using lds_v4s = __attribute__((address_space(3))) v4s;
+  const int r = g * 8 + (c >> 2), col = col0 + (c & 3) * 4;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(plane + pl_at(r, col)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(plane + pl_at(r + 4, col)));
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 template <bool BUF>  // BUF: row loads through buffer resources (X and dY under 2 GB)
 __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __restrict__ X,
                                                                 const float* __restrict__ dY,
@@ -527,8 +552,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
                                                                 const int32_t* __restrict__ chunk_order, int K, int chunk,
                                                                 int Cin, int Cout, int64_t n_in, int64_t n_out,
                                                                 float* __restrict__ partials) {
-  constexpr int STAGE = 32 * kWvPitchF;  // floats per operand per wave
-  constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(float);
+  constexpr int STAGE = 32 * 64;  // bf16 elements per plane (4 planes per wave: X hi, X lo, dY hi, dY lo)
+  constexpr int STAGE_BYTES = 4 * 4 * STAGE * 2;
   constexpr int RP = 68;
   constexpr int RED_BYTES = 4 * 64 * RP * (int)sizeof(float);
   __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
@@ -541,8 +566,10 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
 
   const int ntn = Cout / 64;
   const int cm0 = (blockIdx.z / ntn) * 64, cn0 = (blockIdx.z % ntn) * 64;
-  float* xs = reinterpret_cast<float*>(lds) + wid * 2 * STAGE;
-  float* ys = xs + STAGE;
+  __bf16* xh = reinterpret_cast<__bf16*>(lds) + wid * 4 * STAGE;
+  __bf16* xl = xh + STAGE;
+  __bf16* yh = xl + STAGE;
+  __bf16* yl = yh + STAGE;
   float* red = reinterpret_cast<float*>(lds);
   const int lr = lane >> 4, lc = lane & 15;  // loader lanes: row lr of each 4-row group, 16-byte chunk lc
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * 4 : 0);
@@ -581,8 +608,23 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
     for (; q < p1; q += 128) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        *reinterpret_cast<v4f*>(&xs[wv_at(v * 4 + lr, lc * 4)]) = xr[v];
-        *reinterpret_cast<v4f*>(&ys[wv_at(v * 4 + lr, lc * 4)]) = yr[v];
+        // split once per element as it is staged: hi = bf16(x), lo = bf16(x - hi)
+        v4bf h, l;
+        const int at = pl_at(v * 4 + lr, lc * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h[e] = (__bf16)xr[v][e];
+          l[e] = (__bf16)(xr[v][e] - (float)h[e]);
+        }
+        *reinterpret_cast<v4bf*>(&xh[at]) = h;
+        *reinterpret_cast<v4bf*>(&xl[at]) = l;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h[e] = (__bf16)yr[v][e];
+          l[e] = (__bf16)(yr[v][e] - (float)h[e]);
+        }
+        *reinterpret_cast<v4bf*>(&yh[at]) = h;
+        *reinterpret_cast<v4bf*>(&yl[at]) = l;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -591,24 +633,13 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
       v8bf bh[4], bl[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        v4f y0, y1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          y0[e] = ys[wv_at(e * 4 + g, j * 16 + c)];
-          y1[e] = ys[wv_at((e + 4) * 4 + g, j * 16 + c)];
-        }
-        split8(y0, y1, bh[j], bl[j]);
+        bh[j] = tr_plane(yh, g, c, j * 16);
+        bl[j] = tr_plane(yl, g, c, j * 16);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        v4f x0, x1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x0[e] = xs[wv_at(e * 4 + g, i * 16 + c)];
-          x1[e] = xs[wv_at((e + 4) * 4 + g, i * 16 + c)];
-        }
-        v8bf ah, al;
-        split8(x0, x1, ah, al);
+        const v8bf ah = tr_plane(xh, g, c, i * 16);
+        const v8bf al = tr_plane(xl, g, c, i * 16);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_x3(ah, al, bh[j], bl[j], acc[i][j]);
       }
