@@ -451,13 +451,30 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
           split8(a_ring[SL][0][jj][0], a_ring[SL][0][jj][1], ah[0], al[0]);
           split8(a_ring[SL][1][jj][0], a_ring[SL][1][jj][1], ah[1], al[1]);
         }
+        // the three products in three rounds over all 2 * NBLK accumulators, so that
+        // consecutive MFMAs never feed each other (one round per product keeps
+        // 2 * NBLK independent accumulations between dependent ones)
+        v8bf bh[NBLK], bl[NBLK];
 #pragma unroll
         for (int nb = 0; nb < NBLK; ++nb) {
           const int off = bpos(nb * 16 + c, jj * 4 + g);
-          const v8bf bh = *reinterpret_cast<const v8bf*>(&bt_s[buf][0][off]);
-          const v8bf bl = *reinterpret_cast<const v8bf*>(&bt_s[buf][1][off]);
-          acc[0][nb] = mfma_x3(ah[0], al[0], bh, bl, acc[0][nb]);
-          acc[1][nb] = mfma_x3(ah[1], al[1], bh, bl, acc[1][nb]);
+          bh[nb] = *reinterpret_cast<const v8bf*>(&bt_s[buf][0][off]);
+          bl[nb] = *reinterpret_cast<const v8bf*>(&bt_s[buf][1][off]);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[0], bh[nb], acc[0][nb], 0, 0, 0);
+          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[1], bh[nb], acc[1][nb], 0, 0, 0);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[0], bl[nb], acc[0][nb], 0, 0, 0);
+          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[1], bl[nb], acc[1][nb], 0, 0, 0);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[0], bh[nb], acc[0][nb], 0, 0, 0);
+          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[1], bh[nb], acc[1][nb], 0, 0, 0);
         }
       }
     }
@@ -636,13 +653,25 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
         bh[j] = tr_plane(yh, g, c, j * 16);
         bl[j] = tr_plane(yl, g, c, j * 16);
       }
+      v8bf ah[4], al[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const v8bf ah = tr_plane(xh, g, c, i * 16);
-        const v8bf al = tr_plane(xl, g, c, i * 16);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_x3(ah, al, bh[j], bl[j], acc[i][j]);
+        ah[i] = tr_plane(xh, g, c, i * 16);
+        al[i] = tr_plane(xl, g, c, i * 16);
       }
+      // one round per product over all 16 accumulators: no MFMA waits on the one before it
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
