@@ -298,13 +298,24 @@ int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const 
 int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mode, int dtype, st_stream_t stream);
 
 /*
+ * out[c] = sum over rows of Y[:, c] (Y (n, C) of `dtype`, fp32 sums, out of
+ * `out_dtype`): the bias gradient of a convolution, which the reference gets
+ * from autograd through its `out_feats += bias` (conv.py:227-228).  Two
+ * passes, each column's rows summed in a fixed order (deterministic).
+ * partials holds 1024 * C floats.
+ */
+int st_column_sum(const void* Y, int64_t n, int C, int dtype, float* partials, void* out, int out_dtype,
+                  st_stream_t stream);
+
+/*
  * Output-stationary gather-GEMM, the forward of ConvPrecomputedNeighborGEMM
  * (precomputed_fwd_kernel, implicit_precomputed_gemm.py:64-126) and, with the
  * transposed map, its input-gradient (precomputed_bwd_feat_kernel :129-177,
  * here a gather with no atomics):
- *   out[r, :] = sum over k of A[map(k, r), :] @ Bt[k]^T  (map < 0 or >= n_src adds 0)
- * A (n_src, Kd), Bt (K, Nd, Kd), out (n_dst, Nd), all of `dtype`, fp32
- * accumulation on MFMA.  map(k, r) = map[k * map_k_stride + r * map_r_stride]
+ *   out[r, :] = sum over k of A[map(k, r), :] @ Bt[k]^T (+ bias)  (map < 0 or >= n_src adds 0)
+ * A (n_src, Kd), Bt (K, Nd, Kd), bias (Nd, optional: NULL adds nothing; the
+ * reference's `out_feats += bias`, conv.py:227-228, fused into the store),
+ * out (n_dst, Nd), all of `dtype`, fp32 accumulation on MFMA.  map(k, r) = map[k * map_k_stride + r * map_r_stride]
  * and row_masks (n_dst, mask_words, optional) are indexed by destination row.
  * perm (optional) is the order destination rows are tiled in -- tile row t is
  * row perm[t] -- normally the mask-sorted order from st_kmap_sort_rows, so
@@ -313,8 +324,8 @@ int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mod
  * by that wave.
  */
 int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
-                   const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, void* out,
-                   int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
+                   const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, const void* bias,
+                   void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
 
 /*
  * st_gather_gemm over a tile plan (st_tile_plan built with the same perm):
@@ -324,8 +335,8 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
  * ST_F32_BF16X3) or 64 (ST_F32) return ST_ERR_UNSUPPORTED.
  */
 int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
-                         const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, void* out, int64_t n_dst,
-                         int K, int Kd, int Nd, int dtype, st_stream_t stream);
+                         const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, const void* bias,
+                         void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
 
 /*
  * Weight gradient of ConvPrecomputedNeighborGEMM (precomputed_bwd_weight_kernel,
@@ -384,7 +395,8 @@ typedef struct st_lookup {
  */
 int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int coord_dtype, int64_t n_dst,
                     const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,
-                    int64_t capacity, const void* Bt, void* out, int Kd, int Nd, int dtype, st_stream_t stream);
+                    int64_t capacity, const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype,
+                    st_stream_t stream);
 
 /*
  * Weight gradient of ConvHashOnTheFlyImplicitGEMM (implicit_gemm_bwd_weight_kernel,

@@ -89,10 +89,11 @@ _SIGNATURES = {
     "st_wgrad_pairs": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _L, _P, _I, _I, _I, _P, _P, _I, _P],
     "st_weight_prep": [_P, _P, _I, _I, _I, _I, _I, _P],
     "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],
-    "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
-    "st_gather_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _P, _P, _L, _I, _I, _I, _I, _P],
+    "st_column_sum": [_P, _L, _I, _I, _P, _P, _I, _P],
+    "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
+    "st_gather_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
     "st_wgrad": [_P, _L, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P, _L, _P, _I, _P],
-    "st_hashfly_gemm": [_P, _L, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _P, _P, _I, _I, _I, _P],
+    "st_hashfly_gemm": [_P, _L, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _P, _P, _P, _I, _I, _I, _P],
     "st_hashfly_wgrad": [_P, _L, _P, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _I, _I, _I, _P, _L, _P,
                          _I, _P],
 }

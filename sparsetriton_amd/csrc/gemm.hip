@@ -8,13 +8,13 @@ ST_GEMM_OPS(extern, __bf16)
 
 namespace st {
 int ops_gather_map_x3(const float* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs,
-                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, int64_t n_dst,
+                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst,
                       int K, int Kd, int Nd, hipStream_t stream);
 int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
                        const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const float* Bt,
-                       float* out, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
+                       float* out, const float* bias, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
 int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
-                        const int32_t* tmap, const float* Bt, float* out, int64_t n_dst, int K, int Kd, int Nd,
+                        const int32_t* tmap, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
                         hipStream_t stream);
 int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,
                        const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
@@ -46,22 +46,138 @@ using namespace st;
   }
 
 namespace st {
-// out[0 .. n) (16-bit units) = 0.
-__global__ __launch_bounds__(256) void zero_u16_kernel(uint16_t* __restrict__ p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+// out (rows x nd elements of U) = bias broadcast over the rows, or 0.
+template <typename U>
+__global__ __launch_bounds__(256) void fill_rows_kernel(U* __restrict__ out, int64_t n, int nd,
+                                                        const U* __restrict__ bias) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    out[i] = bias ? bias[i % nd] : (U)0;
 }
 }  // namespace st
 
-// A gather-GEMM with no source rows writes zero rows.  The kernels read a
-// clamped row 0 for every missing source, so they are not launched then (an
-// empty A may have no storage at all).
-static int zero_output(void* out, int64_t n_dst, int Nd, int dtype, hipStream_t stream) {
-  const int64_t n = n_dst * Nd * ((dtype == ST_F16 || dtype == ST_BF16) ? 1 : 2);
+// A gather-GEMM with no source rows writes its rows as the bias alone (or
+// zeros).  The kernels read a clamped row 0 for every missing source, so
+// they are not launched then (an empty A may have no storage at all).
+static int fill_output(void* out, int64_t n_dst, int Nd, int dtype, const void* bias, hipStream_t stream) {
+  const int64_t n = n_dst * Nd;
   const int64_t blocks = (n + 255) / 256;
-  st::zero_u16_kernel<<<(unsigned)(blocks < 65536 ? blocks : 65536), 256, 0, stream>>>((uint16_t*)out, n);
+  const unsigned g = (unsigned)(blocks < 65536 ? blocks : 65536);
+  if (dtype == ST_F16 || dtype == ST_BF16)
+    st::fill_rows_kernel<uint16_t><<<g, 256, 0, stream>>>((uint16_t*)out, n, Nd, (const uint16_t*)bias);
+  else
+    st::fill_rows_kernel<uint32_t><<<g, 256, 0, stream>>>((uint32_t*)out, n, Nd, (const uint32_t*)bias);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }
+
+namespace st {
+constexpr int kColSumBlocks = 1024;  // row ranges of the first pass (partials: kColSumBlocks x C fp32)
+
+// Pass 1: workgroup b sums rows [b n / G, (b + 1) n / G) of Y (n x C) into
+// partial[b][:] in a fixed order.  Vector path (C * sizeof(T) a multiple of
+// 16 bytes, at most 256 16-byte chunks per row): a thread owns one 16-byte
+// column chunk of every RPI-th row, four rows' loads in flight, and the RPI
+// row phases are summed in LDS.  Otherwise a thread owns a column.
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_partial_kernel(const T* __restrict__ Y, int64_t n, int C, int vec,
+                                                             float* __restrict__ partial) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  typedef T vec_t __attribute__((ext_vector_type(VEC)));
+  __shared__ float red[256 * VEC];
+  const int G = gridDim.x, tid = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * n / G, r1 = (int64_t)(blockIdx.x + 1) * n / G;
+  if (vec) {
+    const int tpr = C / VEC, rpi = 256 / tpr, q = tid % tpr, sub = tid / tpr;
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    if (sub < rpi) {
+      constexpr int U = 4;
+      int64_t r = r0 + sub;
+      for (; r + (U - 1) * rpi < r1; r += U * rpi) {
+        vec_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = *reinterpret_cast<const vec_t*>(Y + (r + u * rpi) * C + q * VEC);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] += (float)v[u][e];
+      }
+      for (; r < r1; r += rpi) {
+        const vec_t v = *reinterpret_cast<const vec_t*>(Y + r * C + q * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += (float)v[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[tid * VEC + e] = acc[e];
+    __syncthreads();
+    for (int col = tid; col < C; col += 256) {
+      const int cq = col / VEC, ce = col % VEC;
+      float t = 0.f;
+      for (int j = 0; j < rpi; ++j) t += red[(j * tpr + cq) * VEC + ce];
+      partial[(int64_t)blockIdx.x * C + col] = t;
+    }
+  } else {
+    for (int col = tid; col < C; col += 256) {
+      float s = 0.f;
+      int64_t r = r0;
+      for (; r + 7 < r1; r += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = (float)Y[(r + u) * C + col];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+      }
+      for (; r < r1; ++r) s += (float)Y[r * C + col];
+      partial[(int64_t)blockIdx.x * C + col] = s;
+    }
+  }
+}
+
+// Pass 2: workgroup c sums column c of the G partials: thread t takes
+// b = t, t + 256, ..., then a fixed-order tree over the threads.
+template <typename TO>
+__global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ partial, int G, int C,
+                                                           TO* __restrict__ out) {
+  __shared__ float red[256];
+  const int c = blockIdx.x, tid = threadIdx.x;
+  float s = 0.f;
+  for (int b = tid; b < G; b += 256) s += partial[(int64_t)b * C + c];
+  red[tid] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) out[c] = from_f32<TO>(red[0]);
+}
+
+template <typename T>
+static int column_sum(const T* Y, int64_t n, int C, float* partials, void* out, int out_dtype, hipStream_t stream) {
+  const int G = (int)(n < kColSumBlocks ? (n > 0 ? n : 1) : kColSumBlocks);
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int vec = C % VEC == 0 && C / VEC <= 256 && 256 % (C / VEC) == 0 && (uintptr_t)Y % 16 == 0;
+  colsum_partial_kernel<T><<<G, 256, 0, stream>>>(Y, n, C, vec, partials);
+  const unsigned g2 = (unsigned)C;
+  switch (out_dtype) {
+    case ST_F32:
+    case ST_F32_BF16X3:
+      colsum_final_kernel<float><<<g2, 256, 0, stream>>>(partials, G, C, (float*)out);
+      break;
+    case ST_F16:
+      colsum_final_kernel<_Float16><<<g2, 256, 0, stream>>>(partials, G, C, (_Float16*)out);
+      break;
+    case ST_BF16:
+      colsum_final_kernel<__bf16><<<g2, 256, 0, stream>>>(partials, G, C, (__bf16*)out);
+      break;
+    default:
+      return ST_ERR_UNSUPPORTED;
+  }
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+}  // namespace st
 
 static bool lookup_ok(const st_lookup* lk) {
   return lk && lk->K > 0 && lk->K <= ST_MAX_KVOL && lk->mul >= 1 && lk->div >= 1 && (lk->sign == 1 || lk->sign == -1);
@@ -69,43 +185,50 @@ static bool lookup_ok(const st_lookup* lk) {
 
 extern "C" {
 
+int st_column_sum(const void* Y, int64_t n, int C, int dtype, float* partials, void* out, int out_dtype,
+                  st_stream_t stream) {
+  if (n < 0 || C <= 0 || !partials || !out || (n > 0 && !Y)) return ST_ERR_ARG;
+  ST_DISPATCH_DTYPE(dtype, T, st::column_sum<T>((const T*)Y, n, C, partials, out, out_dtype, stream));
+}
+
 int st_weight_prep(const void* w, void* out, int K, int C_in, int C_out, int mode, int dtype, st_stream_t stream) {
   if (!w || !out || K <= 0 || C_in <= 0 || C_out <= 0 || mode < 0 || mode > 2) return ST_ERR_ARG;
   ST_DISPATCH_DTYPE(dtype, T, ops_weight_prep<T>((const T*)w, (T*)out, K, C_in, C_out, mode, stream));
 }
 
 int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
-                   const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, void* out,
+                   const uint32_t* row_masks, int mask_words, const int32_t* perm, const void* Bt, const void* bias, void* out,
                    int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream) {
   if (n_src < 0 || n_dst < 0 || K <= 0 || K > ST_MAX_KVOL || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
   if (n_dst >= (1ll << 31) || n_src >= (1ll << 31)) return ST_ERR_ARG;
   if (row_masks && mask_words != (K + 31) / 32) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
-  if (n_src == 0) return zero_output(out, n_dst, Nd, dtype, stream);
+  if (n_src == 0) return fill_output(out, n_dst, Nd, dtype, bias, stream);
   const int W = (K + 31) / 32;
   if (dtype == ST_F32_BF16X3)
     return ops_gather_map_x3((const float*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
-                             (const float*)Bt, (float*)out, n_dst, K, Kd, Nd, stream);
+                             (const float*)Bt, (float*)out, (const float*)bias, n_dst, K, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_map<T>((const T*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
-                                      (const T*)Bt, (T*)out, n_dst, K, Kd, Nd, stream));
+                                      (const T*)Bt, (T*)out, (const T*)bias, n_dst, K, Kd, Nd, stream));
 }
 
 int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
-                         const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, void* out, int64_t n_dst,
+                         const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, const void* bias, void* out,
+                         int64_t n_dst,
                          int K, int Kd, int Nd, int dtype, st_stream_t stream) {
   if (n_src < 0 || n_dst < 0 || K <= 0 || K > ST_MAX_KVOL || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
   if (n_dst >= (1ll << 31) || n_src >= (1ll << 31)) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!perm || !tile_nk || !tile_klist || !tile_map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
-  if (n_src == 0) return zero_output(out, n_dst, Nd, dtype, stream);
+  if (n_src == 0) return fill_output(out, n_dst, Nd, dtype, bias, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
-                               (float*)out, n_dst, K, Kd, Nd, stream);
+                               (float*)out, (const float*)bias, n_dst, K, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_tiled<T>((const T*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const T*)Bt,
-                                        (T*)out, n_dst, K, Kd, Nd, stream));
+                                        (T*)out, (const T*)bias, n_dst, K, Kd, Nd, stream));
 }
 
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,
@@ -138,18 +261,19 @@ int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, c
 
 int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int coord_dtype, int64_t n_dst,
                     const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,
-                    int64_t capacity, const void* Bt, void* out, int Kd, int Nd, int dtype, st_stream_t stream) {
+                    int64_t capacity, const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype,
+                    st_stream_t stream) {
   if (!lookup_ok(lk) || n_src < 0 || n_dst < 0 || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
   if (capacity <= 0 || capacity >= (1ll << 31) || n_dst >= (1ll << 31)) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!dst_coords || !offsets || !keys || !vals || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
-  if (n_src == 0) return zero_output(out, n_dst, Nd, dtype, stream);
+  if (n_src == 0) return fill_output(out, n_dst, Nd, dtype, bias, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_hash_x3((const float*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
-                              (const float*)Bt, (float*)out, n_dst, Kd, Nd, stream);
+                              (const float*)Bt, (float*)out, (const float*)bias, n_dst, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_hash<T>((const T*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
-                                       (const T*)Bt, (T*)out, n_dst, Kd, Nd, stream));
+                                       (const T*)Bt, (T*)out, (const T*)bias, n_dst, Kd, Nd, stream));
 }
 
 int st_hashfly_wgrad(const void* X, int64_t n_in, const void* dY, const void* out_coords, int coord_dtype,

@@ -5,7 +5,8 @@ Same signature, argument rules and results as the reference
 
 * cubic kernel, uniform stride / dilation / padding (``AssertionError`` otherwise);
 * submanifold forces padding ``(k-1)*d//2`` and excludes ``transposed``;
-* ``weight`` is (k^3, C_in, C_out); ``bias`` is added after the GEMM;
+* ``weight`` is (k^3, C_in, C_out); ``bias`` is added to the GEMM's output (fused into its store on
+  the precomputed path);
 * the coordinate hash table and, per geometry
   ``(k, s, p, d, submanifold, transposed)``, the output coordinates and kernel
   map are cached on the input's ``TensorCache``; a submanifold result shares
@@ -135,7 +136,7 @@ def sparse_conv3d(
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
         if out_coords.shape[0] == 0:
             return _empty(tensor, C_out, new_shape)
-        out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap)
+        out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap, bias)
         if hit is None and torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
             # the weight gradient's pair list on a side stream, queued after the forward (which
             # needs the tile plan first) and running alongside it
@@ -163,12 +164,12 @@ def sparse_conv3d(
         out_feats = ConvHashOnTheFlyImplicitGEMM.apply(
             tensor.F, weight, out_coords, offsets, in_table.table_keys, in_table.table_values, lookup_shape,
             1 if transposed else s, tensor.C, gl)
+        if bias is not None:
+            # in the features' dtype, as the reference's in-place `out_feats += bias` (conv.py:227-228);
+            # the precomputed path adds it inside the GEMM's store instead
+            out_feats = out_feats + bias.to(out_feats.dtype)
     else:
         raise ValueError(f"unknown convolution algorithm {algo}")
-
-    if bias is not None:
-        # in the features' dtype, as the reference's in-place `out_feats += bias` (conv.py:227-228)
-        out_feats = out_feats + bias.to(out_feats.dtype)
 
     if submanifold and (out_coords is tensor.C or (out_coords.shape == tensor.C.shape
                                                    and torch.equal(out_coords, tensor.C))):

@@ -52,7 +52,7 @@ def hashfly_gemm(A, dst_coords, offsets_i32, lk, keys, vals, Bt, n_dst):
     out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
     _lib.call("st_hashfly_gemm", _lib.ptr(A), A.shape[0], _lib.ptr(dst_coords), _lib.coord_code(dst_coords.dtype),
               n_dst, _lib.ptr(offsets_i32), ctypes.byref(lk), _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
-              _lib.ptr(Bt), _lib.ptr(out), Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+              _lib.ptr(Bt), None, _lib.ptr(out), Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
     return out
 
 

@@ -43,14 +43,14 @@ def _as_kmap(neighbor_indices, n_in: int) -> KernelMap:
 
 
 def gather_gemm(A: torch.Tensor, map_t: torch.Tensor, k_stride: int, r_stride: int, masks, Bt: torch.Tensor,
-                n_dst: int, K: int, rows=None) -> torch.Tensor:
-    """out[rows[r]] = sum_k A[map[k, r]] @ Bt[k]^T on the GPU (rows = identity when None)."""
+                n_dst: int, K: int, rows=None, bias=None) -> torch.Tensor:
+    """out[rows[r]] = sum_k A[map[k, r]] @ Bt[k]^T (+ bias) on the GPU (rows = identity when None)."""
     Kd = A.shape[1]
     Nd = Bt.shape[1]
     out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
     W = (K + 31) // 32
     _lib.call("st_gather_gemm", _lib.ptr(A), A.shape[0], _lib.ptr(map_t), k_stride, r_stride,
-              _lib.ptr(masks), W, _lib.ptr(rows), _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd,
+              _lib.ptr(masks), W, _lib.ptr(rows), _lib.ptr(Bt), _lib.ptr(bias), _lib.ptr(out), n_dst, K, Kd, Nd,
               _lib.compute_code(A.dtype), _lib.stream_of(A.device))
     return out
 
@@ -60,24 +60,25 @@ def tiled_ok(dtype: torch.dtype, Kd: int) -> bool:
     return Kd <= (64 if _lib.compute_code(dtype) == 0 else 128)
 
 
-def gather_gemm_tiled(A: torch.Tensor, tiles, Bt: torch.Tensor, n_dst: int, K: int) -> torch.Tensor:
-    """out[perm[t]] = sum over the tile's offsets of A[source] @ Bt[k]^T, over a tile plan."""
+def gather_gemm_tiled(A: torch.Tensor, tiles, Bt: torch.Tensor, n_dst: int, K: int, bias=None) -> torch.Tensor:
+    """out[perm[t]] = sum over the tile's offsets of A[source] @ Bt[k]^T (+ bias), over a tile plan."""
     Kd = A.shape[1]
     Nd = Bt.shape[1]
     out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
     _lib.call("st_gather_gemm_tiled", _lib.ptr(A), A.shape[0], _lib.ptr(tiles.perm), _lib.ptr(tiles.nk),
-              _lib.ptr(tiles.klist), _lib.ptr(tiles.tmap), _lib.ptr(Bt), _lib.ptr(out), n_dst, K, Kd, Nd,
-              _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+              _lib.ptr(tiles.klist), _lib.ptr(tiles.tmap), _lib.ptr(Bt), _lib.ptr(bias), _lib.ptr(out), n_dst, K,
+              Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
     return out
 
 
-def gather_gemm_fwd(A: torch.Tensor, kmap: KernelMap, Bt: torch.Tensor) -> torch.Tensor:
-    """Forward: out rows in the mask-sorted order of the forward plan, over its tile plan."""
+def gather_gemm_fwd(A: torch.Tensor, kmap: KernelMap, Bt: torch.Tensor, bias=None) -> torch.Tensor:
+    """Forward: out rows in the mask-sorted order of the forward plan, over its tile plan; ``bias``
+    (C_out, A's dtype) is added as the rows are stored."""
     if tiled_ok(A.dtype, A.shape[1]):
-        return gather_gemm_tiled(A, kmap.forward_tiles(), Bt, kmap.n_out, kmap.K)
+        return gather_gemm_tiled(A, kmap.forward_tiles(), Bt, kmap.n_out, kmap.K, bias=bias)
     plan = kmap.forward_plan()
     return gather_gemm(A, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, Bt, kmap.n_out, kmap.K,
-                       rows=plan.perm)
+                       rows=plan.perm, bias=bias)
 
 
 def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> torch.Tensor:
@@ -102,6 +103,16 @@ def weight_prep(weights: torch.Tensor, mode: int) -> torch.Tensor:
     out = torch.empty(shape, dtype=weights.dtype, device=weights.device)
     _lib.call("st_weight_prep", _lib.ptr(weights), _lib.ptr(out), K, C_in, C_out, mode,
               _lib.feat_code(weights.dtype), _lib.stream_of(weights.device))
+    return out
+
+
+def column_sum(Y: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """Sum over the rows of Y (n, C) with fp32 accumulation, in a fixed order (the bias gradient)."""
+    n, C = Y.shape
+    partials = torch.empty((1024 * C,), dtype=torch.float32, device=Y.device)
+    out = torch.empty((C,), dtype=out_dtype, device=Y.device)
+    _lib.call("st_column_sum", _lib.ptr(Y), n, C, _lib.feat_code(Y.dtype), _lib.ptr(partials), _lib.ptr(out),
+              _lib.feat_code(out_dtype), _lib.stream_of(Y.device))
     return out
 
 
@@ -135,7 +146,9 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
     """Sparse convolution with a precomputed neighbour map (gather-GEMM on MFMA)."""
 
     @staticmethod
-    def forward(ctx, features, weights, neighbor_indices):
+    def forward(ctx, features, weights, neighbor_indices, bias=None):
+        """The reference's three arguments, plus an optional ``bias`` (C_out) added in the GEMM's
+        store (the reference adds it afterwards, ``conv.py:227-228``)."""
         _lib.require_device(features, "features")
         N_in, C_in = features.shape
         K, C_in_w, C_out = weights.shape
@@ -145,9 +158,14 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
         features = features.contiguous()
         w = weights.to(features.dtype).contiguous()
         wt = weight_prep(w, _lib.W_TRANSPOSE)
-        out = gather_gemm_fwd(features, kmap, wt)
+        b = None
+        if bias is not None:
+            assert bias.shape == (C_out,), f"bias must have shape ({C_out},), got {tuple(bias.shape)}"
+            b = bias.to(features.dtype).contiguous()
+        out = gather_gemm_fwd(features, kmap, wt, bias=b)
         ctx.save_for_backward(features, weights)
         ctx.kmap = kmap
+        ctx.bias_dtype = None if bias is None else bias.dtype
         return out
 
     @staticmethod
@@ -162,4 +180,7 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
             grad_input = gather_gemm_dgrad(grad_output, kmap, w)
         if ctx.needs_input_grad[1]:
             grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
-        return grad_input, grad_weights, None
+        grad_bias = None
+        if ctx.bias_dtype is not None and len(ctx.needs_input_grad) > 3 and ctx.needs_input_grad[3]:
+            grad_bias = column_sum(grad_output, ctx.bias_dtype)
+        return grad_input, grad_weights, None, grad_bias

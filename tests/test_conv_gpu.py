@@ -348,3 +348,66 @@ def test_config2_full_size_properties(device):
         nbr = O.exact_kmap(c, c[rows], O.target_offsets(3, 1, 1, False), 1, shape)
         y_ref = O.fwd_f64(Xq.float().numpy(), Wq.float().numpy(), nbr)
         assert rel(y[rows].numpy(), y_ref) < tol
+
+
+# --------------------------------------------------------------- fused bias
+
+@pytest.mark.parametrize("algo", list(ConvAlgo))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cin,cout", [(16, 32), (64, 64), (256, 32), (20, 36)])
+def test_bias_vs_oracle(device, algo, dtype, cin, cout):
+    """out = conv + bias (the reference's `out_feats += bias`, conv.py:227-228; fused into the
+    GEMM's store on the precomputed path, tiled and untiled reductions alike), dbias = sum of dY."""
+    rng = np.random.default_rng(cin + 7 * cout)
+    c = _rand_coords(rng, 3000, 18)
+    X = torch.as_tensor(rng.standard_normal((3000, cin)).astype(np.float32)).to(dtype).float().numpy()
+    W = torch.as_tensor((rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cin)).astype(np.float32)).to(dtype)
+    b = torch.as_tensor(rng.standard_normal(cout).astype(np.float32)).to(dtype)
+    dY = torch.as_tensor(rng.standard_normal((3000, cout)).astype(np.float32)).to(dtype).float().numpy()
+    set_conv_algo(algo)
+    feats = torch.as_tensor(X, device=device).to(dtype).requires_grad_(True)
+    w = W.to(device).requires_grad_(True)
+    bias = b.to(device).requires_grad_(True)
+    sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=(18, 18, 18))
+    out = sparse_conv3d(sp, w, 3, bias=bias)
+    out.F.backward(torch.as_tensor(dY, device=device).to(dtype))
+    y, gx, gw = _oracle(c, c, (18, 18, 18), X, W.float().numpy(), dY, 3, 1, 1, 1, False)
+    y = y + b.float().numpy()[None, :]
+    tol = TOL[dtype]
+    assert rel(out.F.detach().float().cpu(), y) < tol
+    assert rel(feats.grad.float().cpu(), gx) < tol
+    assert rel(w.grad.float().cpu(), gw) < tol
+    assert bias.grad.dtype == dtype
+    assert rel(bias.grad.float().cpu(), dY.sum(0)) < tol
+
+
+def test_bias_without_sources(device):
+    """A gather with no source rows stores the bias broadcast over its rows."""
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import gather_gemm, gather_gemm_tiled
+    from sparsetriton_amd.nn.functional.conv.kmap import TileMap, TilePlan
+    K, n_dst = 27, 300
+    nbr = torch.full((K, n_dst), -1, dtype=torch.int32, device=device)
+    masks = torch.zeros((n_dst, 1), dtype=torch.int32, device=device)
+    perm = TilePlan.build(n_dst, K, masks).perm
+    tiles = TileMap.build(nbr, n_dst, 1, masks, K, perm, n_dst, 0)
+    for dt in (torch.float32, torch.bfloat16):
+        A = torch.empty((0, 64), dtype=dt, device=device)
+        Bt = torch.randn((K, 48, 64), device=device).to(dt)
+        b = torch.randn(48, device=device).to(dt)
+        for out in (gather_gemm_tiled(A, tiles, Bt, n_dst, K, bias=b),
+                    gather_gemm(A, nbr, n_dst, 1, masks, Bt, n_dst, K, bias=b)):
+            assert torch.equal(out, b[None, :].expand(n_dst, 48))
+
+
+@pytest.mark.parametrize("n,C", [(0, 16), (1, 7), (1000, 64), (470_532, 64), (3001, 300), (50_000, 128)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_column_sum(device, n, C, dtype):
+    """st_column_sum (the bias gradient) against a float64 sum, and bitwise repeatable."""
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import column_sum
+    Y = torch.randn((n, C), device=device).to(dtype)
+    s = column_sum(Y, torch.float32)
+    ref = Y.double().sum(0).cpu()
+    err = (s.double().cpu() - ref).abs().max().item() if n else s.abs().max().item()
+    assert err <= 1e-5 * max(1.0, n ** 0.5) * 4
+    assert torch.equal(s, column_sum(Y, torch.float32))
+    assert column_sum(Y, dtype).dtype == dtype

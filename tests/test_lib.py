@@ -38,5 +38,5 @@ def test_version_and_arg_checks():
     assert lib.st_version().startswith(b"sparsetriton_amd")
     # argument validation runs on the host: no device memory is touched
     assert lib.st_hash_insert(None, 0, 5, 1, None, None, 10, None, None) == -1
-    assert lib.st_gather_gemm(None, 0, None, 0, 0, None, 1, None, None, None, 0, 0, 8, 8, 0, None) == -1
+    assert lib.st_gather_gemm(None, 0, None, 0, 0, None, 1, None, None, None, None, 0, 0, 8, 8, 0, None) == -1
     assert lib.st_weight_prep(None, None, 27, 4, 4, 0, 0, None) == -1
