@@ -139,7 +139,10 @@ EXTRA = {
                 3, 1, 1, False, True, "bf16", "precomputed"),
     "config5-hashfly": ("SubMConv3D 128->128 k3, same set (ImplicitHashFlyGEMM)", 128, 128, 3, 1, 1, False, True,
                         "bf16", "hashfly"),
+    "config2-bias": ("SubMConv3D 64->64 k3 with bias (the module default), config-2 set", 64, 64, 3, 1, 1, False,
+                     True, "f32", "precomputed"),
 }
+WITH_BIAS = {"config2-bias"}
 
 
 def run_extra(args):
@@ -174,6 +177,9 @@ def run_extra(args):
     X = torch.randn(N, Cin, generator=g).to(dev, dtype)
     bound = 1.0 / np.sqrt(Cin * k ** 3)
     W = ((torch.rand(k ** 3, Cin, Cout, generator=g) * 2 - 1) * bound).to(dev, dtype).requires_grad_(True)
+    b = None
+    if args.workload in WITH_BIAS:
+        b = ((torch.rand(Cout, generator=g) * 2 - 1) * bound).to(dev, dtype).requires_grad_(True)
 
     def fresh():
         feats = X.clone().requires_grad_(True)
@@ -182,7 +188,7 @@ def run_extra(args):
     def build():
         # a new coordinate set: table, kernel map (or hash-fly lookups) and all plans
         feats, sp = fresh()
-        out = sparse_conv3d(sp, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)
+        out = sparse_conv3d(sp, W, k, bias=b, stride=s, padding=p, transposed=tr, submanifold=subm)
         return sp, out
 
     # map build = first call's extra time over a cached call, both fwd only
@@ -204,7 +210,9 @@ def run_extra(args):
     def step():
         feats.grad = None
         W.grad = None
-        o = sparse_conv3d(sp, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)
+        if b is not None:
+            b.grad = None
+        o = sparse_conv3d(sp, W, k, bias=b, stride=s, padding=p, transposed=tr, submanifold=subm)
         o.F.backward(dY)
 
     for _ in range(args.warmup):
