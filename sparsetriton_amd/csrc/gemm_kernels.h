@@ -339,6 +339,29 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     }
 }
 
+// Row tile and column tile of a ring-kernel workgroup.  With one column tile
+// the grid is the row tiles in order.  With several, the grid is 1-D over
+// (row tiles rounded up to a multiple of 8) x (column tiles), and the column
+// tiles of one row tile are consecutive workgroups of one XCD (the hardware
+// deals workgroups to the 8 XCDs round-robin by id), so the A rows they all
+// gather come into that XCD's L2 once.  Row tiles past the end are padding.
+struct RingTile {
+  int64_t rt;
+  int ct;
+};
+__device__ __forceinline__ RingTile ring_tile(int Nd, int BN) {
+  const int ncol = (Nd + BN - 1) / BN;
+  const int64_t b = blockIdx.x;
+  if (ncol == 1) return RingTile{b, 0};
+  const int64_t s = b >> 3;
+  return RingTile{(s / ncol) * 8 + (b & 7), (int)(s % ncol)};
+}
+// Grid of the ring kernels for n_dst rows and Nd columns in BN-wide tiles.
+static inline unsigned ring_grid(int64_t n_dst, int Nd, int BN) {
+  const int64_t rt = (n_dst + kGemmBM - 1) / kGemmBM, ncol = (Nd + BN - 1) / BN;
+  return (unsigned)(ncol == 1 ? rt : ((rt + 7) / 8) * 8 * ncol);
+}
+
 // ------------------------------------------ gather-GEMM, D-deep load ring
 //
 // As gather_gemm_pipe_kernel, but the A rows and the B tile of an offset are
@@ -388,16 +411,18 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
-  const int n0 = blockIdx.y * BN;
+  const RingTile tile = ring_tile(Nd, BN);
+  if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
+  const int64_t row0 = tile.rt * kGemmBM;
+  const int n0 = tile.ct * BN;
 
   if (tid < kGemmBM) {
     const int64_t r = row0 + tid;
     drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
   }
   if constexpr (Src::kTiled) {
-    const int nkt = src.nk[blockIdx.x];
-    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[(int64_t)blockIdx.x * src.K + j];
+    const int nkt = src.nk[tile.rt];
+    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[tile.rt * src.K + j];
     if (tid == 0) nk_s = nkt;
   } else {
     if (tid < W) tmask_s[tid] = 0;
@@ -435,7 +460,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     for (int j = tid >> 7; j < ng; j += 2) {
       int32_t v;
       if constexpr (Src::kTiled)
-        v = src.get_tile(blockIdx.x, g0 + j, tid & (kGemmBM - 1));
+        v = src.get_tile(tile.rt, g0 + j, tid & (kGemmBM - 1));
       else
         v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
       if ((int64_t)v >= n_src) v = -1;
@@ -616,6 +641,28 @@ __device__ __forceinline__ ChunkRange chunk_range(int total) {
   const int G = gridDim.x;
   const int L = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
   return ChunkRange{(int)((int64_t)L * total / G), (int)((int64_t)(L + 1) * total / G)};
+}
+
+// Chunk range and channel tile of a workgroup in a 1-D grid of G x ntiles
+// workgroups.  Consecutive workgroups of one XCD (blockIdx mod 8) take the
+// ntiles channel tiles of one chunk range, so the rows they all read come into
+// that XCD's L2 once; as in chunk_range, each XCD takes a contiguous run of
+// ranges.
+struct ChunkTile {
+  int q0, q1, tile;
+};
+__device__ __forceinline__ ChunkTile chunk_tile(int total, int ntiles) {
+  const int b = (int)blockIdx.x, G = (int)gridDim.x / ntiles;
+  int L, t;
+  if (G % 8 == 0) {
+    const int s = b >> 3;
+    L = (b & 7) * (G / 8) + s / ntiles;
+    t = s % ntiles;
+  } else {
+    L = b / ntiles;
+    t = b % ntiles;
+  }
+  return ChunkTile{(int)((int64_t)L * total / G), (int)((int64_t)(L + 1) * total / G), t};
 }
 
 __device__ __forceinline__ int chunk_offset(const int32_t* cstart_s, int K, int c) {
@@ -860,7 +907,7 @@ __device__ __forceinline__ F tr_frag(const T* st, int g, int c, int col0) {
 }
 
 template <typename T, bool BUF>  // BUF: row loads through buffer resources (X and dY under 2 GB)
-__global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
+__global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
                                                                const int32_t* __restrict__ kstart,
                                                                const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
@@ -871,7 +918,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
   constexpr int STAGE = 32 * kWvPitch;  // elements per operand per wave
   constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(T);
   constexpr int RP = 68;                // row pitch (floats) of the per-wave tiles summed at the end
-  constexpr int RED_BYTES = 4 * 64 * RP * (int)sizeof(float);
+  constexpr int RED_BYTES = 4 * 32 * RP * (int)sizeof(float);  // half a tile per wave at a time
   __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -881,7 +928,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
   const int total = cstart_s[K];
 
   const int ntn = Cout / 64;
-  const int cm0 = (blockIdx.z / ntn) * 64, cn0 = (blockIdx.z % ntn) * 64;
+  const ChunkTile ct = chunk_tile(total, (Cin / 64) * ntn);
+  const int cm0 = (ct.tile / ntn) * 64, cn0 = (ct.tile % ntn) * 64;
   T* xs = reinterpret_cast<T*>(lds) + wid * 2 * STAGE;
   T* ys = xs + STAGE;
   float* red = reinterpret_cast<float*>(lds);
@@ -894,8 +942,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * (int64_t)sizeof(T) : 0);
   const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, BUF ? n_out * Cout * (int64_t)sizeof(T) : 0);
 
-  const ChunkRange cr = chunk_range(total);
-  for (int cq = cr.q0; cq < cr.q1; ++cq) {
+  for (int cq = ct.q0; cq < ct.q1; ++cq) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
@@ -950,25 +997,29 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_wave_kernel(const T* __res
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    // sum the four waves' tiles through LDS; every thread then adds and stores
-    // 16 elements of the 64 x 64 partial, row-contiguous
-    __syncthreads();
-    float* mine = red + wid * 64 * RP;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * RP + j * 16 + c] = acc[i][j][r];
-    __syncthreads();
+    // sum the four waves' tiles through LDS, 32 rows at a time (so the sum
+    // area fits in the staging area); every thread then adds and stores 8
+    // elements of each half of the 64 x 64 partial, row-contiguous
     float* part = partials + (int64_t)cidx * Cin * Cout;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __syncthreads();
+      float* mine = red + wid * 32 * RP;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * RP + j * 16 + c] = acc[h * 2 + i][j][r];
+      __syncthreads();
 #pragma unroll 4
-    for (int m = 0; m < 16; ++m) {
-      const int e = tid + m * 256;
-      const int row = e >> 6, col = e & 63;
-      const float s = red[row * RP + col] + red[64 * RP + row * RP + col] + red[128 * RP + row * RP + col] +
-                      red[192 * RP + row * RP + col];
-      part[(int64_t)(cm0 + row) * Cout + cn0 + col] = s;
+      for (int m = 0; m < 8; ++m) {
+        const int e = tid + m * 256;
+        const int row = e >> 6, col = e & 63;
+        const float s = red[row * RP + col] + red[32 * RP + row * RP + col] + red[64 * RP + row * RP + col] +
+                        red[96 * RP + row * RP + col];
+        part[(int64_t)(cm0 + h * 32 + row) * Cout + cn0 + col] = s;
+      }
     }
     __syncthreads();
   }
@@ -1179,14 +1230,15 @@ static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_
                         const T* Bt, T* out, const T* bias, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
+  const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   // (IEEE fp32 keeps the register path: its MFMAs dominate and the A stage only costs occupancy there)
   if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2 &&
       buffer_ok(n_src, K, Kd, Nd, sizeof(T)))
     gather_gemm_ring_kernel<T, BN, KS, 2, Src, true>
-        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
   else if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)
     gather_gemm_ring_kernel<T, BN, KS, 2, Src, false>
-        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
   else
     gather_gemm_pipe_kernel<T, BN, KS, Src>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
@@ -1201,7 +1253,7 @@ static void launch_pipe_ks(const T* A, int64_t n_src, const Src& src, const uint
     launch_pipe<T, 16, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if (Nd <= 32)
     launch_pipe<T, 32, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
-  else if (Nd <= 64 || LDS128 > 65536)
+  else if (Nd <= 64 || LDS128 > 65536)  // (a 128-wide tile at KS = 4 costs occupancy more than its gathers save)
     launch_pipe<T, 64, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if constexpr (LDS128 <= 65536)
     launch_pipe<T, 128, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
@@ -1354,12 +1406,12 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
       const int2* pr = reinterpret_cast<const int2*>(pairs);
       const int mode = wgrad16_mode();
       if (mode == 0 && Cin % 64 == 0 && Cout % 64 == 0 && vec_x && vec_y) {
-        const unsigned gz64 = (unsigned)((Cin / 64) * (Cout / 64));
+        const unsigned grid = gx * (unsigned)((Cin / 64) * (Cout / 64));
         if (rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T)))
-          wgrad_pairs_wave_kernel<T, true><<<dim3(gx, 1, gz64), 256, 0, stream>>>(
+          wgrad_pairs_wave_kernel<T, true><<<grid, 256, 0, stream>>>(
               X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
         else
-          wgrad_pairs_wave_kernel<T, false><<<dim3(gx, 1, gz64), 256, 0, stream>>>(
+          wgrad_pairs_wave_kernel<T, false><<<grid, 256, 0, stream>>>(
               X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
         ST_CHECK_LAUNCH();
         return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);

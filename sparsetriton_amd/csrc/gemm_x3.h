@@ -289,16 +289,18 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int64_t row0 = (int64_t)blockIdx.x * kGemmBM;
-  const int n0 = blockIdx.y * BN;
+  const RingTile tile = ring_tile(Nd, BN);
+  if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
+  const int64_t row0 = tile.rt * kGemmBM;
+  const int n0 = tile.ct * BN;
 
   if (tid < kGemmBM) {
     const int64_t r = row0 + tid;
     drow_s[tid] = r < n_dst ? (rows ? rows[r] : (int32_t)r) : -1;
   }
   if constexpr (Src::kTiled) {
-    const int nkt = src.nk[blockIdx.x];
-    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[(int64_t)blockIdx.x * src.K + j];
+    const int nkt = src.nk[tile.rt];
+    for (int j = tid; j < nkt; j += 256) klist_s[j] = src.klist[tile.rt * src.K + j];
     if (tid == 0) nk_s = nkt;
   } else {
     if (tid < W) tmask_s[tid] = 0;
@@ -336,7 +338,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
     for (int j = tid >> 7; j < ng; j += 2) {
       int32_t v;
       if constexpr (Src::kTiled)
-        v = src.get_tile(blockIdx.x, g0 + j, tid & (kGemmBM - 1));
+        v = src.get_tile(tile.rt, g0 + j, tid & (kGemmBM - 1));
       else
         v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
       if ((int64_t)v >= n_src) v = -1;
@@ -597,7 +599,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   const int total = cstart_s[K];
 
   const int ntn = Cout / 64;
-  const int cm0 = (blockIdx.z / ntn) * 64, cn0 = (blockIdx.z % ntn) * 64;
+  const ChunkTile ct = chunk_tile(total, (Cin / 64) * ntn);
+  const int cm0 = (ct.tile / ntn) * 64, cn0 = (ct.tile % ntn) * 64;
   __bf16* xh = reinterpret_cast<__bf16*>(lds) + wid * 4 * STAGE;
   __bf16* xl = xh + STAGE;
   __bf16* yh = xl + STAGE;
@@ -607,8 +610,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * 4 : 0);
   const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, BUF ? n_out * Cout * 4 : 0);
 
-  const ChunkRange cr = chunk_range(total);
-  for (int cq = cr.q0; cq < cr.q1; ++cq) {
+  for (int cq = ct.q0; cq < ct.q1; ++cq) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
@@ -720,12 +722,13 @@ static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint3
                       const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
+  const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines() && buffer_ok(n_src, K, Kd, Nd, 4))
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true>
-        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, bias);
   else if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, false>
-        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, bias);
   else
     gather_gemm_x3_kernel<BN, KS, Src>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);

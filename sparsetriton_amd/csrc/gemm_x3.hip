@@ -40,14 +40,14 @@ int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_
                                   Cout, partials, dW, dw_dtype, stream);
   if (max_chunks > 0) {
     const unsigned gx = wgrad_grid(max_chunks);
-    const unsigned gz = (unsigned)((Cin / 64) * (Cout / 64));
+    const unsigned grid = gx * (unsigned)((Cin / 64) * (Cout / 64));
     const int2* pr = reinterpret_cast<const int2*>(pairs);
     if (rows_fit_buffer(n_in, Cin, n_out, Cout, 4))
-      wgrad_pairs_x3_kernel<true><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk,
-                                                                       Cin, Cout, n_in, n_out, partials);
+      wgrad_pairs_x3_kernel<true><<<grid, 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
+                                                            Cout, n_in, n_out, partials);
     else
-      wgrad_pairs_x3_kernel<false><<<dim3(gx, 1, gz), 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K,
-                                                                        chunk, Cin, Cout, n_in, n_out, partials);
+      wgrad_pairs_x3_kernel<false><<<grid, 256, 0, stream>>>(X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin,
+                                                             Cout, n_in, n_out, partials);
     ST_CHECK_LAUNCH();
   }
   return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
