@@ -245,6 +245,110 @@ def run_extra(args):
     print(json.dumps(line), flush=True)
 
 
+def run_resnet(args):
+    """SparseResNet21D (reference nn/backbones/resnet.py:81-109) forward + backward on the config-2
+    voxel set with 4 input channels: 13 convolutions (4 strided), 13 per-sample batch norms with
+    their ReLU / residual add fused, one JSON line.  A step takes a new SparseTensor over the same
+    coordinates, so every kernel map, tile plan and pair list is rebuilt inside the step, as in a
+    training loop over new scans; the step with the maps cached is logged beside it."""
+    import torch
+
+    from sparsetriton_amd import SparseTensor, workloads
+    from sparsetriton_amd.config import set_fp32_precision
+    from sparsetriton_amd.nn import SparseConv3DBase, SparseResNet21D
+
+    set_fp32_precision(args.fp32_precision)
+    dev = torch.device("cuda:0")
+    dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
+    seed = 0
+    torch.manual_seed(seed)
+    coords_np, shape = workloads.config2(seed=seed)
+    coords = torch.as_tensor(coords_np, device=dev).to(torch.int16)
+    N = coords.shape[0]
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    X = torch.randn(N, 4, generator=g).to(dev, dtype)
+    model = SparseResNet21D(in_channels=4).to(dev)
+    convs = [m for m in model.modules() if isinstance(m, SparseConv3DBase)]
+    for m in convs:
+        m.to(dtype)  # batch-norm parameters and statistics stay fp32
+
+    # useful flops: 2 P C_in C_out per pass; forward, input gradient (not for the first layer,
+    # whose input is data) and weight gradient
+    pairs = {}
+
+    def hook(mod, inputs, output):
+        t = inputs[0]
+        k, s, d = mod.kernel_size[0], mod.stride[0], mod.dilation[0]
+        p = ((k - 1) * d) // 2 if mod.subm else mod.padding[0]
+        km = t._cache.neighbor_indices[(k, s, p, d, mod.subm, mod.transposed)][1]
+        pairs[id(mod)] = km.num_pairs()
+
+    hs = [m.register_forward_hook(hook) for m in convs]
+    with torch.no_grad():
+        outs = model(SparseTensor(X, coords, spatial_shape=shape, batch_size=4))
+    for h in hs:
+        h.remove()
+    flops = sum(2.0 * pairs[id(m)] * m.in_channels * m.out_channels * (2 if i == 0 else 3)
+                for i, m in enumerate(convs))
+    grads = [torch.randn(tuple(o.F.shape), generator=g).to(dev, dtype) for o in outs]
+    voxels = [int(o.F.shape[0]) for o in outs]
+    del outs
+
+    def step(sp):
+        model.zero_grad(set_to_none=True)
+        outs = model(sp)
+        torch.autograd.backward([o.F for o in outs], grads)
+
+    def timed(make, steps):
+        for _ in range(args.warmup):
+            step(make())
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step(make())
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(lambda: SparseTensor(X, coords, spatial_shape=shape, batch_size=4), args.steps)
+    cached = SparseTensor(X, coords, spatial_shape=shape, batch_size=4)
+    ms_cached = timed(lambda: cached, args.steps)
+
+    # inference: evaluation mode under no_grad, where each block's batch norm, residual add and
+    # ReLU run in its convolutions' GEMM stores (maps cached)
+    model.eval()
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(cached)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            model(cached)
+        e1.record()
+        torch.cuda.synchronize()
+    ms_infer = e0.elapsed_time(e1) / args.steps
+    model.train()
+    value = flops / (ms * 1e-3) / 1e12
+    log(f"resnet21d {args.dtype}: N={N}, stage voxels {voxels}; step {ms:.3f} ms with map builds "
+        f"({value:.2f} TFLOP/s), {ms_cached:.3f} ms with maps cached ({flops / (ms_cached * 1e-3) / 1e12:.2f}); "
+        f"inference forward (eval, fused epilogues) {ms_infer:.3f} ms")
+    line = {
+        "metric": METRIC, "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.dtype,
+        "fp32_precision": args.fp32_precision if args.dtype == "f32" else None,
+        "data": "synthetic (seeded LiDAR-like voxel set, N(0,1) features, random-init weights)",
+        "config": {"workload": "resnet21d: SparseResNet21D(in_channels=4) fwd+bwd, config-2 voxel set, B=4, "
+                               "maps rebuilt every step", "voxels": N, "stage_voxels": voxels,
+                   "useful_flops_per_step": flops, "seed": seed},
+        "ms_per_step_maps_cached": ms_cached,
+        "inference_forward_ms_maps_cached": ms_infer,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,7 +359,7 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="short run for counter collection: few repetitions, plus a 256 MiB device copy whose "
                          "HBM counters calibrate the per-kernel traffic figures")
-    ap.add_argument("--workload", choices=["config2"] + sorted(EXTRA), default="config2",
+    ap.add_argument("--workload", choices=["config2", "resnet21d"] + sorted(EXTRA), default="config2",
                     help="config2 is the headline; the others measure BASELINE's other configurations")
     ap.add_argument("--fp32-precision", choices=["bf16x3", "ieee"], default="bf16x3",
                     help="fp32 matrix-core arithmetic (split-bf16 MFMA, the default, or IEEE fp32 MFMA)")
@@ -264,7 +368,7 @@ def main():
         if args.gpus != 1:
             print("bench.py: one GPU only", file=sys.stderr)
             sys.exit(2)
-        return run_extra(args)
+        return run_resnet(args) if args.workload == "resnet21d" else run_extra(args)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
               "the sparse-convolution path is not sharded across GPUs here", file=sys.stderr)

@@ -339,6 +339,22 @@ int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, cons
                          void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
 
 /*
+ * st_gather_gemm_tiled with the store epilogue of an evaluation-mode conv +
+ * batch norm (+ residual) + ReLU block (nn/modules/blocks.py:21-124,
+ * norm.py:105-112 with the running statistics):
+ *   out[r, c] = act((sum + bias[c]) * scale[c] + shift[c] + residual[r, c])
+ * bias and residual (n_dst x Nd, output rows) of `dtype`; scale, shift fp32
+ * (Nd); NULL drops a term (shift needs scale); relu 0 / 1.  With
+ * scale = weight / sqrt(running_var + eps) and
+ * shift = beta - running_mean * scale this is the block's output in one pass.
+ */
+int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
+                                  const int16_t* tile_klist, const int32_t* tile_map, const void* Bt,
+                                  const void* bias, const float* scale, const float* shift, const void* residual,
+                                  int relu, void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype,
+                                  st_stream_t stream);
+
+/*
  * Weight gradient of ConvPrecomputedNeighborGEMM (precomputed_bwd_weight_kernel,
  * implicit_precomputed_gemm.py:180-230):
  *   dW[k] = sum over o with map(k, o) >= 0 of X[map(k, o)]^T @ dY[o]
@@ -408,6 +424,45 @@ int st_hashfly_wgrad(const void* X, int64_t n_in, const void* dY, const void* ou
                      const int32_t* offsets, const st_lookup* lk, const uint64_t* keys, const uint32_t* vals,
                      int64_t capacity, int C_in, int C_out, int dtype, float* partials, int64_t splits, void* dW,
                      int dw_dtype, st_stream_t stream);
+
+/* ------------------------------------------------------------ batch norm
+ *
+ * Per-sample batch normalisation of sparse features (sparse_batch_norm,
+ * nn/functional/norm.py:20-112) with the residual add and ReLU of the
+ * reference's blocks (nn/modules/blocks.py:21-124) fused into its output pass:
+ *   out = act((Y - mean[b, c]) * invstd[b, c] * weight[c] + bias[c] + residual)
+ * b = coords[r, 0] (rows with b outside [0, B) are written as zeros and left
+ * out of the statistics).  Training: mean and biased variance of each sample's
+ * rows (two passes, deterministic sums), running statistics (when given) move
+ * by `momentum` towards their mean over the B samples (norm.py:86-90).
+ * Evaluation: mean = running_mean, var = running_var, per channel.
+ * Y, residual (optional), out: (n, C) of `dtype`; weight, bias (optional:
+ * NULL means 1 and 0), running statistics: fp32 (C); mean, invstd: fp32
+ * (B, C) in training, (C) in evaluation; counts: int32 (B), rows per sample.
+ */
+#define ST_BN_MAX_BATCH 4096
+int st_bn_workspace(int64_t n, int C, int B, int64_t* floats);
+int st_bn_forward(const void* Y, int64_t n, int C, int dtype, const void* coords, int coord_dtype, int B,
+                  const float* weight, const float* bias, const void* residual, int relu, int training, float eps,
+                  float momentum, float* running_mean, float* running_var, float* mean, float* invstd,
+                  int32_t* counts, float* workspace, int64_t workspace_floats, void* out, st_stream_t stream);
+
+/*
+ * Gradients of st_bn_forward (the reference gets them from torch autograd
+ * through its formula, including the paths through the sample mean and
+ * variance): with g = dout masked by out > 0 under relu,
+ *   dres = g (optional), dweight[c] = sum g * xhat, dbias[c] = sum g (fp32, optional),
+ *   training:   dY = weight * invstd * (g - mean_b(g) - xhat * mean_b(g * xhat))
+ *   evaluation: dY = weight * invstd * g
+ * xhat = (Y - mean) * invstd.  Y and out are the forward's input and output
+ * (out is read only under relu, and may be NULL otherwise); mean, invstd and
+ * counts its saved statistics.  The workspace is
+ * st_bn_workspace(n, C, training ? B : 1) floats.
+ */
+int st_bn_backward(const void* Y, const void* out, const void* dout, int64_t n, int C, int dtype, const void* coords,
+                   int coord_dtype, int B, const float* weight, int relu, int training, const float* mean,
+                   const float* invstd, const int32_t* counts, float* workspace, int64_t workspace_floats, void* dY,
+                   void* dres, float* dweight, float* dbias, st_stream_t stream);
 
 #ifdef __cplusplus
 }

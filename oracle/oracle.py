@@ -275,3 +275,80 @@ def dense_conv_at(in_coords, feats, weight, kernel_size, stride, padding, dilati
         y = F.conv3d(dense, wt, stride=stride, padding=padding, dilation=dilation)
     oc = torch.as_tensor(np.asarray(out_coords), dtype=torch.long)
     return y[oc[:, 0], :, oc[:, 1], oc[:, 2], oc[:, 3]].numpy()
+
+
+# ------------------------------------------------------------ batch norm
+
+def batch_norm_f64(feats, batch_idx, B, weight=None, bias=None, running_mean=None, running_var=None, training=True,
+                   eps=1e-5, momentum=0.1, residual=None, relu=False):
+    """Per-sample batch norm (nn/functional/norm.py:66-112) followed by the blocks' residual add and
+    ReLU (nn/modules/blocks.py:121-124), float64, one loop per sample.
+
+    Training: each sample's rows are normalised by their own mean and biased variance (sum of centred
+    squares over the count, the count clamped to 1); the running statistics become
+    (1 - momentum) * running + momentum * (mean over the B samples).  Evaluation: the running statistics.
+    Returns (out, running_mean', running_var')."""
+    x = np.asarray(feats, dtype=np.float64)
+    bi = np.asarray(batch_idx, dtype=np.int64)
+    C = x.shape[1]
+    w = np.ones(C) if weight is None else np.asarray(weight, dtype=np.float64)
+    bb = np.zeros(C) if bias is None else np.asarray(bias, dtype=np.float64)
+    rm = None if running_mean is None else np.asarray(running_mean, dtype=np.float64)
+    rv = None if running_var is None else np.asarray(running_var, dtype=np.float64)
+    if training:
+        mean = np.zeros((B, C))
+        var = np.zeros((B, C))
+        for b in range(B):
+            rows = x[bi == b]
+            cnt = max(rows.shape[0], 1)
+            mean[b] = rows.sum(0) / cnt
+            var[b] = ((rows - mean[b]) ** 2).sum(0) / cnt
+        if rm is not None:
+            rm = (1 - momentum) * rm + momentum * mean.mean(0)
+        if rv is not None:
+            rv = (1 - momentum) * rv + momentum * var.mean(0)
+        m_rows, v_rows = mean[bi], var[bi]
+    else:
+        m_rows, v_rows = rm[None, :], rv[None, :]
+    out = (x - m_rows) / np.sqrt(v_rows + eps) * w + bb
+    if residual is not None:
+        out = out + np.asarray(residual, dtype=np.float64)
+    if relu:
+        out = np.maximum(out, 0.0)
+    return out, rm, rv
+
+
+def batch_norm_grads_f64(feats, batch_idx, B, weight, bias, running_mean, running_var, training, dout, eps=1e-5,
+                         residual=None, relu=False):
+    """(dfeats, dweight, dbias, dresidual) of batch_norm_f64 by torch autograd in float64 on the CPU,
+    with the normalisation done by the library routine torch.nn.functional.batch_norm applied sample by
+    sample (training) or with the running statistics (evaluation), in place of the reference's
+    index_add formulation."""
+    import torch
+    import torch.nn.functional as F
+
+    x = torch.tensor(np.asarray(feats, dtype=np.float64), requires_grad=True)
+    bi = torch.as_tensor(np.asarray(batch_idx, dtype=np.int64))
+    C = x.shape[1]
+    w = torch.tensor(np.ones(C) if weight is None else np.asarray(weight, dtype=np.float64), requires_grad=True)
+    b = torch.tensor(np.zeros(C) if bias is None else np.asarray(bias, dtype=np.float64), requires_grad=True)
+    res = None
+    if residual is not None:
+        res = torch.tensor(np.asarray(residual, dtype=np.float64), requires_grad=True)
+    if training:
+        xh = torch.zeros_like(x)
+        for s in range(B):
+            rows = (bi == s).nonzero().flatten()
+            if rows.numel():
+                xh = xh.index_copy(0, rows, F.batch_norm(x[rows], None, None, training=True, eps=eps))
+    else:
+        rm = torch.as_tensor(np.asarray(running_mean, dtype=np.float64))
+        rv = torch.as_tensor(np.asarray(running_var, dtype=np.float64))
+        xh = F.batch_norm(x, rm, rv, training=False, eps=eps)
+    out = xh * w + b
+    if res is not None:
+        out = out + res
+    if relu:
+        out = torch.relu(out)
+    out.backward(torch.as_tensor(np.asarray(dout, dtype=np.float64)))
+    return (x.grad.numpy(), w.grad.numpy(), b.grad.numpy(), None if res is None else res.grad.numpy())

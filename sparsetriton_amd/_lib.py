@@ -91,9 +91,15 @@ _SIGNATURES = {
     "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],
     "st_column_sum": [_P, _L, _I, _I, _P, _P, _I, _P],
     "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
+    "st_gather_gemm_tiled_epilogue": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _L, _I, _I, _I, _I,
+                                      _P],
     "st_gather_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
     "st_wgrad": [_P, _L, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P, _L, _P, _I, _P],
     "st_hashfly_gemm": [_P, _L, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _P, _P, _P, _I, _I, _I, _P],
+    "st_bn_workspace": [_L, _I, _I, ctypes.POINTER(_L)],
+    "st_bn_forward": [_P, _L, _I, _I, _P, _I, _I, _P, _P, _P, _I, _I, ctypes.c_float, ctypes.c_float, _P, _P, _P,
+                      _P, _P, _P, _L, _P, _P],
+    "st_bn_backward": [_P, _P, _P, _L, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P],
     "st_hashfly_wgrad": [_P, _L, _P, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _I, _I, _I, _P, _L, _P,
                          _I, _P],
 }

@@ -8,13 +8,13 @@ ST_GEMM_OPS(extern, __bf16)
 
 namespace st {
 int ops_gather_map_x3(const float* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs,
-                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst,
+                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst,
                       int K, int Kd, int Nd, hipStream_t stream);
 int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
                        const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const float* Bt,
-                       float* out, const float* bias, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
+                       float* out, Epi<float> epi, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
 int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
-                        const int32_t* tmap, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
+                        const int32_t* tmap, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
                         hipStream_t stream);
 int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,
                        const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
@@ -52,6 +52,27 @@ __global__ __launch_bounds__(256) void fill_rows_kernel(U* __restrict__ out, int
                                                         const U* __restrict__ bias) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
     out[i] = bias ? bias[i % nd] : (U)0;
+}
+
+// out (rows x nd of T) = the epilogue of a zero sum, column by column.
+template <typename T>
+__global__ __launch_bounds__(256) void fill_rows_epi_kernel(T* __restrict__ out, int64_t n, int nd, Epi<T> epi) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float mul, add;
+    const int col = (int)(i % nd);
+    epi.column(col, nd, mul, add);
+    out[i] = (T)epi.apply(0.f, mul, add, i / nd, nd, col);
+  }
+}
+
+template <typename T>
+static int fill_output_epi(void* out, int64_t n_dst, int Nd, Epi<T> epi, hipStream_t stream) {
+  const int64_t n = n_dst * Nd;
+  const int64_t blocks = (n + 255) / 256;
+  const unsigned g = (unsigned)(blocks < 65536 ? blocks : 65536);
+  fill_rows_epi_kernel<T><<<g, 256, 0, stream>>>((T*)out, n, Nd, epi);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
 }
 }  // namespace st
 
@@ -208,10 +229,10 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
   const int W = (K + 31) / 32;
   if (dtype == ST_F32_BF16X3)
     return ops_gather_map_x3((const float*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
-                             (const float*)Bt, (float*)out, (const float*)bias, n_dst, K, Kd, Nd, stream);
+                             (const float*)Bt, (float*)out, bias_epi<float>(bias), n_dst, K, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_map<T>((const T*)A, n_src, map, map_k_stride, map_r_stride, row_masks, W, perm,
-                                      (const T*)Bt, (T*)out, (const T*)bias, n_dst, K, Kd, Nd, stream));
+                                      (const T*)Bt, (T*)out, bias_epi<T>(bias), n_dst, K, Kd, Nd, stream));
 }
 
 int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
@@ -225,10 +246,35 @@ int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, cons
   if (n_src == 0) return fill_output(out, n_dst, Nd, dtype, bias, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
-                               (float*)out, (const float*)bias, n_dst, K, Kd, Nd, stream);
+                               (float*)out, bias_epi<float>(bias), n_dst, K, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_tiled<T>((const T*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const T*)Bt,
-                                        (T*)out, (const T*)bias, n_dst, K, Kd, Nd, stream));
+                                        (T*)out, bias_epi<T>(bias), n_dst, K, Kd, Nd, stream));
+}
+
+int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
+                                  const int16_t* tile_klist, const int32_t* tile_map, const void* Bt,
+                                  const void* bias, const float* scale, const float* shift, const void* residual,
+                                  int relu, void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype,
+                                  st_stream_t stream) {
+  if (n_src < 0 || n_dst < 0 || K <= 0 || K > ST_MAX_KVOL || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
+  if (n_dst >= (1ll << 31) || n_src >= (1ll << 31)) return ST_ERR_ARG;
+  if (n_dst == 0) return ST_OK;
+  if (!perm || !tile_nk || !tile_klist || !tile_map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
+  if (shift && !scale) return ST_ERR_ARG;
+  if (dtype == ST_F32_BF16X3) {
+    const Epi<float> epi{(const float*)bias, scale, shift, (const float*)residual, relu ? 1 : 0};
+    if (n_src == 0) return fill_output_epi<float>(out, n_dst, Nd, epi, stream);
+    return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
+                               (float*)out, epi, n_dst, K, Kd, Nd, stream);
+  }
+  ST_DISPATCH_DTYPE(dtype, T, (n_src == 0)
+                                  ? fill_output_epi<T>(out, n_dst, Nd, Epi<T>{(const T*)bias, scale, shift, (const T*)residual, relu ? 1 : 0},
+                                                       stream)
+                                  : ops_gather_tiled<T>((const T*)A, n_src, perm, tile_nk, tile_klist, tile_map,
+                                                        (const T*)Bt, (T*)out,
+                                                        Epi<T>{(const T*)bias, scale, shift, (const T*)residual, relu ? 1 : 0}, n_dst, K,
+                                                        Kd, Nd, stream));
 }
 
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,
@@ -270,10 +316,10 @@ int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int co
   if (n_src == 0) return fill_output(out, n_dst, Nd, dtype, bias, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_hash_x3((const float*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
-                              (const float*)Bt, (float*)out, (const float*)bias, n_dst, Kd, Nd, stream);
+                              (const float*)Bt, (float*)out, bias_epi<float>(bias), n_dst, Kd, Nd, stream);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_hash<T>((const T*)A, n_src, dst_coords, coord_dtype, offsets, lk, keys, vals, capacity,
-                                       (const T*)Bt, (T*)out, (const T*)bias, n_dst, Kd, Nd, stream));
+                                       (const T*)Bt, (T*)out, bias_epi<T>(bias), n_dst, Kd, Nd, stream));
 }
 
 int st_hashfly_wgrad(const void* X, int64_t n_in, const void* dY, const void* out_coords, int coord_dtype,

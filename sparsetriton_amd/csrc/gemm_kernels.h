@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
                                                           const int32_t* __restrict__ perm, const T* __restrict__ Bt,
                                                           T* __restrict__ out, int64_t n_src, int64_t n_dst, int K,
                                                           int Kd, int Nd, int vec_a, int vec_b,
-                                                          const T* __restrict__ bias) {
+                                                          Epi<T> epi) {
   using F = typename Frag<T>::type;
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -120,13 +120,10 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
     }
   }
 
-  // the bias of each output column (the reference adds it after the GEMM, conv.py:227-228)
-  float bv[NBLK];
+  // per-column store epilogue (bias, optional affine map, optional ReLU)
+  float em[NBLK], ea[NBLK];
 #pragma unroll
-  for (int nb = 0; nb < NBLK; ++nb) {
-    const int col = n0 + nb * 16 + c;
-    bv[nb] = (bias && col < Nd) ? (float)bias[col] : 0.f;
-  }
+  for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -137,7 +134,7 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
 #pragma unroll
       for (int nb = 0; nb < NBLK; ++nb) {
         const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = from_f32<T>(acc[m][nb][r] + bv[nb]);
+        if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
       }
     }
 }
@@ -154,7 +151,7 @@ template <typename T, int BN, int KS, typename Src>
 __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
-    int vec_b, const T* __restrict__ bias) {
+    int vec_b, Epi<T> epi) {
   using F = typename Frag<T>::type;
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -317,13 +314,10 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     }
   }
 
-  // the bias of each output column (the reference adds it after the GEMM, conv.py:227-228)
-  float bv[NBLK];
+  // per-column store epilogue (bias, optional affine map, optional ReLU)
+  float em[NBLK], ea[NBLK];
 #pragma unroll
-  for (int nb = 0; nb < NBLK; ++nb) {
-    const int col = n0 + nb * 16 + c;
-    bv[nb] = (bias && col < Nd) ? (float)bias[col] : 0.f;
-  }
+  for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -334,7 +328,7 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
 #pragma unroll
       for (int nb = 0; nb < NBLK; ++nb) {
         const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = from_f32<T>(acc[m][nb][r] + bv[nb]);
+        if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
       }
     }
 }
@@ -376,7 +370,7 @@ template <typename T, int BN, int KS, int D, typename Src, bool LINES>
 __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
-    int vec_b, const T* __restrict__ bias) {
+    int vec_b, Epi<T> epi) {
   using F = typename Frag<T>::type;
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -600,13 +594,10 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     }
   }
 
-  // the bias of each output column (the reference adds it after the GEMM, conv.py:227-228)
-  float bv[NBLK];
+  // per-column store epilogue (bias, optional affine map, optional ReLU)
+  float em[NBLK], ea[NBLK];
 #pragma unroll
-  for (int nb = 0; nb < NBLK; ++nb) {
-    const int col = n0 + nb * 16 + c;
-    bv[nb] = (bias && col < Nd) ? (float)bias[col] : 0.f;
-  }
+  for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -617,7 +608,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 #pragma unroll
       for (int nb = 0; nb < NBLK; ++nb) {
         const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = from_f32<T>(acc[m][nb][r] + bv[nb]);
+        if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
       }
     }
 }
@@ -1227,7 +1218,7 @@ static bool buffer_ok(int64_t n_src, int K, int Kd, int Nd, size_t esz) {
 
 template <typename T, int BN, int KS, typename Src>
 static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W, const int32_t* rows,
-                        const T* Bt, T* out, const T* bias, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
+                        const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
   const unsigned rgrid = ring_grid(n_dst, Nd, BN);
@@ -1235,33 +1226,33 @@ static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_
   if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2 &&
       buffer_ok(n_src, K, Kd, Nd, sizeof(T)))
     gather_gemm_ring_kernel<T, BN, KS, 2, Src, true>
-        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
   else if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)
     gather_gemm_ring_kernel<T, BN, KS, 2, Src, false>
-        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
   else
     gather_gemm_pipe_kernel<T, BN, KS, Src>
-        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
 }
 
 template <typename T, int KS, typename Src>
 static void launch_pipe_ks(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                           const int32_t* rows, const T* Bt, T* out, const T* bias, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
+                           const int32_t* rows, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
                            int vec_b, hipStream_t stream) {
   constexpr int LDS128 = 2 * 128 * (KS * Frag<T>::KSTEP + Frag<T>::VEC) * (int)sizeof(T) + kSrcGroup * kGemmBM * 4;
   if (Nd <= 16)
-    launch_pipe<T, 16, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe<T, 16, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if (Nd <= 32)
-    launch_pipe<T, 32, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe<T, 32, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if (Nd <= 64 || LDS128 > 65536)  // (a 128-wide tile at KS = 4 costs occupancy more than its gathers save)
-    launch_pipe<T, 64, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe<T, 64, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if constexpr (LDS128 <= 65536)
-    launch_pipe<T, 128, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe<T, 128, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
 }
 
 template <typename T, typename Src>
 static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                         const int32_t* rows, const T* Bt, T* out, const T* bias, int64_t n_dst, int K, int Kd, int Nd,
+                         const int32_t* rows, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd,
                          hipStream_t stream) {
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -1269,11 +1260,11 @@ static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32
   const int vec_b = (Kd % VEC == 0) && ((uintptr_t)Bt % 16 == 0);
   const int ks = (Kd + KSTEP - 1) / KSTEP;
   if (ks == 1) {
-    launch_pipe_ks<T, 1>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe_ks<T, 1>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   } else if (ks == 2) {
-    launch_pipe_ks<T, 2>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe_ks<T, 2>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   } else if (ks <= 4) {
-    launch_pipe_ks<T, 4>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_pipe_ks<T, 4>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   } else if constexpr (Src::kTiled) {
     return ST_ERR_UNSUPPORTED;  // deep reductions take the untiled kernels
   } else {
@@ -1281,16 +1272,16 @@ static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32
     const unsigned gx = st_blocks(n_dst, kGemmBM);
     if (Nd <= 16)
       gather_gemm_kernel<T, 16, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
-                                                                       K, Kd, Nd, vec_a, vec_b, bias);
+                                                                       K, Kd, Nd, vec_a, vec_b, epi);
     else if (Nd <= 32)
       gather_gemm_kernel<T, 32, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
-                                                                       K, Kd, Nd, vec_a, vec_b, bias);
+                                                                       K, Kd, Nd, vec_a, vec_b, epi);
     else if (Nd <= 64)
       gather_gemm_kernel<T, 64, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
-                                                                       K, Kd, Nd, vec_a, vec_b, bias);
+                                                                       K, Kd, Nd, vec_a, vec_b, epi);
     else
       gather_gemm_kernel<T, 128, Src><<<dim3(gx, st_blocks(Nd, 128)), 256, 0, stream>>>(
-          A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+          A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
   }
   ST_CHECK_LAUNCH();
   return ST_OK;
@@ -1435,18 +1426,18 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
 
 template <typename T>
 int ops_gather_map(const T* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs, const uint32_t* masks, int W,
-                   const int32_t* rows, const T* Bt, T* out, const T* bias, int64_t n_dst, int K, int Kd, int Nd,
+                   const int32_t* rows, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd,
                    hipStream_t stream) {
   MapSrc src{map, ks, rs};
-  return launch_gather<T>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, stream);
+  return launch_gather<T>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 
 template <typename T>
 int ops_gather_tiled(const T* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
-                     const int32_t* tmap, const T* Bt, T* out, const T* bias, int64_t n_dst, int K, int Kd, int Nd,
+                     const int32_t* tmap, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd,
                      hipStream_t stream) {
   TiledSrc src{nk, klist, tmap, K};
-  return launch_gather<T>(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, bias, n_dst, K, Kd, Nd, stream);
+  return launch_gather<T>(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 
 template <typename CT>
@@ -1459,15 +1450,15 @@ static HashSrc<CT> make_hash_src(const void* coords, const int32_t* offsets, con
 
 template <typename T>
 int ops_gather_hash(const T* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
-                    const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const T* Bt, T* out, const T* bias,
+                    const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const T* Bt, T* out, Epi<T> epi,
                     int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
   const int W = (lk->K + 31) / 32;
   if (coord_dtype == ST_COORD_I16)
     return launch_gather<T>(A, n_src, make_hash_src<int16_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
-                            nullptr, Bt, out, bias, n_dst, lk->K, Kd, Nd, stream);
+                            nullptr, Bt, out, epi, n_dst, lk->K, Kd, Nd, stream);
   if (coord_dtype == ST_COORD_I32)
     return launch_gather<T>(A, n_src, make_hash_src<int32_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
-                            nullptr, Bt, out, bias, n_dst, lk->K, Kd, Nd, stream);
+                            nullptr, Bt, out, epi, n_dst, lk->K, Kd, Nd, stream);
   return ST_ERR_UNSUPPORTED;
 }
 
@@ -1507,9 +1498,9 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
 #define ST_GEMM_OPS(X, T)                                                                                            \
   namespace st {                                                                                                     \
   X template int ops_gather_map<T>(const T*, int64_t, const int32_t*, int64_t, int64_t, const uint32_t*, int,        \
-                                   const int32_t*, const T*, T*, const T*, int64_t, int, int, int, hipStream_t);    \
+                                   const int32_t*, const T*, T*, Epi<T>, int64_t, int, int, int, hipStream_t);    \
   X template int ops_gather_hash<T>(const T*, int64_t, const void*, int, const int32_t*, const st_lookup*,            \
-                                    const uint64_t*, const uint32_t*, int64_t, const T*, T*, const T*, int64_t, int, \
+                                    const uint64_t*, const uint32_t*, int64_t, const T*, T*, Epi<T>, int64_t, int, \
                                     int,                                                                             \
                                     hipStream_t);                                                                    \
   X template int ops_wgrad_map<T>(const T*, int64_t, const T*, const int32_t*, int64_t, int64_t, int64_t, int, int,  \
@@ -1522,5 +1513,5 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
                                     hipStream_t);                                                                    \
   X template int ops_weight_prep<T>(const T*, T*, int, int, int, int, hipStream_t);                                  \
   X template int ops_gather_tiled<T>(const T*, int64_t, const int32_t*, const int32_t*, const int16_t*,              \
-                                     const int32_t*, const T*, T*, const T*, int64_t, int, int, int, hipStream_t);   \
+                                     const int32_t*, const T*, T*, Epi<T>, int64_t, int, int, int, hipStream_t);   \
   }

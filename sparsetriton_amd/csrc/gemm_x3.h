@@ -52,7 +52,7 @@ template <int BN, int KS, typename Src>
 __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
     const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd,
-    int vec_a, int vec_b, const float* __restrict__ bias) {
+    int vec_a, int vec_b, Epi<float> epi) {
   constexpr int KDP = KS * 32;
   constexpr int PITCH = KDP + 8;  // bf16 elements per LDS row of the B tile
   constexpr int NBLK = BN / 16;
@@ -230,13 +230,10 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
     }
   }
 
-  // the bias of each output column (the reference adds it after the GEMM, conv.py:227-228)
-  float bv[NBLK];
+  // per-column store epilogue (bias, optional affine map, optional ReLU)
+  float em[NBLK], ea[NBLK];
 #pragma unroll
-  for (int nb = 0; nb < NBLK; ++nb) {
-    const int col = n0 + nb * 16 + c;
-    bv[nb] = (bias && col < Nd) ? bias[col] : 0.f;
-  }
+  for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -247,7 +244,7 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
 #pragma unroll
       for (int nb = 0; nb < NBLK; ++nb) {
         const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = acc[m][nb][r] + bv[nb];
+        if (col < Nd) orow[col] = epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col);
       }
     }
 }
@@ -262,7 +259,7 @@ template <int BN, int KS, int D, typename Src, bool LINES>
 __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
     const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd,
-    const float* __restrict__ bias) {
+    Epi<float> epi) {
   constexpr int KDP = KS * 32;
   constexpr int PITCH = KDP + 8;
   constexpr int NBLK = BN / 16;
@@ -505,13 +502,10 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
     }
   }
 
-  // the bias of each output column (the reference adds it after the GEMM, conv.py:227-228)
-  float bv[NBLK];
+  // per-column store epilogue (bias, optional affine map, optional ReLU)
+  float em[NBLK], ea[NBLK];
 #pragma unroll
-  for (int nb = 0; nb < NBLK; ++nb) {
-    const int col = n0 + nb * 16 + c;
-    bv[nb] = (bias && col < Nd) ? bias[col] : 0.f;
-  }
+  for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -522,7 +516,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 #pragma unroll
       for (int nb = 0; nb < NBLK; ++nb) {
         const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = acc[m][nb][r] + bv[nb];
+        if (col < Nd) orow[col] = epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col);
       }
     }
 }
@@ -719,54 +713,54 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
 
 template <int BN, int KS, typename Src>
 static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                      const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
+                      const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
   const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines() && buffer_ok(n_src, K, Kd, Nd, 4))
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true>
-        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, epi);
   else if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, false>
-        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, bias);
+        <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, epi);
   else
     gather_gemm_x3_kernel<BN, KS, Src>
-        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, bias);
+        <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
 }
 
 template <int KS, typename Src>
 static void launch_x3_ks(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                         const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
+                         const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
                          int vec_a, int vec_b, hipStream_t stream) {
   if (Nd <= 16)
-    launch_x3<16, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_x3<16, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if (Nd <= 32)
-    launch_x3<32, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_x3<32, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else
-    launch_x3<64, KS>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_x3<64, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
 }
 
 // Split-operand gather-GEMM for reductions up to 128 wide; deeper ones use
 // the plain fp32 kernels.
 template <typename Src>
 static int launch_gather_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                            const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
+                            const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
                             hipStream_t stream) {
   const int ks = (Kd + 31) / 32;
   if (ks > 4) {
     if constexpr (Src::kTiled)
       return ST_ERR_UNSUPPORTED;
     else
-      return launch_gather<float>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, stream);
+      return launch_gather<float>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, stream);
   }
   const int vec_a = (Kd % 4 == 0) && ((uintptr_t)A % 16 == 0);
   const int vec_b = (Kd % 4 == 0) && ((uintptr_t)Bt % 16 == 0);
   if (ks == 1)
-    launch_x3_ks<1>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_x3_ks<1>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else if (ks == 2)
-    launch_x3_ks<2>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_x3_ks<2>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   else
-    launch_x3_ks<4>(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
+    launch_x3_ks<4>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

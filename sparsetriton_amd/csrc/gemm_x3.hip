@@ -4,30 +4,30 @@
 namespace st {
 
 int ops_gather_map_x3(const float* A, int64_t n_src, const int32_t* map, int64_t ks, int64_t rs,
-                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, const float* bias, int64_t n_dst,
+                      const uint32_t* masks, int W, const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst,
                       int K, int Kd, int Nd, hipStream_t stream) {
   MapSrc src{map, ks, rs};
-  return launch_gather_x3(A, n_src, src, masks, W, rows, Bt, out, bias, n_dst, K, Kd, Nd, stream);
+  return launch_gather_x3(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 
 int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int coord_dtype, const int32_t* offsets,
                        const st_lookup* lk, const uint64_t* keys, const uint32_t* vals, int64_t cap, const float* Bt,
-                       float* out, const float* bias, int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
+                       float* out, Epi<float> epi, int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
   const int W = (lk->K + 31) / 32;
   if (coord_dtype == ST_COORD_I16)
     return launch_gather_x3(A, n_src, make_hash_src<int16_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
-                            nullptr, Bt, out, bias, n_dst, lk->K, Kd, Nd, stream);
+                            nullptr, Bt, out, epi, n_dst, lk->K, Kd, Nd, stream);
   if (coord_dtype == ST_COORD_I32)
     return launch_gather_x3(A, n_src, make_hash_src<int32_t>(coords, offsets, lk, keys, vals, cap), nullptr, W,
-                            nullptr, Bt, out, bias, n_dst, lk->K, Kd, Nd, stream);
+                            nullptr, Bt, out, epi, n_dst, lk->K, Kd, Nd, stream);
   return ST_ERR_UNSUPPORTED;
 }
 
 int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
-                        const int32_t* tmap, const float* Bt, float* out, const float* bias, int64_t n_dst, int K, int Kd, int Nd,
+                        const int32_t* tmap, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
                         hipStream_t stream) {
   TiledSrc src{nk, klist, tmap, K};
-  return launch_gather_x3(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, bias, n_dst, K, Kd, Nd, stream);
+  return launch_gather_x3(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 
 int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,

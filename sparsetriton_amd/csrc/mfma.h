@@ -97,4 +97,39 @@ __device__ __forceinline__ T from_f32(float v) {
   return (T)v;
 }
 
+// Store epilogue of the gather-GEMMs, on the fp32 accumulator of (row r, column c):
+//   v = (acc + bias[c]) * scale[c] + shift[c] + residual[r, c], then ReLU when relu is set
+// bias (the convolution's, conv.py:227-228) and residual (n_dst x Nd, rows in
+// output order: a residual block's shortcut, blocks.py:121-124) have the
+// output dtype; scale and shift are fp32 (an evaluation-mode batch norm folded
+// to one affine map per channel, nn/functional/norm.py:105-112).  A null
+// pointer drops its term.
+template <typename T>
+struct Epi {
+  const T* bias;
+  const float* scale;
+  const float* shift;
+  const T* residual;
+  int relu;
+  __device__ __forceinline__ void column(int col, int Nd, float& mul, float& add) const {
+    const float b = (bias && col < Nd) ? (float)bias[col] : 0.f;
+    if (scale && col < Nd) {
+      mul = scale[col];
+      add = b * mul + (shift ? shift[col] : 0.f);
+    } else {
+      mul = 1.f;
+      add = b;
+    }
+  }
+  __device__ __forceinline__ float apply(float acc, float mul, float add, int64_t row, int Nd, int col) const {
+    float v = scale ? fmaf(acc, mul, add) : acc + add;
+    if (residual) v += (float)residual[row * Nd + col];
+    return (relu && v < 0.f) ? 0.f : v;  // (a NaN stays NaN, as under torch.relu)
+  }
+};
+template <typename T>
+inline Epi<T> bias_epi(const void* bias) {
+  return Epi<T>{(const T*)bias, nullptr, nullptr, nullptr, 0};
+}
+
 }  // namespace st

@@ -1,4 +1,6 @@
 from . import functional
-from .modules import SparseConv3D, SparseConv3DBase, SparseConvTransposed3D, SubMConv3D
+from .modules import *  # noqa: F401,F403
+from .modules import __all__ as _modules_all
+from .backbones import SparseResNet, SparseResNet21D
 
-__all__ = ["functional", "SparseConv3DBase", "SparseConv3D", "SubMConv3D", "SparseConvTransposed3D"]
+__all__ = ["functional", "SparseResNet", "SparseResNet21D"] + list(_modules_all)

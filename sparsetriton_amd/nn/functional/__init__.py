@@ -1,4 +1,6 @@
 from . import conv
-from .conv import build_out_coords, compute_neighbor_indices, sparse_conv3d
+from .conv import build_out_coords, compute_neighbor_indices, sparse_conv3d, sparse_conv3d_fused
+from .norm import sparse_batch_norm, sparse_batch_norm_act
 
-__all__ = ["conv", "sparse_conv3d", "compute_neighbor_indices", "build_out_coords"]
+__all__ = ["conv", "sparse_conv3d", "sparse_conv3d_fused", "compute_neighbor_indices", "build_out_coords", "sparse_batch_norm",
+           "sparse_batch_norm_act"]

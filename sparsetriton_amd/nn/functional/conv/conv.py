@@ -27,7 +27,7 @@ from sparsetriton_amd.tensor import SparseTensor
 from sparsetriton_amd.utils.hash import HashTable
 
 from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, InputGradLookup
-from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM
+from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM, conv_forward_epilogue
 from .kmap import KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map
 
 __all__ = ["sparse_conv3d", "compute_neighbor_indices", "table_capacity"]
@@ -96,6 +96,38 @@ def sparse_conv3d(
     submanifold: bool = True,
 ) -> SparseTensor:
     """3-D sparse convolution of ``tensor`` with ``weight`` (k^3, C_in, C_out)."""
+    return _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding, transposed, submanifold)
+
+
+def sparse_conv3d_fused(
+    tensor: SparseTensor,
+    weight: torch.Tensor,
+    kernel_size: Union[int, Tuple[int, int, int]],
+    bias: torch.Tensor = None,
+    stride: Union[int, Tuple[int, int, int]] = 1,
+    dilation: Union[int, Tuple[int, int, int]] = 1,
+    padding: Union[int, Tuple[int, int, int]] = 0,
+    transposed: bool = False,
+    submanifold: bool = True,
+    scale: torch.Tensor = None,
+    shift: torch.Tensor = None,
+    residual: torch.Tensor = None,
+    relu: bool = False,
+) -> SparseTensor:
+    """Inference convolution with ``act((conv + bias) * scale + shift + residual)`` applied as the
+    GEMM stores its rows (an evaluation-mode conv / batch norm / ReLU block in one pass).  Needs the
+    precomputed-map algorithm and no autograd."""
+    if get_conv_algo() != ConvAlgo.PrecomputedNeighborGEMM:
+        raise ValueError("the fused epilogue runs on the precomputed-map algorithm")
+    if torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad or
+                                    (bias is not None and bias.requires_grad)):
+        raise ValueError("the fused epilogue is an inference path (no autograd); call it under torch.no_grad()")
+    return _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding, transposed, submanifold,
+                          epilogue=(scale, shift, residual, relu))
+
+
+def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding, transposed, submanifold,
+                   epilogue=None) -> SparseTensor:
     if isinstance(kernel_size, (tuple, list)):
         assert kernel_size[0] == kernel_size[1] == kernel_size[2], "Only cubic kernels supported for now"
     k = _uniform(kernel_size, "kernel")
@@ -136,7 +168,10 @@ def sparse_conv3d(
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
         if out_coords.shape[0] == 0:
             return _empty(tensor, C_out, new_shape)
-        out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap, bias)
+        if epilogue is not None:
+            out_feats = conv_forward_epilogue(tensor.F, weight, kmap, bias, *epilogue)
+        else:
+            out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap, bias)
         if hit is None and torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
             # the weight gradient's pair list on a side stream, queued after the forward (which
             # needs the tile plan first) and running alongside it

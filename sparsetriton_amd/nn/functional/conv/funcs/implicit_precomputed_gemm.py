@@ -81,6 +81,36 @@ def gather_gemm_fwd(A: torch.Tensor, kmap: KernelMap, Bt: torch.Tensor, bias=Non
                        rows=plan.perm, bias=bias)
 
 
+def conv_forward_epilogue(features: torch.Tensor, weights: torch.Tensor, kmap: KernelMap, bias, scale, shift,
+                          residual, relu: bool) -> torch.Tensor:
+    """Forward with the store epilogue ``act((sum + bias) * scale + shift + residual)`` (inference:
+    no autograd).  ``scale`` / ``shift`` fp32 (C_out) or None; ``bias`` and ``residual`` (N_out, C_out)
+    in the features' dtype, residual rows in output order."""
+    _lib.require_device(features, "features")
+    N_in, C_in = features.shape
+    K, C_in_w, C_out = weights.shape
+    assert C_in_w == C_in, f"weights C_in ({C_in_w}) != features C_in ({C_in})"
+    assert kmap.K == K, f"kernel map has {kmap.K} offsets, weights {K}"
+    if not tiled_ok(features.dtype, C_in):
+        raise ValueError(f"the fused-epilogue forward covers reduction widths up to the tiled kernels' ({C_in})")
+    A = features.contiguous()
+    wt = weight_prep(weights.to(A.dtype).contiguous(), _lib.W_TRANSPOSE)
+    b = None if bias is None else bias.detach().to(A.dtype).contiguous()
+    sc = None if scale is None else scale.detach().to(torch.float32).contiguous()
+    sh = None if shift is None else shift.detach().to(torch.float32).contiguous()
+    res = None
+    if residual is not None:
+        assert residual.shape == (kmap.n_out, C_out), "residual must be (N_out, C_out)"
+        res = residual.detach().to(A.dtype).contiguous()
+    tiles = kmap.forward_tiles()
+    out = torch.empty((kmap.n_out, C_out), dtype=A.dtype, device=A.device)
+    _lib.call("st_gather_gemm_tiled_epilogue", _lib.ptr(A), N_in, _lib.ptr(tiles.perm), _lib.ptr(tiles.nk),
+              _lib.ptr(tiles.klist), _lib.ptr(tiles.tmap), _lib.ptr(wt), _lib.ptr(b), _lib.ptr(sc), _lib.ptr(sh),
+              _lib.ptr(res), int(bool(relu)), _lib.ptr(out), kmap.n_out, K, C_in, C_out,
+              _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+    return out
+
+
 def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> torch.Tensor:
     """Input gradient over the transposed map, in the mask-sorted order of the backward plan.
 

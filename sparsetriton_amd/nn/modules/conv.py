@@ -14,7 +14,7 @@ import torch
 from torch import nn
 
 from sparsetriton_amd.tensor import SparseTensor
-from sparsetriton_amd.nn.functional.conv.conv import sparse_conv3d
+from sparsetriton_amd.nn.functional.conv.conv import sparse_conv3d, sparse_conv3d_fused
 from sparsetriton_amd.utils.utils import make_ntuple
 
 __all__ = ["SparseConv3DBase", "SparseConv3D", "SubMConv3D", "SparseConvTransposed3D"]
@@ -70,6 +70,16 @@ class SparseConv3DBase(nn.Module):
             submanifold=self.subm,
             transposed=self.transposed,
         )
+
+
+    def forward_fused(self, input: SparseTensor, scale=None, shift=None, residual=None,
+                      relu: bool = False) -> SparseTensor:
+        """Inference forward with ``act((conv + bias) * scale + shift + residual)`` fused into the
+        GEMM's store (see ``sparse_conv3d_fused``)."""
+        return sparse_conv3d_fused(
+            input, self.weight, self.kernel_size, bias=self.bias, stride=self.stride, dilation=self.dilation,
+            padding=self.padding, transposed=self.transposed, submanifold=self.subm, scale=scale, shift=shift,
+            residual=residual, relu=relu)
 
 
 class SparseConv3D(SparseConv3DBase):

@@ -411,3 +411,73 @@ def test_column_sum(device, n, C, dtype):
     assert err <= 1e-5 * max(1.0, n ** 0.5) * 4
     assert torch.equal(s, column_sum(Y, torch.float32))
     assert column_sum(Y, dtype).dtype == dtype
+
+
+# ------------------------------------------------------------- store epilogue
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cin,cout", [(16, 32), (64, 64), (128, 128), (32, 48)])
+@pytest.mark.parametrize("s", [1, 2])
+def test_fused_epilogue_vs_oracle(device, dtype, cin, cout, s):
+    """act((conv + bias) * scale + shift + residual) in the GEMM store vs the float64 oracle."""
+    from sparsetriton_amd.nn.functional import sparse_conv3d_fused
+
+    rng = np.random.default_rng(cin * 10 + cout + s)
+    S = 16
+    c = _rand_coords(rng, 1500, S)
+    X = rng.standard_normal((c.shape[0], cin))
+    W = rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cin)
+    bias = rng.standard_normal(cout)
+    scale = rng.uniform(0.5, 1.5, cout)
+    shift = rng.standard_normal(cout)
+    set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)
+    feats = torch.as_tensor(X, device=device).to(dtype)
+    w = torch.as_tensor(W, device=device).to(dtype)
+    b = torch.as_tensor(bias, device=device).to(dtype)
+    sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=(S, S, S))
+    with torch.no_grad():
+        plain = sparse_conv3d(sp, w, 3, bias=b, stride=s, padding=1, submanifold=(s == 1))
+        n_out = plain.F.shape[0]
+        res = torch.as_tensor(rng.standard_normal((n_out, cout)), device=device).to(dtype)
+        sc = torch.as_tensor(scale, device=device, dtype=torch.float32)
+        sh = torch.as_tensor(shift, device=device, dtype=torch.float32)
+        out = sparse_conv3d_fused(sp, w, 3, bias=b, stride=s, padding=1, submanifold=(s == 1), scale=sc, shift=sh,
+                                  residual=res, relu=True)
+        only_relu = sparse_conv3d_fused(sp, w, 3, bias=b, stride=s, padding=1, submanifold=(s == 1), relu=True)
+    assert torch.equal(out.C, plain.C)
+    oc = out.C.cpu().numpy()
+    Xq = feats.double().cpu().numpy()
+    Wq = w.double().cpu().numpy()
+    off = O.target_offsets(3, 1, 1, False)
+    nbr = O.exact_kmap(c, oc, off, s, (S, S, S))
+    y = O.fwd_f64(Xq, Wq, nbr) + b.double().cpu().numpy()
+    ref = np.maximum(y * scale + shift + res.double().cpu().numpy(), 0.0)
+    assert rel(out.F.double().cpu(), ref) < TOL[dtype]
+    assert rel(only_relu.F.double().cpu(), np.maximum(y, 0.0)) < TOL[dtype]
+    # without an affine map or ReLU the epilogue is the plain bias store, bit for bit
+    with torch.no_grad():
+        same = sparse_conv3d_fused(sp, w, 3, bias=b, stride=s, padding=1, submanifold=(s == 1))
+    assert torch.equal(same.F, plain.F)
+
+
+def test_fused_epilogue_without_sources(device):
+    """No source rows: every output row is the epilogue of a zero sum."""
+    import ctypes
+    from sparsetriton_amd import _lib
+
+    n_dst, Nd, K, Kd = 300, 32, 27, 16
+    dev = device
+    perm = torch.arange(n_dst, dtype=torch.int32, device=dev)
+    dummy_i32 = torch.zeros(64, dtype=torch.int32, device=dev)
+    dummy_i16 = torch.zeros(64, dtype=torch.int16, device=dev)
+    Bt = torch.zeros((K, Nd, Kd), dtype=torch.float32, device=dev)
+    bias = torch.randn(Nd, device=dev)
+    scale = torch.rand(Nd, device=dev) + 0.5
+    shift = torch.randn(Nd, device=dev)
+    res = torch.randn(n_dst, Nd, device=dev)
+    out = torch.empty((n_dst, Nd), device=dev)
+    _lib.call("st_gather_gemm_tiled_epilogue", None, 0, _lib.ptr(perm), _lib.ptr(dummy_i32), _lib.ptr(dummy_i16),
+              _lib.ptr(dummy_i32), _lib.ptr(Bt), _lib.ptr(bias), _lib.ptr(scale), _lib.ptr(shift), _lib.ptr(res), 1,
+              _lib.ptr(out), n_dst, K, Kd, Nd, 0, _lib.stream_of(dev))
+    ref = torch.relu(bias * scale + shift + res)
+    assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)

@@ -8,6 +8,9 @@ What pins each oracle function:
                   (golden fixtures, torch float64)
   RefHash         the reference tests' known answers (tests/test_utils_hash.py:95-123)
                   and the closed-form key2 alias of (0,0,0,0) / (1,10,0,29)
+  batch_norm      torch.nn.functional.batch_norm applied sample by sample (outputs), the
+                  unbiased/biased relation to torch's running variance (running statistics),
+                  and central finite differences of the numpy forward (gradients)
 A mistake such as a sign flip in t_k, a transposed weight operand or a wrong
 stride rule breaks one of these.
 """
@@ -176,3 +179,72 @@ def test_hash_coords_helper():
         ref = ((c[:, 1] * np.int32(73856093)) ^ (c[:, 2] * np.int32(19349663)) ^ (c[:, 3] * np.int32(83492791))
                ^ (c[:, 0] * np.int32(1000003))) & np.int32(0x7FFFFFFF)
     assert hash_coords(torch.as_tensor(c)).tolist() == ref.tolist()
+
+
+# ------------------------------------------------------------ batch norm
+
+def test_batch_norm_matches_library_per_sample():
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((400, 6)) * 3 + 1
+    bi = rng.integers(0, 4, 400)
+    bi[bi == 2] = 3  # sample 2 has no rows
+    w, b = rng.standard_normal(6), rng.standard_normal(6)
+    res = rng.standard_normal((400, 6))
+    out, rm, rv = O.batch_norm_f64(x, bi, 4, w, b, np.zeros(6), np.ones(6), True, residual=res, relu=True)
+    for s in (0, 1, 3):
+        r = bi == s
+        ref = F.batch_norm(torch.tensor(x[r]), None, None, torch.tensor(w), torch.tensor(b), training=True).numpy()
+        assert np.abs(out[r] - np.maximum(ref + res[r], 0)).max() < 1e-12
+    # evaluation: the library routine with the running statistics
+    rm0, rv0 = rng.standard_normal(6), rng.uniform(0.5, 2, 6)
+    out_e, _, _ = O.batch_norm_f64(x, bi, 4, w, b, rm0, rv0, False)
+    ref = F.batch_norm(torch.tensor(x), torch.tensor(rm0), torch.tensor(rv0), torch.tensor(w), torch.tensor(b),
+                       training=False).numpy()
+    assert np.abs(out_e - ref).max() < 1e-12
+
+
+def test_batch_norm_running_stats_one_sample():
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(8)
+    n, m = 50, 0.1
+    x = rng.standard_normal((n, 5))
+    rm0, rv0 = rng.standard_normal(5), rng.uniform(0.5, 2, 5)
+    _, rm, rv = O.batch_norm_f64(x, np.zeros(n, np.int64), 1, None, None, rm0, rv0, True, momentum=m)
+    trm, trv = torch.tensor(rm0), torch.tensor(rv0)
+    F.batch_norm(torch.tensor(x), trm, trv, training=True, momentum=m)
+    assert np.abs(rm - trm.numpy()).max() < 1e-12
+    # torch moves towards the unbiased variance, the reference towards the biased one
+    assert np.abs((rv - (1 - m) * rv0) - (trv.numpy() - (1 - m) * rv0) * (n - 1) / n).max() < 1e-12
+
+
+@pytest.mark.parametrize("training,relu", [(True, True), (True, False), (False, True)])
+def test_batch_norm_grads_finite_differences(training, relu):
+    rng = np.random.default_rng(9)
+    n, C, B = 24, 3, 2
+    x = rng.standard_normal((n, C))
+    bi = rng.integers(0, B, n)
+    w, b = rng.standard_normal(C), rng.standard_normal(C)
+    rm0, rv0 = rng.standard_normal(C), rng.uniform(0.5, 2, C)
+    res = rng.standard_normal((n, C))
+    dout = rng.standard_normal((n, C))
+    dx, dw, db, dres = O.batch_norm_grads_f64(x, bi, B, w, b, rm0, rv0, training, dout, residual=res, relu=relu)
+
+    def f(x_, w_, b_, r_):
+        return float((O.batch_norm_f64(x_, bi, B, w_, b_, rm0, rv0, training, residual=r_, relu=relu)[0]
+                      * dout).sum())
+
+    h = 1e-6
+    for (arr, g) in ((x, dx), (w, dw), (b, db), (res, dres)):
+        num = np.zeros_like(arr)
+        for i in np.ndindex(arr.shape):
+            a0 = arr[i]
+            arr[i] = a0 + h
+            fp = f(x, w, b, res)
+            arr[i] = a0 - h
+            fm = f(x, w, b, res)
+            arr[i] = a0
+            num[i] = (fp - fm) / (2 * h)
+        assert np.abs(num - g).max() < 1e-5 * max(1.0, np.abs(g).max())
