@@ -425,6 +425,55 @@ int st_hashfly_wgrad(const void* X, int64_t n_in, const void* dY, const void* ou
                      int64_t capacity, int C_in, int C_out, int dtype, float* partials, int64_t splits, void* dW,
                      int dw_dtype, st_stream_t stream);
 
+/* ------------------------------------------------------------ dense grids
+ *
+ * to_dense (utils/to_dense.py:30-282): out (batches, sx, sy, sz, C) of
+ * `dtype`, channels last, is cleared and row r of feats (n, C) stored at the
+ * cell of coords[r] = (b, x, y, z); coordinates outside the grid are skipped,
+ * and a coordinate given twice keeps one of its rows.  st_from_dense is its
+ * gradient (the reference's _to_dense_bwd_kernel): feats[r] = the cell of
+ * coords[r], zeros outside the grid.
+ */
+int st_to_dense(const void* feats, int64_t n, int C, int dtype, const void* coords, int coord_dtype, int64_t batches,
+                int64_t sx, int64_t sy, int64_t sz, void* out, st_stream_t stream);
+int st_from_dense(const void* dense, int64_t batches, int64_t sx, int64_t sy, int64_t sz, int C, int dtype,
+                  const void* coords, int coord_dtype, int64_t n, void* feats, st_stream_t stream);
+
+/* ------------------------------------------------------------ pooling, upsampling
+ *
+ * sparse_pooling (nn/functional/spatial.py:26-233): row r of coords goes to
+ * the cell (b, floor((x + p - k/2) / s), ...) (spatial.py:104-107); the
+ * outputs are the distinct cells in ascending (b, x, y, z) order.
+ * st_pool_plan sorts the rows by cell (stable) into perm (n), writes the
+ * first sorted position of each output into seg_start (n_out + 1, the last
+ * entry = rows with a valid cell), each row's output into inv (n, -1 for a
+ * cell outside the key range: b outside [0, 32767] or a spatial value outside
+ * int16), the output coordinates into out_coords (rows 0 .. n_out-1 of an
+ * n x 4 buffer of coord_dtype), and counts[0] = n_out, counts[1] = rows
+ * without a valid cell.  workspace: st_pool_workspace(n) bytes.
+ * st_pool_forward: out[o] = max (mode 0) or mean (mode 1) of its rows, fp32
+ * arithmetic, rows in input order (deterministic).  st_pool_backward: each
+ * row gets its output's gradient, whole where it equals the max (mode 0, the
+ * reference's `in == out` rule) or divided by the row count (mode 1).
+ */
+int st_pool_workspace(int64_t n, size_t* bytes);
+int st_pool_plan(const void* coords, int coord_dtype, int64_t n, int kernel_size, int stride, int padding,
+                 void* workspace, size_t workspace_bytes, int32_t* perm, int32_t* seg_start, int32_t* inv,
+                 void* out_coords, int32_t* counts, st_stream_t stream);
+int st_pool_forward(const void* feats, int C, int dtype, const int32_t* perm, const int32_t* seg_start, int64_t n_out,
+                    int mode, void* out, st_stream_t stream);
+int st_pool_backward(const void* feats, const void* out, const void* dout, int64_t n, int C, int dtype,
+                     const int32_t* inv, const int32_t* seg_start, int mode, void* dfeats, st_stream_t stream);
+
+/*
+ * sparse_upsample (spatial.py:236-436): row r becomes rows r * s^3 + q,
+ * q = (dx * s + dy) * s + dz, at (b, x s + dx, y s + dy, z s + dz) with r's
+ * features; the backward sums each row's s^3 output gradients (fp32).
+ */
+int st_upsample(const void* feats, const void* coords, int coord_dtype, int64_t n, int C, int dtype, int scale,
+                void* out_feats, void* out_coords, st_stream_t stream);
+int st_upsample_backward(const void* dout, int64_t n, int C, int dtype, int scale, void* dfeats, st_stream_t stream);
+
 /* ------------------------------------------------------------ batch norm
  *
  * Per-sample batch normalisation of sparse features (sparse_batch_norm,

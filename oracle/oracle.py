@@ -352,3 +352,48 @@ def batch_norm_grads_f64(feats, batch_idx, B, weight, bias, running_mean, runnin
         out = torch.relu(out)
     out.backward(torch.as_tensor(np.asarray(dout, dtype=np.float64)))
     return (x.grad.numpy(), w.grad.numpy(), b.grad.numpy(), None if res is None else res.grad.numpy())
+
+
+# ------------------------------------------------------------ pooling, upsampling
+
+def pool_f64(coords, feats, kernel_size, padding, stride, mode):
+    """Sparse pooling (nn/functional/spatial.py:90-135): row r goes to the cell
+    floor((coord + padding - kernel_size // 2) / stride); outputs are the distinct cells in ascending
+    (b, x, y, z) order, each the max or the mean of its rows.  Cells are kept exact (negative ones too).
+    Returns (out_coords, out_feats, inv) with inv[r] = output of row r."""
+    c = np.asarray(coords, dtype=np.int64)
+    f = np.asarray(feats, dtype=np.float64)
+    cells = np.concatenate([c[:, :1], np.floor_divide(c[:, 1:] + padding - kernel_size // 2, stride)], 1)
+    uniq, inv = np.unique(cells, axis=0, return_inverse=True)
+    inv = inv.reshape(-1)
+    out = np.full((uniq.shape[0], f.shape[1]), -np.inf if mode == "max" else 0.0)
+    cnt = np.zeros(uniq.shape[0])
+    for r in range(c.shape[0]):
+        o = inv[r]
+        out[o] = np.maximum(out[o], f[r]) if mode == "max" else out[o] + f[r]
+        cnt[o] += 1
+    if mode == "avg":
+        out = out / cnt[:, None]
+    return uniq, out, inv
+
+
+def pool_grad_f64(feats, out, inv, dout, mode):
+    """Gradient of pool_f64 as the reference defines it (spatial.py:139-209): each row receives its
+    output's gradient, all of it where the row equals the max, or divided by the output's row count."""
+    f = np.asarray(feats, dtype=np.float64)
+    g = np.asarray(dout, dtype=np.float64)[inv]
+    if mode == "max":
+        return np.where(f == np.asarray(out, dtype=np.float64)[inv], g, 0.0)
+    cnt = np.bincount(inv, minlength=np.asarray(dout).shape[0])
+    return g / cnt[inv][:, None]
+
+
+def upsample_f64(coords, feats, s):
+    """Sparse upsampling (spatial.py:236-436): row r becomes rows r s^3 + q, q = (dx s + dy) s + dz, at
+    coord * s + (dx, dy, dz)."""
+    c = np.asarray(coords, dtype=np.int64)
+    f = np.asarray(feats, dtype=np.float64)
+    d = np.array([(dx, dy, dz) for dx in range(s) for dy in range(s) for dz in range(s)], dtype=np.int64)
+    oc = np.repeat(c, s ** 3, axis=0)
+    oc[:, 1:] = oc[:, 1:] * s + np.tile(d, (c.shape[0], 1))
+    return oc, np.repeat(f, s ** 3, axis=0)

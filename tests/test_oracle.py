@@ -8,6 +8,9 @@ What pins each oracle function:
                   (golden fixtures, torch float64)
   RefHash         the reference tests' known answers (tests/test_utils_hash.py:95-123)
                   and the closed-form key2 alias of (0,0,0,0) / (1,10,0,29)
+  pool            torch max_pool3d / avg_pool3d of dense grids (empty cells -inf / uncounted)
+                  where the cell rule is standard pooling (odd kernel, padding k // 2)
+  upsample        the reference's own known answer (tests/test_pooling.py:14-40)
   batch_norm      torch.nn.functional.batch_norm applied sample by sample (outputs), the
                   unbiased/biased relation to torch's running variance (running statistics),
                   and central finite differences of the numpy forward (gradients)
@@ -248,3 +251,45 @@ def test_batch_norm_grads_finite_differences(training, relu):
             arr[i] = a0
             num[i] = (fp - fm) / (2 * h)
         assert np.abs(num - g).max() < 1e-5 * max(1.0, np.abs(g).max())
+
+
+# ------------------------------------------------------------ pooling, upsampling
+
+@pytest.mark.parametrize("s", [2, 3])
+@pytest.mark.parametrize("mode", ["max", "avg"])
+def test_pool_matches_dense_library_pooling(s, mode):
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(s * 10 + len(mode))
+    S = 12
+    c = _rand_coords(rng, 300, S)
+    f = rng.standard_normal((c.shape[0], 3))
+    k, p = 3, 1  # odd kernel, padding k // 2: the cell of x is floor(x / s), standard pooling
+    oc, out, inv = O.pool_f64(c, f, k, p, s, mode)
+    B = int(c[:, 0].max()) + 1
+    fill = -np.inf if mode == "max" else 0.0
+    dense = torch.full((B, 3, S, S, S), fill, dtype=torch.float64)
+    occ = torch.zeros((B, 1, S, S, S), dtype=torch.float64)
+    ct = torch.as_tensor(c, dtype=torch.long)
+    dense[ct[:, 0], :, ct[:, 1], ct[:, 2], ct[:, 3]] = torch.as_tensor(f)
+    occ[ct[:, 0], 0, ct[:, 1], ct[:, 2], ct[:, 3]] = 1.0
+    if mode == "max":
+        ref = F.max_pool3d(dense, s, s, ceil_mode=True)
+    else:
+        ref = F.avg_pool3d(dense, s, s, ceil_mode=True) / F.avg_pool3d(occ, s, s, ceil_mode=True)
+    o = torch.as_tensor(oc, dtype=torch.long)
+    assert np.abs(out - ref[o[:, 0], :, o[:, 1], o[:, 2], o[:, 3]].numpy()).max() < 1e-12
+    # every occupied cell is an output, in ascending order
+    cnt = F.avg_pool3d(occ, s, s, ceil_mode=True) * s ** 3
+    assert int((cnt > 0).sum()) == oc.shape[0]
+    assert (np.lexsort(oc.T[::-1]) == np.arange(oc.shape[0])).all()
+    assert (oc[inv] == np.concatenate([c[:, :1], c[:, 1:] // s], 1)).all()
+
+
+def test_upsample_reference_kat():
+    # tests/test_pooling.py:14-40: one voxel at the origin, s in 1..3
+    for s in (1, 2, 3):
+        oc, of = O.upsample_f64(np.array([[0, 0, 0, 0]]), np.array([[1.0, 2.0, 3.0]]), s)
+        assert oc.shape == (s ** 3, 4) and (of == [1.0, 2.0, 3.0]).all()
+        expect = [[0, x, y, z] for x in range(s) for y in range(s) for z in range(s)]
+        assert oc.tolist() == expect

@@ -7,7 +7,7 @@ import torch
 from sparsetriton_amd import SparseTensor, randn
 from sparsetriton_amd.nn import SparseConv3D, SparseConvTransposed3D, SubMConv3D
 from sparsetriton_amd.tensor import TensorCache
-from sparsetriton_amd.utils import make_ntuple, to_dense
+from sparsetriton_amd.utils import make_ntuple
 
 C3 = torch.tensor([[0, 1, 2, 3], [0, 1, 2, 4], [0, 1, 3, 3]])
 
@@ -48,15 +48,6 @@ def test_properties_and_methods():
     assert "SparseTensor" in repr(sp) and "spatial_shape=" in repr(sp)
     s = sp + sp
     assert torch.allclose(s.F, 2 * sp.F)
-
-
-def test_dense_layout_kat():
-    # Known answer from the reference's to_dense docstring (utils/to_dense.py:259-270).
-    feats = torch.tensor([[1.0], [2.0], [3.0]])
-    coords = torch.tensor([[0, 0, 0, 0], [0, 0, 0, 1], [1, 0, 0, 0]])
-    d = to_dense(feats, coords, (1, 1, 2))
-    assert d.shape == (2, 1, 1, 2, 1)
-    assert d[0, 0, 0, 0, 0] == 1.0 and d[0, 0, 0, 1, 0] == 2.0 and d[1, 0, 0, 0, 0] == 3.0
 
 
 def test_randn():
@@ -102,3 +93,15 @@ def test_conv_requires_gpu_features():
     conv = SubMConv3D(4, 8, 3)
     with pytest.raises(RuntimeError, match="must live on the GPU"):
         conv(sp)
+
+
+def test_spatial_argument_errors():
+    # tests/test_nn_functional.py:53-56 and tests/test_pooling.py:53-55 (CPU, before any kernel)
+    from sparsetriton_amd.nn import SparsePooling
+    from sparsetriton_amd.nn.functional import sparse_pooling
+
+    sp = randn((16, 16, 16), batch_size=2, nnz=10, channels=4, device="cpu")
+    with pytest.raises(ValueError, match="Unsupported mode"):
+        sparse_pooling(sp, kernel_size=2, padding=0, stride=2, mode="invalid")
+    with pytest.raises(ValueError, match="mode must be"):
+        SparsePooling(kernel_size=2, mode="invalid")
