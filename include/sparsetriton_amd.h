@@ -171,11 +171,16 @@ typedef struct st_outgeom {
   int64_t stride;       /* >= 1                                                      */
   int64_t in_shape[3];  /* input spatial shape (bounds of the neighbour lookup)      */
   int64_t out_shape[3]; /* output spatial shape (range filter of the candidates)     */
+  int64_t chunk;        /* offsets per chunk of the candidate order (the reference's
+                           chunk_size, kmap.py:270-278); <= 0 or >= K: one chunk   */
 } st_outgeom;
 
 /*
  * Dedup-table capacity and per-block counter length the output-coordinate
- * build needs for n input rows.  Fills *dedup_capacity and *num_blocks.
+ * build needs for n input rows.  Fills *dedup_capacity (twice the candidates
+ * that can pass the filters, at most 2^31 - 64; a smaller table works when
+ * it holds the distinct outputs, and an overflow is reported in status) and
+ * *num_blocks (input blocks of 256 rows x offset chunks).
  */
 int st_outcoords_sizes(int64_t n, const st_outgeom* g, int64_t kernel_size, int64_t dilation,
                        int64_t* dedup_capacity, int64_t* num_blocks);
@@ -184,10 +189,11 @@ int st_outcoords_sizes(int64_t n, const st_outgeom* g, int64_t kernel_size, int6
  * Replaces the candidate expansion, stride / range filter and dedup of
  * _build_out_coords_normal / _transposed (kmap.py:213-444, expand_coords_kernel
  * :11-54, filter_unique_kernel :56-97, mask_spatial_range utils/spatial/tile.py).
- * Pass 1 of 2.  Candidates are enumerated input-major, offset-minor (the
- * reference's order); every valid candidate is inserted into the dedup table
- * (dkeys/dvals, cleared to all-ones by the caller, capacity from
- * st_outcoords_sizes) keeping the lowest candidate index per coordinate.
+ * Pass 1 of 2.  Candidates are enumerated chunk by chunk of g->chunk
+ * offsets, input-major and offset-minor inside a chunk (the reference's
+ * order, kmap.py:270-278; one chunk by default); every valid candidate is
+ * inserted into the dedup table (dkeys/dvals, cleared to all-ones by the
+ * caller) keeping the lowest candidate rank per coordinate.
  * block_counts (num_blocks + 1 int32) receives, after an exclusive scan, the
  * output-row offset of each block; block_counts[num_blocks] = N_out.
  */

@@ -231,11 +231,22 @@ def bf_kmap(in_coords, out_coords, offsets, stride, shape, in_scale=1) -> np.nda
     return res
 
 
-def bf_out_coords(in_coords, offsets, stride, transposed, new_shape) -> np.ndarray:
-    """Explicit candidate loop with a seen-set (kmap.py:278-330, 397-444 without chunking)."""
+def bf_out_coords(in_coords, offsets, stride, transposed, new_shape, chunk=None) -> np.ndarray:
+    """Explicit candidate loop with a seen-set (kmap.py:278-330, 397-444): offset chunks of `chunk`
+    offsets in turn (all offsets in one chunk by default), input-major and offset-minor inside a chunk,
+    one seen-set across chunks (the reference's global dedup table)."""
     seen, out = set(), []
+    offs = np.asarray(offsets).tolist()
+    step = len(offs) if not chunk else int(chunk)
+    for c0 in range(0, len(offs), step):
+        out.extend(_bf_chunk(in_coords, offs[c0:c0 + step], stride, transposed, new_shape, seen))
+    return np.asarray(out, dtype=np.int32).reshape(-1, 4)
+
+
+def _bf_chunk(in_coords, offs, stride, transposed, new_shape, seen):
+    out = []
     for b, x, y, z in np.asarray(in_coords).tolist():
-        for tx, ty, tz in np.asarray(offsets).tolist():
+        for tx, ty, tz in offs:
             if transposed:
                 c = (x * stride + tx, y * stride + ty, z * stride + tz)
             else:
@@ -249,7 +260,7 @@ def bf_out_coords(in_coords, offsets, stride, transposed, new_shape) -> np.ndarr
             if key not in seen:
                 seen.add(key)
                 out.append(key)
-    return np.asarray(out, dtype=np.int32).reshape(-1, 4)
+    return out
 
 
 def dense_conv_at(in_coords, feats, weight, kernel_size, stride, padding, dilation, transposed, out_coords,

@@ -35,6 +35,7 @@ class OutGeom(ctypes.Structure):
         ("stride", ctypes.c_int64),
         ("in_shape", ctypes.c_int64 * 3),
         ("out_shape", ctypes.c_int64 * 3),
+        ("chunk", ctypes.c_int64),
     ]
 
 

@@ -21,6 +21,7 @@ namespace st {
 struct Geom {
   int K;
   int transposed;
+  int chunk;  // offsets per chunk of the candidate order (K: one chunk)
   int64_t s;
   int64_t in_shape[3];
   int64_t out_shape[3];
@@ -55,6 +56,15 @@ __device__ __forceinline__ bool input_in_bounds(const Geom& g, int64_t x, int64_
   return x >= 0 && y >= 0 && z >= 0 && x < g.in_shape[0] && y < g.in_shape[1] && z < g.in_shape[2];
 }
 
+// Rank of candidate (input i, offset k) in the enumeration order: offset
+// chunks of `chunk` offsets in turn, inside a chunk input-major and offset-
+// minor (the reference's chunk_size loop, kmap.py:270-278; one chunk is the
+// plain input-major / offset-minor order).
+__device__ __forceinline__ uint32_t cand_rank(const Geom& g, int64_t n, int64_t i, int k) {
+  const int c = k / g.chunk;
+  return (uint32_t)((int64_t)c * n * g.chunk + i * g.chunk + (k - c * g.chunk));
+}
+
 __device__ __forceinline__ void load_offsets(int32_t* off_s, const int32_t* __restrict__ offsets, int K) {
   for (int t = threadIdx.x; t < K * 3; t += blockDim.x) off_s[t] = offsets[t];
   __syncthreads();
@@ -85,26 +95,27 @@ __global__ __launch_bounds__(256) void cand_insert_kernel(const CT* __restrict__
       atomicAdd(&status[ST_STATUS_OVERFLOW], 1);
       continue;
     }
-    atomicMin(&dvals[s], (uint32_t)(i * g.K + k));
+    atomicMin(&dvals[s], cand_rank(g, n, i, k));
   }
 }
 
 // Number of first-occurrence candidates of input row i, with the slot of each
 // one reported through the callback.
 template <typename CT, typename F>
-__device__ __forceinline__ int first_candidates(const CT* __restrict__ coords, int64_t i, const int32_t* off_s,
-                                                const Geom& g, const uint64_t* __restrict__ dkeys,
+__device__ __forceinline__ int first_candidates(const CT* __restrict__ coords, int64_t n, int64_t i,
+                                                const int32_t* off_s, const Geom& g, int k0, int k1,
+                                                const uint64_t* __restrict__ dkeys,
                                                 const uint32_t* __restrict__ dvals, uint32_t dcap, F&& on_first) {
   int64_t b, x, y, z;
   load_coord(coords, i, b, x, y, z);
   int cnt = 0;
-  for (int k = 0; k < g.K; ++k) {
+  for (int k = k0; k < k1; ++k) {
     int64_t ox, oy, oz;
     if (!candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz)) continue;
     uint64_t key;
     if (!pack_key(b, ox, oy, oz, key)) continue;
     uint32_t s = find_slot(dkeys, dcap, key);
-    if (s == ST_NO_VAL || dvals[s] != (uint32_t)(i * g.K + k)) continue;
+    if (s == ST_NO_VAL || dvals[s] != cand_rank(g, n, i, k)) continue;
     on_first(s, b, ox, oy, oz);
     ++cnt;
   }
@@ -121,9 +132,10 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const CT* __restrict__ 
   __shared__ int red[8];
   load_offsets(off_s, offsets, g.K);
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int k0 = blockIdx.y * g.chunk, k1 = min(g.K, k0 + g.chunk);  // this grid row's offset chunk
   int cnt = 0;
   if (i < n)
-    cnt = first_candidates(coords, i, off_s, g, dkeys, dvals, dcap,
+    cnt = first_candidates(coords, n, i, off_s, g, k0, k1, dkeys, dvals, dcap,
                            [](uint32_t, int64_t, int64_t, int64_t, int64_t) {});
   cnt = wave_sum(cnt);
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = cnt;
@@ -131,7 +143,7 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const CT* __restrict__ 
   if (threadIdx.x == 0) {
     int t = 0;
     for (int w = 0; w < (int)(blockDim.x / kWave); ++w) t += red[w];
-    block_counts[blockIdx.x] = t;
+    block_counts[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = t;
   }
 }
 
@@ -198,14 +210,15 @@ __global__ __launch_bounds__(256) void cand_emit_kernel(const CT* __restrict__ c
   __shared__ int scratch[5];
   load_offsets(off_s, offsets, g.K);
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int k0 = blockIdx.y * g.chunk, k1 = min(g.K, k0 + g.chunk);
   int cnt = 0;
   if (i < n)
-    cnt = first_candidates(coords, i, off_s, g, dkeys, dvals, dcap,
+    cnt = first_candidates(coords, n, i, off_s, g, k0, k1, dkeys, dvals, dcap,
                            [](uint32_t, int64_t, int64_t, int64_t, int64_t) {});
   int tot;
-  int pos = block_offsets[blockIdx.x] + block_exclusive_scan(cnt, scratch, &tot);
+  int pos = block_offsets[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] + block_exclusive_scan(cnt, scratch, &tot);
   if (i >= n || cnt == 0) return;
-  first_candidates(coords, i, off_s, g, dkeys, dvals, dcap,
+  first_candidates(coords, n, i, off_s, g, k0, k1, dkeys, dvals, dcap,
                    [&](uint32_t s, int64_t b, int64_t ox, int64_t oy, int64_t oz) {
                      CT* r = out_coords + (int64_t)pos * 4;
                      r[0] = (CT)b;
@@ -270,6 +283,7 @@ static bool make_geom(const st_outgeom* in, Geom& g) {
   if (!in || in->K <= 0 || in->K > ST_MAX_KVOL || in->stride < 1) return false;
   g.K = in->K;
   g.transposed = in->transposed ? 1 : 0;
+  g.chunk = (in->chunk <= 0 || in->chunk >= in->K) ? in->K : (int)in->chunk;
   g.s = in->stride;
   for (int a = 0; a < 3; ++a) {
     g.in_shape[a] = in->in_shape[a];
@@ -308,10 +322,12 @@ int st_outcoords_sizes(int64_t n, const st_outgeom* gin, int64_t kernel_size, in
   }
   int64_t kv = per_axis * per_axis * per_axis;
   if (kv > g.K) kv = g.K;
+  // twice the candidates that can pass the filters (clamped to the 32-bit
+  // slot range; a caller that overflows the table can grow it and retry)
   int64_t cap = 2 * n * kv + 64;
-  if (cap >= (1ll << 31)) return ST_ERR_ARG;
+  if (cap > (1ll << 31) - 64) cap = (1ll << 31) - 64;
   *dedup_capacity = cap;
-  *num_blocks = (n + 255) / 256;
+  *num_blocks = ((n + 255) / 256) * ((g.K + g.chunk - 1) / g.chunk);  // per (input block, offset chunk)
   return ST_OK;
 }
 
@@ -322,14 +338,15 @@ int st_outcoords_plan(const void* in_coords, int coord_dtype, int64_t n, const i
   if (n < 0 || !make_geom(gin, g) || dcap <= 0 || dcap >= (1ll << 31) || !dkeys || !dvals || !block_counts ||
       !status || !offsets)
     return ST_ERR_ARG;
-  if (num_blocks != (n + 255) / 256 || n * (int64_t)g.K >= (1ll << 32) - 1) return ST_ERR_ARG;
+  const int64_t nb = (n + 255) / 256, nchunks = (g.K + g.chunk - 1) / g.chunk;
+  if (num_blocks != nb * nchunks || n * nchunks * (int64_t)g.chunk >= (1ll << 32) - 1) return ST_ERR_ARG;
   if (n > 0 && !in_coords) return ST_ERR_ARG;
   if (n > 0) {
     ST_DISPATCH_COORD(coord_dtype, CT, {
-      cand_insert_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys,
-                                                                       dvals, (uint32_t)dcap, status);
-      cand_count_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys,
-                                                                      dvals, (uint32_t)dcap, block_counts);
+      cand_insert_kernel<CT><<<(unsigned)nb, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys, dvals,
+                                                               (uint32_t)dcap, status);
+      cand_count_kernel<CT><<<dim3((unsigned)nb, (unsigned)nchunks), 256, 0, stream>>>(
+          (const CT*)in_coords, n, offsets, g, dkeys, dvals, (uint32_t)dcap, block_counts);
     });
   }
   exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, num_blocks);
@@ -346,17 +363,17 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
   if (n < 0 || n_out < 0 || !make_geom(gin, g) || dcap <= 0 || dcap >= (1ll << 31) || !dkeys || !dvals ||
       !slot_out || !block_counts || !offsets)
     return ST_ERR_ARG;
-  if (num_blocks != (n + 255) / 256) return ST_ERR_ARG;
+  const int64_t nb = (n + 255) / 256, nchunks = (g.K + g.chunk - 1) / g.chunk;
+  if (num_blocks != nb * nchunks) return ST_ERR_ARG;
   if (in_keys && (!in_vals || in_cap <= 0 || in_cap >= (1ll << 31))) return ST_ERR_ARG;
   if (n == 0 || n_out == 0) return ST_OK;
   if (!in_coords || !out_coords) return ST_ERR_ARG;
   if (nbr && (!invnbr || !out_masks || !in_masks)) return ST_ERR_ARG;
   ST_DISPATCH_COORD(coord_dtype, CT, {
-    cand_emit_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, n, offsets, g, dkeys, dvals,
-                                                                   slot_out, (uint32_t)dcap, block_counts,
-                                                                   (CT*)out_coords);
+    cand_emit_kernel<CT><<<dim3((unsigned)nb, (unsigned)nchunks), 256, 0, stream>>>(
+        (const CT*)in_coords, n, offsets, g, dkeys, dvals, slot_out, (uint32_t)dcap, block_counts, (CT*)out_coords);
     if (nbr)
-      cand_map_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>(
+      cand_map_kernel<CT><<<(unsigned)nb, 256, 0, stream>>>(
         (const CT*)in_coords, n, offsets, g, dkeys, slot_out, (uint32_t)dcap, in_keys, in_vals, (uint32_t)in_cap,
         n_out, nbr, invnbr, out_masks, in_masks);
   });

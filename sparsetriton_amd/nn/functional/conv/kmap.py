@@ -398,11 +398,19 @@ class OutCoordTable:
 
 def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size: int, stride: int, dilation: int,
                              padding: int, transposed: bool, in_table: Optional[HashTable] = None,
-                             with_map: bool = True):
+                             with_map: bool = True, chunk_size: Optional[int] = None):
     """Strided / transposed output coordinates plus (optionally) their kernel map.
 
     Returns (out_coords, new_spatial_shape, kernel_offsets, kmap_or_None, out_table).
     One host synchronisation reads the output count.
+
+    ``chunk_size`` (offsets per chunk, the reference's ``kmap.py:270-278``)
+    orders the candidates chunk by chunk, as the reference's loop does, and
+    bounds the dedup table: it starts at twice the candidates of one chunk
+    and doubles while it overflows (each retry one more pass over the
+    inputs), so its size follows the distinct outputs rather than all
+    candidates.  Without it the table is sized for every candidate up front,
+    and still grows if that size was clamped to the 32-bit slot range.
     """
     dev = in_coords.device
     _lib.require_device(in_coords, "coordinates")
@@ -418,25 +426,35 @@ def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size
     g.K = K
     g.transposed = 1 if transposed else 0
     g.stride = int(stride)
+    g.chunk = int(chunk_size) if chunk_size else 0
     for a in range(3):
         g.in_shape[a] = int(spatial_shape[a])
         g.out_shape[a] = int(new_shape[a])
     dcap, nblocks = ctypes.c_int64(), ctypes.c_int64()
     _lib.call("st_outcoords_sizes", n, ctypes.byref(g), int(kernel_size), int(dilation), ctypes.byref(dcap),
               ctypes.byref(nblocks))
-    dcap, nblocks = dcap.value, nblocks.value
+    max_cap, nblocks = dcap.value, nblocks.value
+    dcap = max_cap
+    if chunk_size and 0 < int(chunk_size) < K:
+        dcap = min(max_cap, 2 * n * int(chunk_size) + 64)
     s = _lib.stream_of(dev)
-    dkeys = _lib.fill_(torch.empty((dcap,), dtype=torch.int64, device=dev), -1)
-    dvals = _lib.fill_(torch.empty((dcap,), dtype=torch.int32, device=dev), -1)
     counts = torch.empty((nblocks + 1,), dtype=torch.int32, device=dev)
-    status = torch.zeros((_lib.STATUS_WORDS,), dtype=torch.int32, device=dev)
+    status = torch.empty((_lib.STATUS_WORDS,), dtype=torch.int32, device=dev)
     offs = _offsets_i32(offsets)
-    _lib.call("st_outcoords_plan", _lib.ptr(in_coords), _lib.coord_code(in_coords.dtype), n, _lib.ptr(offs),
-              ctypes.byref(g), _lib.ptr(dkeys), _lib.ptr(dvals), dcap, _lib.ptr(counts), nblocks, _lib.ptr(status), s)
-    tail = torch.stack([counts[nblocks], status[_lib.STATUS_OVERFLOW], status[_lib.STATUS_BAD_COORD]]).tolist()
-    n_out, overflow, bad = tail
-    if overflow:
-        raise RuntimeError(f"output-coordinate dedup table overflowed ({overflow} candidates dropped)")
+    while True:
+        dkeys = _lib.fill_(torch.empty((dcap,), dtype=torch.int64, device=dev), -1)
+        dvals = _lib.fill_(torch.empty((dcap,), dtype=torch.int32, device=dev), -1)
+        _lib.fill_(status, 0)
+        _lib.call("st_outcoords_plan", _lib.ptr(in_coords), _lib.coord_code(in_coords.dtype), n, _lib.ptr(offs),
+                  ctypes.byref(g), _lib.ptr(dkeys), _lib.ptr(dvals), dcap, _lib.ptr(counts), nblocks,
+                  _lib.ptr(status), s)
+        tail = torch.stack([counts[nblocks], status[_lib.STATUS_OVERFLOW], status[_lib.STATUS_BAD_COORD]]).tolist()
+        n_out, overflow, bad = tail
+        if not overflow:
+            break
+        if dcap >= max_cap:
+            raise RuntimeError(f"output-coordinate dedup table overflowed ({overflow} candidates dropped)")
+        dcap = min(max_cap, 2 * dcap)
     if bad:
         raise RuntimeError(f"{bad} output coordinates fall outside the packable range")
     out_coords = torch.empty((n_out, 4), dtype=in_coords.dtype, device=dev)
@@ -479,12 +497,15 @@ def build_out_coords(
     coordinates unchanged (``kmap.py:261-262``).  Otherwise candidates
     ``in + t_k`` (or ``in * s + t_k`` transposed) pass the stride and range
     filters and are deduplicated, in first-occurrence order of the
-    input-major / offset-minor candidate enumeration.  ``chunk_size`` is
-    accepted for compatibility; candidates are never materialised here.
+    input-major / offset-minor candidate enumeration -- with ``chunk_size``
+    offsets per chunk, chunk by chunk as the reference's loop
+    (``kmap.py:270-278``), the dedup table then sized by the distinct outputs
+    (see ``build_out_coords_and_map``).  Candidates are never materialised.
     """
     offsets = _target_offsets(kernel_size, dilation, padding, transposed, in_coords.device).to(in_coords.dtype)
     if submanifold and stride == 1 and ((kernel_size - 1) * dilation) // 2 == padding:
         return in_coords, spatial_shape, offsets
     out_coords, new_shape, kernel_offsets, _, _ = build_out_coords_and_map(
-        in_coords, spatial_shape, kernel_size, stride, dilation, padding, transposed, with_map=False)
+        in_coords, spatial_shape, kernel_size, stride, dilation, padding, transposed, with_map=False,
+        chunk_size=chunk_size)
     return out_coords, new_shape, kernel_offsets

@@ -166,6 +166,35 @@ def test_build_out_coords_api(device):
     assert oc1 is one and oc1.shape[1] == 4
 
 
+@pytest.mark.parametrize("tr", [False, True])
+@pytest.mark.parametrize("chunk", [1, 4, 9, 26, 27, 100])
+def test_chunked_out_coords(device, tr, chunk):
+    """chunk_size orders the candidates chunk by chunk (kmap.py:270-278) and sizes the dedup table by the
+    distinct outputs (small chunks start with a table too small for them, which must grow)."""
+    rng = np.random.default_rng(chunk * 2 + tr)
+    S = 12
+    c = _rand_coords(rng, 400, S)
+    shape = (S, S, S)
+    off = O.target_offsets(3, 1, 1, tr)
+    ns = O.out_shape(shape, 3, 2, 1, 1, tr)
+    expect = O.bf_out_coords(c, off, 2, tr, ns, chunk=chunk)
+    ct = torch.as_tensor(c, dtype=torch.int16, device=device)
+    oc, ns_gpu, _ = build_out_coords(ct, shape, 3, stride=2, padding=1, transposed=tr, submanifold=False,
+                                     chunk_size=chunk)
+    assert tuple(ns_gpu) == tuple(ns)
+    assert (oc.cpu().numpy() == expect).all()
+    sp = SparseTensor(torch.zeros((c.shape[0], 1), device=device), ct, spatial_shape=shape)
+    table = _input_table(sp, 2 if tr else 1)
+    oc2, _, _, kmap, _ = build_out_coords_and_map(sp.C, shape, 3, 2, 1, 1, tr, in_table=table, with_map=True,
+                                                  chunk_size=chunk)
+    assert torch.equal(oc2, oc)
+    if tr:
+        nbr = O.exact_kmap(c, oc2.cpu().numpy(), off, 1, tuple(v * 2 for v in shape), in_scale=2)
+    else:
+        nbr = O.exact_kmap(c, oc2.cpu().numpy(), off, 2, shape)
+    assert (kmap.neighbor_indices.cpu().numpy() == nbr).all()
+
+
 def test_duplicate_inputs_use_table_row(device):
     c = np.array([[0, 2, 2, 2], [0, 3, 2, 2], [0, 2, 2, 2], [0, 5, 5, 5]], dtype=np.int32)
     out_coords, ns, _, kmap, _ = _strided(device, c, (8, 8, 8), 3, 2, 1, 1, False)
