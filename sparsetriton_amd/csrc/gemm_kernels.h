@@ -1398,11 +1398,17 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
       const int mode = wgrad16_mode();
       if (mode == 0 && Cin % 64 == 0 && Cout % 64 == 0 && vec_x && vec_y) {
         const unsigned grid = gx * (unsigned)((Cin / 64) * (Cout / 64));
+        // The kernel fits three workgroups per CU.  A grid of at most two
+        // rounds at two per CU reserves extra (unused) LDS to stay at two: a
+        // third workgroup per CU would not save a round there, only slow the
+        // other two down.
+        constexpr size_t kStatic = 4 * 2 * 32 * kWvPitch * sizeof(T) + (ST_MAX_KVOL + 1) * 4;
+        const size_t reserve = grid <= 1024 ? 72 * 1024 - kStatic : 0;
         if (rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T)))
-          wgrad_pairs_wave_kernel<T, true><<<grid, 256, 0, stream>>>(
+          wgrad_pairs_wave_kernel<T, true><<<grid, 256, reserve, stream>>>(
               X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
         else
-          wgrad_pairs_wave_kernel<T, false><<<grid, 256, 0, stream>>>(
+          wgrad_pairs_wave_kernel<T, false><<<grid, 256, reserve, stream>>>(
               X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
         ST_CHECK_LAUNCH();
         return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
