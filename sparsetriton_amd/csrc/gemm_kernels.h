@@ -885,19 +885,37 @@ constexpr int kWvPitch = 80;
 // group such a read hands lane l the element l mod 4 of the 4 elements lane
 // 4e + l/4 addresses, for e = 0..3; so lane c addresses pair 8g + 4h + c/4 at
 // channel col0 + 4 (c mod 4) and receives channel col0 + c of pairs 8g + 4h + e.
-template <typename F, typename T>
+template <typename F, typename T, int PITCH = kWvPitch>
 __device__ __forceinline__ F tr_frag(const T* st, int g, int c, int col0) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef short v8s __attribute__((ext_vector_type(8)));
   using lds_v4s = __attribute__((address_space(3))) v4s;
-  const T* p0 = st + (g * 8 + (c >> 2)) * kWvPitch + col0 + (c & 3) * 4;
+  const T* p0 = st + (g * 8 + (c >> 2)) * PITCH + col0 + (c & 3) * 4;
   const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 4 * kWvPitch));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 4 * PITCH));
   const v8s both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(F, both);
 }
 
-template <typename T, bool BUF>  // BUF: row loads through buffer resources (X and dY under 2 GB)
+// Row pitch (16-bit elements) of a per-wave stage of rows `width` channels
+// wide: the transpose reads of a fragment touch four rows at once, which land
+// on distinct 32-byte bank groups when the row stride is 32 or 96 bytes
+// modulo 128 (16, 48 or 80 elements).
+constexpr int wave_pitch(int width) { return width == 16 ? 16 : (width == 32 ? 48 : 80); }
+// LDS of wgrad_pairs_wave_kernel<T, ., MB, NB> (stage or cross-wave sum, plus the chunk starts)
+template <typename T, int MB, int NB>
+constexpr int wave_kernel_lds() {
+  constexpr int stage = 4 * 32 * (wave_pitch(16 * MB) + wave_pitch(16 * NB)) * (int)sizeof(T);
+  constexpr int rh = 16 * MB < 32 ? 16 * MB : 32;
+  constexpr int red = 4 * rh * (16 * NB + 4) * 4;
+  return (stage > red ? stage : red) + (ST_MAX_KVOL + 1) * 4;
+}
+
+// Channel tile of a workgroup: TM = 16 MB input channels x TN = 16 NB output
+// channels (16, 32 or 64 each; a wave computes the whole tile).  A row's TM
+// channels are CPR = TM / 8 chunks of 16 bytes, so one load instruction
+// covers RPI = 64 / CPR whole rows and a 32-pair step takes 32 / RPI of them.
+template <typename T, bool BUF, int MB, int NB>  // BUF: row loads through buffer resources (X and dY under 2 GB)
 __global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
                                                                const int32_t* __restrict__ kstart,
@@ -906,10 +924,15 @@ __global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __res
                                                                int Cin, int Cout, int64_t n_in, int64_t n_out, float* __restrict__ partials) {
   using F = typename Frag<T>::type;
   static_assert(Frag<T>::KSTEP == 32 && Frag<T>::VEC == 8, "16-bit MFMA fragments");
-  constexpr int STAGE = 32 * kWvPitch;  // elements per operand per wave
-  constexpr int STAGE_BYTES = 4 * 2 * STAGE * (int)sizeof(T);
-  constexpr int RP = 68;                // row pitch (floats) of the per-wave tiles summed at the end
-  constexpr int RED_BYTES = 4 * 32 * RP * (int)sizeof(float);  // half a tile per wave at a time
+  constexpr int TM = 16 * MB, TN = 16 * NB;
+  constexpr int CPRX = TM / 8, RPIX = 64 / CPRX, NVX = 32 / RPIX;
+  constexpr int CPRY = TN / 8, RPIY = 64 / CPRY, NVY = 32 / RPIY;
+  constexpr int PX = wave_pitch(TM), PY = wave_pitch(TN);
+  constexpr int STAGE = 32 * (PX + PY);  // elements per wave (X rows, then dY rows)
+  constexpr int STAGE_BYTES = 4 * STAGE * (int)sizeof(T);
+  constexpr int RP = TN + 4;            // row pitch (floats) of the per-wave tiles summed at the end
+  constexpr int RH = TM < 32 ? TM : 32; // rows summed per round
+  constexpr int RED_BYTES = 4 * RH * RP * (int)sizeof(float);
   __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -918,18 +941,15 @@ __global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __res
   __syncthreads();
   const int total = cstart_s[K];
 
-  const int ntn = Cout / 64;
-  const ChunkTile ct = chunk_tile(total, (Cin / 64) * ntn);
-  const int cm0 = (ct.tile / ntn) * 64, cn0 = (ct.tile % ntn) * 64;
-  T* xs = reinterpret_cast<T*>(lds) + wid * 2 * STAGE;
-  T* ys = xs + STAGE;
+  const int ntn = Cout / TN;
+  const ChunkTile ct = chunk_tile(total, (Cin / TM) * ntn);
+  const int cm0 = (ct.tile / ntn) * TM, cn0 = (ct.tile % ntn) * TN;
+  T* xs = reinterpret_cast<T*>(lds) + wid * STAGE;
+  T* ys = xs + 32 * PX;
   float* red = reinterpret_cast<float*>(lds);
-  // loader lanes: a step's 32 rows of 64 elements (128 bytes, one cache line)
-  // are read as 4 instructions of 8 whole rows -- 8 consecutive lanes take one
-  // row's 8 chunks of 16 bytes -- so no instruction splits a line with another.
-  // Each lane keeps pair (lane mod 32) and takes instruction v's row index
-  // from lane 8v + lane / 8.
-  const int lr = lane >> 3, lc = lane & 7;
+  // loader lanes: lane / CPR is the row within an instruction's RPI rows, lane % CPR its chunk;
+  // each lane keeps pair (lane mod 32) and takes instruction v's row index from lane v RPI + lane / CPR
+  const int lrx = lane / CPRX, lcx = lane % CPRX, lry = lane / CPRY, lcy = lane % CPRY;
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * (int64_t)sizeof(T) : 0);
   const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, BUF ? n_out * Cout * (int64_t)sizeof(T) : 0);
 
@@ -938,78 +958,79 @@ __global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __res
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
     const int p1 = min(p0 + chunk, kstart[k + 1]);
-    v4f acc[4][4];
+    v4f acc[MB][NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    F xr[4], yr[4];
+      for (int j = 0; j < NB; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    F xr[NVX], yr[NVY];
     auto load_step = [&](int q) {
       const int p = q + (lane & 31);
       int2 pr = make_int2(-1, -1);
       if (p < p1) pr = pairs[p];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int ix = __shfl(pr.x, v * 8 + lr, 64), iy = __shfl(pr.y, v * 8 + lr, 64);
-        if constexpr (BUF) {
-          xr[v] = load16<F>(x_rsrc, ix >= 0 ? (ix * Cin + cm0 + lc * 8) * (int)sizeof(T) : kOobOffset);
-          yr[v] = load16<F>(y_rsrc, iy >= 0 ? (iy * Cout + cn0 + lc * 8) * (int)sizeof(T) : kOobOffset);
-        } else {
-          xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lc * 8) : zero_frag<T>();
-          yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lc * 8) : zero_frag<T>();
-        }
+      for (int v = 0; v < NVX; ++v) {
+        const int ix = __shfl(pr.x, v * RPIX + lrx, 64);
+        if constexpr (BUF)
+          xr[v] = load16<F>(x_rsrc, ix >= 0 ? (ix * Cin + cm0 + lcx * 8) * (int)sizeof(T) : kOobOffset);
+        else
+          xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lcx * 8) : zero_frag<T>();
+      }
+#pragma unroll
+      for (int v = 0; v < NVY; ++v) {
+        const int iy = __shfl(pr.y, v * RPIY + lry, 64);
+        if constexpr (BUF)
+          yr[v] = load16<F>(y_rsrc, iy >= 0 ? (iy * Cout + cn0 + lcy * 8) * (int)sizeof(T) : kOobOffset);
+        else
+          yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lcy * 8) : zero_frag<T>();
       }
     };
     int q = p0 + wid * 32;
     if (q < p1) load_step(q);
     for (; q < p1; q += 128) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        *reinterpret_cast<F*>(&xs[(v * 8 + lr) * kWvPitch + lc * 8]) = xr[v];
-        *reinterpret_cast<F*>(&ys[(v * 8 + lr) * kWvPitch + lc * 8]) = yr[v];
-      }
+      for (int v = 0; v < NVX; ++v) *reinterpret_cast<F*>(&xs[(v * RPIX + lrx) * PX + lcx * 8]) = xr[v];
+#pragma unroll
+      for (int v = 0; v < NVY; ++v) *reinterpret_cast<F*>(&ys[(v * RPIY + lry) * PY + lcy * 8]) = yr[v];
       // LDS operations of one wave complete in order: the reads below see the
       // stores above; the fence keeps the compiler from moving them across.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (q + 128 < p1) load_step(q + 128);
-      F a[4], b[4];
+      F a[MB], b[NB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = tr_frag<F>(xs, g, c, i * 16);
-        b[i] = tr_frag<F>(ys, g, c, i * 16);
-      }
+      for (int i = 0; i < MB; ++i) a[i] = tr_frag<F, T, PX>(xs, g, c, i * 16);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < NB; ++j) b[j] = tr_frag<F, T, PY>(ys, g, c, j * 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    // sum the four waves' tiles through LDS, 32 rows at a time (so the sum
-    // area fits in the staging area); every thread then adds and stores 8
-    // elements of each half of the 64 x 64 partial, row-contiguous
+    // sum the four waves' tiles through LDS, RH rows at a time (so the sum
+    // area fits in the staging area); every thread then adds and stores
+    // elements of each round's rows of the TM x TN partial, row-contiguous
     float* part = partials + (int64_t)cidx * Cin * Cout;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < TM / RH; ++h) {
       __syncthreads();
-      float* mine = red + wid * 32 * RP;
+      float* mine = red + wid * RH * RP;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RH / 16; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * RP + j * 16 + c] = acc[h * 2 + i][j][r];
+          for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * RP + j * 16 + c] = acc[h * (RH / 16) + i][j][r];
       __syncthreads();
-#pragma unroll 4
-      for (int m = 0; m < 8; ++m) {
-        const int e = tid + m * 256;
-        const int row = e >> 6, col = e & 63;
-        const float s = red[row * RP + col] + red[32 * RP + row * RP + col] + red[64 * RP + row * RP + col] +
-                        red[96 * RP + row * RP + col];
-        part[(int64_t)(cm0 + h * 32 + row) * Cout + cn0 + col] = s;
+      for (int e = tid; e < RH * TN; e += 256) {
+        const int row = e / TN, col = e % TN;
+        const float s = red[row * RP + col] + red[RH * RP + row * RP + col] + red[2 * RH * RP + row * RP + col] +
+                        red[3 * RH * RP + row * RP + col];
+        part[(int64_t)(cm0 + h * RH + row) * Cout + cn0 + col] = s;
       }
     }
     __syncthreads();
@@ -1363,6 +1384,15 @@ static bool rows_fit_buffer(int64_t n_in, int Cin, int64_t n_out, int Cout, size
   return n_in * Cin * (int64_t)esz < (1ll << 31) - 64 && n_out * Cout * (int64_t)esz < (1ll << 31) - 64;
 }
 
+// 16-channel blocks of the per-wave weight-gradient tile for C channels: 1, 2
+// or 4 (C = 16, 32 or a multiple of 64), 0 when the kernel does not cover C.
+static int wave_tile_blocks(int C) {
+  if (C % 64 == 0) return 4;
+  if (C == 32) return 2;
+  if (C == 16) return 1;
+  return 0;
+}
+
 // 16-bit weight-gradient kernel: 0 = per-wave steps (default), 1 = workgroup
 // LDS transpose (ST_WGRAD16=lds selects it, for comparison runs).
 static int wgrad16_mode() {
@@ -1396,20 +1426,28 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
       const unsigned gx = wgrad_grid(max_chunks);
       const int2* pr = reinterpret_cast<const int2*>(pairs);
       const int mode = wgrad16_mode();
-      if (mode == 0 && Cin % 64 == 0 && Cout % 64 == 0 && vec_x && vec_y) {
-        const unsigned grid = gx * (unsigned)((Cin / 64) * (Cout / 64));
-        // The kernel fits three workgroups per CU.  A grid of at most two
+      const int mb = wave_tile_blocks(Cin), nb = wave_tile_blocks(Cout);
+      if (mode == 0 && mb && nb && vec_x && vec_y) {
+        const unsigned grid = gx * (unsigned)((Cin / (16 * mb)) * (Cout / (16 * nb)));
+        const bool buf = rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T));
+        // A 64 x 64 tile fits three workgroups per CU.  A grid of at most two
         // rounds at two per CU reserves extra (unused) LDS to stay at two: a
         // third workgroup per CU would not save a round there, only slow the
-        // other two down.
-        constexpr size_t kStatic = 4 * 2 * 32 * kWvPitch * sizeof(T) + (ST_MAX_KVOL + 1) * 4;
-        const size_t reserve = grid <= 1024 ? 72 * 1024 - kStatic : 0;
-        if (rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T)))
-          wgrad_pairs_wave_kernel<T, true><<<grid, 256, reserve, stream>>>(
-              X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
-        else
-          wgrad_pairs_wave_kernel<T, false><<<grid, 256, reserve, stream>>>(
-              X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);
+        // other two down.  (Smaller tiles fit many more and run in one round.)
+#define ST_WAVE(MB_, NB_)                                                                                         \
+  if (mb == MB_ && nb == NB_) {                                                                                   \
+    constexpr int lds = wave_kernel_lds<T, MB_, NB_>();                                                           \
+    const size_t reserve = (160 * 1024 / lds == 3 && grid <= 1024) ? 72 * 1024 - lds : 0;                        \
+    if (buf)                                                                                                      \
+      wgrad_pairs_wave_kernel<T, true, MB_, NB_><<<grid, 256, reserve, stream>>>(                                 \
+          X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                   \
+    else                                                                                                          \
+      wgrad_pairs_wave_kernel<T, false, MB_, NB_><<<grid, 256, reserve, stream>>>(                                \
+          X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                   \
+  }
+        ST_WAVE(1, 1) ST_WAVE(1, 2) ST_WAVE(1, 4) ST_WAVE(2, 1) ST_WAVE(2, 2) ST_WAVE(2, 4) ST_WAVE(4, 1)
+        ST_WAVE(4, 2) ST_WAVE(4, 4)
+#undef ST_WAVE
         ST_CHECK_LAUNCH();
         return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
       }
