@@ -445,6 +445,14 @@ int st_to_dense(const void* feats, int64_t n, int C, int dtype, const void* coor
 int st_from_dense(const void* dense, int64_t batches, int64_t sx, int64_t sy, int64_t sz, int C, int dtype,
                   const void* coords, int coord_dtype, int64_t n, void* feats, st_stream_t stream);
 
+/*
+ * mask_spatial_range (utils/spatial/tile.py:16-85): mask[r] = 1 when row r's
+ * (x, y, z) lies in [limits[0], limits[1]] x [limits[2], limits[3]] x
+ * [limits[4], limits[5]] (inclusive; a host array of 6), else 0.
+ */
+int st_mask_spatial_range(const void* coords, int coord_dtype, int64_t n, const int64_t* limits, uint8_t* mask,
+                          st_stream_t stream);
+
 /* ------------------------------------------------------------ pooling, upsampling
  *
  * sparse_pooling (nn/functional/spatial.py:26-233): row r of coords goes to

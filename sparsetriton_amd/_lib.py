@@ -99,6 +99,7 @@ _SIGNATURES = {
     "st_hashfly_gemm": [_P, _L, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _P, _P, _P, _I, _I, _I, _P],
     "st_to_dense": [_P, _L, _I, _I, _P, _I, _L, _L, _L, _L, _P, _P],
     "st_from_dense": [_P, _L, _L, _L, _L, _I, _I, _P, _I, _L, _P, _P],
+    "st_mask_spatial_range": [_P, _I, _L, ctypes.POINTER(_L), _P, _P],
     "st_pool_workspace": [_L, ctypes.POINTER(ctypes.c_size_t)],
     "st_pool_plan": [_P, _I, _L, _I, _I, _I, _P, ctypes.c_size_t, _P, _P, _P, _P, _P, _P],
     "st_pool_forward": [_P, _I, _I, _P, _P, _L, _I, _P, _P],

@@ -107,6 +107,41 @@ __device__ __forceinline__ uint32_t insert_slot(uint64_t* __restrict__ keys, uin
   return ST_NO_VAL;
 }
 
+// insert_slot continued from slot s whose key `k` the caller already loaded
+// (so a batch of inserts can have their first loads in flight together).
+__device__ __forceinline__ uint32_t insert_slot_from(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
+                                                     uint32_t s, uint64_t k, bool& was_new) {
+  for (uint32_t step = 0; step < cap; ++step) {
+    if (k == key) {
+      was_new = false;
+      return s;
+    }
+    if (k == ST_EMPTY_KEY) {
+      unsigned long long old =
+          atomicCAS((unsigned long long*)&keys[s], (unsigned long long)ST_EMPTY_KEY, (unsigned long long)key);
+      if (old == ST_EMPTY_KEY) {
+        was_new = true;
+        return s;
+      }
+      if (old == key) {
+        was_new = false;
+        return s;
+      }
+    }
+    s = next_slot(s, cap);
+    k = keys[s];
+  }
+  return ST_NO_VAL;
+}
+
+// (b, x, y, z) of a key made by pack_key
+__device__ __forceinline__ void unpack_key(uint64_t key, int64_t& b, int64_t& x, int64_t& y, int64_t& z) {
+  b = (int64_t)(key >> 48);
+  x = (int16_t)(uint16_t)(key >> 32);
+  y = (int16_t)(uint16_t)(key >> 16);
+  z = (int16_t)(uint16_t)key;
+}
+
 // ------------------------------------------------------- occupancy bitmap
 
 // Device view of an st_occupancy (words == nullptr: no bitmap, always probe).

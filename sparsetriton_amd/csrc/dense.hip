@@ -83,6 +83,18 @@ static int dense_move(const void* src, void* dst, int64_t n, int C, size_t esz, 
   return ST_OK;
 }
 
+// mask[r] = 1 when coords[r] (x, y, z) lies in [lo, hi] on every axis
+template <typename CT>
+__global__ __launch_bounds__(256) void mask_range_kernel(const CT* __restrict__ coords, int64_t n, int64_t x0,
+                                                         int64_t x1, int64_t y0, int64_t y1, int64_t z0, int64_t z1,
+                                                         uint8_t* __restrict__ mask) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= n) return;
+  const CT* p = coords + r * 4;
+  const int64_t x = p[1], y = p[2], z = p[3];
+  mask[r] = (x >= x0 && x <= x1 && y >= y0 && y <= y1 && z >= z0 && z <= z1) ? 1 : 0;
+}
+
 }  // namespace st
 
 using namespace st;
@@ -130,6 +142,18 @@ int st_from_dense(const void* dense, int64_t batches, int64_t sx, int64_t sy, in
   ST_DISPATCH_COORD(coord_dtype, CT,
                     return dense_move<CT>(dense, feats, n, C, esz, (const CT*)coords, batches, sx, sy, sz, false,
                                           stream));
+  return ST_OK;
+}
+
+int st_mask_spatial_range(const void* coords, int coord_dtype, int64_t n, const int64_t* limits, uint8_t* mask,
+                          st_stream_t stream) {
+  if (n < 0 || !limits) return ST_ERR_ARG;
+  if (n == 0) return ST_OK;
+  if (!coords || !mask) return ST_ERR_ARG;
+  ST_DISPATCH_COORD(coord_dtype, CT,
+                    mask_range_kernel<CT><<<st_blocks(n, 256), 256, 0, stream>>>(
+                        (const CT*)coords, n, limits[0], limits[1], limits[2], limits[3], limits[4], limits[5], mask));
+  ST_CHECK_LAUNCH();
   return ST_OK;
 }
 

@@ -70,6 +70,27 @@ __device__ __forceinline__ void load_offsets(int32_t* off_s, const int32_t* __re
   __syncthreads();
 }
 
+// The read-only passes handle candidates kCandGroup offsets at a time: the
+// group's keys and home slots are computed first and their first probes
+// loaded together, so a thread has up to kCandGroup random loads in flight.
+constexpr int kCandGroup = 9;
+
+// Key of candidate (input (b, x, y, z), offset k), or false when filtered out;
+// *bad is set when it passes the filters but cannot be packed.
+__device__ __forceinline__ bool cand_key(const Geom& g, const int32_t* off_s, int64_t b, int64_t x, int64_t y,
+                                         int64_t z, int k, uint64_t& key, bool& bad) {
+  int64_t ox, oy, oz;
+  if (!candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz)) return false;
+  if (!pack_key(b, ox, oy, oz, key)) {
+    bad = true;
+    return false;
+  }
+  return true;
+}
+
+// Inserts stay one candidate at a time: batching their first probes (as the
+// read-only passes below do) put more CAS traffic on hot slots at once and
+// measured slower.
 template <typename CT>
 __global__ __launch_bounds__(256) void cand_insert_kernel(const CT* __restrict__ coords, int64_t n,
                                                           const int32_t* __restrict__ offsets, Geom g,
@@ -82,11 +103,10 @@ __global__ __launch_bounds__(256) void cand_insert_kernel(const CT* __restrict__
   int64_t b, x, y, z;
   load_coord(coords, i, b, x, y, z);
   for (int k = 0; k < g.K; ++k) {
-    int64_t ox, oy, oz;
-    if (!candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz)) continue;
     uint64_t key;
-    if (!pack_key(b, ox, oy, oz, key)) {
-      atomicAdd(&status[ST_STATUS_BAD_COORD], 1);
+    bool bad = false;
+    if (!cand_key(g, off_s, b, x, y, z, k, key, bad)) {
+      if (bad) atomicAdd(&status[ST_STATUS_BAD_COORD], 1);
       continue;
     }
     bool was_new;
@@ -109,15 +129,32 @@ __device__ __forceinline__ int first_candidates(const CT* __restrict__ coords, i
   int64_t b, x, y, z;
   load_coord(coords, i, b, x, y, z);
   int cnt = 0;
-  for (int k = k0; k < k1; ++k) {
-    int64_t ox, oy, oz;
-    if (!candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz)) continue;
-    uint64_t key;
-    if (!pack_key(b, ox, oy, oz, key)) continue;
-    uint32_t s = find_slot(dkeys, dcap, key);
-    if (s == ST_NO_VAL || dvals[s] != cand_rank(g, n, i, k)) continue;
-    on_first(s, b, ox, oy, oz);
-    ++cnt;
+  for (int kb = k0; kb < k1; kb += kCandGroup) {
+    uint64_t key[kCandGroup], first[kCandGroup];
+    uint32_t slot[kCandGroup], val[kCandGroup];
+    bool ok[kCandGroup];
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) {
+      bool bd = false;
+      ok[j] = kb + j < k1 && cand_key(g, off_s, b, x, y, z, kb + j, key[j], bd);
+      slot[j] = ok[j] ? home_slot(key[j], dcap) : 0u;
+      first[j] = ok[j] ? dkeys[slot[j]] : ST_EMPTY_KEY;
+    }
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) {
+      if (ok[j]) slot[j] = find_slot_from(dkeys, dcap, key[j], slot[j], first[j]);
+      ok[j] = ok[j] && slot[j] != ST_NO_VAL;
+    }
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) val[j] = ok[j] ? dvals[slot[j]] : ST_NO_VAL;
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) {
+      if (!ok[j] || val[j] != cand_rank(g, n, i, kb + j)) continue;
+      int64_t ob, ox, oy, oz;
+      unpack_key(key[j], ob, ox, oy, oz);
+      on_first(slot[j], ob, ox, oy, oz);
+      ++cnt;
+    }
   }
   return cnt;
 }
@@ -257,24 +294,38 @@ __global__ __launch_bounds__(256) void cand_map_kernel(const CT* __restrict__ co
   }
   const int W = (g.K + 31) >> 5;
   uint32_t mword = 0;
-  for (int k = 0; k < g.K; ++k) {
-    int64_t ox, oy, oz;
-    uint64_t key;
-    uint32_t o = ST_NO_VAL;
-    if (candidate(g, x, y, z, off_s[3 * k], off_s[3 * k + 1], off_s[3 * k + 2], ox, oy, oz) &&
-        pack_key(b, ox, oy, oz, key)) {
-      const uint32_t s = find_slot(dkeys, dcap, key);
-      if (s != ST_NO_VAL) o = slot_out[s];
+  for (int kb = 0; kb < g.K; kb += kCandGroup) {
+    uint64_t key[kCandGroup], first[kCandGroup];
+    uint32_t slot[kCandGroup], o[kCandGroup];
+    bool ok[kCandGroup];
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) {
+      bool bd = false;
+      ok[j] = kb + j < g.K && cand_key(g, off_s, b, x, y, z, kb + j, key[j], bd);
+      slot[j] = ok[j] ? home_slot(key[j], dcap) : 0u;
+      first[j] = ok[j] ? dkeys[slot[j]] : ST_EMPTY_KEY;
     }
-    if (o != ST_NO_VAL && (int64_t)o < n_out) {
-      invnbr[(int64_t)k * n + i] = (int32_t)o;
-      nbr[(int64_t)k * n_out + o] = (int32_t)i;
-      atomicOr(&out_masks[(int64_t)o * W + (k >> 5)], 1u << (k & 31));
-      mword |= 1u << (k & 31);
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) {
+      if (ok[j]) slot[j] = find_slot_from(dkeys, dcap, key[j], slot[j], first[j]);
+      ok[j] = ok[j] && slot[j] != ST_NO_VAL;
     }
-    if ((k & 31) == 31 || k == g.K - 1) {
-      in_masks[i * W + (k >> 5)] = mword;
-      mword = 0;
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) o[j] = ok[j] ? slot_out[slot[j]] : ST_NO_VAL;
+#pragma unroll
+    for (int j = 0; j < kCandGroup; ++j) {
+      const int k = kb + j;
+      if (k >= g.K) break;
+      if (o[j] != ST_NO_VAL && (int64_t)o[j] < n_out) {
+        invnbr[(int64_t)k * n + i] = (int32_t)o[j];
+        nbr[(int64_t)k * n_out + o[j]] = (int32_t)i;
+        atomicOr(&out_masks[(int64_t)o[j] * W + (k >> 5)], 1u << (k & 31));
+        mword |= 1u << (k & 31);
+      }
+      if ((k & 31) == 31 || k == g.K - 1) {
+        in_masks[i * W + (k >> 5)] = mword;
+        mword = 0;
+      }
     }
   }
 }

@@ -66,3 +66,17 @@ def test_sparse_tensor_dense(device):
     d = sp.dense()
     assert d.shape == (2, 4, 4, 4, 2)
     assert d[0, 1, 2, 3].tolist() == [0.0, 1.0] and d[0, 3, 3, 3].tolist() == [4.0, 5.0]
+
+
+@pytest.mark.parametrize("cdt", [torch.int16, torch.int32, torch.int64])
+def test_mask_spatial_range(device, cdt):
+    from sparsetriton_amd.utils import mask_spatial_range
+
+    rng = np.random.default_rng(3)
+    c = rng.integers(-5, 20, (1000, 4))
+    ct = torch.as_tensor(c, device=device).to(cdt)
+    m = mask_spatial_range(ct, (0, 9), (2, None), (None, 15)).cpu().numpy()
+    ref = (c[:, 1] >= 0) & (c[:, 1] <= 9) & (c[:, 2] >= 2) & (c[:, 3] <= 15)
+    assert (m == ref).all()
+    assert mask_spatial_range(ct).all()
+    assert mask_spatial_range(ct[:0]).shape == (0,)
