@@ -31,13 +31,13 @@ namespace st {
 constexpr int kGemmBM = 128;
 constexpr int kSrcGroup = 32;  // offsets whose source rows are resolved into LDS at once
 
-template <typename T, int BN, typename Src>
+template <typename T, int BN, typename Src, typename E>
 __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ A, Src src,
                                                           const uint32_t* __restrict__ masks, int W,
                                                           const int32_t* __restrict__ perm, const T* __restrict__ Bt,
                                                           T* __restrict__ out, int64_t n_src, int64_t n_dst, int K,
                                                           int Kd, int Nd, int vec_a, int vec_b,
-                                                          Epi<T> epi) {
+                                                          E epi) {
   using F = typename Frag<T>::type;
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -147,11 +147,11 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
 // Tile row r is destination row rows[r] (the mask-sorted permutation) or r
 // itself when rows is null; the map, the row masks and the hash-fly
 // coordinates are indexed by destination row.
-template <typename T, int BN, int KS, typename Src>
+template <typename T, int BN, int KS, typename Src, typename E>
 __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
-    int vec_b, Epi<T> epi) {
+    int vec_b, E epi) {
   using F = typename Frag<T>::type;
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -366,11 +366,11 @@ static inline unsigned ring_grid(int64_t n_dst, int Nd, int BN) {
 // Per step i: issue offset i+D-1's loads, store offset i's B tile into LDS
 // (double-buffered), barrier, MFMAs on offset i.  Requires Kd a multiple of
 // KS * KSTEP and 16-byte aligned A and Bt (every full-vector case).
-template <typename T, int BN, int KS, int D, typename Src, bool LINES>
+template <typename T, int BN, int KS, int D, typename Src, bool LINES, typename E>
 __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
     const T* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const T* __restrict__ Bt, T* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
-    int vec_b, Epi<T> epi) {
+    int vec_b, E epi) {
   using F = typename Frag<T>::type;
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
@@ -902,21 +902,14 @@ __device__ __forceinline__ F tr_frag(const T* st, int g, int c, int col0) {
 // on distinct 32-byte bank groups when the row stride is 32 or 96 bytes
 // modulo 128 (16, 48 or 80 elements).
 constexpr int wave_pitch(int width) { return width == 16 ? 16 : (width == 32 ? 48 : 80); }
-// LDS of wgrad_pairs_wave_kernel<T, ., MB, NB> (stage or cross-wave sum, plus the chunk starts)
-template <typename T, int MB, int NB>
-constexpr int wave_kernel_lds() {
-  constexpr int stage = 4 * 32 * (wave_pitch(16 * MB) + wave_pitch(16 * NB)) * (int)sizeof(T);
-  constexpr int rh = 16 * MB < 32 ? 16 * MB : 32;
-  constexpr int red = 4 * rh * (16 * NB + 4) * 4;
-  return (stage > red ? stage : red) + (ST_MAX_KVOL + 1) * 4;
-}
-
 // Channel tile of a workgroup: TM = 16 MB input channels x TN = 16 NB output
 // channels (16, 32 or 64 each; a wave computes the whole tile).  A row's TM
 // channels are CPR = TM / 8 chunks of 16 bytes, so one load instruction
 // covers RPI = 64 / CPR whole rows and a 32-pair step takes 32 / RPI of them.
-template <typename T, bool BUF, int MB, int NB>  // BUF: row loads through buffer resources (X and dY under 2 GB)
-__global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
+// ONEPASS sums the four waves' tiles through LDS in one round (more LDS: two
+// workgroups per CU for a 64 x 64 tile) instead of rounds of 32 rows (three).
+template <typename T, bool BUF, int MB, int NB, bool ONEPASS>  // BUF: row loads through buffer resources (X and dY under 2 GB)
+__global__ __launch_bounds__(256, ONEPASS ? 2 : 3) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
                                                                const int32_t* __restrict__ kstart,
                                                                const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
@@ -931,7 +924,7 @@ __global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __res
   constexpr int STAGE = 32 * (PX + PY);  // elements per wave (X rows, then dY rows)
   constexpr int STAGE_BYTES = 4 * STAGE * (int)sizeof(T);
   constexpr int RP = TN + 4;            // row pitch (floats) of the per-wave tiles summed at the end
-  constexpr int RH = TM < 32 ? TM : 32; // rows summed per round
+  constexpr int RH = (ONEPASS || TM < 32) ? TM : 32;  // rows summed per round
   constexpr int RED_BYTES = 4 * RH * RP * (int)sizeof(float);
   __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
@@ -968,30 +961,33 @@ __global__ __launch_bounds__(256, 3) void wgrad_pairs_wave_kernel(const T* __res
       const int p = q + (lane & 31);
       int2 pr = make_int2(-1, -1);
       if (p < p1) pr = pairs[p];
+      // X and dY loads interleaved (x0, y0, x1, y1, ...)
 #pragma unroll
-      for (int v = 0; v < NVX; ++v) {
-        const int ix = __shfl(pr.x, v * RPIX + lrx, 64);
-        if constexpr (BUF)
-          xr[v] = load16<F>(x_rsrc, ix >= 0 ? (ix * Cin + cm0 + lcx * 8) * (int)sizeof(T) : kOobOffset);
-        else
-          xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lcx * 8) : zero_frag<T>();
-      }
-#pragma unroll
-      for (int v = 0; v < NVY; ++v) {
-        const int iy = __shfl(pr.y, v * RPIY + lry, 64);
-        if constexpr (BUF)
-          yr[v] = load16<F>(y_rsrc, iy >= 0 ? (iy * Cout + cn0 + lcy * 8) * (int)sizeof(T) : kOobOffset);
-        else
-          yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lcy * 8) : zero_frag<T>();
+      for (int v = 0; v < (NVX > NVY ? NVX : NVY); ++v) {
+        if (v < NVX) {
+          const int ix = __shfl(pr.x, v * RPIX + lrx, 64);
+          if constexpr (BUF)
+            xr[v] = load16<F>(x_rsrc, ix >= 0 ? (ix * Cin + cm0 + lcx * 8) * (int)sizeof(T) : kOobOffset);
+          else
+            xr[v] = ix >= 0 ? *reinterpret_cast<const F*>(X + (int64_t)ix * Cin + cm0 + lcx * 8) : zero_frag<T>();
+        }
+        if (v < NVY) {
+          const int iy = __shfl(pr.y, v * RPIY + lry, 64);
+          if constexpr (BUF)
+            yr[v] = load16<F>(y_rsrc, iy >= 0 ? (iy * Cout + cn0 + lcy * 8) * (int)sizeof(T) : kOobOffset);
+          else
+            yr[v] = iy >= 0 ? *reinterpret_cast<const F*>(dY + (int64_t)iy * Cout + cn0 + lcy * 8) : zero_frag<T>();
+        }
       }
     };
     int q = p0 + wid * 32;
     if (q < p1) load_step(q);
     for (; q < p1; q += 128) {
 #pragma unroll
-      for (int v = 0; v < NVX; ++v) *reinterpret_cast<F*>(&xs[(v * RPIX + lrx) * PX + lcx * 8]) = xr[v];
-#pragma unroll
-      for (int v = 0; v < NVY; ++v) *reinterpret_cast<F*>(&ys[(v * RPIY + lry) * PY + lcy * 8]) = yr[v];
+      for (int v = 0; v < (NVX > NVY ? NVX : NVY); ++v) {
+        if (v < NVX) *reinterpret_cast<F*>(&xs[(v * RPIX + lrx) * PX + lcx * 8]) = xr[v];
+        if (v < NVY) *reinterpret_cast<F*>(&ys[(v * RPIY + lry) * PY + lcy * 8]) = yr[v];
+      }
       // LDS operations of one wave complete in order: the reads below see the
       // stores above; the fence keeps the compiler from moving them across.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1237,28 +1233,28 @@ static bool buffer_ok(int64_t n_src, int K, int Kd, int Nd, size_t esz) {
   return n_src * Kd * (int64_t)esz < (1ll << 31) - 64 && (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
 }
 
-template <typename T, int BN, int KS, typename Src>
+template <typename T, int BN, int KS, typename Src, typename E>
 static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W, const int32_t* rows,
-                        const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
+                        const T* Bt, T* out, E epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
   const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   // (IEEE fp32 keeps the register path: its MFMAs dominate and the A stage only costs occupancy there)
   if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2 &&
       buffer_ok(n_src, K, Kd, Nd, sizeof(T)))
-    gather_gemm_ring_kernel<T, BN, KS, 2, Src, true>
+    gather_gemm_ring_kernel<T, BN, KS, 2, Src, true, E>
         <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
   else if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2)
-    gather_gemm_ring_kernel<T, BN, KS, 2, Src, false>
+    gather_gemm_ring_kernel<T, BN, KS, 2, Src, false, E>
         <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
   else
-    gather_gemm_pipe_kernel<T, BN, KS, Src>
+    gather_gemm_pipe_kernel<T, BN, KS, Src, E>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
 }
 
-template <typename T, int KS, typename Src>
+template <typename T, int KS, typename Src, typename E>
 static void launch_pipe_ks(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                           const int32_t* rows, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
+                           const int32_t* rows, const T* Bt, T* out, E epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a,
                            int vec_b, hipStream_t stream) {
   constexpr int LDS128 = 2 * 128 * (KS * Frag<T>::KSTEP + Frag<T>::VEC) * (int)sizeof(T) + kSrcGroup * kGemmBM * 4;
   if (Nd <= 16)
@@ -1271,10 +1267,10 @@ static void launch_pipe_ks(const T* A, int64_t n_src, const Src& src, const uint
     launch_pipe<T, 128, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
 }
 
-template <typename T, typename Src>
-static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                         const int32_t* rows, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd,
-                         hipStream_t stream) {
+template <typename T, typename Src, typename E>
+static int launch_gather_e(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                           const int32_t* rows, const T* Bt, T* out, E epi, int64_t n_dst, int K, int Kd, int Nd,
+                           hipStream_t stream) {
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
   const int vec_a = (Kd % VEC == 0) && ((uintptr_t)A % 16 == 0);
@@ -1292,20 +1288,36 @@ static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32
     // Deep reductions: the single-buffered kernel stages Bt in chunks.
     const unsigned gx = st_blocks(n_dst, kGemmBM);
     if (Nd <= 16)
-      gather_gemm_kernel<T, 16, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
+      gather_gemm_kernel<T, 16, Src, E><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
                                                                        K, Kd, Nd, vec_a, vec_b, epi);
     else if (Nd <= 32)
-      gather_gemm_kernel<T, 32, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
+      gather_gemm_kernel<T, 32, Src, E><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
                                                                        K, Kd, Nd, vec_a, vec_b, epi);
     else if (Nd <= 64)
-      gather_gemm_kernel<T, 64, Src><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
+      gather_gemm_kernel<T, 64, Src, E><<<dim3(gx, 1), 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst,
                                                                        K, Kd, Nd, vec_a, vec_b, epi);
     else
-      gather_gemm_kernel<T, 128, Src><<<dim3(gx, st_blocks(Nd, 128)), 256, 0, stream>>>(
+      gather_gemm_kernel<T, 128, Src, E><<<dim3(gx, st_blocks(Nd, 128)), 256, 0, stream>>>(
           A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
   }
   ST_CHECK_LAUNCH();
   return ST_OK;
+}
+
+// The general store epilogue (affine map, residual, ReLU) runs on the tiled
+// kernels only; everything else stores acc + bias.
+template <typename T, typename Src>
+static int launch_gather(const T* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                         const int32_t* rows, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd,
+                         hipStream_t stream) {
+  if (epi.scale || epi.shift || epi.residual || epi.relu) {
+    if constexpr (Src::kTiled)
+      return launch_gather_e<T, Src, Epi<T>>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, stream);
+    else
+      return ST_ERR_UNSUPPORTED;
+  }
+  return launch_gather_e<T, Src, BiasEpi<T>>(A, n_src, src, masks, W, rows, Bt, out, BiasEpi<T>{epi.bias}, n_dst,
+                                              K, Kd, Nd, stream);
 }
 
 static int launch_wgrad_reduce(const float* partials, const int32_t* cstart_or_null, int64_t splits, int K,
@@ -1430,20 +1442,27 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
       if (mode == 0 && mb && nb && vec_x && vec_y) {
         const unsigned grid = gx * (unsigned)((Cin / (16 * mb)) * (Cout / (16 * nb)));
         const bool buf = rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T));
-        // A 64 x 64 tile fits three workgroups per CU.  A grid of at most two
-        // rounds at two per CU reserves extra (unused) LDS to stay at two: a
-        // third workgroup per CU would not save a round there, only slow the
-        // other two down.  (Smaller tiles fit many more and run in one round.)
+        // A 64 x 64 tile with its cross-wave sum in 32-row rounds fits three
+        // workgroups per CU.  A grid of at most two rounds at two per CU takes
+        // the one-round sum instead (two per CU): a third workgroup per CU
+        // would not save a round there, only slow the other two down.
+        const bool onepass = grid <= 1024;
 #define ST_WAVE(MB_, NB_)                                                                                         \
   if (mb == MB_ && nb == NB_) {                                                                                   \
-    constexpr int lds = wave_kernel_lds<T, MB_, NB_>();                                                           \
-    const size_t reserve = (160 * 1024 / lds == 3 && grid <= 1024) ? 72 * 1024 - lds : 0;                        \
-    if (buf)                                                                                                      \
-      wgrad_pairs_wave_kernel<T, true, MB_, NB_><<<grid, 256, reserve, stream>>>(                                 \
+    if (onepass && MB_ == 4) {                                                                                    \
+      if (buf)                                                                                                    \
+        wgrad_pairs_wave_kernel<T, true, MB_, NB_, true><<<grid, 256, 0, stream>>>(                               \
+            X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                 \
+      else                                                                                                        \
+        wgrad_pairs_wave_kernel<T, false, MB_, NB_, true><<<grid, 256, 0, stream>>>(                              \
+            X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                 \
+    } else if (buf) {                                                                                             \
+      wgrad_pairs_wave_kernel<T, true, MB_, NB_, false><<<grid, 256, 0, stream>>>(                                \
           X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                   \
-    else                                                                                                          \
-      wgrad_pairs_wave_kernel<T, false, MB_, NB_><<<grid, 256, reserve, stream>>>(                                \
+    } else {                                                                                                      \
+      wgrad_pairs_wave_kernel<T, false, MB_, NB_, false><<<grid, 256, 0, stream>>>(                               \
           X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                   \
+    }                                                                                                             \
   }
         ST_WAVE(1, 1) ST_WAVE(1, 2) ST_WAVE(1, 4) ST_WAVE(2, 1) ST_WAVE(2, 2) ST_WAVE(2, 4) ST_WAVE(4, 1)
         ST_WAVE(4, 2) ST_WAVE(4, 4)

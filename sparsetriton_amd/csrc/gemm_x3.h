@@ -48,11 +48,11 @@ __device__ __forceinline__ v4f mfma_x3(const v8bf& ah, const v8bf& al, const v8b
 // workgroup (a wave owns 32), BN output columns, the tile's active offsets
 // in klist order, sources of up to kSrcGroup offsets resolved into LDS at
 // once.  Reduction steps are 32 wide (KS steps cover Kd).
-template <int BN, int KS, typename Src>
+template <int BN, int KS, typename Src, typename E>
 __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
     const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd,
-    int vec_a, int vec_b, Epi<float> epi) {
+    int vec_a, int vec_b, E epi) {
   constexpr int KDP = KS * 32;
   constexpr int PITCH = KDP + 8;  // bf16 elements per LDS row of the B tile
   constexpr int NBLK = BN / 16;
@@ -255,11 +255,11 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
 // tile are loaded D-1 offsets ahead into a register ring; B is split into
 // hi / lo planes when stored to LDS, A when it is used.  Requires Kd =
 // KS * 32 and 16-byte aligned A and Bt.
-template <int BN, int KS, int D, typename Src, bool LINES>
+template <int BN, int KS, int D, typename Src, bool LINES, typename E>
 __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
     const float* __restrict__ A, Src src, const uint32_t* __restrict__ masks, int W, const int32_t* __restrict__ rows,
     const float* __restrict__ Bt, float* __restrict__ out, int64_t n_src, int64_t n_dst, int K, int Kd, int Nd,
-    Epi<float> epi) {
+    E epi) {
   constexpr int KDP = KS * 32;
   constexpr int PITCH = KDP + 8;
   constexpr int NBLK = BN / 16;
@@ -711,26 +711,26 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
 
 // ------------------------------------------------------------ launchers
 
-template <int BN, int KS, typename Src>
+template <int BN, int KS, typename Src, typename E>
 static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                      const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
+                      const int32_t* rows, const float* Bt, float* out, E epi, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
   const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines() && buffer_ok(n_src, K, Kd, Nd, 4))
-    gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true>
+    gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true, E>
         <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, epi);
   else if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2)
-    gather_gemm_ring_x3_kernel<BN, KS, 2, Src, false>
+    gather_gemm_ring_x3_kernel<BN, KS, 2, Src, false, E>
         <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, epi);
   else
-    gather_gemm_x3_kernel<BN, KS, Src>
+    gather_gemm_x3_kernel<BN, KS, Src, E>
         <<<grid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, vec_a, vec_b, epi);
 }
 
-template <int KS, typename Src>
+template <int KS, typename Src, typename E>
 static void launch_x3_ks(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                         const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
+                         const int32_t* rows, const float* Bt, float* out, E epi, int64_t n_dst, int K, int Kd, int Nd,
                          int vec_a, int vec_b, hipStream_t stream) {
   if (Nd <= 16)
     launch_x3<16, KS>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
@@ -742,16 +742,16 @@ static void launch_x3_ks(const float* A, int64_t n_src, const Src& src, const ui
 
 // Split-operand gather-GEMM for reductions up to 128 wide; deeper ones use
 // the plain fp32 kernels.
-template <typename Src>
-static int launch_gather_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
-                            const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
-                            hipStream_t stream) {
+template <typename Src, typename E>
+static int launch_gather_x3_e(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                              const int32_t* rows, const float* Bt, float* out, E epi, int64_t n_dst, int K, int Kd,
+                              int Nd, hipStream_t stream) {
   const int ks = (Kd + 31) / 32;
   if (ks > 4) {
     if constexpr (Src::kTiled)
       return ST_ERR_UNSUPPORTED;
     else
-      return launch_gather<float>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, stream);
+      return launch_gather_e<float, Src, E>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, stream);
   }
   const int vec_a = (Kd % 4 == 0) && ((uintptr_t)A % 16 == 0);
   const int vec_b = (Kd % 4 == 0) && ((uintptr_t)Bt % 16 == 0);
@@ -763,6 +763,21 @@ static int launch_gather_x3(const float* A, int64_t n_src, const Src& src, const
     launch_x3_ks<4>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd, vec_a, vec_b, stream);
   ST_CHECK_LAUNCH();
   return ST_OK;
+}
+
+template <typename Src>
+static int launch_gather_x3(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
+                            const int32_t* rows, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K,
+                            int Kd, int Nd, hipStream_t stream) {
+  if (epi.scale || epi.shift || epi.residual || epi.relu) {
+    if constexpr (Src::kTiled)
+      return launch_gather_x3_e<Src, Epi<float>>(A, n_src, src, masks, W, rows, Bt, out, epi, n_dst, K, Kd, Nd,
+                                                 stream);
+    else
+      return ST_ERR_UNSUPPORTED;
+  }
+  return launch_gather_x3_e<Src, BiasEpi<float>>(A, n_src, src, masks, W, rows, Bt, out, BiasEpi<float>{epi.bias},
+                                                 n_dst, K, Kd, Nd, stream);
 }
 
 }  // namespace st

@@ -127,6 +127,20 @@ struct Epi {
     return (relu && v < 0.f) ? 0.f : v;  // (a NaN stays NaN, as under torch.relu)
   }
 };
+// The store epilogue of the plain convolution: acc + bias[c] and nothing
+// else, so the store loop has no other memory access (the general epilogue's
+// possible residual read, which may alias the output, serialises the stores:
+// the split-fp32 gather measured 152 vs 184 us).
+template <typename T>
+struct BiasEpi {
+  const T* bias;
+  __device__ __forceinline__ void column(int col, int Nd, float& mul, float& add) const {
+    mul = 1.f;
+    add = (bias && col < Nd) ? (float)bias[col] : 0.f;
+  }
+  __device__ __forceinline__ float apply(float acc, float, float add, int64_t, int, int) const { return acc + add; }
+};
+
 template <typename T>
 inline Epi<T> bias_epi(const void* bias) {
   return Epi<T>{(const T*)bias, nullptr, nullptr, nullptr, 0};
