@@ -124,19 +124,49 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ 
   float em[NBLK], ea[NBLK];
 #pragma unroll
   for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
+  if constexpr (E::kReads) {
+    // values first, stores after: an epilogue that reads (the residual) issues
+    // all its loads before the first store, which may alias them
+    float ov[2][4][NBLK];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
-      if (drow < 0) continue;
-      T* orow = out + (int64_t)drow * Nd;
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
 #pragma unroll
-      for (int nb = 0; nb < NBLK; ++nb) {
-        const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          ov[m][r][nb] = (drow >= 0 && col < Nd) ? epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col) : 0.f;
+        }
       }
-    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+        if (drow < 0) continue;
+        T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          if (col < Nd) orow[col] = from_f32<T>(ov[m][r][nb]);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+        if (drow < 0) continue;
+        T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
+        }
+      }
+  }
 }
 
 // Pipelined gather-GEMM for reduction depths known at compile time
@@ -318,19 +348,49 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
   float em[NBLK], ea[NBLK];
 #pragma unroll
   for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
+  if constexpr (E::kReads) {
+    // values first, stores after: an epilogue that reads (the residual) issues
+    // all its loads before the first store, which may alias them
+    float ov[2][4][NBLK];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
-      if (drow < 0) continue;
-      T* orow = out + (int64_t)drow * Nd;
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
 #pragma unroll
-      for (int nb = 0; nb < NBLK; ++nb) {
-        const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          ov[m][r][nb] = (drow >= 0 && col < Nd) ? epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col) : 0.f;
+        }
       }
-    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+        if (drow < 0) continue;
+        T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          if (col < Nd) orow[col] = from_f32<T>(ov[m][r][nb]);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+        if (drow < 0) continue;
+        T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
+        }
+      }
+  }
 }
 
 // Row tile and column tile of a ring-kernel workgroup.  With one column tile
@@ -598,19 +658,49 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   float em[NBLK], ea[NBLK];
 #pragma unroll
   for (int nb = 0; nb < NBLK; ++nb) epi.column(n0 + nb * 16 + c, Nd, em[nb], ea[nb]);
+  if constexpr (E::kReads) {
+    // values first, stores after: an epilogue that reads (the residual) issues
+    // all its loads before the first store, which may alias them
+    float ov[2][4][NBLK];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
-      if (drow < 0) continue;
-      T* orow = out + (int64_t)drow * Nd;
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
 #pragma unroll
-      for (int nb = 0; nb < NBLK; ++nb) {
-        const int col = n0 + nb * 16 + c;
-        if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          ov[m][r][nb] = (drow >= 0 && col < Nd) ? epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col) : 0.f;
+        }
       }
-    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+        if (drow < 0) continue;
+        T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          if (col < Nd) orow[col] = from_f32<T>(ov[m][r][nb]);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t drow = drow_s[wid * 32 + m * 16 + g * 4 + r];
+        if (drow < 0) continue;
+        T* orow = out + (int64_t)drow * Nd;
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int col = n0 + nb * 16 + c;
+          if (col < Nd) orow[col] = from_f32<T>(epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, Nd, col));
+        }
+      }
+  }
 }
 
 // ------------------------------------------- weight gradient over pair lists

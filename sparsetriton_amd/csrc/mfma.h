@@ -106,6 +106,7 @@ __device__ __forceinline__ T from_f32(float v) {
 // pointer drops its term.
 template <typename T>
 struct Epi {
+  static constexpr bool kReads = true;  // reads memory per element (the residual)
   const T* bias;
   const float* scale;
   const float* shift;
@@ -133,6 +134,7 @@ struct Epi {
 // the split-fp32 gather measured 152 vs 184 us).
 template <typename T>
 struct BiasEpi {
+  static constexpr bool kReads = false;
   const T* bias;
   __device__ __forceinline__ void column(int col, int Nd, float& mul, float& add) const {
     mul = 1.f;
