@@ -360,3 +360,35 @@ def test_resnet21d_eval_fused_vs_oracle(device):
             c, h, s = _block_eval_oracle(block, c, h, s)
         assert np.array_equal(got.C.cpu().numpy(), c)
         assert rel(got.F, h) < 5e-3
+
+
+def test_conv_transpose_block_vs_oracle(device):
+    """SparseConvTransposeBlock (blocks.py:50-81): transposed conv + batch norm + ReLU, training."""
+    from sparsetriton_amd.nn import SparseConvTransposeBlock
+
+    rng = np.random.default_rng(51)
+    torch.manual_seed(4)
+    coords, shape = _rand_set(rng, B=2, S=12, n=400)
+    C = 16
+    x = rng.standard_normal((coords.shape[0], C))
+    block = SparseConvTransposeBlock(C, 8, 3, stride=2).to(device)
+    _randomise_bn(block, rng)
+    sp, f = _sp(device, coords, x, torch.float32, 2, shape=shape)
+    out = block(sp)
+    conv = block[0]
+    k, s, p, d = conv.kernel_size[0], conv.stride[0], conv.padding[0], conv.dilation[0]
+    off = O.target_offsets(k, d, p, True)
+    ns = O.out_shape(shape, k, s, d, p, True)
+    oc = out.C.cpu().numpy()
+    assert sorted(map(tuple, oc.tolist())) == sorted(map(tuple, O.out_coords(coords, off, s, True, ns).tolist()))
+    nbr = O.exact_kmap(coords, oc, off, 1, tuple(v * s for v in shape), in_scale=s)
+    y = O.fwd_f64(x, conv.weight.detach().double().cpu().numpy(), nbr) + conv.bias.detach().double().cpu().numpy()
+    ref = _bn_oracle(block[1], oc[:, 0], 2, y, relu=True)
+    assert rel(out.F, ref) < 2e-3
+    # gradient through the fused path equals the unfused children's
+    sp2, f2 = _sp(device, coords, x, torch.float32, 2, shape=shape)
+    h = block[2](block[1](block[0](sp2)))
+    dout = torch.randn(tuple(out.F.shape), device=device)
+    out.F.backward(dout)
+    h.F.backward(dout)
+    assert rel(f.grad, f2.grad) < 1e-4
