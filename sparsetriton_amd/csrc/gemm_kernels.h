@@ -1148,6 +1148,52 @@ __global__ __launch_bounds__(256) void wgrad_pairs_reduce_kernel(const float* __
   }
 }
 
+// Vector form of the sum above for per_k % 4 == 0 and 16-byte aligned
+// partials: a workgroup sums 64 consecutive elements of one offset as 16
+// lanes of float4 times 16 parts; part p takes chunks p, p + 16, ... with four
+// loads in flight, and the parts are added in part order (deterministic).
+// Sixteen parts keep the centre offset of a submanifold map, which owns far
+// more chunks than the others, from becoming one long dependent load chain.
+template <typename TW>
+__global__ __launch_bounds__(256) void wgrad_pairs_reduce4_kernel(const float* __restrict__ partials,
+                                                                  const int32_t* __restrict__ cstart, int64_t per_k,
+                                                                  int K, TW* __restrict__ dW) {
+  __shared__ float4 red[16][16];
+  const int64_t blocks_per_k = (per_k + 63) / 64;
+  const int64_t k = blockIdx.x / blocks_per_k;
+  const int lane = threadIdx.x & 15, part = threadIdx.x >> 4;
+  const int64_t e = (blockIdx.x - k * blocks_per_k) * 64 + lane * 4;
+  float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0, s2 = s0, s3 = s0;
+  if (e < per_k) {
+    const float* p = partials + e;
+    const int c1 = cstart[k + 1];
+    int c = cstart[k] + part;
+    for (; c + 48 < c1; c += 64) {
+      const float4 a = *(const float4*)(p + (int64_t)c * per_k);
+      const float4 b = *(const float4*)(p + (int64_t)(c + 16) * per_k);
+      const float4 d = *(const float4*)(p + (int64_t)(c + 32) * per_k);
+      const float4 f = *(const float4*)(p + (int64_t)(c + 48) * per_k);
+      s0 += a;
+      s1 += b;
+      s2 += d;
+      s3 += f;
+    }
+    for (; c < c1; c += 16) s0 += *(const float4*)(p + (int64_t)c * per_k);
+  }
+  red[part][lane] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (part == 0 && e < per_k) {
+    float4 t = red[0][lane];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) t += red[j][lane];
+    TW* o = dW + k * per_k + e;
+    o[0] = from_f32<TW>(t.x);
+    o[1] = from_f32<TW>(t.y);
+    o[2] = from_f32<TW>(t.z);
+    o[3] = from_f32<TW>(t.w);
+  }
+}
+
 constexpr int kWgQB = 32;       // pairs per MFMA batch
 constexpr int kWgRows = 1024;   // map rows compacted per step (4 per thread)
 constexpr int kWgTileBlk = 8;   // 16x16 blocks per workgroup sub-tile side (128 channels)
@@ -1414,8 +1460,12 @@ static int launch_wgrad_reduce(const float* partials, const int32_t* cstart_or_n
                                int Cin, int Cout, void* dW, int dw_dtype, hipStream_t stream) {
   const int64_t per_k = (int64_t)Cin * Cout;
   const unsigned gr = st_blocks(per_k * K, 256);
+  const bool vec4 = per_k % 4 == 0 && (uintptr_t)partials % 16 == 0;
 #define ST_REDUCE(TW)                                                                                        \
-  if (cstart_or_null)                                                                                        \
+  if (cstart_or_null && vec4)                                                                                \
+    wgrad_pairs_reduce4_kernel<TW><<<(unsigned)(K * ((per_k + 63) / 64)), 256, 0, stream>>>(                 \
+        partials, cstart_or_null, per_k, K, (TW*)dW);                                                        \
+  else if (cstart_or_null)                                                                                   \
     wgrad_pairs_reduce_kernel<TW><<<(unsigned)(K * ((per_k + 31) / 32)), 256, 0, stream>>>(                  \
         partials, cstart_or_null, per_k, K, (TW*)dW);                                                        \
   else                                                                                                       \

@@ -17,14 +17,16 @@
 //
 // The sort is a stable LSD radix sort, 9-bit digits, one pass per digit of
 // the significant key bits (27-bit masks: 3 passes).  Each pass:
-//   radix_hist_kernel    per 4096-element tile, a 512-bin digit histogram;
-//   exclusive scan       the digit-major (digit, tile) counts, scanned as one
-//                        flat array, are each tile's first output position
-//                        for each digit;
-//   radix_scatter_kernel each tile re-reads its elements in order and writes
-//                        them at offset + stable rank, the rank coming from
-//                        running per-digit counters in LDS plus, inside a
-//                        wave, the lanes below with the same digit (9 ballots).
+//   radix_hist_kernel    per 4096-element tile, a 512-bin digit histogram,
+//                        stored digit-major (digit, tile);
+//   radix_colscan_kernel per digit, the tile counts become each tile's
+//                        exclusive prefix among the tiles, plus the digit's
+//                        total;
+//   radix_scatter_kernel each tile scans the 512 digit totals itself, re-reads
+//                        its elements in order and writes them at offset +
+//                        stable rank, the rank coming from running per-digit
+//                        counters in LDS plus, inside a wave, the lanes below
+//                        with the same digit (9 ballots).
 #include "common.h"
 #include "nbr_src.h"
 
@@ -70,67 +72,131 @@ __global__ __launch_bounds__(256) void mask_keys_kernel(const uint32_t* __restri
   rows[i] = (int32_t)i;
 }
 
+// Every thread loads its 16 keys before the first LDS atomic, so a tile's
+// loads are all in flight together.
 __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift,
                                                          int64_t ntiles, int32_t* __restrict__ hist) {
+  constexpr int J = kRadixTile / 256;
   __shared__ int h[kRadixBins];
 #pragma unroll
   for (int e = 0; e < kBinsPerThread; ++e) h[threadIdx.x + e * 256] = 0;
-  __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kRadixTile;
-  for (int j = 0; j < kRadixTile / 256; ++j) {
+  uint32_t d[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
     const int64_t i = base + j * 256 + threadIdx.x;
-    if (i < n) atomicAdd(&h[(keys[i] >> shift) & (kRadixBins - 1)], 1);
+    d[j] = i < n ? (keys[i] >> shift) & (kRadixBins - 1) : (uint32_t)kRadixBins;
   }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (d[j] < (uint32_t)kRadixBins) atomicAdd(&h[d[j]], 1);
   __syncthreads();
 #pragma unroll
   for (int e = 0; e < kBinsPerThread; ++e)
     hist[(int64_t)(threadIdx.x + e * 256) * ntiles + blockIdx.x] = h[threadIdx.x + e * 256];
 }
 
+// One wave per digit: the digit's per-tile counts (a contiguous column of the
+// digit-major histogram) become, in place, each tile's exclusive prefix among
+// the tiles; totals[d] receives the digit's count.
+__global__ __launch_bounds__(256) void radix_colscan_kernel(int32_t* __restrict__ hist, int64_t ntiles,
+                                                            int32_t* __restrict__ totals) {
+  const int lane = threadIdx.x & 63;
+  const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
+  int32_t* col = hist + (int64_t)d * ntiles;
+  int carry = 0;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += 64) {
+    const int64_t t = t0 + lane;
+    const int v = t < ntiles ? col[t] : 0;
+    const int inc = wave_inclusive_scan(v);
+    if (t < ntiles) col[t] = carry + inc - v;
+    carry += __shfl(inc, 63, 64);
+  }
+  if (lane == 0) totals[d] = carry;
+}
+
+// Scatter of one 4096-element tile.  The tile's first output position for
+// digit d is (elements of smaller digits, an exclusive scan of the digit
+// totals done here) + (elements of digit d in earlier tiles, the column
+// scan).  The tile's keys and values are loaded up front; then each
+// 256-element step ranks its elements by digit: inside a wave from 9 ballots,
+// across waves from per-wave digit counts published in LDS.  Those counts
+// carry their step's tag (step + 1 in the bits above 8), so a stale entry of
+// an earlier step reads as 0 and nothing is cleared, and the counts and the
+// running per-digit positions alternate between two buffers by step parity,
+// which leaves one barrier per step.
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
                                                             const int32_t* __restrict__ vals_in, int64_t n, int shift,
                                                             int64_t ntiles, const int32_t* __restrict__ offsets,
+                                                            const int32_t* __restrict__ totals,
                                                             uint32_t* __restrict__ keys_out,
                                                             int32_t* __restrict__ vals_out) {
-  __shared__ int run_s[kRadixBins];    // elements of each digit already placed by this tile
-  __shared__ int wcnt_s[4][kRadixBins];  // per-wave digit counts of the current 256-element step
+  constexpr int J = kRadixTile / 256;
+  static_assert(kBinsPerThread == 2, "two digits per thread");
+  __shared__ int run_s[2][kRadixBins];     // next output position of each digit, by step parity
+  __shared__ int wcnt_s[2][4][kRadixBins];  // tagged per-wave digit counts, by step parity
+  __shared__ int scan_s[8];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-#pragma unroll
-  for (int e = 0; e < kBinsPerThread; ++e)
-    run_s[tid + e * 256] = offsets[(int64_t)(tid + e * 256) * ntiles + blockIdx.x];
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int64_t base = (int64_t)blockIdx.x * kRadixTile;
-  for (int j = 0; j < kRadixTile / 256; ++j) {
+  uint32_t kk[J];
+  int32_t vv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
     const int64_t i = base + j * 256 + tid;
-    const bool ok = i < n;
-    const uint32_t key = ok ? keys_in[i] : 0u;
-    const int32_t val = ok ? vals_in[i] : 0;
-    const int d = (key >> shift) & (kRadixBins - 1);
+    kk[j] = i < n ? keys_in[i] : 0u;
+    vv[j] = i < n ? vals_in[i] : 0;
+  }
+  {
+    const int d0 = 2 * tid;
+    const int t0 = totals[d0], t1 = totals[d0 + 1];
+    int all;
+    const int ex = block_exclusive_scan(t0 + t1, scan_s, &all);
+    run_s[0][d0] = ex + offsets[(int64_t)d0 * ntiles + blockIdx.x];
+    run_s[0][d0 + 1] = ex + t0 + offsets[(int64_t)(d0 + 1) * ntiles + blockIdx.x];
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    wcnt_s[0][w][tid] = 0;
+    wcnt_s[0][w][tid + 256] = 0;
+    wcnt_s[1][w][tid] = 0;
+    wcnt_s[1][w][tid + 256] = 0;
+  }
+  __syncthreads();
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int par = j & 1, tag = (j + 1) << 8;
+    const bool ok = base + j * 256 + tid < n;
+    const int d = (kk[j] >> shift) & (kRadixBins - 1);
     uint64_t same = __ballot(ok);
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
       const uint64_t bal = __ballot((d >> b) & 1);
       same &= ((d >> b) & 1) ? bal : ~bal;
     }
-#pragma unroll
-    for (int e = 0; e < kBinsPerThread; ++e)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) wcnt_s[w][tid + e * 256] = 0;
-    __syncthreads();
     // the lowest lane of each digit group publishes the group's size
-    if (ok && (same & below) == 0) wcnt_s[wid][d] = (int)__popcll(same);
+    if (ok && (same & below) == 0) wcnt_s[par][wid][d] = tag | (int)__popcll(same);
     __syncthreads();
     if (ok) {
-      int pos = run_s[d] + (int)__popcll(same & below);
-      for (int w = 0; w < wid; ++w) pos += wcnt_s[w][d];
-      if (keys_out) keys_out[pos] = key;
-      vals_out[pos] = val;
+      int pos = run_s[par][d] + (int)__popcll(same & below);
+      for (int w = 0; w < wid; ++w) {
+        const int c = wcnt_s[par][w][d];
+        pos += (c & ~255) == tag ? (c & 255) : 0;
+      }
+      if (keys_out) keys_out[pos] = kk[j];
+      vals_out[pos] = vv[j];
     }
-    __syncthreads();
 #pragma unroll
-    for (int e = 0; e < kBinsPerThread; ++e) {
-      const int d2 = tid + e * 256;
-      run_s[d2] += wcnt_s[0][d2] + wcnt_s[1][d2] + wcnt_s[2][d2] + wcnt_s[3][d2];
+    for (int e = 0; e < 2; ++e) {
+      const int d2 = 2 * tid + e;
+      int add = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int c = wcnt_s[par][w][d2];
+        add += (c & ~255) == tag ? (c & 255) : 0;
+      }
+      run_s[par ^ 1][d2] = run_s[par][d2] + add;
     }
   }
 }
@@ -202,7 +268,7 @@ static int radix_passes(int K) {
 extern "C" int st_kmap_sort_workspace(int64_t n, size_t* bytes) {
   if (n < 0 || n >= (1ll << 31) || !bytes) return ST_ERR_ARG;
   const int64_t ntiles = (n + st::kRadixTile - 1) / st::kRadixTile;
-  *bytes = (size_t)(st::kRadixBins * (ntiles > 0 ? ntiles : 1) + 1) * sizeof(int32_t);
+  *bytes = (size_t)(st::kRadixBins * ((ntiles > 0 ? ntiles : 1) + 1)) * sizeof(int32_t);
   return ST_OK;
 }
 
@@ -213,21 +279,23 @@ extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, i
   if (n == 0) return ST_OK;
   if (!masks || !keys_tmp || !rows_tmp || !perm || !workspace) return ST_ERR_ARG;
   const int64_t ntiles = (n + st::kRadixTile - 1) / st::kRadixTile;
-  if (workspace_bytes < (size_t)(st::kRadixBins * ntiles + 1) * sizeof(int32_t)) return ST_ERR_ARG;
+  if (workspace_bytes < (size_t)(st::kRadixBins * (ntiles + 1)) * sizeof(int32_t)) return ST_ERR_ARG;
   const int passes = st::radix_passes(K);
   // Values ping-pong between rows_tmp and perm; start so the last pass lands in perm.
   int32_t* vbuf[2] = {(passes % 2) ? rows_tmp : perm, (passes % 2) ? perm : rows_tmp};
   uint32_t* kbuf[2] = {keys_tmp, keys_tmp + n};
   int32_t* hist = (int32_t*)workspace;
+  int32_t* totals = hist + st::kRadixBins * ntiles;
   st::mask_keys_kernel<<<st_blocks(n, 256), 256, 0, stream>>>(masks, mask_words, K == 27, n, kbuf[0],
                                                                vbuf[0]);
   for (int p = 0; p < passes; ++p) {
     const int shift = p * st::kRadixBits;
     const int in = p & 1, out = in ^ 1;
     st::radix_hist_kernel<<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], n, shift, ntiles, hist);
-    if (st::launch_exclusive_scan(hist, st::kRadixBins * ntiles, stream) != ST_OK) return ST_ERR_HIP;
+    st::radix_colscan_kernel<<<st::kRadixBins / 4, 256, 0, stream>>>(hist, ntiles, totals);
     st::radix_scatter_kernel<<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], vbuf[in], n, shift, ntiles, hist,
-                                                                   p + 1 < passes ? kbuf[out] : nullptr, vbuf[out]);
+                                                                   totals, p + 1 < passes ? kbuf[out] : nullptr,
+                                                                   vbuf[out]);
   }
   ST_CHECK_LAUNCH();
   return ST_OK;

@@ -356,8 +356,8 @@ def _fold_keys(masks, K):
                                  (1_100_000, 27)])
 def test_sort_rows_stable(device, n, K):
     """st_kmap_sort_rows is a stable sort of rows by their (folded) offset mask:
-    equal to numpy's stable argsort across many 4096-row tiles and all digits (up to 256 tiles
-    the scatter sums its offsets from the count table itself; 1.1M rows take the scan launch)."""
+    equal to numpy's stable argsort across many 4096-row tiles and all digits (1.1M rows: 269
+    tiles, so the per-digit column scans cover several 64-tile steps)."""
     from sparsetriton_amd.nn.functional.conv.kmap import TilePlan
     rng = np.random.default_rng(n + K)
     W = (K + 31) // 32
