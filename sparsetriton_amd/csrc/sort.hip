@@ -17,7 +17,8 @@
 //
 // The sort is a stable LSD radix sort, 9-bit digits, one pass per digit of
 // the significant key bits (27-bit masks: 3 passes).  Each pass:
-//   radix_hist_kernel    per 4096-element tile, a 512-bin digit histogram,
+//   radix_hist_kernel    per tile (1024 elements, 4096 above 4M), a 512-bin
+//                        digit histogram,
 //                        stored digit-major (digit, tile);
 //   radix_colscan_kernel per digit, the tile counts become each tile's
 //                        exclusive prefix among the tiles, plus the digit's
@@ -34,7 +35,12 @@ namespace st {
 
 constexpr int kRadixBits = 9;
 constexpr int kRadixBins = 1 << kRadixBits;
-constexpr int kRadixTile = 4096;  // elements per workgroup (256 threads x 16)
+// elements per workgroup: 256 threads x 4 up to 4M elements (enough workgroups
+// to fill the chip: a tile's steps are a serial chain of LDS round trips), 256
+// threads x 16 above (a smaller count table)
+constexpr int kRadixTileSmall = 1024;
+constexpr int kRadixTileLarge = 4096;
+__host__ __device__ constexpr int radix_tile(int64_t n) { return n <= (1 << 22) ? kRadixTileSmall : kRadixTileLarge; }
 constexpr int kBinsPerThread = kRadixBins / 256;
 
 // Key bit of each offset of a 3x3x3 kernel: offsets ordered by the number of
@@ -72,15 +78,16 @@ __global__ __launch_bounds__(256) void mask_keys_kernel(const uint32_t* __restri
   rows[i] = (int32_t)i;
 }
 
-// Every thread loads its 16 keys before the first LDS atomic, so a tile's
+// Every thread loads its J keys before the first LDS atomic, so a tile's
 // loads are all in flight together.
+template <int J>
 __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift,
                                                          int64_t ntiles, int32_t* __restrict__ hist) {
-  constexpr int J = kRadixTile / 256;
+  constexpr int kTile = J * 256;
   __shared__ int h[kRadixBins];
 #pragma unroll
   for (int e = 0; e < kBinsPerThread; ++e) h[threadIdx.x + e * 256] = 0;
-  const int64_t base = (int64_t)blockIdx.x * kRadixTile;
+  const int64_t base = (int64_t)blockIdx.x * kTile;
   uint32_t d[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -99,24 +106,34 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restr
 
 // One wave per digit: the digit's per-tile counts (a contiguous column of the
 // digit-major histogram) become, in place, each tile's exclusive prefix among
-// the tiles; totals[d] receives the digit's count.
+// the tiles; totals[d] receives the digit's count.  The counts of 512 tiles
+// are loaded at once, then scanned 64 at a time in registers.
 __global__ __launch_bounds__(256) void radix_colscan_kernel(int32_t* __restrict__ hist, int64_t ntiles,
                                                             int32_t* __restrict__ totals) {
+  constexpr int B = 8;
   const int lane = threadIdx.x & 63;
   const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
   int32_t* col = hist + (int64_t)d * ntiles;
   int carry = 0;
-  for (int64_t t0 = 0; t0 < ntiles; t0 += 64) {
-    const int64_t t = t0 + lane;
-    const int v = t < ntiles ? col[t] : 0;
-    const int inc = wave_inclusive_scan(v);
-    if (t < ntiles) col[t] = carry + inc - v;
-    carry += __shfl(inc, 63, 64);
+  for (int64_t t0 = 0; t0 < ntiles; t0 += 64 * B) {
+    int v[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int64_t t = t0 + b * 64 + lane;
+      v[b] = t < ntiles ? col[t] : 0;
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int64_t t = t0 + b * 64 + lane;
+      const int inc = wave_inclusive_scan(v[b]);
+      if (t < ntiles) col[t] = carry + inc - v[b];
+      carry += __shfl(inc, 63, 64);
+    }
   }
   if (lane == 0) totals[d] = carry;
 }
 
-// Scatter of one 4096-element tile.  The tile's first output position for
+// Scatter of one tile of J * 256 elements.  The tile's first output position for
 // digit d is (elements of smaller digits, an exclusive scan of the digit
 // totals done here) + (elements of digit d in earlier tiles, the column
 // scan).  The tile's keys and values are loaded up front; then each
@@ -126,19 +143,20 @@ __global__ __launch_bounds__(256) void radix_colscan_kernel(int32_t* __restrict_
 // an earlier step reads as 0 and nothing is cleared, and the counts and the
 // running per-digit positions alternate between two buffers by step parity,
 // which leaves one barrier per step.
+template <int J>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
                                                             const int32_t* __restrict__ vals_in, int64_t n, int shift,
                                                             int64_t ntiles, const int32_t* __restrict__ offsets,
                                                             const int32_t* __restrict__ totals,
                                                             uint32_t* __restrict__ keys_out,
                                                             int32_t* __restrict__ vals_out) {
-  constexpr int J = kRadixTile / 256;
+  constexpr int kTile = J * 256;
   static_assert(kBinsPerThread == 2, "two digits per thread");
   __shared__ int run_s[2][kRadixBins];     // next output position of each digit, by step parity
   __shared__ int wcnt_s[2][4][kRadixBins];  // tagged per-wave digit counts, by step parity
   __shared__ int scan_s[8];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int64_t base = (int64_t)blockIdx.x * kRadixTile;
+  const int64_t base = (int64_t)blockIdx.x * kTile;
   uint32_t kk[J];
   int32_t vv[J];
 #pragma unroll
@@ -267,7 +285,7 @@ static int radix_passes(int K) {
 
 extern "C" int st_kmap_sort_workspace(int64_t n, size_t* bytes) {
   if (n < 0 || n >= (1ll << 31) || !bytes) return ST_ERR_ARG;
-  const int64_t ntiles = (n + st::kRadixTile - 1) / st::kRadixTile;
+  const int64_t tile = st::radix_tile(n), ntiles = (n + tile - 1) / tile;
   *bytes = (size_t)(st::kRadixBins * ((ntiles > 0 ? ntiles : 1) + 1)) * sizeof(int32_t);
   return ST_OK;
 }
@@ -278,7 +296,7 @@ extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, i
   if (n < 0 || n >= (1ll << 31) || K <= 0 || K > ST_MAX_KVOL || mask_words != (K + 31) / 32) return ST_ERR_ARG;
   if (n == 0) return ST_OK;
   if (!masks || !keys_tmp || !rows_tmp || !perm || !workspace) return ST_ERR_ARG;
-  const int64_t ntiles = (n + st::kRadixTile - 1) / st::kRadixTile;
+  const int64_t tile = st::radix_tile(n), ntiles = (n + tile - 1) / tile;
   if (workspace_bytes < (size_t)(st::kRadixBins * (ntiles + 1)) * sizeof(int32_t)) return ST_ERR_ARG;
   const int passes = st::radix_passes(K);
   // Values ping-pong between rows_tmp and perm; start so the last pass lands in perm.
@@ -291,11 +309,20 @@ extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, i
   for (int p = 0; p < passes; ++p) {
     const int shift = p * st::kRadixBits;
     const int in = p & 1, out = in ^ 1;
-    st::radix_hist_kernel<<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], n, shift, ntiles, hist);
+    uint32_t* kout = p + 1 < passes ? kbuf[out] : nullptr;
+    if (tile == st::kRadixTileSmall)
+      st::radix_hist_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], n, shift,
+                                                                                             ntiles, hist);
+    else
+      st::radix_hist_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], n, shift,
+                                                                                             ntiles, hist);
     st::radix_colscan_kernel<<<st::kRadixBins / 4, 256, 0, stream>>>(hist, ntiles, totals);
-    st::radix_scatter_kernel<<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], vbuf[in], n, shift, ntiles, hist,
-                                                                   totals, p + 1 < passes ? kbuf[out] : nullptr,
-                                                                   vbuf[out]);
+    if (tile == st::kRadixTileSmall)
+      st::radix_scatter_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(
+          kbuf[in], vbuf[in], n, shift, ntiles, hist, totals, kout, vbuf[out]);
+    else
+      st::radix_scatter_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(
+          kbuf[in], vbuf[in], n, shift, ntiles, hist, totals, kout, vbuf[out]);
   }
   ST_CHECK_LAUNCH();
   return ST_OK;

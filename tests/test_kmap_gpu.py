@@ -352,12 +352,13 @@ def _fold_keys(masks, K):
     return key.astype(np.uint32)
 
 
-@pytest.mark.parametrize("n,K", [(0, 27), (1, 27), (4095, 8), (4097, 1), (300_001, 27), (123_457, 125), (70_000, 343),
-                                 (1_100_000, 27)])
+@pytest.mark.parametrize("n,K", [(0, 27), (1, 27), (1025, 27), (4095, 8), (4097, 1), (300_001, 27), (123_457, 125),
+                                 (70_000, 343), (1_100_000, 27), (4_500_000, 27)])
 def test_sort_rows_stable(device, n, K):
     """st_kmap_sort_rows is a stable sort of rows by their (folded) offset mask:
-    equal to numpy's stable argsort across many 4096-row tiles and all digits (1.1M rows: 269
-    tiles, so the per-digit column scans cover several 64-tile steps)."""
+    equal to numpy's stable argsort across many tiles and all digits (1.1M rows: 1075 tiles of
+    1024 rows, so the per-digit column scans take three 512-tile batches; 4.5M rows take the
+    4096-row tiles of large inputs)."""
     from sparsetriton_amd.nn.functional.conv.kmap import TilePlan
     rng = np.random.default_rng(n + K)
     W = (K + 31) // 32
