@@ -14,9 +14,11 @@
 // Statistics are sums over a sample's rows.  They are deterministic: the
 // rows are cut into G contiguous ranges, one per workgroup; in a workgroup
 // each thread owns a (row group, channel vector) pair and adds its rows in
-// order, first in registers and, when the sample index changes, into its own
-// LDS slots; the row groups are then summed in a fixed order into one partial
-// per workgroup, and the G partials of each (sample, channel) are summed by a
+// order in registers; when the sample index changes it adds them into LDS
+// slots of its wave, the wave's row groups taking turns in a fixed order, so
+// every slot sees its additions in an order set by the data alone.  The
+// waves' slots are then summed in a fixed order into one partial per
+// workgroup, and the G partials of each (sample, channel) are summed by a
 // fixed tree.  Sample counts are integers (exact under atomics).
 #include "common.h"
 
@@ -40,7 +42,7 @@
 
 namespace st {
 
-constexpr int kBnLds = 16384;        // 4-byte words of per-row-group sums in LDS (64 KB)
+constexpr int kBnLds = 16384;        // 4-byte words of per-slot sums in LDS (64 KB)
 constexpr int kBnMaxBlocks = 1024;   // row ranges of a statistics pass
 constexpr int kBnRowsPerBlock = 512;
 constexpr int kBnUnroll = 4;         // rows whose loads are issued together
@@ -109,8 +111,12 @@ __device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&v)
 //   MODE 0: y (and, for column block 0, the rows per sample)
 //   MODE 1: (y - mean)^2
 //   MODE 2: g and g * xhat, g = dout masked by out > 0 when relu, xhat = (y - mean) * invstd
-// partials[wg][o][bl][c], o < NOUT.  rg row groups of TPR threads; LDS holds
-// rg * NOUT * bw * CW floats, then (MODE 0) rg * bw row counts.
+// partials[wg][o][bl][c], o < NOUT.  rg row groups of TPR threads.  LDS slots
+// belong to waves (to a row group when TPR >= 64, which spans whole waves):
+// nslot = 256 / max(TPR, 64) sets of NOUT * bw * CW floats, then (MODE 0)
+// nslot * bw row counts.
+__host__ __device__ inline int bn_slots(int TPR) { return 256 / (TPR > 64 ? TPR : 64); }
+
 template <typename T, typename CT, int V, int MODE>
 __global__ __launch_bounds__(256) void bn_stats_kernel(const T* __restrict__ Y, const T* __restrict__ dout,
                                                        const T* __restrict__ out, int64_t n, int C,
@@ -123,28 +129,42 @@ __global__ __launch_bounds__(256) void bn_stats_kernel(const T* __restrict__ Y, 
   extern __shared__ __attribute__((aligned(16))) float acc_s[];
   const int tid = threadIdx.x, q = tid % TPR, sub = tid / TPR;
   const int CW = TPR * V;            // channels of this column block
-  const int per = NOUT * bw * CW;    // floats per row group
+  const int per = NOUT * bw * CW;    // floats per slot
+  const int nslot = bn_slots(TPR);
+  // slot of this thread; its row group's turn among the row groups sharing the slot
+  const int slot = TPR >= 64 ? sub : tid >> 6;
+  const int turn = TPR >= 64 ? 0 : sub - (tid & ~63) / TPR;
+  // a wave holds at most 64 / TPR + 2 row groups (partial ones at both ends)
+  const int turns = TPR >= 64 ? 1 : 64 / TPR + 2;
   const bool with_counts = MODE == 0 && counts && blockIdx.y == 0;
-  int* cnt_s = reinterpret_cast<int*>(acc_s + rg * per);
-  for (int e = tid; e < rg * per; e += 256) acc_s[e] = 0.f;
+  int* cnt_s = reinterpret_cast<int*>(acc_s + nslot * per);
+  for (int e = tid; e < nslot * per; e += 256) acc_s[e] = 0.f;
   if (with_counts)
-    for (int e = tid; e < rg * bw; e += 256) cnt_s[e] = 0;
+    for (int e = tid; e < nslot * bw; e += 256) cnt_s[e] = 0;
   __syncthreads();
   const int c = blockIdx.y * CW + q * V;
   const int G = gridDim.x;
   const int64_t r0 = (int64_t)blockIdx.x * n / G, r1 = (int64_t)(blockIdx.x + 1) * n / G;
   if (sub < rg && c < C) {
-    float* mine = acc_s + sub * per + q * V;
+    float* mine = acc_s + slot * per + q * V;
     const bool counter = with_counts && q == 0;
     float ra[NOUT][V];
     int cur = -1, cnt = 0;
+    // The row groups of a slot add in turn order: one wave's LDS accesses complete
+    // in program order, and the empty asm keeps the compiler from merging the turns
+    // (lanes of one instruction adding into the same word would lose updates).
     auto flush = [&]() {
       if (cur < 0) return;
+      for (int j = 0; j < turns; ++j) {
+        if (j == turn) {
 #pragma unroll
-      for (int o = 0; o < NOUT; ++o)
+          for (int o = 0; o < NOUT; ++o)
 #pragma unroll
-        for (int e = 0; e < V; ++e) mine[(o * bw + cur) * CW + e] += ra[o][e];
-      if (counter) cnt_s[sub * bw + cur] += cnt;
+            for (int e = 0; e < V; ++e) mine[(o * bw + cur) * CW + e] += ra[o][e];
+          if (counter) cnt_s[slot * bw + cur] += cnt;
+        }
+        asm volatile("" ::: "memory");
+      }
     };
     for (int64_t r = r0 + sub; r < r1; r += (int64_t)U * rg) {
       // loads of U rows first (rows past the range read the range's first row and are dropped)
@@ -210,10 +230,10 @@ __global__ __launch_bounds__(256) void bn_stats_kernel(const T* __restrict__ Y, 
     flush();
   }
   __syncthreads();
-  // row groups summed in order; one partial per workgroup
+  // slots summed in order; one partial per workgroup
   for (int e = tid; e < per; e += 256) {
     float s = 0.f;
-    for (int j = 0; j < rg; ++j) s += acc_s[j * per + e];
+    for (int j = 0; j < nslot; ++j) s += acc_s[j * per + e];
     const int cc = e % CW, ob = e / CW;
     const int ch = blockIdx.y * CW + cc;
     if (ch < C) partials[((int64_t)blockIdx.x * NOUT * bw + ob) * C + ch] = s;
@@ -221,7 +241,7 @@ __global__ __launch_bounds__(256) void bn_stats_kernel(const T* __restrict__ Y, 
   if (with_counts)
     for (int bl = tid; bl < bw; bl += 256) {
       int t = 0;
-      for (int j = 0; j < rg; ++j) t += cnt_s[j * bw + bl];
+      for (int j = 0; j < nslot; ++j) t += cnt_s[j * bw + bl];
       if (t) atomicAdd(&counts[b0 + bl], t);
     }
 }
@@ -443,21 +463,15 @@ static void bn_stats_v(const T* Y, const T* dout, const T* out, int64_t n, int C
   constexpr int NOUT = MODE == 2 ? 2 : 1;
   const int G = bn_blocks(n);
   const int CW = gm.TPR * V;
-  const int per_b = NOUT * CW + (MODE == 0 ? 1 : 0);  // words per sample per row group (+ its row count)
-  int rg, bw;
-  if ((int64_t)B * per_b * gm.RG <= kBnLds) {
-    rg = gm.RG, bw = B;
-  } else if ((int64_t)B * per_b <= kBnLds) {
-    rg = kBnLds / (B * per_b), bw = B;
-  } else {
-    rg = 1, bw = kBnLds / per_b;
-  }
+  const int per_b = NOUT * CW + (MODE == 0 ? 1 : 0);  // words per sample per slot (+ its row count)
+  const int nslot = bn_slots(gm.TPR);
+  const int bw = (int64_t)B * per_b * nslot <= kBnLds ? B : kBnLds / (per_b * nslot);
   for (int b0 = 0; b0 < B; b0 += bw) {
     const int w = B - b0 < bw ? B - b0 : bw;
     const dim3 grid((unsigned)G, (unsigned)gm.ncb);
-    const size_t lds = (size_t)rg * w * per_b * 4;
-    bn_stats_kernel<T, CT, V, MODE><<<grid, 256, lds, stream>>>(Y, dout, out, n, C, coords, b0, w, rg, gm.TPR, mean,
-                                                                invstd, relu, partials, counts);
+    const size_t lds = (size_t)nslot * w * per_b * 4;
+    bn_stats_kernel<T, CT, V, MODE><<<grid, 256, lds, stream>>>(Y, dout, out, n, C, coords, b0, w, gm.RG, gm.TPR,
+                                                                mean, invstd, relu, partials, counts);
     bn_reduce_kernel<<<(unsigned)(NOUT * w * C), 256, 0, stream>>>(partials, G, NOUT, w, C, b0, B, S);
   }
 }

@@ -142,6 +142,22 @@ def test_bn_many_samples_windows(device):
     assert rel(f.grad.cpu(), gdx) < 1e-4
 
 
+def test_bn_large_offset_moments(device):
+    """Features with a mean 1000x their spread: the variance pass sums squares of deviations
+    from the sample mean, so it stays accurate where E[y^2] - mean^2 in fp32 would not."""
+    rng = np.random.default_rng(14)
+    n, C, B = 40000, 32, 3
+    coords, bi, x = _case(rng, n, C, B, empty=None)
+    x = x * 0.5 + 1000.0 + np.arange(B)[bi][:, None] * 10.0
+    sp, _ = _sp(device, coords, x, torch.float32, B, grad=False)
+    rm, rv = torch.zeros(C, device=device), torch.ones(C, device=device)
+    out = sparse_batch_norm(sp, None, None, rm, rv, training=True, momentum=1.0)
+    x_q = sp.F.double().cpu().numpy()
+    ref, ref_rm, ref_rv = O.batch_norm_f64(x_q, bi, B, None, None, np.zeros(C), np.ones(C), True, momentum=1.0)
+    assert rel(out.F.cpu(), ref) < 1e-4
+    assert rel(rm.cpu(), ref_rm) < 1e-6 and rel(rv.cpu(), ref_rv) < 1e-4
+
+
 def test_bn_deterministic_and_empty(device):
     rng = np.random.default_rng(13)
     coords, bi, x = _case(rng, 50000, 64, 4)
@@ -149,6 +165,15 @@ def test_bn_deterministic_and_empty(device):
     a = sparse_batch_norm(sp, training=True).F
     b = sparse_batch_norm(sp, training=True).F
     assert torch.equal(a, b)
+    # the backward statistics (rows of the 4 samples interleaved at random) are deterministic too
+    dout = torch.as_tensor(rng.standard_normal((50000, 64)), device=device, dtype=torch.float32)
+    grads = []
+    for _ in range(2):
+        sp2, f2 = _sp(device, coords, x, torch.float32, 4)
+        w2 = torch.ones(64, device=device, requires_grad=True)
+        sparse_batch_norm(sp2, w2, None, training=True).F.backward(dout)
+        grads.append((f2.grad.clone(), w2.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
     rm = torch.zeros(64, device=device)
     rv = torch.ones(64, device=device)
     empty = SparseTensor(torch.zeros((0, 64), device=device), torch.zeros((0, 4), dtype=torch.int32, device=device),
