@@ -403,12 +403,17 @@ struct RingTile {
   int64_t rt;
   int ct;
 };
-__device__ __forceinline__ RingTile ring_tile(int Nd, int BN) {
+// Row tiles run in descending order: destination rows are sorted by ascending
+// offset-mask key, so the last row tiles hold the rows with the most
+// neighbours (the costliest tiles); starting with them leaves the cheap tiles
+// for the tail of the grid.
+__device__ __forceinline__ RingTile ring_tile(int64_t n_dst, int Nd, int BN) {
   const int ncol = (Nd + BN - 1) / BN;
+  const int64_t nrt = (n_dst + kGemmBM - 1) / kGemmBM;
   const int64_t b = blockIdx.x;
-  if (ncol == 1) return RingTile{b, 0};
-  const int64_t s = b >> 3;
-  return RingTile{(s / ncol) * 8 + (b & 7), (int)(s % ncol)};
+  if (ncol == 1) return RingTile{nrt - 1 - b, 0};
+  const int64_t s = b >> 3, padded = (nrt + 7) / 8 * 8;
+  return RingTile{padded - 1 - ((s / ncol) * 8 + (b & 7)), (int)(s % ncol)};
 }
 // Grid of the ring kernels for n_dst rows and Nd columns in BN-wide tiles.
 static inline unsigned ring_grid(int64_t n_dst, int Nd, int BN) {
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const RingTile tile = ring_tile(Nd, BN);
+  const RingTile tile = ring_tile(n_dst, Nd, BN);
   if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
   const int64_t row0 = tile.rt * kGemmBM;
   const int n0 = tile.ct * BN;

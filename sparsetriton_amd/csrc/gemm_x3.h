@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const RingTile tile = ring_tile(Nd, BN);
+  const RingTile tile = ring_tile(n_dst, Nd, BN);
   if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
   const int64_t row0 = tile.rt * kGemmBM;
   const int n0 = tile.ct * BN;
