@@ -23,6 +23,7 @@ then touches each offset's column with coalesced accesses; the reference's
 from typing import Optional, Tuple
 
 import ctypes
+import functools
 import torch
 
 from sparsetriton_amd import _lib
@@ -61,7 +62,9 @@ def compute_target_offsets_transposed(base_offsets, padding, dilation, kernel_si
     return base_offsets - padding + (kernel_size - 1) * dilation // 2
 
 
-def _target_offsets(kernel_size: int, dilation: int, padding: int, transposed: bool, device) -> torch.Tensor:
+@functools.lru_cache(maxsize=256)
+def _target_offsets_on(kernel_size: int, dilation: int, padding: int, transposed: bool,
+                       device: torch.device) -> torch.Tensor:
     ks = torch.tensor([kernel_size] * 3)
     dil = torch.tensor([dilation] * 3)
     pad = torch.tensor([padding] * 3)
@@ -70,7 +73,17 @@ def _target_offsets(kernel_size: int, dilation: int, padding: int, transposed: b
         t = compute_target_offsets_transposed(base, pad, dil, ks)
     else:
         t = compute_target_offsets_normal(base, pad, dil, ks)
-    return t.to(device)
+    return t.to(torch.int32).to(device)
+
+
+def _target_offsets(kernel_size: int, dilation: int, padding: int, transposed: bool, device) -> torch.Tensor:
+    """(K, 3) int32 offsets on ``device``, built once per geometry and device: every map build
+    of a layer reuses them (no host-side tensor ops, host-to-device copy or dtype conversion).
+    The returned tensor is shared; callers must not modify it."""
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return _target_offsets_on(int(kernel_size), int(dilation), int(padding), bool(transposed), dev)
 
 
 def out_spatial_shape(spatial_shape, kernel_size: int, stride: int, dilation: int, padding: int,
@@ -280,13 +293,24 @@ class TileMap:
     @classmethod
     def build(cls, map_t, k_stride, r_stride, masks, K, perm, n_dst, n_src) -> "TileMap":
         dev = map_t.device
-        ntiles = (n_dst + _lib.TILE_ROWS - 1) // _lib.TILE_ROWS
-        nk = torch.empty((max(ntiles, 1),), dtype=torch.int32, device=dev)
-        klist = torch.empty((max(ntiles, 1) * K,), dtype=torch.int16, device=dev)
-        tmap = torch.empty((max(ntiles, 1) * K * _lib.TILE_ROWS,), dtype=torch.int32, device=dev)
+        nt = max((n_dst + _lib.TILE_ROWS - 1) // _lib.TILE_ROWS, 1)
+        # one allocation: nk (nt) | klist (nt * K int16) | tmap (nt * K * 128), tmap on a 256-byte boundary
+        kw = (nt * K + 1) // 2
+        hdr = (nt + kw + 63) // 64 * 64
+        buf = torch.empty((hdr + nt * K * _lib.TILE_ROWS,), dtype=torch.int32, device=dev)
+        nk = buf[:nt]
+        klist = buf[nt:nt + kw].view(torch.int16)[:nt * K]
+        tmap = buf[hdr:]
         _lib.call("st_tile_plan", _lib.ptr(map_t), k_stride, r_stride, _lib.ptr(masks), _mask_words(K), K,
                   _lib.ptr(perm), n_dst, n_src, _lib.ptr(nk), _lib.ptr(klist), _lib.ptr(tmap), _lib.stream_of(dev))
         return cls(perm, nk, klist, tmap)
+
+
+@functools.lru_cache(maxsize=64)
+def _sort_workspace_bytes(n: int) -> int:
+    nbytes = ctypes.c_size_t()
+    _lib.call("st_kmap_sort_workspace", n, ctypes.byref(nbytes))
+    return max(int(nbytes.value), 1)
 
 
 class TilePlan:
@@ -300,14 +324,12 @@ class TilePlan:
     def build(cls, n, K, masks) -> "TilePlan":
         dev = masks.device
         W = _mask_words(K)
-        nbytes = ctypes.c_size_t()
-        _lib.call("st_kmap_sort_workspace", n, ctypes.byref(nbytes))
-        ws = torch.empty((max(nbytes.value, 1),), dtype=torch.uint8, device=dev)
-        keys = torch.empty((2 * n,), dtype=torch.int32, device=dev)
-        rows = torch.empty((n,), dtype=torch.int32, device=dev)
+        nbytes = _sort_workspace_bytes(n)
+        # one scratch allocation: keys (2n) | rows (n) | sort workspace; perm is kept
+        scratch = torch.empty((3 * n + (nbytes + 3) // 4,), dtype=torch.int32, device=dev)
         perm = torch.empty((n,), dtype=torch.int32, device=dev)
-        _lib.call("st_kmap_sort_rows", _lib.ptr(masks), W, K, n, _lib.ptr(keys), _lib.ptr(rows), _lib.ptr(perm),
-                  _lib.ptr(ws), nbytes.value, _lib.stream_of(dev))
+        _lib.call("st_kmap_sort_rows", _lib.ptr(masks), W, K, n, scratch.data_ptr(), scratch.data_ptr() + 8 * n,
+                  _lib.ptr(perm), scratch.data_ptr() + 12 * n, nbytes, _lib.stream_of(dev))
         return cls(perm)
 
 
@@ -417,7 +439,7 @@ def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size
     in_coords = in_coords.contiguous()
     n = in_coords.shape[0]
     offsets = _target_offsets(kernel_size, dilation, padding, transposed, dev)
-    kernel_offsets = offsets.to(in_coords.dtype)
+    kernel_offsets = offsets.to(in_coords.dtype, copy=True)  # returned to the caller: not the shared tensor
     K = offsets.shape[0]
     if K > _lib.MAX_KVOL:
         raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
