@@ -1,5 +1,5 @@
 #!/usr/bin/env python
-"""Benchmark: SubMConv3D k3 64->64 forward + backward on one MI355X.
+"""Benchmark: SubMConv3D k3 64->64 forward + backward on one MI355X (headline configuration 2).
 
 Workload: the seeded LiDAR-like voxel set of config 2 (B=4, 1440x1440x41,
 ~118k voxels per sample), SubMConv3D 64->64, kernel 3, synthetic N(0,1)
@@ -23,7 +23,7 @@ per-offset weight gradient; fp32, OpenMP) on the same voxel set.
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--dtype f32|bf16] [--no-cpu]
                        [--fp32-precision bf16x3|ieee] [--profile] [--workload config2|config3|...]
 
-``--workload`` other than config2 measures another BASELINE configuration (strided conv,
+``--workload`` other than config2 measures another benchmark configuration (strided conv,
 transposed conv, the 1M-voxel submanifold layer with either algorithm): one JSON line with the
 same fields, the step timed the same way, plus the first-call time (map build + forward).
 """
@@ -146,7 +146,7 @@ WITH_BIAS = {"config2-bias"}
 
 
 def run_extra(args):
-    """One JSON line for a BASELINE configuration other than the headline one: the layer's
+    """One JSON line for a benchmark configuration other than the headline one: the layer's
     fwd+bwd step (map cached) and its kernel-map build, timed like the headline."""
     import torch
 
@@ -360,7 +360,7 @@ def main():
                     help="short run for counter collection: few repetitions, plus a 256 MiB device copy whose "
                          "HBM counters calibrate the per-kernel traffic figures")
     ap.add_argument("--workload", choices=["config2", "resnet21d"] + sorted(EXTRA), default="config2",
-                    help="config2 is the headline; the others measure BASELINE's other configurations")
+                    help="config2 is the headline; the others measure the other benchmark configurations")
     ap.add_argument("--fp32-precision", choices=["bf16x3", "ieee"], default="bf16x3",
                     help="fp32 matrix-core arithmetic (split-bf16 MFMA, the default, or IEEE fp32 MFMA)")
     args = ap.parse_args()

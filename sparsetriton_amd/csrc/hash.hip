@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
           state[j] = occ_locate(occ, (int)b, (int)qx, (int)qy, (int)qz, word[j], bit[j]);
       }
     }
-    // round 1: occupancy words (and, with a rank index, the words' rank prefixes)
+    // pass 1: occupancy words (and, with a rank index, the words' rank prefixes)
     uint64_t w[kQGroup];
     int32_t pre[kQGroup];
     const bool ranked = occ.rowmap != nullptr;
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
       w[j] = state[j] == 1 ? occ.words[word[j]] : 0ull;
       pre[j] = (ranked && state[j] == 1) ? occ.prefix[word[j]] : 0;
     }
-    // round 2: rows by rank for in-box hits, home-slot keys for what must be probed
+    // pass 2: rows by rank for in-box hits, home-slot keys for what must be probed
     // (with no table -- keys == nullptr, rank index only -- nothing is probed)
     uint32_t slot[kQGroup];
     uint64_t hk[kQGroup];
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
       slot[j] = probe ? home_slot(key[j], cap) : ST_NO_VAL;
       hk[j] = probe ? keys[slot[j]] : ST_EMPTY_KEY;
     }
-    // finish the rare chains that met another key; round 3: values of the probed hits
+    // finish the rare chains that met another key; pass 3: values of the probed hits
 #pragma unroll
     for (int j = 0; j < kQGroup; ++j) {
       if (slot[j] != ST_NO_VAL) slot[j] = find_slot_from(keys, cap, key[j], slot[j], hk[j]);

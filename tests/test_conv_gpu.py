@@ -321,7 +321,7 @@ def test_empty_tensor(device):
         assert out.F.shape == (0, 4)
 
 
-# --------------------------------------------------- BASELINE-size properties
+# ------------------------------------------------ benchmark-size properties
 
 def test_config2_full_size_properties(device):
     """SubM 64->64 on the full config-2 set: exact rows on a sample, adjoint identities overall."""
