@@ -5,7 +5,7 @@ coordinates are compared in order (first occurrence in the input-major /
 offset-minor candidate enumeration) and their maps entry by entry, which
 implies equality of the canonical sorted (in, out, k) triples.  The
 transposed map is checked for consistency with the forward map, and the row
-masks against the map.  Full-size BASELINE coordinate sets are included.
+masks against the map.  Full-size benchmark coordinate sets are included.
 """
 
 import numpy as np
@@ -212,7 +212,7 @@ def test_empty_and_all_filtered(device):
     assert out_coords.shape == (0, 4)
 
 
-# ------------------------------------------------------------ BASELINE sizes
+# ------------------------------------------------------------ benchmark sizes
 
 @pytest.fixture(scope="module")
 def cfg2():
