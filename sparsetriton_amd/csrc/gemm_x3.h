@@ -675,10 +675,13 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
     v4f xr[8], yr[8];
-    auto load_step = [&](int q) {
+    // pair indices one step ahead of the rows they address (no index load in
+    // front of a step's row gathers)
+    auto load_pairs = [&](int q) {
       const int p = q + (lane & 31);
-      int2 pr = make_int2(-1, -1);
-      if (p < p1) pr = pairs[p];
+      return p < p1 ? pairs[p] : make_int2(-1, -1);
+    };
+    auto load_rows = [&](int2 pr) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         const int ix = __shfl(pr.x, v * 4 + lr, 64), iy = __shfl(pr.y, v * 4 + lr, 64);
@@ -692,7 +695,9 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
       }
     };
     int q = p0 + wid * 32;
-    if (q < p1) load_step(q);
+    int2 prn = load_pairs(q);
+    if (q < p1) load_rows(prn);
+    prn = load_pairs(q + 128);
     for (; q < p1; q += 128) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
@@ -717,7 +722,10 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (q + 128 < p1) load_step(q + 128);
+      if (q + 128 < p1) {
+        load_rows(prn);
+        prn = load_pairs(q + 256);
+      }
       v8bf bh[4], bl[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
