@@ -247,9 +247,12 @@ __global__ __launch_bounds__(256) void bn_stats_kernel(const T* __restrict__ Y, 
 }
 
 // S[o][b0 + bl][c] = sum over workgroups of partials[wg][o][bl][c] (fixed tree);
-// one workgroup per (o, bl, c).
+// one workgroup per (o, bl, c).  With `mean` (the MODE 0 sums, whose sample
+// counts are complete by now) it also writes mean[b][c] = S / max(count[b], 1).
 __global__ __launch_bounds__(256) void bn_reduce_kernel(const float* __restrict__ partials, int G, int NOUT, int bw,
-                                                        int C, int b0, int B, float* __restrict__ S) {
+                                                        int C, int b0, int B, float* __restrict__ S,
+                                                        const int32_t* __restrict__ counts,
+                                                        float* __restrict__ mean) {
   __shared__ float red[256];
   const int col = blockIdx.x, tid = threadIdx.x;
   const int width = NOUT * bw * C;
@@ -264,6 +267,10 @@ __global__ __launch_bounds__(256) void bn_reduce_kernel(const float* __restrict_
   if (tid == 0) {
     const int c = col % C, ob = col / C, bl = ob % bw, o = ob / bw;
     S[((int64_t)o * B + b0 + bl) * C + c] = red[0];
+    if (mean) {
+      const int cnt = counts[b0 + bl];
+      mean[(int64_t)(b0 + bl) * C + c] = red[0] / (float)(cnt > 1 ? cnt : 1);
+    }
   }
 }
 
@@ -459,7 +466,7 @@ __global__ __launch_bounds__(256) void bn_backward_kernel(const T* __restrict__ 
 template <typename T, typename CT, int MODE, int V>
 static void bn_stats_v(const T* Y, const T* dout, const T* out, int64_t n, int C, const CT* coords, int B,
                        const float* mean, const float* invstd, int relu, const BnGeom& gm, float* partials,
-                       float* S, int32_t* counts, hipStream_t stream) {
+                       float* S, int32_t* counts, float* mean_out, hipStream_t stream) {
   constexpr int NOUT = MODE == 2 ? 2 : 1;
   const int G = bn_blocks(n);
   const int CW = gm.TPR * V;
@@ -472,21 +479,25 @@ static void bn_stats_v(const T* Y, const T* dout, const T* out, int64_t n, int C
     const size_t lds = (size_t)nslot * w * per_b * 4;
     bn_stats_kernel<T, CT, V, MODE><<<grid, 256, lds, stream>>>(Y, dout, out, n, C, coords, b0, w, gm.RG, gm.TPR,
                                                                 mean, invstd, relu, partials, counts);
-    bn_reduce_kernel<<<(unsigned)(NOUT * w * C), 256, 0, stream>>>(partials, G, NOUT, w, C, b0, B, S);
+    bn_reduce_kernel<<<(unsigned)(NOUT * w * C), 256, 0, stream>>>(partials, G, NOUT, w, C, b0, B, S, counts,
+                                                                   MODE == 0 ? mean_out : nullptr);
   }
 }
 
 template <typename T, typename CT, int MODE>
 static int bn_stats(const T* Y, const T* dout, const T* out, int64_t n, int C, const CT* coords, int B,
                     const float* mean, const float* invstd, int relu, const BnGeom& gm, float* partials, float* S,
-                    int32_t* counts, hipStream_t stream) {
+                    int32_t* counts, float* mean_out, hipStream_t stream) {
   if (gm.V == 8) {
     if constexpr (sizeof(T) == 2)
-      bn_stats_v<T, CT, MODE, 8>(Y, dout, out, n, C, coords, B, mean, invstd, relu, gm, partials, S, counts, stream);
+      bn_stats_v<T, CT, MODE, 8>(Y, dout, out, n, C, coords, B, mean, invstd, relu, gm, partials, S, counts, mean_out,
+                                 stream);
   } else if (gm.V == 4) {
-    bn_stats_v<T, CT, MODE, 4>(Y, dout, out, n, C, coords, B, mean, invstd, relu, gm, partials, S, counts, stream);
+    bn_stats_v<T, CT, MODE, 4>(Y, dout, out, n, C, coords, B, mean, invstd, relu, gm, partials, S, counts, mean_out,
+                                 stream);
   } else {
-    bn_stats_v<T, CT, MODE, 1>(Y, dout, out, n, C, coords, B, mean, invstd, relu, gm, partials, S, counts, stream);
+    bn_stats_v<T, CT, MODE, 1>(Y, dout, out, n, C, coords, B, mean, invstd, relu, gm, partials, S, counts, mean_out,
+                                 stream);
   }
   ST_CHECK_LAUNCH();
   return ST_OK;
@@ -515,15 +526,16 @@ static int bn_forward(const T* Y, int64_t n, int C, const CT* coords, int B, con
     if (n == 0) {
       rc = st_fill_u32((uint32_t*)ws, 2 * BC, 0u, stream);
       if (rc != ST_OK) return rc;
+      bn_mean_kernel<<<st_blocks(BC, 256), 256, 0, stream>>>(S, counts, B, C, mean);
     } else {
+      // the reduce of these sums also writes the per-sample means
       rc = bn_stats<T, CT, 0>(Y, nullptr, nullptr, n, C, coords, B, nullptr, nullptr, 0, gm, partials, S, counts,
-                              stream);
+                              mean, stream);
       if (rc != ST_OK) return rc;
     }
-    bn_mean_kernel<<<st_blocks(BC, 256), 256, 0, stream>>>(S, counts, B, C, mean);
     if (n > 0) {
       rc = bn_stats<T, CT, 1>(Y, nullptr, nullptr, n, C, coords, B, mean, nullptr, 0, gm, partials, S2, nullptr,
-                              stream);
+                              nullptr, stream);
       if (rc != ST_OK) return rc;
     }
     const int64_t th = BC > C ? BC : C;
@@ -570,7 +582,7 @@ static int bn_backward(const T* Y, const T* out, const T* dout, int64_t n, int C
     // evaluation: per-channel sums over every row, as the statistics of one sample
     // (no coordinates: every row is sample 0; mean / invstd are per channel)
     const int rc = bn_stats<T, CT, 2>(Y, dout, out, n, C, training ? coords : (const CT*)nullptr, Bs, mean, invstd,
-                                      relu, gm, partials, S, nullptr, stream);
+                                      relu, gm, partials, S, nullptr, nullptr, stream);
     if (rc != ST_OK) return rc;
   }
   if (dweight || dbias)
