@@ -57,11 +57,9 @@ struct CubeKeyBits {
 };
 __constant__ CubeKeyBits kCubeKeyBits = CubeKeyBits();
 
-__global__ __launch_bounds__(256) void mask_keys_kernel(const uint32_t* __restrict__ masks, int W, int cube3,
-                                                        int64_t n, uint32_t* __restrict__ keys,
-                                                        int32_t* __restrict__ rows) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+// Sort key of row i: its mask words folded into 32 bits, for a 3x3x3 kernel
+// with the bits reordered by the offset's distance from the centre.
+__device__ __forceinline__ uint32_t mask_key(const uint32_t* __restrict__ masks, int W, int cube3, int64_t i) {
   uint32_t key = masks[i * W];
   for (int w = 1; w < W; ++w) {
     const uint32_t v = masks[i * W + w];
@@ -74,15 +72,25 @@ __global__ __launch_bounds__(256) void mask_keys_kernel(const uint32_t* __restri
 #pragma unroll
     for (int k = 0; k < 27; ++k) key |= ((m >> k) & 1u) << kCubeKeyBits.pos[k];
   }
-  keys[i] = key;
-  rows[i] = (int32_t)i;
+  return key;
 }
+
+// Keys of the first pass: computed from the masks (Keys::masks set, values =
+// row ids) instead of read from the key / value buffers of the previous pass.
+struct Keys {
+  const uint32_t* keys;
+  const int32_t* vals;
+  const uint32_t* masks;
+  int W, cube3;
+  __device__ __forceinline__ uint32_t key(int64_t i) const { return masks ? mask_key(masks, W, cube3, i) : keys[i]; }
+  __device__ __forceinline__ int32_t val(int64_t i) const { return masks ? (int32_t)i : vals[i]; }
+};
 
 // Every thread loads its J keys before the first LDS atomic, so a tile's
 // loads are all in flight together.
 template <int J>
-__global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift,
-                                                         int64_t ntiles, int32_t* __restrict__ hist) {
+__global__ __launch_bounds__(256) void radix_hist_kernel(Keys keys, int64_t n, int shift, int64_t ntiles,
+                                                         int32_t* __restrict__ hist) {
   constexpr int kTile = J * 256;
   __shared__ int h[kRadixBins];
 #pragma unroll
@@ -92,7 +100,7 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restr
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int64_t i = base + j * 256 + threadIdx.x;
-    d[j] = i < n ? (keys[i] >> shift) & (kRadixBins - 1) : (uint32_t)kRadixBins;
+    d[j] = i < n ? (keys.key(i) >> shift) & (kRadixBins - 1) : (uint32_t)kRadixBins;
   }
   __syncthreads();
 #pragma unroll
@@ -144,8 +152,7 @@ __global__ __launch_bounds__(256) void radix_colscan_kernel(int32_t* __restrict_
 // running per-digit positions alternate between two buffers by step parity,
 // which leaves one barrier per step.
 template <int J>
-__global__ __launch_bounds__(256) void radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
-                                                            const int32_t* __restrict__ vals_in, int64_t n, int shift,
+__global__ __launch_bounds__(256) void radix_scatter_kernel(Keys in, int64_t n, int shift,
                                                             int64_t ntiles, const int32_t* __restrict__ offsets,
                                                             const int32_t* __restrict__ totals,
                                                             uint32_t* __restrict__ keys_out,
@@ -162,8 +169,8 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint32_t* __re
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int64_t i = base + j * 256 + tid;
-    kk[j] = i < n ? keys_in[i] : 0u;
-    vv[j] = i < n ? vals_in[i] : 0;
+    kk[j] = i < n ? in.key(i) : 0u;
+    vv[j] = i < n ? in.val(i) : 0;
   }
   {
     const int d0 = 2 * tid;
@@ -304,25 +311,26 @@ extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, i
   uint32_t* kbuf[2] = {keys_tmp, keys_tmp + n};
   int32_t* hist = (int32_t*)workspace;
   int32_t* totals = hist + st::kRadixBins * ntiles;
-  st::mask_keys_kernel<<<st_blocks(n, 256), 256, 0, stream>>>(masks, mask_words, K == 27, n, kbuf[0],
-                                                               vbuf[0]);
   for (int p = 0; p < passes; ++p) {
     const int shift = p * st::kRadixBits;
     const int in = p & 1, out = in ^ 1;
     uint32_t* kout = p + 1 < passes ? kbuf[out] : nullptr;
+    // the first pass computes the keys from the masks; later ones read the previous pass's output
+    const st::Keys ks = p == 0 ? st::Keys{nullptr, nullptr, masks, mask_words, K == 27}
+                               : st::Keys{kbuf[in], vbuf[in], nullptr, 0, 0};
     if (tile == st::kRadixTileSmall)
-      st::radix_hist_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], n, shift,
-                                                                                             ntiles, hist);
+      st::radix_hist_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles,
+                                                                                             hist);
     else
-      st::radix_hist_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(kbuf[in], n, shift,
-                                                                                             ntiles, hist);
+      st::radix_hist_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles,
+                                                                                             hist);
     st::radix_colscan_kernel<<<st::kRadixBins / 4, 256, 0, stream>>>(hist, ntiles, totals);
     if (tile == st::kRadixTileSmall)
       st::radix_scatter_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(
-          kbuf[in], vbuf[in], n, shift, ntiles, hist, totals, kout, vbuf[out]);
+          ks, n, shift, ntiles, hist, totals, kout, vbuf[out]);
     else
       st::radix_scatter_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(
-          kbuf[in], vbuf[in], n, shift, ntiles, hist, totals, kout, vbuf[out]);
+          ks, n, shift, ntiles, hist, totals, kout, vbuf[out]);
   }
   ST_CHECK_LAUNCH();
   return ST_OK;
