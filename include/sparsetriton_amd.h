@@ -53,7 +53,10 @@ enum st_dtype { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2, ST_F32_BF16X3 = 3 };
 enum st_status_word {
   ST_STATUS_OVERFLOW = 0,  /* inserts that found the table full               */
   ST_STATUS_BAD_COORD = 1, /* coordinates that do not pack into a 64-bit key  */
-  ST_STATUS_DUPLICATE = 2, /* inserts whose key was already present           */
+  ST_STATUS_DUPLICATE = 2, /* rows whose coordinate an earlier row already has
+                              (counted by each pass that sees it: nonzero means
+                              the coordinate set has repeats)                 */
+  ST_STATUS_OUT_OF_BOX = 3, /* kernel-map query rows outside [0, shape)       */
   ST_STATUS_WORDS = 4,
 };
 
@@ -124,9 +127,13 @@ typedef struct st_occupancy {
 int st_occupancy_words(int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* words);
 
 /* Clears `words` and sets the bit of every coordinate row inside the box
- * (rows outside it are left to the table).  words: st_occupancy_words() u64s. */
+ * (rows outside it are left to the table).  words: st_occupancy_words() u64s.
+ * status (optional, ST_STATUS_WORDS int32): rows that do not pack into a key
+ * add to ST_STATUS_BAD_COORD, rows repeating an earlier row's coordinate to
+ * ST_STATUS_DUPLICATE (a submanifold map over repeated coordinates is not its
+ * own transpose). */
 int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t* words, int64_t batches, int64_t sx,
-                       int64_t sy, int64_t sz, st_stream_t stream);
+                       int64_t sy, int64_t sz, int32_t* status, st_stream_t stream);
 
 /*
  * Rank index of a built bitmap (no reference counterpart): the voxels of the
@@ -158,11 +165,17 @@ int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_o
  * The package stores maps offset-major, (K, n_out) (nbr_k_stride = n_out,
  * nbr_r_stride = 1): every kernel that walks rows then reads and writes each
  * offset's column with coalesced accesses.
+ * status (optional, ST_STATUS_WORDS int32): rows whose out_coords.xyz * stride
+ * lie outside [0, shape) add to ST_STATUS_OUT_OF_BOX.  Such a row keeps its
+ * in-bounds neighbours (the reference checks the neighbour only), but no row
+ * finds it as a neighbour, so a submanifold map is its own transpose (offsets
+ * reversed) only when this count and ST_STATUS_DUPLICATE are both zero.
  */
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
                   const uint32_t* vals, int64_t capacity, const st_occupancy* occ, int32_t* nbr,
-                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, st_stream_t stream);
+                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, int32_t* status,
+                  st_stream_t stream);
 
 /* Geometry of a strided or transposed convolution's output-coordinate build. */
 typedef struct st_outgeom {
@@ -229,11 +242,15 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
  * invnbr, and, if out_masks is non-null, out_masks (n_out, W) row masks of
  * nbr.  invnbr must be pre-filled with -1 and in_masks with 0.  Used when a
  * caller hands ConvPrecomputedNeighborGEMM a plain (N_out, K) map
- * (implicit_precomputed_gemm.py:237-242) and for the submanifold map, whose
- * transposed map feeds the atomic-free input gradient.
+ * (implicit_precomputed_gemm.py:237-242) and for a submanifold map that is not
+ * its own transpose, whose transposed map feeds the atomic-free input gradient.
+ * conflicts (optional, one int32, caller-zeroed): entries (k, o) -> i whose
+ * (k, i) another output already holds -- a map invnbr cannot represent (one
+ * input feeding two outputs through one offset: repeated output coordinates).
  */
 int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride, int64_t n_out, int K,
-                   int64_t n_in, int32_t* invnbr, uint32_t* in_masks, uint32_t* out_masks, st_stream_t stream);
+                   int64_t n_in, int32_t* invnbr, uint32_t* in_masks, uint32_t* out_masks, int32_t* conflicts,
+                   st_stream_t stream);
 
 /*
  * Destination-row order for the gather-GEMM (no reference counterpart; the
@@ -397,13 +414,17 @@ int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, c
 
 /* Lookup rule of the hash-fly kernels: for row r with coordinate c and offset k
  *   q = (c.xyz * mul + sign * offsets[k]) / div    (only when divisible)
- * looked up in the table if 0 <= q < bounds per axis. */
+ * looked up in the table if 0 <= q < bounds on every axis whose bound is > 0.
+ * The forward bounds the input coordinate (the reference's in-bounds test,
+ * implicit_hashfly_gemm.py:127); the input-gradient direction bounds the row
+ * (row_bounds = the input shape) and leaves the output unbounded, since the
+ * forward gives output rows outside the shape their in-bounds neighbours. */
 typedef struct st_lookup {
   int32_t K;
   int32_t sign;          /* -1 forward (q = c*s - t_k), +1 input-gradient direction   */
   int64_t mul;
   int64_t div;
-  int64_t bounds[3];     /* q must satisfy 0 <= q < bounds                            */
+  int64_t bounds[3];     /* if > 0: q must satisfy 0 <= q < bounds on that axis       */
   int64_t row_bounds[3]; /* if > 0: rows with c outside [0, row_bounds) get no pairs  */
 } st_lookup;
 

@@ -156,6 +156,48 @@ def wgrad_f64(X, dY, nbr, K) -> np.ndarray:
     return dW
 
 
+def _valid_pairs(nbr, k):
+    o = np.nonzero(nbr[:, k] >= 0)[0]
+    return nbr[o, k].astype(np.int64), o
+
+
+def fwd_f64_blas(X, W, nbr) -> np.ndarray:
+    """fwd_f64 as one float64 matrix product per offset (BLAS): the benchmark-size checker.
+    out[o] = sum_k X[nbr[o, k]] @ W[k] (implicit_precomputed_gemm.py:64-126)."""
+    X, W, nbr = _f64(X), _f64(W), _i32(nbr)
+    out = np.zeros((nbr.shape[0], W.shape[2]), dtype=np.float64)
+    for k in range(W.shape[0]):
+        i, o = _valid_pairs(nbr, k)
+        out[o] += X[i] @ W[k]  # o is unique within one offset
+    return out
+
+
+def dgrad_f64_blas(dY, W, nbr, n_in) -> np.ndarray:
+    """dgrad_f64 per offset (BLAS): dX[nbr[o, k]] += dY[o] @ W[k]^T, the reference's scatter
+    (implicit_precomputed_gemm.py:129-177); rows repeated within one offset accumulate."""
+    dY, W, nbr = _f64(dY), _f64(W), _i32(nbr)
+    dX = np.zeros((n_in, W.shape[1]), dtype=np.float64)
+    for k in range(W.shape[0]):
+        i, o = _valid_pairs(nbr, k)
+        contrib = dY[o] @ W[k].T
+        if np.unique(i).shape[0] == i.shape[0]:
+            dX[i] += contrib
+        else:
+            np.add.at(dX, i, contrib)
+    return dX
+
+
+def wgrad_f64_blas(X, dY, nbr, K) -> np.ndarray:
+    """wgrad_f64 per offset (BLAS): dW[k] = sum over pairs X[nbr[o, k]]^T dY[o]
+    (implicit_precomputed_gemm.py:180-230)."""
+    X, dY, nbr = _f64(X), _f64(dY), _i32(nbr)
+    dW = np.zeros((K, X.shape[1], dY.shape[1]), dtype=np.float64)
+    for k in range(K):
+        i, o = _valid_pairs(nbr, k)
+        dW[k] = X[i].T @ dY[o]
+    return dW
+
+
 # ------------------------------------------------- reference-algorithm port
 
 class RefHash:

@@ -104,6 +104,7 @@ int or_exact_kmap(const int32_t* in_coords, int64_t n_in, int64_t in_scale, cons
                   int32_t* nbr) {
   int64_t m;
   kv_t* kv = sorted_keys(in_coords, n_in, in_scale, &m);
+#pragma omp parallel for schedule(static)
   for (int64_t o = 0; o < n_out; ++o) {
     const int32_t* c = out_coords + 4 * o;
     for (int k = 0; k < K; ++k) {
@@ -290,6 +291,69 @@ void ref_kmap(const int32_t* out_coords, int64_t n_out, const int32_t* offsets, 
       nbr[o * K + k] = r;
     }
   }
+}
+
+/* Output coordinates as the reference builds them (kmap.py:213-444, one chunk): candidates
+ * in input-major / offset-minor order (expand_coords_kernel, :11-54) -- in + t_k, kept when
+ * every axis divides by the stride and divided (normal), or in * stride + t_k (transposed) --
+ * then the range filter [0, new_shape) (tile.py:6-85) and filter_unique_kernel's dedup
+ * (:56-97): a table of T = 2 * n * K int32 keys (key2 of the candidate, -1 empty), probe slots
+ * (h1 + 83492791 * (step / 8) + step) mod T, at most 1024 steps.  A candidate is kept when its
+ * CAS finds an empty slot and dropped when the slot already holds its key2, which happens for
+ * its own coordinate and for any other coordinate with the same key2 whose probe sequence
+ * passes that slot.  The GPU resolves candidates in lockstep blocks; this runs them one at a
+ * time in order, so it keeps each coordinate's first candidate.  Returns the number kept
+ * (written to out, at most n * K rows); *exhausted counts candidates that ran out of probes
+ * (dropped, as the reference drops them). */
+int64_t ref_out_coords(const int32_t* in, int64_t n, const int32_t* offsets, int K, int64_t stride, int transposed,
+                       int64_t sx, int64_t sy, int64_t sz, int32_t* out, int64_t* exhausted) {
+  const int64_t T = 2 * n * (int64_t)K;
+  int32_t* keys = (int32_t*)malloc(sizeof(int32_t) * (size_t)(T > 0 ? T : 1));
+  for (int64_t t = 0; t < T; ++t) keys[t] = -1;
+  const int64_t lim[3] = {sx, sy, sz};
+  int64_t m = 0, ex = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t* c = in + 4 * i;
+    for (int k = 0; k < K; ++k) {
+      int64_t o[3];
+      int ok = 1;
+      for (int a = 0; a < 3; ++a) {
+        int64_t v = transposed ? (int64_t)c[1 + a] * stride + offsets[3 * k + a] : (int64_t)c[1 + a] + offsets[3 * k + a];
+        if (!transposed && stride > 1) {
+          int64_t r = v % stride;
+          if (r < 0) r += stride; /* torch's % is a floor modulo */
+          if (r != 0) ok = 0;
+          v = (v - r) / stride;   /* floor division, as //= */
+        }
+        if (v < 0 || v > lim[a] - 1) ok = 0;
+        o[a] = v;
+      }
+      if (!ok) continue;
+      const uint32_t h = ref_h1(c[0], (int32_t)o[0], (int32_t)o[1], (int32_t)o[2]);
+      const int32_t key = ref_key2(c[0], (int32_t)o[0], (int32_t)o[1], (int32_t)o[2]);
+      int kept = 0, done = 0;
+      for (uint32_t step = 0; step < 1024 && !done; ++step) {
+        const uint32_t sl = ref_slot(h, step, (uint32_t)T);
+        if (keys[sl] == -1) {
+          keys[sl] = key;
+          kept = done = 1;
+        } else if (keys[sl] == key) {
+          done = 1;
+        }
+      }
+      if (!done) ++ex;
+      if (kept) {
+        int32_t* r = out + 4 * m++;
+        r[0] = c[0];
+        r[1] = (int32_t)o[0];
+        r[2] = (int32_t)o[1];
+        r[3] = (int32_t)o[2];
+      }
+    }
+  }
+  free(keys);
+  *exhausted = ex;
+  return m;
 }
 
 void ref_fwd_f32(const float* X, int Cin, const float* W, int K, int Cout, const int32_t* nbr, int64_t n_out,

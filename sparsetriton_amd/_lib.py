@@ -21,7 +21,7 @@ COORD_DTYPES = {torch.int16: 0, torch.int32: 1, torch.int64: 2}
 FEAT_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 STATUS_WORDS = 4
-STATUS_OVERFLOW, STATUS_BAD_COORD, STATUS_DUPLICATE = 0, 1, 2
+STATUS_OVERFLOW, STATUS_BAD_COORD, STATUS_DUPLICATE, STATUS_OUT_OF_BOX = 0, 1, 2, 3
 
 W_TRANSPOSE, W_REVERSE, W_COPY = 0, 1, 2
 MAX_KVOL = 512
@@ -73,15 +73,15 @@ _SIGNATURES = {
     "st_hash_insert": [_P, _I, _L, _L, _P, _P, _L, _P, _P],
     "st_hash_query": [_P, _I, _L, _P, _P, _L, _P, _P],
     "st_occupancy_words": [_L, _L, _L, _L, ctypes.POINTER(_L)],
-    "st_occupancy_build": [_P, _I, _L, _P, _L, _L, _L, _L, _P],
+    "st_occupancy_build": [_P, _I, _L, _P, _L, _L, _L, _L, _P, _P],
     "st_occupancy_rank": [_P, _I, _L, ctypes.POINTER(Occupancy), _P, _P, _P, _P],
     "st_kmap_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, ctypes.POINTER(Occupancy), _P, _L, _L, _P,
-                      _P],
+                      _P, _P],
     "st_outcoords_sizes": [_L, ctypes.POINTER(OutGeom), _L, _L, ctypes.POINTER(_L), ctypes.POINTER(_L)],
     "st_outcoords_plan": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _L, _P, _L, _P, _P],
     "st_outcoords_emit": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _P, _L, _P, _L, _P, _P, _L, _P, _L,
                           _P, _P, _P, _P, _P],
-    "st_kmap_invert": [_P, _L, _L, _L, _I, _L, _P, _P, _P, _P],
+    "st_kmap_invert": [_P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P],
     "st_kmap_sort_workspace": [_L, ctypes.POINTER(ctypes.c_size_t)],
     "st_kmap_sort_rows": [_P, _I, _I, _L, _P, _P, _P, _P, ctypes.c_size_t, _P],
     "st_kmap_pairs_sizes": [_L, _I, ctypes.POINTER(_L)],

@@ -58,17 +58,26 @@ __global__ __launch_bounds__(256) void hash_query_kernel(const CT* __restrict__ 
   out[i] = r;
 }
 
-// Sets the occupancy bit of every row inside the box.
+// Sets the occupancy bit of every row inside the box.  With `status`, a row
+// whose coordinate does not pack into a key counts as ST_STATUS_BAD_COORD and a
+// row that finds its bit already set (a repeated coordinate) as
+// ST_STATUS_DUPLICATE -- the bitmap path never runs the hash insert that would
+// otherwise report both.
 template <typename CT>
 __global__ __launch_bounds__(256) void occupancy_build_kernel(const CT* __restrict__ coords, int64_t n, Occ occ,
-                                                              uint64_t* __restrict__ words) {
+                                                              uint64_t* __restrict__ words,
+                                                              int32_t* __restrict__ status) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   int64_t b, x, y, z;
   load_coord(coords, i, b, x, y, z);
+  uint64_t key;
+  if (status && !pack_key(b, x, y, z, key)) atomicAdd(&status[ST_STATUS_BAD_COORD], 1);
   if (b < 0 || b >= occ.nb || x < 0 || x >= occ.sx || y < 0 || y >= occ.sy || z < 0 || z >= occ.sz) return;
-  atomicOr((unsigned long long*)&words[occ_word(occ, (int)b, (int)x, (int)y, (int)z)],
-           1ull << occ_bit((int)x, (int)y, (int)z));
+  const uint64_t bit = 1ull << occ_bit((int)x, (int)y, (int)z);
+  const unsigned long long old =
+      atomicOr((unsigned long long*)&words[occ_word(occ, (int)b, (int)x, (int)y, (int)z)], bit);
+  if (status && (old & bit)) atomicAdd(&status[ST_STATUS_DUPLICATE], 1);
 }
 
 // Rank index: popcount sums per 4096-word block, then per word the exclusive
@@ -165,7 +174,8 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
                                                          const uint64_t* __restrict__ keys,
                                                          const uint32_t* __restrict__ vals, uint32_t cap, Occ occ,
                                                          int32_t* __restrict__ nbr, int64_t ks, int64_t rs,
-                                                         uint32_t* __restrict__ row_masks) {
+                                                         uint32_t* __restrict__ row_masks,
+                                                         int32_t* __restrict__ status) {
   __shared__ int32_t off_s[ST_MAX_KVOL * 3];
   for (int t = threadIdx.x; t < K * 3; t += blockDim.x) off_s[t] = offsets[t];
   __syncthreads();
@@ -176,6 +186,10 @@ __global__ __launch_bounds__(256) void kmap_query_kernel(const CT* __restrict__ 
   x *= stride;
   y *= stride;
   z *= stride;
+  // rows outside the bounds still get their in-bounds neighbours, but no row finds them
+  // as a neighbour: the map is then not its own transpose (the caller's status tells it)
+  if (status && (x < 0 || x >= sx || y < 0 || y >= sy || z < 0 || z >= sz))
+    atomicAdd(&status[ST_STATUS_OUT_OF_BOX], 1);
   const int W = (K + 31) >> 5;
   uint32_t mword = 0;
   for (int k0 = 0; k0 < K; k0 += kQGroup) {
@@ -303,7 +317,7 @@ int st_occupancy_words(int64_t batches, int64_t sx, int64_t sy, int64_t sz, int6
 }
 
 int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t* words, int64_t batches, int64_t sx,
-                       int64_t sy, int64_t sz, st_stream_t stream) {
+                       int64_t sy, int64_t sz, int32_t* status, st_stream_t stream) {
   int64_t nw = 0;
   if (st_occupancy_words(batches, sx, sy, sz, &nw) != ST_OK || !words || n < 0 || n >= (1ll << 31))
     return ST_ERR_ARG;
@@ -316,7 +330,7 @@ int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t*
   if (n > 0) {
     ST_DISPATCH_COORD(coord_dtype, CT,
                       occupancy_build_kernel<CT><<<st_blocks(n, 256), 256, 0, stream>>>((const CT*)coords, n, occ,
-                                                                                         words));
+                                                                                         words, status));
   }
   ST_CHECK_LAUNCH();
   return ST_OK;
@@ -348,7 +362,8 @@ int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_o
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
                   const uint32_t* vals, int64_t capacity, const st_occupancy* occ, int32_t* nbr,
-                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, st_stream_t stream) {
+                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, int32_t* status,
+                  st_stream_t stream) {
   const bool rank_only = !keys && occ && occ->words && occ->prefix && occ->rowmap;
   if (n_out < 0 || K <= 0 || K > ST_MAX_KVOL || stride < 1 || capacity >= (1ll << 31)) return ST_ERR_ARG;
   if (!rank_only && capacity <= 0) return ST_ERR_ARG;
@@ -359,7 +374,7 @@ int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const 
   ST_DISPATCH_COORD(coord_dtype, CT,
                     kmap_query_kernel<CT><<<st_blocks(n_out, 256), 256, 0, stream>>>(
                         (const CT*)out_coords, n_out, offsets, K, stride, shape_x, shape_y, shape_z, keys, vals,
-                        (uint32_t)capacity, make_occ(occ), nbr, nbr_k_stride, nbr_r_stride, row_masks));
+                        (uint32_t)capacity, make_occ(occ), nbr, nbr_k_stride, nbr_r_stride, row_masks, status));
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

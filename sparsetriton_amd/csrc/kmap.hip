@@ -439,12 +439,15 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
 namespace st {
 
 // One thread per output row o: every valid (k, o) -> i entry becomes
-// invnbr[k][i] = o (offset-major, like the map).  For a convolution map each
-// (i, k) has at most one o, so the scatter has no write conflicts.
+// invnbr[k][i] = o (offset-major, like the map).  For a convolution map of
+// unique output coordinates each (i, k) has at most one o, so the scatter has
+// no write conflicts; the in-mask bit a row's atomic OR finds already set
+// reveals one, and is counted into `conflicts` (optional).
 __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restrict__ nbr, int64_t ks, int64_t rs,
                                                           int64_t n_out, int K, int64_t n_in,
                                                           int32_t* __restrict__ invnbr, uint32_t* __restrict__ in_masks,
-                                                          uint32_t* __restrict__ out_masks) {
+                                                          uint32_t* __restrict__ out_masks,
+                                                          int32_t* __restrict__ conflicts) {
   const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (o >= n_out) return;
   const int W = (K + 31) >> 5;
@@ -453,8 +456,10 @@ __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restr
     const int32_t i = nbr[(int64_t)k * ks + o * rs];
     if (i >= 0 && (int64_t)i < n_in) {
       invnbr[(int64_t)k * n_in + i] = (int32_t)o;
-      atomicOr(&in_masks[(int64_t)i * W + (k >> 5)], 1u << (k & 31));
-      mword |= 1u << (k & 31);
+      const uint32_t bit = 1u << (k & 31);
+      const uint32_t old = atomicOr(&in_masks[(int64_t)i * W + (k >> 5)], bit);
+      if (conflicts && (old & bit)) atomicAdd(conflicts, 1);
+      mword |= bit;
     }
     if ((k & 31) == 31 || k == K - 1) {
       if (out_masks) out_masks[o * W + (k >> 5)] = mword;
@@ -467,13 +472,13 @@ __global__ __launch_bounds__(256) void kmap_invert_kernel(const int32_t* __restr
 
 extern "C" int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride, int64_t n_out, int K,
                               int64_t n_in, int32_t* invnbr, uint32_t* in_masks, uint32_t* out_masks,
-                              st_stream_t stream) {
+                              int32_t* conflicts, st_stream_t stream) {
   if (n_out < 0 || n_in < 0 || K <= 0 || K > ST_MAX_KVOL) return ST_ERR_ARG;
   if (n_out >= (1ll << 31) || n_in >= (1ll << 31)) return ST_ERR_ARG;
   if (n_out == 0) return ST_OK;
   if (!nbr || (n_in > 0 && (!invnbr || !in_masks))) return ST_ERR_ARG;
   st::kmap_invert_kernel<<<st_blocks(n_out, 256), 256, 0, stream>>>(nbr, nbr_k_stride, nbr_r_stride, n_out, K, n_in,
-                                                                    invnbr, in_masks, out_masks);
+                                                                    invnbr, in_masks, out_masks, conflicts);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

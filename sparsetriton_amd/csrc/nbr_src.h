@@ -8,8 +8,9 @@
 //             coalesced 512-byte loads instead of one cache line per entry.
 //   HashSrc : probe the coordinate table inside the GEMM (implicit hash-fly):
 //             q = (c.xyz * mul + sign * offsets[k]) / div, kept only when the
-//             division is exact and 0 <= q < bounds, then looked up.  Rows whose
-//             own c lies outside [0, row_bounds) (when given) have no pairs.
+//             division is exact and 0 <= q < bounds (on each axis whose bound
+//             is > 0), then looked up.  Rows whose own c lies outside
+//             [0, row_bounds) (when given) have no pairs.
 //
 // A source is used as  rc = src.row(r)  (once per row)  then  src.get(rc, k).
 // k is uniform across the workgroup in every caller, so offsets[k] is a
@@ -78,14 +79,14 @@ struct HashSrc {
     int64_t qx = c.x + sign * (int64_t)offsets[3 * k];
     int64_t qy = c.y + sign * (int64_t)offsets[3 * k + 1];
     int64_t qz = c.z + sign * (int64_t)offsets[3 * k + 2];
-    if (qx < 0 || qy < 0 || qz < 0) return -1;
     if (div > 1) {
       if (qx % div || qy % div || qz % div) return -1;
       qx /= div;
       qy /= div;
       qz /= div;
     }
-    if (qx >= bx || qy >= by || qz >= bz) return -1;
+    if ((bx > 0 && (qx < 0 || qx >= bx)) || (by > 0 && (qy < 0 || qy >= by)) || (bz > 0 && (qz < 0 || qz >= bz)))
+      return -1;
     uint64_t key;
     if (!pack_key(c.b, qx, qy, qz, key)) return -1;
     const uint32_t s = find_slot(keys, cap, key);

@@ -152,6 +152,10 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
     cache_key = (k, s, p, d, submanifold, transposed)
     algo = get_conv_algo()
 
+    # A fresh map build ends with an asynchronous copy of the table's status words; once the
+    # forward is queued the host waits for that copy (not for the forward) and raises if a
+    # coordinate could not be keyed or the table overflowed -- rows the map would silently lack.
+    table_status = None
     if algo == ConvAlgo.PrecomputedNeighborGEMM:
         hit = tensor._cache.neighbor_indices.get(cache_key)
         if hit is not None:
@@ -160,13 +164,16 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
             if subm_fast:
                 out_coords, new_shape = tensor.C, tensor.spatial_shape
                 offsets = _target_offsets(k, d, p, False, device)
+                # the symmetric claim is checked against the query's duplicate / out-of-bounds counts
                 kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1, tensor.C.shape[0],
                                         symmetric=(k % 2 == 1))
             else:
                 out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
                     tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
+            table_status = in_table.snapshot()
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
         if out_coords.shape[0] == 0:
+            _raise_table_errors(table_status, in_table)
             return _empty(tensor, C_out, new_shape)
         if epilogue is not None:
             out_feats = conv_forward_epilogue(tensor.F, weight, kmap, bias, *epilogue)
@@ -179,25 +186,29 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
     elif algo == ConvAlgo.ImplicitHashFlyGEMM:
         hkey = ("hashfly",) + cache_key
         hit = tensor._cache.kmaps.get(hkey)
+        in_keys, in_vals = in_table.table_keys, in_table.table_values  # runs a deferred insert
         if hit is None:
             if subm_fast:
                 out_coords, new_shape = tensor.C, tensor.spatial_shape
                 offsets = _target_offsets(k, d, p, False, device).to(tensor.C.dtype)
-                gl = InputGradLookup(in_table.table_keys, in_table.table_values, 1, 1, new_shape,
-                                     tensor.spatial_shape)
+                table_status = in_table.snapshot()
+                gl = InputGradLookup(in_keys, in_vals, 1, 1, new_shape, tensor.spatial_shape,
+                                     duplicate_check=table_status)
             else:
                 out_coords, new_shape, offsets, _, out_table = build_out_coords_and_map(
                     tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=False)
                 mul, div = (s, 1) if transposed else (1, s)
+                table_status = in_table.snapshot()
                 gl = InputGradLookup(out_table.table_keys, out_table.table_values, mul, div, new_shape,
-                                     tensor.spatial_shape)
+                                     tensor.spatial_shape, duplicate_check=table_status)
             hit = (out_coords, new_shape, offsets, gl)
             tensor._cache.kmaps[hkey] = hit
         out_coords, new_shape, offsets, gl = hit
         if out_coords.shape[0] == 0:
+            _raise_table_errors(table_status, in_table)
             return _empty(tensor, C_out, new_shape)
         out_feats = ConvHashOnTheFlyImplicitGEMM.apply(
-            tensor.F, weight, out_coords, offsets, in_table.table_keys, in_table.table_values, lookup_shape,
+            tensor.F, weight, out_coords, offsets, in_keys, in_vals, lookup_shape,
             1 if transposed else s, tensor.C, gl)
         if bias is not None:
             # in the features' dtype, as the reference's in-place `out_feats += bias` (conv.py:227-228);
@@ -205,11 +216,17 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
             out_feats = out_feats + bias.to(out_feats.dtype)
     else:
         raise ValueError(f"unknown convolution algorithm {algo}")
+    _raise_table_errors(table_status, in_table)
 
     if submanifold and (out_coords is tensor.C or (out_coords.shape == tensor.C.shape
                                                    and torch.equal(out_coords, tensor.C))):
         return tensor.replace(out_feats)
     return SparseTensor(feats=out_feats, coords=out_coords, spatial_shape=new_shape, batch_size=tensor.batch_size)
+
+
+def _raise_table_errors(status, table: HashTable) -> None:
+    if status is not None:
+        status.raise_errors(table.capacity)
 
 
 def _empty(tensor: SparseTensor, C_out: int, new_shape) -> SparseTensor:

@@ -28,7 +28,7 @@ from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import 
     weight_prep,
     wgrad_splits,
 )
-from sparsetriton_amd.nn.functional.conv.kmap import KernelMap
+from sparsetriton_amd.nn.functional.conv.kmap import KernelMap, row_representatives
 
 __all__ = ["ConvHashOnTheFlyImplicitGEMM", "InputGradLookup"]
 
@@ -75,19 +75,35 @@ class InputGradLookup:
 
     Forward pairs satisfy ``out * s - t_k = in_key``; solved for the output:
     ``out = (in * mul + t_k) / div``, looked up in ``table_keys`` /
-    ``table_values`` (a table of the output coordinates) within ``out_shape``.
-    Input rows outside ``in_shape`` have no forward pairs.
+    ``table_values`` (a table of the output coordinates).  Input rows outside
+    ``in_shape`` have no forward pairs; the output is not bounded (a
+    submanifold output row outside ``out_shape`` still takes its in-bounds
+    neighbours in the forward).
 
       submanifold / stride 1 : mul 1, div 1, table = input table
       strided (s)            : mul 1, div s, table = output dedup table
       transposed (s)         : mul s, div 1, table = output dedup table
+
+    The rule finds one output row per coordinate and assumes each input
+    coordinate is one row: with repeated input coordinates the forward reads
+    only the lowest of them, so the lookup is disabled (``usable()`` False)
+    when ``duplicate_check`` -- a StatusSnapshot of the input table -- counts
+    any, and the input gradient takes the transposed-map path instead.
     """
 
-    def __init__(self, table_keys, table_values, mul: int, div: int, out_shape, in_shape):
+    def __init__(self, table_keys, table_values, mul: int, div: int, out_shape, in_shape, duplicate_check=None):
         self.table_keys, self.table_values = table_keys, table_values
         self.mul, self.div = int(mul), int(div)
         self.out_shape = tuple(int(v) for v in out_shape)
         self.in_shape = tuple(int(v) for v in in_shape)
+        self._check = duplicate_check
+        self._usable = True
+
+    def usable(self) -> bool:
+        if self._check is not None:
+            self._usable = self._check.counters()["duplicate"] == 0
+            self._check = None
+        return self._usable
 
 
 class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
@@ -126,17 +142,20 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             w = weights.to(features.dtype).contiguous()
             gl = ctx.grad_lookup
-            if ctx.in_coords is not None and gl is not None:
-                lk = _lookup(K, +1, gl.mul, gl.div, gl.out_shape, gl.in_shape)
+            if ctx.in_coords is not None and gl is not None and gl.usable():
+                lk = _lookup(K, +1, gl.mul, gl.div, (0, 0, 0), gl.in_shape)
                 grad_input = hashfly_gemm(grad_output, ctx.in_coords.contiguous(), offs, lk, gl.table_keys,
                                           gl.table_values, w, N_in)
             else:
                 nbr = torch.empty((K, coords.shape[0]), dtype=torch.int32, device=coords.device)
                 _lib.call("st_kmap_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0],
                           _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0], None,
-                          _lib.ptr(nbr), coords.shape[0], 1, None, _lib.stream_of(coords.device))
-                kmap = KernelMap(nbr, N_in, coords.shape[0], K).ensure_inverse()
-                grad_input = gather_gemm(grad_output, kmap.invnbr, N_in, 1, kmap.in_masks, w, N_in, K)
+                          _lib.ptr(nbr), coords.shape[0], 1, None, None, _lib.stream_of(coords.device))
+                kmap = KernelMap(nbr, N_in, coords.shape[0], K)
+                kmap.set_row_representatives(row_representatives(coords))  # repeated output coordinates
+                kmap.ensure_inverse()
+                grad_input = gather_gemm(kmap.fold_output_rows(grad_output), kmap.invnbr, N_in, 1, kmap.in_masks,
+                                         w, N_in, K)
         if ctx.needs_input_grad[1]:
             lk = _lookup(K, -1, s, 1, ctx.shape)
             grad_weights = hashfly_wgrad(features, grad_output, coords, offs, lk, keys, vals, weights.dtype)

@@ -118,6 +118,7 @@ def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> tor
     with offsets reversed: dX[i] = sum_j dY[nbr[j, i]] @ W[K-1-j]^T."""
     if kmap.symmetric:
         W = weight_prep(W, _lib.W_REVERSE)
+    dY = kmap.fold_output_rows(dY)
     if tiled_ok(dY.dtype, dY.shape[1]):
         return gather_gemm_tiled(dY, kmap.backward_tiles(), W, kmap.n_in, kmap.K)
     plan = kmap.backward_plan()

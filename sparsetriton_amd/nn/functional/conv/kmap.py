@@ -35,6 +35,7 @@ __all__ = [
     "compute_target_offsets_transposed",
     "build_out_coords",
     "KernelMap",
+    "row_representatives",
     "TilePlan",
     "PairList",
     "out_spatial_shape",
@@ -113,13 +114,28 @@ class KernelMap:
 
     def __init__(self, nbr: torch.Tensor, n_in: int, n_out: int, K: int, out_masks: Optional[torch.Tensor] = None,
                  invnbr: Optional[torch.Tensor] = None, in_masks: Optional[torch.Tensor] = None,
-                 k_stride: Optional[int] = None, r_stride: Optional[int] = None, symmetric: bool = False):
+                 k_stride: Optional[int] = None, r_stride: Optional[int] = None, symmetric: bool = False,
+                 symmetry_check=None):
         self.nbr = nbr
         # A submanifold map of an odd kernel is its own transpose with the offsets
-        # reversed: base_{K-1-k} = -base_k, so nbr[k, o] = i <=> nbr[K-1-k, i] = o
-        # (coordinates unique).  The input gradient then gathers through ``nbr``
-        # itself, with the forward's masks and tile order and reversed weights.
-        self.symmetric = bool(symmetric) and int(n_in) == int(n_out)
+        # reversed: base_{K-1-k} = -base_k, so nbr[k, o] = i <=> nbr[K-1-k, i] = o --
+        # provided the coordinates are unique and inside the query bounds (a row
+        # outside them keeps its in-bounds neighbours, but no row finds it).  The
+        # input gradient then gathers through ``nbr`` itself, with the forward's
+        # masks and tile order and reversed weights.  ``symmetry_check`` (a
+        # StatusSnapshot of the query's duplicate / out-of-bounds counts) confirms
+        # the claim the first time it is needed; otherwise the transpose is built.
+        self._symmetric = bool(symmetric) and int(n_in) == int(n_out)
+        self._symmetry_check = symmetry_check if self._symmetric else None
+        # Output rows repeating a coordinate have identical map rows: one input then feeds
+        # several outputs through one offset, which ``invnbr`` cannot hold.  ``row_rep`` (the
+        # lowest row of each output's coordinate, when any repeat) folds them: the transposed
+        # map is built over the representatives only and the input gradient first sums dY
+        # over each coordinate's rows.  ``_out_coords`` lets the symmetry check find them.
+        self.row_rep = None
+        self._out_coords = None
+        self.raw = False  # a caller's map: its transpose is checked for conflicts
+        self._conflicts = None
         self.n_in, self.n_out, self.K = int(n_in), int(n_out), int(K)
         self.k_stride = int(n_out) if k_stride is None else int(k_stride)
         self.r_stride = 1 if r_stride is None else int(r_stride)
@@ -147,8 +163,31 @@ class KernelMap:
         if nbr.dtype != torch.int32:
             nbr = nbr.to(torch.int32)
         n_out, K = nbr.shape
-        return cls(nbr, n_in, n_out, K, k_stride=nbr.stride(1), r_stride=nbr.stride(0))
+        km = cls(nbr, n_in, n_out, K, k_stride=nbr.stride(1), r_stride=nbr.stride(0))
+        km.raw = True
+        return km
 
+    @property
+    def symmetric(self) -> bool:
+        """Whether ``nbr`` read with offsets reversed is the transposed map (resolved once,
+        waiting at most for the map build's status copy)."""
+        chk = self._symmetry_check
+        if chk is not None:
+            c = chk.counters()
+            self._symmetric = c["duplicate"] == 0 and c["out_of_box"] == 0
+            self._symmetry_check = None
+            if c["duplicate"] and self._out_coords is not None:
+                self.set_row_representatives(row_representatives(self._out_coords))
+            self._out_coords = None
+        return self._symmetric
+
+    def set_row_representatives(self, rep: Optional[torch.Tensor]) -> "KernelMap":
+        """Declare repeated output coordinates (``rep`` from ``row_representatives``, or None)."""
+        assert self.invnbr is None, "set the representatives before the transposed map is built"
+        self.row_rep = rep
+        if rep is not None:
+            self._symmetric = False
+        return self
     @property
     def mask_words(self) -> int:
         return _mask_words(self.K)
@@ -163,15 +202,51 @@ class KernelMap:
             return self
         dev = self.nbr.device
         W = self.mask_words
-        self.invnbr = _lib.fill_(torch.empty((self.K, self.n_in), dtype=torch.int32, device=dev), -1)
-        self.in_masks = _lib.fill_(torch.empty((self.n_in, W), dtype=torch.int32, device=dev), 0)
         need_out = self.out_masks is None
         if need_out:
             self.out_masks = torch.empty((self.n_out, W), dtype=torch.int32, device=dev)
-        _lib.call("st_kmap_invert", _lib.ptr(self.nbr), self.k_stride, self.r_stride, self.n_out, self.K, self.n_in,
-                  _lib.ptr(self.invnbr), _lib.ptr(self.in_masks), _lib.ptr(self.out_masks) if need_out else None,
-                  _lib.stream_of(dev))
+        src, ks, rs = self.nbr, self.k_stride, self.r_stride
+        if self.row_rep is not None:
+            if need_out:  # the forward's masks come from the whole map
+                self._invert(src, ks, rs, self.out_masks, None)
+                need_out = False
+            keep = self.row_rep == torch.arange(self.n_out, dtype=self.row_rep.dtype, device=dev)
+            full = torch.as_strided(self.nbr, (self.K, self.n_out), (self.k_stride, self.r_stride))
+            src, ks, rs = torch.where(keep[None, :], full, torch.full_like(full, -1)).contiguous(), self.n_out, 1
+        self._conflicts = torch.zeros((1,), dtype=torch.int32, device=dev) if self.raw else None
+        self.invnbr, self.in_masks = self._invert(src, ks, rs, self.out_masks if need_out else None,
+                                                  self._conflicts)
         return self
+
+    def _check_transposable(self) -> None:
+        """Before the transposed map feeds an input gradient: a caller's map must send each
+        (input, offset) to at most one output (synchronises once, caller's maps only)."""
+        c = self._conflicts
+        if c is not None:
+            self._conflicts = None
+            n = int(c.item())
+            if n:
+                raise ValueError(
+                    f"neighbor_indices sends one input row to several output rows through one offset ({n} "
+                    "entries); the gather input gradient needs a convolution map, where each (input, offset) "
+                    "feeds at most one output")
+
+    def _invert(self, src, ks, rs, out_masks, conflicts):
+        dev = src.device
+        invnbr = _lib.fill_(torch.empty((self.K, self.n_in), dtype=torch.int32, device=dev), -1)
+        in_masks = _lib.fill_(torch.empty((self.n_in, self.mask_words), dtype=torch.int32, device=dev), 0)
+        _lib.call("st_kmap_invert", _lib.ptr(src), ks, rs, self.n_out, self.K, self.n_in, _lib.ptr(invnbr),
+                  _lib.ptr(in_masks), _lib.ptr(out_masks), _lib.ptr(conflicts), _lib.stream_of(dev))
+        return invnbr, in_masks
+
+    def fold_output_rows(self, dY: torch.Tensor) -> torch.Tensor:
+        """dY summed over the rows of each repeated output coordinate into its lowest row (the
+        row the transposed map holds); dY itself when no coordinate repeats."""
+        if self.row_rep is None:
+            return dY
+        acc = torch.zeros(dY.shape, dtype=torch.float32, device=dY.device)
+        acc.index_add_(0, self.row_rep.long(), dY.float())
+        return acc.to(dY.dtype)
 
     def ensure_out_masks(self) -> "KernelMap":
         if self.out_masks is None:
@@ -200,6 +275,7 @@ class KernelMap:
             return self.forward_tiles()
         if self._bwd_tiles is None:
             plan = self.backward_plan()
+            self._check_transposable()
             self._bwd_tiles = TileMap.build(self.invnbr, self.n_in, 1, self.in_masks, self.K, plan.perm, self.n_in,
                                             self.n_out)
         return self._bwd_tiles
@@ -210,6 +286,7 @@ class KernelMap:
             return self.forward_plan()
         if self._bwd is None:
             self.ensure_inverse()
+            self._check_transposable()
             self._bwd = TilePlan.build(self.n_in, self.K, self.in_masks)
         return self._bwd
 
@@ -268,6 +345,22 @@ class KernelMap:
         t = torch.stack([nb[o, k], o, k], dim=1)
         key = (t[:, 0] * (self.n_out + 1) + t[:, 1]) * (self.K + 1) + t[:, 2]
         return t[torch.argsort(key)]
+
+
+def row_representatives(coords: torch.Tensor) -> Optional[torch.Tensor]:
+    """For (N, 4) coordinates with repeats: int32 (N,) lowest row holding each row's coordinate;
+    None when every coordinate is unique (synchronises: only the repeated-coordinate path
+    calls it)."""
+    n = coords.shape[0]
+    c = coords.to(torch.int64)
+    key = (c[:, 0] << 48) | ((c[:, 1] & 0xFFFF) << 32) | ((c[:, 2] & 0xFFFF) << 16) | (c[:, 3] & 0xFFFF)
+    uniq, inv = torch.unique(key, return_inverse=True)
+    if uniq.shape[0] == n:
+        return None
+    rows = torch.arange(n, dtype=torch.int64, device=coords.device)
+    first = torch.full((uniq.shape[0],), n, dtype=torch.int64, device=coords.device)
+    first.scatter_reduce_(0, inv, rows, reduce="amin")
+    return first[inv].to(torch.int32)
 
 
 _SIDE_STREAMS = {}
@@ -378,7 +471,11 @@ def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets:
     """nbr[k, o] = row of out_o * stride - t_k (bounds [0, shape)), via ``st_kmap_query``.
 
     ``symmetric`` declares a submanifold map of an odd kernel (offsets ``t`` and
-    ``-t`` at k and K-1-k), whose transpose is the map itself read backwards."""
+    ``-t`` at k and K-1-k) over the table's own coordinates, whose transpose is
+    the map itself read backwards when those coordinates are unique and inside
+    ``spatial_shape``: the query counts rows outside it into the table's status
+    words (the table build counts repeats), and the map checks both counts
+    before it first relies on the claim."""
     out_coords = out_coords.contiguous()
     dev = out_coords.device
     _lib.require_device(out_coords, "out_coords")
@@ -400,10 +497,14 @@ def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets:
         cap = 0
     else:
         keys, vals, cap = _lib.ptr(table.table_keys), _lib.ptr(table.table_values), table.capacity
+    status = table.status_tensor() if symmetric else None
     _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out,
               _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, keys, vals, cap, occ,
-              _lib.ptr(nbr), n_out, 1, _lib.ptr(masks), _lib.stream_of(dev))
-    return KernelMap(nbr, n_in, n_out, K, out_masks=masks, symmetric=symmetric)
+              _lib.ptr(nbr), n_out, 1, _lib.ptr(masks), _lib.ptr(status), _lib.stream_of(dev))
+    check = table.snapshot() if symmetric else None
+    km = KernelMap(nbr, n_in, n_out, K, out_masks=masks, symmetric=symmetric, symmetry_check=check)
+    km._out_coords = out_coords if symmetric else None
+    return km
 
 
 class OutCoordTable:

@@ -31,7 +31,43 @@ import torch
 from sparsetriton_amd import _lib
 from sparsetriton_amd.config import get_coords_dtype
 
-__all__ = ["HashTable", "flatten_coord", "hash_coords", "unflatten_coord"]
+__all__ = ["HashTable", "StatusSnapshot", "flatten_coord", "hash_coords", "unflatten_coord"]
+
+
+class StatusSnapshot:
+    """Host copy of a device status buffer (``ST_STATUS_WORDS`` int32), taken without stalling
+    the stream: the copy into pinned memory is queued behind the kernels that fill the buffer,
+    and ``values()`` waits only for that copy -- not for whatever the stream runs after it."""
+
+    def __init__(self, status: torch.Tensor):
+        self._host = torch.empty(tuple(status.shape), dtype=status.dtype, pin_memory=True)
+        self._host.copy_(status, non_blocking=True)
+        self._event = torch.cuda.Event()
+        self._event.record(torch.cuda.current_stream(status.device))
+        self._values = None
+
+    def values(self) -> list:
+        if self._values is None:
+            self._event.synchronize()
+            self._values = self._host.tolist()
+        return self._values
+
+    def counters(self) -> dict:
+        v = self.values()
+        return {"overflow": v[_lib.STATUS_OVERFLOW], "bad_coord": v[_lib.STATUS_BAD_COORD],
+                "duplicate": v[_lib.STATUS_DUPLICATE], "out_of_box": v[_lib.STATUS_OUT_OF_BOX]}
+
+    def raise_errors(self, capacity: int) -> None:
+        """Raise on a full table or coordinates that cannot be keyed (rows the kernels could not
+        place: their neighbours would silently be missing)."""
+        c = self.counters()
+        if c["overflow"]:
+            raise RuntimeError(f"HashTable: {c['overflow']} inserts found the table full (capacity {capacity})")
+        if c["bad_coord"]:
+            raise RuntimeError(
+                f"HashTable: {c['bad_coord']} coordinates outside the packable range "
+                "(batch in [0, 32767], x/y/z in [-32768, 32767])"
+            )
 
 
 def flatten_coord(coords: torch.Tensor) -> torch.Tensor:
@@ -215,7 +251,7 @@ class HashTable:
         words = torch.empty((nw.value,), dtype=torch.int64, device=self.device)
         stream = _lib.stream_of(self.device)
         _lib.call("st_occupancy_build", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(words),
-                  int(batch_size), sx, sy, sz, stream)
+                  int(batch_size), sx, sy, sz, _lib.ptr(self._status()), stream)
         occ = _lib.Occupancy(words.data_ptr(), int(batch_size), (_lib.ctypes.c_int64 * 3)(sx, sy, sz), int(scale),
                              None, None)
         keep = [words]
@@ -247,20 +283,23 @@ class HashTable:
                   _lib.ptr(self.table_values), self.capacity, _lib.ptr(out), _lib.stream_of(self.device))
         return out
 
+    def status_tensor(self) -> torch.Tensor:
+        """The device status words the table's kernels count into (``ST_STATUS_WORDS`` int32):
+        overflow, bad_coord, duplicate and out_of_box (rows of a submanifold map query outside
+        its bounds)."""
+        return self._status()
+
+    def snapshot(self) -> StatusSnapshot:
+        """Asynchronous host copy of the status words as of the work queued so far (the deferred
+        insert is not forced: a table used only through its rank index never runs it)."""
+        return StatusSnapshot(self._status())
+
     def counters(self) -> dict:
-        """Device failure counters (synchronises): overflow, bad_coord, duplicate."""
+        """Device failure counters (synchronises): overflow, bad_coord, duplicate, out_of_box."""
         self._materialize()
-        s = self._status().tolist()
-        return {"overflow": s[_lib.STATUS_OVERFLOW], "bad_coord": s[_lib.STATUS_BAD_COORD],
-                "duplicate": s[_lib.STATUS_DUPLICATE]}
+        return self.snapshot().counters()
 
     def check(self) -> None:
         """Raise if any insert found the table full or a coordinate unpackable."""
-        c = self.counters()
-        if c["overflow"]:
-            raise RuntimeError(f"HashTable: {c['overflow']} inserts found the table full (capacity {self.capacity})")
-        if c["bad_coord"]:
-            raise RuntimeError(
-                f"HashTable: {c['bad_coord']} coordinates outside the packable range "
-                "(batch in [0, 32767], x/y/z in [-32768, 32767])"
-            )
+        self._materialize()
+        self.snapshot().raise_errors(self.capacity)

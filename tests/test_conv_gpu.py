@@ -142,6 +142,59 @@ def test_general_geometries(device, dtype, k, s, p, d, tr):
         assert rel(w.grad.float().cpu(), gw) < tol, algo
 
 
+@pytest.mark.parametrize("algo", list(ConvAlgo))
+@pytest.mark.parametrize("case", ["in_box", "out_of_box", "duplicates", "both"])
+def test_subm_rows_outside_shape_or_repeated(device, algo, case):
+    """Submanifold fwd + dX + dW when rows lie outside spatial_shape or repeat a coordinate.
+
+    Such a map is not its own transpose: a row outside the shape keeps its in-bounds
+    neighbours (the reference bounds the neighbour only, conv.py:55-59) but no row finds it,
+    and a repeated coordinate resolves to its lowest row.  The input gradient must still be
+    the adjoint of the forward -- the reference's scatter over the forward map
+    (implicit_precomputed_gemm.py:129-177), which the oracle's dgrad restates."""
+    rng = np.random.default_rng(31)
+    n, S = 2000, 20
+    c = _rand_coords(rng, n, S)
+    shape = (S, S, S)
+    if case in ("out_of_box", "both"):
+        shape = (15, 18, 20)
+    if case in ("duplicates", "both"):
+        rows = rng.choice(n, 150, replace=False)
+        c[rows[75:]] = c[rows[:75]]  # 75 rows repeat another row's coordinate
+    X = rng.standard_normal((n, 32)).astype(np.float32)
+    W = (rng.standard_normal((27, 32, 24)) / np.sqrt(27 * 32)).astype(np.float32)
+    dY = rng.standard_normal((n, 24)).astype(np.float32)
+    set_conv_algo(algo)
+    feats = torch.as_tensor(X, device=device).requires_grad_(True)
+    w = torch.as_tensor(W, device=device).requires_grad_(True)
+    sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=shape, batch_size=2)
+    out = sparse_conv3d(sp, w, 3)
+    out.F.backward(torch.as_tensor(dY, device=device))
+    y, gx, gw = _oracle(c, c, shape, X, W, dY, 3, 1, 1, 1, False)
+    assert rel(out.F.detach().cpu(), y) < 1e-4
+    assert rel(feats.grad.cpu(), gx) < 1e-4, case
+    assert rel(w.grad.cpu(), gw) < 1e-4
+    if algo == ConvAlgo.PrecomputedNeighborGEMM:
+        kmap = sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)][1]
+        assert kmap.symmetric == (case == "in_box")
+    else:
+        gl = sp._cache.kmaps[("hashfly", 3, 1, 1, 1, True, False)][3]
+        assert gl.usable() == (case in ("in_box", "out_of_box"))
+
+
+@pytest.mark.parametrize("algo", list(ConvAlgo))
+def test_unpackable_coordinates_raise(device, algo):
+    """A coordinate the table cannot key (negative batch) raises instead of silently losing its
+    row's neighbours."""
+    c = _rand_coords(np.random.default_rng(32), 500, 12)
+    c[7, 0] = -1
+    set_conv_algo(algo)
+    sp = SparseTensor(torch.randn(500, 8, device=device), torch.as_tensor(c, device=device),
+                      spatial_shape=(12, 12, 12), batch_size=2)
+    with pytest.raises(RuntimeError, match="packable range"):
+        sparse_conv3d(sp, torch.randn(27, 8, 8, device=device), 3)
+
+
 def test_mixed_precision_weight_grad_dtype(device):
     # bf16 activations with fp32 master weights: dW comes back in fp32
     rng = np.random.default_rng(2)
@@ -224,6 +277,22 @@ def test_plain_neighbor_indices_tensor(device):
     assert rel(out.detach().cpu(), O.fwd_f64(X, W, nbr)) < 1e-5
     assert rel(feats.grad.cpu(), O.dgrad_f64(dY, W, nbr, 3000)) < 1e-5
     assert rel(w.grad.cpu(), O.wgrad_f64(X, dY, nbr, 27)) < 1e-5
+
+
+def test_plain_map_with_one_input_to_two_outputs(device):
+    """A caller's map where an (input, offset) feeds two outputs: the forward is fine; the gather
+    input gradient cannot represent it and says so instead of dropping a term."""
+    from sparsetriton_amd.nn.functional.conv.funcs import ConvPrecomputedNeighborGEMM
+    nbr = torch.full((4, 27), -1, dtype=torch.int32)
+    nbr[0, 3] = nbr[2, 3] = 1  # input 1 feeds outputs 0 and 2 through offset 3
+    nbr[1, 13] = 0
+    feats = torch.randn(2, 8, device=device, requires_grad=True)
+    w = torch.randn(27, 8, 8, device=device, requires_grad=True)
+    out = ConvPrecomputedNeighborGEMM.apply(feats, w, nbr.to(device))
+    ref = O.fwd_f64(feats.detach().cpu().numpy(), w.detach().cpu().numpy(), nbr.numpy())
+    assert rel(out.detach().cpu(), ref) < 1e-5
+    with pytest.raises(ValueError, match="several output rows"):
+        out.sum().backward()
 
 
 # --------------------------------------------- reference test parametrisations

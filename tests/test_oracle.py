@@ -68,6 +68,56 @@ def test_subm_kmap_vs_bruteforce_with_out_of_bounds():
     assert (O.exact_kmap(c, c, off, 1, shape) == O.bf_kmap(c, c, off, 1, shape)).all()
 
 
+@pytest.mark.parametrize("case", ["in_box", "out_of_box", "duplicates"])
+def test_subm_symmetric_gather_is_the_adjoint_only_when_clean(case):
+    """The submanifold input-gradient shortcut -- gather dY through nbr[K-1-k, i] -- equals the
+    scatter adjoint over the forward map (dgrad_f64, the reference's implicit_precomputed_gemm.py
+    :129-177) exactly when every row is unique and inside the shape; otherwise it drops terms.
+    The GEMM path may take it only under that condition."""
+    rng = np.random.default_rng(9)
+    n, S = 1500, 12
+    c = _rand_coords(rng, n, S)
+    shape = (9, 11, 12) if case == "out_of_box" else (S, S, S)
+    if case == "duplicates":
+        c[rng.choice(n, 40, replace=False)] = c[rng.choice(n, 40, replace=False)]
+    off = O.target_offsets(3, 1, 1, False)
+    nbr = O.exact_kmap(c, c, off, 1, shape)
+    X = rng.standard_normal((n, 5))
+    W = rng.standard_normal((27, 5, 6))
+    dY = rng.standard_normal((n, 6))
+    scatter = O.dgrad_f64(dY, W, nbr, n)
+    gather = np.zeros((n, 5))
+    for k in range(27):
+        o = nbr[:, 26 - k]
+        ok = o >= 0
+        gather[ok] += dY[o[ok]] @ W[k].T
+    err = np.abs(gather - scatter).max()
+    if case == "in_box":
+        assert err < 1e-9
+    else:
+        assert err > 1e-3
+    # adjoint identity of the oracle pair itself: <dY, fwd(X)> = <dgrad(dY), X>
+    assert abs((dY * O.fwd_f64(X, W, nbr)).sum() - (scatter * X).sum()) < 1e-8 * n
+
+
+@pytest.mark.parametrize("dup", [False, True])
+def test_blas_gemms_equal_the_loop_oracle(dup):
+    """The per-offset BLAS restatements (benchmark-size checkers) equal the pinned loop
+    versions, including maps with absent entries and an input row repeated within an offset."""
+    rng = np.random.default_rng(12)
+    n_in, n_out, K = 300, 260, 27
+    nbr = rng.integers(-1, n_in, (n_out, K)).astype(np.int32)
+    nbr[rng.random((n_out, K)) < 0.6] = -1
+    if dup:
+        nbr[5, 3] = nbr[9, 3] = 17
+    X = rng.standard_normal((n_in, 6))
+    W = rng.standard_normal((K, 6, 7))
+    dY = rng.standard_normal((n_out, 7))
+    assert np.allclose(O.fwd_f64_blas(X, W, nbr), O.fwd_f64(X, W, nbr), rtol=1e-12, atol=1e-12)
+    assert np.allclose(O.dgrad_f64_blas(dY, W, nbr, n_in), O.dgrad_f64(dY, W, nbr, n_in), rtol=1e-12, atol=1e-12)
+    assert np.allclose(O.wgrad_f64_blas(X, dY, nbr, K), O.wgrad_f64(X, dY, nbr, K), rtol=1e-12, atol=1e-12)
+
+
 def _cases():
     z = np.load(GOLD / "conv_cases.npz")
     names = sorted({k.split("/")[0] for k in z.files})
