@@ -331,6 +331,21 @@ int st_column_sum(const void* Y, int64_t n, int C, int dtype, float* partials, v
                   st_stream_t stream);
 
 /*
+ * No counterpart in the reference.  st_column_sum for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same kernels and result, bit for bit,
+ * with the 1024 * C fp32 partials in a library-owned device array instead of a
+ * caller workspace.  The array holds C <= ST_COLUMN_SUM_NOALLOC_MAX_C columns
+ * (8 MiB per GPU, allocated with the library's code object on each GPU it runs
+ * on and held until the process ends); larger C returns ST_ERR_ARG.  Nothing
+ * here allocates.  `stream` (or the null stream) must belong to the current
+ * device.  All calls on one GPU share its array: calls that overlap on one GPU
+ * (concurrent streams or threads) race and must be serialised by the caller.
+ */
+#define ST_COLUMN_SUM_NOALLOC_MAX_C 2048
+int st_column_sum_noalloc(const void* Y, int64_t n, int C, int dtype, void* out, int out_dtype, st_stream_t stream);
+
+/*
  * Output-stationary gather-GEMM, the forward of ConvPrecomputedNeighborGEMM
  * (precomputed_fwd_kernel, implicit_precomputed_gemm.py:64-126) and, with the
  * transposed map, its input-gradient (precomputed_bwd_feat_kernel :129-177,

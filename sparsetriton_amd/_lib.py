@@ -24,6 +24,7 @@ STATUS_WORDS = 4
 STATUS_OVERFLOW, STATUS_BAD_COORD, STATUS_DUPLICATE, STATUS_OUT_OF_BOX = 0, 1, 2, 3
 
 W_TRANSPOSE, W_REVERSE, W_COPY = 0, 1, 2
+COLUMN_SUM_NOALLOC_MAX_C = 2048
 MAX_KVOL = 512
 TILE_ROWS = 128
 
@@ -91,6 +92,7 @@ _SIGNATURES = {
     "st_weight_prep": [_P, _P, _I, _I, _I, _I, _I, _P],
     "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],
     "st_column_sum": [_P, _L, _I, _I, _P, _P, _I, _P],
+    "st_column_sum_noalloc": [_P, _L, _I, _I, _P, _I, _P],
     "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
     "st_gather_gemm_tiled_epilogue": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _L, _I, _I, _I, _I,
                                       _P],

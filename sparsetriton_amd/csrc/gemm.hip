@@ -1,5 +1,7 @@
 // C entry points of the gather-GEMM and weight-gradient kernels
 // (kernels in gemm_kernels.h, instantiated per dtype in gemm_{f32,f16,bf16}.hip).
+#include <mutex>
+
 #include "gemm_kernels.h"
 
 ST_GEMM_OPS(extern, float)
@@ -200,6 +202,33 @@ static int column_sum(const T* Y, int64_t n, int C, float* partials, void* out, 
 }
 }  // namespace st
 
+// ------------------------------------------------ allocation-free column sum
+//
+// st_column_sum_noalloc keeps the column sum's partials in `scratch`, a
+// library-owned device array (one copy per GPU, alive until the process
+// ends), instead of a caller workspace.  In host code `scratch` names a
+// host-side stand-in, not device memory: the device address comes from
+// hipGetSymbolAddress, taken once per device with that device current, and
+// only that address is ever handed to a kernel.
+static constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) float scratch[st::kColSumBlocks * ST_COLUMN_SUM_NOALLOC_MAX_C];
+static float* g_scratch_dev[kNoAllocMaxDevices] = {};
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the device's first call).
+static int scratch_address(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) return ST_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return ST_ERR_HIP;
+    g_scratch_dev[dev] = (float*)p;
+  }
+  *out = g_scratch_dev[dev];
+  return ST_OK;
+}
+
 static bool lookup_ok(const st_lookup* lk) {
   return lk && lk->K > 0 && lk->K <= ST_MAX_KVOL && lk->mul >= 1 && lk->div >= 1 && (lk->sign == 1 || lk->sign == -1);
 }
@@ -209,6 +238,21 @@ extern "C" {
 int st_column_sum(const void* Y, int64_t n, int C, int dtype, float* partials, void* out, int out_dtype,
                   st_stream_t stream) {
   if (n < 0 || C <= 0 || !partials || !out || (n > 0 && !Y)) return ST_ERR_ARG;
+  ST_DISPATCH_DTYPE(dtype, T, st::column_sum<T>((const T*)Y, n, C, partials, out, out_dtype, stream));
+}
+
+int st_column_sum_noalloc(const void* Y, int64_t n, int C, int dtype, void* out, int out_dtype,
+                          st_stream_t stream) {
+  if (n < 0 || C <= 0 || C > ST_COLUMN_SUM_NOALLOC_MAX_C || !out || (n > 0 && !Y)) return ST_ERR_ARG;
+  if (stream) {  // the stream must run on the current device, whose copy of the array is used
+    int cur = -1, sdev = -1;
+    if (hipGetDevice(&cur) != hipSuccess || hipStreamGetDevice(stream, &sdev) != hipSuccess) return ST_ERR_HIP;
+    if (cur != sdev) return ST_ERR_ARG;
+  }
+  float* partials = nullptr;
+  const int rc = scratch_address(&partials);
+  if (rc != ST_OK) return rc;
+  // every partial row the second pass reads is written by the first: nothing to clear
   ST_DISPATCH_DTYPE(dtype, T, st::column_sum<T>((const T*)Y, n, C, partials, out, out_dtype, stream));
 }
 
