@@ -40,6 +40,7 @@ _SIG = {
     "ref_hash_build": ([_P, _L, _P, _P, _L], _L),
     "ref_hash_query": ([_P, _L, _P, _P, _L, _P], None),
     "ref_kmap": ([_P, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, _P], None),
+    "ref_out_coords": ([_P, _L, _P, _I, _L, _I, _L, _L, _L, _P, _P], _L),
     "ref_fwd_f32": ([_P, _I, _P, _I, _I, _P, _L, _P], None),
     "ref_dgrad_f32": ([_P, _I, _P, _I, _I, _P, _L, _L, _P], None),
     "ref_wgrad_f32": ([_P, _I, _P, _I, _P, _L, _I, _P], None),
@@ -224,6 +225,71 @@ class RefHash:
         return nbr
 
 
+def ref_out_coords(in_coords, offsets, stride, transposed, new_shape):
+    """Output coordinates through the reference's own dedup (kmap.py:213-444, filter_unique_kernel
+    :56-97), lossy 31-bit key2 and 1024-probe cap included, candidates resolved one at a time in
+    order.  Returns (coords, exhausted) -- exhausted counts candidates that ran out of probes."""
+    ic, off = _i32(in_coords), _i32(offsets)
+    n, K = ic.shape[0], off.shape[0]
+    buf = np.empty((max(n * K, 1), 4), dtype=np.int32)
+    ex = ctypes.c_int64()
+    m = lib().ref_out_coords(_p(ic), n, _p(off), K, stride, 1 if transposed else 0, *map(int, new_shape), _p(buf),
+                             ctypes.byref(ex))
+    return buf[:m].copy(), int(ex.value)
+
+
+def _key_rows(c: np.ndarray) -> np.ndarray:
+    c = np.asarray(c, dtype=np.int64)
+    return (c[:, 0] << 48) | ((c[:, 1] & 0xFFFF) << 32) | ((c[:, 2] & 0xFFFF) << 16) | (c[:, 3] & 0xFFFF)
+
+
+def map_ledger(ref_nbr, exact_nbr) -> dict:
+    """Entry-by-entry comparison of a kernel map built by the reference's algorithm with the exact
+    one over the same output rows: missing (exact has a row, reference -1), false (reference has a
+    row where there is none) and wrong (both present, different rows)."""
+    r, e = np.asarray(ref_nbr), np.asarray(exact_nbr)
+    return {"entries": int((e >= 0).sum()), "missing": int(((e >= 0) & (r < 0)).sum()),
+            "false": int(((e < 0) & (r >= 0)).sum()), "wrong": int(((e >= 0) & (r >= 0) & (e != r)).sum())}
+
+
+def ledger(in_coords, shape, kernel_size=3, stride=1, padding=1, transposed=False, submanifold=True) -> dict:
+    """Defect ledger of the reference's lossy hash on one convolution geometry: what its table
+    build drops (128-probe cap, utils/hash.py:240-258), what its dedup loses (output coordinates
+    whose key2 aliases an earlier one, kmap.py:56-97), and how its kernel map
+    (conv.py:12-75 over that table, lossy key2 lookups) differs from the exact map over the
+    reference's own output rows.  Inserts and candidates run one at a time in order (the GPU
+    runs them in lockstep blocks, so which of two colliding keys wins can differ there)."""
+    c = _i32(in_coords)
+    off = target_offsets(kernel_size, 1, padding, transposed)
+    scale = stride if (transposed and stride > 1) else 1
+    table_coords = c.copy()
+    table_coords[:, 1:] *= scale
+    h = RefHash(table_coords)
+    out = {"n_in": int(c.shape[0]), "table_slots": h.T, "insert_dropped": h.dropped}
+    lookup_shape = tuple(int(v) * scale for v in shape)
+    if submanifold and stride == 1:
+        oc = c
+        out["n_out"] = int(c.shape[0])
+    else:
+        ns = out_shape(shape, kernel_size, stride, 1, padding, transposed)
+        oc, exhausted = ref_out_coords(c, off, stride, transposed, ns)
+        exact_oc = out_coords(c, off, stride, transposed, ns)
+        ek, rk = _key_rows(exact_oc), _key_rows(oc)
+        out.update({"n_out": int(exact_oc.shape[0]), "ref_n_out": int(oc.shape[0]),
+                    "outputs_lost": int(np.setdiff1d(ek, rk).shape[0]),
+                    "outputs_spurious": int(np.setdiff1d(rk, ek).shape[0]),
+                    "dedup_probe_exhausted": exhausted,
+                    "same_order_as_first_occurrence": bool(oc.shape == exact_oc.shape and (oc == exact_oc).all())})
+    map_stride = 1 if transposed else stride
+    ref_nbr = h.kmap(oc, off, map_stride, lookup_shape)
+    if transposed:
+        exact = exact_kmap(c, oc, off, 1, lookup_shape, in_scale=scale)
+    else:
+        exact = exact_kmap(c, oc, off, map_stride, shape)
+    out.update(map_ledger(ref_nbr, exact))
+    return out
+
+
 def ref_fwd_f32(X, W, nbr):
     X, W, nbr = _f32(X), _f32(W), _i32(nbr)
     K, Cin, Cout = W.shape
@@ -405,6 +471,39 @@ def batch_norm_grads_f64(feats, batch_idx, B, weight, bias, running_mean, runnin
         out = torch.relu(out)
     out.backward(torch.as_tensor(np.asarray(dout, dtype=np.float64)))
     return (x.grad.numpy(), w.grad.numpy(), b.grad.numpy(), None if res is None else res.grad.numpy())
+
+
+def conv_f64_torch(x, w, b, nbr):
+    """fwd_f64 (+ bias) as a differentiable float64 torch expression: out = sum_k x[nbr[:, k]] @ w[k]
+    (+ b), x (n_in, C_in), w (K, C_in, C_out) torch float64; its autograd is the reference's
+    input / weight gradient (implicit_precomputed_gemm.py:129-230) by construction."""
+    import torch
+
+    nb = torch.as_tensor(np.asarray(nbr, dtype=np.int64))
+    out = torch.zeros((nb.shape[0], w.shape[2]), dtype=torch.float64)
+    for k in range(w.shape[0]):
+        o = (nb[:, k] >= 0).nonzero().flatten()
+        if o.numel():
+            out = out.index_add(0, o, x[nb[o, k]] @ w[k])
+    return out if b is None else out + b
+
+
+def batch_norm_f64_torch(x, batch_idx, B, w, b, residual=None, relu=False, eps=1e-5):
+    """batch_norm_f64 (training statistics) as a differentiable float64 torch expression, by the
+    library routine F.batch_norm sample by sample (nn/functional/norm.py:66-112, blocks.py:121-124)."""
+    import torch
+    import torch.nn.functional as F
+
+    bi = torch.as_tensor(np.asarray(batch_idx, dtype=np.int64))
+    xh = torch.zeros_like(x)
+    for s in range(B):
+        rows = (bi == s).nonzero().flatten()
+        if rows.numel():
+            xh = xh.index_copy(0, rows, F.batch_norm(x[rows], None, None, training=True, eps=eps))
+    out = xh * w + b
+    if residual is not None:
+        out = out + residual
+    return torch.relu(out) if relu else out
 
 
 # ------------------------------------------------------------ pooling, upsampling

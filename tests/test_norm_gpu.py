@@ -282,6 +282,122 @@ def test_block_fused_matches_oracle_and_unfused(device, kind):
     assert rel(f.grad.cpu(), f2.grad.cpu()) < 1e-4
 
 
+def _f64_params(module):
+    """float64 CPU leaf copies of a module's parameters, keyed by the parameter's id."""
+    return {id(p): torch.tensor(p.detach().double().cpu().numpy(), requires_grad=True) for p in module.parameters()}
+
+
+def _conv_torch(conv, P, coords, x_t, shape):
+    k, s, d = conv.kernel_size[0], conv.stride[0], conv.dilation[0]
+    p = ((k - 1) * d) // 2
+    off = O.target_offsets(k, d, p, False)
+    if s == 1:
+        oc, new_shape = coords, shape
+    else:
+        new_shape = O.out_shape(shape, k, s, d, p, False)
+        oc = O.out_coords(coords, off, s, False, new_shape)
+    nbr = O.exact_kmap(coords, oc, off, s, shape)
+    b = None if conv.bias is None else P[id(conv.bias)]
+    return oc, O.conv_f64_torch(x_t, P[id(conv.weight)], b, nbr), tuple(int(v) for v in new_shape)
+
+
+def _block_torch(block, P, coords, x_t, shape, B):
+    """The block as a float64 autograd expression of the oracle's convolution and batch norm."""
+    if isinstance(block, SparseConvBlock):
+        oc, y, ns = _conv_torch(block[0], P, coords, x_t, shape)
+        bn = block[1]
+        return oc, O.batch_norm_f64_torch(y, oc[:, 0], B, P[id(bn.weight)], P[id(bn.bias)], relu=True), ns
+    m = block.main
+    oc, h, ns = _conv_torch(m[0], P, coords, x_t, shape)
+    h = O.batch_norm_f64_torch(h, oc[:, 0], B, P[id(m[1].weight)], P[id(m[1].bias)], relu=True)
+    _, h, _ = _conv_torch(m[3], P, oc, h, ns)
+    return oc, O.batch_norm_f64_torch(h, oc[:, 0], B, P[id(m[4].weight)], P[id(m[4].bias)], residual=x_t,
+                                      relu=True), ns
+
+
+@pytest.mark.parametrize("kind", ["conv", "res"])
+def test_block_backward_vs_f64_autograd(device, kind):
+    """Training block (fused batch norm / residual / ReLU kernels): input and every parameter's
+    gradient against autograd of the float64 oracle composition.  The tolerance (5e-3) leaves room
+    for a ReLU decision that rounding flips at the kink."""
+    rng = np.random.default_rng(41 if kind == "conv" else 42)
+    torch.manual_seed(0)
+    coords, shape = _rand_set(rng)
+    C = 16
+    x = rng.standard_normal((coords.shape[0], C))
+    block = (SparseConvBlock(C, 32, 3, stride=2) if kind == "conv" else SparseResBlock(C, C, 3)).to(device)
+    _randomise_bn(block, rng)
+    sp, f = _sp(device, coords, x, torch.float32, 2, shape=shape)
+    out = block(sp)
+    dout = rng.standard_normal(tuple(out.F.shape))
+    out.F.backward(torch.as_tensor(dout, device=device, dtype=torch.float32))
+    P = _f64_params(block)
+    x_t = torch.tensor(x, requires_grad=True)
+    oc, ref, _ = _block_torch(block, P, coords, x_t, shape, 2)
+    assert np.array_equal(out.C.cpu().numpy(), oc)
+    ref.backward(torch.as_tensor(dout))
+    assert rel(f.grad, x_t.grad) < 5e-3
+    _check_param_grads(block, P, 5e-3)
+
+
+def _check_param_grads(module, P, tol):
+    """Each parameter's gradient within tol of the float64 one, relative to its own norm -- or, for
+    a gradient that is zero in exact arithmetic (a convolution bias feeding a training-mode batch
+    norm, which removes it), to the largest parameter gradient of the module."""
+    ref = {name: _np(P[id(prm)].grad) for name, prm in module.named_parameters()}
+    scale = max(np.linalg.norm(g) for g in ref.values())
+    errs = {}
+    for name, prm in module.named_parameters():
+        denom = max(np.linalg.norm(ref[name]), 1e-3 * scale)
+        errs[name] = float(np.linalg.norm(_np(prm.grad) - ref[name]) / denom)
+    worst = max(errs.items(), key=lambda kv: kv[1])
+    assert worst[1] < tol, worst
+    return errs
+
+
+@pytest.mark.parametrize("precision,stages,tol", [("ieee", 5, 1e-4), ("bf16x3", 2, 1e-3)])
+def test_resnet21d_backward_vs_f64_autograd(device, precision, stages, tol):
+    """SparseResNet21D training step (fp32): input and all 84 parameter gradients (21 convolutions,
+    21 batch norms) against autograd of the float64 oracle composition, stage by stage, with a loss
+    over the first `stages` stages' outputs.
+
+    The last stages of this small set hold 128 and 16 voxels, and batch norm over so few rows makes
+    the gradient ill-conditioned: a relative perturbation of 4.4e-6 on every convolution output of
+    the float64 composition itself moves the input gradient by 1.3 % (ReLU decisions flip).  IEEE
+    fp32 convolutions (~1e-7) stay clear of that and are checked through all five stages; the
+    split-bf16 mode (~4e-6 per convolution, pinned per layer elsewhere) through the first two."""
+    from sparsetriton_amd.config import set_fp32_precision
+
+    set_fp32_precision(precision)
+    rng = np.random.default_rng(33)
+    torch.manual_seed(2)
+    coords, shape = _rand_set(rng, B=2, S=32, n=3000)
+    x = rng.standard_normal((coords.shape[0], 4))
+    model = SparseResNet21D(in_channels=4).to(device)
+    _randomise_bn(model, rng)
+    sp, f = _sp(device, coords, x, torch.float32, 2, shape=shape)
+    outs = model(sp)
+    sum(o.F.square().mean() for o in outs[:stages]).backward()
+    P = _f64_params(model)
+    x_t = torch.tensor(x, requires_grad=True)
+    c, h, s = coords, x_t, shape
+    ref_outs = []
+    for stage in model:
+        for block in stage:
+            c, h, s = _block_torch(block, P, c, h, s, 2)
+        ref_outs.append(h)
+    sum(o.square().mean() for o in ref_outs[:stages]).backward()
+    for got, want in zip(outs, ref_outs):
+        assert rel(got.F.detach(), want.detach()) < tol
+    assert rel(f.grad, x_t.grad) < tol
+    for prm in model.parameters():  # parameters past the loss's last stage get no gradient
+        if P[id(prm)].grad is None:
+            assert prm.grad is None or not prm.grad.any()
+            P[id(prm)].grad = torch.zeros_like(P[id(prm)])
+            prm.grad = torch.zeros_like(prm)
+    assert len(_check_param_grads(model, P, tol)) == 84
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_resnet21d_forward_backward(device, dtype):
     rng = np.random.default_rng(31)

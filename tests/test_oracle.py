@@ -9,7 +9,12 @@ What pins each oracle function:
   RefHash         the reference tests' known answers (tests/test_utils_hash.py:95-123)
                   and the closed-form key2 alias of (0,0,0,0) / (1,10,0,29)
   pool            torch max_pool3d / avg_pool3d of dense grids (empty cells -inf / uncounted)
-                  where the cell rule is standard pooling (odd kernel, padding k // 2)
+                  where the cell rule is standard pooling (odd kernel, padding k // 2); the
+                  cell rule for any kernel / padding by a search over cells
+  pool_grad       torch autograd through the same dense max_pool3d / avg_pool3d
+  ledger port     ref_out_coords equals the exact build where nothing aliases; every map
+                  difference is traced to a key2 alias or a lost row (tests/test_ledger.py)
+  *_f64_blas      equality with the loop versions (fwd/dgrad/wgrad_f64)
   upsample        the reference's own known answer (tests/test_pooling.py:14-40)
   batch_norm      torch.nn.functional.batch_norm applied sample by sample (outputs), the
                   unbiased/biased relation to torch's running variance (running statistics),
@@ -334,6 +339,84 @@ def test_pool_matches_dense_library_pooling(s, mode):
     assert int((cnt > 0).sum()) == oc.shape[0]
     assert (np.lexsort(oc.T[::-1]) == np.arange(oc.shape[0])).all()
     assert (oc[inv] == np.concatenate([c[:, :1], c[:, 1:] // s], 1)).all()
+
+
+@pytest.mark.parametrize("s", [2, 3])
+@pytest.mark.parametrize("mode", ["max", "avg"])
+def test_pool_grad_matches_dense_library_autograd(s, mode):
+    """pool_grad_f64 (the reference's backward rule, spatial.py:139-209) equals torch autograd
+    through dense max_pool3d / avg_pool3d of the occupancy grid (random floats: no ties)."""
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(s * 7 + len(mode))
+    S, C = 12, 3
+    c = _rand_coords(rng, 300, S)
+    f = rng.standard_normal((c.shape[0], C))
+    oc, out, inv = O.pool_f64(c, f, 3, 1, s, mode)
+    dout = rng.standard_normal(out.shape)
+    B = int(c[:, 0].max()) + 1
+    ct = torch.as_tensor(c, dtype=torch.long)
+    vals = torch.as_tensor(f).requires_grad_(True)
+    base = torch.full((B, C, S, S, S), -np.inf if mode == "max" else 0.0, dtype=torch.float64)
+    dense = base.clone()
+    dense[ct[:, 0], :, ct[:, 1], ct[:, 2], ct[:, 3]] = vals
+    occ = torch.zeros((B, 1, S, S, S), dtype=torch.float64)
+    occ[ct[:, 0], 0, ct[:, 1], ct[:, 2], ct[:, 3]] = 1.0
+    if mode == "max":
+        pooled = F.max_pool3d(dense, s, s, ceil_mode=True)
+    else:
+        pooled = F.avg_pool3d(dense, s, s, ceil_mode=True) / F.avg_pool3d(occ, s, s, ceil_mode=True).clamp_min(1e-30)
+    o = torch.as_tensor(oc, dtype=torch.long)
+    sel = pooled[o[:, 0], :, o[:, 1], o[:, 2], o[:, 3]]
+    (sel * torch.as_tensor(dout)).sum().backward()
+    assert np.abs(O.pool_grad_f64(f, out, inv, dout, mode) - vals.grad.numpy()).max() < 1e-12
+
+
+@pytest.mark.parametrize("k,p,s", [(2, 0, 2), (2, 1, 2), (4, 1, 2), (4, 2, 3), (3, 0, 2), (3, 2, 2), (1, 0, 1)])
+def test_pool_cell_rule_by_search(k, p, s):
+    """Cells for even kernels and any padding (negative cells included) equal a search for the
+    one cell o with o * s <= x + p - k // 2 < (o + 1) * s (spatial.py:118-119), so a truncating
+    division or a dropped term cannot pass."""
+    rng = np.random.default_rng(k * 100 + p * 10 + s)
+    c = _rand_coords(rng, 200, 9)
+    oc, _, inv = O.pool_f64(c, rng.standard_normal((c.shape[0], 1)), k, p, s, "avg")
+    for r in range(c.shape[0]):
+        want = [c[r, 0]]
+        for a in range(1, 4):
+            v = int(c[r, a]) + p - k // 2
+            o = next(o for o in range(-10, 20) if o * s <= v < (o + 1) * s)
+            want.append(o)
+        assert list(oc[inv[r]]) == want
+    if k // 2 > p:
+        assert (oc[:, 1:] < 0).any()  # the rule sends coordinate 0 to a negative cell here
+
+
+def test_torch_f64_compositions_equal_the_numpy_oracle():
+    """conv_f64_torch / batch_norm_f64_torch (the differentiable block / backbone checkers) equal
+    fwd_f64 and batch_norm_f64, and their autograd equals dgrad_f64 / wgrad_f64 /
+    batch_norm_grads_f64."""
+    rng = np.random.default_rng(17)
+    c = _rand_coords(rng, 200, 8)
+    nbr = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, (8, 8, 8))
+    X, W, dY = rng.standard_normal((200, 4)), rng.standard_normal((27, 4, 5)), rng.standard_normal((200, 5))
+    x = torch.tensor(X, requires_grad=True)
+    w = torch.tensor(W, requires_grad=True)
+    y = O.conv_f64_torch(x, w, None, nbr)
+    y.backward(torch.as_tensor(dY))
+    assert np.abs(y.detach().numpy() - O.fwd_f64(X, W, nbr)).max() < 1e-12
+    assert np.abs(x.grad.numpy() - O.dgrad_f64(dY, W, nbr, 200)).max() < 1e-12
+    assert np.abs(w.grad.numpy() - O.wgrad_f64(X, dY, nbr, 27)).max() < 1e-12
+    bi = c[:, 0]
+    g, bb, res = rng.uniform(0.5, 1.5, 5), rng.standard_normal(5), rng.standard_normal((200, 5))
+    yt = torch.tensor(O.fwd_f64(X, W, nbr), requires_grad=True)
+    z = O.batch_norm_f64_torch(yt, bi, 2, torch.as_tensor(g), torch.as_tensor(bb), torch.as_tensor(res), relu=True)
+    ref, _, _ = O.batch_norm_f64(yt.detach().numpy(), bi, 2, g, bb, np.zeros(5), np.ones(5), True, residual=res,
+                                 relu=True)
+    assert np.abs(z.detach().numpy() - ref).max() < 1e-12
+    z.backward(torch.as_tensor(dY))
+    gx = O.batch_norm_grads_f64(yt.detach().numpy(), bi, 2, g, bb, np.zeros(5), np.ones(5), True, dY, residual=res,
+                                relu=True)[0]
+    assert np.abs(yt.grad.numpy() - gx).max() < 1e-12
 
 
 def test_upsample_reference_kat():
