@@ -10,8 +10,8 @@ A step = one forward + backward (input and weight gradient) of the layer
 through the public API (``sparse_conv3d`` + autograd), with the kernel map
 already cached on the tensor -- as in a stack of submanifold layers, where it
 is built once per coordinate set.  The kernel-map build (hash insert +
-neighbour query + transposed map + mask-sorted tile plans + pair list) is
-timed separately and reported as ``kmap_build_ms``.
+neighbour query in one cooperative launch + mask-sorted tile plan + pair list) is timed
+separately and reported as ``kmap_build_ms``.
 
 value = effective TFLOP/s = 6 * P * C_in * C_out / step time, P = exact number
 of (input, output, offset) pairs.  ``roofline`` covers the dominant kernel,
@@ -97,10 +97,8 @@ def _stats(t):
     return {"median": float(np.median(t)), "p10": float(np.percentile(t, 10)), "p90": float(np.percentile(t, 90))}
 
 
-def cpu_baseline(coords, shape, X, W, dY):
-    from oracle import oracle as O
-
-    threads = O.num_threads()
+def _port_pass(O, coords, shape, X, W, dY):
+    """One pass of the reference-algorithm port: its hash + map build, fwd, dgrad, wgrad (seconds)."""
     off = O.target_offsets(3, 1, 1, False)
     t0 = time.perf_counter()
     h = O.RefHash(coords)
@@ -110,23 +108,114 @@ def cpu_baseline(coords, shape, X, W, dY):
     t2 = time.perf_counter()
     O.ref_dgrad_f32(dY, W, nbr, coords.shape[0])
     t3 = time.perf_counter()
-    O.ref_wgrad_f32(X, dY, nbr, 27)
+    O.ref_wgrad_f32(X, dY, nbr, W.shape[0])
     t4 = time.perf_counter()
-    P_ref = int((nbr >= 0).sum())
-    gemm_s = t4 - t1
+    return (t1 - t0, t2 - t1, t3 - t2, t4 - t3), int((nbr >= 0).sum()), h.dropped
+
+
+def _port_timed(O, threads, coords, shape, X, W, dY, warmup, iters, budget_s=None):
+    """Median / p10 / p90 (ms) of each stage over `iters` timed passes after `warmup`, on `threads`
+    OpenMP threads (stops early once `budget_s` seconds of timed passes are spent)."""
+    O.set_threads(threads)
+    for _ in range(warmup):
+        _port_pass(O, coords, shape, X, W, dY)
+    rows, P, dropped = [], 0, 0
+    t_start = time.perf_counter()
+    for _ in range(iters):
+        t, P, dropped = _port_pass(O, coords, shape, X, W, dY)
+        rows.append(t)
+        if budget_s is not None and time.perf_counter() - t_start > budget_s:
+            break
+    a = np.array(rows) * 1e3
+    gemm = a[:, 1] + a[:, 2] + a[:, 3]
+    flops = 6.0 * P * X.shape[1] * W.shape[2]
+    gflops = flops / (gemm * 1e-3) / 1e9
+    return {"threads": threads, "iters": len(rows), "warmup": warmup, "pairs": P, "inserts_dropped": dropped,
+            "kmap_build_ms": _stats(a[:, 0]), "fwd_ms": _stats(a[:, 1]), "dgrad_ms": _stats(a[:, 2]),
+            "wgrad_ms": _stats(a[:, 3]), "fwd_bwd_GFLOPs": _stats(gflops)}
+
+
+def config1_inputs(seed=0):
+    """SubMConv3D 16->32 on 4096 uniform voxels in 2 x 64^3, X ~ N(0,1), dY ~ N(0,1),
+    W ~ U(+-1/sqrt(16*27))."""
+    from sparsetriton_amd import workloads
+
+    coords, shape = workloads.config1(seed=seed)
+    rng = np.random.default_rng(seed + 1)
+    X = rng.standard_normal((coords.shape[0], 16)).astype(np.float32)
+    bound = 1.0 / np.sqrt(16 * 27)
+    W = rng.uniform(-bound, bound, (27, 16, 32)).astype(np.float32)
+    dY = rng.standard_normal((coords.shape[0], 32)).astype(np.float32)
+    return coords, shape, X, W, dY
+
+
+def cpu_baseline(coords, shape, X, W, dY, profile=False):
+    """The reference algorithm's CPU port (oracle/st_oracle.c ref_*: 31-bit key2 table with the
+    128-probe cap, output-major map, output-stationary forward, scatter input gradient, per-offset
+    weight gradient; fp32, OpenMP), as planned for the CPU baseline: config 1 with >= 10 warmup and
+    >= 50 timed passes on all host threads and on one, and beside it a bounded sample of the
+    benchmark workload itself (config 2) on all host threads -- its figure is `value`."""
+    from oracle import oracle as O
+
+    all_threads = O.num_threads()
+    c1 = config1_inputs()
+    iters1 = 5 if profile else 50
+    cfg1 = {"all": _port_timed(O, all_threads, *c1, warmup=2 if profile else 10, iters=iters1),
+            "one": _port_timed(O, 1, *c1, warmup=2 if profile else 10, iters=iters1)}
+    cfg2 = _port_timed(O, all_threads, coords, shape, X, W, dY, warmup=1, iters=1 if profile else 20,
+                       budget_s=20.0)
+    O.set_threads(all_threads)
+    P = cfg2["pairs"]
+    gemm_ms = cfg2["fwd_ms"]["median"] + cfg2["dgrad_ms"]["median"] + cfg2["wgrad_ms"]["median"]
     return {
-        "value": 6.0 * P_ref * X.shape[1] * W.shape[2] / gemm_s / 1e12,
+        "value": 6.0 * P * X.shape[1] * W.shape[2] / (gemm_ms * 1e-3) / 1e12,
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": all_threads,
         "kind": "port",
-        "sample": (f"full config-2 voxel set (N={coords.shape[0]}), one fwd+dgrad+wgrad pass in fp32 over the "
-                   f"reference-hash kernel map ({P_ref} pairs, {h.dropped} inserts dropped by the 128-probe cap)"),
-        "kmap_build_ms": (t1 - t0) * 1e3,
-        "fwd_ms": (t2 - t1) * 1e3,
-        "dgrad_ms": (t3 - t2) * 1e3,
-        "wgrad_ms": (t4 - t3) * 1e3,
-        "pairs": P_ref,
+        "sample": (f"config-2 voxel set (N={coords.shape[0]}), fwd+dgrad+wgrad in fp32 over the reference-hash "
+                   f"kernel map ({P} pairs, {cfg2['inserts_dropped']} inserts dropped by the 128-probe cap); "
+                   f"median of {cfg2['iters']} passes after 1 warmup on {all_threads} OpenMP threads"),
+        "os_cpu_count": os.cpu_count(),
+        "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+        "config2": cfg2,
+        "config1": cfg1,
     }
+
+
+def gpu_config1(torch, reps):
+    """BASELINE config 1 on the GPU in the same run as the CPU baseline: the layer's kernel-map build
+    (new coordinate set + forward) and its fwd+bwd step with the map cached, fp32."""
+    from sparsetriton_amd import SparseTensor
+    from sparsetriton_amd.nn.functional import sparse_conv3d
+
+    coords, shape, X, W, dY = config1_inputs()
+    dev = torch.device("cuda:0")
+    c = torch.as_tensor(coords, device=dev).to(torch.int16)
+    x = torch.as_tensor(X, device=dev)
+    w = torch.as_tensor(W, device=dev).requires_grad_(True)
+    g = torch.as_tensor(dY, device=dev)
+
+    def first():
+        sp = SparseTensor(x.clone().requires_grad_(True), c, spatial_shape=shape, batch_size=2)
+        return sp, sparse_conv3d(sp, w, 3)
+
+    sp, out = first()
+    feats = sp.F
+
+    def step():
+        feats.grad = None
+        w.grad = None
+        sparse_conv3d(sp, w, 3).F.backward(g)
+
+    for _ in range(10):
+        step()
+    first_t = _events(torch, lambda: first(), reps)
+    step_t = _events(torch, step, reps)
+    km = sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)][1]
+    P = km.num_pairs()
+    return {"workload": "config1: SubMConv3D 16->32 k3, B=2, 64^3, 4096 uniform voxels, fp32", "pairs": P,
+            "first_call_build_plus_fwd_ms": _stats(first_t), "fwd_bwd_step_ms": _stats(step_t),
+            "fwd_bwd_GFLOPs": 6.0 * P * 16 * 32 / (np.median(step_t) * 1e-3) / 1e9}
 
 
 EXTRA = {
@@ -386,7 +475,7 @@ def main():
         weight_prep,
         wgrad,
     )
-    from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets, query_kernel_map
+    from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets, subm_kernel_map
     from sparsetriton_amd.utils.hash import HashTable
 
     from sparsetriton_amd.config import set_fp32_precision
@@ -410,38 +499,36 @@ def main():
 
     # ------------------------------------------------ kernel-map build timing
     def build_kmap():
-        # what sparse_conv3d does for a new coordinate set: table (its hash part deferred,
-        # a submanifold map needs only the bitmap's rank index), neighbour query, plans
-        t = HashTable(table_capacity(N), device=dev)
-        t.insert(coords)
-        t.build_occupancy(coords, 4, shape)
-        km = query_kernel_map(t, coords, offsets, shape, 1, N, symmetric=True)
-        km.prepare()  # mask-sorted tile plan, pair list and chunk order
-        return t, km
+        # what sparse_conv3d does for a new coordinate set: the brick index and the neighbour query
+        # in one launch, then the plans (mask-sorted tile plan; pair list and chunk order on a side
+        # stream)
+        km, _ = subm_kernel_map(coords, 4, shape, offsets, symmetric=True)
+        km.prepare()
+        return km
 
     for _ in range(3):
         build_kmap()
     torch.cuda.synchronize()
     R = 3 if args.profile else 20
     kmap_t = _events(torch, build_kmap, R)
-    table, kmap = build_kmap()
-    table.check()
+    kmap = build_kmap()
+    kmap.symmetric  # resolves the duplicate / out-of-box check
     P = kmap.num_pairs()
     log(f"pairs P={P} (P/N={P / N:.2f}); kmap build median {np.median(kmap_t):.3f} ms")
 
     # per-stage kernel timings of the map build
+    table = HashTable(table_capacity(N), device=dev)
+
     def t_insert():  # the hash table itself (strided / transposed / hash-fly paths use it)
         table.clear()
         table.insert(coords)
         table.table_keys  # runs the deferred clear + insert
 
-    def t_index():  # occupancy bitmap + rank index
-        table.build_occupancy(coords, 4, shape)
-
     ins_t = _events(torch, t_insert, R)
-    idx_t = _events(torch, t_index, R)
-    q_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N), R)
-    prep_t = _events(torch, lambda: query_kernel_map(table, coords, offsets, shape, 1, N, symmetric=True).prepare(), R) - np.median(q_t)
+    table.check()
+    q_t = _events(torch, lambda: subm_kernel_map(coords, 4, shape, offsets, symmetric=False), R)
+    prep_t = _events(torch, lambda: subm_kernel_map(coords, 4, shape, offsets, symmetric=True)[0].prepare(),
+                     R) - np.median(q_t)
 
     # --------------------------------------------------------- train step
     X = torch.as_tensor(X_np, device=dev).to(dtype)
@@ -449,7 +536,6 @@ def main():
     w = torch.as_tensor(W_np, device=dev).to(dtype).requires_grad_(True)
     feats = X.clone().requires_grad_(True)
     sp = SparseTensor(feats, coords, spatial_shape=shape, batch_size=4)
-    sp._cache.hashtable = table
     sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)] = (sp.C, kmap, sp.spatial_shape)
 
     def step():
@@ -513,14 +599,18 @@ def main():
                     "frac": tflops / mfma_peak, **common}
     T = table.capacity
     ins_bytes = 8 * N + 12 * T + 12 * N  # int16 coords read + table clear + one slot written per insert
-    # query through the rank index: int16 coords read, the (K, N) map and (N, 1) row masks written,
-    # and per found neighbour its rank prefix and row id read
-    q_bytes = 8 * N + 4 * 27 * N + 4 * N + 8 * P
+    # submanifold map (brick index + query, one launch), by the fixed formula 16 N + 12 Q + 4 N K:
+    # coordinates read, one 12-byte slot-equivalent read per in-bound query, the (K, N) map written
+    off_np = offsets.cpu().numpy()
+    Q = int(sum(((coords_np[:, 1:] - o >= 0) & (coords_np[:, 1:] - o < np.array(shape))).all(axis=1).sum()
+                for o in off_np))
+    q_bytes = 16 * N + 12 * Q + 4 * 27 * N
     kmap_info = {
         "kmap_build_ms": _stats(kmap_t),
         "hash_insert_ms": float(np.median(ins_t)), "hash_insert_GBps": ins_bytes / (np.median(ins_t) * 1e-3) / 1e9,
-        "occupancy_rank_index_ms": float(np.median(idx_t)),
-        "kmap_query_ms": float(np.median(q_t)), "kmap_query_GBps": q_bytes / (np.median(q_t) * 1e-3) / 1e9,
+        "subm_index_and_query_ms": float(np.median(q_t)),
+        "subm_index_and_query_GBps": q_bytes / (np.median(q_t) * 1e-3) / 1e9,
+        "in_bound_queries": Q,
         "plans_ms": float(np.median(prep_t)),
     }
     log(f"kernels (avg ms): {kern}; roofline {dom}: {roofline['achieved']:.1f} {roofline['unit']} = "
@@ -535,13 +625,19 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    cfg1_gpu = gpu_config1(torch, 5 if args.profile else 50)
+    log(f"config 1 on the GPU: step {cfg1_gpu['fwd_bwd_step_ms']['median']:.3f} ms, "
+        f"first call {cfg1_gpu['first_call_build_plus_fwd_ms']['median']:.3f} ms")
     cpu = None
     if not args.no_cpu:
         W_use = torch.as_tensor(W_np).to(dtype).float().numpy()
         X_use = X.float().cpu().numpy()
         dY_use = dY.float().cpu().numpy()
-        cpu = cpu_baseline(coords_np, shape, X_use, W_use, dY_use)
-        log(f"cpu baseline: {cpu['value'] * 1e3:.2f} GFLOP/s on {cpu['cores']} threads")
+        cpu = cpu_baseline(coords_np, shape, X_use, W_use, dY_use, profile=args.profile)
+        c1 = cpu["config1"]
+        log(f"cpu baseline: config 2 {cpu['value'] * 1e3:.2f} GFLOP/s on {cpu['cores']} threads; config 1 "
+            f"{c1['all']['fwd_bwd_GFLOPs']['median']:.2f} GFLOP/s ({c1['all']['threads']} threads), "
+            f"{c1['one']['fwd_bwd_GFLOPs']['median']:.2f} GFLOP/s (1 thread)")
 
     line = {
         "metric": METRIC,
@@ -564,6 +660,7 @@ def main():
         "kernels_avg_ms": kern,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "gpu_config1": cfg1_gpu,
     }
     print(json.dumps(line), flush=True)
 

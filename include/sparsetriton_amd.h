@@ -103,52 +103,6 @@ int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale
 int st_hash_query(const void* coords, int coord_dtype, int64_t m, const uint64_t* keys, const uint32_t* vals,
                   int64_t capacity, int32_t* out, st_stream_t stream);
 
-/*
- * Occupancy bitmap of a coordinate set (no reference counterpart; the
- * reference probes its table for every neighbour).  One bit per voxel of the
- * box [0, batches) x [0, shape[0]) x [0, shape[1]) x [0, shape[2]), stored in
- * 4x4x4 bricks of one u64 word each: voxel (b, x, y, z) is bit
- * (x%4)*16 + (y%4)*4 + z%4 of word ((b*BX + x/4)*BY + y/4)*BZ + z/4, where
- * BX = ceil(shape[0]/4) and likewise BY, BZ.  A kernel-map query tests the
- * bit before probing, so an absent neighbour -- most of the 27 on a surface
- * -- costs one cached word load instead of a hash probe.  A query outside the
- * box is probed as usual, so the bitmap never changes a result.
- */
-typedef struct st_occupancy {
-  const uint64_t* words; /* st_occupancy_words() words written by st_occupancy_build */
-  int64_t batches;
-  int64_t shape[3];
-  int64_t scale;         /* table keys are coords * scale: a query off that lattice is absent */
-  const int32_t* prefix; /* optional rank index (st_occupancy_rank): set bits before word w */
-  const int32_t* rowmap; /* optional: row of the voxel of each rank                          */
-} st_occupancy;
-
-/* Number of u64 words of the bitmap of a (batches, sx, sy, sz) box. */
-int st_occupancy_words(int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* words);
-
-/* Clears `words` and sets the bit of every coordinate row inside the box
- * (rows outside it are left to the table).  words: st_occupancy_words() u64s.
- * status (optional, ST_STATUS_WORDS int32): rows that do not pack into a key
- * add to ST_STATUS_BAD_COORD, rows repeating an earlier row's coordinate to
- * ST_STATUS_DUPLICATE (a submanifold map over repeated coordinates is not its
- * own transpose). */
-int st_occupancy_build(const void* coords, int coord_dtype, int64_t n, uint64_t* words, int64_t batches, int64_t sx,
-                       int64_t sy, int64_t sz, int32_t* status, st_stream_t stream);
-
-/*
- * Rank index of a built bitmap (no reference counterpart): the voxels of the
- * box are ranked in word / bit order; prefix[w] (nw + 1 int32) = set bits in
- * words[0..w), rowmap[rank] (n int32) = row of that voxel (the lowest row for
- * duplicate coordinates).  With occ->prefix / occ->rowmap set, st_kmap_query
- * resolves every in-box neighbour as
- *   rank = prefix[w] + popcount(words[w] & bits below b);  row = rowmap[rank]
- * -- reads that follow the spatial order of the bitmap -- instead of probing
- * the hash table.  occ->words must be built; workspace: (nw + 4095) / 4096 + 1
- * int32.  Rows outside the box are not indexed (no in-bounds query reaches them).
- */
-int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_occupancy* occ, int32_t* prefix,
-                      int32_t* rowmap, int32_t* workspace, st_stream_t stream);
-
 /* ------------------------------------------------------------ kernel maps */
 
 /*
@@ -158,10 +112,6 @@ int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_o
  *   nbr[k * nbr_k_stride + o * nbr_r_stride] = row of q in the table if
  *       0 <= q < shape (per axis) and present, else -1.
  * row_masks (n_out, ceil(K/32)) u32, optional: bit k set iff nbr[o, k] >= 0.
- * occ, optional: the occupancy bitmap of the table's coordinates (a filter
- * only), with its rank index the source of every in-box hit.  keys / vals may
- * be NULL when occ carries a rank index: queries outside the bitmap's box are
- * then absent (a submanifold query of in-range coordinates never leaves it).
  * The package stores maps offset-major, (K, n_out) (nbr_k_stride = n_out,
  * nbr_r_stride = 1): every kernel that walks rows then reads and writes each
  * offset's column with coalesced accesses.
@@ -173,9 +123,32 @@ int st_occupancy_rank(const void* coords, int coord_dtype, int64_t n, const st_o
  */
 int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets, int K,
                   int64_t stride, int64_t shape_x, int64_t shape_y, int64_t shape_z, const uint64_t* keys,
-                  const uint32_t* vals, int64_t capacity, const st_occupancy* occ, int32_t* nbr,
-                  int64_t nbr_k_stride, int64_t nbr_r_stride, uint32_t* row_masks, int32_t* status,
-                  st_stream_t stream);
+                  const uint32_t* vals, int64_t capacity, int32_t* nbr, int64_t nbr_k_stride, int64_t nbr_r_stride,
+                  uint32_t* row_masks, int32_t* status, st_stream_t stream);
+
+/*
+ * Replaces compute_neighbor_indices (conv.py:12-75) with its hash table
+ * (HashTable.insert + query, utils/hash.py:193-366) for the submanifold case
+ * -- out_coords == in_coords, stride 1 -- with no hash table: seven short
+ * kernels build a brick index of the coords over the box [0, batches) x
+ * [0, shape) in `workspace` (st_kmap_subm_workspace bytes; 4x4x4-voxel
+ * bricks, a bit per occupied brick and a bit per voxel of each occupied brick,
+ * with rank prefixes and a rank -> lowest-row map; a few MB, so lookups stay
+ * in L2) and then write, for every row o and offset k,
+ *   nbr[k * n + o] = row of coords[o].xyz - offsets[k] if it lies in
+ *                    [0, shape) and is present (lowest row of repeats), else -1,
+ * and row_masks (n, ceil(K/32)) u32 (optional).  The same map as
+ * st_kmap_query over a table of coords, bit for bit.  status (optional,
+ * ST_STATUS_WORDS int32, cleared by the call) counts BAD_COORD (rows that do
+ * not pack into a key), DUPLICATE (rows repeating a coordinate) and
+ * OUT_OF_BOX (rows outside [0, batches) x [0, shape)).
+ * st_kmap_subm_workspace returns ST_ERR_ARG when the box is far larger than
+ * the set (level 1 would exceed 64 bytes a row): query a hash table instead.
+ */
+int st_kmap_subm_workspace(int64_t n, int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* bytes);
+int st_kmap_subm(const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K, int64_t batches,
+                 int64_t sx, int64_t sy, int64_t sz, void* workspace, int64_t workspace_bytes, int32_t* nbr,
+                 uint32_t* row_masks, int32_t* status, st_stream_t stream);
 
 /* Geometry of a strided or transposed convolution's output-coordinate build. */
 typedef struct st_outgeom {

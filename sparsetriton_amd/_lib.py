@@ -51,17 +51,6 @@ class Lookup(ctypes.Structure):
     ]
 
 
-class Occupancy(ctypes.Structure):
-    _fields_ = [
-        ("words", ctypes.c_void_p),
-        ("batches", ctypes.c_int64),
-        ("shape", ctypes.c_int64 * 3),
-        ("scale", ctypes.c_int64),
-        ("prefix", ctypes.c_void_p),
-        ("rowmap", ctypes.c_void_p),
-    ]
-
-
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
@@ -73,11 +62,9 @@ _SIGNATURES = {
     "st_fill_u64": [_P, _L, ctypes.c_uint64, _P],
     "st_hash_insert": [_P, _I, _L, _L, _P, _P, _L, _P, _P],
     "st_hash_query": [_P, _I, _L, _P, _P, _L, _P, _P],
-    "st_occupancy_words": [_L, _L, _L, _L, ctypes.POINTER(_L)],
-    "st_occupancy_build": [_P, _I, _L, _P, _L, _L, _L, _L, _P, _P],
-    "st_occupancy_rank": [_P, _I, _L, ctypes.POINTER(Occupancy), _P, _P, _P, _P],
-    "st_kmap_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, ctypes.POINTER(Occupancy), _P, _L, _L, _P,
-                      _P, _P],
+    "st_kmap_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, _P, _L, _L, _P, _P, _P],
+    "st_kmap_subm_workspace": [_L, _L, _L, _L, _L, ctypes.POINTER(_L)],
+    "st_kmap_subm": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _L, _P, _P, _P, _P],
     "st_outcoords_sizes": [_L, ctypes.POINTER(OutGeom), _L, _L, ctypes.POINTER(_L), ctypes.POINTER(_L)],
     "st_outcoords_plan": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _L, _P, _L, _P, _P],
     "st_outcoords_emit": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _P, _L, _P, _L, _P, _P, _L, _P, _L,

@@ -142,78 +142,6 @@ __device__ __forceinline__ void unpack_key(uint64_t key, int64_t& b, int64_t& x,
   z = (int16_t)(uint16_t)key;
 }
 
-// ------------------------------------------------------- occupancy bitmap
-
-// Device view of an st_occupancy (words == nullptr: no bitmap, always probe).
-struct Occ {
-  const uint64_t* words;
-  const int32_t* prefix;  // rank index (optional)
-  const int32_t* rowmap;
-  int nb, sx, sy, sz, bx, by, bz, scale;
-};
-
-__host__ __forceinline__ Occ make_occ(const st_occupancy* o) {
-  Occ d{};
-  if (!o || !o->words) return d;
-  d.words = o->words;
-  d.prefix = o->prefix;
-  d.rowmap = o->rowmap;
-  d.nb = (int)o->batches;
-  d.sx = (int)o->shape[0];
-  d.sy = (int)o->shape[1];
-  d.sz = (int)o->shape[2];
-  d.bx = (d.sx + 3) >> 2;
-  d.by = (d.sy + 3) >> 2;
-  d.bz = (d.sz + 3) >> 2;
-  d.scale = o->scale > 1 ? (int)o->scale : 1;
-  return d;
-}
-
-__host__ inline bool occ_valid(const st_occupancy* o) {
-  if (!o || !o->words) return true;
-  return o->batches > 0 && o->batches <= 32768 && o->scale >= 1 && o->scale <= 32768 && o->shape[0] > 0 &&
-         o->shape[0] <= 65536 && o->shape[1] > 0 && o->shape[1] <= 65536 && o->shape[2] > 0 &&
-         o->shape[2] <= 65536;
-}
-
-__device__ __forceinline__ int64_t occ_word(const Occ& o, int b, int x, int y, int z) {
-  return (((int64_t)b * o.bx + (x >> 2)) * o.by + (y >> 2)) * o.bz + (z >> 2);
-}
-
-__device__ __forceinline__ int occ_bit(int x, int y, int z) { return ((x & 3) << 4) | ((y & 3) << 2) | (z & 3); }
-
-// Occupancy test split in two so that many tests can have their word loads in
-// flight together: occ_locate() returns 0 when the coordinate (table-key
-// space, components packable) is certainly absent, 1 when bit `bit` of word
-// `word` decides, 2 when it must be probed (no bitmap, or outside the box).
-__device__ __forceinline__ int occ_locate(const Occ& o, int b, int x, int y, int z, int64_t& word, int& bit) {
-  if (!o.words) return 2;
-  if (o.scale > 1) {
-    if (x % o.scale || y % o.scale || z % o.scale) return 0;
-    x /= o.scale;
-    y /= o.scale;
-    z /= o.scale;
-  }
-  if (b < 0 || b >= o.nb || x < 0 || x >= o.sx || y < 0 || y >= o.sy || z < 0 || z >= o.sz) return 2;
-  word = occ_word(o, b, x, y, z);
-  bit = occ_bit(x, y, z);
-  return 1;
-}
-
-// False only when the coordinate (in table-key space, components packable)
-// is certainly absent; true means "probe the table".
-__device__ __forceinline__ bool occ_maybe(const Occ& o, int b, int x, int y, int z) {
-  if (!o.words) return true;
-  if (o.scale > 1) {
-    if (x % o.scale || y % o.scale || z % o.scale) return false;
-    x /= o.scale;
-    y /= o.scale;
-    z /= o.scale;
-  }
-  if (b < 0 || b >= o.nb || x < 0 || x >= o.sx || y < 0 || y >= o.sy || z < 0 || z >= o.sz) return true;
-  return (o.words[occ_word(o, b, x, y, z)] >> occ_bit(x, y, z)) & 1ull;
-}
-
 // ------------------------------------------------------------- coordinates
 
 template <typename CT>

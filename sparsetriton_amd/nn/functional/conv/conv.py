@@ -28,7 +28,7 @@ from sparsetriton_amd.utils.hash import HashTable
 
 from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, InputGradLookup
 from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM, conv_forward_epilogue
-from .kmap import KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map
+from .kmap import KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map, subm_kernel_map
 
 __all__ = ["sparse_conv3d", "compute_neighbor_indices", "table_capacity"]
 
@@ -59,20 +59,19 @@ def compute_neighbor_indices(
 
 
 def _input_table(tensor: SparseTensor, scale: int) -> HashTable:
-    """The coordinate table of ``tensor`` (coordinates * scale for transposed convs), cached."""
+    """The coordinate table of ``tensor`` (coordinates * scale for transposed convs), cached.  Its
+    clear and insert run when a kernel first reads it (a submanifold precomputed map never does)."""
     cache = tensor._cache
     if scale == 1:
         if cache.hashtable is None:
             t = HashTable(table_capacity(tensor.C.shape[0]), device=tensor.F.device)
             t.insert(tensor.C)
-            t.build_occupancy(tensor.C, tensor.batch_size, tensor.spatial_shape)
             cache.hashtable = t
         return cache.hashtable
     key = ("scaled_table", scale)
     if key not in cache.kmaps:
         t = HashTable(table_capacity(tensor.C.shape[0]), device=tensor.F.device)
         t.insert(tensor.C, scale=scale)
-        t.build_occupancy(tensor.C, tensor.batch_size, tensor.spatial_shape, scale=scale)
         cache.kmaps[key] = t
     return cache.kmaps[key]
 
@@ -146,7 +145,6 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
     _lib.require_device(tensor.F, "SparseTensor features")
 
     scale = s if (transposed and s > 1) else 1
-    in_table = _input_table(tensor, scale)
     lookup_shape = tuple(int(v) * scale for v in tensor.spatial_shape)
     subm_fast = submanifold and s == 1 and ((k - 1) * d) // 2 == p
     cache_key = (k, s, p, d, submanifold, transposed)
@@ -156,21 +154,32 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
     # forward is queued the host waits for that copy (not for the forward) and raises if a
     # coordinate could not be keyed or the table overflowed -- rows the map would silently lack.
     table_status = None
+    in_table = None
     if algo == ConvAlgo.PrecomputedNeighborGEMM:
         hit = tensor._cache.neighbor_indices.get(cache_key)
         if hit is not None:
             out_coords, kmap, new_shape = hit
         else:
+            built = None
             if subm_fast:
                 out_coords, new_shape = tensor.C, tensor.spatial_shape
                 offsets = _target_offsets(k, d, p, False, device)
-                # the symmetric claim is checked against the query's duplicate / out-of-bounds counts
-                kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1, tensor.C.shape[0],
+                # brick index + query in one launch; the symmetric claim is checked against its
+                # duplicate / out-of-bounds counts
+                built = subm_kernel_map(tensor.C, tensor.batch_size, tensor.spatial_shape, offsets,
                                         symmetric=(k % 2 == 1))
+                if built is not None:
+                    kmap, table_status = built
+                else:
+                    in_table = _input_table(tensor, scale)
+                    kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1,
+                                            tensor.C.shape[0], symmetric=(k % 2 == 1))
             else:
+                in_table = _input_table(tensor, scale)
                 out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
                     tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
-            table_status = in_table.snapshot()
+            if built is None:
+                table_status = in_table.snapshot()
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)
         if out_coords.shape[0] == 0:
             _raise_table_errors(table_status, in_table)
@@ -186,6 +195,7 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
     elif algo == ConvAlgo.ImplicitHashFlyGEMM:
         hkey = ("hashfly",) + cache_key
         hit = tensor._cache.kmaps.get(hkey)
+        in_table = _input_table(tensor, scale)
         in_keys, in_vals = in_table.table_keys, in_table.table_values  # runs a deferred insert
         if hit is None:
             if subm_fast:
@@ -224,9 +234,9 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
     return SparseTensor(feats=out_feats, coords=out_coords, spatial_shape=new_shape, batch_size=tensor.batch_size)
 
 
-def _raise_table_errors(status, table: HashTable) -> None:
+def _raise_table_errors(status, table) -> None:
     if status is not None:
-        status.raise_errors(table.capacity)
+        status.raise_errors(table.capacity if table is not None else 0)
 
 
 def _empty(tensor: SparseTensor, C_out: int, new_shape) -> SparseTensor:

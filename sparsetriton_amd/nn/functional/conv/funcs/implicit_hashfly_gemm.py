@@ -149,7 +149,7 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
             else:
                 nbr = torch.empty((K, coords.shape[0]), dtype=torch.int32, device=coords.device)
                 _lib.call("st_kmap_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0],
-                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0], None,
+                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
                           _lib.ptr(nbr), coords.shape[0], 1, None, None, _lib.stream_of(coords.device))
                 kmap = KernelMap(nbr, N_in, coords.shape[0], K)
                 kmap.set_row_representatives(row_representatives(coords))  # repeated output coordinates

@@ -35,6 +35,8 @@ __all__ = [
     "compute_target_offsets_transposed",
     "build_out_coords",
     "KernelMap",
+    "query_kernel_map",
+    "subm_kernel_map",
     "row_representatives",
     "TilePlan",
     "PairList",
@@ -461,14 +463,9 @@ def _offsets_i32(kernel_offsets: torch.Tensor) -> torch.Tensor:
     return kernel_offsets.to(torch.int32).contiguous()
 
 
-def _occupancy_ref(table):
-    ref = getattr(table, "occupancy_ref", None)
-    return ref() if ref is not None else None
-
-
 def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets: torch.Tensor, spatial_shape,
                      stride: int, n_in: int, symmetric: bool = False) -> KernelMap:
-    """nbr[k, o] = row of out_o * stride - t_k (bounds [0, shape)), via ``st_kmap_query``.
+    """nbr[k, o] = row of out_o * stride - t_k (bounds [0, shape)), via ``st_kmap_query`` (hash table).
 
     ``symmetric`` declares a submanifold map of an odd kernel (offsets ``t`` and
     ``-t`` at k and K-1-k) over the table's own coordinates, whose transpose is
@@ -486,25 +483,61 @@ def query_kernel_map(table: HashTable, out_coords: torch.Tensor, kernel_offsets:
     nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
     masks = torch.empty((n_out, _mask_words(K)), dtype=torch.int32, device=dev)
     sx, sy, sz = (int(v) for v in spatial_shape)
-    occ = _occupancy_ref(table)
-    # With a rank index of these very coordinates over the query box no hash probe is
-    # needed: a submanifold query stays in the box (its bounds are the query bounds)
-    # and in the batches of the rows it comes from.
-    rank_only = (getattr(table, "has_rank_index", lambda c=None: False)(out_coords) and int(stride) == 1
-                 and tuple(int(v) for v in table.occupancy[1].shape) == (sx, sy, sz))
-    if rank_only:
-        keys = vals = None
-        cap = 0
-    else:
-        keys, vals, cap = _lib.ptr(table.table_keys), _lib.ptr(table.table_values), table.capacity
     status = table.status_tensor() if symmetric else None
-    _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out,
-              _lib.ptr(_offsets_i32(kernel_offsets)), K, int(stride), sx, sy, sz, keys, vals, cap, occ,
-              _lib.ptr(nbr), n_out, 1, _lib.ptr(masks), _lib.ptr(status), _lib.stream_of(dev))
+    keys, vals = table.table_keys, table.table_values  # runs a deferred insert first
+    offs = _offsets_i32(kernel_offsets)  # held until the launch is queued (it may be a temporary)
+    _lib.call("st_kmap_query", _lib.ptr(out_coords), _lib.coord_code(out_coords.dtype), n_out, _lib.ptr(offs), K,
+              int(stride), sx, sy, sz, _lib.ptr(keys), _lib.ptr(vals), table.capacity, _lib.ptr(nbr), n_out, 1,
+              _lib.ptr(masks), _lib.ptr(status), _lib.stream_of(dev))
     check = table.snapshot() if symmetric else None
     km = KernelMap(nbr, n_in, n_out, K, out_masks=masks, symmetric=symmetric, symmetry_check=check)
     km._out_coords = out_coords if symmetric else None
     return km
+
+
+@functools.lru_cache(maxsize=64)
+def _subm_workspace_bytes(n: int, batches: int, sx: int, sy: int, sz: int) -> int:
+    nbytes = ctypes.c_int64()
+    rc = _lib.lib().st_kmap_subm_workspace(n, batches, sx, sy, sz, ctypes.byref(nbytes))
+    return int(nbytes.value) if rc == _lib.ST_OK else -1
+
+
+def subm_kernel_map(coords: torch.Tensor, batch_size: int, spatial_shape, kernel_offsets: torch.Tensor,
+                    symmetric: bool = True):
+    """Submanifold map of ``coords`` over themselves (out = in, stride 1, bounds ``spatial_shape``) by
+    ``st_kmap_subm``, which indexes the coordinates by 4x4x4 bricks (no hash table).
+
+    Returns (KernelMap, StatusSnapshot of the build's bad-coordinate / duplicate / out-of-box counts), or
+    None when the box cannot be indexed (batch or shape out of range, or far larger than the set) -- the
+    caller then queries a hash table."""
+    from sparsetriton_amd.utils.hash import StatusSnapshot
+
+    coords = coords.contiguous()
+    dev = coords.device
+    _lib.require_device(coords, "coordinates")
+    n = coords.shape[0]
+    K = kernel_offsets.shape[0]
+    if K > _lib.MAX_KVOL:
+        raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
+    sx, sy, sz = (int(v) for v in spatial_shape)
+    nbytes = _subm_workspace_bytes(int(n), int(batch_size), sx, sy, sz)
+    if nbytes < 0:
+        return None
+    work = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    # cleared by the launch (which an empty set skips)
+    status = (torch.empty if n else torch.zeros)((_lib.STATUS_WORDS,), dtype=torch.int32, device=dev)
+    nbr = torch.empty((K, n), dtype=torch.int32, device=dev)
+    masks = torch.empty((n, _mask_words(K)), dtype=torch.int32, device=dev)
+    offs = _offsets_i32(kernel_offsets)  # held until the launch is queued (it may be a temporary)
+    rc = _lib.lib().st_kmap_subm(_lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(offs), K,
+                                 int(batch_size), sx, sy, sz,
+                                 _lib.ptr(work), nbytes, _lib.ptr(nbr), _lib.ptr(masks), _lib.ptr(status),
+                                 _lib.stream_of(dev))
+    _lib.check(rc, "st_kmap_subm")
+    snap = StatusSnapshot(status)
+    km = KernelMap(nbr, n, n, K, out_masks=masks, symmetric=symmetric, symmetry_check=snap if symmetric else None)
+    km._out_coords = coords if symmetric else None
+    return km, snap
 
 
 class OutCoordTable:

@@ -18,9 +18,8 @@ What differs, by design:
 * Duplicate coordinates resolve to the lowest row index, on every run.
 * ``insert`` records the rows; the insert kernel runs when the table arrays
   are first needed (``table_keys`` / ``table_values``, ``query``,
-  ``counters``, moving devices).  A submanifold kernel map over the
-  occupancy bitmap's rank index never needs them, so it never pays for the
-  hash build.
+  ``counters``, moving devices).  A submanifold kernel map is built from its
+  own brick index (``st_kmap_subm``) and never needs the table.
 
 Insert and query run as HIP kernels (``st_hash_insert`` / ``st_hash_query``);
 there is no CPU implementation of them.
@@ -65,7 +64,7 @@ class StatusSnapshot:
             raise RuntimeError(f"HashTable: {c['overflow']} inserts found the table full (capacity {capacity})")
         if c["bad_coord"]:
             raise RuntimeError(
-                f"HashTable: {c['bad_coord']} coordinates outside the packable range "
+                f"{c['bad_coord']} coordinates outside the packable range "
                 "(batch in [0, 32767], x/y/z in [-32768, 32767])"
             )
 
@@ -111,7 +110,6 @@ class HashTable:
         self._pending = None  # (coords, scale) recorded by insert(), applied by _materialize()
         self._needs_clear = False
         self.status = None
-        self.occupancy = None  # (words, ctypes st_occupancy, tensors kept alive) once build_occupancy() ran
         if table_keys is not None and table_values is not None:
             assert table_keys.shape == table_values.shape, "table_keys and table_values must have the same shape."
             self._keys, self._vals = table_keys, table_values
@@ -168,17 +166,9 @@ class HashTable:
     def capacity(self) -> int:
         return self._keys.shape[0]
 
-    def has_rank_index(self, coords: torch.Tensor = None) -> bool:
-        """Whether the occupancy bitmap carries a rank index (so queries need no hash probe),
-        and, if ``coords`` is given, was built from that very tensor."""
-        if self.occupancy is None or not self.occupancy[1].rowmap:
-            return False
-        return coords is None or coords is self.occupancy[3]
-
     # ------------------------------------------------------------ operations
     def clear(self) -> "HashTable":
         """Mark every slot empty (keys and values all-ones, i.e. -1)."""
-        self.occupancy = None
         self._pending = None
         if self._keys.is_cuda:
             self._needs_clear = True  # filled when the table is next needed
@@ -225,51 +215,9 @@ class HashTable:
             "HashTable arrays must be int64 keys / int32 values"
         )
         _lib.coord_code(keys.dtype)  # rejects unsupported coordinate dtypes now
-        self._materialize()  # an earlier pending insert goes first
+        if self._pending is not None:
+            self._materialize()  # an earlier pending insert goes first (the clear stays deferred otherwise)
         self._pending = (keys, int(scale))
-
-    def build_occupancy(self, coords: torch.Tensor, batch_size: int, spatial_shape, scale: int = 1) -> bool:
-        """Occupancy bitmap of the inserted ``coords`` over (batch_size, *spatial_shape).
-
-        Kernel-map queries test a voxel's bit before probing, so absent
-        neighbours cost one cached word load.  The bitmap (1 bit per voxel of
-        the box) is built only when it is no larger than one 8-byte read per
-        query of a 27-offset map (216 bytes per row) and at most 1 GiB;
-        returns whether it was built.  ``scale`` is the insert's scale.
-        """
-        n = coords.shape[0]
-        sx, sy, sz = (int(v) for v in spatial_shape)
-        if n == 0 or batch_size <= 0 or min(sx, sy, sz) <= 0 or max(sx, sy, sz) > 65536 or batch_size > 32768:
-            self.occupancy = None
-            return False
-        nw = _lib.ctypes.c_int64()
-        _lib.call("st_occupancy_words", int(batch_size), sx, sy, sz, _lib.ctypes.byref(nw))
-        if nw.value * 8 > min(216 * n, 1 << 30):
-            self.occupancy = None
-            return False
-        coords = coords.contiguous()
-        words = torch.empty((nw.value,), dtype=torch.int64, device=self.device)
-        stream = _lib.stream_of(self.device)
-        _lib.call("st_occupancy_build", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(words),
-                  int(batch_size), sx, sy, sz, _lib.ptr(self._status()), stream)
-        occ = _lib.Occupancy(words.data_ptr(), int(batch_size), (_lib.ctypes.c_int64 * 3)(sx, sy, sz), int(scale),
-                             None, None)
-        keep = [words]
-        if scale == 1:
-            # rank index: in-box neighbours resolve by rank, with no hash probe
-            prefix = torch.empty((nw.value + 1,), dtype=torch.int32, device=self.device)
-            rowmap = torch.empty((n,), dtype=torch.int32, device=self.device)
-            work = torch.empty(((nw.value + 4095) // 4096 + 1,), dtype=torch.int32, device=self.device)
-            _lib.call("st_occupancy_rank", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ctypes.byref(occ),
-                      _lib.ptr(prefix), _lib.ptr(rowmap), _lib.ptr(work), stream)
-            occ.prefix, occ.rowmap = prefix.data_ptr(), rowmap.data_ptr()
-            keep += [prefix, rowmap]
-        self.occupancy = (words, occ, keep, coords)
-        return True
-
-    def occupancy_ref(self):
-        """ctypes pointer to the bitmap descriptor, or None."""
-        return None if self.occupancy is None else _lib.ctypes.byref(self.occupancy[1])
 
     def query(self, keys: torch.Tensor) -> torch.Tensor:
         """Row index of each (N, 4) coordinate, or -1 when absent (int32, shape (N,))."""

@@ -111,61 +111,3 @@ def test_empty(device):
     t = HashTable(capacity=4, device=device)
     t.insert(torch.empty((0, 4), dtype=torch.int16, device=device))
     assert t.query(torch.empty((0, 4), dtype=torch.int16, device=device)).shape == (0,)
-
-
-def _occupancy_np(c, B, shape):
-    """Bitmap in the documented brick layout: bit (x%4)*16+(y%4)*4+z%4 of word ((b*BX+x/4)*BY+y/4)*BZ+z/4."""
-    BX, BY, BZ = ((s + 3) // 4 for s in shape)
-    words = np.zeros(B * BX * BY * BZ, dtype=np.uint64)
-    inside = ((c[:, 0] >= 0) & (c[:, 0] < B) & (c[:, 1] >= 0) & (c[:, 1] < shape[0]) & (c[:, 2] >= 0)
-              & (c[:, 2] < shape[1]) & (c[:, 3] >= 0) & (c[:, 3] < shape[2]))
-    b, x, y, z = (c[inside, j].astype(np.int64) for j in range(4))
-    w = ((b * BX + x // 4) * BY + y // 4) * BZ + z // 4
-    bit = ((x % 4) * 16 + (y % 4) * 4 + z % 4).astype(np.uint64)
-    np.bitwise_or.at(words, w, np.uint64(1) << bit)
-    return words
-
-
-@pytest.mark.parametrize("shape", [(37, 21, 13), (64, 64, 64), (1, 1, 1)])
-def test_occupancy_bitmap_layout(device, shape):
-    rng = np.random.default_rng(sum(shape))
-    B = 3
-    n = min(5000, B * shape[0] * shape[1] * shape[2] // 2 + 1)
-    c = np.stack([rng.integers(0, B, n), rng.integers(0, shape[0], n), rng.integers(0, shape[1], n),
-                  rng.integers(0, shape[2], n)], 1)
-    c = np.concatenate([c, [[0, shape[0], 0, 0], [B, 0, 0, 0]]])  # outside the box: not in the bitmap
-    t = HashTable(capacity=2 * c.shape[0], device=device)
-    ct = torch.tensor(c, dtype=torch.int32, device=device)
-    t.insert(ct)
-    assert t.build_occupancy(ct, B, shape)
-    got = t.occupancy[0].cpu().numpy().view(np.uint64)
-    assert np.array_equal(got, _occupancy_np(c, B, shape))
-    # rank index: prefix = exclusive popcount prefix of the words; rowmap[rank] = lowest row
-    # of the rank-th set voxel in word / bit order
-    prefix, rowmap = (x.cpu().numpy() for x in t.occupancy[2][1:3])
-    pcs = np.array([bin(int(v)).count("1") for v in got], dtype=np.int64)
-    assert np.array_equal(prefix, np.concatenate([[0], np.cumsum(pcs)]))
-    BX, BY, BZ = ((s + 3) // 4 for s in shape)
-    inside = (c[:, 0] < B) & (c[:, 1] < shape[0])
-    ci = c[inside].astype(np.int64)
-    rows = np.nonzero(inside)[0]
-    lin = (((ci[:, 0] * BX + ci[:, 1] // 4) * BY + ci[:, 2] // 4) * BZ + ci[:, 3] // 4) * 64 + \
-        (ci[:, 1] % 4) * 16 + (ci[:, 2] % 4) * 4 + ci[:, 3] % 4
-    uniq, first = np.unique(lin, return_index=True)  # sorted = rank order; first = lowest row (rows ascend)
-    assert np.array_equal(rowmap[:len(uniq)], rows[first])
-    # rebuilding over other coordinates clears the previous bits
-    half = c.shape[0] // 2
-    assert t.build_occupancy(ct[:half], B, shape)
-    assert np.array_equal(t.occupancy[0].cpu().numpy().view(np.uint64), _occupancy_np(c[:half], B, shape))
-    t.clear()
-    assert t.occupancy is None
-
-
-def test_occupancy_size_rule(device):
-    t = HashTable(capacity=64, device=device)
-    c = torch.tensor([[0, 1, 2, 3]], dtype=torch.int32, device=device)
-    t.insert(c)
-    # a 4096^3 box for one voxel is far more than the probes it would save: not built
-    assert not t.build_occupancy(c, 1, (4096, 4096, 4096))
-    assert t.occupancy is None and t.occupancy_ref() is None
-    assert t.build_occupancy(c, 1, (8, 8, 8))

@@ -14,6 +14,7 @@ import torch
 
 from oracle import oracle as O
 from sparsetriton_amd import SparseTensor, workloads
+from sparsetriton_amd.nn.functional import sparse_conv3d
 from sparsetriton_amd.nn.functional.conv.conv import _input_table, compute_neighbor_indices
 from sparsetriton_amd.nn.functional.conv.kmap import (
     _target_offsets,
@@ -393,35 +394,108 @@ def test_wgrad_scan_matches_pairs(device):
             assert err < (2e-3 if dtype == torch.float32 else 2e-2)
 
 
-@pytest.mark.parametrize("case", ["subm", "transposed"])
-def test_occupancy_filter_changes_nothing(device, case):
-    """Kernel maps with and without the occupancy bitmap are identical (the bitmap only skips
-    probes that would miss), for the plain table and for a scaled (transposed) table."""
-    rng = np.random.default_rng(77)
-    c = _rand_coords(rng, 9000, 24, B=3)
+SUBM_CASES = [
+    # name, batches, shape, n, coordinate dtype, kernel, dilation
+    ("small-box", 3, (37, 21, 13), 4000, torch.int16, 3, 1),
+    ("dense", 2, (12, 12, 12), 3000, torch.int32, 3, 1),
+    ("k5", 2, (30, 30, 30), 5000, torch.int16, 5, 1),
+    ("dilated", 2, (30, 30, 30), 5000, torch.int16, 3, 2),
+    ("one-voxel-box", 1, (1, 1, 1), 1, torch.int16, 3, 1),
+    ("wide", 4, (1440, 1440, 41), 60000, torch.int16, 3, 1),
+    ("int64", 2, (40, 50, 60), 6000, torch.int64, 3, 1),
+]
+
+
+@pytest.mark.parametrize("case", SUBM_CASES, ids=[c[0] for c in SUBM_CASES])
+def test_subm_brick_index_map_exact(device, case):
+    """st_kmap_subm (brick index + query, one cooperative launch) equals the exact map, the hash-table
+    query and the row masks, on boxes with partial bricks, dense sets, k = 5 and dilation 2."""
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    name, B, shape, n, dt, k, d = case
+    rng = np.random.default_rng(len(name) * 31 + n)
+    vol = B * shape[0] * shape[1] * shape[2]
+    lin = np.sort(rng.choice(vol, min(n, vol), replace=False))
+    sx, sy, sz = shape
+    c = np.stack([lin // (sx * sy * sz), (lin // (sy * sz)) % sx, (lin // sz) % sy, lin % sz], 1).astype(np.int32)
+    coords = torch.as_tensor(c, dtype=dt, device=device)
+    offs = _target_offsets(k, d, (k - 1) * d // 2, False, device)
+    km, snap = subm_kernel_map(coords, B, shape, offs)
+    expect = O.exact_kmap(c, c, O.target_offsets(k, d, (k - 1) * d // 2, False), 1, shape)
+    assert (km.neighbor_indices.cpu().numpy() == expect).all()
+    _check_masks(km)
+    assert snap.counters() == {"overflow": 0, "bad_coord": 0, "duplicate": 0, "out_of_box": 0}
+    assert km.symmetric == (k % 2 == 1)
+    # the hash-table path gives the same map
+    sp = SparseTensor(torch.zeros((c.shape[0], 1), device=device), coords, spatial_shape=shape, batch_size=B)
+    table = _input_table(sp, 1)
+    hashed = query_kernel_map(table, sp.C, offs, shape, 1, c.shape[0])
+    assert torch.equal(hashed.nbr, km.nbr) and torch.equal(hashed.out_masks, km.out_masks)
+
+
+def test_subm_brick_index_out_of_box_and_repeats(device):
+    """Rows outside the box keep their in-box neighbours; repeats resolve to the lowest row; the
+    status counts both (and the map is then not treated as its own transpose)."""
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    rng = np.random.default_rng(88)
+    c = _rand_coords(rng, 3000, 20)
+    shape = (15, 18, 20)
+    c[rng.choice(3000, 40, replace=False)] = c[rng.choice(3000, 40, replace=False)]
     coords = torch.as_tensor(c, dtype=torch.int16, device=device)
-    sp = SparseTensor(torch.zeros((c.shape[0], 1), device=device), coords, spatial_shape=(24, 24, 24))
-    if case == "subm":
-        table = _input_table(sp, 1)
-        assert table.occupancy is not None
-        offs = _target_offsets(3, 1, 1, False, device)
-        q, shape, stride = sp.C, (24, 24, 24), 1
-    else:
-        s = 2
-        table = _input_table(sp, s)
-        assert table.occupancy is not None and table.occupancy[1].scale == s
-        offs = _target_offsets(3, 1, 1, True, device)
-        q, shape, stride = build_out_coords(sp.C, (24, 24, 24), 3, stride=s, padding=1, transposed=True,
-                                            submanifold=False)[0], (48, 48, 48), 1
-    with_bm = query_kernel_map(table, q, offs, shape, stride, c.shape[0]).neighbor_indices.clone()
-    occ = table.occupancy
-    table.occupancy = None
-    try:
-        without = query_kernel_map(table, q, offs, shape, stride, c.shape[0]).neighbor_indices
-    finally:
-        table.occupancy = occ
-    assert torch.equal(with_bm, without)
-    assert int((with_bm >= 0).sum()) > c.shape[0]
+    offs = _target_offsets(3, 1, 1, False, device)
+    km, snap = subm_kernel_map(coords, 2, shape, offs)
+    expect = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, shape)
+    assert (km.neighbor_indices.cpu().numpy() == expect).all()
+    oob = ~((c[:, 1] < 15) & (c[:, 2] < 18))
+    cnt = snap.counters()
+    assert cnt["out_of_box"] == int(oob.sum()) and cnt["duplicate"] > 0 and cnt["bad_coord"] == 0
+    assert not km.symmetric
+
+
+def test_subm_brick_index_bad_coordinates(device):
+    """int32 coordinates beyond the 16-bit key range (inside a box up to 65536 wide) are counted as
+    unkeyable, and sparse_conv3d raises for them."""
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    c = np.array([[0, 40000, 1, 1], [0, 40001, 1, 1], [0, 5, 5, 5]], dtype=np.int32)
+    coords = torch.as_tensor(c, device=device)
+    km, snap = subm_kernel_map(coords, 1, (40002, 8, 8), _target_offsets(3, 1, 1, False, device))
+    assert snap.counters()["bad_coord"] == 2
+
+
+def test_subm_brick_index_declines_a_box_far_larger_than_the_set(device):
+    """More than 64 bricks a row (plus slack): no brick index -- sparse_conv3d takes the hash table
+    and gives the same exact map."""
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    rng = np.random.default_rng(3)
+    c = np.stack([np.zeros(500, np.int64), rng.integers(0, 4000, 500), rng.integers(0, 4000, 500),
+                  rng.integers(0, 400, 500)], 1).astype(np.int32)
+    c = np.unique(c, axis=0)
+    coords = torch.as_tensor(c, dtype=torch.int16, device=device)
+    offs = _target_offsets(3, 1, 1, False, device)
+    assert subm_kernel_map(coords, 1, (4000, 4000, 400), offs) is None
+    sp = SparseTensor(torch.randn((c.shape[0], 4), device=device), coords, spatial_shape=(4000, 4000, 400),
+                      batch_size=1)
+    out = sparse_conv3d(sp, torch.randn((27, 4, 4), device=device), 3)
+    km = sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)][1]
+    assert (km.neighbor_indices.cpu().numpy() == O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1,
+                                                             (4000, 4000, 400))).all()
+    assert out.F.shape == (c.shape[0], 4)
+
+
+def test_subm_brick_index_empty(device):
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    coords = torch.empty((0, 4), dtype=torch.int16, device=device)
+    km, snap = subm_kernel_map(coords, 1, (8, 8, 8), _target_offsets(3, 1, 1, False, device))
+    assert km.nbr.shape == (27, 0)
+
+
+def test_config5_subm_brick_index_exact(device):
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    c, shape = workloads.config5()
+    coords = torch.as_tensor(c, dtype=torch.int16, device=device)
+    km, snap = subm_kernel_map(coords, 1, shape, _target_offsets(3, 1, 1, False, device))
+    expect = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, shape)
+    assert (km.neighbor_indices.cpu().numpy() == expect).all()
+    assert km.symmetric
 
 
 def test_gather_without_sources_writes_zeros(device):
