@@ -284,6 +284,55 @@ int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride
 int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
                              int64_t max_chunks, int64_t n_out, uint32_t* keys, st_stream_t stream);
 
+/*
+ * The same chunk order in one launch: the keys above are nondecreasing within
+ * each offset's run of chunks, so a chunk's place in their stable order follows
+ * from a per-(offset, bucket) count table and one binary search in its own run
+ * (keys and table in one workgroup's LDS).
+ * order: max_chunks int32.  ST_ERR_UNSUPPORTED above 16384 chunks or 28
+ * offsets (use the keys and st_kmap_sort_rows there).
+ */
+int st_kmap_pairs_chunk_order(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
+                              int64_t max_chunks, int64_t n_out, int32_t* order, st_stream_t stream);
+
+/*
+ * Everything the gather-GEMMs and the weight gradient need from one map, in
+ * one call: the mask-sorted row order and the tile plan (st_kmap_sort_rows +
+ * st_tile_plan) on `stream` and, with chunk > 0, the pair list and its chunk
+ * order (st_kmap_pairs + st_kmap_pairs_chunk_order) on a stream of the
+ * library's that forks from `stream` at the call and joins it again before
+ * the tile plan ends -- so work queued on `stream` after the call sees every
+ * buffer complete, and nothing else has to be synchronised.  Calls from
+ * several host threads are serialised per device.
+ *
+ * st_kmap_plans_layout fills layout[ST_PLAN_FIELDS]: byte offsets into the
+ * caller's `plan` buffer of the outputs below (each on a 256-byte boundary),
+ * the two buffer sizes, the tile count and max_chunks.  `scratch` is only
+ * used during the call's work on the GPU (stream order).
+ * Row order and tiles cover the n_dst destination rows; the pairs are
+ * (map[k, o], o) over the same map, o < n_dst, map entries >= n_src skipped.
+ * No counterpart in the reference, whose GEMMs read the (N_out, K) map
+ * directly (implicit_precomputed_gemm.py:64-126, 180-230).
+ */
+enum {
+  ST_PLAN_PERM = 0,       /* int32 [n_dst]                                   */
+  ST_PLAN_TILE_NK,        /* int32 [tiles]                                   */
+  ST_PLAN_TILE_KLIST,     /* int16 [tiles * K]                               */
+  ST_PLAN_TILE_MAP,       /* int32 [tiles * K * 128]                         */
+  ST_PLAN_PAIRS,          /* int32 [2 * K * n_dst] (in, out); chunk > 0      */
+  ST_PLAN_KSTART,         /* int32 [K + 1]                                   */
+  ST_PLAN_CSTART,         /* int32 [K + 1]                                   */
+  ST_PLAN_CORDER,         /* int32 [max_chunks]                              */
+  ST_PLAN_BYTES,          /* size of `plan`                                  */
+  ST_PLAN_SCRATCH_BYTES,  /* size of `scratch`                               */
+  ST_PLAN_TILES,          /* ceil(n_dst / 128)                               */
+  ST_PLAN_MAX_CHUNKS,     /* K * n_dst / chunk + K (0 without a pair list)   */
+  ST_PLAN_FIELDS
+};
+int st_kmap_plans_layout(int64_t n_dst, int K, int chunk, int64_t* layout);
+int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks, int K,
+                  int64_t n_dst, int64_t n_src, int chunk, void* plan, void* scratch, st_stream_t stream);
+
 /* ------------------------------------------------------------- gather-GEMM */
 
 /*

@@ -221,6 +221,21 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* to
 // (one workgroup; defined in kmap.hip).
 int launch_exclusive_scan(int32_t* counts, int64_t n, hipStream_t stream);
 
+constexpr int kPairRows = 4096;        // map rows per (row block, offset) workgroup of the pair list
+constexpr int kChunkOrderMax = 16384;  // chunks whose keys one workgroup holds in LDS (uint16 each)
+constexpr int kChunkOrderMaxK = 28;    // offsets of its per-(offset, bucket) count table
+
+// Pair list of a map (count, scan + kstart / cstart, emit) and its chunk order
+// (defined in kmap.hip; arguments checked by the caller).  launch_chunk_order
+// returns ST_ERR_UNSUPPORTED above kChunkOrderMax chunks or kChunkOrderMaxK offsets.
+int launch_pairs(const int32_t* map, int64_t ks, int64_t rs, int64_t n_out, int K, int64_t n_in,
+                 int32_t* block_counts, int64_t nb, int chunk, int32_t* kstart, int32_t* cstart, int32_t* pairs,
+                 hipStream_t stream);
+int launch_chunk_order(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
+                       int64_t max_chunks, int64_t n_out, int32_t* order, hipStream_t stream);
+int launch_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
+                      int64_t max_chunks, int64_t n_out, uint32_t* keys, hipStream_t stream);
+
 }  // namespace st
 
 // ------------------------------------------------------------- host helpers

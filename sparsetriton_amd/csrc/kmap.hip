@@ -189,7 +189,17 @@ __global__ __launch_bounds__(256) void cand_count_kernel(const CT* __restrict__ 
 // consecutive ones per thread read and written as two 16-byte vectors (a
 // wave covers 2 KB contiguously), with one workgroup scan per round.
 constexpr int kScanPer = 8;
-__global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restrict__ counts, int64_t n) {
+// In-place exclusive scan of counts[0..n), counts[n] = total, by one workgroup.
+// With `pl` set (the per-(offset, row block) pair counts of st_kmap_pairs,
+// n = K * nb) it also writes the pair list's kstart / cstart: kstart[k] is the
+// scanned count of (k, block 0), cstart[k] the chunks of the offsets before k.
+struct PairsFinal {
+  int32_t* kstart;
+  int32_t* cstart;
+  int64_t nb;
+  int K, chunk;
+};
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restrict__ counts, int64_t n, PairsFinal pl) {
   __shared__ int scratch[17];
   const bool vec = (reinterpret_cast<uintptr_t>(counts) & 15) == 0;
   int carry = 0;
@@ -228,10 +238,27 @@ __global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restric
     carry += tot;
   }
   if (threadIdx.x == 0) counts[n] = carry;
+  if (!pl.kstart) return;
+  __syncthreads();  // the scanned counts of the other threads are visible to the workgroup
+  // thread k < K (K <= 512): offset k's first pair and chunk count; cstart is the scan of the latter
+  const int k = threadIdx.x;
+  int nch = 0;
+  if (k < pl.K) {
+    const int32_t s0 = counts[(int64_t)k * pl.nb], s1 = k + 1 < pl.K ? counts[(int64_t)(k + 1) * pl.nb] : carry;
+    pl.kstart[k] = s0;
+    nch = (s1 - s0 + pl.chunk - 1) / pl.chunk;
+  }
+  int chunks;
+  const int cex = block_exclusive_scan(nch, scratch, &chunks);
+  if (k < pl.K) pl.cstart[k] = cex;
+  if (k == 0) {
+    pl.kstart[pl.K] = carry;
+    pl.cstart[pl.K] = chunks;
+  }
 }
 
 int launch_exclusive_scan(int32_t* counts, int64_t n, hipStream_t stream) {
-  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(counts, n);
+  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(counts, n, PairsFinal{nullptr, nullptr, 0, 0, 0});
   return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
 }
 
@@ -400,7 +427,7 @@ int st_outcoords_plan(const void* in_coords, int coord_dtype, int64_t n, const i
           (const CT*)in_coords, n, offsets, g, dkeys, dvals, (uint32_t)dcap, block_counts);
     });
   }
-  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, num_blocks);
+  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, num_blocks, PairsFinal{nullptr, nullptr, 0, 0, 0});
   ST_CHECK_LAUNCH();
   return ST_OK;
 }
@@ -487,7 +514,6 @@ extern "C" int st_kmap_invert(const int32_t* nbr, int64_t nbr_k_stride, int64_t 
 
 namespace st {
 
-constexpr int kPairRows = 4096;  // map rows per (block, offset) workgroup
 constexpr int kPairPer = kPairRows / 256;
 
 __device__ __forceinline__ bool pair_valid(int32_t i, int64_t n_in) { return i >= 0 && (int64_t)i < n_in; }
@@ -513,23 +539,6 @@ __global__ __launch_bounds__(256) void pairs_count_kernel(const int32_t* __restr
   if (lane == 0) wsum_s[wid] = c;
   __syncthreads();
   if (threadIdx.x == 0) counts[(int64_t)k * nb + blockIdx.x] = wsum_s[0] + wsum_s[1] + wsum_s[2] + wsum_s[3];
-}
-
-// kstart[k] = first pair of offset k (kstart[K] = P); cstart[k] = first chunk of
-// offset k, chunks of `chunk` pairs never straddling two offsets.
-__global__ void pairs_finalize_kernel(const int32_t* __restrict__ counts, int64_t nb, int K, int chunk,
-                                      int32_t* __restrict__ kstart, int32_t* __restrict__ cstart) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t c = 0;
-  for (int k = 0; k < K; ++k) {
-    const int32_t s = counts[(int64_t)k * nb];
-    const int32_t e = (k + 1 < K) ? counts[(int64_t)(k + 1) * nb] : counts[(int64_t)K * nb];
-    kstart[k] = s;
-    cstart[k] = c;
-    c += (e - s + chunk - 1) / chunk;
-  }
-  kstart[K] = counts[(int64_t)K * nb];
-  cstart[K] = c;
 }
 
 // Writes the (in, out) pairs of one (row block, offset) at offsets[k * nb + b]
@@ -580,6 +589,19 @@ extern "C" int st_kmap_pairs_sizes(int64_t n_out, int K, int64_t* num_blocks) {
   return ST_OK;
 }
 
+namespace st {
+// count, scan (+ kstart / cstart), emit; arguments checked by the caller
+int launch_pairs(const int32_t* map, int64_t ks, int64_t rs, int64_t n_out, int K, int64_t n_in,
+                 int32_t* block_counts, int64_t nb, int chunk, int32_t* kstart, int32_t* cstart, int32_t* pairs,
+                 hipStream_t stream) {
+  const dim3 grid((unsigned)nb, (unsigned)K);
+  if (nb > 0) pairs_count_kernel<<<grid, 256, 0, stream>>>(map, ks, rs, n_out, n_in, nb, block_counts);
+  exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, (int64_t)K * nb, PairsFinal{kstart, cstart, nb, K, chunk});
+  if (nb > 0) pairs_emit_kernel<<<grid, 256, 0, stream>>>(map, ks, rs, n_out, n_in, nb, block_counts, pairs);
+  return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
+}
+}  // namespace st
+
 extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n_out, int K,
                              int64_t n_in, int32_t* block_counts, int64_t num_blocks, int chunk, int32_t* kstart,
                              int32_t* cstart, int32_t* pairs, int64_t pair_capacity, st_stream_t stream) {
@@ -587,17 +609,8 @@ extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t m
   if (num_blocks != (n_out + st::kPairRows - 1) / st::kPairRows) return ST_ERR_ARG;
   if ((int64_t)K * n_out >= (1ll << 31) || pair_capacity < (int64_t)K * n_out) return ST_ERR_ARG;
   if (!block_counts || !kstart || !cstart || (n_out > 0 && (!map || !pairs))) return ST_ERR_ARG;
-  const dim3 grid((unsigned)num_blocks, (unsigned)K);
-  if (num_blocks > 0)
-    st::pairs_count_kernel<<<grid, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, num_blocks,
-                                                     block_counts);
-  st::exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, (int64_t)K * num_blocks);
-  st::pairs_finalize_kernel<<<1, 64, 0, stream>>>(block_counts, num_blocks, K, chunk, kstart, cstart);
-  if (num_blocks > 0)
-    st::pairs_emit_kernel<<<grid, 256, 0, stream>>>(map, map_k_stride, map_r_stride, n_out, n_in, num_blocks,
-                                                    block_counts, pairs);
-  ST_CHECK_LAUNCH();
-  return ST_OK;
+  return st::launch_pairs(map, map_k_stride, map_r_stride, n_out, K, n_in, block_counts, num_blocks, chunk, kstart,
+                          cstart, pairs, stream);
 }
 
 namespace st {
@@ -636,8 +649,111 @@ extern "C" int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kst
   if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0 || max_chunks >= (1ll << 31)) return ST_ERR_ARG;
   if (max_chunks == 0) return ST_OK;
   if (!pairs || !kstart || !cstart || !keys) return ST_ERR_ARG;
-  st::chunk_keys_kernel<<<st_blocks(max_chunks, 256), 256, 0, stream>>>(pairs, kstart, cstart, K, chunk, max_chunks,
-                                                                        n_out, keys);
-  ST_CHECK_LAUNCH();
-  return ST_OK;
+  return st::launch_chunk_keys(pairs, kstart, cstart, K, chunk, max_chunks, n_out, keys, stream);
+}
+
+int st::launch_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
+                          int64_t max_chunks, int64_t n_out, uint32_t* keys, hipStream_t stream) {
+  chunk_keys_kernel<<<st_blocks(max_chunks, 256), 256, 0, stream>>>(pairs, kstart, cstart, K, chunk, max_chunks,
+                                                                    n_out, keys);
+  return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
+}
+
+namespace st {
+// Chunk order without a sort: the chunk keys of chunk_keys_kernel (9-bit
+// bucket of the first output row) are nondecreasing within each offset's run
+// of chunks, so in the stable order by key chunk c (offset k, index j in its
+// run, bucket b) lands at
+//   #(chunks of any run with bucket < b) + #(runs k' < k with bucket b)
+//   + (j - #(run k's chunks with bucket < b)),
+// the first two from a per-(run, bucket) count table scanned over runs and
+// buckets, the last from a binary search in run k.  One workgroup holds the
+// keys and the table in LDS (K <= kChunkOrderMaxK, up to kChunkOrderMax
+// chunks); chunks past cstart[K] keep their index.  Same order as the stable
+// radix sort of the keys.
+constexpr int kChunkBuckets = 512;
+
+__device__ __forceinline__ int chunk_run(const int32_t* cstart_s, int K, int c) {
+  int lo = 0, hi = K - 1;  // largest k with cstart[k] <= c
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cstart_s[mid] <= c) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(1024) void chunk_order_kernel(const int32_t* __restrict__ pairs,
+                                                           const int32_t* __restrict__ kstart,
+                                                           const int32_t* __restrict__ cstart, int K, int chunk,
+                                                           int64_t max_chunks, int64_t n_out,
+                                                           int32_t* __restrict__ order) {
+  __shared__ uint16_t keys_s[kChunkOrderMax];
+  __shared__ int16_t cnt_s[kChunkOrderMaxK][kChunkBuckets];  // counts, then prefix over runs
+  __shared__ int32_t below_s[kChunkBuckets];                  // chunks of all runs in lower buckets
+  __shared__ int32_t cst_s[kChunkOrderMaxK + 1], kst_s[kChunkOrderMaxK + 1];
+  __shared__ int scan_s[17];
+  const int tid = threadIdx.x;
+  for (int t = tid; t <= K; t += 1024) {
+    cst_s[t] = cstart[t];
+    kst_s[t] = kstart[t];
+  }
+  for (int t = tid; t < K * kChunkBuckets; t += 1024) (&cnt_s[0][0])[t] = 0;
+  __syncthreads();
+  const int total = cst_s[K];
+  for (int c = tid; c < total; c += 1024) {
+    const int k = chunk_run(cst_s, K, c);
+    const int64_t p0 = kst_s[k] + (int64_t)(c - cst_s[k]) * chunk;
+    const int64_t row = pairs[2 * p0 + 1];
+    int64_t key = row * kChunkBuckets / (n_out > 0 ? n_out : 1);
+    key = key > kChunkBuckets - 1 ? kChunkBuckets - 1 : key;
+    keys_s[c] = (uint16_t)key;
+    atomicAdd(reinterpret_cast<int*>(&cnt_s[k][key & ~1]), (key & 1) ? 0x10000 : 1);  // 16-bit halves
+  }
+  __syncthreads();
+  // prefix over runs per bucket, then over buckets of the bucket totals
+  int tot = 0;
+  if (tid < kChunkBuckets)
+    for (int k = 0; k < K; ++k) {
+      const int v = cnt_s[k][tid];
+      cnt_s[k][tid] = (int16_t)tot;
+      tot += v;
+    }
+  int all;
+  const int ex = block_exclusive_scan(tid < kChunkBuckets ? tot : 0, scan_s, &all);
+  if (tid < kChunkBuckets) below_s[tid] = ex;
+  __syncthreads();
+  for (int64_t c = tid; c < max_chunks; c += 1024) {
+    if (c >= total) {
+      order[c] = (int32_t)c;
+      continue;
+    }
+    const int k = chunk_run(cst_s, K, (int)c);
+    const int key = keys_s[c];
+    int lo = cst_s[k], hi = (int)c;  // first chunk of run k with bucket >= key
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((int)keys_s[mid] < key) lo = mid + 1;
+      else hi = mid;
+    }
+    order[below_s[key] + cnt_s[k][key] + ((int)c - lo)] = (int32_t)c;
+  }
+}
+
+int launch_chunk_order(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
+                       int64_t max_chunks, int64_t n_out, int32_t* order, hipStream_t stream) {
+  if (max_chunks > kChunkOrderMax || K > kChunkOrderMaxK) return ST_ERR_UNSUPPORTED;
+  if (max_chunks == 0) return ST_OK;
+  chunk_order_kernel<<<1, 1024, 0, stream>>>(pairs, kstart, cstart, K, chunk, max_chunks, n_out, order);
+  return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
+}
+}  // namespace st
+
+extern "C" int st_kmap_pairs_chunk_order(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K,
+                                         int chunk, int64_t max_chunks, int64_t n_out, int32_t* order,
+                                         st_stream_t stream) {
+  if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0) return ST_ERR_ARG;
+  if (max_chunks > st::kChunkOrderMax) return ST_ERR_UNSUPPORTED;
+  if (max_chunks > 0 && (!pairs || !kstart || !cstart || !order)) return ST_ERR_ARG;
+  return st::launch_chunk_order(pairs, kstart, cstart, K, chunk, max_chunks, n_out, order, stream);
 }

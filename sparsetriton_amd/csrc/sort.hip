@@ -31,6 +31,8 @@
 #include "common.h"
 #include "nbr_src.h"
 
+#include <mutex>
+
 namespace st {
 
 constexpr int kRadixBits = 9;
@@ -229,40 +231,41 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(Keys in, int64_t n, 
 // Tile plan: one workgroup per 128-row destination tile (rows in perm order).
 // The union of the rows' masks gives the tile's active offsets (ascending);
 // for each of them the 128 source rows are gathered from the map once and
-// stored contiguously.  Source rows >= n_src are stored as -1.
+// stored contiguously.  Source rows >= n_src are stored as -1.  Thread t
+// serves row t % 128 and every other active offset from t / 128; its map
+// loads are issued kPlanBatch at a time before any store, so a tile costs
+// about three memory round trips (perm, mask, map) rather than one per offset.
+constexpr int kPlanBatch = 16;
 __global__ __launch_bounds__(256) void tile_plan_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
                                                         const uint32_t* __restrict__ masks, int W, int K,
                                                         const int32_t* __restrict__ perm, int64_t n_dst,
                                                         int64_t n_src, int32_t* __restrict__ tile_nk,
                                                         int16_t* __restrict__ tile_klist,
                                                         int32_t* __restrict__ tile_map) {
-  __shared__ int32_t row_s[kTileRows];
-  __shared__ uint32_t tmask_s[ST_MAX_KVOL / 32];
+  __shared__ uint32_t tmask_s[2][ST_MAX_KVOL / 32];
   __shared__ int16_t klist_s[ST_MAX_KVOL];
   __shared__ int nk_s;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r = tid & (kTileRows - 1), half = tid >> 7;
   const int64_t tile = blockIdx.x;
-  if (tid < kTileRows) {
-    const int64_t r = tile * kTileRows + tid;
-    row_s[tid] = r < n_dst ? perm[r] : -1;
-  }
-  if (tid < W) tmask_s[tid] = 0;
-  __syncthreads();
+  const int64_t gr = tile * kTileRows + r;
+  const int32_t row = gr < n_dst ? perm[gr] : -1;
   if (masks) {
+    // waves 0 and 1 hold the tile's 128 rows; waves 2 and 3 repeat them
     for (int w = 0; w < W; ++w) {
-      uint32_t v = 0;
-      if (tid < kTileRows && row_s[tid] >= 0) v = masks[(int64_t)row_s[tid] * W + w];
+      uint32_t v = (half == 0 && row >= 0) ? masks[(int64_t)row * W + w] : 0u;
       v = wave_or(v);
-      if (lane == 0 && v) atomicOr(&tmask_s[w], v);
+      if (half == 0 && lane == 0) tmask_s[wid][w] = v;
     }
   } else if (tid < W) {
-    tmask_s[tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+    tmask_s[0][tid] = (tid == W - 1 && (K & 31)) ? ((1u << (K & 31)) - 1u) : 0xFFFFFFFFu;
+    tmask_s[1][tid] = 0u;
   }
   __syncthreads();
   if (tid == 0) {
     int nk = 0;
     for (int w = 0; w < W; ++w) {
-      uint32_t bits = tmask_s[w];
+      uint32_t bits = tmask_s[0][w] | tmask_s[1][w];
       while (bits) {
         klist_s[nk++] = (int16_t)(w * 32 + __builtin_ctz(bits));
         bits &= bits - 1;
@@ -274,12 +277,19 @@ __global__ __launch_bounds__(256) void tile_plan_kernel(const int32_t* __restric
   __syncthreads();
   const int nk = nk_s;
   for (int j = tid; j < nk; j += 256) tile_klist[tile * K + j] = klist_s[j];
-  for (int e = tid; e < nk * kTileRows; e += 256) {
-    const int j = e / kTileRows, r = e - j * kTileRows;
-    const int32_t row = row_s[r];
-    int32_t v = row >= 0 ? map[(int64_t)klist_s[j] * ks + (int64_t)row * rs] : -1;
-    if ((int64_t)v >= n_src) v = -1;
-    tile_map[(tile * K + j) * kTileRows + r] = v;
+  int32_t* out = tile_map + tile * K * kTileRows + r;
+  for (int j0 = half; j0 < nk; j0 += 2 * kPlanBatch) {
+    int32_t v[kPlanBatch];
+#pragma unroll
+    for (int u = 0; u < kPlanBatch; ++u) {
+      const int j = j0 + 2 * u;
+      v[u] = (j < nk && row >= 0) ? map[(int64_t)klist_s[j] * ks + (int64_t)row * rs] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kPlanBatch; ++u) {
+      const int j = j0 + 2 * u;
+      if (j < nk) out[(int64_t)j * kTileRows] = (int64_t)v[u] >= n_src ? -1 : v[u];
+    }
   }
 }
 
@@ -297,6 +307,38 @@ extern "C" int st_kmap_sort_workspace(int64_t n, size_t* bytes) {
   return ST_OK;
 }
 
+namespace st {
+// LSD radix sort of rows by mask key into perm; buffers checked by the caller
+static int launch_sort(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp,
+                       int32_t* rows_tmp, int32_t* perm, int32_t* hist, hipStream_t stream) {
+  const int64_t tile = radix_tile(n), ntiles = (n + tile - 1) / tile;
+  const int passes = radix_passes(K);
+  // Values ping-pong between rows_tmp and perm; start so the last pass lands in perm.
+  int32_t* vbuf[2] = {(passes % 2) ? rows_tmp : perm, (passes % 2) ? perm : rows_tmp};
+  uint32_t* kbuf[2] = {keys_tmp, keys_tmp + n};
+  int32_t* totals = hist + kRadixBins * ntiles;
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * kRadixBits;
+    const int in = p & 1, out = in ^ 1;
+    uint32_t* kout = p + 1 < passes ? kbuf[out] : nullptr;
+    // the first pass computes the keys from the masks; later ones read the previous pass's output
+    const Keys ks = p == 0 ? Keys{nullptr, nullptr, masks, mask_words, K == 27} : Keys{kbuf[in], vbuf[in], nullptr, 0, 0};
+    if (tile == kRadixTileSmall)
+      radix_hist_kernel<kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles, hist);
+    else
+      radix_hist_kernel<kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles, hist);
+    radix_colscan_kernel<<<kRadixBins / 4, 256, 0, stream>>>(hist, ntiles, totals);
+    if (tile == kRadixTileSmall)
+      radix_scatter_kernel<kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles, hist,
+                                                                                          totals, kout, vbuf[out]);
+    else
+      radix_scatter_kernel<kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles, hist,
+                                                                                          totals, kout, vbuf[out]);
+  }
+  return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
+}
+}  // namespace st
+
 extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp,
                                  int32_t* rows_tmp, int32_t* perm, void* workspace, size_t workspace_bytes,
                                  st_stream_t stream) {
@@ -305,35 +347,7 @@ extern "C" int st_kmap_sort_rows(const uint32_t* masks, int mask_words, int K, i
   if (!masks || !keys_tmp || !rows_tmp || !perm || !workspace) return ST_ERR_ARG;
   const int64_t tile = st::radix_tile(n), ntiles = (n + tile - 1) / tile;
   if (workspace_bytes < (size_t)(st::kRadixBins * (ntiles + 1)) * sizeof(int32_t)) return ST_ERR_ARG;
-  const int passes = st::radix_passes(K);
-  // Values ping-pong between rows_tmp and perm; start so the last pass lands in perm.
-  int32_t* vbuf[2] = {(passes % 2) ? rows_tmp : perm, (passes % 2) ? perm : rows_tmp};
-  uint32_t* kbuf[2] = {keys_tmp, keys_tmp + n};
-  int32_t* hist = (int32_t*)workspace;
-  int32_t* totals = hist + st::kRadixBins * ntiles;
-  for (int p = 0; p < passes; ++p) {
-    const int shift = p * st::kRadixBits;
-    const int in = p & 1, out = in ^ 1;
-    uint32_t* kout = p + 1 < passes ? kbuf[out] : nullptr;
-    // the first pass computes the keys from the masks; later ones read the previous pass's output
-    const st::Keys ks = p == 0 ? st::Keys{nullptr, nullptr, masks, mask_words, K == 27}
-                               : st::Keys{kbuf[in], vbuf[in], nullptr, 0, 0};
-    if (tile == st::kRadixTileSmall)
-      st::radix_hist_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles,
-                                                                                             hist);
-    else
-      st::radix_hist_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles,
-                                                                                             hist);
-    st::radix_colscan_kernel<<<st::kRadixBins / 4, 256, 0, stream>>>(hist, ntiles, totals);
-    if (tile == st::kRadixTileSmall)
-      st::radix_scatter_kernel<st::kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(
-          ks, n, shift, ntiles, hist, totals, kout, vbuf[out]);
-    else
-      st::radix_scatter_kernel<st::kRadixTileLarge / 256><<<(unsigned)ntiles, 256, 0, stream>>>(
-          ks, n, shift, ntiles, hist, totals, kout, vbuf[out]);
-  }
-  ST_CHECK_LAUNCH();
-  return ST_OK;
+  return st::launch_sort(masks, mask_words, K, n, keys_tmp, rows_tmp, perm, (int32_t*)workspace, stream);
 }
 
 extern "C" int st_tile_plan(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks,
@@ -348,5 +362,152 @@ extern "C" int st_tile_plan(const int32_t* map, int64_t map_k_stride, int64_t ma
                                                              (K + 31) / 32, K, perm, n_dst, n_src, tile_nk,
                                                              tile_klist, tile_map);
   ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
+// ------------------------------------------------------------ whole plan
+
+namespace {
+
+constexpr int64_t kAlign = 256;
+inline int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct PlanScratch {
+  int64_t sort_keys, sort_rows, sort_hist, pair_counts, ck_keys, ck_tmp, ck_rows, ck_hist, bytes;
+};
+
+int64_t sort_hist_bytes(int64_t n) {
+  const int64_t tile = st::radix_tile(n), ntiles = (n + tile - 1) / tile;
+  return (int64_t)st::kRadixBins * ((ntiles > 0 ? ntiles : 1) + 1) * (int64_t)sizeof(int32_t);
+}
+
+PlanScratch plan_scratch(int64_t n, int K, int64_t max_chunks) {
+  PlanScratch s{};
+  int64_t at = 0;
+  s.sort_keys = at, at = align_up(at + 8 * n);
+  s.sort_rows = at, at = align_up(at + 4 * n);
+  s.sort_hist = at, at = align_up(at + sort_hist_bytes(n));
+  const int64_t nb = (n + st::kPairRows - 1) / st::kPairRows;
+  s.pair_counts = at, at = align_up(at + 4 * ((int64_t)K * nb + 1));
+  s.ck_keys = s.ck_tmp = s.ck_rows = s.ck_hist = at;
+  if (max_chunks > st::kChunkOrderMax || K > st::kChunkOrderMaxK) {  // chunk order by keys + radix sort
+    s.ck_keys = at, at = align_up(at + 4 * max_chunks);
+    s.ck_tmp = at, at = align_up(at + 8 * max_chunks);
+    s.ck_rows = at, at = align_up(at + 4 * max_chunks);
+    s.ck_hist = at, at = align_up(at + sort_hist_bytes(max_chunks));
+  }
+  s.bytes = at > 0 ? at : kAlign;
+  return s;
+}
+
+bool plan_layout(int64_t n, int K, int chunk, int64_t* L) {
+  if (n < 0 || n >= (1ll << 31) || K <= 0 || K > ST_MAX_KVOL || chunk < 0) return false;
+  if ((int64_t)K * n >= (1ll << 31)) return false;
+  const int64_t tiles = (n + st::kTileRows - 1) / st::kTileRows;
+  const int64_t mc = chunk > 0 ? (int64_t)K * n / chunk + K : 0;
+  int64_t at = 0;
+  L[ST_PLAN_PERM] = at, at = align_up(at + 4 * n);
+  L[ST_PLAN_TILE_NK] = at, at = align_up(at + 4 * tiles);
+  L[ST_PLAN_TILE_KLIST] = at, at = align_up(at + 2 * tiles * K);
+  L[ST_PLAN_TILE_MAP] = at, at = align_up(at + 4 * tiles * K * st::kTileRows);
+  L[ST_PLAN_PAIRS] = at, at = align_up(at + (chunk > 0 ? 8 * (int64_t)K * n : 0));
+  L[ST_PLAN_KSTART] = at, at = align_up(at + (chunk > 0 ? 4 * (K + 1) : 0));
+  L[ST_PLAN_CSTART] = at, at = align_up(at + (chunk > 0 ? 4 * (K + 1) : 0));
+  L[ST_PLAN_CORDER] = at, at = align_up(at + 4 * mc);
+  L[ST_PLAN_BYTES] = at > 0 ? at : kAlign;
+  L[ST_PLAN_SCRATCH_BYTES] = plan_scratch(n, K, mc).bytes;
+  L[ST_PLAN_TILES] = tiles;
+  L[ST_PLAN_MAX_CHUNKS] = mc;
+  return true;
+}
+
+// One side stream and a fork / join event pair per device, created on first use.
+constexpr int kMaxDevices = 64;
+struct SideStream {
+  std::mutex mu;
+  bool init = false, ok = false;
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+SideStream g_side[kMaxDevices];
+
+}  // namespace
+
+extern "C" int st_kmap_plans_layout(int64_t n_dst, int K, int chunk, int64_t* layout) {
+  if (!layout) return ST_ERR_ARG;
+  return plan_layout(n_dst, K, chunk, layout) ? ST_OK : ST_ERR_ARG;
+}
+
+extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks,
+                             int K, int64_t n_dst, int64_t n_src, int chunk, void* plan, void* scratch,
+                             st_stream_t stream) {
+  int64_t L[ST_PLAN_FIELDS];
+  if (!plan_layout(n_dst, K, chunk, L) || n_src < 0) return ST_ERR_ARG;
+  if (n_dst == 0 && chunk == 0) return ST_OK;
+  if (!plan || !scratch || (n_dst > 0 && (!map || !row_masks))) return ST_ERR_ARG;
+  const int W = (K + 31) / 32;
+  char* pb = (char*)plan;
+  char* sb = (char*)scratch;
+  const PlanScratch S = plan_scratch(n_dst, K, L[ST_PLAN_MAX_CHUNKS]);
+  int32_t* perm = (int32_t*)(pb + L[ST_PLAN_PERM]);
+
+  SideStream* side = nullptr;
+  std::unique_lock<std::mutex> lock;
+  if (chunk > 0) {
+    int dev = 0;
+    ST_CHECK_HIP(hipGetDevice(&dev));
+    if (dev >= 0 && dev < kMaxDevices) {
+      SideStream& s = g_side[dev];
+      lock = std::unique_lock<std::mutex>(s.mu);
+      if (!s.init) {
+        s.init = true;
+        s.ok = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) == hipSuccess &&
+               hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) == hipSuccess &&
+               hipEventCreateWithFlags(&s.join, hipEventDisableTiming) == hipSuccess;
+      }
+      if (s.ok) side = &s;
+    }
+  }
+  hipStream_t ps = stream;  // the pair list's stream
+  if (side) {
+    ST_CHECK_HIP(hipEventRecord(side->fork, stream));
+    ST_CHECK_HIP(hipStreamWaitEvent(side->stream, side->fork, 0));
+    ps = side->stream;
+  }
+  if (chunk > 0) {
+    const int64_t nb = (n_dst + st::kPairRows - 1) / st::kPairRows;
+    int32_t* pairs = (int32_t*)(pb + L[ST_PLAN_PAIRS]);
+    int32_t* kstart = (int32_t*)(pb + L[ST_PLAN_KSTART]);
+    int32_t* cstart = (int32_t*)(pb + L[ST_PLAN_CSTART]);
+    int32_t* corder = (int32_t*)(pb + L[ST_PLAN_CORDER]);
+    const int64_t mc = L[ST_PLAN_MAX_CHUNKS];
+    int rc = st::launch_pairs(map, map_k_stride, map_r_stride, n_dst, K, n_src, (int32_t*)(sb + S.pair_counts), nb,
+                              chunk, kstart, cstart, pairs, ps);
+    if (rc == ST_OK) {
+      if (mc <= st::kChunkOrderMax && K <= st::kChunkOrderMaxK) {
+        rc = st::launch_chunk_order(pairs, kstart, cstart, K, chunk, mc, n_dst, corder, ps);
+      } else {
+        uint32_t* ck = (uint32_t*)(sb + S.ck_keys);
+        rc = st::launch_chunk_keys(pairs, kstart, cstart, K, chunk, mc, n_dst, ck, ps);
+        if (rc == ST_OK)
+          rc = st::launch_sort(ck, 1, 9, mc, (uint32_t*)(sb + S.ck_tmp), (int32_t*)(sb + S.ck_rows), corder,
+                               (int32_t*)(sb + S.ck_hist), ps);
+      }
+    }
+    if (rc != ST_OK) return rc;
+  }
+  if (n_dst > 0) {
+    const int rc = st::launch_sort(row_masks, W, K, n_dst, (uint32_t*)(sb + S.sort_keys), (int32_t*)(sb + S.sort_rows),
+                                   perm, (int32_t*)(sb + S.sort_hist), stream);
+    if (rc != ST_OK) return rc;
+    st::tile_plan_kernel<<<(unsigned)L[ST_PLAN_TILES], 256, 0, stream>>>(
+        map, map_k_stride, map_r_stride, row_masks, W, K, perm, n_dst, n_src, (int32_t*)(pb + L[ST_PLAN_TILE_NK]),
+        (int16_t*)(pb + L[ST_PLAN_TILE_KLIST]), (int32_t*)(pb + L[ST_PLAN_TILE_MAP]));
+    ST_CHECK_LAUNCH();
+  }
+  if (side) {
+    ST_CHECK_HIP(hipEventRecord(side->join, side->stream));
+    ST_CHECK_HIP(hipStreamWaitEvent(stream, side->join, 0));
+  }
   return ST_OK;
 }

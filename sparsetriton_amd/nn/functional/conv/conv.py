@@ -184,14 +184,13 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
         if out_coords.shape[0] == 0:
             _raise_table_errors(table_status, in_table)
             return _empty(tensor, C_out, new_shape)
+        if hit is None and torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
+            # the weight gradient's pair list is built with the tile plan, alongside it
+            kmap.forward_tiles(with_pairs=True)
         if epilogue is not None:
             out_feats = conv_forward_epilogue(tensor.F, weight, kmap, bias, *epilogue)
         else:
             out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap, bias)
-        if hit is None and torch.is_grad_enabled() and (tensor.F.requires_grad or weight.requires_grad):
-            # the weight gradient's pair list on a side stream, queued after the forward (which
-            # needs the tile plan first) and running alongside it
-            kmap.start_pair_list()
     elif algo == ConvAlgo.ImplicitHashFlyGEMM:
         hkey = ("hashfly",) + cache_key
         hit = tensor._cache.kmaps.get(hkey)

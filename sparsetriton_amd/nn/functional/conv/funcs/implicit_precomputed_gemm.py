@@ -65,8 +65,8 @@ def gather_gemm_tiled(A: torch.Tensor, tiles, Bt: torch.Tensor, n_dst: int, K: i
     Kd = A.shape[1]
     Nd = Bt.shape[1]
     out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
-    _lib.call("st_gather_gemm_tiled", _lib.ptr(A), A.shape[0], _lib.ptr(tiles.perm), _lib.ptr(tiles.nk),
-              _lib.ptr(tiles.klist), _lib.ptr(tiles.tmap), _lib.ptr(Bt), _lib.ptr(bias), _lib.ptr(out), n_dst, K,
+    _lib.call("st_gather_gemm_tiled", _lib.ptr(A), A.shape[0], tiles.perm_ptr, tiles.nk_ptr,
+              tiles.klist_ptr, tiles.tmap_ptr, _lib.ptr(Bt), _lib.ptr(bias), _lib.ptr(out), n_dst, K,
               Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
     return out
 
@@ -104,8 +104,8 @@ def conv_forward_epilogue(features: torch.Tensor, weights: torch.Tensor, kmap: K
         res = residual.detach().to(A.dtype).contiguous()
     tiles = kmap.forward_tiles()
     out = torch.empty((kmap.n_out, C_out), dtype=A.dtype, device=A.device)
-    _lib.call("st_gather_gemm_tiled_epilogue", _lib.ptr(A), N_in, _lib.ptr(tiles.perm), _lib.ptr(tiles.nk),
-              _lib.ptr(tiles.klist), _lib.ptr(tiles.tmap), _lib.ptr(wt), _lib.ptr(b), _lib.ptr(sc), _lib.ptr(sh),
+    _lib.call("st_gather_gemm_tiled_epilogue", _lib.ptr(A), N_in, tiles.perm_ptr, tiles.nk_ptr,
+              tiles.klist_ptr, tiles.tmap_ptr, _lib.ptr(wt), _lib.ptr(b), _lib.ptr(sc), _lib.ptr(sh),
               _lib.ptr(res), int(bool(relu)), _lib.ptr(out), kmap.n_out, K, C_in, C_out,
               _lib.compute_code(A.dtype), _lib.stream_of(A.device))
     return out
@@ -153,8 +153,8 @@ def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dt
     pl = kmap.pair_list()
     partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
     dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
-    _lib.call("st_wgrad_pairs", _lib.ptr(X), X.shape[0], _lib.ptr(dY), dY.shape[0], _lib.ptr(pl.pairs),
-              _lib.ptr(pl.kstart), _lib.ptr(pl.cstart), K, pl.chunk, pl.max_chunks, _lib.ptr(pl.corder), C_in, C_out,
+    _lib.call("st_wgrad_pairs", _lib.ptr(X), X.shape[0], _lib.ptr(dY), dY.shape[0], pl.pairs_ptr,
+              pl.kstart_ptr, pl.cstart_ptr, K, pl.chunk, pl.max_chunks, pl.corder_ptr, C_in, C_out,
               _lib.compute_code(X.dtype),
               _lib.ptr(partials), _lib.ptr(dW), _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
     return dW

@@ -39,7 +39,9 @@ __all__ = [
     "subm_kernel_map",
     "row_representatives",
     "TilePlan",
+    "TileMap",
     "PairList",
+    "MapPlan",
     "out_spatial_shape",
 ]
 
@@ -149,13 +151,6 @@ class KernelMap:
         self._fwd_tiles = None
         self._bwd_tiles = None
         self._pairs = {}
-        self._pairs_ready = {}  # chunk -> event of a pair list being built on the side stream
-        # the map is complete on the creating stream once this event has passed, so side-stream
-        # work can start before whatever the creating stream queues after it
-        self._built = None
-        if nbr.is_cuda:
-            self._built = torch.cuda.Event()
-            self._built.record(torch.cuda.current_stream(nbr.device))
 
     @classmethod
     def from_neighbor_indices(cls, neighbor_indices: torch.Tensor, n_in: int) -> "KernelMap":
@@ -256,19 +251,26 @@ class KernelMap:
         return self
 
     # ------------------------------------------------------------ GEMM plans
-    def forward_plan(self) -> "TilePlan":
-        """Mask-sorted order of the output rows (forward)."""
-        if self._fwd is None:
-            self.ensure_out_masks()
-            self._fwd = TilePlan.build(self.n_out, self.K, self.out_masks)
-        return self._fwd
+    def _build_plans(self, chunk: int) -> None:
+        """Row order + tile plan of the forward (and with chunk > 0 the pair list and its chunk
+        order, on the library's side stream, joined back before the call's work ends): one
+        ``st_kmap_plans`` call over one buffer."""
+        self.ensure_out_masks()
+        plan = MapPlan.build(self.nbr, self.k_stride, self.r_stride, self.out_masks, self.K, self.n_out, self.n_in,
+                             chunk)
+        self._fwd_tiles = plan.tiles
+        if chunk > 0:
+            self._pairs[chunk] = plan.pairs
 
-    def forward_tiles(self) -> "TileMap":
-        """Tile plan of the forward gather-GEMM (offsets and source rows per 128-row tile)."""
+    def forward_plan(self) -> "TileMap":
+        """Mask-sorted order of the output rows (forward): ``.perm`` of the forward tile plan."""
+        return self.forward_tiles()
+
+    def forward_tiles(self, with_pairs: bool = False) -> "TileMap":
+        """Tile plan of the forward gather-GEMM (offsets and source rows per 128-row tile); with
+        ``with_pairs`` the weight gradient's pair list is built in the same call."""
         if self._fwd_tiles is None:
-            plan = self.forward_plan()
-            self._fwd_tiles = TileMap.build(self.nbr, self.k_stride, self.r_stride, self.out_masks, self.K,
-                                            plan.perm, self.n_out, self.n_in)
+            self._build_plans(_PAIR_CHUNK if with_pairs and _PAIR_CHUNK not in self._pairs else 0)
         return self._fwd_tiles
 
     def backward_tiles(self) -> "TileMap":
@@ -276,63 +278,32 @@ class KernelMap:
         if self.symmetric:
             return self.forward_tiles()
         if self._bwd_tiles is None:
-            plan = self.backward_plan()
-            self._check_transposable()
-            self._bwd_tiles = TileMap.build(self.invnbr, self.n_in, 1, self.in_masks, self.K, plan.perm, self.n_in,
-                                            self.n_out)
-        return self._bwd_tiles
-
-    def backward_plan(self) -> "TilePlan":
-        """Mask-sorted order of the input rows over the transposed map (input gradient)."""
-        if self.symmetric:
-            return self.forward_plan()
-        if self._bwd is None:
             self.ensure_inverse()
             self._check_transposable()
-            self._bwd = TilePlan.build(self.n_in, self.K, self.in_masks)
-        return self._bwd
+            self._bwd_tiles = MapPlan.build(self.invnbr, self.n_in, 1, self.in_masks, self.K, self.n_in, self.n_out,
+                                            0).tiles
+        return self._bwd_tiles
+
+    def backward_plan(self) -> "TileMap":
+        """Mask-sorted order of the input rows over the transposed map (input gradient)."""
+        return self.backward_tiles()
 
     def pair_list(self, chunk: int = 2048) -> "PairList":
         """(in, out) pairs sorted by (offset, out) with equal-size chunks, for the weight gradient."""
         pl = self._pairs.get(chunk)
         if pl is None:
+            if chunk == _PAIR_CHUNK and self._fwd_tiles is None:
+                self._build_plans(chunk)
+                return self._pairs[chunk]
             pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)
             self._pairs[chunk] = pl
-        ev = self._pairs_ready.pop(chunk, None)
-        if ev is not None:
-            torch.cuda.current_stream(self.nbr.device).wait_event(ev)
         return pl
 
-    def start_pair_list(self, chunk: int = 2048) -> None:
-        """Begin building the pair list on a side stream, so it overlaps the tile plans and the
-        forward GEMM; ``pair_list()`` makes the calling stream wait for it.  The side stream
-        waits only for the map itself, so this may be called after the forward is queued."""
-        if chunk in self._pairs:
-            return
-        dev = self.nbr.device
-        main = torch.cuda.current_stream(dev)
-        side = _side_stream(dev)
-        if self._built is not None:
-            side.wait_event(self._built)
-        else:
-            side.wait_stream(main)
-        self.nbr.record_stream(side)  # read on the side stream
-        with torch.cuda.stream(side):
-            pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)
-            ev = torch.cuda.Event()
-            ev.record(side)
-        for t in (pl.pairs, pl.kstart, pl.cstart, pl.corder):
-            t.record_stream(main)  # the main stream reads them; keep the allocator from recycling early
-        self._pairs[chunk] = pl
-        self._pairs_ready[chunk] = ev
-
     def prepare(self) -> "KernelMap":
-        """Build everything forward and backward need (idempotent); the pair list is built on a
-        side stream alongside the tile plans (queued after them: host launch time is the scarcer
-        resource, and the forward needs the plans first)."""
-        self.forward_tiles()
+        """Build everything forward and backward need (idempotent): the tile plans and the pair
+        list, the latter alongside the former on a side stream."""
+        self.forward_tiles(with_pairs=True)
         self.backward_tiles()
-        self.start_pair_list()
         self.pair_list()
         return self
 
@@ -365,28 +336,73 @@ def row_representatives(coords: torch.Tensor) -> Optional[torch.Tensor]:
     return first[inv].to(torch.int32)
 
 
-_SIDE_STREAMS = {}
+_PAIR_CHUNK = 2048  # pairs per weight-gradient task
+
+# st_kmap_plans_layout fields (include/sparsetriton_amd.h)
+(_PL_PERM, _PL_TILE_NK, _PL_TILE_KLIST, _PL_TILE_MAP, _PL_PAIRS, _PL_KSTART, _PL_CSTART, _PL_CORDER, _PL_BYTES,
+ _PL_SCRATCH_BYTES, _PL_TILES, _PL_MAX_CHUNKS) = range(12)
 
 
-def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
-    """One extra stream per device (default priority) for map-building work that can overlap."""
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
-    s = _SIDE_STREAMS.get(key)
-    if s is None:
-        s = torch.cuda.Stream(device=dev)
-        _SIDE_STREAMS[key] = s
-    return s
+@functools.lru_cache(maxsize=256)
+def _plan_layout(n: int, K: int, chunk: int) -> tuple:
+    arr = (ctypes.c_int64 * 12)()
+    _lib.call("st_kmap_plans_layout", n, K, chunk, arr)
+    return tuple(arr)
+
+
+def _buf_view(buf: torch.Tensor, off: int, count: int, dtype: torch.dtype) -> torch.Tensor:
+    size = torch.tensor([], dtype=dtype).element_size()
+    return buf[off:off + count * size].view(dtype)
 
 
 class TileMap:
-    """Per-tile offsets and source rows of a gather-GEMM (``st_tile_plan``), in the tile order of
-    a ``TilePlan``: ``nk`` (ntiles), ``klist`` (ntiles, K) int16, ``tmap`` (ntiles, K, 128) int32."""
+    """Per-tile offsets and source rows of a gather-GEMM, in the tile order of the row order
+    ``perm`` (n): ``nk`` (ntiles), ``klist`` (ntiles, K) int16, ``tmap`` (ntiles, K, 128) int32.
+    ``*_ptr`` are the device addresses the GEMM entry points take; the tensors are views made
+    on first use."""
 
     def __init__(self, perm, nk, klist, tmap):
-        self.perm, self.nk, self.klist, self.tmap = perm, nk, klist, tmap
+        self._perm, self._nk, self._klist, self._tmap = perm, nk, klist, tmap
+        self.perm_ptr, self.nk_ptr, self.klist_ptr, self.tmap_ptr = (t.data_ptr() for t in (perm, nk, klist, tmap))
+
+    @classmethod
+    def in_plan(cls, buf: torch.Tensor, L: tuple, n: int, K: int) -> "TileMap":
+        tm = cls.__new__(cls)
+        tm._buf, tm._L, tm._n, tm._K = buf, L, n, K
+        tm._perm = tm._nk = tm._klist = tm._tmap = None
+        base = buf.data_ptr()
+        tm.perm_ptr, tm.nk_ptr = base + L[_PL_PERM], base + L[_PL_TILE_NK]
+        tm.klist_ptr, tm.tmap_ptr = base + L[_PL_TILE_KLIST], base + L[_PL_TILE_MAP]
+        return tm
+
+    @property
+    def perm(self) -> torch.Tensor:
+        if self._perm is None:
+            self._perm = _buf_view(self._buf, self._L[_PL_PERM], self._n, torch.int32)
+        return self._perm
+
+    @property
+    def nk(self) -> torch.Tensor:
+        if self._nk is None:
+            self._nk = _buf_view(self._buf, self._L[_PL_TILE_NK], self._L[_PL_TILES], torch.int32)
+        return self._nk
+
+    @property
+    def klist(self) -> torch.Tensor:
+        if self._klist is None:
+            self._klist = _buf_view(self._buf, self._L[_PL_TILE_KLIST], self._L[_PL_TILES] * self._K, torch.int16)
+        return self._klist
+
+    @property
+    def tmap(self) -> torch.Tensor:
+        if self._tmap is None:
+            self._tmap = _buf_view(self._buf, self._L[_PL_TILE_MAP], self._L[_PL_TILES] * self._K * _lib.TILE_ROWS,
+                                   torch.int32)
+        return self._tmap
 
     @classmethod
     def build(cls, map_t, k_stride, r_stride, masks, K, perm, n_dst, n_src) -> "TileMap":
+        """Tile plan of a given row order (``st_tile_plan``)."""
         dev = map_t.device
         nt = max((n_dst + _lib.TILE_ROWS - 1) // _lib.TILE_ROWS, 1)
         # one allocation: nk (nt) | klist (nt * K int16) | tmap (nt * K * 128), tmap on a 256-byte boundary
@@ -399,6 +415,99 @@ class TileMap:
         _lib.call("st_tile_plan", _lib.ptr(map_t), k_stride, r_stride, _lib.ptr(masks), _mask_words(K), K,
                   _lib.ptr(perm), n_dst, n_src, _lib.ptr(nk), _lib.ptr(klist), _lib.ptr(tmap), _lib.stream_of(dev))
         return cls(perm, nk, klist, tmap)
+
+
+class PairList:
+    """(in, out) int32 pairs sorted by (offset, out); ``kstart`` / ``cstart`` (K + 1) the first pair /
+    chunk of each offset; ``max_chunks`` bounds the chunk count without reading it back;
+    ``corder`` the chunk ids sorted by their first output row (the weight gradient's order)."""
+
+    def __init__(self, pairs, kstart, cstart, chunk, max_chunks, corder):
+        self._pairs, self._kstart, self._cstart, self._corder = pairs, kstart, cstart, corder
+        self.chunk, self.max_chunks = int(chunk), int(max_chunks)
+        self.pairs_ptr, self.kstart_ptr, self.cstart_ptr, self.corder_ptr = (
+            t.data_ptr() for t in (pairs, kstart, cstart, corder))
+
+    @classmethod
+    def in_plan(cls, buf: torch.Tensor, L: tuple, n: int, K: int, chunk: int) -> "PairList":
+        pl = cls.__new__(cls)
+        pl._buf, pl._L, pl._n, pl._K = buf, L, n, K
+        pl._pairs = pl._kstart = pl._cstart = pl._corder = None
+        pl.chunk, pl.max_chunks = int(chunk), int(L[_PL_MAX_CHUNKS])
+        base = buf.data_ptr()
+        pl.pairs_ptr, pl.kstart_ptr = base + L[_PL_PAIRS], base + L[_PL_KSTART]
+        pl.cstart_ptr, pl.corder_ptr = base + L[_PL_CSTART], base + L[_PL_CORDER]
+        return pl
+
+    @property
+    def pairs(self) -> torch.Tensor:
+        if self._pairs is None:
+            self._pairs = _buf_view(self._buf, self._L[_PL_PAIRS], 2 * max(self._K * self._n, 1), torch.int32)
+        return self._pairs
+
+    @property
+    def kstart(self) -> torch.Tensor:
+        if self._kstart is None:
+            self._kstart = _buf_view(self._buf, self._L[_PL_KSTART], self._K + 1, torch.int32)
+        return self._kstart
+
+    @property
+    def cstart(self) -> torch.Tensor:
+        if self._cstart is None:
+            self._cstart = _buf_view(self._buf, self._L[_PL_CSTART], self._K + 1, torch.int32)
+        return self._cstart
+
+    @property
+    def corder(self) -> torch.Tensor:
+        if self._corder is None:
+            self._corder = _buf_view(self._buf, self._L[_PL_CORDER], self.max_chunks, torch.int32)
+        return self._corder
+
+    @classmethod
+    def build(cls, map_t, k_stride, r_stride, n_out, K, n_in, chunk) -> "PairList":
+        """A pair list with its own chunk size (``st_kmap_pairs`` + its chunk order)."""
+        dev = map_t.device
+        nb = ctypes.c_int64()
+        _lib.call("st_kmap_pairs_sizes", n_out, K, ctypes.byref(nb))
+        cap = K * n_out
+        counts = torch.empty((K * nb.value + 1,), dtype=torch.int32, device=dev)
+        kstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
+        cstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
+        pairs = torch.empty((2 * max(cap, 1),), dtype=torch.int32, device=dev)
+        _lib.call("st_kmap_pairs", _lib.ptr(map_t), k_stride, r_stride, n_out, K, n_in, _lib.ptr(counts), nb.value,
+                  int(chunk), _lib.ptr(kstart), _lib.ptr(cstart), _lib.ptr(pairs), cap, _lib.stream_of(dev))
+        max_chunks = cap // int(chunk) + K
+        corder = torch.empty((max(max_chunks, 1),), dtype=torch.int32, device=dev)
+        if max_chunks <= _CHUNK_ORDER_MAX and K <= _CHUNK_ORDER_MAX_K:
+            _lib.call("st_kmap_pairs_chunk_order", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
+                      max_chunks, n_out, _lib.ptr(corder), _lib.stream_of(dev))
+        else:
+            keys = torch.empty((max_chunks, 1), dtype=torch.int32, device=dev)
+            _lib.call("st_kmap_pairs_chunk_keys", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
+                      max_chunks, n_out, _lib.ptr(keys), _lib.stream_of(dev))
+            corder = TilePlan.build(max_chunks, 9, keys).perm
+        return cls(pairs, kstart, cstart, int(chunk), max_chunks, corder)
+
+
+_CHUNK_ORDER_MAX, _CHUNK_ORDER_MAX_K = 16384, 28  # st_kmap_pairs_chunk_order's limits
+
+
+class MapPlan:
+    """The buffers of one ``st_kmap_plans`` call: ``tiles`` (TileMap) and, when built with a
+    chunk size, ``pairs`` (PairList), all views of one allocation."""
+
+    def __init__(self, tiles: TileMap, pairs: Optional[PairList]):
+        self.tiles, self.pairs = tiles, pairs
+
+    @classmethod
+    def build(cls, map_t, k_stride, r_stride, masks, K, n_dst, n_src, chunk) -> "MapPlan":
+        dev = map_t.device
+        L = _plan_layout(int(n_dst), int(K), int(chunk))
+        buf = torch.empty((L[_PL_BYTES],), dtype=torch.uint8, device=dev)
+        scratch = torch.empty((L[_PL_SCRATCH_BYTES],), dtype=torch.uint8, device=dev)
+        _lib.call("st_kmap_plans", map_t.data_ptr(), k_stride, r_stride, masks.data_ptr(), K, n_dst, n_src, chunk,
+                  buf.data_ptr(), scratch.data_ptr(), _lib.stream_of(dev))
+        return cls(TileMap.in_plan(buf, L, n_dst, K), PairList.in_plan(buf, L, n_dst, K, chunk) if chunk > 0 else None)
 
 
 @functools.lru_cache(maxsize=64)
@@ -426,35 +535,6 @@ class TilePlan:
         _lib.call("st_kmap_sort_rows", _lib.ptr(masks), W, K, n, scratch.data_ptr(), scratch.data_ptr() + 8 * n,
                   _lib.ptr(perm), scratch.data_ptr() + 12 * n, nbytes, _lib.stream_of(dev))
         return cls(perm)
-
-
-class PairList:
-    """(in, out) int32 pairs sorted by (offset, out); ``kstart`` / ``cstart`` (K + 1) the first pair /
-    chunk of each offset; ``max_chunks`` bounds the chunk count without reading it back."""
-
-    def __init__(self, pairs, kstart, cstart, chunk, max_chunks, corder=None):
-        self.pairs, self.kstart, self.cstart = pairs, kstart, cstart
-        self.chunk, self.max_chunks = chunk, max_chunks
-        self.corder = corder  # chunk ids sorted by their first output row (weight-gradient order)
-
-    @classmethod
-    def build(cls, map_t, k_stride, r_stride, n_out, K, n_in, chunk) -> "PairList":
-        dev = map_t.device
-        nb = ctypes.c_int64()
-        _lib.call("st_kmap_pairs_sizes", n_out, K, ctypes.byref(nb))
-        cap = K * n_out
-        counts = torch.empty((K * nb.value + 1,), dtype=torch.int32, device=dev)
-        kstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
-        cstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
-        pairs = torch.empty((2 * max(cap, 1),), dtype=torch.int32, device=dev)
-        _lib.call("st_kmap_pairs", _lib.ptr(map_t), k_stride, r_stride, n_out, K, n_in, _lib.ptr(counts), nb.value,
-                  int(chunk), _lib.ptr(kstart), _lib.ptr(cstart), _lib.ptr(pairs), cap, _lib.stream_of(dev))
-        max_chunks = cap // int(chunk) + K
-        keys = torch.empty((max_chunks, 1), dtype=torch.int32, device=dev)
-        _lib.call("st_kmap_pairs_chunk_keys", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
-                  max_chunks, n_out, _lib.ptr(keys), _lib.stream_of(dev))
-        corder = TilePlan.build(max_chunks, 9, keys).perm
-        return cls(pairs, kstart, cstart, int(chunk), max_chunks, corder)
 
 
 # ----------------------------------------------------------------- builders

@@ -305,6 +305,65 @@ def test_tile_plan_and_pair_list(device):
     assert np.array_equal(corder[:total], np.argsort(np.array(bucket), kind="stable"))
 
 
+def _chunk_order_ref(pairs, ks, cs, chunk, n_out, max_chunks):
+    total = int(cs[-1])
+    bucket = []
+    for cidx in range(total):
+        k = int(np.searchsorted(cs, cidx, side="right") - 1)
+        p0 = ks[k] + (cidx - cs[k]) * chunk
+        bucket.append(min(pairs[p0, 1] * 512 // n_out, 511))
+    return np.concatenate([np.argsort(np.array(bucket, dtype=np.int64), kind="stable"), np.arange(total, max_chunks)])
+
+
+@pytest.mark.parametrize("k,chunk", [(3, 2048), (3, 64), (3, 8), (5, 512)])
+def test_one_call_plans_match_the_separate_builders(device, k, chunk):
+    """st_kmap_plans (sort + tile plan on the caller's stream, pair list + chunk order on the
+    library's side stream) gives the same buffers as the separate entry points; chunk 8 has more
+    chunks, and the 5x5x5 kernel more offsets, than the one-workgroup chunk order holds (the keys +
+    radix sort route)."""
+    from sparsetriton_amd.nn.functional.conv.kmap import MapPlan, PairList, TileMap, TilePlan
+    rng = np.random.default_rng(32)
+    c = _rand_coords(rng, 5000, 24)
+    kmap = _subm(device, c, (24, 24, 24), k=k)
+    kmap.ensure_out_masks()
+    K, N = kmap.K, kmap.n_out
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):  # a caller's non-default stream
+        plan = MapPlan.build(kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, K, N, kmap.n_in, chunk)
+        perm = TilePlan.build(N, K, kmap.out_masks).perm
+        tiles = TileMap.build(kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, K, perm, N, kmap.n_in)
+        pl = PairList.build(kmap.nbr, kmap.k_stride, kmap.r_stride, N, K, kmap.n_in, chunk)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.tiles.perm, perm)
+    assert torch.equal(plan.tiles.nk, tiles.nk)
+    nt = tiles.nk.shape[0]
+    kl_a, kl_b = plan.tiles.klist.view(nt, K), tiles.klist.view(nt, K)
+    tm_a, tm_b = plan.tiles.tmap.view(nt, K, 128), tiles.tmap.view(nt, K, 128)
+    for t in range(nt):
+        n = int(tiles.nk[t])
+        assert torch.equal(kl_a[t, :n], kl_b[t, :n]) and torch.equal(tm_a[t, :n], tm_b[t, :n])
+    q = plan.pairs
+    assert q.max_chunks == pl.max_chunks and q.chunk == pl.chunk == chunk
+    assert torch.equal(q.kstart, pl.kstart) and torch.equal(q.cstart, pl.cstart)
+    P = int(pl.kstart[-1])
+    assert torch.equal(q.pairs[:2 * P], pl.pairs[:2 * P])
+    assert torch.equal(q.corder, pl.corder[:q.max_chunks])
+    ks, cs = pl.kstart.cpu().numpy(), pl.cstart.cpu().numpy()
+    ref = _chunk_order_ref(pl.pairs.cpu().numpy()[:2 * P].reshape(-1, 2), ks, cs, chunk, N, pl.max_chunks)
+    assert np.array_equal(q.corder.cpu().numpy(), ref)
+
+
+def test_one_call_plans_of_an_empty_map(device):
+    from sparsetriton_amd.nn.functional.conv.kmap import MapPlan
+    nbr = torch.empty((27, 0), dtype=torch.int32, device=device)
+    masks = torch.empty((0, 1), dtype=torch.int32, device=device)
+    plan = MapPlan.build(nbr, 0, 1, masks, 27, 0, 0, 2048)
+    torch.cuda.synchronize()
+    assert plan.pairs.kstart.cpu().tolist() == [0] * 28 and plan.pairs.cstart.cpu().tolist() == [0] * 28
+    assert plan.pairs.corder.cpu().tolist() == list(range(27))
+
+
 @pytest.mark.parametrize("k,d", [(3, 1), (5, 1), (3, 2)])
 def test_subm_map_is_its_own_transpose(device, k, d):
     """An odd-kernel submanifold map read with offsets reversed equals the explicit
