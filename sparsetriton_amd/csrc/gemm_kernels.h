@@ -30,6 +30,7 @@ namespace st {
 
 constexpr int kGemmBM = 128;
 constexpr int kSrcGroup = 32;  // offsets whose source rows are resolved into LDS at once
+constexpr int kProbeGroup = 28;  // the same for table probes (a 3x3x3 kernel in one group)
 
 template <typename T, int BN, typename Src, typename E>
 __global__ __launch_bounds__(256) void gather_gemm_kernel(const T* __restrict__ A, Src src,
@@ -454,8 +455,9 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   constexpr int CPR = KDP / VEC;
   constexpr int RPI = 64 / CPR;
   static_assert(!LINES || (CPR >= 4 && CPR <= 16 && 2 * KS * RPI == 32), "whole-line gather shape");
-  // offsets whose sources are resolved at once (fewer with the A stage, to keep 4 workgroups per CU)
-  constexpr int SG = LINES ? 8 : kSrcGroup;
+  // offsets whose sources are resolved at once (fewer with the A stage, to keep 4 workgroups per CU;
+  // a probing source resolves all of a 3x3x3 kernel's offsets in one batch)
+  constexpr int SG = Src::kProbe ? kProbeGroup : (LINES ? 8 : kSrcGroup);
   // LINES: the B tile unpadded, chunk ch of row n at ch ^ bswz(n) -- the 16
   // rows one fragment read touches land on 16 distinct 4-bank groups
   constexpr int BPITCH = LINES ? KDP : PITCH;
@@ -467,6 +469,10 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   __shared__ int16_t klist_s[ST_MAX_KVOL];
   __shared__ int32_t src_s[SG][kGemmBM];
   __shared__ int nk_s;
+  // probing sources: the group's offsets with a source in the tile (bit j) and their list
+  __shared__ uint32_t gmask_s;
+  __shared__ int8_t jl_s[Src::kProbe ? SG : 1];
+  __shared__ int gn_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
@@ -474,6 +480,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
   const int64_t row0 = tile.rt * kGemmBM;
   const int n0 = tile.ct * BN;
+  if (Src::kProbe && tid == 0) gmask_s = 0u;
 
   if (tid < kGemmBM) {
     const int64_t r = row0 + tid;
@@ -514,16 +521,63 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 
   const int32_t ld_row = drow_s[tid & (kGemmBM - 1)];
   const typename Src::RowCtx rc = src.row(ld_row >= 0 ? ld_row : 0);
-  auto resolve_group = [&](int g0) {
+  // Sources of the group's offsets into src_s; returns how many of its offsets run.  A probing
+  // source issues all its probes' first loads together (thread t: row t % 128, every other
+  // offset from t / 128), then drops the offsets no row of the tile has (jl_s lists the rest).
+  auto resolve_group = [&](int g0) -> int {
     const int ng = min(SG, nk - g0);
-    for (int j = tid >> 7; j < ng; j += 2) {
-      int32_t v;
-      if constexpr (Src::kTiled)
-        v = src.get_tile(tile.rt, g0 + j, tid & (kGemmBM - 1));
-      else
-        v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
-      if ((int64_t)v >= n_src) v = -1;
-      src_s[j][tid & (kGemmBM - 1)] = v;
+    if constexpr (Src::kProbe) {
+      constexpr int PB = (SG + 1) / 2;
+      const int half = tid >> 7, r = tid & (kGemmBM - 1);
+      uint64_t key[PB], k0[PB];
+      uint32_t slot[PB];
+      bool ok[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int j = half + 2 * u;
+        ok[u] = j < ng && ld_row >= 0 && src.prep(rc, klist_s[g0 + j], key[u], slot[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u) k0[u] = ok[u] ? src.keys[slot[u]] : ST_EMPTY_KEY;
+      uint32_t hit[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) hit[u] = ok[u] ? find_slot_from(src.keys, src.cap, key[u], slot[u], k0[u]) : ST_NO_VAL;
+      int32_t v[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) v[u] = hit[u] != ST_NO_VAL ? (int32_t)src.vals[hit[u]] : -1;
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int j = half + 2 * u;  // uniform across the wave
+        if (j < ng) {
+          const int32_t vv = (int64_t)v[u] >= n_src ? -1 : v[u];
+          src_s[j][r] = vv;
+          if (__ballot(vv >= 0) != 0ull && lane == 0) atomicOr(&gmask_s, 1u << j);
+        }
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t m = gmask_s;
+        int n = 0;
+        while (m) {
+          jl_s[n++] = (int8_t)__builtin_ctz(m);
+          m &= m - 1;
+        }
+        gn_s = n;
+        gmask_s = 0u;  // the next group's bits come after at least one more barrier
+      }
+      __syncthreads();
+      return gn_s;
+    } else {
+      for (int j = tid >> 7; j < ng; j += 2) {
+        int32_t v;
+        if constexpr (Src::kTiled)
+          v = src.get_tile(tile.rt, g0 + j, tid & (kGemmBM - 1));
+        else
+          v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+        if ((int64_t)v >= n_src) v = -1;
+        src_s[j][tid & (kGemmBM - 1)] = v;
+      }
+      return ng;
     }
   };
 
@@ -551,7 +605,8 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
   // loads of offset i (its sources must be resolved) into ring slot SL
   auto issue = [&](int i, auto slot) {
     constexpr int SL = decltype(slot)::value;
-    const int j = i % SG;
+    const int loc = i % SG;                          // position in the group's run list
+    const int j = Src::kProbe ? jl_s[loc] : loc;     // the offset's index in the group
     if constexpr (LINES) {
       bool any = false;
 #pragma unroll
@@ -577,7 +632,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
         if (s1 < 0) a_ring[SL][1][jj] = zero_frag<T>();
       }
     }
-    const int k = klist_s[i];
+    const int k = klist_s[i - loc + j];
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
       const int idx = tid + jb * 256;
@@ -644,10 +699,10 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 
   static_assert(D >= 2 && D <= 4, "ring depth 2..4");  // 2 is the one launched
   for (int g0 = 0; g0 < nk; g0 += SG) {
-    const int gn = min(SG, nk - g0);
     if (g0 > 0) __syncthreads();  // the previous group's sources are all issued
-    resolve_group(g0);
+    const int gn = resolve_group(g0);
     __syncthreads();
+    if (gn == 0) continue;  // (uniform: no row of the tile has any of the group's offsets)
     issue(g0, std::integral_constant<int, 0>());
     if constexpr (D > 2) issue(g0 + min(1, gn - 1), std::integral_constant<int, 1>());
     if constexpr (D > 3) issue(g0 + min(2, gn - 1), std::integral_constant<int, 2>());

@@ -23,6 +23,7 @@ namespace st {
 
 struct MapSrc {
   static constexpr bool kTiled = false;
+  static constexpr bool kProbe = false;
   const int32_t* __restrict__ map;
   int64_t ks, rs;
   typedef int64_t RowCtx;
@@ -37,6 +38,7 @@ struct MapSrc {
 constexpr int kTileRows = 128;
 struct TiledSrc {
   static constexpr bool kTiled = true;
+  static constexpr bool kProbe = false;
   const int32_t* __restrict__ nk;
   const int16_t* __restrict__ klist;
   const int32_t* __restrict__ tmap;
@@ -51,6 +53,7 @@ struct TiledSrc {
 template <typename CT>
 struct HashSrc {
   static constexpr bool kTiled = false;
+  static constexpr bool kProbe = true;  // get() is a table probe: callers batch prep / home-slot loads / finish
   const CT* __restrict__ coords;
   const int32_t* __restrict__ offsets;
   const uint64_t* __restrict__ keys;
@@ -74,22 +77,29 @@ struct HashSrc {
     c.z *= mul;
     return c;
   }
-  __device__ __forceinline__ int32_t get(const RowCtx& c, int k) const {
-    if (!c.ok) return -1;
+  // The key of row c's neighbour through offset k and its home slot; false when it has none.
+  __device__ __forceinline__ bool prep(const RowCtx& c, int k, uint64_t& key, uint32_t& slot) const {
+    if (!c.ok) return false;
     int64_t qx = c.x + sign * (int64_t)offsets[3 * k];
     int64_t qy = c.y + sign * (int64_t)offsets[3 * k + 1];
     int64_t qz = c.z + sign * (int64_t)offsets[3 * k + 2];
     if (div > 1) {
-      if (qx % div || qy % div || qz % div) return -1;
+      if (qx % div || qy % div || qz % div) return false;
       qx /= div;
       qy /= div;
       qz /= div;
     }
     if ((bx > 0 && (qx < 0 || qx >= bx)) || (by > 0 && (qy < 0 || qy >= by)) || (bz > 0 && (qz < 0 || qz >= bz)))
-      return -1;
+      return false;
+    if (!pack_key(c.b, qx, qy, qz, key)) return false;
+    slot = home_slot(key, cap);
+    return true;
+  }
+  __device__ __forceinline__ int32_t get(const RowCtx& c, int k) const {
     uint64_t key;
-    if (!pack_key(c.b, qx, qy, qz, key)) return -1;
-    const uint32_t s = find_slot(keys, cap, key);
+    uint32_t slot;
+    if (!prep(c, k, key, slot)) return -1;
+    const uint32_t s = find_slot_from(keys, cap, key, slot, keys[slot]);
     return s == ST_NO_VAL ? -1 : (int32_t)vals[s];
   }
 };

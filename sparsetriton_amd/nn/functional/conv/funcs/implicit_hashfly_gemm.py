@@ -15,7 +15,8 @@ trailing arguments make the backward a gather like the forward:
 ``InputGradLookup``: a table of the output coordinates and the rule that
 finds them from an input row).  Given both, the input gradient probes that
 table; without them it builds the transposed map once from the forward
-lookups.  The weight gradient always probes the input table.
+lookups.  The weight gradient probes the input table once per (row, offset)
+into a map that lives only for the backward call and walks its pair list.
 """
 
 import ctypes
@@ -26,6 +27,7 @@ from sparsetriton_amd import _lib
 from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
     gather_gemm,
     weight_prep,
+    wgrad,
     wgrad_splits,
 )
 from sparsetriton_amd.nn.functional.conv.kmap import KernelMap, row_representatives
@@ -56,7 +58,9 @@ def hashfly_gemm(A, dst_coords, offsets_i32, lk, keys, vals, Bt, n_dst):
     return out
 
 
-def hashfly_wgrad(X, dY, out_coords, offsets_i32, lk, keys, vals, dw_dtype):
+def hashfly_wgrad_probing(X, dY, out_coords, offsets_i32, lk, keys, vals, dw_dtype):
+    """Weight gradient probing the table inside the kernel (``st_hashfly_wgrad``): one probe per
+    (row, offset) per row split, partials per (offset, split)."""
     K, C_in, C_out = lk.K, X.shape[1], dY.shape[1]
     n_out = out_coords.shape[0]
     splits = wgrad_splits(n_out)
@@ -139,6 +143,18 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
         grad_output = grad_output.to(features.dtype).contiguous()
         s = ctx.lookup_stride
         grad_input = grad_weights = None
+        n_out = coords.shape[0]
+        probes = []  # the forward's lookups, probed once into a map that lives until this function returns
+
+        def probed_map() -> torch.Tensor:
+            if not probes:
+                nbr = torch.empty((K, n_out), dtype=torch.int32, device=coords.device)
+                _lib.call("st_kmap_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), n_out,
+                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
+                          _lib.ptr(nbr), n_out, 1, None, None, _lib.stream_of(coords.device))
+                probes.append(nbr)
+            return probes[0]
+
         if ctx.needs_input_grad[0]:
             w = weights.to(features.dtype).contiguous()
             gl = ctx.grad_lookup
@@ -147,16 +163,16 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
                 grad_input = hashfly_gemm(grad_output, ctx.in_coords.contiguous(), offs, lk, gl.table_keys,
                                           gl.table_values, w, N_in)
             else:
-                nbr = torch.empty((K, coords.shape[0]), dtype=torch.int32, device=coords.device)
-                _lib.call("st_kmap_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0],
-                          _lib.ptr(offs), K, s, *ctx.shape, _lib.ptr(keys), _lib.ptr(vals), keys.shape[0],
-                          _lib.ptr(nbr), coords.shape[0], 1, None, None, _lib.stream_of(coords.device))
-                kmap = KernelMap(nbr, N_in, coords.shape[0], K)
+                kmap = KernelMap(probed_map(), N_in, n_out, K)
                 kmap.set_row_representatives(row_representatives(coords))  # repeated output coordinates
                 kmap.ensure_inverse()
                 grad_input = gather_gemm(kmap.fold_output_rows(grad_output), kmap.invnbr, N_in, 1, kmap.in_masks,
                                          w, N_in, K)
         if ctx.needs_input_grad[1]:
-            lk = _lookup(K, -1, s, 1, ctx.shape)
-            grad_weights = hashfly_wgrad(features, grad_output, coords, offs, lk, keys, vals, weights.dtype)
+            # One probe per (row, offset) into the map above, compacted into the (offset, output)-sorted
+            # pair list the pair-list weight gradient walks: a probe inside the weight-gradient kernel
+            # would be repeated for every C_in x C_out tile and leaves its MFMAs waiting on the probes.
+            kmap = KernelMap(probed_map(), N_in, n_out, K)
+            grad_weights = wgrad(features, grad_output, kmap, weights.dtype,
+                                 pairs=kmap.pair_list(with_tiles=False))
         return grad_input, grad_weights, None, None, None, None, None, None, None, None

@@ -147,10 +147,11 @@ def column_sum(Y: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     return out
 
 
-def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype) -> torch.Tensor:
-    """dW[k] = sum over pairs (i, o) of offset k of X[i]^T dY[o], over the map's pair list."""
+def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype, pairs=None) -> torch.Tensor:
+    """dW[k] = sum over pairs (i, o) of offset k of X[i]^T dY[o], over the map's pair list (or
+    ``pairs``, a PairList of it)."""
     K, C_in, C_out = kmap.K, X.shape[1], dY.shape[1]
-    pl = kmap.pair_list()
+    pl = kmap.pair_list() if pairs is None else pairs
     partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
     dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
     _lib.call("st_wgrad_pairs", _lib.ptr(X), X.shape[0], _lib.ptr(dY), dY.shape[0], pl.pairs_ptr,

@@ -288,11 +288,12 @@ class KernelMap:
         """Mask-sorted order of the input rows over the transposed map (input gradient)."""
         return self.backward_tiles()
 
-    def pair_list(self, chunk: int = 2048) -> "PairList":
-        """(in, out) pairs sorted by (offset, out) with equal-size chunks, for the weight gradient."""
+    def pair_list(self, chunk: int = 2048, with_tiles: bool = True) -> "PairList":
+        """(in, out) pairs sorted by (offset, out) with equal-size chunks, for the weight gradient;
+        the default chunk size comes with the forward tile plan unless ``with_tiles`` is False."""
         pl = self._pairs.get(chunk)
         if pl is None:
-            if chunk == _PAIR_CHUNK and self._fwd_tiles is None:
+            if chunk == _PAIR_CHUNK and self._fwd_tiles is None and with_tiles:
                 self._build_plans(chunk)
                 return self._pairs[chunk]
             pl = PairList.build(self.nbr, self.k_stride, self.r_stride, self.n_out, self.K, self.n_in, chunk)

@@ -248,6 +248,30 @@ def test_hashfly_equals_precomputed(device):
     assert rel(res[0][2].cpu(), res[1][2].cpu()) < 1e-6
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_probing_weight_gradient_entry(device, dtype, tol):
+    """st_hashfly_wgrad, which probes the table inside the weight-gradient kernel (the autograd
+    path probes once into a pair list instead), against the oracle."""
+    from sparsetriton_amd.nn.functional.conv.conv import _input_table
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_hashfly_gemm import _lookup, hashfly_wgrad_probing
+    from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets
+    rng = np.random.default_rng(24)
+    c = _rand_coords(rng, 3000, 20)
+    X = rng.standard_normal((3000, 32)).astype(np.float32)
+    dY = rng.standard_normal((3000, 16)).astype(np.float32)
+    sp = SparseTensor(torch.as_tensor(X, device=device), torch.as_tensor(c, device=device),
+                      spatial_shape=(20, 20, 20), batch_size=2)
+    table = _input_table(sp, 1)
+    offs = _target_offsets(3, 1, 1, False, device).to(torch.int32).contiguous()
+    dW = hashfly_wgrad_probing(sp.F.to(dtype), torch.as_tensor(dY, device=device).to(dtype), sp.C, offs,
+                               _lookup(27, -1, 1, 1, (20, 20, 20)), table.table_keys, table.table_values,
+                               torch.float32)
+    Xr = torch.as_tensor(X).to(dtype).double().numpy()
+    dYr = torch.as_tensor(dY).to(dtype).double().numpy()
+    nbr = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, (20, 20, 20))
+    assert rel(dW.cpu(), O.wgrad_f64(Xr, dYr, nbr, 27)) < tol
+
+
 def test_deterministic(device):
     rng = np.random.default_rng(22)
     c = _rand_coords(rng, 8000, 24)
