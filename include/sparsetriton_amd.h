@@ -311,6 +311,11 @@ int st_kmap_pairs_chunk_order(const int32_t* pairs, const int32_t* kstart, const
  * used during the call's work on the GPU (stream order).
  * Row order and tiles cover the n_dst destination rows; the pairs are
  * (map[k, o], o) over the same map, o < n_dst, map entries >= n_src skipped.
+ * bucket_bits (0..8; used when K + bucket_bits <= 32): rows are first
+ * grouped into 2^bucket_bits slabs of the caller's row order (slab =
+ * row * 2^bits / n_dst) and sorted by mask within each slab, so the tiles
+ * that run together gather from one slab of input rows (more L2 reuse when
+ * the rows are in spatial order, at the cost of tiles mixing more masks).
  * No counterpart in the reference, whose GEMMs read the (N_out, K) map
  * directly (implicit_precomputed_gemm.py:64-126, 180-230).
  */
@@ -331,7 +336,8 @@ enum {
 };
 int st_kmap_plans_layout(int64_t n_dst, int K, int chunk, int64_t* layout);
 int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks, int K,
-                  int64_t n_dst, int64_t n_src, int chunk, void* plan, void* scratch, st_stream_t stream);
+                  int64_t n_dst, int64_t n_src, int chunk, int bucket_bits, void* plan, void* scratch,
+                  st_stream_t stream);
 
 /* ------------------------------------------------------------- gather-GEMM */
 

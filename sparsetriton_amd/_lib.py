@@ -77,7 +77,7 @@ _SIGNATURES = {
     "st_kmap_pairs_chunk_keys": [_P, _P, _P, _I, _I, _L, _L, _P, _P],
     "st_kmap_pairs_chunk_order": [_P, _P, _P, _I, _I, _L, _L, _P, _P],
     "st_kmap_plans_layout": [_L, _I, _I, _P],
-    "st_kmap_plans": [_P, _L, _L, _P, _I, _L, _L, _I, _P, _P, _P],
+    "st_kmap_plans": [_P, _L, _L, _P, _I, _L, _L, _I, _I, _P, _P, _P],
     "st_wgrad_pairs": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _L, _P, _I, _I, _I, _P, _P, _I, _P],
     "st_weight_prep": [_P, _P, _I, _I, _I, _I, _I, _P],
     "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],

@@ -44,6 +44,8 @@ __all__ = [
     "set_fp32_precision",
     "get_fp32_precision",
     "FP32_PRECISIONS",
+    "set_tile_slab_bits",
+    "get_tile_slab_bits",
     "MIN_TABLE_FACTOR",
 ]
 
@@ -72,6 +74,7 @@ _STATE: dict = {
     "h_tbl_factor": 1.5,
     "h_tbl_max_probe_n": 16,
     "fp32_precision": "bf16x3",
+    "tile_slab_bits": 0,
 }
 
 
@@ -139,3 +142,17 @@ def set_fp32_precision(precision: str) -> None:
 def get_fp32_precision() -> str:
     """Current fp32 matrix-core arithmetic (``"bf16x3"`` or ``"ieee"``)."""
     return _STATE["fp32_precision"]
+
+
+def set_tile_slab_bits(bits: int) -> None:
+    """Group the gather-GEMM's destination rows into 2**bits slabs of their row order before
+    sorting them by offset mask (0..8; 0 = one slab).  With rows in spatial order the tiles that
+    run together then gather from one slab of input rows, which stays in L2, at the price of
+    tiles that mix more masks.  Read when a kernel map's plans are built."""
+    bits = int(bits)
+    assert 0 <= bits <= 8, "tile slab bits must be in [0, 8]"
+    _STATE["tile_slab_bits"] = bits
+
+
+def get_tile_slab_bits() -> int:
+    return _STATE["tile_slab_bits"]

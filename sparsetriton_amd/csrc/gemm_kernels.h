@@ -1438,6 +1438,12 @@ static bool gather_lines() {
   return on == 1;
 }
 
+}  // namespace st
+
+#include "gemm_wide.h"
+
+namespace st {
+
 // Whole-line kernels address A and Bt through 32-bit buffer offsets.
 static bool buffer_ok(int64_t n_src, int K, int Kd, int Nd, size_t esz) {
   return n_src * Kd * (int64_t)esz < (1ll << 31) - 64 && (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
@@ -1483,6 +1489,13 @@ static int launch_gather_e(const T* A, int64_t n_src, const Src& src, const uint
                            hipStream_t stream) {
   constexpr int VEC = Frag<T>::VEC;
   constexpr int KSTEP = Frag<T>::KSTEP;
+  if constexpr (Src::kTiled && sizeof(T) == 2) {
+    if (gather_wide_mode() && wide_ok(Kd, Nd, K, sizeof(T), false, n_src, A, Bt)) {
+      launch_wide<T, false, E>(A, n_src, src, rows, Bt, out, epi, n_dst, Kd, Nd, stream);
+      ST_CHECK_LAUNCH();
+      return ST_OK;
+    }
+  }
   const int vec_a = (Kd % VEC == 0) && ((uintptr_t)A % 16 == 0);
   const int vec_b = (Kd % VEC == 0) && ((uintptr_t)Bt % 16 == 0);
   const int ks = (Kd + KSTEP - 1) / KSTEP;

@@ -21,26 +21,6 @@
 
 namespace st {
 
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-
-// hi/lo bf16 split of 8 consecutive fp32 values.
-__device__ __forceinline__ void split8(const v4f& x0, const v4f& x1, v8bf& hi, v8bf& lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const __bf16 h0 = (__bf16)x0[e];
-    const __bf16 h1 = (__bf16)x1[e];
-    hi[e] = h0;
-    hi[e + 4] = h1;
-    lo[e] = (__bf16)(x0[e] - (float)h0);
-    lo[e + 4] = (__bf16)(x1[e] - (float)h1);
-  }
-}
-
-__device__ __forceinline__ v4f mfma_x3(const v8bf& ah, const v8bf& al, const v8bf& bh, const v8bf& bl, v4f acc) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
-}
 
 // ------------------------------------------------------ forward / dgrad
 //
@@ -814,6 +794,13 @@ template <typename Src, typename E>
 static int launch_gather_x3_e(const float* A, int64_t n_src, const Src& src, const uint32_t* masks, int W,
                               const int32_t* rows, const float* Bt, float* out, E epi, int64_t n_dst, int K, int Kd,
                               int Nd, hipStream_t stream) {
+  if constexpr (Src::kTiled) {
+    if (gather_wide_mode() && wide_ok(Kd, Nd, K, sizeof(float), true, n_src, A, Bt)) {
+      launch_wide<float, true, E>(A, n_src, src, rows, Bt, out, epi, n_dst, Kd, Nd, stream);
+      ST_CHECK_LAUNCH();
+      return ST_OK;
+    }
+  }
   const int ks = (Kd + 31) / 32;
   if (ks > 4) {
     if constexpr (Src::kTiled)

@@ -56,6 +56,30 @@ __device__ __forceinline__ v4f mfma(const v8bf& a, const v8bf& b, v4f acc) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
 
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+
+// hi/lo bf16 split of 8 consecutive fp32 values (the split-operand fp32
+// products: x = hi + lo + d, |d| <= 2^-18 |x|).
+__device__ __forceinline__ void split8(const v4f& x0, const v4f& x1, v8bf& hi, v8bf& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const __bf16 h0 = (__bf16)x0[e];
+    const __bf16 h1 = (__bf16)x1[e];
+    hi[e] = h0;
+    hi[e + 4] = h1;
+    lo[e] = (__bf16)(x0[e] - (float)h0);
+    lo[e + 4] = (__bf16)(x1[e] - (float)h1);
+  }
+}
+
+// a*b ~= al*bh + ah*bl + ah*bh, in that order (every kernel that must agree
+// bitwise with another adds the three products in this order)
+__device__ __forceinline__ v4f mfma_x3(const v8bf& ah, const v8bf& al, const v8bf& bh, const v8bf& bl, v4f acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
 template <typename T>
 __device__ __forceinline__ typename Frag<T>::type zero_frag() {
   typename Frag<T>::type f;

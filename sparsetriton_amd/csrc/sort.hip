@@ -79,12 +79,20 @@ __device__ __forceinline__ uint32_t mask_key(const uint32_t* __restrict__ masks,
 
 // Keys of the first pass: computed from the masks (Keys::masks set, values =
 // row ids) instead of read from the key / value buffers of the previous pass.
+// With bbits > 0 the first pass also puts the row's bucket -- row * 2^bbits / n,
+// a slab of the caller's row order -- above the K mask bits.
 struct Keys {
   const uint32_t* keys;
   const int32_t* vals;
   const uint32_t* masks;
-  int W, cube3;
-  __device__ __forceinline__ uint32_t key(int64_t i) const { return masks ? mask_key(masks, W, cube3, i) : keys[i]; }
+  int W, cube3, K, bbits;
+  int64_t n;
+  __device__ __forceinline__ uint32_t key(int64_t i) const {
+    if (!masks) return keys[i];
+    uint32_t k = mask_key(masks, W, cube3, i);
+    if (bbits) k |= (uint32_t)((i << bbits) / n) << K;
+    return k;
+  }
   __device__ __forceinline__ int32_t val(int64_t i) const { return masks ? (int32_t)i : vals[i]; }
 };
 
@@ -293,8 +301,8 @@ __global__ __launch_bounds__(256) void tile_plan_kernel(const int32_t* __restric
   }
 }
 
-static int radix_passes(int K) {
-  const int bits = K < 32 ? K : 32;
+static int radix_passes(int K, int bbits = 0) {
+  const int bits = K + bbits < 32 ? K + bbits : 32;
   return (bits + kRadixBits - 1) / kRadixBits;
 }
 
@@ -310,9 +318,10 @@ extern "C" int st_kmap_sort_workspace(int64_t n, size_t* bytes) {
 namespace st {
 // LSD radix sort of rows by mask key into perm; buffers checked by the caller
 static int launch_sort(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp,
-                       int32_t* rows_tmp, int32_t* perm, int32_t* hist, hipStream_t stream) {
+                       int32_t* rows_tmp, int32_t* perm, int32_t* hist, hipStream_t stream, int bbits = 0) {
   const int64_t tile = radix_tile(n), ntiles = (n + tile - 1) / tile;
-  const int passes = radix_passes(K);
+  if (K + bbits > 32) bbits = 0;
+  const int passes = radix_passes(K, bbits);
   // Values ping-pong between rows_tmp and perm; start so the last pass lands in perm.
   int32_t* vbuf[2] = {(passes % 2) ? rows_tmp : perm, (passes % 2) ? perm : rows_tmp};
   uint32_t* kbuf[2] = {keys_tmp, keys_tmp + n};
@@ -322,7 +331,8 @@ static int launch_sort(const uint32_t* masks, int mask_words, int K, int64_t n, 
     const int in = p & 1, out = in ^ 1;
     uint32_t* kout = p + 1 < passes ? kbuf[out] : nullptr;
     // the first pass computes the keys from the masks; later ones read the previous pass's output
-    const Keys ks = p == 0 ? Keys{nullptr, nullptr, masks, mask_words, K == 27} : Keys{kbuf[in], vbuf[in], nullptr, 0, 0};
+    const Keys ks = p == 0 ? Keys{nullptr, nullptr, masks, mask_words, K == 27, K, bbits, n}
+                           : Keys{kbuf[in], vbuf[in], nullptr, 0, 0, 0, 0, 1};
     if (tile == kRadixTileSmall)
       radix_hist_kernel<kRadixTileSmall / 256><<<(unsigned)ntiles, 256, 0, stream>>>(ks, n, shift, ntiles, hist);
     else
@@ -439,10 +449,10 @@ extern "C" int st_kmap_plans_layout(int64_t n_dst, int K, int chunk, int64_t* la
 }
 
 extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, const uint32_t* row_masks,
-                             int K, int64_t n_dst, int64_t n_src, int chunk, void* plan, void* scratch,
+                             int K, int64_t n_dst, int64_t n_src, int chunk, int bucket_bits, void* plan, void* scratch,
                              st_stream_t stream) {
   int64_t L[ST_PLAN_FIELDS];
-  if (!plan_layout(n_dst, K, chunk, L) || n_src < 0) return ST_ERR_ARG;
+  if (!plan_layout(n_dst, K, chunk, L) || n_src < 0 || bucket_bits < 0 || bucket_bits > 8) return ST_ERR_ARG;
   if (n_dst == 0 && chunk == 0) return ST_OK;
   if (!plan || !scratch || (n_dst > 0 && (!map || !row_masks))) return ST_ERR_ARG;
   const int W = (K + 31) / 32;
@@ -498,7 +508,7 @@ extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t m
   }
   if (n_dst > 0) {
     const int rc = st::launch_sort(row_masks, W, K, n_dst, (uint32_t*)(sb + S.sort_keys), (int32_t*)(sb + S.sort_rows),
-                                   perm, (int32_t*)(sb + S.sort_hist), stream);
+                                   perm, (int32_t*)(sb + S.sort_hist), stream, bucket_bits);
     if (rc != ST_OK) return rc;
     st::tile_plan_kernel<<<(unsigned)L[ST_PLAN_TILES], 256, 0, stream>>>(
         map, map_k_stride, map_r_stride, row_masks, W, K, perm, n_dst, n_src, (int32_t*)(pb + L[ST_PLAN_TILE_NK]),

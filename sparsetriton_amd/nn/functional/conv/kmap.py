@@ -27,6 +27,7 @@ import functools
 import torch
 
 from sparsetriton_amd import _lib
+from sparsetriton_amd.config import get_tile_slab_bits
 from sparsetriton_amd.utils.hash import HashTable
 
 __all__ = [
@@ -507,7 +508,7 @@ class MapPlan:
         buf = torch.empty((L[_PL_BYTES],), dtype=torch.uint8, device=dev)
         scratch = torch.empty((L[_PL_SCRATCH_BYTES],), dtype=torch.uint8, device=dev)
         _lib.call("st_kmap_plans", map_t.data_ptr(), k_stride, r_stride, masks.data_ptr(), K, n_dst, n_src, chunk,
-                  buf.data_ptr(), scratch.data_ptr(), _lib.stream_of(dev))
+                  get_tile_slab_bits(), buf.data_ptr(), scratch.data_ptr(), _lib.stream_of(dev))
         return cls(TileMap.in_plan(buf, L, n_dst, K), PairList.in_plan(buf, L, n_dst, K, chunk) if chunk > 0 else None)
 
 
