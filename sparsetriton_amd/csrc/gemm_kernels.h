@@ -1051,15 +1051,20 @@ __device__ __forceinline__ F tr_frag(const T* st, int g, int c, int col0) {
 // wide: the transpose reads of a fragment touch four rows at once, which land
 // on distinct 32-byte bank groups when the row stride is 32 or 96 bytes
 // modulo 128 (16, 48 or 80 elements).
-constexpr int wave_pitch(int width) { return width == 16 ? 16 : (width == 32 ? 48 : 80); }
+constexpr int wave_pitch(int width) { return width == 16 ? 16 : (width == 32 ? 48 : (width == 64 ? 80 : 144)); }
 // Channel tile of a workgroup: TM = 16 MB input channels x TN = 16 NB output
-// channels (16, 32 or 64 each; a wave computes the whole tile).  A row's TM
-// channels are CPR = TM / 8 chunks of 16 bytes, so one load instruction
+// channels (16, 32, 64 or 128 each; a wave computes the whole tile).  A row's
+// TM channels are CPR = TM / 8 chunks of 16 bytes, so one load instruction
 // covers RPI = 64 / CPR whole rows and a 32-pair step takes 32 / RPI of them.
 // ONEPASS sums the four waves' tiles through LDS in one round (more LDS: two
 // workgroups per CU for a 64 x 64 tile) instead of rounds of 32 rows (three).
+// A 128-wide side (BIG) halves the LDS bytes per MFMA of the 64 x 64 tile --
+// every staged row and every fragment read serves twice the MFMAs, the
+// LDS-bound part of this kernel -- at one workgroup per CU (the 128 x 128
+// accumulators take the AGPRs); its pair indices are then loaded a step ahead
+// as with ONEPASS.
 template <typename T, bool BUF, int MB, int NB, bool ONEPASS>  // BUF: row loads through buffer resources (X and dY under 2 GB)
-__global__ __launch_bounds__(256, ONEPASS ? 2 : 3) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
+__global__ __launch_bounds__(256, (MB > 4 || NB > 4) ? 1 : (ONEPASS ? 2 : 3)) void wgrad_pairs_wave_kernel(const T* __restrict__ X, const T* __restrict__ dY,
                                                                const int2* __restrict__ pairs,
                                                                const int32_t* __restrict__ kstart,
                                                                const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
@@ -1067,6 +1072,9 @@ __global__ __launch_bounds__(256, ONEPASS ? 2 : 3) void wgrad_pairs_wave_kernel(
                                                                int Cin, int Cout, int64_t n_in, int64_t n_out, float* __restrict__ partials) {
   using F = typename Frag<T>::type;
   static_assert(Frag<T>::KSTEP == 32 && Frag<T>::VEC == 8, "16-bit MFMA fragments");
+  constexpr bool BIG = MB > 4 || NB > 4;
+  constexpr bool PREFETCH = ONEPASS || BIG;  // pair indices one step ahead of their rows
+  static_assert(!(ONEPASS && BIG), "a 128-wide tile sums in rounds");
   constexpr int TM = 16 * MB, TN = 16 * NB;
   constexpr int CPRX = TM / 8, RPIX = 64 / CPRX, NVX = 32 / RPIX;
   constexpr int CPRY = TN / 8, RPIY = 64 / CPRY, NVY = 32 / RPIY;
@@ -1138,7 +1146,7 @@ __global__ __launch_bounds__(256, ONEPASS ? 2 : 3) void wgrad_pairs_wave_kernel(
     int q = p0 + wid * 32;
     int2 prn = load_pairs(q);
     if (q < p1) load_rows(prn);
-    if constexpr (ONEPASS) prn = load_pairs(q + 128);
+    if constexpr (PREFETCH) prn = load_pairs(q + 128);
     for (; q < p1; q += 128) {
 #pragma unroll
       for (int v = 0; v < (NVX > NVY ? NVX : NVY); ++v) {
@@ -1151,7 +1159,7 @@ __global__ __launch_bounds__(256, ONEPASS ? 2 : 3) void wgrad_pairs_wave_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (q + 128 < p1) {
-        if constexpr (ONEPASS) {
+        if constexpr (PREFETCH) {
           load_rows(prn);
           prn = load_pairs(q + 256);
         } else {
@@ -1623,24 +1631,27 @@ static bool rows_fit_buffer(int64_t n_in, int Cin, int64_t n_out, int Cout, size
   return n_in * Cin * (int64_t)esz < (1ll << 31) - 64 && n_out * Cout * (int64_t)esz < (1ll << 31) - 64;
 }
 
-// 16-channel blocks of the per-wave weight-gradient tile for C channels: 1, 2
-// or 4 (C = 16, 32 or a multiple of 64), 0 when the kernel does not cover C.
-static int wave_tile_blocks(int C) {
-  if (C % 64 == 0) return 4;
-  if (C == 32) return 2;
-  if (C == 16) return 1;
-  return 0;
-}
-
 // 16-bit weight-gradient kernel: 0 = per-wave steps (default), 1 = workgroup
-// LDS transpose (ST_WGRAD16=lds selects it, for comparison runs).
+// LDS transpose (ST_WGRAD16=lds), 2 = per-wave steps with tiles of at most
+// 64 x 64 channels (ST_WGRAD16=small); the last two for comparison runs.
 static int wgrad16_mode() {
   static int mode = -1;
   if (mode < 0) {
     const char* e = getenv("ST_WGRAD16");
-    mode = (e && e[0] == 'l') ? 1 : 0;
+    mode = (e && e[0] == 'l') ? 1 : (e && e[0] == 's') ? 2 : 0;
   }
   return mode;
+}
+
+// 16-channel blocks of the per-wave weight-gradient tile for C channels: 1, 2,
+// 4 or 8 (C = 16, 32, a multiple of 64, a multiple of 128), 0 when the kernel
+// does not cover C.
+static int wave_tile_blocks(int C) {
+  if (C % 128 == 0 && wgrad16_mode() != 2) return 8;
+  if (C % 64 == 0) return 4;
+  if (C == 32) return 2;
+  if (C == 16) return 1;
+  return 0;
 }
 
 template <typename T>
@@ -1665,8 +1676,10 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
       const unsigned gx = wgrad_grid(max_chunks);
       const int2* pr = reinterpret_cast<const int2*>(pairs);
       const int mode = wgrad16_mode();
-      const int mb = wave_tile_blocks(Cin), nb = wave_tile_blocks(Cout);
-      if (mode == 0 && mb && nb && vec_x && vec_y) {
+      int mb = wave_tile_blocks(Cin), nb = wave_tile_blocks(Cout);
+      if (mb == 8 && nb < 4) mb = 4;  // a 128-wide side only beside a side of 64 or more
+      if (nb == 8 && mb < 4) nb = 4;
+      if (mode != 1 && mb && nb && vec_x && vec_y) {
         const unsigned grid = gx * (unsigned)((Cin / (16 * mb)) * (Cout / (16 * nb)));
         const bool buf = rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T));
         // A 64 x 64 tile with its cross-wave sum in 32-row rounds fits three
@@ -1676,12 +1689,12 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
         const bool onepass = grid <= 1024;
 #define ST_WAVE(MB_, NB_)                                                                                         \
   if (mb == MB_ && nb == NB_) {                                                                                   \
-    if (onepass && MB_ == 4) {                                                                                    \
+    if (onepass && MB_ == 4 && NB_ <= 4) {                                                                        \
       if (buf)                                                                                                    \
-        wgrad_pairs_wave_kernel<T, true, MB_, NB_, true><<<grid, 256, 0, stream>>>(                               \
+        wgrad_pairs_wave_kernel<T, true, MB_, NB_, (MB_ <= 4 && NB_ <= 4)><<<grid, 256, 0, stream>>>(                         \
             X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                 \
       else                                                                                                        \
-        wgrad_pairs_wave_kernel<T, false, MB_, NB_, true><<<grid, 256, 0, stream>>>(                              \
+        wgrad_pairs_wave_kernel<T, false, MB_, NB_, (MB_ <= 4 && NB_ <= 4)><<<grid, 256, 0, stream>>>(                        \
             X, dY, pr, kstart, cstart, chunk_order, K, chunk, Cin, Cout, n_in, n_out, partials);                 \
     } else if (buf) {                                                                                             \
       wgrad_pairs_wave_kernel<T, true, MB_, NB_, false><<<grid, 256, 0, stream>>>(                                \
@@ -1692,7 +1705,7 @@ int ops_wgrad_pairs(const T* X, int64_t n_in, const T* dY, int64_t n_out, const 
     }                                                                                                             \
   }
         ST_WAVE(1, 1) ST_WAVE(1, 2) ST_WAVE(1, 4) ST_WAVE(2, 1) ST_WAVE(2, 2) ST_WAVE(2, 4) ST_WAVE(4, 1)
-        ST_WAVE(4, 2) ST_WAVE(4, 4)
+        ST_WAVE(4, 2) ST_WAVE(4, 4) ST_WAVE(4, 8) ST_WAVE(8, 4) ST_WAVE(8, 8)
 #undef ST_WAVE
         ST_CHECK_LAUNCH();
         return launch_wgrad_reduce(partials, cstart, 0, K, Cin, Cout, dW, dw_dtype, stream);
