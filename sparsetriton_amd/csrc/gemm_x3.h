@@ -644,7 +644,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, BUF ? n_in * Cin * 4 : 0);
   const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, BUF ? n_out * Cout * 4 : 0);
 
-  for (int cq = ct.q0; cq < ct.q1; ++cq) {
+  for (int cq = ct.q0; cq < ct.q1; cq += ct.step) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
     const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
