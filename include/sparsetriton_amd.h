@@ -82,6 +82,17 @@ int st_fill_u64(uint64_t* dst, int64_t n, uint64_t value, st_stream_t stream);
 /* -------------------------------------------------------- coordinate hash */
 
 /*
+ * Probe style of st_hash_insert, st_hash_query and st_kmap_query: 0 = one
+ * thread per key, linear probing with several keys' first loads in flight
+ * (default); 1 = a 16-lane group per key, lane j loading slot s + j of a
+ * 16-slot window and one ballot finding the first matching or empty slot.
+ * Same table, same results; kept for timing comparisons.  mode -1 only
+ * reads.  Returns the mode before the call.  No counterpart in the
+ * reference, whose probes are per thread (utils/hash.py:174-299).
+ */
+int st_hash_probe_mode(int mode);
+
+/*
  * Replaces HashTable.insert -> build_hash_table_kernel (utils/hash.py:193-258, 516-544).
  * Inserts the n rows of coords (n, 4) = (b, x, y, z), x/y/z multiplied by
  * `scale` (1 normally; the stride for the transposed-conv table that

@@ -60,6 +60,7 @@ _SIGNATURES = {
     "st_version": [],
     "st_fill_u32": [_P, _L, ctypes.c_uint32, _P],
     "st_fill_u64": [_P, _L, ctypes.c_uint64, _P],
+    "st_hash_probe_mode": [_I],
     "st_hash_insert": [_P, _I, _L, _L, _P, _P, _L, _P, _P],
     "st_hash_query": [_P, _I, _L, _P, _P, _L, _P, _P],
     "st_kmap_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, _P, _L, _L, _P, _P, _P],

@@ -111,3 +111,47 @@ def test_empty(device):
     t = HashTable(capacity=4, device=device)
     t.insert(torch.empty((0, 4), dtype=torch.int16, device=device))
     assert t.query(torch.empty((0, 4), dtype=torch.int16, device=device)).shape == (0,)
+
+
+@pytest.fixture
+def group_probes():
+    """Switch the table's probes to 16-lane groups for one test (st_hash_probe_mode)."""
+    from sparsetriton_amd import _lib
+    fn = _lib.lib().st_hash_probe_mode
+    prev = fn(1)
+    yield
+    fn(prev)
+
+
+def test_group_probes_exact(device, group_probes):
+    """The 16-lane group probes (insert, query, kernel-map query) give the per-thread probes'
+    answers: exact lookups, duplicates counted, a full table terminating, the map bit-exact."""
+    from oracle import oracle as O
+    from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets, query_kernel_map
+    rng = np.random.default_rng(12)
+    n = 100_000
+    lin = rng.choice(2 * 256 * 256 * 32, n, replace=False)
+    c = np.stack([lin // (256 * 256 * 32), (lin // (256 * 32)) % 256, (lin // 32) % 256, lin % 32], 1)
+    miss = np.stack([rng.integers(0, 2, n), rng.integers(0, 256, n), rng.integers(0, 256, n),
+                     rng.integers(32, 64, n)], 1)
+    t = HashTable(capacity=2 * n, device=device)
+    t.insert(torch.as_tensor(np.concatenate([c, c[:500]]), dtype=torch.int32, device=device))
+    assert t.counters()["duplicate"] == 500
+    got = t.query(torch.as_tensor(np.concatenate([c, miss]), dtype=torch.int32, device=device)).cpu().numpy()
+    assert (got == np.concatenate([np.arange(n), np.full(n, -1)])).all()
+    full = HashTable(capacity=10, device=device)
+    cf = torch.tensor([[0, i, 0, 0] for i in range(15)], dtype=torch.int32, device=device)
+    full.insert(cf[:10])
+    assert full.counters()["overflow"] == 0
+    assert full.query(cf).tolist() == list(range(10)) + [-1] * 5
+    # kernel map through the group probes == the exact map
+    cs = c[:20_000].copy()
+    cs[:, 1:] %= 24
+    _, keep = np.unique(cs, axis=0, return_index=True)
+    cs = cs[np.sort(keep)].astype(np.int32)
+    tab = HashTable(capacity=2 * cs.shape[0], device=device)
+    tab.insert(torch.as_tensor(cs, device=device))
+    offs = _target_offsets(3, 1, 1, False, device)
+    km = query_kernel_map(tab, torch.as_tensor(cs, device=device), offs, (24, 24, 24), 1, cs.shape[0])
+    want = O.exact_kmap(cs, cs, O.target_offsets(3, 1, 1, False), 1, (24, 24, 24))
+    assert np.array_equal(km.neighbor_indices.cpu().numpy(), want)
