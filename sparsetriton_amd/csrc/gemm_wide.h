@@ -228,15 +228,18 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
 
 // Whether the wide kernel takes a tiled gather.  Shapes where it measured
 // faster: 16-bit 128 x 128 (config 5: 1.16 -> 0.87 ms per gather); split fp32
-// with either width 128 (config 3, 64 -> 128: step 0.88 -> 0.77 ms).  At 64 x 64
-// (config 2: bf16 56 vs 64 us, fp32 133 vs 148 us) and 16-bit 64 x 128 / 128 x 64
-// (config 4: step 2.20 vs 2.32 ms) the four-wave kernels stay ahead, their
-// whole-line A gathers touching half as many cache lines per load.  Also: a
+// with exactly one width 128 (config 3, 64 -> 128: step 0.88 -> 0.77 ms).  At
+// 64 x 64 (config 2: bf16 56 vs 64 us, fp32 133 vs 148 us) and 16-bit 64 x 128 /
+// 128 x 64 (config 4: step 2.20 vs 2.32 ms) the four-wave kernels stay ahead,
+// their whole-line A gathers touching half as many cache lines per load.  Split
+// fp32 at 128 x 128 stages 64 KB of fp32 B per offset in registers: with the
+// 128 x 128 accumulators that overflows the VGPRs into AGPR copies
+// (SparseResNet21D fp32 step 24.4 -> 39.8 ms with it).  Also: a
 // 3x3x3-sized offset list, 16-byte aligned operands, A and Bt under 2 GB
 // (32-bit buffer offsets).
 inline bool wide_ok(int Kd, int Nd, int K, size_t esz, bool x3, int64_t n_src, const void* A, const void* Bt) {
   const bool built = (Kd == 64 || Kd == 128) && (Nd == 64 || Nd == 128);
-  const bool faster = x3 ? (Kd == 128 || Nd == 128) : (Kd == 128 && Nd == 128);
+  const bool faster = x3 ? ((Kd == 128) != (Nd == 128)) : (Kd == 128 && Nd == 128);
   return built && (faster || gather_wide_mode() == 2) && K <= kWideMaxK && (uintptr_t)A % 16 == 0 &&
          (uintptr_t)Bt % 16 == 0 && n_src * Kd * (int64_t)esz < (1ll << 31) - 64 &&
          (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
