@@ -313,8 +313,10 @@ int st_kmap_pairs_chunk_order(const int32_t* pairs, const int32_t* kstart, const
  * order (st_kmap_pairs + st_kmap_pairs_chunk_order) on a stream of the
  * library's that forks from `stream` at the call and joins it again before
  * the tile plan ends -- so work queued on `stream` after the call sees every
- * buffer complete, and nothing else has to be synchronised.  Calls from
- * several host threads are serialised per device.
+ * buffer complete, and nothing else has to be synchronised.  That stream and
+ * its two events are created on the first call with chunk > 0 on a device
+ * (the one resource this library creates; none is allocated in device
+ * memory).  Calls from several host threads are serialised per device.
  *
  * st_kmap_plans_layout fills layout[ST_PLAN_FIELDS]: byte offsets into the
  * caller's `plan` buffer of the outputs below (each on a 256-byte boundary),
