@@ -1020,28 +1020,32 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
 // inside a chunk: the four waves take the chunk's 32-pair steps round-robin.
 // Each wave stages its step's X and dY rows in its own LDS area row-major
 // (pair-major, 16-byte stores straight from the gathered rows) and reads the
-// MFMA fragments -- 8 pairs of one channel per lane -- with 16-bit LDS reads.
-// Pair p of a step lives in LDS row p, and lane group g takes pairs 4e + g
-// (e = 0..7) for both operands (any common assignment gives the same sum), so
-// with an 80-element row pitch the four groups hit disjoint LDS banks.
+// MFMA fragments -- 8 pairs of one channel per lane -- with transpose LDS
+// reads (tr_frag; pair p of a step lives in LDS row p, both operands take the
+// same pairs per lane group).
 // The wave tile is the workgroup's whole 64 x 64 channel tile (16 blocks);
 // the waves' accumulators are summed through LDS once per chunk.  Requires
 // C_in and C_out multiples of 64 and 16-byte aligned rows.
 constexpr int kWvPitch = 80;
 // MFMA operand fragment of a 32-pair step staged row-major (pitch kWvPitch
-// 16-bit elements): lane (c, g) gets channel col0 + c of pairs 8g .. 8g+7,
-// with two gfx950 transpose reads (ds_read_b64_tr_b16).  Within a 16-lane
-// group such a read hands lane l the element l mod 4 of the 4 elements lane
-// 4e + l/4 addresses, for e = 0..3; so lane c addresses pair 8g + 4h + c/4 at
-// channel col0 + 4 (c mod 4) and receives channel col0 + c of pairs 8g + 4h + e.
+// 16-bit elements): lane (c, g) gets channel col0 + c of pairs 4g .. 4g+3 and
+// 16 + 4g .. 16 + 4g+3, with two gfx950 transpose reads (ds_read_b64_tr_b16).
+// Within a 16-lane group such a read hands lane l the element l mod 4 of the
+// 4 elements lane 4e + l/4 addresses, for e = 0..3; so lane c addresses pair
+// 16h + 4g + c/4 at channel col0 + 4 (c mod 4) and receives channel col0 + c
+// of pairs 16h + 4g + e.  (Both operands take the same pairs, so the sum is the
+// step's; which pairs a lane group takes only decides the banks: the two
+// groups of a half-wave read rows 0-3 and 4-7 of an 8-row block, which the
+// 80- and 144-element pitches put on eight distinct 32-byte bank groups --
+// groups 8 rows apart, the earlier assignment, met on the same banks.)
 template <typename F, typename T, int PITCH = kWvPitch>
 __device__ __forceinline__ F tr_frag(const T* st, int g, int c, int col0) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef short v8s __attribute__((ext_vector_type(8)));
   using lds_v4s = __attribute__((address_space(3))) v4s;
-  const T* p0 = st + (g * 8 + (c >> 2)) * PITCH + col0 + (c & 3) * 4;
+  const T* p0 = st + (g * 4 + (c >> 2)) * PITCH + col0 + (c & 3) * 4;
   const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 4 * PITCH));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 16 * PITCH));
   const v8s both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(F, both);
 }
