@@ -278,7 +278,16 @@ int st_tile_plan(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride,
  * cstart (K + 1) = first chunk of each offset when each offset's pairs are
  * cut into chunks of `chunk` pairs.  block_counts holds K * num_blocks + 1
  * int32 (num_blocks from st_kmap_pairs_sizes); pair_capacity >= K * n_out.
+ * chunk = ST_PAIR_CHUNK_AUTO: the list picks the size itself, on the GPU, from
+ * its pair count P -- the least power of two >= 1024 with P <= 2048 * size, so
+ * at most min(2048 + K, K * n_out / 1024 + K) chunks (ST_PAIR_CHUNKS_AUTO_MAX)
+ * -- and stores it in cstart[K + 1] (cstart then holds K + 2 entries).  Pass
+ * ST_PAIR_CHUNK_AUTO on to the calls below that take the list; they read the
+ * size from there.
  */
+#define ST_PAIR_CHUNK_AUTO (-1)
+#define ST_PAIR_CHUNKS_AUTO_MAX(n_out, K) \
+  ((int64_t)(K) * (n_out) / 1024 + (K) < 2048 + (K) ? (int64_t)(K) * (n_out) / 1024 + (K) : 2048 + (int64_t)(K))
 int st_kmap_pairs_sizes(int64_t n_out, int K, int64_t* num_blocks);
 int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n_out, int K, int64_t n_in,
                   int32_t* block_counts, int64_t num_blocks, int chunk, int32_t* kstart, int32_t* cstart,
@@ -309,12 +318,12 @@ int st_kmap_pairs_chunk_order(const int32_t* pairs, const int32_t* kstart, const
 /*
  * Everything the gather-GEMMs and the weight gradient need from one map, in
  * one call: the mask-sorted row order and the tile plan (st_kmap_sort_rows +
- * st_tile_plan) on `stream` and, with chunk > 0, the pair list and its chunk
+ * st_tile_plan) on `stream` and, with chunk > 0 or ST_PAIR_CHUNK_AUTO, the pair list and its chunk
  * order (st_kmap_pairs + st_kmap_pairs_chunk_order) on a stream of the
  * library's that forks from `stream` at the call and joins it again before
  * the tile plan ends -- so work queued on `stream` after the call sees every
  * buffer complete, and nothing else has to be synchronised.  That stream and
- * its two events are created on the first call with chunk > 0 on a device
+ * its two events are created on the first call with a pair list on a device
  * (the one resource this library creates; none is allocated in device
  * memory).  Calls from several host threads are serialised per device.
  *
@@ -337,14 +346,15 @@ enum {
   ST_PLAN_TILE_NK,        /* int32 [tiles]                                   */
   ST_PLAN_TILE_KLIST,     /* int16 [tiles * K]                               */
   ST_PLAN_TILE_MAP,       /* int32 [tiles * K * 128]                         */
-  ST_PLAN_PAIRS,          /* int32 [2 * K * n_dst] (in, out); chunk > 0      */
+  ST_PLAN_PAIRS,          /* int32 [2 * K * n_dst] (in, out); chunk != 0     */
   ST_PLAN_KSTART,         /* int32 [K + 1]                                   */
-  ST_PLAN_CSTART,         /* int32 [K + 1]                                   */
+  ST_PLAN_CSTART,         /* int32 [K + 1] (K + 2 with ST_PAIR_CHUNK_AUTO)   */
   ST_PLAN_CORDER,         /* int32 [max_chunks]                              */
   ST_PLAN_BYTES,          /* size of `plan`                                  */
   ST_PLAN_SCRATCH_BYTES,  /* size of `scratch`                               */
   ST_PLAN_TILES,          /* ceil(n_dst / 128)                               */
-  ST_PLAN_MAX_CHUNKS,     /* K * n_dst / chunk + K (0 without a pair list)   */
+  ST_PLAN_MAX_CHUNKS,     /* K * n_dst / chunk + K (0 without a pair list;   *
+                           * ST_PAIR_CHUNKS_AUTO_MAX with ST_PAIR_CHUNK_AUTO) */
   ST_PLAN_FIELDS
 };
 int st_kmap_plans_layout(int64_t n_dst, int K, int chunk, int64_t* layout);
@@ -452,8 +462,9 @@ int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, in
  * Weight gradient over a pair list from st_kmap_pairs: every chunk of
  * `chunk` pairs is one equal-sized task (the centre offset of a submanifold
  * map has N pairs, the others far fewer), its C_in x C_out partial goes to
- * partials[chunk] (max_chunks * C_in * C_out fp32; max_chunks >= P / chunk + K)
- * and each offset's chunks are summed in order.  Deterministic; fp32
+ * partials[chunk] (max_chunks * C_in * C_out fp32; max_chunks >= P / chunk + K,
+ * or ST_PAIR_CHUNKS_AUTO_MAX for a list cut at ST_PAIR_CHUNK_AUTO, which is
+ * passed here too) and each offset's chunks are summed in order.  Deterministic; fp32
  * gathers feed MFMA operands straight from HBM, 16-bit ones go through LDS.
  * chunk_order (optional, max_chunks int32): the order chunks are taken in
  * (st_kmap_pairs_chunk_keys); each workgroup takes a contiguous run of it and

@@ -228,6 +228,14 @@ int launch_exclusive_scan(int32_t* counts, int64_t n, hipStream_t stream);
 constexpr int kPairRows = 4096;        // map rows per (row block, offset) workgroup of the pair list
 constexpr int kChunkOrderMax = 16384;  // chunks whose keys one workgroup holds in LDS (uint16 each)
 constexpr int kChunkOrderMaxK = 28;    // offsets of its per-(offset, bucket) count table
+constexpr int kPairChunkMin = 1024;    // smallest chunk size ST_PAIR_CHUNK_AUTO picks
+constexpr int kPairChunksAuto = 2048;  // ... for at most this many chunks' worth of pairs
+
+// Chunks of an ST_PAIR_CHUNK_AUTO pair list over n rows and K offsets, at most.
+inline int64_t auto_max_chunks(int64_t n, int K) {
+  const int64_t by_rows = (int64_t)K * n / kPairChunkMin + K;
+  return by_rows < kPairChunksAuto + K ? by_rows : kPairChunksAuto + K;
+}
 
 // Pair list of a map (count, scan + kstart / cstart, emit) and its chunk order
 // (defined in kmap.hip; arguments checked by the caller).  launch_chunk_order

@@ -337,7 +337,8 @@ int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, c
                    const int32_t* kstart, const int32_t* cstart, int K, int chunk, int64_t max_chunks,
                    const int32_t* chunk_order, int C_in, int C_out, int dtype, float* partials, void* dW, int dw_dtype,
                    st_stream_t stream) {
-  if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0 || max_chunks >= (1ll << 31) || C_in <= 0 ||
+  if (K <= 0 || K > ST_MAX_KVOL || (chunk <= 0 && chunk != ST_PAIR_CHUNK_AUTO) || max_chunks < 0 ||
+      max_chunks >= (1ll << 31) || C_in <= 0 ||
       C_out <= 0 || n_in < 0 || n_out < 0)
     return ST_ERR_ARG;
   if (!kstart || !cstart || !partials || !dW || (max_chunks > 0 && (!pairs || !X || !dY))) return ST_ERR_ARG;

@@ -827,11 +827,11 @@ __global__ __launch_bounds__(256) void wgrad_pairs_f32_kernel(const float* __res
                                                               const int32_t* __restrict__ cstart, const int32_t* __restrict__ chunk_order,
     int K, int chunk,
                                                               int Cin, int Cout, float* __restrict__ partials) {
-  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 2];
   __shared__ float red_s[3][MT * NT * 4][64];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  for (int t = tid; t <= K + (chunk <= 0); t += 256) cstart_s[t] = cstart[t];  // + the size, when chosen by the list
   __syncthreads();
   const int total = cstart_s[K];
 
@@ -850,8 +850,9 @@ __global__ __launch_bounds__(256) void wgrad_pairs_f32_kernel(const float* __res
   for (int cq = cr.q0; cq < cr.q1; cq += cr.step) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
-    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
-    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    const int ch = chunk > 0 ? chunk : cstart_s[K + 1];  // the plan's own size when not given
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * ch;
+    const int p1 = min(p0 + ch, kstart[k + 1]);
     v4f acc[MT][NT];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -935,13 +936,13 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
   constexpr int KSTEP = Frag<T>::KSTEP;
   constexpr int PITCH = kWpQB + 8;
   constexpr int TB = 8;  // 16x16 blocks per side of the workgroup tile (128 channels)
-  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 2];
   __shared__ int2 pr_s[kWpQB];
   __shared__ __attribute__((aligned(16))) T xt_s[TB * 16 * PITCH];
   __shared__ __attribute__((aligned(16))) T yt_s[TB * 16 * PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  for (int t = tid; t <= K + (chunk <= 0); t += 256) cstart_s[t] = cstart[t];  // + the size, when chosen by the list
   __syncthreads();
   const int total = cstart_s[K];
 
@@ -958,8 +959,9 @@ __global__ __launch_bounds__(256) void wgrad_pairs_lds_kernel(const T* __restric
   for (int cq = cr.q0; cq < cr.q1; cq += cr.step) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
-    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
-    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    const int ch = chunk > 0 ? chunk : cstart_s[K + 1];  // the plan's own size when not given
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * ch;
+    const int p1 = min(p0 + ch, kstart[k + 1]);
     v4f acc[JB];
 #pragma unroll
     for (int j = 0; j < JB; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -1087,11 +1089,11 @@ __global__ __launch_bounds__(256, (MB > 4 || NB > 4) ? 1 : (ONEPASS ? 2 : 3)) vo
   constexpr int RP = TN + 4;            // row pitch (floats) of the per-wave tiles summed at the end
   constexpr int RH = (ONEPASS || TM < 32) ? TM : 32;  // rows summed per round
   constexpr int RED_BYTES = 4 * RH * RP * (int)sizeof(float);
-  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 2];
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  for (int t = tid; t <= K + (chunk <= 0); t += 256) cstart_s[t] = cstart[t];  // + the size, when chosen by the list
   __syncthreads();
   const int total = cstart_s[K];
 
@@ -1110,8 +1112,9 @@ __global__ __launch_bounds__(256, (MB > 4 || NB > 4) ? 1 : (ONEPASS ? 2 : 3)) vo
   for (int cq = ct.q0; cq < ct.q1; cq += ct.step) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
-    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
-    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    const int ch = chunk > 0 ? chunk : cstart_s[K + 1];  // the plan's own size when not given
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * ch;
+    const int p1 = min(p0 + ch, kstart[k + 1]);
     v4f acc[MB][NB];
 #pragma unroll
     for (int i = 0; i < MB; ++i)

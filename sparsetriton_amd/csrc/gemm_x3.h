@@ -624,11 +624,11 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   constexpr int STAGE_BYTES = 4 * 4 * STAGE * 2;
   constexpr int RP = 68;
   constexpr int RED_BYTES = 4 * 64 * RP * (int)sizeof(float);
-  __shared__ int32_t cstart_s[ST_MAX_KVOL + 1];
+  __shared__ int32_t cstart_s[ST_MAX_KVOL + 2];
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  for (int t = tid; t <= K; t += 256) cstart_s[t] = cstart[t];
+  for (int t = tid; t <= K + (chunk <= 0); t += 256) cstart_s[t] = cstart[t];  // + the size, when chosen by the list
   __syncthreads();
   const int total = cstart_s[K];
 
@@ -647,8 +647,9 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
   for (int cq = ct.q0; cq < ct.q1; cq += ct.step) {
     const int cidx = chunk_order ? chunk_order[cq] : cq;
     const int k = chunk_offset(cstart_s, K, cidx);
-    const int p0 = kstart[k] + (cidx - cstart_s[k]) * chunk;
-    const int p1 = min(p0 + chunk, kstart[k + 1]);
+    const int ch = chunk > 0 ? chunk : cstart_s[K + 1];  // the plan's own size when not given
+    const int p0 = kstart[k] + (cidx - cstart_s[k]) * ch;
+    const int p1 = min(p0 + ch, kstart[k + 1]);
     v4f acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)

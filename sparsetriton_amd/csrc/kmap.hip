@@ -240,13 +240,20 @@ __global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restric
   if (threadIdx.x == 0) counts[n] = carry;
   if (!pl.kstart) return;
   __syncthreads();  // the scanned counts of the other threads are visible to the workgroup
+  // the chunk size: the caller's, or (ST_PAIR_CHUNK_AUTO) the least power of two >= 1024 with at
+  // most 2048 chunks' worth of pairs in total -- so the list has at most 2048 + K chunks
+  int chunk = pl.chunk;
+  if (chunk <= 0) {
+    chunk = kPairChunkMin;
+    while ((int64_t)chunk * kPairChunksAuto < (int64_t)carry) chunk <<= 1;
+  }
   // thread k < K (K <= 512): offset k's first pair and chunk count; cstart is the scan of the latter
   const int k = threadIdx.x;
   int nch = 0;
   if (k < pl.K) {
     const int32_t s0 = counts[(int64_t)k * pl.nb], s1 = k + 1 < pl.K ? counts[(int64_t)(k + 1) * pl.nb] : carry;
     pl.kstart[k] = s0;
-    nch = (s1 - s0 + pl.chunk - 1) / pl.chunk;
+    nch = (s1 - s0 + chunk - 1) / chunk;
   }
   int chunks;
   const int cex = block_exclusive_scan(nch, scratch, &chunks);
@@ -254,6 +261,7 @@ __global__ __launch_bounds__(1024) void exclusive_scan_kernel(int32_t* __restric
   if (k == 0) {
     pl.kstart[pl.K] = carry;
     pl.cstart[pl.K] = chunks;
+    if (pl.chunk <= 0) pl.cstart[pl.K + 1] = chunk;  // the size the chunks were cut at
   }
 }
 
@@ -605,7 +613,8 @@ int launch_pairs(const int32_t* map, int64_t ks, int64_t rs, int64_t n_out, int 
 extern "C" int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride, int64_t n_out, int K,
                              int64_t n_in, int32_t* block_counts, int64_t num_blocks, int chunk, int32_t* kstart,
                              int32_t* cstart, int32_t* pairs, int64_t pair_capacity, st_stream_t stream) {
-  if (n_out < 0 || n_in < 0 || K <= 0 || K > ST_MAX_KVOL || chunk <= 0) return ST_ERR_ARG;
+  if (n_out < 0 || n_in < 0 || K <= 0 || K > ST_MAX_KVOL || (chunk <= 0 && chunk != ST_PAIR_CHUNK_AUTO))
+    return ST_ERR_ARG;
   if (num_blocks != (n_out + st::kPairRows - 1) / st::kPairRows) return ST_ERR_ARG;
   if ((int64_t)K * n_out >= (1ll << 31) || pair_capacity < (int64_t)K * n_out) return ST_ERR_ARG;
   if (!block_counts || !kstart || !cstart || (n_out > 0 && (!map || !pairs))) return ST_ERR_ARG;
@@ -626,6 +635,7 @@ __global__ __launch_bounds__(256) void chunk_keys_kernel(const int32_t* __restri
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= max_chunks) return;
   const int total = cstart[K];
+  if (chunk <= 0) chunk = cstart[K + 1];
   uint32_t key = 511u;
   if (c < total) {
     int lo = 0, hi = K - 1;  // offset of chunk c: largest k with cstart[k] <= c
@@ -646,7 +656,9 @@ __global__ __launch_bounds__(256) void chunk_keys_kernel(const int32_t* __restri
 extern "C" int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K,
                                         int chunk, int64_t max_chunks, int64_t n_out, uint32_t* keys,
                                         st_stream_t stream) {
-  if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0 || max_chunks >= (1ll << 31)) return ST_ERR_ARG;
+  if (K <= 0 || K > ST_MAX_KVOL || (chunk <= 0 && chunk != ST_PAIR_CHUNK_AUTO) || max_chunks < 0 ||
+      max_chunks >= (1ll << 31))
+    return ST_ERR_ARG;
   if (max_chunks == 0) return ST_OK;
   if (!pairs || !kstart || !cstart || !keys) return ST_ERR_ARG;
   return st::launch_chunk_keys(pairs, kstart, cstart, K, chunk, max_chunks, n_out, keys, stream);
@@ -691,16 +703,17 @@ __global__ __launch_bounds__(1024) void chunk_order_kernel(const int32_t* __rest
   __shared__ uint16_t keys_s[kChunkOrderMax];
   __shared__ int16_t cnt_s[kChunkOrderMaxK][kChunkBuckets];  // counts, then prefix over runs
   __shared__ int32_t below_s[kChunkBuckets];                  // chunks of all runs in lower buckets
-  __shared__ int32_t cst_s[kChunkOrderMaxK + 1], kst_s[kChunkOrderMaxK + 1];
+  __shared__ int32_t cst_s[kChunkOrderMaxK + 2], kst_s[kChunkOrderMaxK + 1];
   __shared__ int scan_s[17];
   const int tid = threadIdx.x;
-  for (int t = tid; t <= K; t += 1024) {
+  for (int t = tid; t <= K + (chunk <= 0); t += 1024) {
     cst_s[t] = cstart[t];
-    kst_s[t] = kstart[t];
+    if (t <= K) kst_s[t] = kstart[t];
   }
   for (int t = tid; t < K * kChunkBuckets; t += 1024) (&cnt_s[0][0])[t] = 0;
   __syncthreads();
   const int total = cst_s[K];
+  if (chunk <= 0) chunk = cst_s[K + 1];
   for (int c = tid; c < total; c += 1024) {
     const int k = chunk_run(cst_s, K, c);
     const int64_t p0 = kst_s[k] + (int64_t)(c - cst_s[k]) * chunk;
@@ -752,7 +765,7 @@ int launch_chunk_order(const int32_t* pairs, const int32_t* kstart, const int32_
 extern "C" int st_kmap_pairs_chunk_order(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K,
                                          int chunk, int64_t max_chunks, int64_t n_out, int32_t* order,
                                          st_stream_t stream) {
-  if (K <= 0 || K > ST_MAX_KVOL || chunk <= 0 || max_chunks < 0) return ST_ERR_ARG;
+  if (K <= 0 || K > ST_MAX_KVOL || (chunk <= 0 && chunk != ST_PAIR_CHUNK_AUTO) || max_chunks < 0) return ST_ERR_ARG;
   if (max_chunks > st::kChunkOrderMax) return ST_ERR_UNSUPPORTED;
   if (max_chunks > 0 && (!pairs || !kstart || !cstart || !order)) return ST_ERR_ARG;
   return st::launch_chunk_order(pairs, kstart, cstart, K, chunk, max_chunks, n_out, order, stream);

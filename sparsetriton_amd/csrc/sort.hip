@@ -411,18 +411,19 @@ PlanScratch plan_scratch(int64_t n, int K, int64_t max_chunks) {
 }
 
 bool plan_layout(int64_t n, int K, int chunk, int64_t* L) {
-  if (n < 0 || n >= (1ll << 31) || K <= 0 || K > ST_MAX_KVOL || chunk < 0) return false;
+  if (n < 0 || n >= (1ll << 31) || K <= 0 || K > ST_MAX_KVOL || (chunk < 0 && chunk != ST_PAIR_CHUNK_AUTO))
+    return false;
   if ((int64_t)K * n >= (1ll << 31)) return false;
   const int64_t tiles = (n + st::kTileRows - 1) / st::kTileRows;
-  const int64_t mc = chunk > 0 ? (int64_t)K * n / chunk + K : 0;
+  const int64_t mc = chunk > 0 ? (int64_t)K * n / chunk + K : (chunk < 0 ? st::auto_max_chunks(n, K) : 0);
   int64_t at = 0;
   L[ST_PLAN_PERM] = at, at = align_up(at + 4 * n);
   L[ST_PLAN_TILE_NK] = at, at = align_up(at + 4 * tiles);
   L[ST_PLAN_TILE_KLIST] = at, at = align_up(at + 2 * tiles * K);
   L[ST_PLAN_TILE_MAP] = at, at = align_up(at + 4 * tiles * K * st::kTileRows);
-  L[ST_PLAN_PAIRS] = at, at = align_up(at + (chunk > 0 ? 8 * (int64_t)K * n : 0));
-  L[ST_PLAN_KSTART] = at, at = align_up(at + (chunk > 0 ? 4 * (K + 1) : 0));
-  L[ST_PLAN_CSTART] = at, at = align_up(at + (chunk > 0 ? 4 * (K + 1) : 0));
+  L[ST_PLAN_PAIRS] = at, at = align_up(at + (chunk != 0 ? 8 * (int64_t)K * n : 0));
+  L[ST_PLAN_KSTART] = at, at = align_up(at + (chunk != 0 ? 4 * (K + 1) : 0));
+  L[ST_PLAN_CSTART] = at, at = align_up(at + (chunk != 0 ? 4 * (K + 2) : 0));
   L[ST_PLAN_CORDER] = at, at = align_up(at + 4 * mc);
   L[ST_PLAN_BYTES] = at > 0 ? at : kAlign;
   L[ST_PLAN_SCRATCH_BYTES] = plan_scratch(n, K, mc).bytes;
@@ -463,7 +464,7 @@ extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t m
 
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> lock;
-  if (chunk > 0) {
+  if (chunk != 0) {
     int dev = 0;
     ST_CHECK_HIP(hipGetDevice(&dev));
     if (dev >= 0 && dev < kMaxDevices) {
@@ -484,7 +485,7 @@ extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t m
     ST_CHECK_HIP(hipStreamWaitEvent(side->stream, side->fork, 0));
     ps = side->stream;
   }
-  if (chunk > 0) {
+  if (chunk != 0) {
     const int64_t nb = (n_dst + st::kPairRows - 1) / st::kPairRows;
     int32_t* pairs = (int32_t*)(pb + L[ST_PLAN_PAIRS]);
     int32_t* kstart = (int32_t*)(pb + L[ST_PLAN_KSTART]);

@@ -253,14 +253,14 @@ class KernelMap:
 
     # ------------------------------------------------------------ GEMM plans
     def _build_plans(self, chunk: int) -> None:
-        """Row order + tile plan of the forward (and with chunk > 0 the pair list and its chunk
+        """Row order + tile plan of the forward (and with chunk != 0 the pair list and its chunk
         order, on the library's side stream, joined back before the call's work ends): one
         ``st_kmap_plans`` call over one buffer."""
         self.ensure_out_masks()
         plan = MapPlan.build(self.nbr, self.k_stride, self.r_stride, self.out_masks, self.K, self.n_out, self.n_in,
                              chunk)
         self._fwd_tiles = plan.tiles
-        if chunk > 0:
+        if chunk != 0:
             self._pairs[chunk] = plan.pairs
 
     def forward_plan(self) -> "TileMap":
@@ -289,9 +289,11 @@ class KernelMap:
         """Mask-sorted order of the input rows over the transposed map (input gradient)."""
         return self.backward_tiles()
 
-    def pair_list(self, chunk: int = 2048, with_tiles: bool = True) -> "PairList":
+    def pair_list(self, chunk: Optional[int] = None, with_tiles: bool = True) -> "PairList":
         """(in, out) pairs sorted by (offset, out) with equal-size chunks, for the weight gradient;
         the default chunk size comes with the forward tile plan unless ``with_tiles`` is False."""
+        if chunk is None:
+            chunk = _PAIR_CHUNK
         pl = self._pairs.get(chunk)
         if pl is None:
             if chunk == _PAIR_CHUNK and self._fwd_tiles is None and with_tiles:
@@ -338,7 +340,10 @@ def row_representatives(coords: torch.Tensor) -> Optional[torch.Tensor]:
     return first[inv].to(torch.int32)
 
 
-_PAIR_CHUNK = 2048  # pairs per weight-gradient task
+# pairs per weight-gradient task: ST_PAIR_CHUNK_AUTO, chosen on the GPU from the pair count P
+# (the least power of two >= 1024 with at most 2048 chunks' worth of pairs): small lists keep
+# 1024-pair tasks for parallelism, large ones take longer tasks and fewer partial sums
+_PAIR_CHUNK = -1
 
 # st_kmap_plans_layout fields (include/sparsetriton_amd.h)
 (_PL_PERM, _PL_TILE_NK, _PL_TILE_KLIST, _PL_TILE_MAP, _PL_PAIRS, _PL_KSTART, _PL_CSTART, _PL_CORDER, _PL_BYTES,
@@ -422,7 +427,9 @@ class TileMap:
 class PairList:
     """(in, out) int32 pairs sorted by (offset, out); ``kstart`` / ``cstart`` (K + 1) the first pair /
     chunk of each offset; ``max_chunks`` bounds the chunk count without reading it back;
-    ``corder`` the chunk ids sorted by their first output row (the weight gradient's order)."""
+    ``corder`` the chunk ids sorted by their first output row (the weight gradient's order).
+    ``chunk`` is the size given to the builder; for -1 (chosen on the GPU) the size sits in the
+    device word after ``cstart`` (``chunk_size()`` reads it back)."""
 
     def __init__(self, pairs, kstart, cstart, chunk, max_chunks, corder):
         self._pairs, self._kstart, self._cstart, self._corder = pairs, kstart, cstart, corder
@@ -474,11 +481,11 @@ class PairList:
         cap = K * n_out
         counts = torch.empty((K * nb.value + 1,), dtype=torch.int32, device=dev)
         kstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
-        cstart = torch.empty((K + 1,), dtype=torch.int32, device=dev)
+        cstart = torch.empty((K + 2,), dtype=torch.int32, device=dev)
         pairs = torch.empty((2 * max(cap, 1),), dtype=torch.int32, device=dev)
         _lib.call("st_kmap_pairs", _lib.ptr(map_t), k_stride, r_stride, n_out, K, n_in, _lib.ptr(counts), nb.value,
                   int(chunk), _lib.ptr(kstart), _lib.ptr(cstart), _lib.ptr(pairs), cap, _lib.stream_of(dev))
-        max_chunks = cap // int(chunk) + K
+        max_chunks = _plan_layout(int(n_out), int(K), int(chunk))[_PL_MAX_CHUNKS]
         corder = torch.empty((max(max_chunks, 1),), dtype=torch.int32, device=dev)
         if max_chunks <= _CHUNK_ORDER_MAX and K <= _CHUNK_ORDER_MAX_K:
             _lib.call("st_kmap_pairs_chunk_order", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
@@ -488,7 +495,18 @@ class PairList:
             _lib.call("st_kmap_pairs_chunk_keys", _lib.ptr(pairs), _lib.ptr(kstart), _lib.ptr(cstart), K, int(chunk),
                       max_chunks, n_out, _lib.ptr(keys), _lib.stream_of(dev))
             corder = TilePlan.build(max_chunks, 9, keys).perm
-        return cls(pairs, kstart, cstart, int(chunk), max_chunks, corder)
+        pl = cls(pairs, kstart, cstart[:K + 1], int(chunk), max_chunks, corder)
+        pl._size_word = cstart[K + 1:]
+        return pl
+
+    def chunk_size(self) -> int:
+        """Pairs per chunk (reads the device word back for a list that chose its own size)."""
+        if self.chunk > 0:
+            return self.chunk
+        word = getattr(self, "_size_word", None)
+        if word is None:
+            word = _buf_view(self._buf, self._L[_PL_CSTART] + 4 * (self._K + 1), 1, torch.int32)
+        return int(word.item())
 
 
 _CHUNK_ORDER_MAX, _CHUNK_ORDER_MAX_K = 16384, 28  # st_kmap_pairs_chunk_order's limits
@@ -509,7 +527,8 @@ class MapPlan:
         scratch = torch.empty((L[_PL_SCRATCH_BYTES],), dtype=torch.uint8, device=dev)
         _lib.call("st_kmap_plans", map_t.data_ptr(), k_stride, r_stride, masks.data_ptr(), K, n_dst, n_src, chunk,
                   get_tile_slab_bits(), buf.data_ptr(), scratch.data_ptr(), _lib.stream_of(dev))
-        return cls(TileMap.in_plan(buf, L, n_dst, K), PairList.in_plan(buf, L, n_dst, K, chunk) if chunk > 0 else None)
+        return cls(TileMap.in_plan(buf, L, n_dst, K),
+                   PairList.in_plan(buf, L, n_dst, K, chunk) if chunk != 0 else None)
 
 
 @functools.lru_cache(maxsize=64)

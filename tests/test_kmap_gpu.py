@@ -354,6 +354,40 @@ def test_one_call_plans_match_the_separate_builders(device, k, chunk):
     assert np.array_equal(q.corder.cpu().numpy(), ref)
 
 
+
+@pytest.mark.parametrize("n,S", [(5000, 24), (300000, 64)])
+def test_pair_list_chooses_its_chunk_size(device, n, S):
+    """ST_PAIR_CHUNK_AUTO: the size is the least power of two >= 1024 with P <= 2048 * size,
+    stored after cstart; the list, its chunk starts and its chunk order equal those built with
+    that size given, through both builders; the weight gradient over either is the same."""
+    from sparsetriton_amd.nn.functional.conv.kmap import MapPlan, PairList
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import wgrad
+    rng = np.random.default_rng(33)
+    c = _rand_coords(rng, n, S)
+    kmap = _subm(device, c, (S, S, S))
+    kmap.ensure_out_masks()
+    K, N = kmap.K, kmap.n_out
+    auto = PairList.build(kmap.nbr, kmap.k_stride, kmap.r_stride, N, K, kmap.n_in, -1)
+    plan = MapPlan.build(kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, K, N, kmap.n_in, -1).pairs
+    P = int((kmap.nbr >= 0).sum())
+    size = 1024
+    while size * 2048 < P:
+        size *= 2
+    assert auto.chunk_size() == plan.chunk_size() == size
+    assert auto.max_chunks == plan.max_chunks == min(2048 + K, K * N // 1024 + K)
+    fixed = PairList.build(kmap.nbr, kmap.k_stride, kmap.r_stride, N, K, kmap.n_in, size)
+    for q in (auto, plan):
+        assert torch.equal(q.kstart, fixed.kstart) and torch.equal(q.cstart, fixed.cstart)
+        assert int(q.cstart[-1]) <= q.max_chunks
+        assert torch.equal(q.pairs[:2 * P], fixed.pairs[:2 * P])
+        total = int(fixed.cstart[-1])
+        assert torch.equal(q.corder[:total], fixed.corder[:total])
+        assert np.array_equal(np.sort(q.corder.cpu().numpy()), np.arange(q.max_chunks))
+    X = torch.randn((N, 32), device=device)
+    dY = torch.randn((N, 48), device=device)
+    dw = [wgrad(X, dY, kmap, torch.float32, pairs=q) for q in (auto, plan, fixed)]
+    assert torch.equal(dw[0], dw[2]) and torch.equal(dw[1], dw[2])
+
 def test_one_call_plans_of_an_empty_map(device):
     from sparsetriton_amd.nn.functional.conv.kmap import MapPlan
     nbr = torch.empty((27, 0), dtype=torch.int32, device=device)

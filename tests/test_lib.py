@@ -40,3 +40,17 @@ def test_version_and_arg_checks():
     assert lib.st_hash_insert(None, 0, 5, 1, None, None, 10, None, None) == -1
     assert lib.st_gather_gemm(None, 0, None, 0, 0, None, 1, None, None, None, None, 0, 0, 8, 8, 0, None) == -1
     assert lib.st_weight_prep(None, None, 27, 4, 4, 0, 0, None) == -1
+
+
+def test_plan_layout_with_an_automatic_chunk_size():
+    """st_kmap_plans_layout is host arithmetic: a pair list cut at ST_PAIR_CHUNK_AUTO (-1) is
+    bounded by min(2048 + K, K * n / 1024 + K) chunks and keeps K + 2 cstart words."""
+    lib = _lib.lib()
+    L = (ctypes.c_int64 * 12)()
+    for n, K in ((100, 27), (5000, 27), (1_000_000, 27), (300_000, 125)):
+        assert lib.st_kmap_plans_layout(n, K, -1, L) == 0
+        assert L[11] == min(2048 + K, K * n // 1024 + K)
+        assert L[7] - L[6] >= 4 * (K + 2)  # cstart region (ends at the chunk order)
+        assert lib.st_kmap_plans_layout(n, K, 2048, L) == 0
+        assert L[11] == K * n // 2048 + K
+    assert lib.st_kmap_plans_layout(100, 27, -2, L) == -1
