@@ -152,14 +152,22 @@ int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const 
  * st_kmap_query over a table of coords, bit for bit.  status (optional,
  * ST_STATUS_WORDS int32, cleared by the call) counts BAD_COORD (rows that do
  * not pack into a key), DUPLICATE (rows repeating a coordinate) and
- * OUT_OF_BOX (rows outside [0, batches) x [0, shape)).
+ * OUT_OF_BOX (rows whose xyz lie outside [0, shape)).
  * st_kmap_subm_workspace returns ST_ERR_ARG when the box is far larger than
  * the set (level 1 would exceed 64 bytes a row): query a hash table instead.
+ * st_kmap_subm = st_subm_index (the index alone, with the status counts) +
+ * st_kmap_subm_query (the map from a built index; the index stays valid
+ * while `workspace` and the coordinates are unchanged, for any offsets).
  */
 int st_kmap_subm_workspace(int64_t n, int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* bytes);
 int st_kmap_subm(const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K, int64_t batches,
                  int64_t sx, int64_t sy, int64_t sz, void* workspace, int64_t workspace_bytes, int32_t* nbr,
                  uint32_t* row_masks, int32_t* status, st_stream_t stream);
+int st_subm_index(const void* coords, int coord_dtype, int64_t n, int64_t batches, int64_t sx, int64_t sy,
+                  int64_t sz, void* workspace, int64_t workspace_bytes, int32_t* status, st_stream_t stream);
+int st_kmap_subm_query(const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
+                       int64_t batches, int64_t sx, int64_t sy, int64_t sz, const void* workspace,
+                       int64_t workspace_bytes, int32_t* nbr, uint32_t* row_masks, st_stream_t stream);
 
 /* Geometry of a strided or transposed convolution's output-coordinate build. */
 typedef struct st_outgeom {
@@ -494,6 +502,29 @@ typedef struct st_lookup {
   int64_t bounds[3];     /* if > 0: q must satisfy 0 <= q < bounds on that axis       */
   int64_t row_bounds[3]; /* if > 0: rows with c outside [0, row_bounds) get no pairs  */
 } st_lookup;
+
+/*
+ * Forward of ConvHashOnTheFlyImplicitGEMM (implicit_gemm_hash_on_fly_fwd_kernel,
+ * implicit_hashfly_gemm.py:45-148) for a submanifold convolution (out = in
+ * coordinates, stride 1, bounds = the index box), with the neighbours found
+ * inside the GEMM in the coordinates' brick index (st_subm_index, same
+ * geometry) instead of a hash table: no kernel map is stored.  Per 128-row
+ * tile (rows in their given order) each row looks up its K neighbours
+ * (coords[r].xyz - offsets[k]; the lowest row of a repeated coordinate, as
+ * the table holds), the tile's offset list is the union of its rows', and
+ * out[r] = sum_k A[nbr(k, r)] Bt[k]^T (+ bias), Bt as st_gather_gemm's.
+ * The input gradient of a submanifold map that is its own transpose (status
+ * DUPLICATE and OUT_OF_BOX zero, offsets symmetric) is the same call with the
+ * weights of st_weight_prep(ST_W_REVERSE).  Bitwise equal to st_hashfly_gemm
+ * and st_gather_gemm_tiled on the same rows.  st_subm_fly_ok(Kd, Nd, K,
+ * dtype) = 1 for the shapes built: Kd, Nd in {64, 128} (split fp32 not at
+ * 128 x 128), K <= 27, dtype ST_BF16, ST_F16 or ST_F32_BF16X3; others (and
+ * int64 coordinates) return ST_ERR_UNSUPPORTED.
+ */
+int st_subm_fly_ok(int Kd, int Nd, int K, int dtype);
+int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
+                     int64_t batches, int64_t sx, int64_t sy, int64_t sz, const void* index, int64_t index_bytes,
+                     const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype, st_stream_t stream);
 
 /*
  * Forward / input-gradient of ConvHashOnTheFlyImplicitGEMM

@@ -22,6 +22,9 @@ int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_
                        const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
                        int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
                        hipStream_t stream);
+int ops_gather_fly_x3(const float* A, int64_t n, const void* coords, int coord_dtype, const int32_t* offsets, int K,
+                      const SubmIndex& ix, const float* Bt, float* out, const float* bias, int Kd, int Nd,
+                      hipStream_t stream);
 }  // namespace st
 
 using namespace st;
@@ -348,6 +351,37 @@ int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, c
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_wgrad_pairs<T>((const T*)X, n_in, (const T*)dY, n_out, pairs, kstart, cstart, chunk_order, K,
                                        chunk, max_chunks, C_in, C_out, partials, dW, dw_dtype, stream));
+}
+
+int st_subm_fly_ok(int Kd, int Nd, int K, int dtype) {
+  if (dtype != ST_BF16 && dtype != ST_F16 && dtype != ST_F32_BF16X3) return 0;
+  // alignment and operand sizes are checked per call; 16 is the alignment torch allocations have
+  return fly_ok(Kd, Nd, K, dtype == ST_F32_BF16X3 ? 4 : 2, dtype == ST_F32_BF16X3, 1, nullptr, nullptr) ? 1 : 0;
+}
+
+int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
+                     int64_t batches, int64_t sx, int64_t sy, int64_t sz, const void* index, int64_t index_bytes,
+                     const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype, st_stream_t stream) {
+  const int64_t need = subm_workspace_bytes(n, batches, sx, sy, sz);
+  if (need < 0 || index_bytes < need || K <= 0 || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
+  if (!st_subm_fly_ok(Kd, Nd, K, dtype)) return ST_ERR_UNSUPPORTED;
+  if (n == 0) return ST_OK;
+  if (!A || !coords || !offsets || !index || !Bt || !out) return ST_ERR_ARG;
+  SubmIndex ix;
+  subm_view(const_cast<void*>(index), n, batches, sx, sy, sz, &ix);
+  switch (dtype) {
+    case ST_F32_BF16X3:
+      return ops_gather_fly_x3((const float*)A, n, coords, coord_dtype, offsets, K, ix, (const float*)Bt, (float*)out,
+                               (const float*)bias, Kd, Nd, stream);
+    case ST_BF16:
+      return ops_gather_fly<__bf16>((const __bf16*)A, n, coords, coord_dtype, offsets, K, ix, (const __bf16*)Bt,
+                                    (__bf16*)out, (const __bf16*)bias, Kd, Nd, stream);
+    case ST_F16:
+      return ops_gather_fly<_Float16>((const _Float16*)A, n, coords, coord_dtype, offsets, K, ix,
+                                      (const _Float16*)Bt, (_Float16*)out, (const _Float16*)bias, Kd, Nd, stream);
+    default:
+      return ST_ERR_UNSUPPORTED;
+  }
 }
 
 int st_hashfly_gemm(const void* A, int64_t n_src, const void* dst_coords, int coord_dtype, int64_t n_dst,

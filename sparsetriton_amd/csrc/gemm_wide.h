@@ -21,16 +21,36 @@
 // with one MFMA per 32-element step (fp32: the three split products in the
 // order of mfma_x3), exactly as the ring kernels do, so the two agree bitwise.
 // The tile's source rows (nk x 128) are copied to LDS first, so nk <= kWideMaxK.
+//
+// With a FlySrc (submanifold, no kernel map) the tile is 128 consecutive rows
+// and the prologue finds the sources itself: each thread looks its row's K
+// neighbours up in the coordinates' brick index (subm_index.h), the tile's
+// offset list is the union of its rows' (offsets no row of the tile has are
+// never loaded), and the main loop is the same.  A row with a neighbour
+// through offset k gets the same sum as from a map or a hash-table probe:
+// offsets it lacks add exact zeros.
 #pragma once
 
 #include <type_traits>
 
 #include "mfma.h"
 #include "nbr_src.h"
+#include "subm_index.h"
 
 namespace st {
 
 constexpr int kWideMaxK = 27;  // offsets whose sources a wide workgroup holds (a 3x3x3 kernel)
+
+// Neighbours of destination row r looked up in a brick index (source rows are
+// the same coordinate set's rows: out = in, stride 1).
+template <typename CT>
+struct FlySrc {
+  static constexpr bool kTiled = false;
+  const CT* __restrict__ coords;
+  const int32_t* __restrict__ offsets;  // K x 3
+  SubmIndex ix;
+  int K;
+};
 
 // ST_GATHER_WIDE=0 keeps the four-wave kernels everywhere, =2 takes the wide one
 // for every width it is built for (A/B timing); default: 128 x 128 only.
@@ -43,8 +63,8 @@ inline int gather_wide_mode() {
   return mode;
 }
 
-template <typename T, bool X3, int KD, int BN, int D, typename E>
-__global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restrict__ A, TiledSrc src,
+template <typename T, bool X3, int KD, int BN, int D, typename E, typename S>
+__global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restrict__ A, S src,
                                                                const int32_t* __restrict__ rows,
                                                                const T* __restrict__ Bt, T* __restrict__ out,
                                                                int64_t n_src, int64_t n_dst, E epi) {
@@ -74,23 +94,53 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
   const RingTile tile = ring_tile(n_dst, BN, BN);
   const int64_t t = tile.rt;
   if (t * kGemmBM >= n_dst) return;
-  const int nk = src.nk[t];
+  int nk;
 
-  {
+  if constexpr (S::kTiled) {
+    nk = src.nk[t];
+    {
+      const int64_t r = t * kGemmBM + tid;
+      drow_s[tid] = r < n_dst ? rows[r] : -1;
+    }
+    if (tid < nk) klist_s[tid] = src.klist[t * src.K + tid];
+    {
+      // the tile's sources, offset-major as the plan stores them: thread tid takes row tid of every offset,
+      // all loads in flight together
+      const int32_t* tm = src.tmap + t * (int64_t)src.K * kGemmBM + tid;
+      int32_t v[kWideMaxK];
+#pragma unroll
+      for (int j = 0; j < kWideMaxK; ++j) v[j] = j < nk ? tm[j * kGemmBM] : -1;
+#pragma unroll
+      for (int j = 0; j < kWideMaxK; ++j)
+        if (j < nk) src_s[j][tid] = (int64_t)v[j] >= n_src ? -1 : v[j];
+    }
+  } else {
+    // sources by offset (src_s[k]), the tile's offsets in klist_s
+    __shared__ int32_t off_s[kWideMaxK * 3];
+    __shared__ uint32_t tmask_s;
+    const int K = src.K;
+    if (tid == 0) tmask_s = 0u;
+    for (int j = tid; j < 3 * K; j += 128) off_s[j] = src.offsets[j];
+    __syncthreads();
     const int64_t r = t * kGemmBM + tid;
-    drow_s[tid] = r < n_dst ? rows[r] : -1;
-  }
-  if (tid < nk) klist_s[tid] = src.klist[t * src.K + tid];
-  {
-    // the tile's sources, offset-major as the plan stores them: thread tid takes row tid of every offset,
-    // all loads in flight together
-    const int32_t* tm = src.tmap + t * (int64_t)src.K * kGemmBM + tid;
-    int32_t v[kWideMaxK];
-#pragma unroll
-    for (int j = 0; j < kWideMaxK; ++j) v[j] = j < nk ? tm[j * kGemmBM] : -1;
-#pragma unroll
-    for (int j = 0; j < kWideMaxK; ++j)
-      if (j < nk) src_s[j][tid] = (int64_t)v[j] >= n_src ? -1 : v[j];
+    drow_s[tid] = r < n_dst ? (int32_t)r : -1;
+    uint32_t m = 0u;
+    if (r < n_dst) {
+      int64_t b, x, y, z;
+      load_coord(src.coords, r, b, x, y, z);
+      subm_neighbours(src.ix, b, x, y, z, off_s, K, subm_unit_offsets(off_s, K), [&](int k, int32_t v) {
+        v = (int64_t)v >= n_src ? -1 : v;
+        src_s[k][tid] = v;
+        m |= (v >= 0 ? 1u : 0u) << k;
+      });
+    } else {
+      for (int k = 0; k < K; ++k) src_s[k][tid] = -1;
+    }
+    if (m) atomicOr(&tmask_s, m);
+    __syncthreads();
+    const uint32_t tm = tmask_s;
+    nk = __popc(tm);
+    if (tid < K && ((tm >> tid) & 1u)) klist_s[__popc(tm & ((1u << tid) - 1u))] = (int16_t)tid;
   }
   __syncthreads();
 
@@ -113,9 +163,10 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
   auto issue_a = [&](int i, auto slot) {
     constexpr int SL = decltype(slot)::value;
     bool any = false;
+    const int si = S::kTiled ? i : klist_s[i];
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-      const int32_t sv = src_s[i][wid * 64 + m * 16 + c];
+      const int32_t sv = src_s[si][wid * 64 + m * 16 + c];
       any |= sv >= 0;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s)
@@ -245,13 +296,24 @@ inline bool wide_ok(int Kd, int Nd, int K, size_t esz, bool x3, int64_t n_src, c
          (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
 }
 
-template <typename T, bool X3, typename E>
-inline void launch_wide(const T* A, int64_t n_src, const TiledSrc& src, const int32_t* rows, const T* Bt, T* out,
+// Shapes the wide kernel takes for a brick-index gather (FlySrc), where the
+// alternative is a hash-table probe per (row, offset) in the four-wave
+// kernels: every built width but split fp32 at 128 x 128 (the register
+// overflow above); same operand limits as wide_ok.
+inline bool fly_ok(int Kd, int Nd, int K, size_t esz, bool x3, int64_t n_src, const void* A, const void* Bt) {
+  const bool built = (Kd == 64 || Kd == 128) && (Nd == 64 || Nd == 128);
+  return built && !(x3 && Kd == 128 && Nd == 128) && K > 0 && K <= kWideMaxK && (uintptr_t)A % 16 == 0 &&
+         (uintptr_t)Bt % 16 == 0 && n_src * Kd * (int64_t)esz < (1ll << 31) - 64 &&
+         (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
+}
+
+template <typename T, bool X3, typename E, typename S>
+inline void launch_wide(const T* A, int64_t n_src, const S& src, const int32_t* rows, const T* Bt, T* out,
                         E epi, int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
   const unsigned grid = (unsigned)((n_dst + kGemmBM - 1) / kGemmBM);
-#define ST_WIDE(KD, BN)                                                                                      \
-  gather_gemm_wide_kernel<T, X3, KD, BN, 2, E><<<grid, 128, 0, stream>>>(A, src, rows, Bt, out, n_src, n_dst, \
-                                                                          epi)
+#define ST_WIDE(KD, BN)                                                                                         \
+  gather_gemm_wide_kernel<T, X3, KD, BN, 2, E, S><<<grid, 128, 0, stream>>>(A, src, rows, Bt, out, n_src, n_dst, \
+                                                                             epi)
   if (Kd == 64 && Nd == 64)
     ST_WIDE(64, 64);
   else if (Kd == 64 && Nd == 128)

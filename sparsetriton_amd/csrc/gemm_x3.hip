@@ -30,6 +30,23 @@ int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, cons
   return launch_gather_x3(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 
+int ops_gather_fly_x3(const float* A, int64_t n, const void* coords, int coord_dtype, const int32_t* offsets, int K,
+                      const SubmIndex& ix, const float* Bt, float* out, const float* bias, int Kd, int Nd,
+                      hipStream_t stream) {
+  if (!fly_ok(Kd, Nd, K, sizeof(float), true, n, A, Bt)) return ST_ERR_UNSUPPORTED;
+  const BiasEpi<float> epi{bias};
+  if (coord_dtype == ST_COORD_I16)
+    launch_wide<float, true>(A, n, FlySrc<int16_t>{(const int16_t*)coords, offsets, ix, K}, nullptr, Bt, out, epi, n,
+                             Kd, Nd, stream);
+  else if (coord_dtype == ST_COORD_I32)
+    launch_wide<float, true>(A, n, FlySrc<int32_t>{(const int32_t*)coords, offsets, ix, K}, nullptr, Bt, out, epi, n,
+                             Kd, Nd, stream);
+  else
+    return ST_ERR_UNSUPPORTED;
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
+
 int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,
                        const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
                        int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,

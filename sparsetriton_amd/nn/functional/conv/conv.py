@@ -26,9 +26,9 @@ from sparsetriton_amd.config import ConvAlgo, MIN_TABLE_FACTOR, get_conv_algo, g
 from sparsetriton_amd.tensor import SparseTensor
 from sparsetriton_amd.utils.hash import HashTable
 
-from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, InputGradLookup
+from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, ConvSubmFlyGEMM, InputGradLookup, subm_fly_ok
 from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM, conv_forward_epilogue
-from .kmap import KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map, subm_kernel_map
+from .kmap import BrickIndex, KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map, subm_kernel_map
 
 __all__ = ["sparse_conv3d", "compute_neighbor_indices", "table_capacity"]
 
@@ -191,6 +191,18 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
             out_feats = conv_forward_epilogue(tensor.F, weight, kmap, bias, *epilogue)
         else:
             out_feats = ConvPrecomputedNeighborGEMM.apply(tensor.F, weight, kmap, bias)
+    elif algo == ConvAlgo.ImplicitHashFlyGEMM and _brick_index(tensor, subm_fast and k % 2 == 1, K, C_in, C_out):
+        # submanifold, odd kernel, built shape: lookups in the coordinates' brick index inside the GEMM
+        index = _brick_index(tensor, True, K, C_in, C_out)
+        table_status = index.status
+        out_coords, new_shape = tensor.C, tensor.spatial_shape
+        if out_coords.shape[0] == 0:
+            _raise_table_errors(table_status, None)
+            return _empty(tensor, C_out, new_shape)
+        offsets = _target_offsets(k, d, p, False, device)
+        out_feats = ConvSubmFlyGEMM.apply(tensor.F, weight, index, offsets)
+        if bias is not None:
+            out_feats = out_feats + bias.to(out_feats.dtype)  # as the hash-probing branch below
     elif algo == ConvAlgo.ImplicitHashFlyGEMM:
         hkey = ("hashfly",) + cache_key
         hit = tensor._cache.kmaps.get(hkey)
@@ -231,6 +243,19 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
                                                    and torch.equal(out_coords, tensor.C))):
         return tensor.replace(out_feats)
     return SparseTensor(feats=out_feats, coords=out_coords, spatial_shape=new_shape, batch_size=tensor.batch_size)
+
+
+def _brick_index(tensor: SparseTensor, eligible: bool, K: int, C_in: int, C_out: int):
+    """The tensor's cached brick index when the hash-fly algorithm can look a submanifold
+    convolution's neighbours up in it (``st_subm_fly_gemm`` built for the shape, box indexable),
+    else None.  The index depends on the coordinates only, so every layer over them shares it."""
+    if not eligible or tensor.C.dtype not in (torch.int16, torch.int32) or \
+            not subm_fly_ok(C_in, C_out, K, tensor.F.dtype):
+        return None
+    key = ("brick_index",)
+    if key not in tensor._cache.kmaps:
+        tensor._cache.kmaps[key] = BrickIndex.build(tensor.C, tensor.batch_size, tensor.spatial_shape)
+    return tensor._cache.kmaps[key]
 
 
 def _raise_table_errors(status, table) -> None:

@@ -17,6 +17,13 @@ finds them from an input row).  Given both, the input gradient probes that
 table; without them it builds the transposed map once from the forward
 lookups.  The weight gradient probes the input table once per (row, offset)
 into a map that lives only for the backward call and walks its pair list.
+
+``ConvSubmFlyGEMM`` is the same algorithm for a submanifold convolution with
+the lookups in the coordinates' brick index (``BrickIndex``) instead of the
+table: the index answers a lookup from L2 in three dependent loads where a
+table probe reads a random line of a table several times larger, and the
+GEMM's prologue looks up its whole tile before the MFMA loop, skipping
+offsets none of the tile's rows has.
 """
 
 import ctypes
@@ -30,9 +37,9 @@ from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import 
     wgrad,
     wgrad_splits,
 )
-from sparsetriton_amd.nn.functional.conv.kmap import KernelMap, row_representatives
+from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex, KernelMap, row_representatives
 
-__all__ = ["ConvHashOnTheFlyImplicitGEMM", "InputGradLookup"]
+__all__ = ["ConvHashOnTheFlyImplicitGEMM", "ConvSubmFlyGEMM", "InputGradLookup", "subm_fly_ok"]
 
 
 def _lookup(K: int, sign: int, mul: int, div: int, bounds, row_bounds=(0, 0, 0)) -> _lib.Lookup:
@@ -176,3 +183,75 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
             grad_weights = wgrad(features, grad_output, kmap, weights.dtype,
                                  pairs=kmap.pair_list(with_tiles=False))
         return grad_input, grad_weights, None, None, None, None, None, None, None, None
+
+
+def subm_fly_ok(C_in: int, C_out: int, K: int, dtype: torch.dtype) -> bool:
+    """Whether ``st_subm_fly_gemm`` is built for both directions of a C_in -> C_out convolution."""
+    code = _lib.compute_code(dtype)
+    lib = _lib.lib()
+    return bool(lib.st_subm_fly_ok(C_in, C_out, K, code)) and bool(lib.st_subm_fly_ok(C_out, C_in, K, code))
+
+
+def subm_fly_gemm(A: torch.Tensor, index: BrickIndex, offsets_i32: torch.Tensor, Bt: torch.Tensor) -> torch.Tensor:
+    """out[r] = sum_k A[nbr(k, r)] @ Bt[k]^T over the submanifold neighbours found in ``index``."""
+    n, Kd, Nd = index.n, A.shape[1], Bt.shape[1]
+    out = torch.empty((n, Nd), dtype=A.dtype, device=A.device)
+    _lib.call("st_subm_fly_gemm", _lib.ptr(A), _lib.ptr(index.coords), _lib.coord_code(index.coords.dtype), n,
+              _lib.ptr(offsets_i32), offsets_i32.shape[0], *index.geometry, _lib.ptr(index.work), index.nbytes,
+              _lib.ptr(Bt), None, _lib.ptr(out), Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+    return out
+
+
+class ConvSubmFlyGEMM(torch.autograd.Function):
+    """Submanifold convolution (out = in coordinates, stride 1, odd kernel: offsets t and -t at k
+    and K-1-k) with no stored kernel map: every GEMM looks its neighbours up in ``index``.
+
+    Forward and, when the map is its own transpose (unique coordinates inside the box), the input
+    gradient run ``st_subm_fly_gemm`` (the latter with the weights reversed); the weight gradient --
+    and the input gradient otherwise -- take a map queried from the index that lives only for
+    the backward call."""
+
+    @staticmethod
+    def forward(ctx, features, weights, index: BrickIndex, kernel_offsets):
+        _lib.require_device(features, "features")
+        K, C_in, C_out = weights.shape
+        assert C_in == features.shape[1], f"weights C_in ({C_in}) != features C_in ({features.shape[1]})"
+        assert kernel_offsets.shape[0] == K, "kernel_offsets rows must equal the kernel volume"
+        assert features.shape[0] == index.n, "features rows must equal the indexed coordinates"
+        features = features.contiguous()
+        offs = kernel_offsets.to(torch.int32).contiguous()
+        wt = weight_prep(weights.to(features.dtype).contiguous(), _lib.W_TRANSPOSE)
+        out = subm_fly_gemm(features, index, offs, wt)
+        ctx.save_for_backward(features, weights, offs)
+        ctx.index = index
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        features, weights, offs = ctx.saved_tensors
+        index = ctx.index
+        K = weights.shape[0]
+        grad_output = grad_output.to(features.dtype).contiguous()
+        grad_input = grad_weights = None
+        maps = []  # queried once from the index, held until this function returns
+
+        def queried() -> KernelMap:
+            if not maps:
+                maps.append(index.query(offs))
+            return maps[0]
+
+        if ctx.needs_input_grad[0]:
+            w = weights.to(features.dtype).contiguous()
+            if index.transposable():
+                grad_input = subm_fly_gemm(grad_output, index, offs, weight_prep(w, _lib.W_REVERSE))
+            else:
+                n = index.n
+                kmap = KernelMap(queried().nbr, n, n, K)
+                kmap.set_row_representatives(row_representatives(index.coords))  # repeated coordinates
+                kmap.ensure_inverse()
+                grad_input = gather_gemm(kmap.fold_output_rows(grad_output), kmap.invnbr, n, 1, kmap.in_masks, w,
+                                         n, K)
+        if ctx.needs_input_grad[1]:
+            kmap = queried()
+            grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=kmap.pair_list(with_tiles=False))
+        return grad_input, grad_weights, None, None

@@ -641,6 +641,60 @@ def subm_kernel_map(coords: torch.Tensor, batch_size: int, spatial_shape, kernel
     return km, snap
 
 
+
+class BrickIndex:
+    """Brick index of a coordinate set over the box [0, batch_size) x [0, spatial_shape)
+    (``st_subm_index``): what a submanifold lookup needs -- ``st_kmap_subm_query`` builds maps
+    from it, ``st_subm_fly_gemm`` looks neighbours up in it inside the GEMM.  ``status`` (a
+    StatusSnapshot) holds the build's bad-coordinate / duplicate / out-of-box counts."""
+
+    def __init__(self, coords, batch_size, spatial_shape, work, nbytes, status):
+        self.coords = coords
+        self.geometry = (int(batch_size),) + tuple(int(v) for v in spatial_shape)
+        self.work, self.nbytes, self.status = work, int(nbytes), status
+
+    @classmethod
+    def build(cls, coords: torch.Tensor, batch_size: int, spatial_shape) -> Optional["BrickIndex"]:
+        """The index, or None when the box cannot be indexed (see ``subm_kernel_map``)."""
+        from sparsetriton_amd.utils.hash import StatusSnapshot
+
+        coords = coords.contiguous()
+        dev = coords.device
+        _lib.require_device(coords, "coordinates")
+        n = coords.shape[0]
+        sx, sy, sz = (int(v) for v in spatial_shape)
+        nbytes = _subm_workspace_bytes(int(n), int(batch_size), sx, sy, sz)
+        if nbytes < 0:
+            return None
+        work = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=dev)
+        status = (torch.empty if n else torch.zeros)((_lib.STATUS_WORDS,), dtype=torch.int32, device=dev)
+        _lib.call("st_subm_index", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, int(batch_size), sx, sy, sz,
+                  _lib.ptr(work), nbytes, _lib.ptr(status), _lib.stream_of(dev))
+        return cls(coords, batch_size, spatial_shape, work, nbytes, StatusSnapshot(status))
+
+    @property
+    def n(self) -> int:
+        return self.coords.shape[0]
+
+    def transposable(self) -> bool:
+        """Whether a submanifold map of an odd kernel over these coordinates is its own transpose
+        (offsets reversed): every coordinate unique and inside the box (waits for the counts)."""
+        c = self.status.counters()
+        return c["duplicate"] == 0 and c["out_of_box"] == 0
+
+    def query(self, kernel_offsets: torch.Tensor) -> KernelMap:
+        """The (K, n) submanifold map and its row masks from the index (``st_kmap_subm_query``)."""
+        n = self.n
+        K = kernel_offsets.shape[0]
+        dev = self.coords.device
+        nbr = torch.empty((K, n), dtype=torch.int32, device=dev)
+        masks = torch.empty((n, _mask_words(K)), dtype=torch.int32, device=dev)
+        offs = _offsets_i32(kernel_offsets)
+        _lib.call("st_kmap_subm_query", _lib.ptr(self.coords), _lib.coord_code(self.coords.dtype), n, _lib.ptr(offs),
+                  K, *self.geometry, _lib.ptr(self.work), self.nbytes, _lib.ptr(nbr), _lib.ptr(masks),
+                  _lib.stream_of(dev))
+        return KernelMap(nbr, n, n, K, out_masks=masks)
+
 class OutCoordTable:
     """Dedup table of a strided / transposed build: output coordinate -> output row."""
 

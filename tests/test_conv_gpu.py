@@ -248,6 +248,75 @@ def test_hashfly_equals_precomputed(device):
     assert rel(res[0][2].cpu(), res[1][2].cpu()) < 1e-6
 
 
+@pytest.mark.parametrize("case", ["in_box", "out_of_box", "duplicates", "both"])
+@pytest.mark.parametrize("cin,cout,dtype,d", [(64, 64, torch.bfloat16, 1), (128, 128, torch.bfloat16, 1),
+                                              (64, 128, torch.float32, 1), (128, 64, torch.float16, 1),
+                                              (64, 64, torch.float32, 2)])
+def test_subm_brick_fly_path(device, case, cin, cout, dtype, d):
+    """Hash-fly submanifold convolutions at built shapes look neighbours up in the brick index
+    inside the GEMM (ConvSubmFlyGEMM).  Forward, dX and dW against the float64 oracle; the
+    forward and the weight gradient bitwise equal to the precomputed path (same per-row
+    offset order, same pair list); the input gradient through the reversed-weight fly GEMM
+    (unique coordinates in the box) or the transposed map queried from the index."""
+    from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex
+    rng = np.random.default_rng(37 + cin + d)
+    n, S = 3000, 20
+    c = _rand_coords(rng, n, S)
+    shape = (S, S, S)
+    if case in ("out_of_box", "both"):
+        shape = (15, 18, 20)
+    if case in ("duplicates", "both"):
+        rows = rng.choice(n, 150, replace=False)
+        c[rows[75:]] = c[rows[:75]]
+    X = rng.standard_normal((n, cin)).astype(np.float32)
+    W = (rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cin)).astype(np.float32)
+    dY = rng.standard_normal((n, cout)).astype(np.float32)
+    res = {}
+    for algo in ConvAlgo:
+        set_conv_algo(algo)
+        feats = torch.as_tensor(X, device=device).to(dtype).requires_grad_(True)
+        w = torch.as_tensor(W, device=device).to(dtype).requires_grad_(True)
+        sp = SparseTensor(feats, torch.as_tensor(c, device=device), spatial_shape=shape, batch_size=2)
+        out = sparse_conv3d(sp, w, 3, dilation=d)
+        out.F.backward(torch.as_tensor(dY, device=device).to(dtype))
+        res[algo] = (out.F.detach(), feats.grad, w.grad)
+        if algo == ConvAlgo.ImplicitHashFlyGEMM:
+            index = sp._cache.kmaps[("brick_index",)]
+            assert isinstance(index, BrickIndex)  # the fly path ran
+            assert index.transposable() == (case == "in_box")
+    set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)
+    fly, pre = res[ConvAlgo.ImplicitHashFlyGEMM], res[ConvAlgo.PrecomputedNeighborGEMM]
+    assert torch.equal(fly[0], pre[0])
+    assert torch.equal(fly[2], pre[2])
+    Xq = torch.as_tensor(X).to(dtype).float().numpy()
+    Wq = torch.as_tensor(W).to(dtype).float().numpy()
+    dYq = torch.as_tensor(dY).to(dtype).float().numpy()
+    y, gx, gw = _oracle(c, c, shape, Xq, Wq, dYq, 3, 1, d, d, False)
+    tol = TOL[dtype]
+    assert rel(fly[0].float().cpu(), y) < tol
+    assert rel(fly[1].float().cpu(), gx) < tol, case
+    assert rel(fly[2].float().cpu(), gw) < tol
+    assert rel(fly[1].float().cpu(), pre[1].float().cpu()) < tol / 4
+
+
+def test_brick_index_query_equals_subm_map(device):
+    """st_subm_index + st_kmap_subm_query give st_kmap_subm's map and masks; the index's status
+    words count the same duplicates and out-of-box rows."""
+    from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex, _target_offsets, subm_kernel_map
+    rng = np.random.default_rng(38)
+    c = _rand_coords(rng, 5000, 24)
+    c[:40] = c[40:80]
+    coords = torch.as_tensor(c, device=device)
+    for shape, d in (((24, 24, 24), 1), ((20, 24, 22), 2)):
+        offs = _target_offsets(3, d, d, False, device)
+        km, snap = subm_kernel_map(coords, 2, shape, offs, symmetric=False)
+        index = BrickIndex.build(coords, 2, shape)
+        q = index.query(offs)
+        assert torch.equal(q.nbr, km.nbr) and torch.equal(q.out_masks, km.out_masks)
+        assert index.status.counters() == snap.counters()
+        if shape == (24, 24, 24):  # (repeats outside a smaller box are not indexed, so not counted)
+            assert snap.counters()["duplicate"] == 40 and snap.counters()["out_of_box"] == 0
+
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
 def test_probing_weight_gradient_entry(device, dtype, tol):
     """st_hashfly_wgrad, which probes the table inside the weight-gradient kernel (the autograd
