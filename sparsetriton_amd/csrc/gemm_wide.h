@@ -63,14 +63,16 @@ inline int gather_wide_mode() {
   return mode;
 }
 
-template <typename T, bool X3, int KD, int BN, int D, typename E, typename S>
-__global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restrict__ A, S src,
-                                                               const int32_t* __restrict__ rows,
-                                                               const T* __restrict__ Bt, T* __restrict__ out,
-                                                               int64_t n_src, int64_t n_dst, E epi) {
+template <typename T, bool X3, int KD, int BN, int D, typename E, typename S, int TP>
+__global__ __launch_bounds__(128 * TP) void gather_gemm_wide_kernel(const T* __restrict__ A, S src,
+                                                                    const int32_t* __restrict__ rows,
+                                                                    const T* __restrict__ Bt, T* __restrict__ out,
+                                                                    int64_t n_src, int64_t n_dst, E epi) {
   static_assert(X3 == std::is_same<T, float>::value, "fp32 runs split, 16-bit types direct");
+  static_assert(TP == 1 || TP == 2, "one or two tiles per workgroup");
   using L16 = typename std::conditional<X3, __bf16, T>::type;  // LDS / MFMA element
   using F16 = typename Frag<L16>::type;                          // 8 x 16-bit MFMA operand
+  constexpr int NT = 128 * TP;                                   // threads
   constexpr int KSTEPS = KD / 32;
   constexpr int NBLK = BN / 16;
   constexpr int MB = 4;
@@ -78,69 +80,101 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
   constexpr int BRPB = 16 / CV > 0 ? 16 / CV : 1;  // B rows per 256 bytes
   constexpr int PLANES = X3 ? 2 : 1;
   constexpr int GCH = X3 ? KD / 4 : KD / 8;  // 16-byte global chunks per B row
-  constexpr int BREGS = BN * GCH / 128;
+  constexpr int BREGS = BN * GCH / NT;
   constexpr int AH = X3 ? 2 : 1;  // 16-byte loads per A fragment
-  static_assert(KD % 32 == 0 && BN % 16 == 0 && (BN * GCH) % 128 == 0, "wide tile shape");
+  static_assert(KD % 32 == 0 && BN % 16 == 0 && (BN * GCH) % NT == 0, "wide tile shape");
   static_assert(D >= 2 && D <= 3, "ring depth 2..3");
   using GV = typename std::conditional<X3, v4f, F16>::type;  // one 16-byte global load
 
   __shared__ __attribute__((aligned(16))) L16 bt_s[2][PLANES][BN * KD];
-  __shared__ int32_t src_s[kWideMaxK][kGemmBM];
-  __shared__ int32_t drow_s[kGemmBM];
-  __shared__ int16_t klist_s[kWideMaxK];
+  __shared__ int32_t src_s[TP][kWideMaxK][kGemmBM];  // per tile: sources by list position (tiled) or offset (fly)
+  __shared__ int32_t drow_s[TP][kGemmBM];
+  __shared__ int16_t klist_s[TP][kWideMaxK];  // per tile's offset list (tiled)
+  __shared__ int16_t uk_s[kWideMaxK];         // the workgroup's offsets: the union of its tiles'
+  __shared__ int8_t pos_s[TP][kWideMaxK];     // per union offset and tile: its src_s index, -1 if absent
+  __shared__ uint32_t tmask_s[TP];
+  __shared__ int nk_s[TP];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const RingTile tile = ring_tile(n_dst, BN, BN);
-  const int64_t t = tile.rt;
-  if (t * kGemmBM >= n_dst) return;
-  int nk;
+  const int hw = wid >> 1, wt = wid & 1;       // the wave's tile and its 64-row half
+  const int ht = tid >> 7, r = tid & 127;      // the thread's tile and row in the prologue
+  // tiles in descending order (the mask sort puts the rows with the most neighbours last); with
+  // two tiles per workgroup, tiles 2p and 2p + 1
+  const int64_t nrt = (n_dst + kGemmBM - 1) / kGemmBM;
+  int64_t t0;
+  if constexpr (TP == 1) {
+    const RingTile tile = ring_tile(n_dst, BN, BN);
+    t0 = tile.rt;
+    if (t0 * kGemmBM >= n_dst) return;
+  } else {
+    t0 = 2 * ((nrt + 1) / 2 - 1 - (int64_t)blockIdx.x);
+  }
+  const int64_t th = t0 + ht;  // this thread's tile
+  const bool tvalid = th < nrt;
+  if (tid < TP) tmask_s[tid] = 0u;
 
   if constexpr (S::kTiled) {
-    nk = src.nk[t];
+    const int nkh = tvalid ? src.nk[th] : 0;
+    if (r == 0) nk_s[ht] = nkh;
     {
-      const int64_t r = t * kGemmBM + tid;
-      drow_s[tid] = r < n_dst ? rows[r] : -1;
+      const int64_t gr = th * kGemmBM + r;
+      drow_s[ht][r] = (tvalid && gr < n_dst) ? rows[gr] : -1;
     }
-    if (tid < nk) klist_s[tid] = src.klist[t * src.K + tid];
+    if (r < nkh) klist_s[ht][r] = src.klist[th * src.K + r];
     {
-      // the tile's sources, offset-major as the plan stores them: thread tid takes row tid of every offset,
+      // the tile's sources, offset-major as the plan stores them: thread r takes row r of every offset,
       // all loads in flight together
-      const int32_t* tm = src.tmap + t * (int64_t)src.K * kGemmBM + tid;
+      const int32_t* tm = src.tmap + th * (int64_t)src.K * kGemmBM + r;
       int32_t v[kWideMaxK];
 #pragma unroll
-      for (int j = 0; j < kWideMaxK; ++j) v[j] = j < nk ? tm[j * kGemmBM] : -1;
+      for (int j = 0; j < kWideMaxK; ++j) v[j] = j < nkh ? tm[j * kGemmBM] : -1;
 #pragma unroll
       for (int j = 0; j < kWideMaxK; ++j)
-        if (j < nk) src_s[j][tid] = (int64_t)v[j] >= n_src ? -1 : v[j];
+        if (j < nkh) src_s[ht][j][r] = (int64_t)v[j] >= n_src ? -1 : v[j];
+    }
+    __syncthreads();
+    if (tid < TP) {
+      uint32_t m = 0u;
+      for (int j = 0; j < nk_s[tid]; ++j) m |= 1u << klist_s[tid][j];
+      tmask_s[tid] = m;
     }
   } else {
-    // sources by offset (src_s[k]), the tile's offsets in klist_s
+    // sources by offset (src_s[.][k])
     __shared__ int32_t off_s[kWideMaxK * 3];
-    __shared__ uint32_t tmask_s;
     const int K = src.K;
-    if (tid == 0) tmask_s = 0u;
-    for (int j = tid; j < 3 * K; j += 128) off_s[j] = src.offsets[j];
+    for (int j = tid; j < 3 * K; j += NT) off_s[j] = src.offsets[j];
     __syncthreads();
-    const int64_t r = t * kGemmBM + tid;
-    drow_s[tid] = r < n_dst ? (int32_t)r : -1;
+    const int64_t gr = th * kGemmBM + r;
+    drow_s[ht][r] = (tvalid && gr < n_dst) ? (int32_t)gr : -1;
     uint32_t m = 0u;
-    if (r < n_dst) {
+    if (tvalid && gr < n_dst) {
       int64_t b, x, y, z;
-      load_coord(src.coords, r, b, x, y, z);
+      load_coord(src.coords, gr, b, x, y, z);
       subm_neighbours(src.ix, b, x, y, z, off_s, K, subm_unit_offsets(off_s, K), [&](int k, int32_t v) {
         v = (int64_t)v >= n_src ? -1 : v;
-        src_s[k][tid] = v;
+        src_s[ht][k][r] = v;
         m |= (v >= 0 ? 1u : 0u) << k;
       });
     } else {
-      for (int k = 0; k < K; ++k) src_s[k][tid] = -1;
+      for (int k = 0; k < K; ++k) src_s[ht][k][r] = -1;
     }
-    if (m) atomicOr(&tmask_s, m);
-    __syncthreads();
-    const uint32_t tm = tmask_s;
-    nk = __popc(tm);
-    if (tid < K && ((tm >> tid) & 1u)) klist_s[__popc(tm & ((1u << tid) - 1u))] = (int16_t)tid;
+    if (m) atomicOr(&tmask_s[ht], m);
+  }
+  __syncthreads();
+  // the union of the tiles' offsets, ascending; per tile, where each sits in its sources
+  uint32_t um = 0u;
+#pragma unroll
+  for (int h = 0; h < TP; ++h) um |= tmask_s[h];
+  const int nk = __popc(um);
+  if (tid < kWideMaxK && ((um >> tid) & 1u)) {
+    const int i = __popc(um & ((1u << tid) - 1u));
+    uk_s[i] = (int16_t)tid;
+#pragma unroll
+    for (int h = 0; h < TP; ++h) {
+      const uint32_t mh = tmask_s[h];
+      pos_s[h][i] = ((mh >> tid) & 1u) ? (int8_t)(S::kTiled ? __popc(mh & ((1u << tid) - 1u)) : tid) : (int8_t)-1;
+    }
   }
   __syncthreads();
 
@@ -163,10 +197,10 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
   auto issue_a = [&](int i, auto slot) {
     constexpr int SL = decltype(slot)::value;
     bool any = false;
-    const int si = S::kTiled ? i : klist_s[i];
+    const int si = pos_s[hw][i];
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-      const int32_t sv = src_s[si][wid * 64 + m * 16 + c];
+      const int32_t sv = si >= 0 ? src_s[hw][si][wt * 64 + m * 16 + c] : -1;
       any |= sv >= 0;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s)
@@ -180,10 +214,10 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
     any_ring[SL] = __ballot(any) != 0ull;
   };
   auto issue_b = [&](int i) {
-    const int k = klist_s[i];
+    const int k = uk_s[i];
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
-      const int idx = tid + jb * 128;
+      const int idx = tid + jb * NT;
       const int nr = idx / GCH, cv = idx - nr * GCH;
       b_reg[jb] = load16<GV>(b_rsrc, ((k * BN + nr) * KD + cv * (16 / (int)sizeof(T))) * (int)sizeof(T));
     }
@@ -191,7 +225,7 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
   auto store_b = [&](int buf) {
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
-      const int idx = tid + jb * 128;
+      const int idx = tid + jb * NT;
       const int nr = idx / GCH, cv = idx - nr * GCH;
       if constexpr (X3) {
         v4bf hi, lo;
@@ -265,12 +299,12 @@ __global__ __launch_bounds__(128) void gather_gemm_wide_kernel(const T* __restri
 #pragma unroll
   for (int m = 0; m < MB; ++m)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int32_t drow = drow_s[wid * 64 + m * 16 + g * 4 + r];
+    for (int rr = 0; rr < 4; ++rr) {
+      const int32_t drow = drow_s[hw][wt * 64 + m * 16 + g * 4 + rr];
       if (drow < 0) continue;
       float ov[NBLK];
 #pragma unroll
-      for (int nb = 0; nb < NBLK; ++nb) ov[nb] = epi.apply(acc[m][nb][r], em[nb], ea[nb], drow, BN, nb * 16 + c);
+      for (int nb = 0; nb < NBLK; ++nb) ov[nb] = epi.apply(acc[m][nb][rr], em[nb], ea[nb], drow, BN, nb * 16 + c);
       T* orow = out + (int64_t)drow * BN;
 #pragma unroll
       for (int nb = 0; nb < NBLK; ++nb) orow[nb * 16 + c] = from_f32<T>(ov[nb]);
@@ -307,13 +341,30 @@ inline bool fly_ok(int Kd, int Nd, int K, size_t esz, bool x3, int64_t n_src, co
          (int64_t)K * Nd * Kd * (int64_t)esz < (1ll << 31) - 64;
 }
 
+// Tiles per workgroup: two at 128 x 128 (16-bit), where one B slice per offset then serves 256
+// rows (the B loads were a third of the address unit's work); ST_WIDE_TILES=1 / 2 overrides.
+inline int wide_tiles(int Kd, int Nd, bool x3) {
+  static int mode = -1;
+  if (mode < 0) {
+    const char* e = getenv("ST_WIDE_TILES");
+    mode = (e && e[0] == '1') ? 1 : (e && e[0] == '2') ? 2 : 0;
+  }
+  if (mode) return mode;
+  return (!x3 && Kd == 128 && Nd == 128) ? 2 : 1;
+}
+
 template <typename T, bool X3, typename E, typename S>
 inline void launch_wide(const T* A, int64_t n_src, const S& src, const int32_t* rows, const T* Bt, T* out,
                         E epi, int64_t n_dst, int Kd, int Nd, hipStream_t stream) {
-  const unsigned grid = (unsigned)((n_dst + kGemmBM - 1) / kGemmBM);
-#define ST_WIDE(KD, BN)                                                                                         \
-  gather_gemm_wide_kernel<T, X3, KD, BN, 2, E, S><<<grid, 128, 0, stream>>>(A, src, rows, Bt, out, n_src, n_dst, \
-                                                                             epi)
+  const int64_t nrt = (n_dst + kGemmBM - 1) / kGemmBM;
+  const int tp = wide_tiles(Kd, Nd, X3);
+#define ST_WIDE(KD, BN)                                                                                           \
+  if (tp == 2)                                                                                                    \
+    gather_gemm_wide_kernel<T, X3, KD, BN, 2, E, S, 2><<<(unsigned)((nrt + 1) / 2), 256, 0, stream>>>(            \
+        A, src, rows, Bt, out, n_src, n_dst, epi);                                                                \
+  else                                                                                                            \
+    gather_gemm_wide_kernel<T, X3, KD, BN, 2, E, S, 1><<<(unsigned)nrt, 128, 0, stream>>>(A, src, rows, Bt, out, \
+                                                                                          n_src, n_dst, epi)
   if (Kd == 64 && Nd == 64)
     ST_WIDE(64, 64);
   else if (Kd == 64 && Nd == 128)
