@@ -252,7 +252,7 @@ def _brick_index(tensor: SparseTensor, eligible: bool, K: int, C_in: int, C_out:
     if not eligible or tensor.C.dtype not in (torch.int16, torch.int32) or \
             not subm_fly_ok(C_in, C_out, K, tensor.F.dtype):
         return None
-    key = ("brick_index",)
+    key = ("brick_index", int(tensor.batch_size), tuple(int(v) for v in tensor.spatial_shape))
     if key not in tensor._cache.kmaps:
         tensor._cache.kmaps[key] = BrickIndex.build(tensor.C, tensor.batch_size, tensor.spatial_shape)
     return tensor._cache.kmaps[key]

@@ -281,7 +281,7 @@ def test_subm_brick_fly_path(device, case, cin, cout, dtype, d):
         out.F.backward(torch.as_tensor(dY, device=device).to(dtype))
         res[algo] = (out.F.detach(), feats.grad, w.grad)
         if algo == ConvAlgo.ImplicitHashFlyGEMM:
-            index = sp._cache.kmaps[("brick_index",)]
+            index = sp._cache.kmaps[("brick_index", 2, shape)]
             assert isinstance(index, BrickIndex)  # the fly path ran
             assert index.transposable() == (case == "in_box")
     set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)
