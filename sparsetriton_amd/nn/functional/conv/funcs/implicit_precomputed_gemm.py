@@ -23,6 +23,8 @@ Kernels (``libsparsetriton_amd.so``):
             equal-size chunks, fixed-order reduce.
 """
 
+import os
+
 import torch
 
 from sparsetriton_amd import _lib
@@ -147,13 +149,20 @@ def column_sum(Y: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     return out
 
 
-def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype, pairs=None) -> torch.Tensor:
+def wgrad_buffers(X: torch.Tensor, dY: torch.Tensor, pl, K: int, dw_dtype: torch.dtype):
+    """(partials, dW) for ``wgrad`` over the pair list ``pl``."""
+    C_in, C_out = X.shape[1], dY.shape[1]
+    partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
+    return partials, torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
+
+
+def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype, pairs=None,
+          buffers=None) -> torch.Tensor:
     """dW[k] = sum over pairs (i, o) of offset k of X[i]^T dY[o], over the map's pair list (or
-    ``pairs``, a PairList of it)."""
+    ``pairs``, a PairList of it); ``buffers`` from ``wgrad_buffers`` (else allocated here)."""
     K, C_in, C_out = kmap.K, X.shape[1], dY.shape[1]
     pl = kmap.pair_list() if pairs is None else pairs
-    partials = torch.empty((max(pl.max_chunks, 1) * C_in * C_out,), dtype=torch.float32, device=X.device)
-    dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
+    partials, dW = wgrad_buffers(X, dY, pl, K, dw_dtype) if buffers is None else buffers
     _lib.call("st_wgrad_pairs", _lib.ptr(X), X.shape[0], _lib.ptr(dY), dY.shape[0], pl.pairs_ptr,
               pl.kstart_ptr, pl.cstart_ptr, K, pl.chunk, pl.max_chunks, pl.corder_ptr, C_in, C_out,
               _lib.compute_code(X.dtype),
@@ -172,6 +181,30 @@ def wgrad_scan(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: tor
               K, C_in, C_out, _lib.feat_code(X.dtype), _lib.ptr(partials), splits, _lib.ptr(dW),
               _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
     return dW
+
+
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device: torch.device) -> "torch.cuda.Stream":
+    """One extra stream per device (default priority) for the weight gradient."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _SIDE_STREAMS:
+        _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return _SIDE_STREAMS[idx]
+
+
+def _concurrent_backward(X: torch.Tensor, C_out: int, n_rows: int) -> bool:
+    """Whether the weight gradient runs beside the input gradient.  At 16-bit 128 x 128 both run
+    one workgroup per CU (the two-tile wide gather, the 128 x 128 per-wave weight gradient), which
+    leaves issue slots the other kernel fills: config 5 step 2.65 -> 2.53 ms.  Elsewhere the kernels
+    already fill the CUs and the cross-stream waits cost more than the overlap gains (config 2 bf16
+    0.186 -> 0.21 ms, config 3 / 4 3-8 % slower).  ST_CONCURRENT_BACKWARD=0 / 2 forces it off / on."""
+    mode = os.environ.get("ST_CONCURRENT_BACKWARD", "1")
+    if mode in ("0", "2"):
+        return mode == "2"
+    return (X.dtype in (torch.bfloat16, torch.float16) and X.shape[1] % 128 == 0 and C_out % 128 == 0 and
+            n_rows >= 1 << 18)
 
 
 class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
@@ -206,12 +239,28 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
         kmap = ctx.kmap
         grad_output = grad_output.to(features.dtype).contiguous()
         grad_input = grad_weights = None
-        if ctx.needs_input_grad[0]:
+        if (ctx.needs_input_grad[0] and ctx.needs_input_grad[1] and
+                _concurrent_backward(features, weights.shape[2], min(kmap.n_in, kmap.n_out))):
+            # The two gradients are independent: the weight gradient runs on a second stream beside
+            # the input gradient (every buffer it touches is allocated on this stream first, and this
+            # stream waits for it before returning).
+            pl = kmap.pair_list()
+            bufs = wgrad_buffers(features, grad_output, pl, kmap.K, weights.dtype)
+            main = torch.cuda.current_stream(features.device)
+            side = _side_stream(features.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=pl, buffers=bufs)
             w = weights.to(features.dtype).contiguous()
-            # dX[i] = sum_k dY[invnbr[k, i]] @ W[k]^T: W[k] (C_in, C_out) is already the (Nd, Kd) operand.
             grad_input = gather_gemm_dgrad(grad_output, kmap, w)
-        if ctx.needs_input_grad[1]:
-            grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
+            main.wait_stream(side)
+        else:
+            if ctx.needs_input_grad[0]:
+                w = weights.to(features.dtype).contiguous()
+                # dX[i] = sum_k dY[invnbr[k, i]] @ W[k]^T: W[k] (C_in, C_out) is already the (Nd, Kd) operand.
+                grad_input = gather_gemm_dgrad(grad_output, kmap, w)
+            if ctx.needs_input_grad[1]:
+                grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
         grad_bias = None
         if ctx.bias_dtype is not None and len(ctx.needs_input_grad) > 3 and ctx.needs_input_grad[3]:
             grad_bias = column_sum(grad_output, ctx.bias_dtype)
