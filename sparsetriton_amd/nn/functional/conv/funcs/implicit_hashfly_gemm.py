@@ -32,9 +32,12 @@ import torch
 
 from sparsetriton_amd import _lib
 from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
+    _concurrent_backward,
+    _side_stream,
     gather_gemm,
     weight_prep,
     wgrad,
+    wgrad_buffers,
     wgrad_splits,
 )
 from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex, KernelMap, row_representatives
@@ -240,6 +243,22 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
                 maps.append(index.query(offs))
             return maps[0]
 
+        if (ctx.needs_input_grad[0] and ctx.needs_input_grad[1] and index.transposable() and
+                _concurrent_backward(features, weights.shape[2], index.n)):
+            # the weight gradient on a second stream beside the input gradient (its map, pair list and
+            # buffers allocated on this stream first; this stream waits for it before returning)
+            kmap = queried()
+            pl = kmap.pair_list(with_tiles=False)
+            bufs = wgrad_buffers(features, grad_output, pl, K, weights.dtype)
+            main = torch.cuda.current_stream(features.device)
+            side = _side_stream(features.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=pl, buffers=bufs)
+            w = weights.to(features.dtype).contiguous()
+            grad_input = subm_fly_gemm(grad_output, index, offs, weight_prep(w, _lib.W_REVERSE))
+            main.wait_stream(side)
+            return grad_input, grad_weights, None, None
         if ctx.needs_input_grad[0]:
             w = weights.to(features.dtype).contiguous()
             if index.transposable():
