@@ -229,6 +229,73 @@ int st_outcoords_emit(const void* in_coords, int coord_dtype, int64_t n, const i
                       int32_t* invnbr, uint32_t* out_masks, uint32_t* in_masks, st_stream_t stream);
 
 /*
+ * Brick-index form of st_outcoords_sizes / _plan / _emit: the same output
+ * coordinates in the same order (_build_out_coords_normal / _transposed,
+ * kmap.py:213-444), deduplicated without a hash table.  The candidates'
+ * output coordinates are indexed in 4x4x4 bricks of the output box
+ * [0, batches) x [0, g->out_shape) and each distinct one keeps its lowest
+ * candidate rank; a candidate whose rank is that minimum is the first
+ * occurrence.  kernel_size / dilation bound the candidates per input row (as
+ * in st_outcoords_sizes).  st_outcoords_brick_sizes fills the workspace bytes
+ * and the block-counter length (blocks of 256 candidate ranks), or returns
+ * ST_ERR_UNSUPPORTED when the box cannot be indexed (far larger than the
+ * candidates, or an output shape beyond 32768): the caller then uses the hash
+ * build.
+ */
+int st_outcoords_brick_sizes(int64_t n, const st_outgeom* g, int64_t batches, int64_t kernel_size,
+                             int64_t dilation, int64_t* workspace_bytes, int64_t* num_blocks);
+
+/*
+ * Pass 1 of 2: index, lowest ranks, per-block first-occurrence counts;
+ * block_counts (num_blocks + 1 int32) receives their exclusive scan and
+ * block_counts[num_blocks] = N_out.  status (ST_STATUS_WORDS int32, cleared by
+ * the call): ST_STATUS_OUT_OF_BOX counts candidates whose batch index lies
+ * outside [0, batches) -- the index cannot hold them, so a nonzero count means
+ * the caller must use the hash build instead.
+ */
+int st_outcoords_brick_plan(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                            const st_outgeom* g, int64_t batches, int64_t kernel_size, int64_t dilation,
+                            void* workspace, int64_t workspace_bytes, int32_t* block_counts, int64_t num_blocks,
+                            int32_t* status, st_stream_t stream);
+
+/*
+ * Pass 2 of 2: out_coords (N_out, 4) in the input's coordinate dtype; also
+ * records each output's row in the workspace for st_outcoords_brick_inverse.
+ */
+int st_outcoords_brick_emit(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                            const st_outgeom* g, int64_t batches, int64_t kernel_size, int64_t dilation,
+                            void* workspace, int64_t workspace_bytes, const int32_t* block_counts,
+                            int64_t num_blocks, void* out_coords, int64_t n_out, st_stream_t stream);
+
+/*
+ * Kernel map of a strided / transposed convolution by query, the
+ * reference's compute_neighbor_indices over the output coordinates
+ * (conv.py:12-75, 180-188): for output row o and offset k the input
+ * coordinate (b, o * s - t_k), or transposed (b, (o - t_k) / s) when s
+ * divides every component, looked up in the brick index of the n_in input
+ * rows (st_subm_index over [0, batches) x g->in_shape; a repeated coordinate
+ * resolves to its lowest row).  Writes nbr (K, n_out) and out_masks
+ * (n_out, W) whole: the map st_outcoords_emit writes with the
+ * input-coordinate table.
+ */
+int st_kmap_strided_query(const void* out_coords, int coord_dtype, int64_t n_out, const int32_t* offsets,
+                          const st_outgeom* g, int64_t batches, const void* in_index, int64_t in_index_bytes,
+                          int64_t n_in, int32_t* nbr, uint32_t* out_masks, st_stream_t stream);
+
+/*
+ * The transposed map of the same convolution after st_outcoords_brick_emit
+ * (same arguments and workspace), input-major: invnbr (K, n) = output row of
+ * candidate (input i, offset k), -1 when the filters drop it or row i is not
+ * the row the query resolves its coordinate to (in_index as for
+ * st_kmap_strided_query), and in_masks (n, W); both written whole -- the
+ * invnbr / in_masks st_outcoords_emit writes.
+ */
+int st_outcoords_brick_inverse(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
+                               const st_outgeom* g, int64_t batches, int64_t kernel_size, int64_t dilation,
+                               const void* workspace, int64_t workspace_bytes, const void* in_index,
+                               int64_t in_index_bytes, int32_t* invnbr, uint32_t* in_masks, st_stream_t stream);
+
+/*
  * Transposed kernel map of an arbitrary map nbr (k, o) -> i (strides as in
  * st_kmap_query): invnbr[k * n_in + i] = o (offset-major), in_masks (n_in, W) row masks of
  * invnbr, and, if out_masks is non-null, out_masks (n_out, W) row masks of

@@ -15,6 +15,7 @@ import torch
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsetriton_amd.so"
 
 ST_OK = 0
+ERR_UNSUPPORTED = -3
 ERRORS = {-1: "invalid argument", -2: "HIP runtime error", -3: "unsupported dtype or size"}
 
 COORD_DTYPES = {torch.int16: 0, torch.int32: 1, torch.int64: 2}
@@ -74,6 +75,11 @@ _SIGNATURES = {
     "st_outcoords_plan": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _L, _P, _L, _P, _P],
     "st_outcoords_emit": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _P, _L, _P, _L, _P, _P, _L, _P, _L,
                           _P, _P, _P, _P, _P],
+    "st_outcoords_brick_sizes": [_L, ctypes.POINTER(OutGeom), _L, _L, _L, ctypes.POINTER(_L), ctypes.POINTER(_L)],
+    "st_outcoords_brick_plan": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _L, _L, _L, _P, _L, _P, _L, _P, _P],
+    "st_outcoords_brick_emit": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _L, _L, _L, _P, _L, _P, _L, _P, _L, _P],
+    "st_kmap_strided_query": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _L, _P, _L, _L, _P, _P, _P],
+    "st_outcoords_brick_inverse": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _L, _L, _L, _P, _L, _P, _L, _P, _P, _P],
     "st_kmap_invert": [_P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P],
     "st_kmap_sort_workspace": [_L, ctypes.POINTER(ctypes.c_size_t)],
     "st_kmap_sort_rows": [_P, _I, _I, _L, _P, _P, _P, _P, ctypes.c_size_t, _P],

@@ -69,6 +69,54 @@ __device__ __forceinline__ bool subm_unit_offsets(const int32_t* off_s, int K) {
   return unit;
 }
 
+// The rows of the coordinates (b, q) that q_of(k, qx, qy, qz) yields (false:
+// none), passed to emit(k, row) in ascending k = 0 .. K-1 (row -1: no
+// coordinate, outside the box or absent).  kSubmGroup lookups are in flight at
+// a time, each three dependent loads (level-1 entry; level-2 bits and base;
+// rowmap).
+template <typename Q, typename Emit>
+__device__ __forceinline__ void subm_lookup(const SubmIndex& ix, int64_t b, int K, Q&& q_of, Emit&& emit) {
+  for (int k0 = 0; k0 < K; k0 += kSubmGroup) {
+    int64_t brk[kSubmGroup];
+    int vb[kSubmGroup];
+    bool in[kSubmGroup];
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j) {
+      const int k = k0 + j;
+      in[j] = false;
+      brk[j] = 0;
+      vb[j] = 0;
+      int64_t qx, qy, qz;
+      if (k < K && q_of(k, qx, qy, qz) && subm_in_box(ix, b, qx, qy, qz)) {
+        in[j] = true;
+        brk[j] = subm_brick(ix, b, qx, qy, qz);
+        vb[j] = subm_vbit(qx, qy, qz);
+      }
+    }
+    SubmL1 e1[kSubmGroup];
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j) e1[j] = in[j] ? ix.l1[brk[j] >> 6] : SubmL1{0ull, 0, 0};
+    unsigned long long bits[kSubmGroup];
+    int32_t pre[kSubmGroup];
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j) {
+      in[j] = in[j] && ((e1[j].bits >> (brk[j] & 63)) & 1ull);
+      const int r = in[j] ? subm_brick_rank(e1[j], brk[j]) : 0;
+      bits[j] = in[j] ? ix.l2bits[r] : 0ull;
+      pre[j] = in[j] ? ix.l2pre[r] : 0;
+    }
+    int32_t rr[kSubmGroup];
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j) {
+      const bool has = in[j] && ((bits[j] >> vb[j]) & 1ull);
+      rr[j] = has ? ix.rowmap[pre[j] + (int)__popcll(bits[j] & below(vb[j]))] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j)
+      if (k0 + j < K) emit(k0 + j, rr[j]);
+  }
+}
+
 // The rows of (b, x, y, z) - off_s[k] for k = 0 .. K-1, passed to emit(k, row)
 // in ascending k (row -1: outside the box or absent).  kSubmGroup lookups are
 // in flight at a time, each three dependent loads (level-1 entry; level-2
@@ -134,47 +182,14 @@ __device__ __forceinline__ void subm_neighbours(const SubmIndex& ix, int64_t b, 
     }
     return;
   }
-  for (int k0 = 0; k0 < K; k0 += kSubmGroup) {
-    int64_t brk[kSubmGroup];
-    int vb[kSubmGroup];
-    bool in[kSubmGroup];
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
-      const int k = k0 + j;
-      in[j] = false;
-      brk[j] = 0;
-      vb[j] = 0;
-      if (k < K) {
-        const int64_t qx = x - off_s[3 * k], qy = y - off_s[3 * k + 1], qz = z - off_s[3 * k + 2];
-        if (subm_in_box(ix, b, qx, qy, qz)) {
-          in[j] = true;
-          brk[j] = subm_brick(ix, b, qx, qy, qz);
-          vb[j] = subm_vbit(qx, qy, qz);
-        }
-      }
-    }
-    SubmL1 e1[kSubmGroup];
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) e1[j] = in[j] ? ix.l1[brk[j] >> 6] : SubmL1{0ull, 0, 0};
-    unsigned long long bits[kSubmGroup];
-    int32_t pre[kSubmGroup];
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
-      in[j] = in[j] && ((e1[j].bits >> (brk[j] & 63)) & 1ull);
-      const int r = in[j] ? subm_brick_rank(e1[j], brk[j]) : 0;
-      bits[j] = in[j] ? ix.l2bits[r] : 0ull;
-      pre[j] = in[j] ? ix.l2pre[r] : 0;
-    }
-    int32_t rr[kSubmGroup];
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
-      const bool has = in[j] && ((bits[j] >> vb[j]) & 1ull);
-      rr[j] = has ? ix.rowmap[pre[j] + (int)__popcll(bits[j] & below(vb[j]))] : -1;
-    }
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j)
-      if (k0 + j < K) emit(k0 + j, rr[j]);
-  }
+  subm_lookup(ix, b, K,
+              [&](int k, int64_t& qx, int64_t& qy, int64_t& qz) {
+                qx = x - off_s[3 * k];
+                qy = y - off_s[3 * k + 1];
+                qz = z - off_s[3 * k + 2];
+                return true;
+              },
+              emit);
 }
 
 // Geometry of the index of n rows over [0, batches) x [0, sx) x [0, sy) x [0, sz);

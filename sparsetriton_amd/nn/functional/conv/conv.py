@@ -28,7 +28,8 @@ from sparsetriton_amd.utils.hash import HashTable
 
 from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, ConvSubmFlyGEMM, InputGradLookup, subm_fly_ok
 from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM, conv_forward_epilogue
-from .kmap import BrickIndex, KernelMap, _target_offsets, build_out_coords_and_map, query_kernel_map, subm_kernel_map
+from .kmap import (BrickIndex, KernelMap, _target_offsets, brick_out_coords_and_map, build_out_coords_and_map,
+                   query_kernel_map, subm_kernel_map)
 
 __all__ = ["sparse_conv3d", "compute_neighbor_indices", "table_capacity"]
 
@@ -175,9 +176,16 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
                     kmap = query_kernel_map(in_table, tensor.C, offsets, tensor.spatial_shape, 1,
                                             tensor.C.shape[0], symmetric=(k % 2 == 1))
             else:
-                in_table = _input_table(tensor, scale)
-                out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
-                    tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
+                # brick indexes of the candidates and of the inputs; the hash tables when a box cannot
+                # be indexed or a row's batch index lies outside the tensor's batch count
+                built = brick_out_coords_and_map(tensor.C, tensor.batch_size, tensor.spatial_shape, k, s, d, p,
+                                                 transposed)
+                if built is not None:
+                    out_coords, new_shape, _, kmap, table_status = built
+                else:
+                    in_table = _input_table(tensor, scale)
+                    out_coords, new_shape, _, kmap, _ = build_out_coords_and_map(
+                        tensor.C, tensor.spatial_shape, k, s, d, p, transposed, in_table=in_table, with_map=True)
             if built is None:
                 table_status = in_table.snapshot()
             tensor._cache.neighbor_indices[cache_key] = (out_coords, kmap, new_shape)

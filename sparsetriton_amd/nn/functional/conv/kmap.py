@@ -791,6 +791,87 @@ def build_out_coords_and_map(in_coords: torch.Tensor, spatial_shape, kernel_size
     return out_coords, torch.Size(new_shape), kernel_offsets, kmap, OutCoordTable(dkeys, slot_out)
 
 
+def brick_out_coords_and_map(in_coords: torch.Tensor, batch_size: int, spatial_shape, kernel_size: int,
+                             stride: int, dilation: int, padding: int, transposed: bool, with_map: bool = True,
+                             chunk_size: Optional[int] = None):
+    """``build_out_coords_and_map`` without hash tables: the same output coordinates in the same
+    order and the same map, through brick indexes (``st_outcoords_brick_*`` over the candidates'
+    output box, ``st_kmap_strided_query`` over the input coordinates' index).
+
+    Returns (out_coords, new_spatial_shape, kernel_offsets, kmap_or_None, status) -- ``status``
+    (a StatusSnapshot of the input index, or None without a map) carries the bad-coordinate count
+    the input hash table would report -- or None when the boxes cannot be indexed or a row's
+    batch index lies outside [0, batch_size); the caller then uses ``build_out_coords_and_map``.
+    One host synchronisation reads the output count.
+    """
+    from sparsetriton_amd.utils.hash import StatusSnapshot
+
+    dev = in_coords.device
+    _lib.require_device(in_coords, "coordinates")
+    in_coords = in_coords.contiguous()
+    n = in_coords.shape[0]
+    if n == 0 or batch_size < 1:
+        return None
+    offsets = _target_offsets(kernel_size, dilation, padding, transposed, dev)
+    K = offsets.shape[0]
+    if K > _lib.MAX_KVOL:
+        raise ValueError(f"kernel volume {K} exceeds the supported maximum {_lib.MAX_KVOL}")
+    new_shape = out_spatial_shape(spatial_shape, kernel_size, stride, dilation, padding, transposed)
+    g = _lib.OutGeom()
+    g.K = K
+    g.transposed = 1 if transposed else 0
+    g.stride = int(stride)
+    g.chunk = int(chunk_size) if chunk_size else 0
+    for a in range(3):
+        g.in_shape[a] = int(spatial_shape[a])
+        g.out_shape[a] = int(new_shape[a])
+    in_bytes = _subm_workspace_bytes(int(n), int(batch_size), *(int(v) for v in spatial_shape)) if with_map else 0
+    if in_bytes < 0:
+        return None
+    wbytes, nblocks = ctypes.c_int64(), ctypes.c_int64()
+    rc = _lib.lib().st_outcoords_brick_sizes(n, ctypes.byref(g), int(batch_size), int(kernel_size), int(dilation),
+                                            ctypes.byref(wbytes), ctypes.byref(nblocks))
+    if rc == _lib.ERR_UNSUPPORTED:
+        return None
+    _lib.check(rc, "st_outcoords_brick_sizes")
+    wbytes, nblocks = wbytes.value, nblocks.value
+    s = _lib.stream_of(dev)
+    cc = _lib.coord_code(in_coords.dtype)
+    work = torch.empty((wbytes,), dtype=torch.uint8, device=dev)
+    counts = torch.empty((nblocks + 1,), dtype=torch.int32, device=dev)
+    status = torch.empty((_lib.STATUS_WORDS,), dtype=torch.int32, device=dev)
+    offs = _offsets_i32(offsets)
+    _lib.call("st_outcoords_brick_plan", _lib.ptr(in_coords), cc, n, _lib.ptr(offs), ctypes.byref(g),
+              int(batch_size), int(kernel_size), int(dilation), _lib.ptr(work), wbytes, _lib.ptr(counts), nblocks,
+              _lib.ptr(status), s)
+    index = None
+    if with_map:
+        # the input index is queued before the host waits for the output count
+        index = BrickIndex.build(in_coords, batch_size, spatial_shape)
+    n_out, outside = torch.stack([counts[nblocks], status[_lib.STATUS_OUT_OF_BOX]]).tolist()
+    if outside:
+        return None
+    kernel_offsets = offsets.to(in_coords.dtype, copy=True)  # returned to the caller: not the shared tensor
+    out_coords = torch.empty((n_out, 4), dtype=in_coords.dtype, device=dev)
+    _lib.call("st_outcoords_brick_emit", _lib.ptr(in_coords), cc, n, _lib.ptr(offs), ctypes.byref(g),
+              int(batch_size), int(kernel_size), int(dilation), _lib.ptr(work), wbytes, _lib.ptr(counts), nblocks,
+              _lib.ptr(out_coords), n_out, s)
+    if not with_map:
+        return out_coords, torch.Size(new_shape), kernel_offsets, None, None
+    W = _mask_words(K)
+    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
+    invnbr = torch.empty((K, n), dtype=torch.int32, device=dev)
+    out_masks = torch.empty((n_out, W), dtype=torch.int32, device=dev)
+    in_masks = torch.empty((n, W), dtype=torch.int32, device=dev)
+    _lib.call("st_kmap_strided_query", _lib.ptr(out_coords), cc, n_out, _lib.ptr(offs), ctypes.byref(g),
+              int(batch_size), _lib.ptr(index.work), index.nbytes, n, _lib.ptr(nbr), _lib.ptr(out_masks), s)
+    _lib.call("st_outcoords_brick_inverse", _lib.ptr(in_coords), cc, n, _lib.ptr(offs), ctypes.byref(g),
+              int(batch_size), int(kernel_size), int(dilation), _lib.ptr(work), wbytes, _lib.ptr(index.work),
+              index.nbytes, _lib.ptr(invnbr), _lib.ptr(in_masks), s)
+    kmap = KernelMap(nbr, n, n_out, K, out_masks=out_masks, invnbr=invnbr, in_masks=in_masks)
+    return out_coords, torch.Size(new_shape), kernel_offsets, kmap, index.status
+
+
 def build_out_coords(
     in_coords: torch.Tensor,
     spatial_shape,
