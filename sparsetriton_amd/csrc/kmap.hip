@@ -506,6 +506,82 @@ __global__ __launch_bounds__(256) void pairs_emit_kernel(const int32_t* __restri
   }
 }
 
+// The same two passes for a map whose rows are contiguous (rs = 1) and whose
+// columns start 16-byte aligned: 16-byte loads, a wave reading 1 KB per
+// instruction.  Thread t covers rows base + 1024 q + 4 t .. + 3 for q = 0..3, so
+// row order is (q, thread, element) order.  With 4-byte loads these passes
+// read config 4's 768 MB map at ~3 TB/s.
+__device__ __forceinline__ int4 pair_load4(const int32_t* __restrict__ col, int64_t r, int64_t n_out) {
+  if (r + 4 <= n_out) return *reinterpret_cast<const int4*>(col + r);
+  int4 v = make_int4(-1, -1, -1, -1);
+  if (r < n_out) v.x = col[r];
+  if (r + 1 < n_out) v.y = col[r + 1];
+  if (r + 2 < n_out) v.z = col[r + 2];
+  return v;
+}
+
+__device__ __forceinline__ uint32_t pair_bits4(int4 v, int64_t n_in) {
+  return (pair_valid(v.x, n_in) ? 1u : 0u) | (pair_valid(v.y, n_in) ? 2u : 0u) | (pair_valid(v.z, n_in) ? 4u : 0u) |
+         (pair_valid(v.w, n_in) ? 8u : 0u);
+}
+
+__global__ __launch_bounds__(256) void pairs_count_vec_kernel(const int32_t* __restrict__ map, int64_t ks,
+                                                              int64_t n_out, int64_t n_in, int64_t nb,
+                                                              int32_t* __restrict__ counts) {
+  __shared__ int wsum_s[4];
+  const int k = blockIdx.y;
+  const int32_t* col = map + (int64_t)k * ks;
+  const int64_t r0 = (int64_t)blockIdx.x * kPairRows + 4 * threadIdx.x;
+  int4 v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = pair_load4(col, r0 + 1024 * q, n_out);
+  int c = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) c += __popc(pair_bits4(v[q], n_in));
+  c = wave_sum(c);
+  if ((threadIdx.x & 63) == 0) wsum_s[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[(int64_t)k * nb + blockIdx.x] = wsum_s[0] + wsum_s[1] + wsum_s[2] + wsum_s[3];
+}
+
+__global__ __launch_bounds__(256) void pairs_emit_vec_kernel(const int32_t* __restrict__ map, int64_t ks,
+                                                             int64_t n_out, int64_t n_in, int64_t nb,
+                                                             const int32_t* __restrict__ offsets,
+                                                             int32_t* __restrict__ pairs) {
+  __shared__ int wsum_s[4][4];  // [q][wave]
+  const int k = blockIdx.y;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int32_t* col = map + (int64_t)k * ks;
+  const int64_t r0 = (int64_t)blockIdx.x * kPairRows + 4 * threadIdx.x;
+  int4 v[4];
+  uint32_t m[4];
+  int ex[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[q] = pair_load4(col, r0 + 1024 * q, n_out);
+    m[q] = pair_bits4(v[q], n_in);
+    const int c = __popc(m[q]);
+    const int inc = wave_inclusive_scan(c);
+    ex[q] = inc - c;
+    if (lane == 63) wsum_s[q][wid] = inc;
+  }
+  __syncthreads();
+  int base = offsets[(int64_t)k * nb + blockIdx.x];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int pos = base + ex[q];
+    for (int w = 0; w < wid; ++w) pos += wsum_s[q][w];
+    const int32_t e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if ((m[q] >> j) & 1u) {
+        *reinterpret_cast<int2*>(pairs + 2 * (int64_t)pos) = make_int2(e[j], (int32_t)(r0 + 1024 * q + j));
+        ++pos;
+      }
+    base += wsum_s[q][0] + wsum_s[q][1] + wsum_s[q][2] + wsum_s[q][3];
+  }
+}
+
 }  // namespace st
 
 extern "C" int st_kmap_pairs_sizes(int64_t n_out, int K, int64_t* num_blocks) {
@@ -520,9 +596,20 @@ int launch_pairs(const int32_t* map, int64_t ks, int64_t rs, int64_t n_out, int 
                  int32_t* block_counts, int64_t nb, int chunk, int32_t* kstart, int32_t* cstart, int32_t* pairs,
                  hipStream_t stream) {
   const dim3 grid((unsigned)nb, (unsigned)K);
-  if (nb > 0) pairs_count_kernel<<<grid, 256, 0, stream>>>(map, ks, rs, n_out, n_in, nb, block_counts);
+  const bool vec = rs == 1 && ks % 4 == 0 && (reinterpret_cast<uintptr_t>(map) & 15) == 0;
+  if (nb > 0) {
+    if (vec)
+      pairs_count_vec_kernel<<<grid, 256, 0, stream>>>(map, ks, n_out, n_in, nb, block_counts);
+    else
+      pairs_count_kernel<<<grid, 256, 0, stream>>>(map, ks, rs, n_out, n_in, nb, block_counts);
+  }
   exclusive_scan_kernel<<<1, 1024, 0, stream>>>(block_counts, (int64_t)K * nb, PairsFinal{kstart, cstart, nb, K, chunk});
-  if (nb > 0) pairs_emit_kernel<<<grid, 256, 0, stream>>>(map, ks, rs, n_out, n_in, nb, block_counts, pairs);
+  if (nb > 0) {
+    if (vec)
+      pairs_emit_vec_kernel<<<grid, 256, 0, stream>>>(map, ks, n_out, n_in, nb, block_counts, pairs);
+    else
+      pairs_emit_kernel<<<grid, 256, 0, stream>>>(map, ks, rs, n_out, n_in, nb, block_counts, pairs);
+  }
   return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
 }
 }  // namespace st

@@ -388,6 +388,32 @@ def test_pair_list_chooses_its_chunk_size(device, n, S):
     dw = [wgrad(X, dY, kmap, torch.float32, pairs=q) for q in (auto, plan, fixed)]
     assert torch.equal(dw[0], dw[2]) and torch.equal(dw[1], dw[2])
 
+@pytest.mark.parametrize("n", [4096, 6000, 9001, 12288])
+def test_pair_list_wide_loads_equal_the_scalar_pass(device, n):
+    """A map with contiguous rows and 16-byte aligned columns takes the 16-byte-load count / emit
+    kernels; the same map with a padded column stride takes the 4-byte ones: identical lists
+    (pairs sorted by (offset, output row)), also across partial last row blocks."""
+    from sparsetriton_amd.nn.functional.conv.kmap import PairList
+    rng = np.random.default_rng(n)
+    K = 27
+    n_in = 5000
+    nbr = torch.as_tensor(rng.integers(-3 * n_in, n_in, size=(K, n)), dtype=torch.int32, device=device)
+    nbr[nbr < 0] = -1
+    nbr[3, ::7] = n_in + 5  # out-of-range sources are not pairs
+    padded = torch.full((K, n + 3), -1, dtype=torch.int32, device=device)
+    padded[:, :n] = nbr
+    for chunk in (-1, 1024):
+        a = PairList.build(nbr, n, 1, n, K, n_in, chunk)              # 16-byte loads when n % 4 == 0
+        b = PairList.build(padded, n + 3, 1, n, K, n_in, chunk)       # 4-byte loads
+        P = int(((nbr >= 0) & (nbr < n_in)).sum())
+        assert torch.equal(a.kstart, b.kstart) and torch.equal(a.cstart, b.cstart)
+        assert int(a.kstart[-1]) == P
+        assert torch.equal(a.pairs[:2 * P], b.pairs[:2 * P])
+        got = a.pairs[:2 * P].view(-1, 2).cpu().numpy()
+        ks, os_ = np.nonzero(((nbr >= 0) & (nbr < n_in)).cpu().numpy())
+        assert (got[:, 1] == os_).all() and (got[:, 0] == nbr.cpu().numpy()[ks, os_]).all()
+
+
 def test_one_call_plans_of_an_empty_map(device):
     from sparsetriton_amd.nn.functional.conv.kmap import MapPlan
     nbr = torch.empty((27, 0), dtype=torch.int32, device=device)
