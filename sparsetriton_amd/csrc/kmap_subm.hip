@@ -502,7 +502,7 @@ __global__ __launch_bounds__(256) void ocb_emit_kernel(const CT* __restrict__ co
 // ocb_inverse_kernel, input-major: scattered from here, its 4-byte stores
 // (14.2M on config 4) each cost a partial line (1.5 GB written per launch
 // against 0.85 GB of map), and atomic ORs into its masks serialised.
-constexpr int kQueryGroup = 8;  // a transposed stride-2 query row has at most 8 valid offsets
+constexpr int kQueryGroup = 4;  // lookups in flight per transposed query row (config 4 rows average 2 valid offsets)
 inline size_t query_lds_bytes(int K) { return sizeof(int32_t) * ((size_t)(K < 32 ? K : 32) * 256 + 4 * (size_t)K); }
 template <typename CT, bool TR>
 __global__ __launch_bounds__(256) void strided_query_kernel(const CT* __restrict__ out_coords, int64_t n_out,
