@@ -289,8 +289,8 @@ __global__ __launch_bounds__(kSubmThreads) void subm_query_kernel(const CT* __re
   };
   if (unit)
     unit_rows(ix, b, x, y, z, offsets, K, lds.bits, lds.pre, emit);
-  else
-    subm_neighbours(ix, b, x, y, z, off_s, K, false, emit);
+  else  // (small lookup groups: this path's registers set the kernel's occupancy)
+    subm_neighbours<3>(ix, b, x, y, z, off_s, K, false, emit);
 }
 
 // ------------------------------------- strided / transposed output coordinates
@@ -552,7 +552,7 @@ __global__ __launch_bounds__(256) void strided_query_kernel(const CT* __restrict
     if (unit)
       unit_rows(ix, b, x * g.s, y * g.s, z * g.s, offsets, K, lds.bits, lds.pre, emit);
     else
-      subm_neighbours(ix, b, x * g.s, y * g.s, z * g.s, off_s, K, false, emit);
+      subm_neighbours<3>(ix, b, x * g.s, y * g.s, z * g.s, off_s, K, false, emit);
     return;
   }
   // (o - t_k) / s: s divides it when o and t_k agree mod s on every axis, and then it is

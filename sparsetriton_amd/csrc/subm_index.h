@@ -73,15 +73,15 @@ __device__ __forceinline__ bool subm_unit_offsets(const int32_t* off_s, int K) {
 // none), passed to emit(k, row) in ascending k = 0 .. K-1 (row -1: no
 // coordinate, outside the box or absent).  kSubmGroup lookups are in flight at
 // a time, each three dependent loads (level-1 entry; level-2 bits and base;
-// rowmap).
-template <typename Q, typename Emit>
+// rowmap); G (default kSubmGroup) sets how many.
+template <int G = kSubmGroup, typename Q, typename Emit>
 __device__ __forceinline__ void subm_lookup(const SubmIndex& ix, int64_t b, int K, Q&& q_of, Emit&& emit) {
-  for (int k0 = 0; k0 < K; k0 += kSubmGroup) {
-    int64_t brk[kSubmGroup];
-    int vb[kSubmGroup];
-    bool in[kSubmGroup];
+  for (int k0 = 0; k0 < K; k0 += G) {
+    int64_t brk[G];
+    int vb[G];
+    bool in[G];
 #pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
+    for (int j = 0; j < G; ++j) {
       const int k = k0 + j;
       in[j] = false;
       brk[j] = 0;
@@ -93,26 +93,26 @@ __device__ __forceinline__ void subm_lookup(const SubmIndex& ix, int64_t b, int 
         vb[j] = subm_vbit(qx, qy, qz);
       }
     }
-    SubmL1 e1[kSubmGroup];
+    SubmL1 e1[G];
 #pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) e1[j] = in[j] ? ix.l1[brk[j] >> 6] : SubmL1{0ull, 0, 0};
-    unsigned long long bits[kSubmGroup];
-    int32_t pre[kSubmGroup];
+    for (int j = 0; j < G; ++j) e1[j] = in[j] ? ix.l1[brk[j] >> 6] : SubmL1{0ull, 0, 0};
+    unsigned long long bits[G];
+    int32_t pre[G];
 #pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
+    for (int j = 0; j < G; ++j) {
       in[j] = in[j] && ((e1[j].bits >> (brk[j] & 63)) & 1ull);
       const int r = in[j] ? subm_brick_rank(e1[j], brk[j]) : 0;
       bits[j] = in[j] ? ix.l2bits[r] : 0ull;
       pre[j] = in[j] ? ix.l2pre[r] : 0;
     }
-    int32_t rr[kSubmGroup];
+    int32_t rr[G];
 #pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
+    for (int j = 0; j < G; ++j) {
       const bool has = in[j] && ((bits[j] >> vb[j]) & 1ull);
       rr[j] = has ? ix.rowmap[pre[j] + (int)__popcll(bits[j] & below(vb[j]))] : -1;
     }
 #pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j)
+    for (int j = 0; j < G; ++j)
       if (k0 + j < K) emit(k0 + j, rr[j]);
   }
 }
@@ -123,7 +123,7 @@ __device__ __forceinline__ void subm_lookup(const SubmIndex& ix, int64_t b, int 
 // bits and base; rowmap), all L2-resident.  With unit offsets (the 3x3x3
 // kernel) the neighbours lie in the at most 2 x 2 x 2 bricks around the row,
 // each looked up once.
-template <typename Emit>
+template <int G = kSubmGroup, typename Emit>
 __device__ __forceinline__ void subm_neighbours(const SubmIndex& ix, int64_t b, int64_t x, int64_t y, int64_t z,
                                                 const int32_t* off_s, int K, bool unit, Emit&& emit) {
   if (unit) {
@@ -182,7 +182,7 @@ __device__ __forceinline__ void subm_neighbours(const SubmIndex& ix, int64_t b, 
     }
     return;
   }
-  subm_lookup(ix, b, K,
+  subm_lookup<G>(ix, b, K,
               [&](int k, int64_t& qx, int64_t& qy, int64_t& qz) {
                 qx = x - off_s[3 * k];
                 qy = y - off_s[3 * k + 1];
