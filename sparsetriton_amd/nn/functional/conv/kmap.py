@@ -10,9 +10,13 @@ Public functions keep the reference's names and meaning
   the neighbour lookup subtracts: input = output * stride - t_k.
 * ``build_out_coords`` -- (out_coords, new_spatial_shape, kernel_offsets).
 
-The output coordinates of a strided / transposed convolution and its kernel
-map come out of one HIP pipeline (``st_outcoords_plan`` / ``st_outcoords_emit``);
-the submanifold map comes from ``st_kmap_query``.  Maps are stored
+The output coordinates of a strided / transposed convolution come from a brick
+index of the candidates' output box (``st_outcoords_brick_*``) and its kernel
+map from a query of each output row in the inputs' brick index
+(``st_kmap_strided_query``, ``st_outcoords_brick_inverse``); where a box cannot
+be indexed, from hash tables (``st_outcoords_plan`` / ``st_outcoords_emit``).
+The submanifold map comes from the coordinates' brick index (``st_kmap_subm``),
+or the table query (``st_kmap_query``) for boxes too large for it.  Maps are stored
 offset-major (K, N) int32 with per-row offset bitmasks, in both directions:
 ``nbr[k, o]`` is the input row feeding output ``o`` through offset ``k`` and
 ``invnbr[k, i]`` the output row input ``i`` feeds.  Every kernel that walks rows
@@ -35,6 +39,7 @@ __all__ = [
     "compute_target_offsets_normal",
     "compute_target_offsets_transposed",
     "build_out_coords",
+    "brick_out_coords_and_map",
     "KernelMap",
     "query_kernel_map",
     "subm_kernel_map",
