@@ -31,6 +31,9 @@ GEOMS = [
     (3, 4, 1, 1, True),
     (5, 1, 2, 1, True),
     (2, 2, 0, 1, True),
+    (3, 3, 1, 1, True),  # a stride that is not a power of two: the query's division path
+    (3, 2, 2, 2, True),  # dilated offsets (-2, 0, 2) against stride 2
+    (4, 3, 1, 1, True),
 ]
 
 
