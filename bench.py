@@ -9,9 +9,11 @@ in HBM before timing starts.
 A step = one forward + backward (input and weight gradient) of the layer
 through the public API (``sparse_conv3d`` + autograd), with the kernel map
 already cached on the tensor -- as in a stack of submanifold layers, where it
-is built once per coordinate set.  The kernel-map build (hash insert +
-neighbour query in one cooperative launch + mask-sorted tile plan + pair list) is timed
-separately and reported as ``kmap_build_ms``.
+is built once per coordinate set.  The kernel-map build (the coordinates' brick
+index + neighbour query, mask-sorted tile plan, pair list) is timed separately and reported as
+``kmap_build_ms``.  Before each timed measurement the same work runs back to back, untimed,
+for ``SETTLE_MS`` of wall time (``clock_settle`` in the JSON line): the GPU's clocks ramp up
+under sustained load, and without it the timed window ran 6-10 % below the steady state.
 
 value = effective TFLOP/s = 6 * P * C_in * C_out / step time, P = exact number
 of (input, output, offset) pairs.  ``roofline`` covers the dominant kernel,
@@ -45,6 +47,27 @@ METRIC = "SubMConv3D k3 fwd+bwd effective TFLOP/s + kernel-map build ms, 1 MI355
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+SETTLE_MS = 60.0  # untimed back-to-back work before each timed GPU measurement
+
+
+def _settle(torch, fn, ms=SETTLE_MS):
+    """Run fn back to back for `ms` of wall time, untimed, and return the call count.  The GPU's
+    clocks ramp up under sustained load: a window timed right after the host's map builds and
+    data uploads ran 6-10 % slower than the steady state (config 2 fp32: 0.427 ms a step after 10
+    warm-up steps, 0.403 ms after 100 or 300; bf16 0.189 vs 0.171 ms).  A synchronisation every 16
+    calls keeps the host from queueing far ahead, so the wall time is GPU time."""
+    fn()  # (a first call may include one-time set-up: the clock starts after it)
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 1
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 
 
 def _events(torch, fn, reps):
@@ -292,6 +315,7 @@ def run_extra(args):
         P = km.num_pairs()
     dY = torch.randn(n_out, Cout, generator=g).to(dev, dtype)
     R = 3 if args.profile else 10
+    settled = {"ms": SETTLE_MS, "calls_before_first_call_timing": _settle(torch, build)}
     build_t = _events(torch, build, R)
 
     feats = sp.F
@@ -304,6 +328,7 @@ def run_extra(args):
         o = sparse_conv3d(sp, W, k, bias=b, stride=s, padding=p, transposed=tr, submanifold=subm)
         o.F.backward(dY)
 
+    settled["steps_before_step_timing"] = _settle(torch, step)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -324,8 +349,9 @@ def run_extra(args):
         f"first-call (map build + fwd) median {np.median(build_t):.3f} ms")
     line = {
         "metric": METRIC, "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": dts, "fp32_precision": args.fp32_precision if dts == "f32" else None,
+        "warmup": args.warmup, "clock_settle": settled, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dts,
+        "fp32_precision": args.fp32_precision if dts == "f32" else None,
         "data": "synthetic (seeded voxel set, N(0,1) features)",
         "config": {"workload": f"{args.workload}: {desc}", "voxels_in": N, "voxels_out": n_out, "pairs": P,
                    "C_in": Cin, "C_out": Cout, "seed": seed, "algorithm": algo},
@@ -389,6 +415,7 @@ def run_resnet(args):
         torch.autograd.backward([o.F for o in outs], grads)
 
     def timed(make, steps):
+        _settle(torch, lambda: step(make()))
         for _ in range(args.warmup):
             step(make())
         torch.cuda.synchronize()
@@ -408,6 +435,7 @@ def run_resnet(args):
     # ReLU run in its convolutions' GEMM stores (maps cached)
     model.eval()
     with torch.no_grad():
+        _settle(torch, lambda: model(cached))
         for _ in range(args.warmup):
             model(cached)
         torch.cuda.synchronize()
@@ -425,7 +453,8 @@ def run_resnet(args):
         f"inference forward (eval, fused epilogues) {ms_infer:.3f} ms")
     line = {
         "metric": METRIC, "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "clock_settle": {"ms": SETTLE_MS}, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak",
         "vs_baseline": None, "dtype": args.dtype,
         "fp32_precision": args.fp32_precision if args.dtype == "f32" else None,
         "data": "synthetic (seeded LiDAR-like voxel set, N(0,1) features, random-init weights)",
@@ -509,11 +538,28 @@ def main():
     for _ in range(3):
         build_kmap()
     torch.cuda.synchronize()
-    R = 3 if args.profile else 20
-    kmap_t = _events(torch, build_kmap, R)
     kmap = build_kmap()
     kmap.symmetric  # resolves the duplicate / out-of-box check
     P = kmap.num_pairs()
+
+    # the training step (forward + input and weight gradients through sparse_conv3d and autograd,
+    # the map cached on the tensor)
+    X = torch.as_tensor(X_np, device=dev).to(dtype)
+    dY = torch.as_tensor(dY_np, device=dev).to(dtype)
+    w = torch.as_tensor(W_np, device=dev).to(dtype).requires_grad_(True)
+    feats = X.clone().requires_grad_(True)
+    sp = SparseTensor(feats, coords, spatial_shape=shape, batch_size=4)
+    sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)] = (sp.C, kmap, sp.spatial_shape)
+
+    def step():
+        feats.grad = None
+        w.grad = None
+        out = sparse_conv3d(sp, w, 3)
+        out.F.backward(dY)
+
+    settled = {"ms": SETTLE_MS, "steps_before_map_timing": _settle(torch, step)}
+    R = 3 if args.profile else 20
+    kmap_t = _events(torch, build_kmap, R)
     log(f"pairs P={P} (P/N={P / N:.2f}); kmap build median {np.median(kmap_t):.3f} ms")
 
     # per-stage kernel timings of the map build
@@ -531,19 +577,7 @@ def main():
                      R) - np.median(q_t)
 
     # --------------------------------------------------------- train step
-    X = torch.as_tensor(X_np, device=dev).to(dtype)
-    dY = torch.as_tensor(dY_np, device=dev).to(dtype)
-    w = torch.as_tensor(W_np, device=dev).to(dtype).requires_grad_(True)
-    feats = X.clone().requires_grad_(True)
-    sp = SparseTensor(feats, coords, spatial_shape=shape, batch_size=4)
-    sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)] = (sp.C, kmap, sp.spatial_shape)
-
-    def step():
-        feats.grad = None
-        w.grad = None
-        out = sparse_conv3d(sp, w, 3)
-        out.F.backward(dY)
-
+    settled["steps_before_step_timing"] = _settle(torch, step)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -646,6 +680,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle": settled,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
