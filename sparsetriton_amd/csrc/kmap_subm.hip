@@ -716,7 +716,7 @@ static bool ocb_geom(int64_t n, const Geom& g, int64_t batches, int64_t kernel_s
     if (g.out_shape[a] < 1 || g.out_shape[a] > 32768) return false;  // every output packs into a key
   const int64_t nchunks = (g.K + g.chunk - 1) / g.chunk;
   *nranks = n * nchunks * (int64_t)g.chunk;
-  if (*nranks >= (1ll << 32) - 1) return false;
+  if (*nranks > (1ll << 32) - 512) return false;  // every thread's 32-bit rank, padding included, fits
   *rows = n * cands_per_input(g, kernel_size, dilation);
   const int64_t ws = subm_workspace_bytes(*rows, batches, g.out_shape[0], g.out_shape[1], g.out_shape[2]);
   if (ws < 0) return false;
