@@ -360,6 +360,124 @@ def run_extra(args):
     print(json.dumps(line), flush=True)
 
 
+def run_spatial(args):
+    """The section-8(f) ops beside the convolution -- pooling and upsampling (reference
+    nn/functional/spatial.py:26-535) and to_dense (utils/to_dense.py:30-282) -- on the config-2 voxel
+    set with 64 channels: each op's HIP kernels timed with events (after the clock settle) against
+    their algorithmic bytes and the HBM peak, one JSON line.  value = all ops' bytes over all ops'
+    time."""
+    import ctypes
+
+    import torch
+
+    from sparsetriton_amd import SparseTensor, _lib, workloads
+    from sparsetriton_amd.nn.functional import sparse_pooling
+    from sparsetriton_amd.utils.to_dense import to_dense
+
+    dev = torch.device("cuda:0")
+    dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
+    esz = 4 if args.dtype == "f32" else 2
+    fc = _lib.feat_code(dtype)
+    C = 64
+    g = torch.Generator().manual_seed(0)
+    coords_np, shape = workloads.config2(seed=0)
+    N = coords_np.shape[0]
+    coords = torch.as_tensor(coords_np, device=dev).to(torch.int16)
+    X = torch.randn(N, C, generator=g).to(dev, dtype)
+    st = _lib.stream_of(dev)
+    R = 3 if args.profile else 20
+    ops = {}
+
+    def record(name, fn, nbytes, note):
+        _settle(torch, fn, ms=20.0)
+        t = float(np.median(_events(torch, fn, R)))
+        gbps = nbytes / (t * 1e-3) / 1e9
+        ops[name] = {"ms": t, "algorithmic_bytes": int(nbytes), "GBps": gbps, "frac": gbps / PEAK["hbm_GBps"],
+                     "bytes_counted": note}
+        log(f"{name}: {t:.4f} ms, {nbytes / 1e6:.1f} MB -> {gbps:.0f} GB/s")
+
+    # pooling k2 s2: the plan (cells -> order keys -> stable radix sort -> run heads -> scan), then the
+    # value passes over its runs
+    nb = ctypes.c_size_t()
+    _lib.call("st_pool_workspace", N, ctypes.byref(nb))
+    ws = torch.empty((max(nb.value, 1),), dtype=torch.uint8, device=dev)
+    perm = torch.empty((N,), dtype=torch.int32, device=dev)
+    seg = torch.empty((N + 1,), dtype=torch.int32, device=dev)
+    inv = torch.empty((N,), dtype=torch.int32, device=dev)
+    oc = torch.empty((N, 4), dtype=coords.dtype, device=dev)
+    counts = torch.empty((2,), dtype=torch.int32, device=dev)
+
+    def plan():
+        _lib.call("st_pool_plan", _lib.ptr(coords), _lib.coord_code(coords.dtype), N, 2, 2, 0, _lib.ptr(ws),
+                  nb.value, _lib.ptr(perm), _lib.ptr(seg), _lib.ptr(inv), _lib.ptr(oc), _lib.ptr(counts), st)
+
+    plan()
+    n_out = int(counts[0].item())
+    # counted: its inputs and outputs only (coordinates read; perm, inverse, run starts and pooled
+    # coordinates written) -- not the sort's own passes; left out of the aggregate value
+    record("pool_plan_k2s2", plan, 8 * N + 12 * N + 8 * n_out,
+           "coordinates read, perm / inverse / run starts / pooled coordinates written (the sort's passes not "
+           "counted; not in the aggregate value)")
+    out = torch.empty((n_out, C), dtype=dtype, device=dev)
+    dout = torch.randn(n_out, C, generator=g).to(dev, dtype)
+    dx = torch.empty((N, C), dtype=dtype, device=dev)
+    for mode, mcode in (("max", 0), ("avg", 1)):
+        record(f"pool_{mode}_forward", lambda: _lib.call(
+            "st_pool_forward", _lib.ptr(X), C, fc, _lib.ptr(perm), _lib.ptr(seg), n_out, mcode, _lib.ptr(out), st),
+            esz * (N + n_out) * C + 4 * (N + n_out), "features read once, pooled rows written, perm + run starts")
+        extra = esz * (N + n_out) * C if mode == "max" else 0
+        record(f"pool_{mode}_backward", lambda: _lib.call(
+            "st_pool_backward", _lib.ptr(X), _lib.ptr(out), _lib.ptr(dout), N, C, fc, _lib.ptr(inv), _lib.ptr(seg),
+            mcode, _lib.ptr(dx), st),
+            esz * (n_out + N) * C + extra + 4 * (N + n_out),
+            "pooled gradient read once, input gradient written" + (", inputs and outputs re-read (argmax)"
+                                                                   if mode == "max" else "") + ", inverse + run starts")
+    # upsampling x2: every row to its 8 children
+    up = torch.empty((8 * N, C), dtype=dtype, device=dev)
+    upc = torch.empty((8 * N, 4), dtype=coords.dtype, device=dev)
+    record("upsample_x2_forward", lambda: _lib.call(
+        "st_upsample", _lib.ptr(X), _lib.ptr(coords), _lib.coord_code(coords.dtype), N, C, fc, 2, _lib.ptr(up),
+        _lib.ptr(upc), st), esz * 9 * N * C + 8 * 9 * N, "features read, 8 children written, coordinates alike")
+    dup = torch.randn(8 * N, C, generator=g).to(dev, dtype)
+    record("upsample_x2_backward", lambda: _lib.call(
+        "st_upsample_backward", _lib.ptr(dup), N, C, fc, 2, _lib.ptr(dx), st),
+        esz * 9 * N * C, "children's gradients read, summed rows written")
+    # to_dense of the set max-pooled by 8 (a dense head's input: 4 x 180 x 180 x 5 cells)
+    pooled = sparse_pooling(SparseTensor(X, coords, spatial_shape=shape, batch_size=4), 8, 0, 8, "max")
+    pc, pf = pooled.C, pooled.F.contiguous()
+    pshape = tuple(int(v) for v in pooled.spatial_shape)
+    cells = 4 * pshape[0] * pshape[1] * pshape[2]
+    grid = to_dense(pf, pc, pshape)
+    B, sx, sy, sz = 4, *pshape
+    # the C entry point (the Python wrapper first reads the batch count back to the host)
+    record("to_dense_forward", lambda: _lib.call(
+        "st_to_dense", _lib.ptr(pf), pf.shape[0], C, fc, _lib.ptr(pc), _lib.coord_code(pc.dtype), B, sx, sy, sz,
+        _lib.ptr(grid), st),
+        esz * cells * C + esz * pf.shape[0] * C + 8 * pf.shape[0],
+        "the whole grid written (zeros included), rows and coordinates read")
+    dgrid = torch.randn(tuple(grid.shape), generator=g).to(dev, dtype)
+    dpf = torch.empty_like(pf)
+    record("to_dense_backward", lambda: _lib.call(
+        "st_from_dense", _lib.ptr(dgrid), B, sx, sy, sz, C, fc, _lib.ptr(pc), _lib.coord_code(pc.dtype),
+        pf.shape[0], _lib.ptr(dpf), st),
+        2 * esz * pf.shape[0] * C + 8 * pf.shape[0], "the rows' cells gathered, rows written, coordinates read")
+    value_ops = [o for k, o in ops.items() if k != "pool_plan_k2s2"]
+    tot_b = sum(o["algorithmic_bytes"] for o in value_ops)
+    tot_t = sum(o["ms"] for o in value_ops)
+    value = tot_b / (tot_t * 1e-3) / 1e9
+    line = {
+        "metric": "sparse pooling / upsampling / to_dense HBM GB/s (algorithmic bytes), 1 MI355X", "value": value,
+        "unit": "GB/s", "n_gpus": 1, "steps": R, "warmup": 0, "clock_settle": {"ms": 20.0, "per_op": True},
+        "ms_per_step": tot_t, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.dtype, "data": "synthetic (config-2 voxel set, N(0,1) features)",
+        "config": {"workload": "spatial: max/avg pooling k2 s2, upsampling x2, to_dense of the set pooled by 8; "
+                               "64 channels", "voxels": N, "pooled_k2": n_out, "pooled_k8": int(pf.shape[0]),
+                   "dense_cells": cells, "channels": C},
+        "ops": ops, "hbm_peak_GBps": PEAK["hbm_GBps"],
+    }
+    print(json.dumps(line))
+
+
 def run_resnet(args):
     """SparseResNet21D (reference nn/backbones/resnet.py:81-109) forward + backward on the config-2
     voxel set with 4 input channels: 13 convolutions (4 strided), 13 per-sample batch norms with
@@ -477,7 +595,7 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="short run for counter collection: few repetitions, plus a 256 MiB device copy whose "
                          "HBM counters calibrate the per-kernel traffic figures")
-    ap.add_argument("--workload", choices=["config2", "resnet21d"] + sorted(EXTRA), default="config2",
+    ap.add_argument("--workload", choices=["config2", "resnet21d", "spatial"] + sorted(EXTRA), default="config2",
                     help="config2 is the headline; the others measure the other benchmark configurations")
     ap.add_argument("--fp32-precision", choices=["bf16x3", "ieee"], default="bf16x3",
                     help="fp32 matrix-core arithmetic (split-bf16 MFMA, the default, or IEEE fp32 MFMA)")
@@ -486,6 +604,8 @@ def main():
         if args.gpus != 1:
             print("bench.py: one GPU only", file=sys.stderr)
             sys.exit(2)
+        if args.workload == "spatial":
+            return run_spatial(args)
         return run_resnet(args) if args.workload == "resnet21d" else run_extra(args)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "

@@ -180,51 +180,63 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const T* __restrict_
   st_<T, V>(dfeats + r * C + c, g);
 }
 
-template <typename T, typename CT, int V>
+// Upsampling: thread per (child row, 16-byte feature vector) -- a wave stores
+// whole child rows, contiguous -- with 32-bit index arithmetic whenever the
+// thread count allows (I = uint32_t; 64-bit division costs ~100 instructions)
+// and each child's coordinate row as one vector store.
+template <typename CT>
+__device__ __forceinline__ void store_coord4(CT* __restrict__ p, CT b, CT x, CT y, CT z) {
+  typedef CT vt __attribute__((ext_vector_type(4)));
+  vt q;
+  q[0] = b;
+  q[1] = x;
+  q[2] = y;
+  q[3] = z;
+  *reinterpret_cast<vt*>(p) = q;
+}
+
+template <typename T, typename CT, int V, typename I>
 __global__ __launch_bounds__(256) void upsample_kernel(const T* __restrict__ feats, const CT* __restrict__ coords,
                                                        int64_t n, int C, int s, T* __restrict__ out_feats,
                                                        CT* __restrict__ out_coords) {
-  const int nv = C / V;
-  const int s3 = s * s * s;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n * s3 * nv) return;
-  const int64_t orow = i / nv;
+  const I nv = (I)(C / V);
+  const I s3 = (I)(s * s * s);
+  const I i = (I)blockIdx.x * 256 + threadIdx.x;
+  if ((int64_t)i >= n * (int64_t)s3 * (int64_t)nv) return;
+  const I orow = i / nv;
   const int c = (int)(i - orow * nv) * V;
-  const int64_t r = orow / s3;
+  const I r = orow / s3;
   const int q = (int)(orow - r * s3);
   float v[V];
-  ld<T, V>(feats + r * C + c, v);
-  st_<T, V>(out_feats + orow * C + c, v);
+  ld<T, V>(feats + (int64_t)r * C + c, v);
+  st_<T, V>(out_feats + (int64_t)orow * C + c, v);
   if (c == 0) {
     const int dx = q / (s * s), dy = (q / s) % s, dz = q % s;
-    const CT* ci = coords + r * 4;
-    CT* co = out_coords + orow * 4;
-    co[0] = ci[0];
-    co[1] = (CT)((int64_t)ci[1] * s + dx);
-    co[2] = (CT)((int64_t)ci[2] * s + dy);
-    co[3] = (CT)((int64_t)ci[3] * s + dz);
+    const CT* ci = coords + (int64_t)r * 4;
+    store_coord4<CT>(out_coords + (int64_t)orow * 4, ci[0], (CT)((int64_t)ci[1] * s + dx),
+                     (CT)((int64_t)ci[2] * s + dy), (CT)((int64_t)ci[3] * s + dz));
   }
 }
 
-template <typename T, int V>
+template <typename T, int V, typename I>
 __global__ __launch_bounds__(256) void upsample_backward_kernel(const T* __restrict__ dout, int64_t n, int C, int s,
                                                                 T* __restrict__ dfeats) {
-  const int nv = C / V;
+  const I nv = (I)(C / V);
   const int s3 = s * s * s;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n * nv) return;
-  const int64_t r = i / nv;
+  const I i = (I)blockIdx.x * 256 + threadIdx.x;
+  if ((int64_t)i >= n * (int64_t)nv) return;
+  const I r = i / nv;
   const int c = (int)(i - r * nv) * V;
   float acc[V];
 #pragma unroll
   for (int e = 0; e < V; ++e) acc[e] = 0.f;
   for (int q = 0; q < s3; ++q) {
     float v[V];
-    ld<T, V>(dout + (r * s3 + q) * C + c, v);
+    ld<T, V>(dout + ((int64_t)r * s3 + q) * C + c, v);
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[e] += v[e];
   }
-  st_<T, V>(dfeats + r * C + c, acc);
+  st_<T, V>(dfeats + (int64_t)r * C + c, acc);
 }
 
 // Workspace: keys, sorted keys (8 n bytes each), rows, sorted rows (perm is
@@ -401,16 +413,25 @@ int st_upsample(const void* feats, const void* coords, int coord_dtype, int64_t 
   if (n == 0) return ST_OK;
   if (!feats || !coords || !out_feats || !out_coords) return ST_ERR_ARG;
   const int64_t s3 = (int64_t)scale * scale * scale;
-  const bool v4 = vec4_ok(C, feats, out_feats);
   ST_DISPATCH_COORD(coord_dtype, CT, {
     ST_SP_DISPATCH(dtype, T, {
-      const unsigned g = st_blocks(n * s3 * (C / (v4 ? 4 : 1)), 256);
-      if (v4)
-        upsample_kernel<T, CT, 4><<<g, 256, 0, stream>>>((const T*)feats, (const CT*)coords, n, C, scale,
-                                                         (T*)out_feats, (CT*)out_coords);
+      constexpr int V = 16 / (int)sizeof(T);  // one 16-byte vector
+      const bool vec = C % V == 0 && (uintptr_t)feats % 16 == 0 && (uintptr_t)out_feats % 16 == 0;
+      const int64_t threads = n * s3 * (vec ? C / V : C);
+      const unsigned g = st_blocks(threads, 256);
+      const bool w32 = threads + 256 < (1ll << 32);
+      if (vec && w32)
+        upsample_kernel<T, CT, V, uint32_t><<<g, 256, 0, stream>>>((const T*)feats, (const CT*)coords, n, C, scale,
+                                                                   (T*)out_feats, (CT*)out_coords);
+      else if (vec)
+        upsample_kernel<T, CT, V, int64_t><<<g, 256, 0, stream>>>((const T*)feats, (const CT*)coords, n, C, scale,
+                                                                  (T*)out_feats, (CT*)out_coords);
+      else if (w32)
+        upsample_kernel<T, CT, 1, uint32_t><<<g, 256, 0, stream>>>((const T*)feats, (const CT*)coords, n, C, scale,
+                                                                   (T*)out_feats, (CT*)out_coords);
       else
-        upsample_kernel<T, CT, 1><<<g, 256, 0, stream>>>((const T*)feats, (const CT*)coords, n, C, scale,
-                                                         (T*)out_feats, (CT*)out_coords);
+        upsample_kernel<T, CT, 1, int64_t><<<g, 256, 0, stream>>>((const T*)feats, (const CT*)coords, n, C, scale,
+                                                                  (T*)out_feats, (CT*)out_coords);
     });
   });
   ST_CHECK_LAUNCH();
@@ -421,13 +442,20 @@ int st_upsample_backward(const void* dout, int64_t n, int C, int dtype, int scal
   if (n < 0 || C <= 0 || scale < 1) return ST_ERR_ARG;
   if (n == 0) return ST_OK;
   if (!dout || !dfeats) return ST_ERR_ARG;
-  const bool v4 = vec4_ok(C, dout, dfeats);
   ST_SP_DISPATCH(dtype, T, {
-    const unsigned g = st_blocks(n * (C / (v4 ? 4 : 1)), 256);
-    if (v4)
-      upsample_backward_kernel<T, 4><<<g, 256, 0, stream>>>((const T*)dout, n, C, scale, (T*)dfeats);
+    constexpr int V = 16 / (int)sizeof(T);  // one 16-byte vector
+    const bool vec = C % V == 0 && (uintptr_t)dout % 16 == 0 && (uintptr_t)dfeats % 16 == 0;
+    const int64_t threads = n * (vec ? C / V : C);
+    const unsigned g = st_blocks(threads, 256);
+    const bool w32 = threads + 256 < (1ll << 32);
+    if (vec && w32)
+      upsample_backward_kernel<T, V, uint32_t><<<g, 256, 0, stream>>>((const T*)dout, n, C, scale, (T*)dfeats);
+    else if (vec)
+      upsample_backward_kernel<T, V, int64_t><<<g, 256, 0, stream>>>((const T*)dout, n, C, scale, (T*)dfeats);
+    else if (w32)
+      upsample_backward_kernel<T, 1, uint32_t><<<g, 256, 0, stream>>>((const T*)dout, n, C, scale, (T*)dfeats);
     else
-      upsample_backward_kernel<T, 1><<<g, 256, 0, stream>>>((const T*)dout, n, C, scale, (T*)dfeats);
+      upsample_backward_kernel<T, 1, int64_t><<<g, 256, 0, stream>>>((const T*)dout, n, C, scale, (T*)dfeats);
   });
   ST_CHECK_LAUNCH();
   return ST_OK;
