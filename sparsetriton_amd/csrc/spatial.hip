@@ -180,10 +180,9 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const T* __restrict_
   st_<T, V>(dfeats + r * C + c, g);
 }
 
-// Upsampling: thread per (child row, 16-byte feature vector) -- a wave stores
-// whole child rows, contiguous -- with 32-bit index arithmetic whenever the
-// thread count allows (I = uint32_t; 64-bit division costs ~100 instructions)
-// and each child's coordinate row as one vector store.
+// Upsampling: 16-byte feature vectors, 32-bit index arithmetic whenever the
+// thread count allows (I = uint32_t; a 64-bit division costs ~100
+// instructions), each child's coordinate row as one vector store.
 template <typename CT>
 __device__ __forceinline__ void store_coord4(CT* __restrict__ p, CT b, CT x, CT y, CT z) {
   typedef CT vt __attribute__((ext_vector_type(4)));
@@ -199,22 +198,25 @@ template <typename T, typename CT, int V, typename I>
 __global__ __launch_bounds__(256) void upsample_kernel(const T* __restrict__ feats, const CT* __restrict__ coords,
                                                        int64_t n, int C, int s, T* __restrict__ out_feats,
                                                        CT* __restrict__ out_coords) {
+  // thread per (input row, vector): the vector is read once and stored into each of the row's s^3
+  // children -- for a given child the lanes of a row write one whole child row
   const I nv = (I)(C / V);
-  const I s3 = (I)(s * s * s);
+  const int s3 = s * s * s;
   const I i = (I)blockIdx.x * 256 + threadIdx.x;
-  if ((int64_t)i >= n * (int64_t)s3 * (int64_t)nv) return;
-  const I orow = i / nv;
-  const int c = (int)(i - orow * nv) * V;
-  const I r = orow / s3;
-  const int q = (int)(orow - r * s3);
+  if ((int64_t)i >= n * (int64_t)nv) return;
+  const I r = i / nv;
+  const int c = (int)(i - r * nv) * V;
   float v[V];
   ld<T, V>(feats + (int64_t)r * C + c, v);
-  st_<T, V>(out_feats + (int64_t)orow * C + c, v);
+  T* o = out_feats + (int64_t)r * s3 * C + c;
+  for (int q = 0; q < s3; ++q) st_<T, V>(o + (int64_t)q * C, v);
   if (c == 0) {
-    const int dx = q / (s * s), dy = (q / s) % s, dz = q % s;
     const CT* ci = coords + (int64_t)r * 4;
-    store_coord4<CT>(out_coords + (int64_t)orow * 4, ci[0], (CT)((int64_t)ci[1] * s + dx),
-                     (CT)((int64_t)ci[2] * s + dy), (CT)((int64_t)ci[3] * s + dz));
+    const CT b = ci[0];
+    const int64_t x = (int64_t)ci[1] * s, y = (int64_t)ci[2] * s, z = (int64_t)ci[3] * s;
+    CT* co = out_coords + (int64_t)r * s3 * 4;
+    for (int q = 0; q < s3; ++q)
+      store_coord4<CT>(co + 4 * q, b, (CT)(x + q / (s * s)), (CT)(y + (q / s) % s), (CT)(z + q % s));
   }
 }
 
@@ -417,7 +419,7 @@ int st_upsample(const void* feats, const void* coords, int coord_dtype, int64_t 
     ST_SP_DISPATCH(dtype, T, {
       constexpr int V = 16 / (int)sizeof(T);  // one 16-byte vector
       const bool vec = C % V == 0 && (uintptr_t)feats % 16 == 0 && (uintptr_t)out_feats % 16 == 0;
-      const int64_t threads = n * s3 * (vec ? C / V : C);
+      const int64_t threads = n * (vec ? C / V : C);  // (input row, vector) pairs
       const unsigned g = st_blocks(threads, 256);
       const bool w32 = threads + 256 < (1ll << 32);
       if (vec && w32)
