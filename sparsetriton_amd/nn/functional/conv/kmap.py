@@ -896,12 +896,21 @@ def build_out_coords(
     filters and are deduplicated, in first-occurrence order of the
     input-major / offset-minor candidate enumeration -- with ``chunk_size``
     offsets per chunk, chunk by chunk as the reference's loop
-    (``kmap.py:270-278``), the dedup table then sized by the distinct outputs
-    (see ``build_out_coords_and_map``).  Candidates are never materialised.
+    (``kmap.py:270-278``).  Deduplication runs through a brick index of the
+    candidates' output box (``brick_out_coords_and_map``), or, where the box
+    cannot be indexed, a hash table sized by the distinct outputs (see
+    ``build_out_coords_and_map``).  Candidates are never materialised.
     """
     offsets = _target_offsets(kernel_size, dilation, padding, transposed, in_coords.device).to(in_coords.dtype)
     if submanifold and stride == 1 and ((kernel_size - 1) * dilation) // 2 == padding:
         return in_coords, spatial_shape, offsets
+    if in_coords.shape[0] > 0:
+        # the brick build needs the batch count: one read of the largest batch index
+        batches = int(in_coords[:, 0].max().item()) + 1
+        built = brick_out_coords_and_map(in_coords, batches, spatial_shape, kernel_size, stride, dilation, padding,
+                                         transposed, with_map=False, chunk_size=chunk_size)
+        if built is not None:
+            return built[0], built[1], built[2]
     out_coords, new_shape, kernel_offsets, _, _ = build_out_coords_and_map(
         in_coords, spatial_shape, kernel_size, stride, dilation, padding, transposed, with_map=False,
         chunk_size=chunk_size)
