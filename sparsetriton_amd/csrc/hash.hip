@@ -18,6 +18,20 @@ __global__ void fill_kernel(T* __restrict__ dst, int64_t n, T value) {
   for (; i < n; i += step) dst[i] = value;
 }
 
+// Row of an inserted key: the thread whose CAS claimed the slot stores its row
+// with a plain store (one atomic per row instead of two, on unique rows); a
+// repeated key counts in the status and takes the atomic-min, which
+// hash_insert_fixup_kernel completes after the insert.
+__device__ __forceinline__ void store_row(uint32_t* __restrict__ vals, uint32_t s, uint32_t row, bool was_new,
+                                          int32_t* __restrict__ status) {
+  if (was_new) {
+    vals[s] = row;
+  } else {
+    atomicAdd(&status[ST_STATUS_DUPLICATE], 1);
+    atomicMin(&vals[s], row);
+  }
+}
+
 // One thread per coordinate row (utils/hash.py:203-258 restated with exact keys).
 template <typename CT>
 __global__ __launch_bounds__(256) void hash_insert_kernel(const CT* __restrict__ coords, int64_t n, int64_t scale,
@@ -38,8 +52,27 @@ __global__ __launch_bounds__(256) void hash_insert_kernel(const CT* __restrict__
     atomicAdd(&status[ST_STATUS_OVERFLOW], 1);
     return;
   }
-  if (!was_new) atomicAdd(&status[ST_STATUS_DUPLICATE], 1);
-  atomicMin(&vals[s], (uint32_t)i);
+  store_row(vals, s, (uint32_t)i, was_new, status);
+}
+
+// Repeated keys of an insert: the row stored by each key's slot winner may
+// have landed after a smaller row's atomic-min, so when the status counts any
+// repeat every row takes the atomic-min once more (probes read-only, the
+// table is complete); otherwise each workgroup reads one word and returns.
+template <typename CT>
+__global__ __launch_bounds__(256) void hash_insert_fixup_kernel(const CT* __restrict__ coords, int64_t n,
+                                                                int64_t scale, const uint64_t* __restrict__ keys,
+                                                                uint32_t* __restrict__ vals, uint32_t cap,
+                                                                const int32_t* __restrict__ status) {
+  if (status[ST_STATUS_DUPLICATE] == 0) return;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t b, x, y, z;
+    load_coord(coords, i, b, x, y, z);
+    uint64_t key;
+    if (!pack_key(b, x * scale, y * scale, z * scale, key)) continue;
+    const uint32_t s = find_slot(keys, cap, key);
+    if (s != ST_NO_VAL) atomicMin(&vals[s], (uint32_t)i);
+  }
 }
 
 template <typename CT>
@@ -226,8 +259,7 @@ __global__ __launch_bounds__(256) void hash_insert_group_kernel(const CT* __rest
     atomicAdd(&status[ST_STATUS_OVERFLOW], 1);
     return;
   }
-  if (!was_new) atomicAdd(&status[ST_STATUS_DUPLICATE], 1);
-  atomicMin(&vals[s], (uint32_t)i);
+  store_row(vals, s, (uint32_t)i, was_new, status);
 }
 
 template <typename CT>
@@ -357,6 +389,10 @@ int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale
                       hash_insert_kernel<CT><<<st_blocks(n, 256), 256, 0, stream>>>(
                           (const CT*)coords, n, scale, keys, vals, (uint32_t)capacity, status));
   }
+  const unsigned fg = st_blocks(n, 256) < 256 ? st_blocks(n, 256) : 256;
+  ST_DISPATCH_COORD(coord_dtype, CT,
+                    hash_insert_fixup_kernel<CT><<<fg, 256, 0, stream>>>((const CT*)coords, n, scale, keys, vals,
+                                                                         (uint32_t)capacity, status));
   ST_CHECK_LAUNCH();
   return ST_OK;
 }

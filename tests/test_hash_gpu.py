@@ -80,6 +80,21 @@ def test_duplicates_resolve_to_lowest_row(device):
         assert t.counters()["duplicate"] == 3
 
 
+def test_many_duplicates_resolve_to_lowest_row(device):
+    """Every key repeated three times across the whole launch (copies in shuffled order after the
+    originals): whichever row's CAS claims a slot, the table ends with the key's lowest row."""
+    rng = np.random.default_rng(7)
+    n = 60_000
+    lin = rng.choice(4 * 128 ** 3, n, replace=False)
+    c = np.stack([lin // 128 ** 3, (lin // 128 ** 2) % 128, (lin // 128) % 128, lin % 128], 1)
+    allc = np.concatenate([c, c[rng.permutation(n)], c[::-1]])
+    t = HashTable(capacity=3 * n, device=device)
+    t.insert(torch.as_tensor(allc, dtype=torch.int32, device=device))
+    assert t.counters()["duplicate"] == 2 * n
+    got = t.query(torch.as_tensor(c, dtype=torch.int32, device=device)).cpu().numpy()
+    assert (got == np.arange(n)).all()
+
+
 def test_unpackable_coordinates(device):
     c = torch.tensor([[0, 40000, 0, 0], [-1, 0, 0, 0], [0, 5, 5, 5]], dtype=torch.int32, device=device)
     t = HashTable(capacity=16, device=device)
