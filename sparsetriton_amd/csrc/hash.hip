@@ -32,6 +32,25 @@ __device__ __forceinline__ void store_row(uint32_t* __restrict__ vals, uint32_t 
   }
 }
 
+// insert_slot that claims by CAS at once instead of loading the slot first:
+// one memory round trip less per row on a mostly empty table, a CAS on every
+// occupied slot it passes (config 2, table at the default capacity: clear +
+// insert 53.3 -> 50.4 us)
+__device__ __forceinline__ uint32_t insert_slot_cas(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
+                                                    bool& was_new) {
+  uint32_t s = home_slot(key, cap);
+  for (uint32_t step = 0; step < cap; ++step) {
+    const unsigned long long old =
+        atomicCAS((unsigned long long*)&keys[s], (unsigned long long)ST_EMPTY_KEY, (unsigned long long)key);
+    if (old == ST_EMPTY_KEY || old == key) {
+      was_new = old == ST_EMPTY_KEY;
+      return s;
+    }
+    s = next_slot(s, cap);
+  }
+  return ST_NO_VAL;
+}
+
 // One thread per coordinate row (utils/hash.py:203-258 restated with exact keys).
 template <typename CT>
 __global__ __launch_bounds__(256) void hash_insert_kernel(const CT* __restrict__ coords, int64_t n, int64_t scale,
@@ -47,7 +66,7 @@ __global__ __launch_bounds__(256) void hash_insert_kernel(const CT* __restrict__
     return;
   }
   bool was_new = false;
-  uint32_t s = insert_slot(keys, cap, key, was_new);
+  uint32_t s = insert_slot_cas(keys, cap, key, was_new);
   if (s == ST_NO_VAL) {
     atomicAdd(&status[ST_STATUS_OVERFLOW], 1);
     return;
