@@ -100,9 +100,11 @@ int st_hash_probe_mode(int mode);
  * open-addressing table of `capacity` slots: keys (u64, packed coordinate,
  * all-ones = empty) and vals (u32 row index, all-ones = none).  The caller
  * clears both arrays to all-ones first (st_fill_u64 / st_fill_u32).  Linear
- * probing from a 64-bit-mixed home slot; the key is claimed by a 64-bit CAS,
- * the value by an atomic min, so duplicate coordinates resolve to the lowest
- * row index on every run.
+ * probing from a 64-bit-mixed home slot; the key is claimed by a 64-bit CAS
+ * and the claiming row stores its index; a repeated coordinate takes an atomic
+ * min, and a second pass queued by the same call (a no-op unless the status
+ * counts repeats) applies the min again after every store, so duplicate
+ * coordinates resolve to the lowest row index on every run.
  */
 int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale, uint64_t* keys, uint32_t* vals,
                    int64_t capacity, int32_t* status, st_stream_t stream);
