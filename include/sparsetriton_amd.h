@@ -253,6 +253,11 @@ int st_outcoords_brick_sizes(int64_t n, const st_outgeom* g, int64_t batches, in
  * block_counts[num_blocks] = N_out.  status (ST_STATUS_WORDS int32, cleared by
  * the call): ST_STATUS_OUT_OF_BOX counts candidates whose batch index lies
  * outside [0, batches) -- the index cannot hold them, so a nonzero count means
+ * the caller must use the hash build instead.  ST_STATUS_OVERFLOW is nonzero
+ * when the offsets reach more output bricks or voxels than kernel_size and
+ * dilation bound (offsets that are not that kernel's): the index is then
+ * sized too small, no array past its bound is written, N_out reads 0, emit
+ * writes nothing and st_outcoords_brick_inverse maps every candidate to -1;
  * the caller must use the hash build instead.
  */
 int st_outcoords_brick_plan(const void* in_coords, int coord_dtype, int64_t n, const int32_t* offsets,
@@ -585,12 +590,14 @@ typedef struct st_lookup {
  * The input gradient of a submanifold map that is its own transpose (status
  * DUPLICATE and OUT_OF_BOX zero, offsets symmetric) is the same call with the
  * weights of st_weight_prep(ST_W_REVERSE).  Bitwise equal to st_hashfly_gemm
- * and st_gather_gemm_tiled on the same rows.  st_subm_fly_ok(Kd, Nd, K,
+ * and st_gather_gemm_tiled on the same rows.  st_subm_fly_ok(n, Kd, Nd, K,
  * dtype) = 1 for the shapes built: Kd, Nd in {64, 128} (split fp32 not at
- * 128 x 128), K <= 27, dtype ST_BF16, ST_F16 or ST_F32_BF16X3; others (and
- * int64 coordinates) return ST_ERR_UNSUPPORTED.
+ * 128 x 128), K <= 27, dtype ST_BF16, ST_F16 or ST_F32_BF16X3, and n rows
+ * of Kd elements under 2^31 - 64 bytes (the kernel addresses its operands
+ * with 32-bit buffer offsets); others (and int64 coordinates) return
+ * ST_ERR_UNSUPPORTED.  Host arithmetic only: it touches no device.
  */
-int st_subm_fly_ok(int Kd, int Nd, int K, int dtype);
+int st_subm_fly_ok(int64_t n, int Kd, int Nd, int K, int dtype);
 int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
                      int64_t batches, int64_t sx, int64_t sy, int64_t sz, const void* index, int64_t index_bytes,
                      const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype, st_stream_t stream);

@@ -353,10 +353,12 @@ int st_wgrad_pairs(const void* X, int64_t n_in, const void* dY, int64_t n_out, c
                                        chunk, max_chunks, C_in, C_out, partials, dW, dw_dtype, stream));
 }
 
-int st_subm_fly_ok(int Kd, int Nd, int K, int dtype) {
+int st_subm_fly_ok(int64_t n, int Kd, int Nd, int K, int dtype) {
   if (dtype != ST_BF16 && dtype != ST_F16 && dtype != ST_F32_BF16X3) return 0;
-  // alignment and operand sizes are checked per call; 16 is the alignment torch allocations have
-  return fly_ok(Kd, Nd, K, dtype == ST_F32_BF16X3 ? 4 : 2, dtype == ST_F32_BF16X3, 1, nullptr, nullptr) ? 1 : 0;
+  if (n < 0) return 0;
+  // the operand sizes of n rows (the wide kernel's 32-bit buffer offsets); alignment is checked
+  // per call, 16 bytes being the alignment torch allocations have
+  return fly_ok(Kd, Nd, K, dtype == ST_F32_BF16X3 ? 4 : 2, dtype == ST_F32_BF16X3, n, nullptr, nullptr) ? 1 : 0;
 }
 
 int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
@@ -364,7 +366,7 @@ int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t
                      const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype, st_stream_t stream) {
   const int64_t need = subm_workspace_bytes(n, batches, sx, sy, sz);
   if (need < 0 || index_bytes < need || K <= 0 || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
-  if (!st_subm_fly_ok(Kd, Nd, K, dtype)) return ST_ERR_UNSUPPORTED;
+  if (!st_subm_fly_ok(n, Kd, Nd, K, dtype)) return ST_ERR_UNSUPPORTED;
   if (n == 0) return ST_OK;
   if (!A || !coords || !offsets || !index || !Bt || !out) return ST_ERR_ARG;
   SubmIndex ix;

@@ -24,6 +24,7 @@ __global__ __launch_bounds__(kSubmThreads) void subm_clear_kernel(SubmIndex ix, 
   const int64_t stride = (int64_t)gridDim.x * kSubmThreads;
   const int64_t t = (int64_t)blockIdx.x * kSubmThreads + threadIdx.x;
   if (status && t < ST_STATUS_WORDS) status[t] = 0;
+  if (ix.flag && t == 0) *ix.flag = 0;
   uint4* occ16 = reinterpret_cast<uint4*>(ix.occ);  // the byte array is padded to 16 bytes
   for (int64_t e = t; e < (ix.nbricks + 15) / 16; e += stride) occ16[e] = make_uint4(0u, 0u, 0u, 0u);
   for (int64_t e = t; e < n; e += stride) ix.rowmap[e] = 0x7FFFFFFF;
@@ -63,6 +64,7 @@ __device__ __forceinline__ int subm_entry_count(const SubmIndex& ix, int64_t e) 
 template <bool BRICKS>
 __global__ __launch_bounds__(kSubmThreads) void subm_tile_sum_kernel(SubmIndex ix) {
   __shared__ int red_s[4];
+  if (!BRICKS && subm_overflowed(ix)) return;
   const int tid = threadIdx.x;
   const int64_t e = (int64_t)blockIdx.x * kSubmTile + tid;
   if (BRICKS && e < ix.nw1) {
@@ -96,18 +98,31 @@ __global__ __launch_bounds__(kSubmThreads) void subm_tile_sum_kernel(SubmIndex i
 // BRICKS also clears the level-2 words of the entry's bricks (so only the
 // words in use are cleared); voxels also write each of the entry's bricks'
 // voxel base (l2pre) and, for the last entry, the distinct voxels in all to
-// *voxels (optional).
+// *voxels (optional).  An index with an overflow flag (SubmIndex::flag) sets
+// it when the bricks exceed cap2 (no level-2 word past cap2 is written) or the
+// voxels exceed nrows (*voxels is then 0); the voxel pass of an overflowed
+// index returns at once.
+// The tiles' offsets: with `scanned` the tile sums were replaced by their
+// exclusive scan (launch_subm_prefix, for many tiles); otherwise each
+// workgroup sums the tiles before its own, which costs O(ntiles) loads a
+// workgroup but saves a launch while the tiles are few.
 template <bool BRICKS>
-__global__ __launch_bounds__(kSubmThreads) void subm_prefix_kernel(SubmIndex ix, int32_t* __restrict__ voxels) {
+__global__ __launch_bounds__(kSubmThreads) void subm_prefix_kernel(SubmIndex ix, int32_t* __restrict__ voxels,
+                                                                   bool scanned) {
   __shared__ int red_s[4];
   __shared__ int scan_s[8];
+  if (!BRICKS && subm_overflowed(ix)) return;
   const int tid = threadIdx.x, t = blockIdx.x;
   int off = 0;
-  for (int j = tid; j < t; j += kSubmThreads) off += ix.tile_sums[j];
-  off = wave_sum(off);
-  if ((tid & 63) == 0) red_s[tid >> 6] = off;
-  __syncthreads();
-  off = red_s[0] + red_s[1] + red_s[2] + red_s[3];
+  if (scanned) {
+    off = ix.tile_sums[t];
+  } else {
+    for (int j = tid; j < t; j += kSubmThreads) off += ix.tile_sums[j];
+    off = wave_sum(off);
+    if ((tid & 63) == 0) red_s[tid >> 6] = off;
+    __syncthreads();
+    off = red_s[0] + red_s[1] + red_s[2] + red_s[3];
+  }
   const int64_t e = (int64_t)t * kSubmTile + tid;
   const int c = e < ix.nw1 ? subm_entry_count<BRICKS>(ix, e) : 0;
   int total;
@@ -117,15 +132,18 @@ __global__ __launch_bounds__(kSubmThreads) void subm_prefix_kernel(SubmIndex ix,
     const int nb = (int)__popcll(v.bits);
     if (BRICKS) {
       ix.l1[e].bpre = p;
-      for (int j = 0; j < nb; ++j) ix.l2bits[p + j] = 0ull;
+      for (int j = 0; j < nb && p + j < ix.cap2; ++j) ix.l2bits[p + j] = 0ull;
+      if ((int64_t)p + nb > ix.cap2 && ix.flag) atomicOr(ix.flag, 1);
     } else {
       ix.l1[e].v = p;
-      int q = p;
+      int64_t q = p;
       for (int j = 0; j < nb; ++j) {
-        ix.l2pre[v.bpre + j] = q;
+        ix.l2pre[v.bpre + j] = (int32_t)q;
         q += (int)__popcll(ix.l2bits[v.bpre + j]);
       }
-      if (voxels && e == ix.nw1 - 1) *voxels = q;
+      const bool over = q > ix.nrows && ix.flag;
+      if (over) atomicOr(ix.flag, 1);
+      if (voxels && e == ix.nw1 - 1) *voxels = over ? 0 : (int32_t)q;
     }
   }
 }
@@ -394,6 +412,7 @@ __global__ __launch_bounds__(256) void ocb_l2_kernel(const CT* __restrict__ coor
   __shared__ int32_t off_s[ST_MAX_KVOL * 3];
   __shared__ int32_t key_s[kL2Slots];
   __shared__ unsigned long long bits_s[kL2Slots];
+  if (subm_overflowed(ox)) return;  // more occupied bricks than level-2 words
   for (int e = threadIdx.x; e < kL2Slots; e += 256) {
     key_s[e] = -1;
     bits_s[e] = 0ull;
@@ -418,8 +437,15 @@ __global__ __launch_bounds__(256) void ocb_l2_kernel(const CT* __restrict__ coor
       __hip_atomic_fetch_or(&ox.l2bits[key_s[e]], bits_s[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// rank[v] = all ones for the *total distinct output voxels.
-__global__ __launch_bounds__(256) void ocb_rank_clear_kernel(SubmIndex ox, const int32_t* __restrict__ total) {
+// rank[v] = all ones for the *total distinct output voxels; an overflowed
+// index (more bricks or voxels than the candidate bound sized) is counted
+// into status[ST_STATUS_OVERFLOW].
+__global__ __launch_bounds__(256) void ocb_rank_clear_kernel(SubmIndex ox, const int32_t* __restrict__ total,
+                                                             int32_t* __restrict__ status) {
+  if (subm_overflowed(ox)) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&status[ST_STATUS_OVERFLOW], 1);
+    return;
+  }
   const int64_t nv = *total;
   for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < nv; v += (int64_t)gridDim.x * 256)
     ox.rowmap[v] = -1;
@@ -431,6 +457,7 @@ __global__ __launch_bounds__(256) void ocb_rankmin_kernel(const CT* __restrict__
                                                           const int32_t* __restrict__ offsets, Geom g,
                                                           SubmIndex ox) {
   __shared__ int32_t off_s[ST_MAX_KVOL * 3];
+  if (subm_overflowed(ox)) return;
   load_offsets(off_s, offsets, g.K);
   const uint32_t t = blockIdx.x * 256u + threadIdx.x;
   int64_t b, x, y, z;
@@ -456,6 +483,10 @@ __global__ __launch_bounds__(256) void ocb_count_kernel(const CT* __restrict__ c
                                                         int32_t* __restrict__ block_counts) {
   __shared__ int32_t off_s[ST_MAX_KVOL * 3];
   __shared__ int red_s[4];
+  if (subm_overflowed(ox)) {  // no outputs
+    if (threadIdx.x == 0) block_counts[blockIdx.x] = 0;
+    return;
+  }
   load_offsets(off_s, offsets, g.K);
   const uint32_t t = blockIdx.x * 256u + threadIdx.x;
   int64_t b, x, y, z;
@@ -477,6 +508,7 @@ __global__ __launch_bounds__(256) void ocb_emit_kernel(const CT* __restrict__ co
                                                        int32_t* __restrict__ posmap) {
   __shared__ int32_t off_s[ST_MAX_KVOL * 3];
   __shared__ int scan_s[5];
+  if (subm_overflowed(ox)) return;
   load_offsets(off_s, offsets, g.K);
   const uint32_t t = blockIdx.x * 256u + threadIdx.x;
   int64_t b, x, y, z;
@@ -659,7 +691,8 @@ __global__ __launch_bounds__(256) void ocb_inverse_kernel(const CT* __restrict__
   if (i >= n) return;
   int64_t b, x, y, z;
   load_coord(coords, i, b, x, y, z);
-  bool own = subm_in_box(ix, b, x, y, z);
+  // an overflowed output index holds no outputs: every candidate maps to none
+  bool own = !subm_overflowed(ox) && subm_in_box(ix, b, x, y, z);
   if (own) {
     const int64_t br = subm_brick(ix, b, x, y, z);
     const int r = subm_brick_rank(ix.l1[br >> 6], br);
@@ -705,6 +738,21 @@ __global__ __launch_bounds__(256) void ocb_inverse_kernel(const CT* __restrict__
       }
     }
   }
+}
+
+// Prefix pass of an index level: above kSubmInlineTiles tiles the tile sums
+// are scanned once first (the inline sum's O(ntiles^2) loads over the grid
+// would outgrow the extra launch).
+constexpr int64_t kSubmInlineTiles = 1024;
+template <bool BRICKS>
+int launch_subm_prefix(const SubmIndex& ix, int32_t* voxels, hipStream_t stream) {
+  const bool scan = ix.ntiles > kSubmInlineTiles;
+  if (scan) {
+    const int rc = launch_exclusive_scan(ix.tile_sums, ix.ntiles, stream);
+    if (rc != ST_OK) return rc;
+  }
+  subm_prefix_kernel<BRICKS><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix, voxels, scan);
+  return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
 }
 
 // Output index geometry of a brick build: rows = the candidate bound; false
@@ -759,10 +807,10 @@ int st_subm_index(const void* coords, int coord_dtype, int64_t n, int64_t batche
     const CT* c = (const CT*)coords;
     subm_occ_kernel<CT><<<rows, kSubmThreads, 0, stream>>>(c, n, ix, status);
     subm_tile_sum_kernel<true><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix);
-    subm_prefix_kernel<true><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix, nullptr);
+    if (launch_subm_prefix<true>(ix, nullptr, stream) != ST_OK) return ST_ERR_HIP;
     subm_l2_kernel<CT><<<rows, kSubmThreads, 0, stream>>>(c, n, ix);
     subm_tile_sum_kernel<false><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix);
-    subm_prefix_kernel<false><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix, nullptr);
+    if (launch_subm_prefix<false>(ix, nullptr, stream) != ST_OK) return ST_ERR_HIP;
     subm_rowmap_kernel<CT><<<rows, kSubmThreads, 0, stream>>>(c, n, ix, status);
   });
   ST_CHECK_LAUNCH();
@@ -827,6 +875,7 @@ int st_outcoords_brick_plan(const void* in_coords, int coord_dtype, int64_t n, c
   SubmIndex ox;
   subm_view(workspace, rows, batches, g.out_shape[0], g.out_shape[1], g.out_shape[2], &ox);
   int32_t* total = (int32_t*)((char*)workspace + ixb);
+  ox.flag = total + 1;
   const Ranks rk = make_ranks(g, n, nranks);
   const unsigned grid = (unsigned)num_blocks, tiles = (unsigned)ox.ntiles;
   unsigned cg = st_blocks((ox.nbricks + 15) / 16, kSubmThreads);
@@ -836,11 +885,11 @@ int st_outcoords_brick_plan(const void* in_coords, int coord_dtype, int64_t n, c
     const CT* c = (const CT*)in_coords;
     ocb_occ_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox, status);
     subm_tile_sum_kernel<true><<<tiles, kSubmThreads, 0, stream>>>(ox);
-    subm_prefix_kernel<true><<<tiles, kSubmThreads, 0, stream>>>(ox, nullptr);
+    if (launch_subm_prefix<true>(ox, nullptr, stream) != ST_OK) return ST_ERR_HIP;
     ocb_l2_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox);
     subm_tile_sum_kernel<false><<<tiles, kSubmThreads, 0, stream>>>(ox);
-    subm_prefix_kernel<false><<<tiles, kSubmThreads, 0, stream>>>(ox, total);
-    ocb_rank_clear_kernel<<<2048, 256, 0, stream>>>(ox, total);
+    if (launch_subm_prefix<false>(ox, total, stream) != ST_OK) return ST_ERR_HIP;
+    ocb_rank_clear_kernel<<<2048, 256, 0, stream>>>(ox, total, status);
     ocb_rankmin_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox);
     ocb_count_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox, block_counts);
   });
@@ -863,6 +912,7 @@ int st_outcoords_brick_emit(const void* in_coords, int coord_dtype, int64_t n, c
   if (!out_coords) return ST_ERR_ARG;
   SubmIndex ox;
   subm_view(workspace, rows, batches, g.out_shape[0], g.out_shape[1], g.out_shape[2], &ox);
+  ox.flag = (int32_t*)((char*)workspace + ixb) + 1;
   int32_t* posmap = (int32_t*)((char*)workspace + ixb + 256);
   ST_DISPATCH_COORD(coord_dtype, CT, {
     ocb_emit_kernel<CT><<<(unsigned)num_blocks, 256, 0, stream>>>((const CT*)in_coords, make_ranks(g, n, nranks),
@@ -913,6 +963,7 @@ int st_outcoords_brick_inverse(const void* in_coords, int coord_dtype, int64_t n
   if (!in_index || !invnbr || !in_masks) return ST_ERR_ARG;
   SubmIndex ox, ix;
   subm_view(const_cast<void*>(workspace), rows, batches, g.out_shape[0], g.out_shape[1], g.out_shape[2], &ox);
+  ox.flag = (int32_t*)((char*)workspace + ixb) + 1;
   subm_view(const_cast<void*>(in_index), n, batches, g.in_shape[0], g.in_shape[1], g.in_shape[2], &ix);
   const int32_t* posmap = (const int32_t*)((const char*)workspace + ixb + 256);
   ST_DISPATCH_COORD(coord_dtype, CT, {

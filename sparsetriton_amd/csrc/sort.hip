@@ -485,40 +485,55 @@ extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t m
     ST_CHECK_HIP(hipStreamWaitEvent(side->stream, side->fork, 0));
     ps = side->stream;
   }
-  if (chunk != 0) {
-    const int64_t nb = (n_dst + st::kPairRows - 1) / st::kPairRows;
-    int32_t* pairs = (int32_t*)(pb + L[ST_PLAN_PAIRS]);
-    int32_t* kstart = (int32_t*)(pb + L[ST_PLAN_KSTART]);
-    int32_t* cstart = (int32_t*)(pb + L[ST_PLAN_CSTART]);
-    int32_t* corder = (int32_t*)(pb + L[ST_PLAN_CORDER]);
-    const int64_t mc = L[ST_PLAN_MAX_CHUNKS];
-    int rc = st::launch_pairs(map, map_k_stride, map_r_stride, n_dst, K, n_src, (int32_t*)(sb + S.pair_counts), nb,
-                              chunk, kstart, cstart, pairs, ps);
-    if (rc == ST_OK) {
-      if (mc <= st::kChunkOrderMax && K <= st::kChunkOrderMaxK) {
-        rc = st::launch_chunk_order(pairs, kstart, cstart, K, chunk, mc, n_dst, corder, ps);
-      } else {
-        uint32_t* ck = (uint32_t*)(sb + S.ck_keys);
-        rc = st::launch_chunk_keys(pairs, kstart, cstart, K, chunk, mc, n_dst, ck, ps);
-        if (rc == ST_OK)
-          rc = st::launch_sort(ck, 1, 9, mc, (uint32_t*)(sb + S.ck_tmp), (int32_t*)(sb + S.ck_rows), corder,
-                               (int32_t*)(sb + S.ck_hist), ps);
+  // Everything after the fork runs inside `body`, so that the caller's stream
+  // waits for the side stream on every return path: a launch error on either
+  // stream must not leave pair-list kernels writing into `plan` after the
+  // caller's stream has moved on.
+  auto body = [&]() -> int {
+    if (chunk != 0) {
+      const int64_t nb = (n_dst + st::kPairRows - 1) / st::kPairRows;
+      int32_t* pairs = (int32_t*)(pb + L[ST_PLAN_PAIRS]);
+      int32_t* kstart = (int32_t*)(pb + L[ST_PLAN_KSTART]);
+      int32_t* cstart = (int32_t*)(pb + L[ST_PLAN_CSTART]);
+      int32_t* corder = (int32_t*)(pb + L[ST_PLAN_CORDER]);
+      const int64_t mc = L[ST_PLAN_MAX_CHUNKS];
+      int rc = st::launch_pairs(map, map_k_stride, map_r_stride, n_dst, K, n_src, (int32_t*)(sb + S.pair_counts), nb,
+                                chunk, kstart, cstart, pairs, ps);
+      if (rc == ST_OK) {
+        if (mc <= st::kChunkOrderMax && K <= st::kChunkOrderMaxK) {
+          rc = st::launch_chunk_order(pairs, kstart, cstart, K, chunk, mc, n_dst, corder, ps);
+        } else {
+          uint32_t* ck = (uint32_t*)(sb + S.ck_keys);
+          rc = st::launch_chunk_keys(pairs, kstart, cstart, K, chunk, mc, n_dst, ck, ps);
+          if (rc == ST_OK)
+            rc = st::launch_sort(ck, 1, 9, mc, (uint32_t*)(sb + S.ck_tmp), (int32_t*)(sb + S.ck_rows), corder,
+                                 (int32_t*)(sb + S.ck_hist), ps);
+        }
       }
+      if (rc != ST_OK) return rc;
     }
-    if (rc != ST_OK) return rc;
-  }
-  if (n_dst > 0) {
-    const int rc = st::launch_sort(row_masks, W, K, n_dst, (uint32_t*)(sb + S.sort_keys), (int32_t*)(sb + S.sort_rows),
-                                   perm, (int32_t*)(sb + S.sort_hist), stream, bucket_bits);
-    if (rc != ST_OK) return rc;
-    st::tile_plan_kernel<<<(unsigned)L[ST_PLAN_TILES], 256, 0, stream>>>(
-        map, map_k_stride, map_r_stride, row_masks, W, K, perm, n_dst, n_src, (int32_t*)(pb + L[ST_PLAN_TILE_NK]),
-        (int16_t*)(pb + L[ST_PLAN_TILE_KLIST]), (int32_t*)(pb + L[ST_PLAN_TILE_MAP]));
-    ST_CHECK_LAUNCH();
-  }
+    if (n_dst > 0) {
+      const int rc = st::launch_sort(row_masks, W, K, n_dst, (uint32_t*)(sb + S.sort_keys),
+                                     (int32_t*)(sb + S.sort_rows), perm, (int32_t*)(sb + S.sort_hist), stream,
+                                     bucket_bits);
+      if (rc != ST_OK) return rc;
+      st::tile_plan_kernel<<<(unsigned)L[ST_PLAN_TILES], 256, 0, stream>>>(
+          map, map_k_stride, map_r_stride, row_masks, W, K, perm, n_dst, n_src, (int32_t*)(pb + L[ST_PLAN_TILE_NK]),
+          (int16_t*)(pb + L[ST_PLAN_TILE_KLIST]), (int32_t*)(pb + L[ST_PLAN_TILE_MAP]));
+      ST_CHECK_LAUNCH();
+    }
+    return ST_OK;
+  };
+  const int rc = body();
   if (side) {
-    ST_CHECK_HIP(hipEventRecord(side->join, side->stream));
-    ST_CHECK_HIP(hipStreamWaitEvent(stream, side->join, 0));
+    // the join is recorded whatever `body` returned
+    const hipError_t e1 = hipEventRecord(side->join, side->stream);
+    const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(stream, side->join, 0) : e1;
+    if (e2 != hipSuccess) {
+      // the caller's stream cannot be ordered after the side stream: wait for it here
+      (void)hipStreamSynchronize(side->stream);
+      if (rc == ST_OK) return ST_ERR_HIP;
+    }
   }
-  return ST_OK;
+  return rc;
 }

@@ -34,8 +34,14 @@ struct SubmIndex {
   unsigned long long* l2bits;  // per occupied brick (brick rank order)
   int32_t* l2pre;              // voxels before each occupied brick
   int32_t* rowmap;
-  int32_t* tile_sums;          // per tile of kSubmTile level-1 entries: its bricks or voxels
-  int64_t nbricks, nw1, cap2, ntiles;
+  int32_t* tile_sums;          // per tile of kSubmTile level-1 entries: its bricks or voxels (ntiles + 1)
+  // Overflow flag of an index whose rows bound is not a property of its input (the output
+  // index of a strided / transposed build, sized from the kernel's candidate bound): set when
+  // the occupied bricks exceed cap2 or the distinct voxels exceed nrows, after which the
+  // build's later kernels return without touching the level-2 and rank arrays.  Null for the
+  // index of a coordinate set, which cannot overflow (a row adds one voxel and one brick).
+  int32_t* flag;
+  int64_t nbricks, nw1, cap2, ntiles, nrows;
   int nb, sx, sy, sz, bx, by, bz;
 };
 
@@ -56,6 +62,12 @@ __device__ __forceinline__ int subm_vbit(int64_t x, int64_t y, int64_t z) {
 }
 
 __device__ __forceinline__ unsigned long long below(int bit) { return (1ull << bit) - 1ull; }
+
+// Whether the index's overflow flag is set (a uniform scalar load; false for
+// an index without one).
+__device__ __forceinline__ bool subm_overflowed(const SubmIndex& ix) {
+  return ix.flag && *ix.flag != 0;
+}
 
 // brick rank of an in-box coordinate whose brick is occupied
 __device__ __forceinline__ int subm_brick_rank(const SubmL1& e, int64_t br) {
@@ -216,7 +228,7 @@ inline int64_t subm_workspace_bytes(int64_t n, int64_t batches, int64_t sx, int6
   int64_t nbricks = 0, nw1 = 0, cap2 = 0;
   if (!subm_geom(n, batches, sx, sy, sz, &nbricks, &nw1, &cap2)) return -1;
   const int64_t ntiles = (nw1 + kSubmTile - 1) / kSubmTile;
-  return (int64_t)(subm_align256((size_t)nbricks) + subm_align256(sizeof(int32_t) * (size_t)ntiles) +
+  return (int64_t)(subm_align256((size_t)nbricks) + subm_align256(sizeof(int32_t) * (size_t)(ntiles + 1)) +
                    subm_align256(sizeof(SubmL1) * (size_t)nw1) +
                    subm_align256(sizeof(unsigned long long) * (size_t)cap2) +
                    subm_align256(sizeof(int32_t) * (size_t)cap2) + subm_align256(sizeof(int32_t) * (size_t)(n > 0 ? n : 1)));
@@ -228,11 +240,12 @@ inline bool subm_view(void* workspace, int64_t n, int64_t batches, int64_t sx, i
   *ix = SubmIndex{};
   if (!subm_geom(n, batches, sx, sy, sz, &ix->nbricks, &ix->nw1, &ix->cap2)) return false;
   ix->ntiles = (ix->nw1 + kSubmTile - 1) / kSubmTile;
+  ix->nrows = n;
   char* p = (char*)workspace;
   ix->occ = (uint8_t*)p;
   p += subm_align256((size_t)ix->nbricks);
   ix->tile_sums = (int32_t*)p;
-  p += subm_align256(sizeof(int32_t) * (size_t)ix->ntiles);
+  p += subm_align256(sizeof(int32_t) * (size_t)(ix->ntiles + 1));
   ix->l1 = (SubmL1*)p;
   p += subm_align256(sizeof(SubmL1) * (size_t)ix->nw1);
   ix->l2bits = (unsigned long long*)p;

@@ -258,7 +258,7 @@ def _brick_index(tensor: SparseTensor, eligible: bool, K: int, C_in: int, C_out:
     convolution's neighbours up in it (``st_subm_fly_gemm`` built for the shape, box indexable),
     else None.  The index depends on the coordinates only, so every layer over them shares it."""
     if not eligible or tensor.C.dtype not in (torch.int16, torch.int32) or \
-            not subm_fly_ok(C_in, C_out, K, tensor.F.dtype):
+            not subm_fly_ok(int(tensor.F.shape[0]), C_in, C_out, K, tensor.F.dtype):
         return None
     key = ("brick_index", int(tensor.batch_size), tuple(int(v) for v in tensor.spatial_shape))
     if key not in tensor._cache.kmaps:

@@ -188,11 +188,14 @@ class ConvHashOnTheFlyImplicitGEMM(torch.autograd.Function):
         return grad_input, grad_weights, None, None, None, None, None, None, None, None
 
 
-def subm_fly_ok(C_in: int, C_out: int, K: int, dtype: torch.dtype) -> bool:
-    """Whether ``st_subm_fly_gemm`` is built for both directions of a C_in -> C_out convolution."""
+def subm_fly_ok(n: int, C_in: int, C_out: int, K: int, dtype: torch.dtype) -> bool:
+    """Whether ``st_subm_fly_gemm`` takes both directions of a C_in -> C_out convolution over ``n``
+    rows: the shape is built and the operands of the forward (n x C_in) and of the input gradient
+    (n x C_out) fit the kernel's 32-bit buffer offsets.  Otherwise the convolution runs on the
+    table-probing kernels."""
     code = _lib.compute_code(dtype)
     lib = _lib.lib()
-    return bool(lib.st_subm_fly_ok(C_in, C_out, K, code)) and bool(lib.st_subm_fly_ok(C_out, C_in, K, code))
+    return bool(lib.st_subm_fly_ok(n, C_in, C_out, K, code)) and bool(lib.st_subm_fly_ok(n, C_out, C_in, K, code))
 
 
 def subm_fly_gemm(A: torch.Tensor, index: BrickIndex, offsets_i32: torch.Tensor, Bt: torch.Tensor) -> torch.Tensor:

@@ -853,8 +853,9 @@ def brick_out_coords_and_map(in_coords: torch.Tensor, batch_size: int, spatial_s
     if with_map:
         # the input index is queued before the host waits for the output count
         index = BrickIndex.build(in_coords, batch_size, spatial_shape)
-    n_out, outside = torch.stack([counts[nblocks], status[_lib.STATUS_OUT_OF_BOX]]).tolist()
-    if outside:
+    n_out, outside, over = torch.stack([counts[nblocks], status[_lib.STATUS_OUT_OF_BOX],
+                                        status[_lib.STATUS_OVERFLOW]]).tolist()
+    if outside or over:
         return None
     kernel_offsets = offsets.to(in_coords.dtype, copy=True)  # returned to the caller: not the shared tensor
     out_coords = torch.empty((n_out, 4), dtype=in_coords.dtype, device=dev)

@@ -522,6 +522,9 @@ SUBM_CASES = [
     ("one-voxel-box", 1, (1, 1, 1), 1, torch.int16, 3, 1),
     ("wide", 4, (1440, 1440, 41), 60000, torch.int16, 3, 1),
     ("int64", 2, (40, 50, 60), 6000, torch.int64, 3, 1),
+    # 33.5M bricks: 2048 prefix tiles, above the count whose tile sums are scanned by a launch of
+    # their own instead of summed inline by every workgroup
+    ("many-tiles", 8, (2048, 2048, 64), 500000, torch.int16, 3, 1),
 ]
 
 

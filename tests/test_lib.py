@@ -54,3 +54,29 @@ def test_plan_layout_with_an_automatic_chunk_size():
         assert lib.st_kmap_plans_layout(n, K, 2048, L) == 0
         assert L[11] == K * n // 2048 + K
     assert lib.st_kmap_plans_layout(100, 27, -2, L) == -1
+
+
+def test_subm_fly_eligibility_is_size_aware():
+    """st_subm_fly_ok(n, Kd, Nd, K, dtype) is host arithmetic: the brick-index gather takes n rows
+    only while n * Kd * element size stays under 2^31 - 64 bytes (its 32-bit buffer offsets), so a
+    convolution over more rows goes to the table-probing kernels instead of failing in the call."""
+    import torch
+
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_hashfly_gemm import subm_fly_ok
+
+    lib = _lib.lib()
+    lim = (1 << 31) - 64
+    for code, esz in ((3, 4), (2, 2), (1, 2)):
+        for kd in (64, 128):
+            n_max = (lim - 1) // (kd * esz)  # largest n with n * kd * esz < lim
+            assert lib.st_subm_fly_ok(n_max, kd, 64, 27, code) == 1
+            assert lib.st_subm_fly_ok(n_max + 1, kd, 64, 27, code) == 0
+    assert lib.st_subm_fly_ok(-1, 64, 64, 27, 2) == 0
+    assert lib.st_subm_fly_ok(1000, 64, 64, 27, 0) == 0  # IEEE fp32: not built
+    assert lib.st_subm_fly_ok(1000, 128, 128, 27, 3) == 0  # split fp32 at 128 x 128: not built
+    # the Python predicate checks both directions: with C_out > C_in the input gradient's
+    # operand (n x C_out) is the larger one
+    n_fwd_only = (lim - 1) // (64 * 2)  # fits n x 64 bf16 but not n x 128
+    assert lib.st_subm_fly_ok(n_fwd_only, 64, 128, 27, 2) == 1
+    assert not subm_fly_ok(n_fwd_only, 64, 128, 27, torch.bfloat16)
+    assert subm_fly_ok((lim - 1) // (128 * 2), 64, 128, 27, torch.bfloat16)

@@ -197,3 +197,70 @@ def test_conv_uses_the_brick_build(device, tr):
     ref = O.fwd_f64(X.astype(np.float64), W.astype(np.float64), nbr)
     got = out.F.detach().cpu().numpy().astype(np.float64)
     assert np.abs(got - ref).max() <= 2e-3 * max(np.abs(ref).max(), 1.0)
+
+
+@pytest.mark.parametrize("S", [32, 256])
+def test_brick_plan_flags_offsets_beyond_the_kernel_bound(device, S):
+    """A C-ABI caller whose offsets reach more outputs than kernel_size / dilation bound (here
+    the 27 offsets of a 3x3x3 kernel declared as kernel_size 1, so the output index is sized for
+    one output per input): the plan counts ST_STATUS_OVERFLOW, reports no outputs and writes no
+    level-2 word or rank past the index's bound; emit writes nothing and the inverse map is all
+    -1.  At S = 32 the voxels overflow (the output box has fewer bricks than rows), at S = 256 the
+    occupied bricks do.  The same call with the kernel's own size then builds the exact outputs
+    (a regression test of the bounds: the guarded build must leave the workspace reusable)."""
+    import ctypes
+
+    from sparsetriton_amd import _lib
+    from sparsetriton_amd.nn.functional.conv.kmap import _offsets_i32, _target_offsets, out_spatial_shape
+
+    rng = np.random.default_rng(5)
+    n = 2000
+    c = _rand_coords(rng, n, S)
+    coords = torch.as_tensor(c, device=device)
+    shape = (S, S, S)
+    k, s, p, d = 3, 2, 1, 1
+    offs = _offsets_i32(_target_offsets(k, d, p, False, device))
+    ns = out_spatial_shape(shape, k, s, d, p, False)
+    g = _lib.OutGeom()
+    g.K, g.transposed, g.stride, g.chunk = offs.shape[0], 0, s, 0
+    for a in range(3):
+        g.in_shape[a], g.out_shape[a] = shape[a], ns[a]
+    lib = _lib.lib()
+    st = _lib.stream_of(device)
+
+    def plan(kernel_size):
+        wb, nb = ctypes.c_int64(), ctypes.c_int64()
+        assert lib.st_outcoords_brick_sizes(n, ctypes.byref(g), 2, kernel_size, d, ctypes.byref(wb),
+                                            ctypes.byref(nb)) == 0
+        work = torch.full((wb.value,), 0xAB, dtype=torch.uint8, device=device)
+        counts = torch.empty((nb.value + 1,), dtype=torch.int32, device=device)
+        status = torch.empty((_lib.STATUS_WORDS,), dtype=torch.int32, device=device)
+        _lib.call("st_outcoords_brick_plan", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(offs),
+                  ctypes.byref(g), 2, kernel_size, d, _lib.ptr(work), wb.value, _lib.ptr(counts), nb.value,
+                  _lib.ptr(status), st)
+        return work, wb.value, counts, nb.value, status
+
+    work, wb, counts, nb, status = plan(1)
+    assert int(status[_lib.STATUS_OVERFLOW]) > 0
+    assert int(counts[nb]) == 0
+    out = torch.full((4, 4), -7, dtype=coords.dtype, device=device)
+    _lib.call("st_outcoords_brick_emit", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(offs),
+              ctypes.byref(g), 2, 1, d, _lib.ptr(work), wb, _lib.ptr(counts), nb, _lib.ptr(out), 4, st)
+    assert bool((out == -7).all())
+    from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex
+
+    index = BrickIndex.build(coords, 2, shape)
+    K, W = offs.shape[0], 1
+    inv = torch.full((K, n), 5, dtype=torch.int32, device=device)
+    masks = torch.full((n, W), 5, dtype=torch.int32, device=device)
+    _lib.call("st_outcoords_brick_inverse", _lib.ptr(coords), _lib.coord_code(coords.dtype), n, _lib.ptr(offs),
+              ctypes.byref(g), 2, 1, d, _lib.ptr(work), wb, _lib.ptr(index.work), index.nbytes, _lib.ptr(inv),
+              _lib.ptr(masks), st)
+    assert bool((inv == -1).all()) and bool((masks == 0).all())
+
+    _, _, counts3, nb3, status3 = plan(k)
+    assert int(status3[_lib.STATUS_OVERFLOW]) == 0
+    oc = O.out_coords(c, O.target_offsets(k, d, p, False), s, False, O.out_shape(shape, k, s, d, p, False))
+    assert int(counts3[nb3]) == oc.shape[0]
+    b = _brick(device, c, shape, k, s, p, d, False, batch_size=2)
+    assert b is not None and np.array_equal(b[0].cpu().numpy(), oc)
