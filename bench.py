@@ -19,15 +19,21 @@ value = effective TFLOP/s = 6 * P * C_in * C_out / step time, P = exact number
 of (input, output, offset) pairs.  ``roofline`` covers the dominant kernel,
 timed with HIP events on the stream it runs on.  ``cpu_baseline`` times the
 reference algorithm's CPU port (oracle/st_oracle.c: 31-bit hash with 128-probe
-cap, output-major map, output-stationary forward, scatter input gradient,
-per-offset weight gradient; fp32, OpenMP) on the same voxel set.
+cap, output-major map, output-stationary forward, scatter input gradient, weight
+gradient by row slabs x offsets as the reference's grid; fp32, OpenMP) on the same voxel set.
+
+The default run also measures the other benchmark configurations -- config 2 in bf16, the
+strided (config 3) and transposed (config 4) convolutions, the 1M-voxel layer (config 5) with
+either algorithm -- into ``configs``: one record each with its step time, effective TFLOP/s, the
+three GEMM kernels timed alone and the roofline of the dominant one (``--no-configs`` skips them).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--dtype f32|bf16] [--no-cpu]
-                       [--fp32-precision bf16x3|ieee] [--profile] [--workload config2|config3|...]
+                       [--fp32-precision bf16x3|ieee] [--profile] [--no-configs]
+                       [--workload config2|config3|...]
 
-``--workload`` other than config2 measures another benchmark configuration (strided conv,
-transposed conv, the 1M-voxel submanifold layer with either algorithm): one JSON line with the
-same fields, the step timed the same way, plus the first-call time (map build + forward).
+``--workload`` other than config2 measures one other benchmark configuration on its own: one
+JSON line with the same fields, the step timed the same way, plus the first-call time (map build
++ forward).
 """
 
 import argparse
@@ -101,19 +107,74 @@ def _events_batch(torch, fn, reps):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config2_subm64.md")
+# the sources of the gather and weight-gradient kernels whose counters the traffic file holds
+GEMM_SOURCES = ("gemm_kernels.h", "gemm_wide.h", "gemm_x3.h", "gemm_x3.hip", "mfma.h", "nbr_src.h")
+
+
+def gemm_sources_sha():
+    """sha256 (16 hex digits) over the GEMM kernel sources, in GEMM_SOURCES order: the key that ties
+    a traffic measurement to the kernels it measured."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in GEMM_SOURCES:
+        with open(os.path.join(ROOT, "sparsetriton_amd", "csrc", name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read() + b"\0")
+    return h.hexdigest()[:16]
 
 
 def _measured_traffic(dtype, role):
-    """HBM bytes per launch of a GEMM role, from the committed rocprofv3 counter summary
-    (lines `traffic <dtype> <role> <bytes>`), or None when it has no entry."""
+    """(HBM bytes per launch of a GEMM role, provenance) from the committed rocprofv3 counter summary
+    (lines `traffic <dtype> <role> <bytes>`, `measured_commit <sha>`, `gemm_sources_sha <sha>`).
+    The bytes are None when the file has no entry or when the GEMM sources have changed since the
+    counters were taken (the figure would describe other kernels)."""
+    src = {"file": os.path.relpath(TRAFFIC_FILE, ROOT), "measured_commit": None, "gemm_sources_sha": None,
+           "current_gemm_sources_sha": gemm_sources_sha(), "stale": None}
+    val = None
     try:
         for line in open(TRAFFIC_FILE):
             f = line.split()
             if len(f) == 4 and f[0] == "traffic" and f[1] == dtype and f[2] == role:
-                return float(f[3])
+                val = float(f[3])
+            elif len(f) == 2 and f[0] in ("measured_commit", "gemm_sources_sha"):
+                src[f[0]] = f[1]
     except OSError:
         pass
-    return None
+    src["stale"] = src["gemm_sources_sha"] != src["current_gemm_sources_sha"]
+    return (None if src["stale"] else val), src
+
+
+def gemm_roofline(kernel, kernel_ms, n_in, n_out, cin, cout, K, P, dts, fp32_precision, traffic=None,
+                  traffic_source=None):
+    """Roofline of one gather-GEMM / weight-gradient launch.  Algorithmic work: 2 P C_in C_out flops;
+    bytes = s (N_in C_in + N_out C_out + K C_in C_out) + 8 P (the two feature arrays once, the weights,
+    one int32 (in, out) index pair per map pair; s = element size).  The binding roof is HBM when the
+    intensity lies below the ridge point of the arithmetic the kernel runs (split fp32: a third of
+    the bf16 peak, three bf16 products per fp32 product), else the MFMA peak."""
+    gemm_flops = 2.0 * P * cin * cout
+    esz = 4 if dts == "f32" else 2
+    gemm_bytes = esz * (n_in * cin + n_out * cout + K * cin * cout) + 8 * P
+    if dts == "f32" and fp32_precision == "bf16x3":
+        mfma_peak = PEAK["bf16_TFLOPs"] / 3.0
+        note = "dense bf16 MFMA peak / 3 (three bf16 products per fp32 product)"
+    elif dts == "f32":
+        mfma_peak, note = PEAK["f32_TFLOPs"], "dense f32 MFMA peak"
+    else:
+        mfma_peak, note = PEAK["bf16_TFLOPs"], f"dense {dts} MFMA peak"
+    tflops = gemm_flops / (kernel_ms * 1e-3) / 1e12
+    intensity = gemm_flops / gemm_bytes
+    ridge = mfma_peak * 1e12 / (PEAK["hbm_GBps"] * 1e9)
+    common = {"traffic": traffic, "traffic_unit": "bytes/launch", "traffic_source": traffic_source,
+              "kernel": kernel, "kernel_avg_ms": kernel_ms, "algorithmic_bytes_per_launch": gemm_bytes,
+              "algorithmic_flops_per_launch": gemm_flops, "flops_per_byte": intensity, "ridge_flops_per_byte": ridge,
+              "mfma_TFLOPs": tflops, "mfma_peak_TFLOPs": mfma_peak, "mfma_frac": tflops / mfma_peak,
+              "mfma_peak_note": note}
+    if intensity < ridge:
+        gbps = gemm_bytes / (kernel_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": gbps, "peak": PEAK["hbm_GBps"], "unit": "GB/s",
+                "frac": gbps / PEAK["hbm_GBps"], **common}
+    return {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s", "frac": tflops / mfma_peak,
+            **common}
 
 
 def _stats(t):
@@ -174,7 +235,7 @@ def config1_inputs(seed=0):
 
 def cpu_baseline(coords, shape, X, W, dY, profile=False):
     """The reference algorithm's CPU port (oracle/st_oracle.c ref_*: 31-bit key2 table with the
-    128-probe cap, output-major map, output-stationary forward, scatter input gradient, per-offset
+    128-probe cap, output-major map, output-stationary forward, scatter input gradient, row-slab x offset
     weight gradient; fp32, OpenMP), as planned for the CPU baseline: config 1 with >= 10 warmup and
     >= 50 timed passes on all host threads and on one, and beside it a bounded sample of the
     benchmark workload itself (config 2) on all host threads -- its figure is `value`."""
@@ -243,6 +304,8 @@ def gpu_config1(torch, reps):
 
 EXTRA = {
     # name: (description, C_in, C_out, k, stride, padding, transposed, submanifold, dtype, algorithm)
+    "config2-bf16": ("SubMConv3D 64->64 k3 in bf16 on the config-2 voxel set", 64, 64, 3, 1, 1, False, True,
+                     "bf16", "precomputed"),
     "config3": ("SparseConv3D 64->128 k3 s2 p1 on the config-2 voxel set", 64, 128, 3, 2, 1, False, False, "f32",
                 "precomputed"),
     "config4": ("SparseConvTransposed3D 128->64 k3 s2 p1 on config 3's output coordinates", 128, 64, 3, 2, 1, True,
@@ -255,31 +318,44 @@ EXTRA = {
                      True, "f32", "precomputed"),
 }
 WITH_BIAS = {"config2-bias"}
+# the configurations measured beside the headline in the default run (one record each)
+DEFAULT_CONFIGS = ("config2-bf16", "config3", "config4", "config5", "config5-hashfly")
 
 
-def run_extra(args):
-    """One JSON line for a benchmark configuration other than the headline one: the layer's
-    fwd+bwd step (map cached) and its kernel-map build, timed like the headline."""
+def measure_extra(name, steps, warmup, profile=False, fp32_precision="bf16x3", coords_cache=None):
+    """One benchmark configuration other than the headline one, as a record: the layer's fwd+bwd
+    step (map cached) through sparse_conv3d and autograd, timed like the headline, its first call
+    (map build + forward), the three GEMM kernels timed alone with HIP events on the launch stream
+    (forward gather, input-gradient gather, weight gradient with its reduce; for hash-fly the
+    forward is the in-GEMM-lookup gather) and the roofline of the dominant one.  ``coords_cache``
+    (a dict) keeps the seeded voxel sets across calls."""
     import torch
 
-    from sparsetriton_amd import SparseTensor, workloads
-    from sparsetriton_amd.config import ConvAlgo, set_conv_algo, set_fp32_precision
+    from sparsetriton_amd import SparseTensor, _lib, workloads
+    from sparsetriton_amd.config import ConvAlgo, get_conv_algo, set_conv_algo, set_fp32_precision
     from sparsetriton_amd.nn.functional import sparse_conv3d
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
+        gather_gemm_dgrad,
+        gather_gemm_fwd,
+        weight_prep,
+        wgrad,
+    )
 
-    desc, Cin, Cout, k, s, p, tr, subm, dts, algo = EXTRA[args.workload]
-    set_fp32_precision(args.fp32_precision)
+    desc, Cin, Cout, k, s, p, tr, subm, dts, algo = EXTRA[name]
+    prev_algo = get_conv_algo()
+    set_fp32_precision(fp32_precision)
     set_conv_algo(ConvAlgo.ImplicitHashFlyGEMM if algo == "hashfly" else ConvAlgo.PrecomputedNeighborGEMM)
     dev = torch.device("cuda:0")
     dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[dts]
     seed = 0
-    if args.workload.startswith("config5"):
-        coords_np, shape = workloads.config5(seed=seed)
-        batch = 1
-    else:
-        coords_np, shape = workloads.config2(seed=seed)
-        batch = 4
+    cache = coords_cache if coords_cache is not None else {}
+    setname = "config5" if name.startswith("config5") else "config2"
+    if setname not in cache:
+        cache[setname] = workloads.config5(seed=seed) if setname == "config5" else workloads.config2(seed=seed)
+    coords_np, shape = cache[setname]
+    batch = 1 if setname == "config5" else 4
     coords = torch.as_tensor(coords_np, device=dev).to(torch.int16)
-    if args.workload == "config4":
+    if name == "config4":
         # input = the output coordinates of config 3's strided convolution
         from sparsetriton_amd.nn.functional.conv.kmap import build_out_coords
         coords, shape, _ = build_out_coords(coords, shape, 3, stride=2, padding=1, submanifold=False)
@@ -290,7 +366,7 @@ def run_extra(args):
     bound = 1.0 / np.sqrt(Cin * k ** 3)
     W = ((torch.rand(k ** 3, Cin, Cout, generator=g) * 2 - 1) * bound).to(dev, dtype).requires_grad_(True)
     b = None
-    if args.workload in WITH_BIAS:
+    if name in WITH_BIAS:
         b = ((torch.rand(Cout, generator=g) * 2 - 1) * bound).to(dev, dtype).requires_grad_(True)
 
     def fresh():
@@ -307,6 +383,7 @@ def run_extra(args):
     sp, out = build()
     torch.cuda.synchronize()
     n_out = out.F.shape[0]
+    km = None
     if algo == "hashfly":
         P = None
     else:
@@ -314,7 +391,7 @@ def run_extra(args):
         km.prepare()
         P = km.num_pairs()
     dY = torch.randn(n_out, Cout, generator=g).to(dev, dtype)
-    R = 3 if args.profile else 10
+    R = 3 if profile else 10
     settled = {"ms": SETTLE_MS, "calls_before_first_call_timing": _settle(torch, build)}
     build_t = _events(torch, build, R)
 
@@ -329,33 +406,68 @@ def run_extra(args):
         o.F.backward(dY)
 
     settled["steps_before_step_timing"] = _settle(torch, step)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    if P is None:  # hash-fly: count pairs from an exact map of the same geometry
-        set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)
+    ms = e0.elapsed_time(e1) / steps
+
+    # the GEMM kernels alone (HIP events on the launch stream, back to back)
+    KR = 5 if profile else 20
+    Wd = W.detach()
+    wt = weight_prep(Wd.contiguous(), _lib.W_TRANSPOSE)
+    if algo == "hashfly":
+        from sparsetriton_amd.nn.functional.conv.funcs.implicit_hashfly_gemm import subm_fly_gemm
+        from sparsetriton_amd.nn.functional.conv.kmap import _offsets_i32, _target_offsets
+
+        index = next(v for key, v in sp._cache.kmaps.items() if key[0] == "brick_index")
+        offs = _offsets_i32(_target_offsets(k, 1, p, False, dev))
+        kern = {"gather_fly_fwd": _events_batch(torch, lambda: subm_fly_gemm(X, index, offs, wt), KR)}
+        set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)  # an exact map of the same geometry: P and wgrad
         _, sp2 = fresh()
         sparse_conv3d(sp2, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)
-        P = next(iter(sp2._cache.neighbor_indices.values()))[1].num_pairs()
+        km = next(iter(sp2._cache.neighbor_indices.values()))[1]
+        km.prepare()
+        P = km.num_pairs()
+        kern["wgrad(+reduce)"] = _events_batch(torch, lambda: wgrad(X, dY, km, Wd.dtype), KR)
+    else:
+        kern = {"gather_gemm_fwd": _events_batch(torch, lambda: gather_gemm_fwd(X, km, wt), KR),
+                "gather_gemm_dgrad": _events_batch(torch, lambda: gather_gemm_dgrad(dY, km, Wd.contiguous()), KR),
+                "wgrad(+reduce)": _events_batch(torch, lambda: wgrad(X, dY, km, Wd.dtype), KR)}
+    set_conv_algo(prev_algo)
+    dom = max(kern, key=kern.get)
+    # the input gradient reads dY (N_out x C_out) and writes dX: the same bytes as the forward
+    roof = gemm_roofline(dom, kern[dom], N, n_out, Cin, Cout, k ** 3, P, dts, fp32_precision)
     value = 6.0 * P * Cin * Cout / (ms * 1e-3) / 1e12
-    log(f"{args.workload}: N_in={N} N_out={n_out} P={P}; step {ms:.3f} ms -> {value:.2f} TFLOP/s; "
-        f"first-call (map build + fwd) median {np.median(build_t):.3f} ms")
+    log(f"{name}: N_in={N} N_out={n_out} P={P}; step {ms:.3f} ms -> {value:.2f} TFLOP/s; "
+        f"first-call (map build + fwd) median {np.median(build_t):.3f} ms; kernels {kern}; "
+        f"roofline {dom}: {roof['frac'] * 100:.1f}% of the {roof['bound']} peak")
+    return {
+        "workload": f"{name}: {desc}", "dtype": dts, "fp32_precision": fp32_precision if dts == "f32" else None,
+        "algorithm": algo, "voxels_in": N, "voxels_out": n_out, "pairs": P, "C_in": Cin, "C_out": Cout,
+        "seed": seed, "steps": steps, "warmup": warmup, "clock_settle": settled, "ms_per_step": ms,
+        "effective_TFLOPs": value, "first_call_build_plus_fwd_ms": _stats(build_t), "kernels_avg_ms": kern,
+        "roofline": roof,
+    }
+
+
+def run_extra(args):
+    """One JSON line for a benchmark configuration other than the headline one (measure_extra)."""
+    rec = measure_extra(args.workload, args.steps, args.warmup, args.profile, args.fp32_precision)
     line = {
-        "metric": METRIC, "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "clock_settle": settled, "ms_per_step": ms, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": dts,
-        "fp32_precision": args.fp32_precision if dts == "f32" else None,
-        "data": "synthetic (seeded voxel set, N(0,1) features)",
-        "config": {"workload": f"{args.workload}: {desc}", "voxels_in": N, "voxels_out": n_out, "pairs": P,
-                   "C_in": Cin, "C_out": Cout, "seed": seed, "algorithm": algo},
-        "first_call_build_plus_fwd_ms": _stats(build_t),
+        "metric": METRIC, "value": rec["effective_TFLOPs"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "clock_settle": rec["clock_settle"], "ms_per_step": rec["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": rec["dtype"],
+        "fp32_precision": rec["fp32_precision"], "data": "synthetic (seeded voxel set, N(0,1) features)",
+        "config": {k: rec[k] for k in ("workload", "voxels_in", "voxels_out", "pairs", "C_in", "C_out", "seed",
+                                       "algorithm")},
+        "first_call_build_plus_fwd_ms": rec["first_call_build_plus_fwd_ms"],
+        "kernels_avg_ms": rec["kernels_avg_ms"], "roofline": rec["roofline"],
     }
     print(json.dumps(line), flush=True)
 
@@ -599,6 +711,8 @@ def main():
                     help="config2 is the headline; the others measure the other benchmark configurations")
     ap.add_argument("--fp32-precision", choices=["bf16x3", "ieee"], default="bf16x3",
                     help="fp32 matrix-core arithmetic (split-bf16 MFMA, the default, or IEEE fp32 MFMA)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the records of the other benchmark configurations in the default run")
     args = ap.parse_args()
     if args.workload != "config2":
         if args.gpus != 1:
@@ -722,35 +836,11 @@ def main():
             "gather_gemm_dgrad": _events_batch(torch, lambda: gather_gemm_dgrad(dY, kmap, wd), KR),
             "wgrad(+reduce)": _events_batch(torch, lambda: wgrad(X, dY, kmap, w.dtype), KR)}
     dom = max(kern, key=kern.get)
-    gemm_flops = 2.0 * P * Cin * Cout
-    peak_key = {"f32": "f32_TFLOPs", "bf16": "bf16_TFLOPs"}[args.dtype]
-    mfma_peak = PEAK[peak_key]
-    mfma_note = f"dense {args.dtype} MFMA peak"
-    if args.dtype == "f32" and args.fp32_precision == "bf16x3":
-        # every fp32 product is three bf16 MFMA products: the ceiling is a third of the bf16 peak
-        mfma_peak = PEAK["bf16_TFLOPs"] / 3.0
-        mfma_note = "dense bf16 MFMA peak / 3 (three bf16 products per fp32 product)"
-    tflops = gemm_flops / (kern[dom] * 1e-3) / 1e12
-    esz = 4 if args.dtype == "f32" else 2
-    # algorithmic bytes of one pass (any of the three kernels): the two feature arrays
-    # (A rows read, output rows written / X and dY read), the weights (dW: fp32 partial-free
-    # result), and one (input, output) int32 index pair per map pair
-    gemm_bytes = esz * (N * Cin + N * Cout + 27 * Cin * Cout) + 8 * P
-    intensity = gemm_flops / gemm_bytes
-    ridge = mfma_peak * 1e12 / (PEAK["hbm_GBps"] * 1e9)
     dkey = args.dtype if args.dtype != "f32" else f"f32-{args.fp32_precision}"
-    common = {"traffic": _measured_traffic(dkey, dom), "traffic_unit": "bytes/launch", "kernel": dom,
-              "kernel_avg_ms": kern[dom], "algorithmic_bytes_per_launch": gemm_bytes,
-              "algorithmic_flops_per_launch": gemm_flops, "flops_per_byte": intensity,
-              "ridge_flops_per_byte": ridge, "mfma_TFLOPs": tflops, "mfma_peak_TFLOPs": mfma_peak,
-              "mfma_frac": tflops / mfma_peak, "mfma_peak_note": mfma_note}
-    if intensity < ridge:  # below the ridge point: HBM is the bounding roof
-        gbps = gemm_bytes / (kern[dom] * 1e-3) / 1e9
-        roofline = {"bound": "hbm", "achieved": gbps, "peak": PEAK["hbm_GBps"], "unit": "GB/s",
-                    "frac": gbps / PEAK["hbm_GBps"], **common}
-    else:
-        roofline = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",
-                    "frac": tflops / mfma_peak, **common}
+    traffic, traffic_src = _measured_traffic(dkey, dom)
+    roofline = gemm_roofline(dom, kern[dom], N, N, Cin, Cout, 27, P, args.dtype, args.fp32_precision,
+                             traffic=traffic, traffic_source=traffic_src)
+    tflops = roofline["mfma_TFLOPs"]
     T = table.capacity
     ins_bytes = 8 * N + 12 * T + 12 * N  # int16 coords read + table clear + one slot written per insert
     # submanifold map (brick index + query, one launch), by the fixed formula 16 N + 12 Q + 4 N K:
@@ -778,6 +868,18 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    # the other BASELINE configurations, each a record with its own step time, effective rate,
+    # dominant kernel and roofline (the headline's voxel set is reused)
+    configs = None
+    if not args.no_configs and not args.profile:
+        configs = {}
+        cache = {"config2": (coords_np, shape)}
+        for name in DEFAULT_CONFIGS:
+            configs[name] = measure_extra(name, min(args.steps, 20), min(args.warmup, 5), False,
+                                          args.fp32_precision, coords_cache=cache)
+        set_fp32_precision(args.fp32_precision)
+        torch.cuda.empty_cache()
 
     cfg1_gpu = gpu_config1(torch, 5 if args.profile else 50)
     log(f"config 1 on the GPU: step {cfg1_gpu['fwd_bwd_step_ms']['median']:.3f} ms, "
@@ -816,6 +918,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gpu_config1": cfg1_gpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

@@ -32,7 +32,9 @@
  *      ref_kmap        conv.py:12-75 over that table, (n_out, K) row-major.
  *      ref_fwd_f32 / ref_dgrad_f32 / ref_wgrad_f32
  *                      output-stationary forward, scatter input gradient,
- *                      per-offset weight gradient (fp32 accumulation).
+ *                      weight gradient by row slabs x offsets into per-thread
+ *                      copies of dW (the reference's atomic-add grid; fp32
+ *                      accumulation).
  *
  * Coordinates are int32 rows (b, x, y, z); offsets int32 (K, 3).
  */
@@ -356,6 +358,8 @@ int64_t ref_out_coords(const int32_t* in, int64_t n, const int32_t* offsets, int
   return m;
 }
 
+int or_num_threads(void);
+
 void ref_fwd_f32(const float* X, int Cin, const float* W, int K, int Cout, const int32_t* nbr, int64_t n_out,
                  float* out) {
 #pragma omp parallel for schedule(static)
@@ -379,42 +383,82 @@ void ref_fwd_f32(const float* X, int Cin, const float* W, int K, int Cout, const
 void ref_dgrad_f32(const float* dY, int Cout, const float* W, int K, int Cin, const int32_t* nbr, int64_t n_out,
                    int64_t n_in, float* dX) {
   memset(dX, 0, sizeof(float) * (size_t)(n_in * Cin));
-  /* For a fixed offset each input row receives from at most one output row,
-   * so the scatter is race-free with the offset loop outside. */
+  /* dX[i] += dY[o] W[k]^T for every pair (the reference's input-gradient
+   * kernel, implicit_precomputed_gemm.py:129-177, with its atomic adds).  W[k]
+   * is transposed once to (Cout, Cin) so each pair is Cout row updates of dX[i]
+   * (the product's transpose, as the reference's tl.dot of dY and W^T).  For a
+   * fixed offset each input row receives from at most one output row, so the
+   * scatter is race-free with the offset loop outside. */
+  float* wt = (float*)malloc(sizeof(float) * (size_t)Cin * Cout);
+  if (!wt) return;
   for (int k = 0; k < K; ++k) {
     const float* w = W + (int64_t)k * Cin * Cout;
+    for (int c = 0; c < Cin; ++c)
+      for (int j = 0; j < Cout; ++j) wt[(int64_t)j * Cin + c] = w[(int64_t)c * Cout + j];
 #pragma omp parallel for schedule(static)
     for (int64_t o = 0; o < n_out; ++o) {
       int32_t i = nbr[o * K + k];
       if (i < 0) continue;
       const float* g = dY + o * Cout;
       float* dx = dX + (int64_t)i * Cin;
-      for (int c = 0; c < Cin; ++c) {
-        const float* wr = w + (int64_t)c * Cout;
-        float s = 0.f;
-        for (int j = 0; j < Cout; ++j) s += g[j] * wr[j];
-        dx[c] += s;
+      for (int j = 0; j < Cout; ++j) {
+        const float gj = g[j];
+        const float* wr = wt + (int64_t)j * Cin;
+        for (int c = 0; c < Cin; ++c) dx[c] += gj * wr[c];
       }
     }
   }
+  free(wt);
 }
 
+/* The reference's weight-gradient decomposition (precomputed_bwd_weight_kernel,
+ * implicit_precomputed_gemm.py:180-230): its grid is (row slabs of
+ * BLOCK_SIZE_N output rows) x (offsets) x (channel tiles), each program adding
+ * X[nbr[slab, k]]^T dY[slab] into dW[k] with an atomic add.  Here a thread
+ * takes whole row slabs (64 rows) in turn and, per slab, every offset, adding
+ * into its own copy of dW (the atomic add's place); the copies are summed in
+ * thread order at the end.  Each slab's dY rows stay in cache across its K
+ * offsets, so dY is streamed once. */
 void ref_wgrad_f32(const float* X, int Cin, const float* dY, int Cout, const int32_t* nbr, int64_t n_out, int K,
                    float* dW) {
-  memset(dW, 0, sizeof(float) * (size_t)K * Cin * Cout);
-#pragma omp parallel for schedule(dynamic, 1) collapse(2)
-  for (int k = 0; k < K; ++k) {
-    for (int c = 0; c < Cin; ++c) {
-      float* dw = dW + ((int64_t)k * Cin + c) * Cout;
-      for (int64_t o = 0; o < n_out; ++o) {
-        int32_t i = nbr[o * K + k];
-        if (i < 0) continue;
-        const float xc = X[(int64_t)i * Cin + c];
-        const float* g = dY + o * Cout;
-        for (int j = 0; j < Cout; ++j) dw[j] += xc * g[j];
+  const int64_t nw = (int64_t)K * Cin * Cout;
+  const int64_t slab = 64, nslabs = (n_out + slab - 1) / slab;
+  const int nt = or_num_threads();
+  float* priv = (float*)calloc((size_t)nt * (size_t)nw, sizeof(float));
+  if (!priv) return;
+#pragma omp parallel
+  {
+#ifdef _OPENMP
+    float* dwt = priv + (int64_t)omp_get_thread_num() * nw;
+#else
+    float* dwt = priv;
+#endif
+#pragma omp for schedule(static)
+    for (int64_t s = 0; s < nslabs; ++s) {
+      const int64_t o0 = s * slab, o1 = o0 + slab < n_out ? o0 + slab : n_out;
+      for (int k = 0; k < K; ++k) {
+        float* dwk = dwt + (int64_t)k * Cin * Cout;
+        for (int64_t o = o0; o < o1; ++o) {
+          const int32_t i = nbr[o * K + k];
+          if (i < 0) continue;
+          const float* x = X + (int64_t)i * Cin;
+          const float* g = dY + o * Cout;
+          for (int c = 0; c < Cin; ++c) {
+            const float xc = x[c];
+            float* wr = dwk + (int64_t)c * Cout;
+            for (int j = 0; j < Cout; ++j) wr[j] += xc * g[j];
+          }
+        }
       }
     }
   }
+#pragma omp parallel for schedule(static)
+  for (int64_t e = 0; e < nw; ++e) {
+    float v = 0.f;
+    for (int t = 0; t < nt; ++t) v += priv[(int64_t)t * nw + e];
+    dW[e] = v;
+  }
+  free(priv);
 }
 
 int or_num_threads(void) {

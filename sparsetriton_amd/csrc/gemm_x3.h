@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const RingTile tile = ring_tile(n_dst, Nd, BN);
+  const RingTile tile = ring_tile(n_dst, Nd, BN, src_xcd(src));
   if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
   const int64_t row0 = tile.rt * kGemmBM;
   const int n0 = tile.ct * BN;
@@ -765,7 +765,7 @@ static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint3
                       const int32_t* rows, const float* Bt, float* out, E epi, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  const unsigned rgrid = ring_grid(n_dst, Nd, BN);
+  const unsigned rgrid = ring_grid(n_dst, Nd, BN, src_xcd(src));
   if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines() && buffer_ok(n_src, K, Kd, Nd, 4))
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true, E>
         <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, epi);

@@ -43,6 +43,11 @@ struct TiledSrc {
   const int16_t* __restrict__ klist;
   const int32_t* __restrict__ tmap;
   int K;
+  // Tile order of the ring kernels: 0 = descending over the whole grid; 1 = eight contiguous
+  // ranges of tiles, range x run by XCD x (workgroups are dispatched to the XCDs round-robin),
+  // each descending -- with tiles grouped by slabs of the row order (st_kmap_plans' bucket
+  // bits), each XCD's L2 then serves only its own slabs' source rows.
+  int xcd = 0;
   typedef int64_t RowCtx;
   __device__ __forceinline__ RowCtx row(int64_t r) const { return r; }
   __device__ __forceinline__ int32_t get_tile(int64_t tile, int j, int r) const {

@@ -1,5 +1,5 @@
-"""BASELINE configurations 1, 3, 4 and 5 on the GPU, every output and gradient tensor at full size
-against the float64 oracle (config 2 is covered by test_conv_gpu / test_kmap_gpu).
+"""BASELINE configurations 1 to 5 on the GPU, every output and gradient tensor at full size
+against the float64 oracle.
 
 Inputs are quantised to the compute dtype first, so the oracle sees the operands the kernels see.
 Tolerances (relative Frobenius error per tensor): fp32 2e-3, bf16 2e-2 -- the north-star bounds.
@@ -7,6 +7,10 @@ Output coordinates and kernel maps are compared bit for bit.  The adjoint identi
 <dY, Y> = <dX, X> = <dW, W> are checked beside the per-tensor comparison.
 
   config 1  SubMConv3D 16->32 k3, B=2, 64^3, 4096 uniform voxels, fp32 and bf16, both algorithms
+  config 2  SubMConv3D 64->64 k3, B=4, 1440x1440x41 LiDAR-like set (the benchmark's headline
+            workload), fp32 and bf16, both algorithms: ImplicitHashFlyGEMM runs the brick-index
+            lookups inside the GEMM at 64 channels, its forward and weight gradient bitwise equal
+            to PrecomputedNeighborGEMM's
   config 3  SparseConv3D 64->128 k3 s2 p1 fp32 on the config-2 set, both algorithms
   config 4  SparseConvTransposed3D 128->64 k3 s2 p1 bf16 on config 3's output coordinates
   config 5  SubMConv3D 128->128 k3 bf16, 1M voxels of 2-voxel walls in 256^3, PrecomputedNeighborGEMM
@@ -90,6 +94,59 @@ def test_config1_subm16x32(device, dtype, algo):
     if algo == ConvAlgo.PrecomputedNeighborGEMM:
         kmap = sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)][1]
         assert (kmap.neighbor_indices.cpu().numpy() == nbr).all()
+
+
+# ------------------------------------------------------------------- config 2
+
+@pytest.fixture(scope="module")
+def cfg2_map():
+    c, shape = workloads.config2(seed=0)
+    nbr = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, shape)
+    return c, shape, nbr
+
+
+_CFG2 = {}
+
+
+def _cfg2_case(cfg2_map, dtype):
+    """Inputs and float64 references of config 2 in `dtype` (built once per dtype)."""
+    if dtype not in _CFG2:
+        c, shape, nbr = cfg2_map
+        n = c.shape[0]
+        X, W, dY = _inputs(2, n, n, 64, 64, dtype)
+        ref = (O.fwd_f64_blas(X, W, nbr), O.dgrad_f64_blas(dY, W, nbr, n), O.wgrad_f64_blas(X, dY, nbr, 27))
+        _CFG2[dtype] = (X, W, dY, ref, {})
+    return _CFG2[dtype]
+
+
+@pytest.mark.parametrize("algo", list(ConvAlgo))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config2_subm64x64(device, cfg2_map, dtype, algo):
+    c, shape, nbr = cfg2_map
+    X, W, dY, ref, done = _cfg2_case(cfg2_map, dtype)
+    sp, out, dX, dW = _gpu(device, c, shape, 4, X, W, dY, dtype, algo)
+    assert c.shape[0] == 470_532 and torch.equal(out.C, sp.C)
+    _compare(out, dX, dW, ref, TOL[dtype], f"config2 {dtype} {algo.value}")
+    _adjoint(X, W, dY, out.F.detach().double().cpu().numpy(), dX.double().cpu().numpy(),
+             dW.double().cpu().numpy(), TOL[dtype])
+    if algo == ConvAlgo.PrecomputedNeighborGEMM:
+        kmap = sp._cache.neighbor_indices[(3, 1, 1, 1, True, False)][1]
+        assert (kmap.neighbor_indices.cpu().numpy() == nbr).all()
+        assert kmap.symmetric
+    else:
+        from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex
+
+        # the brick-index lookups inside the GEMM ran (no kernel map was stored)
+        assert isinstance(sp._cache.kmaps.get(("brick_index", 4, tuple(shape))), BrickIndex)
+        assert not sp._cache.neighbor_indices
+    done[algo] = (out.F.detach().clone(), dX.clone(), dW.clone())
+    if len(done) == 2:
+        # forward and weight gradient bitwise equal across the algorithms (same per-row offset
+        # order, same pair list); the input gradients agree to rounding
+        pre, fly = done[ConvAlgo.PrecomputedNeighborGEMM], done[ConvAlgo.ImplicitHashFlyGEMM]
+        assert torch.equal(pre[0], fly[0]) and torch.equal(pre[2], fly[2])
+        assert rel(pre[1].float().cpu(), fly[1].float().cpu()) < TOL[dtype] / 4
+        del _CFG2[dtype]
 
 
 # ------------------------------------------------------------- configs 3, 4
