@@ -110,6 +110,29 @@ int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale
                    int64_t capacity, int32_t* status, st_stream_t stream);
 
 /*
+ * Replaces HashTable.insert -> build_hash_table_kernel (utils/hash.py:193-258,
+ * 516-544), partitioned: the same insert as st_hash_insert (same keys, values,
+ * lowest row of a repeated coordinate, status counts) built segment by
+ * segment in LDS.  Rows are grouped by the segment of their home slot (per
+ * workgroup of 2048 rows, in LDS), then one workgroup per segment of 1024 or
+ * 2048 slots gathers its rows, inserts them by LDS CAS and stores the
+ * segment with coalesced writes; rows whose probe runs past their segment
+ * are inserted by global CAS after every segment is stored.  Three kernels,
+ * no global atomics but the spills'.  fresh = 1 builds into a table that is
+ * treated as empty (no clear needed: every slot is written); fresh = 0
+ * inserts into the table's current contents, as st_hash_insert does.
+ * workspace (st_hash_build_workspace bytes) must be zeroed before its first
+ * use; every call leaves it reusable as is.  Calls that share a workspace
+ * must not overlap.  ST_ERR_UNSUPPORTED above 16.7M slots or 8.4M rows and
+ * while the 16-lane probe mode is on (st_hash_probe_mode): use
+ * st_hash_insert there.
+ */
+int st_hash_build_workspace(int64_t n, int64_t capacity, int64_t* bytes);
+int st_hash_build(const void* coords, int coord_dtype, int64_t n, int64_t scale, uint64_t* keys, uint32_t* vals,
+                  int64_t capacity, int fresh, void* workspace, int64_t workspace_bytes, int32_t* status,
+                  st_stream_t stream);
+
+/*
  * Replaces HashTable.query -> query_hash_table_kernel (utils/hash.py:302-366, 546-580).
  * out[i] = row index stored for coords[i], or -1 when absent.
  */
@@ -503,11 +526,16 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
  * the workgroup reads its tile's offsets and source rows contiguously
  * instead of gathering map entries and masks row by row.  Same result as
  * st_gather_gemm with that map.  Reductions wider than 128 (16-bit and
- * ST_F32_BF16X3) or 64 (ST_F32) return ST_ERR_UNSUPPORTED.
+ * ST_F32_BF16X3) or 64 (ST_F32) return ST_ERR_UNSUPPORTED.  flags:
+ * ST_GATHER_REVERSE_K multiplies offset k's sources by Bt[K - 1 - k] -- the
+ * input gradient of a submanifold map that is its own transpose, read over
+ * the forward's plan with the weights as given (W (K, C_in, C_out) is then
+ * the Bt operand), with no ST_W_REVERSE copy: the same result bit for bit.
  */
+enum st_gather_flags { ST_GATHER_REVERSE_K = 1 };
 int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
                          const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, const void* bias,
-                         void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
+                         void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype, int flags, st_stream_t stream);
 
 /*
  * st_gather_gemm_tiled with the store epilogue of an evaluation-mode conv +

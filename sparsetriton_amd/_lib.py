@@ -25,6 +25,7 @@ STATUS_WORDS = 4
 STATUS_OVERFLOW, STATUS_BAD_COORD, STATUS_DUPLICATE, STATUS_OUT_OF_BOX = 0, 1, 2, 3
 
 W_TRANSPOSE, W_REVERSE, W_COPY = 0, 1, 2
+GATHER_REVERSE_K = 1
 COLUMN_SUM_NOALLOC_MAX_C = 2048
 MAX_KVOL = 512
 TILE_ROWS = 128
@@ -63,6 +64,8 @@ _SIGNATURES = {
     "st_fill_u64": [_P, _L, ctypes.c_uint64, _P],
     "st_hash_probe_mode": [_I],
     "st_hash_insert": [_P, _I, _L, _L, _P, _P, _L, _P, _P],
+    "st_hash_build_workspace": [_L, _L, ctypes.POINTER(_L)],
+    "st_hash_build": [_P, _I, _L, _L, _P, _P, _L, _I, _P, _L, _P, _P],
     "st_hash_query": [_P, _I, _L, _P, _P, _L, _P, _P],
     "st_kmap_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _P, _L, _P, _L, _L, _P, _P, _P],
     "st_kmap_subm_workspace": [_L, _L, _L, _L, _L, ctypes.POINTER(_L)],
@@ -94,7 +97,7 @@ _SIGNATURES = {
     "st_tile_plan": [_P, _L, _L, _P, _I, _I, _P, _L, _L, _P, _P, _P, _P],
     "st_column_sum": [_P, _L, _I, _I, _P, _P, _I, _P],
     "st_column_sum_noalloc": [_P, _L, _I, _I, _P, _I, _P],
-    "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
+    "st_gather_gemm_tiled": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P],
     "st_gather_gemm_tiled_epilogue": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _L, _I, _I, _I, _I,
                                       _P],
     "st_gather_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],

@@ -17,7 +17,7 @@ int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int co
                        float* out, Epi<float> epi, int64_t n_dst, int Kd, int Nd, hipStream_t stream);
 int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
                         const int32_t* tmap, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
-                        hipStream_t stream);
+                        hipStream_t stream, int rev);
 int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_out, const int32_t* pairs,
                        const int32_t* kstart, const int32_t* cstart, const int32_t* chunk_order, int K, int chunk,
                        int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
@@ -284,19 +284,20 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
 
 int st_gather_gemm_tiled(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
                          const int16_t* tile_klist, const int32_t* tile_map, const void* Bt, const void* bias, void* out,
-                         int64_t n_dst,
-                         int K, int Kd, int Nd, int dtype, st_stream_t stream) {
+                         int64_t n_dst, int K, int Kd, int Nd, int dtype, int flags, st_stream_t stream) {
   if (n_src < 0 || n_dst < 0 || K <= 0 || K > ST_MAX_KVOL || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
+  if (flags & ~ST_GATHER_REVERSE_K) return ST_ERR_ARG;
+  const int rev = (flags & ST_GATHER_REVERSE_K) ? 1 : 0;
   if (n_dst >= (1ll << 31) || n_src >= (1ll << 31)) return ST_ERR_ARG;
   if (n_dst == 0) return ST_OK;
   if (!perm || !tile_nk || !tile_klist || !tile_map || !Bt || !out || (n_src > 0 && !A)) return ST_ERR_ARG;
   if (n_src == 0) return fill_output(out, n_dst, Nd, dtype, bias, stream);
   if (dtype == ST_F32_BF16X3)
     return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
-                               (float*)out, bias_epi<float>(bias), n_dst, K, Kd, Nd, stream);
+                               (float*)out, bias_epi<float>(bias), n_dst, K, Kd, Nd, stream, rev);
   ST_DISPATCH_DTYPE(dtype, T,
                     ops_gather_tiled<T>((const T*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const T*)Bt,
-                                        (T*)out, bias_epi<T>(bias), n_dst, K, Kd, Nd, stream));
+                                        (T*)out, bias_epi<T>(bias), n_dst, K, Kd, Nd, stream, rev));
 }
 
 int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* perm, const int32_t* tile_nk,
@@ -313,7 +314,7 @@ int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* p
     const Epi<float> epi{(const float*)bias, scale, shift, (const float*)residual, relu ? 1 : 0};
     if (n_src == 0) return fill_output_epi<float>(out, n_dst, Nd, epi, stream);
     return ops_gather_tiled_x3((const float*)A, n_src, perm, tile_nk, tile_klist, tile_map, (const float*)Bt,
-                               (float*)out, epi, n_dst, K, Kd, Nd, stream);
+                               (float*)out, epi, n_dst, K, Kd, Nd, stream, 0);
   }
   ST_DISPATCH_DTYPE(dtype, T, (n_src == 0)
                                   ? fill_output_epi<T>(out, n_dst, Nd, Epi<T>{(const T*)bias, scale, shift, (const T*)residual, relu ? 1 : 0},
@@ -321,7 +322,7 @@ int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* p
                                   : ops_gather_tiled<T>((const T*)A, n_src, perm, tile_nk, tile_klist, tile_map,
                                                         (const T*)Bt, (T*)out,
                                                         Epi<T>{(const T*)bias, scale, shift, (const T*)residual, relu ? 1 : 0}, n_dst, K,
-                                                        Kd, Nd, stream));
+                                                        Kd, Nd, stream, 0));
 }
 
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,

@@ -302,7 +302,7 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
     F breg[BREGS];
     int32_t s0, s1;
     resolve_group(0);
-    load_b(klist_s[0], breg);
+    load_b(b_slice(src, klist_s[0]), breg);
     store_b(0, breg);
     __syncthreads();
     bool any_cur = sources(0, s0, s1);
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(256) void gather_gemm_pipe_kernel(
         __syncthreads();
       }
       if (has_next) {
-        const int kn = klist_s[i + 1];
+        const int kn = b_slice(src, klist_s[i + 1]);
         int32_t t0, t1;
         any_nxt = sources(i + 1, t0, t1);
         load_a(t0, t1, a_nxt);
@@ -408,33 +408,18 @@ struct RingTile {
 // offset-mask key, so the last row tiles hold the rows with the most
 // neighbours (the costliest tiles); starting with them leaves the cheap tiles
 // for the tail of the grid.
-// With `xcd` (one column tile only) the tiles are cut into eight contiguous
-// ranges, range x taken by the workgroups b = x mod 8 (those dispatched to XCD
-// x), each range descending; padding workgroups get row tile nrt.
-__device__ __forceinline__ RingTile ring_tile(int64_t n_dst, int Nd, int BN, bool xcd = false) {
+__device__ __forceinline__ RingTile ring_tile(int64_t n_dst, int Nd, int BN) {
   const int ncol = (Nd + BN - 1) / BN;
   const int64_t nrt = (n_dst + kGemmBM - 1) / kGemmBM;
   const int64_t b = blockIdx.x;
-  if (ncol == 1 && xcd) {
-    const int64_t x = b & 7, j = b >> 3;
-    const int64_t lo = nrt * x / 8, hi = nrt * (x + 1) / 8;
-    return RingTile{j < hi - lo ? hi - 1 - j : nrt, 0};
-  }
   if (ncol == 1) return RingTile{nrt - 1 - b, 0};
   const int64_t s = b >> 3, padded = (nrt + 7) / 8 * 8;
   return RingTile{padded - 1 - ((s / ncol) * 8 + (b & 7)), (int)(s % ncol)};
 }
 // Grid of the ring kernels for n_dst rows and Nd columns in BN-wide tiles.
-static inline unsigned ring_grid(int64_t n_dst, int Nd, int BN, bool xcd = false) {
+static inline unsigned ring_grid(int64_t n_dst, int Nd, int BN) {
   const int64_t rt = (n_dst + kGemmBM - 1) / kGemmBM, ncol = (Nd + BN - 1) / BN;
-  return (unsigned)(ncol == 1 && !xcd ? rt : ((rt + 7) / 8) * 8 * ncol);
-}
-template <typename Src>
-__host__ __device__ inline bool src_xcd(const Src& src) {
-  if constexpr (Src::kTiled)
-    return src.xcd != 0;
-  else
-    return false;
+  return (unsigned)(ncol == 1 ? rt : ((rt + 7) / 8) * 8 * ncol);
 }
 
 // ------------------------------------------ gather-GEMM, D-deep load ring
@@ -491,7 +476,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const RingTile tile = ring_tile(n_dst, Nd, BN, src_xcd(src));
+  const RingTile tile = ring_tile(n_dst, Nd, BN);
   if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
   const int64_t row0 = tile.rt * kGemmBM;
   const int n0 = tile.ct * BN;
@@ -647,7 +632,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
         if (s1 < 0) a_ring[SL][1][jj] = zero_frag<T>();
       }
     }
-    const int k = klist_s[i - loc + j];
+    const int k = b_slice(src, klist_s[i - loc + j]);
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
       const int idx = tid + jb * 256;
@@ -1456,13 +1441,6 @@ static int gemm_ring_depth() {
   return d;
 }
 
-// Tile order of the tiled ring kernels (TiledSrc::xcd): ST_TILE_XCD=1 takes
-// the XCD-contiguous ranges (read at every launch).
-static inline int tile_xcd_mode() {
-  const char* e = getenv("ST_TILE_XCD");
-  return (e && e[0] == '1') ? 1 : 0;
-}
-
 // Whole-line A gathers staged through LDS (default); ST_GATHER_LINES=0
 // selects fragment-shaped gathers straight into registers (comparison runs).
 static bool gather_lines() {
@@ -1490,7 +1468,7 @@ static void launch_pipe(const T* A, int64_t n_src, const Src& src, const uint32_
                         const T* Bt, T* out, E epi, int64_t n_dst, int K, int Kd, int Nd, int vec_a, int vec_b,
                         hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  const unsigned rgrid = ring_grid(n_dst, Nd, BN, src_xcd(src));
+  const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   // (IEEE fp32 keeps the register path: its MFMAs dominate and the A stage only costs occupancy there)
   if (vec_a && vec_b && Kd == KS * Frag<T>::KSTEP && gemm_ring_depth() == 2 && gather_lines() && sizeof(T) == 2 &&
       buffer_ok(n_src, K, Kd, Nd, sizeof(T)))
@@ -1766,8 +1744,8 @@ int ops_gather_map(const T* A, int64_t n_src, const int32_t* map, int64_t ks, in
 template <typename T>
 int ops_gather_tiled(const T* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
                      const int32_t* tmap, const T* Bt, T* out, Epi<T> epi, int64_t n_dst, int K, int Kd, int Nd,
-                     hipStream_t stream) {
-  TiledSrc src{nk, klist, tmap, K, tile_xcd_mode()};
+                     hipStream_t stream, int rev) {
+  TiledSrc src{nk, klist, tmap, K, rev};
   return launch_gather<T>(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 
@@ -1869,5 +1847,6 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
   X template int ops_gather_fly<T>(const T*, int64_t, const void*, int, const int32_t*, int, const SubmIndex&,       \
                                    const T*, T*, const T*, int, int, hipStream_t);                                  \
   X template int ops_gather_tiled<T>(const T*, int64_t, const int32_t*, const int32_t*, const int16_t*,              \
-                                     const int32_t*, const T*, T*, Epi<T>, int64_t, int, int, int, hipStream_t);   \
+                                     const int32_t*, const T*, T*, Epi<T>, int64_t, int, int, int, hipStream_t,    \
+                                     int);                                                                         \
   }

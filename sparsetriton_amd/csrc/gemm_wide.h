@@ -214,7 +214,7 @@ __global__ __launch_bounds__(128 * TP) void gather_gemm_wide_kernel(const T* __r
     any_ring[SL] = __ballot(any) != 0ull;
   };
   auto issue_b = [&](int i) {
-    const int k = uk_s[i];
+    const int k = b_slice(src, uk_s[i]);
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
       const int idx = tid + jb * NT;

@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
     v4f breg[BREGS];
     int32_t s0, s1;
     resolve_group(0);
-    load_b(klist_s[0], breg);
+    load_b(b_slice(src, klist_s[0]), breg);
     store_b(0, breg);
     __syncthreads();
     bool any_cur = sources(0, s0, s1);
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
         __syncthreads();
       }
       if (has_next) {
-        const int kn = klist_s[i + 1];
+        const int kn = b_slice(src, klist_s[i + 1]);
         int32_t t0, t1;
         any_nxt = sources(i + 1, t0, t1);
         load_a(t0, t1, a_nxt);
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const RingTile tile = ring_tile(n_dst, Nd, BN, src_xcd(src));
+  const RingTile tile = ring_tile(n_dst, Nd, BN);
   if (tile.rt * kGemmBM >= n_dst) return;  // padding of the folded grid (whole workgroup)
   const int64_t row0 = tile.rt * kGemmBM;
   const int n0 = tile.ct * BN;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
           if (s1 < 0) a_ring[SL][1][jj][h] = zero_frag<float>();
         }
     }
-    const int k = klist_s[i];
+    const int k = b_slice(src, klist_s[i]);
 #pragma unroll
     for (int jb = 0; jb < BREGS; ++jb) {
       const int idx = tid + jb * 256;
@@ -765,7 +765,7 @@ static void launch_x3(const float* A, int64_t n_src, const Src& src, const uint3
                       const int32_t* rows, const float* Bt, float* out, E epi, int64_t n_dst, int K, int Kd, int Nd,
                       int vec_a, int vec_b, hipStream_t stream) {
   const dim3 grid(st_blocks(n_dst, kGemmBM), st_blocks(Nd, BN));
-  const unsigned rgrid = ring_grid(n_dst, Nd, BN, src_xcd(src));
+  const unsigned rgrid = ring_grid(n_dst, Nd, BN);
   if (vec_a && vec_b && Kd == KS * 32 && gemm_ring_depth() == 2 && gather_lines() && buffer_ok(n_src, K, Kd, Nd, 4))
     gather_gemm_ring_x3_kernel<BN, KS, 2, Src, true, E>
         <<<rgrid, 256, 0, stream>>>(A, src, masks, W, rows, Bt, out, n_src, n_dst, K, Kd, Nd, epi);

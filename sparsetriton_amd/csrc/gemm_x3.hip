@@ -25,8 +25,8 @@ int ops_gather_hash_x3(const float* A, int64_t n_src, const void* coords, int co
 
 int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, const int32_t* nk, const int16_t* klist,
                         const int32_t* tmap, const float* Bt, float* out, Epi<float> epi, int64_t n_dst, int K, int Kd, int Nd,
-                        hipStream_t stream) {
-  TiledSrc src{nk, klist, tmap, K, tile_xcd_mode()};
+                        hipStream_t stream, int rev) {
+  TiledSrc src{nk, klist, tmap, K, rev};
   return launch_gather_x3(A, n_src, src, nullptr, (K + 31) / 32, perm, Bt, out, epi, n_dst, K, Kd, Nd, stream);
 }
 

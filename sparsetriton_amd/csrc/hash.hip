@@ -358,11 +358,299 @@ static bool group_probe() {
 
 static unsigned group_blocks(int64_t rows) { return (unsigned)((rows * kGroup + 255) / 256); }
 
+// ------------------------------------------------ partitioned table build
+//
+// The table split into segments of S consecutive slots; every row goes to
+// the segment of its home slot, then one workgroup per segment builds that
+// segment in LDS and writes it with coalesced stores -- instead of one
+// returning 64-bit CAS per row at a random slot of a table no XCD's L2 holds
+// (the CAS build runs at the memory-side atomic rate, ~11 G/s).  No global
+// atomics and no fences on the common path: each pass hands its results to
+// the next through a kernel boundary.
+//
+//   hash_bucket_kernel   a workgroup takes kBuildRows rows: their keys and
+//                        segments, counted and ranked per segment in LDS,
+//                        then written to the workgroup's own area grouped by
+//                        segment, with the per-(segment, workgroup) counts
+//                        and run offsets (segment-major).
+//   hash_segment_kernel  a workgroup per segment: the segment's slots in LDS
+//                        (empty for a fresh table, else loaded), its rows
+//                        gathered from every bucketing workgroup's run and
+//                        inserted by LDS CAS with linear probing, the value
+//                        by LDS atomic-min (the lowest row of a repeated
+//                        key); rows whose probe runs past the segment's end
+//                        go to the spill list; the segment stored.
+//   hash_spill_kernel    one workgroup: the spilled rows inserted into the
+//                        finished table by global CAS from their home slots,
+//                        as the CAS build does (returns at once when there
+//                        are none), then the spill count reset.
+// Linear probing never deletes, so a key already in the table sits behind an
+// unbroken run of occupied slots from its home: the LDS probe of the same key
+// (a prefix of the global probe) meets no empty slot before the segment's
+// end, spills, and the global probe finds the key.  The table's key -> row
+// mapping is the CAS build's; slot positions may differ (they depend on the
+// insertion order in either build).
+constexpr int kBuildRows = 2048;      // rows per bucketing workgroup (8 per thread)
+constexpr int kBuildMaxSegs = 8192;   // the bucketing pass's LDS count table
+constexpr int kBuildMaxSlots = 2048;  // slots per segment (24 KB of LDS)
+constexpr int kBuildMaxWgs = 4096;    // bucketing workgroups a segment gathers from
+
+// Slots per segment (1024 or 2048, leaving at most kBuildMaxSegs segments) and
+// the segment count; false for tables or row counts too large for the
+// partitioned build.
+inline bool build_geom(int64_t n, int64_t cap, int64_t* S, int64_t* nseg) {
+  if ((n + kBuildRows - 1) / kBuildRows > kBuildMaxWgs) return false;
+  for (int64_t s = 1024; s <= kBuildMaxSlots; s *= 2) {
+    const int64_t ns = (cap + s - 1) / s;
+    if (ns <= kBuildMaxSegs) {
+      *S = s;
+      *nseg = ns;
+      return true;
+    }
+  }
+  return false;
+}
+
+struct BuildWs {
+  int32_t* spills;     // spilled rows (zero between builds)
+  int32_t* cnt;        // nseg x nwg rows of segment s bucketed by workgroup w (segment-major)
+  int32_t* off;        // nseg x nwg: where that run starts in w's area
+  uint64_t* bkeys;     // nwg x kBuildRows keys, grouped by segment per workgroup
+  uint32_t* brows;     // the same for the rows
+  uint64_t* skeys;     // n spilled keys
+  uint32_t* srows;     // n spilled rows
+  int nwg;
+};
+
+inline int64_t build_align(int64_t v) { return (v + 255) / 256 * 256; }
+
+inline int64_t build_nwg(int64_t n) { return n > 0 ? (n + kBuildRows - 1) / kBuildRows : 1; }
+
+inline int64_t build_ws_bytes(int64_t n, int64_t nseg) {
+  const int64_t nwg = build_nwg(n), rows = nwg * kBuildRows, nn = n > 0 ? n : 1;
+  return build_align(4) + 2 * build_align(4 * nseg * nwg) + build_align(8 * rows) + build_align(4 * rows) +
+         build_align(8 * nn) + build_align(4 * nn);
+}
+
+inline BuildWs build_ws(void* ws, int64_t n, int64_t nseg) {
+  const int64_t nwg = build_nwg(n), rows = nwg * kBuildRows, nn = n > 0 ? n : 1;
+  char* p = (char*)ws;
+  BuildWs w;
+  w.nwg = (int)nwg;
+  w.spills = (int32_t*)p;
+  p += build_align(4);
+  w.cnt = (int32_t*)p;
+  p += build_align(4 * nseg * nwg);
+  w.off = (int32_t*)p;
+  p += build_align(4 * nseg * nwg);
+  w.bkeys = (uint64_t*)p;
+  p += build_align(8 * rows);
+  w.brows = (uint32_t*)p;
+  p += build_align(4 * rows);
+  w.skeys = (uint64_t*)p;
+  p += build_align(8 * nn);
+  w.srows = (uint32_t*)p;
+  return w;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void hash_bucket_kernel(const CT* __restrict__ coords, int64_t n, int64_t scale,
+                                                          uint32_t cap, uint32_t S, int nseg, BuildWs w,
+                                                          int32_t* __restrict__ status) {
+  constexpr int J = kBuildRows / 256;
+  __shared__ int cnt_s[kBuildMaxSegs];
+  __shared__ int scan_s[8];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < nseg; e += 256) cnt_s[e] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kBuildRows;
+  uint64_t key[J];
+  int seg[J], rank[J];
+  int bad = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int64_t i = base + j * 256 + tid;
+    seg[j] = -1;
+    key[j] = 0;
+    rank[j] = 0;
+    if (i < n) {
+      int64_t b, x, y, z;
+      load_coord(coords, i, b, x, y, z);
+      if (pack_key(b, x * scale, y * scale, z * scale, key[j])) {
+        seg[j] = (int)(home_slot(key[j], cap) / S);
+        rank[j] = atomicAdd(&cnt_s[seg[j]], 1);
+      } else {
+        ++bad;
+      }
+    }
+  }
+  bad = wave_sum(bad);
+  if ((tid & 63) == 0 && bad) atomicAdd(&status[ST_STATUS_BAD_COORD], bad);
+  __syncthreads();
+  // the counts -> run offsets in the workgroup's area (exclusive scan over the segments, each
+  // thread a contiguous range of them), both published segment-major
+  const int per = (nseg + 255) / 256, e0 = tid * per, e1 = min(nseg, e0 + per);
+  int sum = 0;
+  for (int e = e0; e < e1; ++e) sum += cnt_s[e];
+  int total;
+  int run = block_exclusive_scan(sum, scan_s, &total);
+  for (int e = e0; e < e1; ++e) {
+    const int c = cnt_s[e];
+    w.cnt[(int64_t)e * w.nwg + blockIdx.x] = c;
+    w.off[(int64_t)e * w.nwg + blockIdx.x] = run;
+    cnt_s[e] = run;
+    run += c;
+  }
+  __syncthreads();
+  const int64_t area = base;  // the workgroup's kBuildRows places
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (seg[j] < 0) continue;
+    const int64_t at = area + cnt_s[seg[j]] + rank[j];
+    w.bkeys[at] = key[j];
+    w.brows[at] = (uint32_t)(base + j * 256 + tid);
+  }
+}
+
+__global__ __launch_bounds__(256) void hash_segment_kernel(uint64_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                                                           uint32_t cap, uint32_t S, int fresh, BuildWs w,
+                                                           int32_t* __restrict__ status) {
+  __shared__ unsigned long long k_s[kBuildMaxSlots];
+  __shared__ uint32_t v_s[kBuildMaxSlots];
+  __shared__ int rs_s[kBuildMaxWgs + 1];  // where workgroup w's run starts among the segment's rows
+  __shared__ int ro_s[kBuildMaxWgs];      // that run's offset in w's area
+  __shared__ int scan_s[8];
+  const int tid = threadIdx.x;
+  const int seg = blockIdx.x;
+  const uint32_t s0 = (uint32_t)seg * S;
+  const uint32_t len = cap - s0 < S ? cap - s0 : S;
+  for (uint32_t e = tid; e < len; e += 256) {
+    k_s[e] = fresh ? ST_EMPTY_KEY : keys[s0 + e];
+    v_s[e] = fresh ? ST_NO_VAL : vals[s0 + e];
+  }
+  const int nwg = w.nwg;
+  const int per = (nwg + 255) / 256, q0 = tid * per, q1 = min(nwg, q0 + per);
+  int sum = 0;
+  for (int q = q0; q < q1; ++q) {
+    const int c = w.cnt[(int64_t)seg * nwg + q];
+    ro_s[q] = w.off[(int64_t)seg * nwg + q];
+    rs_s[q] = c;
+    sum += c;
+  }
+  int total;
+  int run = block_exclusive_scan(sum, scan_s, &total);  // (its barriers also order the LDS stores above)
+  for (int q = q0; q < q1; ++q) {
+    const int c = rs_s[q];
+    rs_s[q] = run;
+    run += c;
+  }
+  if (tid == 0) rs_s[nwg] = total;
+  __syncthreads();
+  int dup = 0;
+  for (int r = tid; r < total; r += 256) {
+    // the run holding row r: the last workgroup whose run starts at or before r
+    int lo = 0, hi = nwg - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (rs_s[mid] <= r)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int64_t at = (int64_t)lo * kBuildRows + ro_s[lo] + (r - rs_s[lo]);
+    const uint64_t key = w.bkeys[at];
+    const uint32_t row = w.brows[at];
+    bool placed = false;
+    for (uint32_t s = home_slot(key, cap) - s0; s < len; ++s) {
+      const unsigned long long old = atomicCAS(&k_s[s], (unsigned long long)ST_EMPTY_KEY, (unsigned long long)key);
+      if (old == ST_EMPTY_KEY || old == key) {
+        atomicMin(&v_s[s], row);
+        dup += old == key ? 1 : 0;
+        placed = true;
+        break;
+      }
+    }
+    if (!placed) {
+      const int q = atomicAdd(w.spills, 1);
+      w.skeys[q] = key;
+      w.srows[q] = row;
+    }
+  }
+  dup = wave_sum(dup);
+  if ((tid & 63) == 0 && dup) atomicAdd(&status[ST_STATUS_DUPLICATE], dup);
+  __syncthreads();
+  for (uint32_t e = tid; e < len; e += 256) {
+    keys[s0 + e] = k_s[e];
+    vals[s0 + e] = v_s[e];
+  }
+}
+
+__global__ __launch_bounds__(1024) void hash_spill_kernel(uint64_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                                                          uint32_t cap, BuildWs w, int32_t* __restrict__ status) {
+  const int ns = *w.spills;
+  if (ns == 0) return;
+  int sdup = 0, over = 0;
+  for (int q = threadIdx.x; q < ns; q += blockDim.x) {
+    const uint64_t key = w.skeys[q];
+    const uint32_t row = w.srows[q];
+    bool was_new = false;
+    const uint32_t s = insert_slot_cas(keys, cap, key, was_new);
+    if (s == ST_NO_VAL) {
+      ++over;
+      continue;
+    }
+    atomicMin(&vals[s], row);
+    sdup += was_new ? 0 : 1;
+  }
+  sdup = wave_sum(sdup);
+  over = wave_sum(over);
+  if ((threadIdx.x & 63) == 0) {
+    if (sdup) atomicAdd(&status[ST_STATUS_DUPLICATE], sdup);
+    if (over) atomicAdd(&status[ST_STATUS_OVERFLOW], over);
+  }
+  __syncthreads();  // every thread has read the count
+  if (threadIdx.x == 0) *w.spills = 0;
+}
+
 }  // namespace st
 
 using namespace st;
 
 extern "C" {
+
+int st_hash_build_workspace(int64_t n, int64_t capacity, int64_t* bytes) {
+  int64_t S, nseg;
+  if (n < 0 || n >= (1ll << 31) || capacity <= 0 || capacity >= (1ll << 31) || !bytes) return ST_ERR_ARG;
+  if (!build_geom(n, capacity, &S, &nseg)) return ST_ERR_UNSUPPORTED;
+  *bytes = build_ws_bytes(n, nseg);
+  return ST_OK;
+}
+
+int st_hash_build(const void* coords, int coord_dtype, int64_t n, int64_t scale, uint64_t* keys, uint32_t* vals,
+                  int64_t capacity, int fresh, void* workspace, int64_t workspace_bytes, int32_t* status,
+                  st_stream_t stream) {
+  int64_t S, nseg;
+  if (n < 0 || n >= (1ll << 31) || capacity <= 0 || capacity >= (1ll << 31) || scale < 1 || !keys || !vals ||
+      !status)
+    return ST_ERR_ARG;
+  if (coord_dtype < ST_COORD_I16 || coord_dtype > ST_COORD_I64) return ST_ERR_UNSUPPORTED;
+  if (group_probe() || !build_geom(n, capacity, &S, &nseg)) return ST_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < build_ws_bytes(n, nseg) || (n > 0 && !coords)) return ST_ERR_ARG;
+  if (n == 0 && !fresh) return ST_OK;
+  BuildWs w = build_ws(workspace, n, nseg);
+  if (n > 0) {
+    ST_DISPATCH_COORD(coord_dtype, CT,
+                      hash_bucket_kernel<CT><<<(unsigned)w.nwg, 256, 0, stream>>>(
+                          (const CT*)coords, n, scale, (uint32_t)capacity, (uint32_t)S, (int)nseg, w, status));
+  } else {
+    w.nwg = 0;  // a fresh empty table: every segment stored empty
+  }
+  hash_segment_kernel<<<(unsigned)nseg, 256, 0, stream>>>(keys, vals, (uint32_t)capacity, (uint32_t)S,
+                                                           fresh ? 1 : 0, w, status);
+  if (n > 0) hash_spill_kernel<<<1, 1024, 0, stream>>>(keys, vals, (uint32_t)capacity, w, status);
+  ST_CHECK_LAUNCH();
+  return ST_OK;
+}
 
 const char* st_version(void) { return "sparsetriton_amd 0.1 gfx950"; }
 

@@ -27,6 +27,7 @@ __global__ __launch_bounds__(kSubmThreads) void subm_clear_kernel(SubmIndex ix, 
   if (ix.flag && t == 0) *ix.flag = 0;
   uint4* occ16 = reinterpret_cast<uint4*>(ix.occ);  // the byte array is padded to 16 bytes
   for (int64_t e = t; e < (ix.nbricks + 15) / 16; e += stride) occ16[e] = make_uint4(0u, 0u, 0u, 0u);
+  for (int64_t e = t; e < 2 * ix.ntiles; e += stride) ix.tile_pub[e] = 0;
   for (int64_t e = t; e < n; e += stride) ix.rowmap[e] = 0x7FFFFFFF;
 }
 
@@ -60,6 +61,25 @@ __device__ __forceinline__ int subm_entry_count(const SubmIndex& ix, int64_t e) 
   return c;
 }
 
+// Level-1 word e from the 64 occupancy bytes of its bricks (the array is padded
+// to 16 bytes, bytes past the last brick are zero).
+__device__ __forceinline__ unsigned long long subm_occ_bits(const SubmIndex& ix, int64_t e) {
+  const uint4* src = reinterpret_cast<const uint4*>(ix.occ + e * 64);
+  unsigned long long bits = 0ull;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (e * 64 + q * 16 >= ix.nbricks) break;
+    const uint4 v = src[q];
+    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb)
+        if ((wv[j] >> (8 * bb)) & 0xFFu) bits |= 1ull << (q * 16 + j * 4 + bb);
+  }
+  return bits;
+}
+
 // tile_sums[t] = bricks (or voxels) of tile t's level-1 entries (one per thread)
 template <bool BRICKS>
 __global__ __launch_bounds__(kSubmThreads) void subm_tile_sum_kernel(SubmIndex ix) {
@@ -67,24 +87,7 @@ __global__ __launch_bounds__(kSubmThreads) void subm_tile_sum_kernel(SubmIndex i
   if (!BRICKS && subm_overflowed(ix)) return;
   const int tid = threadIdx.x;
   const int64_t e = (int64_t)blockIdx.x * kSubmTile + tid;
-  if (BRICKS && e < ix.nw1) {
-    // level-1 word e from the 64 occupancy bytes of its bricks (the array is padded to 16 bytes,
-    // bytes past the last brick are zero)
-    const uint4* src = reinterpret_cast<const uint4*>(ix.occ + e * 64);
-    unsigned long long bits = 0ull;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (e * 64 + q * 16 >= ix.nbricks) break;
-      const uint4 v = src[q];
-      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb)
-          if ((wv[j] >> (8 * bb)) & 0xFFu) bits |= 1ull << (q * 16 + j * 4 + bb);
-    }
-    ix.l1[e].bits = bits;
-  }
+  if (BRICKS && e < ix.nw1) ix.l1[e].bits = subm_occ_bits(ix, e);
   int c = e < ix.nw1 ? subm_entry_count<BRICKS>(ix, e) : 0;
   c = wave_sum(c);
   if ((tid & 63) == 0) red_s[tid >> 6] = c;
@@ -103,9 +106,31 @@ __global__ __launch_bounds__(kSubmThreads) void subm_tile_sum_kernel(SubmIndex i
 // voxels exceed nrows (*voxels is then 0); the voxel pass of an overflowed
 // index returns at once.
 // The tiles' offsets: with `scanned` the tile sums were replaced by their
-// exclusive scan (launch_subm_prefix, for many tiles); otherwise each
-// workgroup sums the tiles before its own, which costs O(ntiles) loads a
-// workgroup but saves a launch while the tiles are few.
+// exclusive scan; otherwise each workgroup sums the tiles before its own.
+// (launch_subm_level takes this kernel only above kSubmInlineTiles tiles, with
+// the scan; below, subm_level_kernel does a level in one launch.)
+template <bool BRICKS>
+__device__ __forceinline__ void subm_entry_write(const SubmIndex& ix, int64_t e, int p, int32_t* __restrict__ voxels) {
+  if (e >= ix.nw1) return;
+  const SubmL1 v = ix.l1[e];
+  const int nb = (int)__popcll(v.bits);
+  if (BRICKS) {
+    ix.l1[e].bpre = p;
+    for (int j = 0; j < nb && p + j < ix.cap2; ++j) ix.l2bits[p + j] = 0ull;
+    if ((int64_t)p + nb > ix.cap2 && ix.flag) atomicOr(ix.flag, 1);
+  } else {
+    ix.l1[e].v = p;
+    int64_t q = p;
+    for (int j = 0; j < nb; ++j) {
+      ix.l2pre[v.bpre + j] = (int32_t)q;
+      q += (int)__popcll(ix.l2bits[v.bpre + j]);
+    }
+    const bool over = q > ix.nrows && ix.flag;
+    if (over) atomicOr(ix.flag, 1);
+    if (voxels && e == ix.nw1 - 1) *voxels = over ? 0 : (int32_t)q;
+  }
+}
+
 template <bool BRICKS>
 __global__ __launch_bounds__(kSubmThreads) void subm_prefix_kernel(SubmIndex ix, int32_t* __restrict__ voxels,
                                                                    bool scanned) {
@@ -127,25 +152,63 @@ __global__ __launch_bounds__(kSubmThreads) void subm_prefix_kernel(SubmIndex ix,
   const int c = e < ix.nw1 ? subm_entry_count<BRICKS>(ix, e) : 0;
   int total;
   const int p = off + block_exclusive_scan(c, scan_s, &total);
-  if (e < ix.nw1) {
-    const SubmL1 v = ix.l1[e];
-    const int nb = (int)__popcll(v.bits);
-    if (BRICKS) {
-      ix.l1[e].bpre = p;
-      for (int j = 0; j < nb && p + j < ix.cap2; ++j) ix.l2bits[p + j] = 0ull;
-      if ((int64_t)p + nb > ix.cap2 && ix.flag) atomicOr(ix.flag, 1);
-    } else {
-      ix.l1[e].v = p;
-      int64_t q = p;
-      for (int j = 0; j < nb; ++j) {
-        ix.l2pre[v.bpre + j] = (int32_t)q;
-        q += (int)__popcll(ix.l2bits[v.bpre + j]);
-      }
-      const bool over = q > ix.nrows && ix.flag;
-      if (over) atomicOr(ix.flag, 1);
-      if (voxels && e == ix.nw1 - 1) *voxels = over ? 0 : (int32_t)q;
-    }
+  subm_entry_write<BRICKS>(ix, e, p, voxels);
+}
+
+// Both passes of a level in one launch for indexes of at most kSubmInlineTiles
+// tiles: each workgroup counts its tile's entries (BRICKS: building their
+// level-1 words first), publishes the tile's total in tile_pub (flag bit 31,
+// cleared by subm_clear_kernel), then adds the totals of the tiles before its
+// own.  Workgroups are dispatched in index order, so every earlier tile is
+// running or done and publishes within microseconds; a total still missing
+// after `spin` polls is computed from the index directly (subm_tile_total),
+// so the wait is bounded and the result exact either way.
+constexpr int32_t kPubFlag = (int32_t)0x80000000u;
+
+// Bricks (from the occupancy bytes: the tile's level-1 words may not be built
+// yet) or voxels of tile j, summed by one thread.
+template <bool BRICKS>
+__device__ int subm_tile_total(const SubmIndex& ix, int64_t j) {
+  int s = 0;
+  const int64_t e1 = min((j + 1) * (int64_t)kSubmTile, ix.nw1);
+  for (int64_t e = j * kSubmTile; e < e1; ++e) {
+    if (BRICKS)
+      s += (int)__popcll(subm_occ_bits(ix, e));
+    else
+      s += subm_entry_count<false>(ix, e);
   }
+  return s;
+}
+
+template <bool BRICKS>
+__global__ __launch_bounds__(kSubmThreads) void subm_level_kernel(SubmIndex ix, int32_t* __restrict__ voxels,
+                                                                  int spin) {
+  __shared__ int red_s[4];
+  __shared__ int scan_s[8];
+  if (!BRICKS && subm_overflowed(ix)) return;
+  const int tid = threadIdx.x;
+  const int64_t t = blockIdx.x;
+  const int64_t e = t * kSubmTile + tid;
+  if (BRICKS && e < ix.nw1) ix.l1[e].bits = subm_occ_bits(ix, e);
+  const int c = e < ix.nw1 ? subm_entry_count<BRICKS>(ix, e) : 0;
+  int total;
+  const int local = block_exclusive_scan(c, scan_s, &total);
+  int32_t* pub = ix.tile_pub + (BRICKS ? 0 : ix.ntiles);
+  if (tid == 0) __hip_atomic_store(&pub[t], total | kPubFlag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int off = 0;
+  for (int64_t j = tid; j < t; j += kSubmThreads) {
+    int v = __hip_atomic_load(&pub[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int s = 0; !(v & kPubFlag) && s < spin; ++s) {
+      __builtin_amdgcn_s_sleep(2);
+      v = __hip_atomic_load(&pub[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    off += (v & kPubFlag) ? (v & ~kPubFlag) : subm_tile_total<BRICKS>(ix, j);
+  }
+  off = wave_sum(off);
+  if ((tid & 63) == 0) red_s[tid >> 6] = off;
+  __syncthreads();
+  off = red_s[0] + red_s[1] + red_s[2] + red_s[3];
+  subm_entry_write<BRICKS>(ix, e, off + local, voxels);
 }
 
 // Level-2 bits at the row's brick rank (one non-returning atomic per row: a
@@ -744,14 +807,27 @@ __global__ __launch_bounds__(256) void ocb_inverse_kernel(const CT* __restrict__
 // are scanned once first (the inline sum's O(ntiles^2) loads over the grid
 // would outgrow the extra launch).
 constexpr int64_t kSubmInlineTiles = 1024;
+// Polls of a missing tile total before subm_level_kernel computes it itself
+// (ST_SUBM_SPIN overrides; 0 computes every earlier tile's total directly).
+static int subm_spin() {
+  const char* e = getenv("ST_SUBM_SPIN");
+  return e ? atoi(e) : 4096;
+}
+
+// One level of the index (bricks or voxels): the counts and prefix of its
+// level-1 entries.  Up to kSubmInlineTiles tiles one launch does both
+// (subm_level_kernel); above, the tile sums, their scan and the prefix run as
+// three launches.
 template <bool BRICKS>
-int launch_subm_prefix(const SubmIndex& ix, int32_t* voxels, hipStream_t stream) {
-  const bool scan = ix.ntiles > kSubmInlineTiles;
-  if (scan) {
-    const int rc = launch_exclusive_scan(ix.tile_sums, ix.ntiles, stream);
-    if (rc != ST_OK) return rc;
+int launch_subm_level(const SubmIndex& ix, int32_t* voxels, hipStream_t stream) {
+  if (ix.ntiles <= kSubmInlineTiles) {
+    subm_level_kernel<BRICKS><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix, voxels, subm_spin());
+    return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
   }
-  subm_prefix_kernel<BRICKS><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix, voxels, scan);
+  subm_tile_sum_kernel<BRICKS><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix);
+  const int rc = launch_exclusive_scan(ix.tile_sums, ix.ntiles, stream);
+  if (rc != ST_OK) return rc;
+  subm_prefix_kernel<BRICKS><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix, voxels, true);
   return hipGetLastError() == hipSuccess ? ST_OK : ST_ERR_HIP;
 }
 
@@ -806,11 +882,9 @@ int st_subm_index(const void* coords, int coord_dtype, int64_t n, int64_t batche
   ST_DISPATCH_COORD(coord_dtype, CT, {
     const CT* c = (const CT*)coords;
     subm_occ_kernel<CT><<<rows, kSubmThreads, 0, stream>>>(c, n, ix, status);
-    subm_tile_sum_kernel<true><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix);
-    if (launch_subm_prefix<true>(ix, nullptr, stream) != ST_OK) return ST_ERR_HIP;
+    if (launch_subm_level<true>(ix, nullptr, stream) != ST_OK) return ST_ERR_HIP;
     subm_l2_kernel<CT><<<rows, kSubmThreads, 0, stream>>>(c, n, ix);
-    subm_tile_sum_kernel<false><<<(unsigned)ix.ntiles, kSubmThreads, 0, stream>>>(ix);
-    if (launch_subm_prefix<false>(ix, nullptr, stream) != ST_OK) return ST_ERR_HIP;
+    if (launch_subm_level<false>(ix, nullptr, stream) != ST_OK) return ST_ERR_HIP;
     subm_rowmap_kernel<CT><<<rows, kSubmThreads, 0, stream>>>(c, n, ix, status);
   });
   ST_CHECK_LAUNCH();
@@ -884,11 +958,9 @@ int st_outcoords_brick_plan(const void* in_coords, int coord_dtype, int64_t n, c
   ST_DISPATCH_COORD(coord_dtype, CT, {
     const CT* c = (const CT*)in_coords;
     ocb_occ_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox, status);
-    subm_tile_sum_kernel<true><<<tiles, kSubmThreads, 0, stream>>>(ox);
-    if (launch_subm_prefix<true>(ox, nullptr, stream) != ST_OK) return ST_ERR_HIP;
+    if (launch_subm_level<true>(ox, nullptr, stream) != ST_OK) return ST_ERR_HIP;
     ocb_l2_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox);
-    subm_tile_sum_kernel<false><<<tiles, kSubmThreads, 0, stream>>>(ox);
-    if (launch_subm_prefix<false>(ox, total, stream) != ST_OK) return ST_ERR_HIP;
+    if (launch_subm_level<false>(ox, total, stream) != ST_OK) return ST_ERR_HIP;
     ocb_rank_clear_kernel<<<2048, 256, 0, stream>>>(ox, total, status);
     ocb_rankmin_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox);
     ocb_count_kernel<CT><<<grid, 256, 0, stream>>>(c, rk, offsets, g, ox, block_counts);

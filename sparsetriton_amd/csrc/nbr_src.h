@@ -43,17 +43,24 @@ struct TiledSrc {
   const int16_t* __restrict__ klist;
   const int32_t* __restrict__ tmap;
   int K;
-  // Tile order of the ring kernels: 0 = descending over the whole grid; 1 = eight contiguous
-  // ranges of tiles, range x run by XCD x (workgroups are dispatched to the XCDs round-robin),
-  // each descending -- with tiles grouped by slabs of the row order (st_kmap_plans' bucket
-  // bits), each XCD's L2 then serves only its own slabs' source rows.
-  int xcd = 0;
+  // rev: the GEMM's B slice of offset k is Bt[K - 1 - k] (the input gradient of a
+  // submanifold map that is its own transpose, with the weights as given)
+  int rev = 0;
   typedef int64_t RowCtx;
   __device__ __forceinline__ RowCtx row(int64_t r) const { return r; }
   __device__ __forceinline__ int32_t get_tile(int64_t tile, int j, int r) const {
     return tmap[((int64_t)tile * K + j) * kTileRows + r];
   }
 };
+
+// Index of the B slice that multiplies the sources of offset k.
+template <typename Src>
+__device__ __forceinline__ int b_slice(const Src& src, int k) {
+  if constexpr (Src::kTiled)
+    return src.rev ? src.K - 1 - k : k;
+  else
+    return k;
+}
 
 template <typename CT>
 struct HashSrc {

@@ -244,12 +244,19 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(Keys in, int64_t n, 
 // loads are issued kPlanBatch at a time before any store, so a tile costs
 // about three memory round trips (perm, mask, map) rather than one per offset.
 constexpr int kPlanBatch = 16;
+//
+// With `skeys` (the sort's keys in sorted order, key_mode 1: the mask itself
+// in the low K bits, 2: a 3x3x3 mask with its bits reordered as mask_key
+// does) the tile's union comes from its rows' keys, read contiguously and
+// independently of perm, instead of from each row's mask through perm.
 __global__ __launch_bounds__(256) void tile_plan_kernel(const int32_t* __restrict__ map, int64_t ks, int64_t rs,
                                                         const uint32_t* __restrict__ masks, int W, int K,
                                                         const int32_t* __restrict__ perm, int64_t n_dst,
                                                         int64_t n_src, int32_t* __restrict__ tile_nk,
                                                         int16_t* __restrict__ tile_klist,
-                                                        int32_t* __restrict__ tile_map) {
+                                                        int32_t* __restrict__ tile_map,
+                                                        const uint32_t* __restrict__ skeys = nullptr,
+                                                        int key_mode = 0) {
   __shared__ uint32_t tmask_s[2][ST_MAX_KVOL / 32];
   __shared__ int16_t klist_s[ST_MAX_KVOL];
   __shared__ int nk_s;
@@ -258,7 +265,22 @@ __global__ __launch_bounds__(256) void tile_plan_kernel(const int32_t* __restric
   const int64_t tile = blockIdx.x;
   const int64_t gr = tile * kTileRows + r;
   const int32_t row = gr < n_dst ? perm[gr] : -1;
-  if (masks) {
+  if (skeys && key_mode) {
+    uint32_t v = (half == 0 && gr < n_dst) ? skeys[gr] : 0u;
+    v = wave_or(v);
+    if (half == 0 && lane == 0) tmask_s[wid][0] = v;
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t kb = tmask_s[0][0] | tmask_s[1][0], m = 0u;
+      if (key_mode == 2) {
+        for (int k = 0; k < 27; ++k) m |= ((kb >> kCubeKeyBits.pos[k]) & 1u) << k;
+      } else {
+        m = K < 32 ? kb & ((1u << K) - 1u) : kb;
+      }
+      tmask_s[0][0] = m;
+      tmask_s[1][0] = 0u;
+    }
+  } else if (masks) {
     // waves 0 and 1 hold the tile's 128 rows; waves 2 and 3 repeat them
     for (int w = 0; w < W; ++w) {
       uint32_t v = (half == 0 && row >= 0) ? masks[(int64_t)row * W + w] : 0u;
@@ -317,8 +339,11 @@ extern "C" int st_kmap_sort_workspace(int64_t n, size_t* bytes) {
 
 namespace st {
 // LSD radix sort of rows by mask key into perm; buffers checked by the caller
+// With `sorted_keys` the last pass also writes the keys in sorted order: keys_tmp + n when the
+// pass count is odd, keys_tmp when even (*sorted_keys), so a caller needs no second buffer.
 static int launch_sort(const uint32_t* masks, int mask_words, int K, int64_t n, uint32_t* keys_tmp,
-                       int32_t* rows_tmp, int32_t* perm, int32_t* hist, hipStream_t stream, int bbits = 0) {
+                       int32_t* rows_tmp, int32_t* perm, int32_t* hist, hipStream_t stream, int bbits = 0,
+                       const uint32_t** sorted_keys = nullptr) {
   const int64_t tile = radix_tile(n), ntiles = (n + tile - 1) / tile;
   if (K + bbits > 32) bbits = 0;
   const int passes = radix_passes(K, bbits);
@@ -329,7 +354,8 @@ static int launch_sort(const uint32_t* masks, int mask_words, int K, int64_t n, 
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
     const int in = p & 1, out = in ^ 1;
-    uint32_t* kout = p + 1 < passes ? kbuf[out] : nullptr;
+    uint32_t* kout = p + 1 < passes ? kbuf[out] : (sorted_keys ? kbuf[out] : nullptr);
+    if (p + 1 == passes && sorted_keys) *sorted_keys = kbuf[out];
     // the first pass computes the keys from the masks; later ones read the previous pass's output
     const Keys ks = p == 0 ? Keys{nullptr, nullptr, masks, mask_words, K == 27, K, bbits, n}
                            : Keys{kbuf[in], vbuf[in], nullptr, 0, 0, 0, 0, 1};
@@ -513,13 +539,16 @@ extern "C" int st_kmap_plans(const int32_t* map, int64_t map_k_stride, int64_t m
       if (rc != ST_OK) return rc;
     }
     if (n_dst > 0) {
+      // the sorted keys give each tile's offset union when they invert to the mask (K <= 32)
+      const int key_mode = W == 1 ? (K == 27 ? 2 : 1) : 0;
+      const uint32_t* skeys = nullptr;
       const int rc = st::launch_sort(row_masks, W, K, n_dst, (uint32_t*)(sb + S.sort_keys),
                                      (int32_t*)(sb + S.sort_rows), perm, (int32_t*)(sb + S.sort_hist), stream,
-                                     bucket_bits);
+                                     bucket_bits, key_mode ? &skeys : nullptr);
       if (rc != ST_OK) return rc;
       st::tile_plan_kernel<<<(unsigned)L[ST_PLAN_TILES], 256, 0, stream>>>(
           map, map_k_stride, map_r_stride, row_masks, W, K, perm, n_dst, n_src, (int32_t*)(pb + L[ST_PLAN_TILE_NK]),
-          (int16_t*)(pb + L[ST_PLAN_TILE_KLIST]), (int32_t*)(pb + L[ST_PLAN_TILE_MAP]));
+          (int16_t*)(pb + L[ST_PLAN_TILE_KLIST]), (int32_t*)(pb + L[ST_PLAN_TILE_MAP]), skeys, key_mode);
       ST_CHECK_LAUNCH();
     }
     return ST_OK;

@@ -35,6 +35,7 @@ struct SubmIndex {
   int32_t* l2pre;              // voxels before each occupied brick
   int32_t* rowmap;
   int32_t* tile_sums;          // per tile of kSubmTile level-1 entries: its bricks or voxels (ntiles + 1)
+  int32_t* tile_pub;           // the tiles' published totals, bricks then voxels (2 x ntiles, cleared)
   // Overflow flag of an index whose rows bound is not a property of its input (the output
   // index of a strided / transposed build, sized from the kernel's candidate bound): set when
   // the occupied bricks exceed cap2 or the distinct voxels exceed nrows, after which the
@@ -229,6 +230,7 @@ inline int64_t subm_workspace_bytes(int64_t n, int64_t batches, int64_t sx, int6
   if (!subm_geom(n, batches, sx, sy, sz, &nbricks, &nw1, &cap2)) return -1;
   const int64_t ntiles = (nw1 + kSubmTile - 1) / kSubmTile;
   return (int64_t)(subm_align256((size_t)nbricks) + subm_align256(sizeof(int32_t) * (size_t)(ntiles + 1)) +
+                   subm_align256(sizeof(int32_t) * (size_t)(2 * ntiles)) +
                    subm_align256(sizeof(SubmL1) * (size_t)nw1) +
                    subm_align256(sizeof(unsigned long long) * (size_t)cap2) +
                    subm_align256(sizeof(int32_t) * (size_t)cap2) + subm_align256(sizeof(int32_t) * (size_t)(n > 0 ? n : 1)));
@@ -246,6 +248,8 @@ inline bool subm_view(void* workspace, int64_t n, int64_t batches, int64_t sx, i
   p += subm_align256((size_t)ix->nbricks);
   ix->tile_sums = (int32_t*)p;
   p += subm_align256(sizeof(int32_t) * (size_t)(ix->ntiles + 1));
+  ix->tile_pub = (int32_t*)p;
+  p += subm_align256(sizeof(int32_t) * (size_t)(2 * ix->ntiles));
   ix->l1 = (SubmL1*)p;
   p += subm_align256(sizeof(SubmL1) * (size_t)ix->nw1);
   ix->l2bits = (unsigned long long*)p;

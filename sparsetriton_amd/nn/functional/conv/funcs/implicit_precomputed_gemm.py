@@ -62,14 +62,17 @@ def tiled_ok(dtype: torch.dtype, Kd: int) -> bool:
     return Kd <= (64 if _lib.compute_code(dtype) == 0 else 128)
 
 
-def gather_gemm_tiled(A: torch.Tensor, tiles, Bt: torch.Tensor, n_dst: int, K: int, bias=None) -> torch.Tensor:
-    """out[perm[t]] = sum over the tile's offsets of A[source] @ Bt[k]^T (+ bias), over a tile plan."""
+def gather_gemm_tiled(A: torch.Tensor, tiles, Bt: torch.Tensor, n_dst: int, K: int, bias=None,
+                      reverse_k: bool = False) -> torch.Tensor:
+    """out[perm[t]] = sum over the tile's offsets of A[source] @ Bt[k]^T (+ bias), over a tile plan;
+    with ``reverse_k`` offset k's sources meet Bt[K - 1 - k]."""
     Kd = A.shape[1]
     Nd = Bt.shape[1]
     out = torch.empty((n_dst, Nd), dtype=A.dtype, device=A.device)
     _lib.call("st_gather_gemm_tiled", _lib.ptr(A), A.shape[0], tiles.perm_ptr, tiles.nk_ptr,
               tiles.klist_ptr, tiles.tmap_ptr, _lib.ptr(Bt), _lib.ptr(bias), _lib.ptr(out), n_dst, K,
-              Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+              Kd, Nd, _lib.compute_code(A.dtype), _lib.GATHER_REVERSE_K if reverse_k else 0,
+              _lib.stream_of(A.device))
     return out
 
 
@@ -117,12 +120,13 @@ def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> tor
     """Input gradient over the transposed map, in the mask-sorted order of the backward plan.
 
     For a symmetric (odd-kernel submanifold) map the transpose is the map read
-    with offsets reversed: dX[i] = sum_j dY[nbr[j, i]] @ W[K-1-j]^T."""
-    if kmap.symmetric:
-        W = weight_prep(W, _lib.W_REVERSE)
+    with offsets reversed: dX[i] = sum_j dY[nbr[j, i]] @ W[K-1-j]^T; the tiled GEMM
+    takes the reversal as it addresses the weights (no reversed copy)."""
     dY = kmap.fold_output_rows(dY)
     if tiled_ok(dY.dtype, dY.shape[1]):
-        return gather_gemm_tiled(dY, kmap.backward_tiles(), W, kmap.n_in, kmap.K)
+        return gather_gemm_tiled(dY, kmap.backward_tiles(), W, kmap.n_in, kmap.K, reverse_k=kmap.symmetric)
+    if kmap.symmetric:
+        W = weight_prep(W, _lib.W_REVERSE)
     plan = kmap.backward_plan()
     if kmap.symmetric:
         return gather_gemm(dY, kmap.nbr, kmap.k_stride, kmap.r_stride, kmap.out_masks, W, kmap.n_in, kmap.K,

@@ -25,6 +25,8 @@ Insert and query run as HIP kernels (``st_hash_insert`` / ``st_hash_query``);
 there is no CPU implementation of them.
 """
 
+import ctypes
+
 import torch
 
 from sparsetriton_amd import _lib
@@ -110,6 +112,7 @@ class HashTable:
         self._pending = None  # (coords, scale) recorded by insert(), applied by _materialize()
         self._needs_clear = False
         self.status = None
+        self._build_ws = None  # zeroed workspace of st_hash_build (left zeroed by every build)
         if table_keys is not None and table_values is not None:
             assert table_keys.shape == table_values.shape, "table_keys and table_values must have the same shape."
             self._keys, self._vals = table_keys, table_values
@@ -178,17 +181,46 @@ class HashTable:
         return self
 
     def _materialize(self) -> None:
-        """Apply the deferred clear and insert."""
-        if self._needs_clear:
-            self._needs_clear = False
-            _lib.fill_(self._keys, -1)
-            _lib.fill_(self._vals, -1)
+        """Apply the deferred clear and insert: a clear followed by an insert is one partitioned
+        build into the table as empty (``st_hash_build``, no fill); the CAS insert
+        (``st_hash_insert``) after a fill where that build is not available."""
         if self._pending is not None:
             keys, scale = self._pending
             self._pending = None
+            fresh = self._needs_clear
+            self._needs_clear = False
+            if self._build(keys, scale, fresh):
+                return
+            if fresh:
+                _lib.fill_(self._keys, -1)
+                _lib.fill_(self._vals, -1)
             _lib.call("st_hash_insert", _lib.ptr(keys), _lib.coord_code(keys.dtype), keys.shape[0], int(scale),
                       _lib.ptr(self._keys), _lib.ptr(self._vals), self.capacity,
                       _lib.ptr(self._status()), _lib.stream_of(self.device))
+        elif self._needs_clear:
+            self._needs_clear = False
+            _lib.fill_(self._keys, -1)
+            _lib.fill_(self._vals, -1)
+
+    def _build(self, keys: torch.Tensor, scale: int, fresh: bool) -> bool:
+        """``st_hash_build`` of ``keys`` into the table; False when the table is too large for it or
+        the 16-lane probe mode is on (the caller then runs the CAS insert)."""
+        lib = _lib.lib()
+        n = keys.shape[0]
+        nbytes = ctypes.c_int64()
+        rc = lib.st_hash_build_workspace(n, self.capacity, ctypes.byref(nbytes))
+        if rc == _lib.ERR_UNSUPPORTED:
+            return False
+        _lib.check(rc, "st_hash_build_workspace")
+        if self._build_ws is None or self._build_ws.numel() < nbytes.value or self._build_ws.device != self.device:
+            self._build_ws = torch.zeros((nbytes.value,), dtype=torch.uint8, device=self.device)
+        rc = lib.st_hash_build(_lib.ptr(keys), _lib.coord_code(keys.dtype), n, int(scale), _lib.ptr(self._keys),
+                               _lib.ptr(self._vals), self.capacity, 1 if fresh else 0, _lib.ptr(self._build_ws),
+                               self._build_ws.numel(), _lib.ptr(self._status()), _lib.stream_of(self.device))
+        if rc == _lib.ERR_UNSUPPORTED:
+            return False
+        _lib.check(rc, "st_hash_build")
+        return True
 
     def _status(self) -> torch.Tensor:
         if self.status is None or self.status.device != self.device:

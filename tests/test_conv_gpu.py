@@ -645,3 +645,29 @@ def test_fused_epilogue_without_sources(device):
               _lib.ptr(out), n_dst, K, Kd, Nd, 0, _lib.stream_of(dev))
     ref = torch.relu(bias * scale + shift + res)
     assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype,C", [(torch.float32, 64), (torch.bfloat16, 64), (torch.float16, 32),
+                                     (torch.bfloat16, 128), (torch.float32, 128)])
+def test_reverse_k_gather_equals_reversed_weights(device, dtype, C):
+    """The input gradient of a symmetric submanifold map over the forward's plan with the weights'
+    offsets reversed as the GEMM addresses them (ST_GATHER_REVERSE_K) equals the same gather over
+    an ST_W_REVERSE copy of the weights, bit for bit (ring kernels at 32 / 64 channels, the wide
+    kernel at 128 x 128 16-bit and 64 x 128 split fp32)."""
+    from sparsetriton_amd import _lib
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import gather_gemm_tiled, weight_prep
+    from sparsetriton_amd.nn.functional.conv.kmap import _target_offsets, subm_kernel_map
+    rng = np.random.default_rng(C + 3)
+    c = _rand_coords(rng, 6000, 24)
+    coords = torch.as_tensor(c, device=device)
+    km, _ = subm_kernel_map(coords, 2, (24, 24, 24), _target_offsets(3, 1, 1, False, device))
+    assert km.symmetric
+    cout = 64 if C == 128 and dtype == torch.float32 else C
+    dY = torch.randn((6000, cout), device=device).to(dtype)
+    W = (torch.randn((27, C, cout), device=device) / 40).to(dtype)
+    tiles = km.backward_tiles()
+    a = gather_gemm_tiled(dY, tiles, W, km.n_in, 27, reverse_k=True)
+    b = gather_gemm_tiled(dY, tiles, weight_prep(W, _lib.W_REVERSE), km.n_in, 27)
+    assert torch.equal(a, b)
+    ref = O.dgrad_f64(dY.float().cpu().numpy(), W.float().cpu().numpy(), km.neighbor_indices.cpu().numpy(), 6000)
+    assert rel(a.float().cpu().numpy(), ref) < TOL[dtype]

@@ -170,3 +170,63 @@ def test_group_probes_exact(device, group_probes):
     km = query_kernel_map(tab, torch.as_tensor(cs, device=device), offs, (24, 24, 24), 1, cs.shape[0])
     want = O.exact_kmap(cs, cs, O.target_offsets(3, 1, 1, False), 1, (24, 24, 24))
     assert np.array_equal(km.neighbor_indices.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("load", [0.5, 0.97])
+def test_partitioned_build_spills_and_second_insert(device, load):
+    """The partitioned build (st_hash_build) at a high load factor, where many probes run past
+    their segment and finish by global CAS, then a second insert into the filled table (rows that
+    repeat earlier keys and new ones): every key maps to its lowest row, repeats are counted, the
+    table holds each key once and stays a valid linear-probing table (every query answers)."""
+    rng = np.random.default_rng(int(load * 100))
+    n1, n2 = 40_000, 5_000
+    cap = int((n1 + n2) / load)
+    lin = rng.choice(2 * 256 ** 3, n1 + n2, replace=False)
+    c = np.stack([lin // 256 ** 3, (lin // 256 ** 2) % 256, (lin // 256) % 256, lin % 256], 1).astype(np.int32)
+    first = c[:n1]
+    # the second insert: 2,000 keys of the first, then n2 new keys
+    pick = rng.choice(n1, 2_000, replace=False)
+    second = np.concatenate([first[pick], c[n1:]])
+    t = HashTable(capacity=cap, device=device)
+    t.insert(torch.as_tensor(first, device=device))
+    t.insert(torch.as_tensor(second, device=device))
+    t.check()
+    assert t.counters()["duplicate"] == 2_000
+    got = t.query(torch.as_tensor(c, device=device)).cpu().numpy()
+    # a key's value: the lowest row it was inserted with (row indices of either insert, as the
+    # CAS insert keeps them: a repeat takes the minimum)
+    expect = np.concatenate([np.arange(n1), 2_000 + np.arange(n2)])
+    expect[pick] = np.minimum(expect[pick], np.arange(2_000))
+    assert (got == expect).all()
+    keys = t.table_keys.cpu().numpy()
+    assert (keys != -1).sum() == n1 + n2
+    assert np.unique(keys[keys != -1]).shape[0] == n1 + n2
+
+
+def test_partitioned_build_equals_cas_insert(device):
+    """st_hash_build and st_hash_insert (the CAS build) give the same key -> row mapping, status
+    counts included, on a set with repeated and unpackable coordinates."""
+    from sparsetriton_amd import _lib
+    rng = np.random.default_rng(21)
+    n = 100_000
+    lin = rng.choice(4 * 512 * 512 * 64, n, replace=False)
+    c = np.stack([lin // (512 * 512 * 64), (lin // (512 * 64)) % 512, (lin // 64) % 512, lin % 64], 1)
+    c = np.concatenate([c, c[rng.choice(n, 3_000, replace=False)], [[0, 40000, 1, 1], [-1, 0, 0, 0]]])
+    coords = torch.as_tensor(c.astype(np.int32), device=device)
+    built = HashTable(capacity=2 * c.shape[0], device=device)
+    built.insert(coords)
+    cas = HashTable(capacity=2 * c.shape[0], device=device)
+    prev = _lib.lib().st_hash_probe_mode(-1)
+    assert prev == 0
+    cas._materialize()
+    _lib.fill_(cas._keys, -1)
+    _lib.fill_(cas._vals, -1)
+    _lib.call("st_hash_insert", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0], 1,
+              _lib.ptr(cas._keys), _lib.ptr(cas._vals), cas.capacity, _lib.ptr(cas._status()),
+              _lib.stream_of(coords.device))
+    assert built.counters() == cas.counters()
+    assert torch.equal(built.query(coords), cas.query(coords))
+    kb, vb = built.table_keys.cpu().numpy(), built.table_values.cpu().numpy()
+    kc, vc = cas.table_keys.cpu().numpy(), cas.table_values.cpu().numpy()
+    ob, oc = np.argsort(kb), np.argsort(kc)
+    assert np.array_equal(kb[ob], kc[oc]) and np.array_equal(vb[ob], vc[oc])

@@ -18,6 +18,7 @@ from sparsetriton_amd.nn.functional import sparse_conv3d
 from sparsetriton_amd.nn.functional.conv.conv import _input_table, compute_neighbor_indices
 from sparsetriton_amd.nn.functional.conv.kmap import (
     _target_offsets,
+    brick_out_coords_and_map,
     build_out_coords,
     build_out_coords_and_map,
     query_kernel_map,
@@ -636,3 +637,30 @@ def test_gather_without_sources_writes_zeros(device):
         Bt = torch.randn((K, 64, 64), device=device).to(dt)
         for out in (gather_gemm_tiled(A, tiles, Bt, n_dst, K), gather_gemm(A, nbr, n_dst, 1, masks, Bt, n_dst, K)):
             assert out.shape == (n_dst, 64) and int(torch.count_nonzero(out)) == 0
+
+
+@pytest.mark.parametrize("spin", ["0", "1"])
+def test_index_level_without_published_totals(device, spin, monkeypatch):
+    """The one-launch index levels (counts + prefix) take the earlier tiles' totals as they are
+    published, and compute any still missing after ST_SUBM_SPIN polls from the index itself.  With
+    0 or 1 polls (nearly every total computed directly) the submanifold map, its masks and the
+    strided brick build equal those of the default run."""
+    from sparsetriton_amd.nn.functional.conv.kmap import subm_kernel_map
+    rng = np.random.default_rng(41)
+    B, shape, n = 4, (1440, 1440, 41), 60000
+    vol = B * shape[0] * shape[1] * shape[2]
+    lin = np.sort(rng.choice(vol, n, replace=False))
+    sx, sy, sz = shape
+    c = np.stack([lin // (sx * sy * sz), (lin // (sy * sz)) % sx, (lin // sz) % sy, lin % sz], 1).astype(np.int32)
+    coords = torch.as_tensor(c, dtype=torch.int16, device=device)
+    offs = _target_offsets(3, 1, 1, False, device)
+    km0, _ = subm_kernel_map(coords, B, shape, offs)
+    ref_strided = brick_out_coords_and_map(coords, B, shape, 3, 2, 1, 1, False)
+    monkeypatch.setenv("ST_SUBM_SPIN", spin)
+    km1, snap = subm_kernel_map(coords, B, shape, offs)
+    got_strided = brick_out_coords_and_map(coords, B, shape, 3, 2, 1, 1, False)
+    assert torch.equal(km0.nbr, km1.nbr) and torch.equal(km0.out_masks, km1.out_masks)
+    assert snap.counters() == {"overflow": 0, "bad_coord": 0, "duplicate": 0, "out_of_box": 0}
+    assert torch.equal(ref_strided[0], got_strided[0])
+    assert torch.equal(ref_strided[3].nbr, got_strided[3].nbr)
+    assert torch.equal(ref_strided[3].invnbr, got_strided[3].invnbr)
