@@ -122,10 +122,11 @@ def gather_gemm_dgrad(dY: torch.Tensor, kmap: KernelMap, W: torch.Tensor) -> tor
     For a symmetric (odd-kernel submanifold) map the transpose is the map read
     with offsets reversed: dX[i] = sum_j dY[nbr[j, i]] @ W[K-1-j]^T; the tiled GEMM
     takes the reversal as it addresses the weights (no reversed copy)."""
+    symmetric = kmap.symmetric  # (first: resolving it also finds repeated output rows, which the fold needs)
     dY = kmap.fold_output_rows(dY)
     if tiled_ok(dY.dtype, dY.shape[1]):
-        return gather_gemm_tiled(dY, kmap.backward_tiles(), W, kmap.n_in, kmap.K, reverse_k=kmap.symmetric)
-    if kmap.symmetric:
+        return gather_gemm_tiled(dY, kmap.backward_tiles(), W, kmap.n_in, kmap.K, reverse_k=symmetric)
+    if symmetric:
         W = weight_prep(W, _lib.W_REVERSE)
     plan = kmap.backward_plan()
     if kmap.symmetric:
