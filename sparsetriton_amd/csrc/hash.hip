@@ -36,9 +36,8 @@ __device__ __forceinline__ void store_row(uint32_t* __restrict__ vals, uint32_t 
 // one memory round trip less per row on a mostly empty table, a CAS on every
 // occupied slot it passes (config 2, table at the default capacity: clear +
 // insert 53.3 -> 50.4 us)
-__device__ __forceinline__ uint32_t insert_slot_cas(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
-                                                    bool& was_new) {
-  uint32_t s = home_slot(key, cap);
+__device__ __forceinline__ uint32_t insert_slot_cas_from(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
+                                                         uint32_t s, bool& was_new) {
   for (uint32_t step = 0; step < cap; ++step) {
     const unsigned long long old =
         atomicCAS((unsigned long long*)&keys[s], (unsigned long long)ST_EMPTY_KEY, (unsigned long long)key);
@@ -49,6 +48,10 @@ __device__ __forceinline__ uint32_t insert_slot_cas(uint64_t* __restrict__ keys,
     s = next_slot(s, cap);
   }
   return ST_NO_VAL;
+}
+__device__ __forceinline__ uint32_t insert_slot_cas(uint64_t* __restrict__ keys, uint32_t cap, uint64_t key,
+                                                    bool& was_new) {
+  return insert_slot_cas_from(keys, cap, key, home_slot(key, cap), was_new);
 }
 
 // One thread per coordinate row (utils/hash.py:203-258 restated with exact keys).
@@ -371,8 +374,9 @@ static unsigned group_blocks(int64_t rows) { return (unsigned)((rows * kGroup + 
 //   hash_bucket_kernel   a workgroup takes kBuildRows rows: their keys and
 //                        segments, counted and ranked per segment in LDS,
 //                        then written to the workgroup's own area grouped by
-//                        segment, with the per-(segment, workgroup) counts
-//                        and run offsets (segment-major).
+//                        segment (runs of ~kBuildRows / segments rows), with
+//                        each run's count and offset packed in one word per
+//                        (workgroup, segment), stored contiguously.
 //   hash_segment_kernel  a workgroup per segment: the segment's slots in LDS
 //                        (empty for a fresh table, else loaded), its rows
 //                        gathered from every bucketing workgroup's run and
@@ -380,45 +384,40 @@ static unsigned group_blocks(int64_t rows) { return (unsigned)((rows * kGroup + 
 //                        by LDS atomic-min (the lowest row of a repeated
 //                        key); rows whose probe runs past the segment's end
 //                        go to the spill list; the segment stored.
-//   hash_spill_kernel    one workgroup: the spilled rows inserted into the
-//                        finished table by global CAS from their home slots,
-//                        as the CAS build does (returns at once when there
-//                        are none), then the spill count reset.
+//   hash_spill_kernel    the spilled rows inserted into the finished table by
+//                        global CAS, as the CAS build does, each from the
+//                        slot after its segment (the slots from its home to
+//                        there hold other keys); returns at once when there
+//                        are none.  The next build's bucketing pass resets the
+//                        spill count.
 // Linear probing never deletes, so a key already in the table sits behind an
 // unbroken run of occupied slots from its home: the LDS probe of the same key
 // (a prefix of the global probe) meets no empty slot before the segment's
 // end, spills, and the global probe finds the key.  The table's key -> row
 // mapping is the CAS build's; slot positions may differ (they depend on the
 // insertion order in either build).
-constexpr int kBuildRows = 2048;      // rows per bucketing workgroup (8 per thread)
+constexpr int kBuildRows = 8192;      // rows per bucketing workgroup (32 per thread)
 constexpr int kBuildMaxSegs = 8192;   // the bucketing pass's LDS count table
-constexpr int kBuildMaxSlots = 2048;  // slots per segment (24 KB of LDS)
-constexpr int kBuildMaxWgs = 4096;    // bucketing workgroups a segment gathers from
+constexpr int kBuildSlots = 2048;     // slots per segment (24 KB of LDS)
+constexpr int kBuildMaxWgs = 2048;    // bucketing workgroups a segment gathers from
 
-// Slots per segment (1024 or 2048, leaving at most kBuildMaxSegs segments) and
-// the segment count; false for tables or row counts too large for the
-// partitioned build.
+// Segments of kBuildSlots slots (the last one partial) and their count; false
+// for tables or row counts too large for the partitioned build.
 inline bool build_geom(int64_t n, int64_t cap, int64_t* S, int64_t* nseg) {
   if ((n + kBuildRows - 1) / kBuildRows > kBuildMaxWgs) return false;
-  for (int64_t s = 1024; s <= kBuildMaxSlots; s *= 2) {
-    const int64_t ns = (cap + s - 1) / s;
-    if (ns <= kBuildMaxSegs) {
-      *S = s;
-      *nseg = ns;
-      return true;
-    }
-  }
-  return false;
+  *S = kBuildSlots;
+  *nseg = (cap + kBuildSlots - 1) / kBuildSlots;
+  return *nseg <= kBuildMaxSegs;
 }
 
 struct BuildWs {
   int32_t* spills;     // spilled rows (zero between builds)
-  int32_t* cnt;        // nseg x nwg rows of segment s bucketed by workgroup w (segment-major)
-  int32_t* off;        // nseg x nwg: where that run starts in w's area
+  uint32_t* runs;      // nwg x nseg: run of workgroup w's rows of segment s, count << 16 | offset
   uint64_t* bkeys;     // nwg x kBuildRows keys, grouped by segment per workgroup
   uint32_t* brows;     // the same for the rows
   uint64_t* skeys;     // n spilled keys
   uint32_t* srows;     // n spilled rows
+  uint32_t* sfrom;     // n spilled rows' first slot to probe
   int nwg;
 };
 
@@ -428,8 +427,8 @@ inline int64_t build_nwg(int64_t n) { return n > 0 ? (n + kBuildRows - 1) / kBui
 
 inline int64_t build_ws_bytes(int64_t n, int64_t nseg) {
   const int64_t nwg = build_nwg(n), rows = nwg * kBuildRows, nn = n > 0 ? n : 1;
-  return build_align(4) + 2 * build_align(4 * nseg * nwg) + build_align(8 * rows) + build_align(4 * rows) +
-         build_align(8 * nn) + build_align(4 * nn);
+  return build_align(4) + build_align(4 * nseg * nwg) + build_align(8 * rows) + build_align(4 * rows) +
+         build_align(8 * nn) + 2 * build_align(4 * nn);
 }
 
 inline BuildWs build_ws(void* ws, int64_t n, int64_t nseg) {
@@ -439,9 +438,7 @@ inline BuildWs build_ws(void* ws, int64_t n, int64_t nseg) {
   w.nwg = (int)nwg;
   w.spills = (int32_t*)p;
   p += build_align(4);
-  w.cnt = (int32_t*)p;
-  p += build_align(4 * nseg * nwg);
-  w.off = (int32_t*)p;
+  w.runs = (uint32_t*)p;
   p += build_align(4 * nseg * nwg);
   w.bkeys = (uint64_t*)p;
   p += build_align(8 * rows);
@@ -450,33 +447,44 @@ inline BuildWs build_ws(void* ws, int64_t n, int64_t nseg) {
   w.skeys = (uint64_t*)p;
   p += build_align(8 * nn);
   w.srows = (uint32_t*)p;
+  p += build_align(4 * nn);
+  w.sfrom = (uint32_t*)p;
   return w;
 }
 
+constexpr int kBucketThreads = 1024;
 template <typename CT>
-__global__ __launch_bounds__(256) void hash_bucket_kernel(const CT* __restrict__ coords, int64_t n, int64_t scale,
-                                                          uint32_t cap, uint32_t S, int nseg, BuildWs w,
-                                                          int32_t* __restrict__ status) {
-  constexpr int J = kBuildRows / 256;
+__global__ __launch_bounds__(kBucketThreads) void hash_bucket_kernel(const CT* __restrict__ coords, int64_t n,
+                                                                     int64_t scale, uint32_t cap, uint32_t S, int nseg,
+                                                                     BuildWs w, int32_t* __restrict__ status) {
+  constexpr int J = kBuildRows / kBucketThreads;
   __shared__ int cnt_s[kBuildMaxSegs];
-  __shared__ int scan_s[8];
+  __shared__ int scan_s[17];
   const int tid = threadIdx.x;
-  for (int e = tid; e < nseg; e += 256) cnt_s[e] = 0;
-  __syncthreads();
+  if (blockIdx.x == 0 && tid == 0) *w.spills = 0;  // (read by the previous build's spill pass, which is done)
+  for (int e = tid; e < nseg; e += kBucketThreads) cnt_s[e] = 0;
   const int64_t base = (int64_t)blockIdx.x * kBuildRows;
+  // every row's coordinates in flight before the first LDS atomic
+  int64_t cb[J], cx[J], cy[J], cz[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int64_t i = base + j * kBucketThreads + tid;
+    cb[j] = -1;
+    cx[j] = cy[j] = cz[j] = 0;
+    if (i < n) load_coord(coords, i, cb[j], cx[j], cy[j], cz[j]);
+  }
+  __syncthreads();
   uint64_t key[J];
   int seg[J], rank[J];
   int bad = 0;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int64_t i = base + j * 256 + tid;
+    const int64_t i = base + j * kBucketThreads + tid;
     seg[j] = -1;
     key[j] = 0;
     rank[j] = 0;
     if (i < n) {
-      int64_t b, x, y, z;
-      load_coord(coords, i, b, x, y, z);
-      if (pack_key(b, x * scale, y * scale, z * scale, key[j])) {
+      if (pack_key(cb[j], cx[j] * scale, cy[j] * scale, cz[j] * scale, key[j])) {
         seg[j] = (int)(home_slot(key[j], cap) / S);
         rank[j] = atomicAdd(&cnt_s[seg[j]], 1);
       } else {
@@ -488,19 +496,21 @@ __global__ __launch_bounds__(256) void hash_bucket_kernel(const CT* __restrict__
   if ((tid & 63) == 0 && bad) atomicAdd(&status[ST_STATUS_BAD_COORD], bad);
   __syncthreads();
   // the counts -> run offsets in the workgroup's area (exclusive scan over the segments, each
-  // thread a contiguous range of them), both published segment-major
-  const int per = (nseg + 255) / 256, e0 = tid * per, e1 = min(nseg, e0 + per);
+  // thread a contiguous range of them), published with the counts in one word per segment
+  const int per = (nseg + kBucketThreads - 1) / kBucketThreads, e0 = tid * per, e1 = min(nseg, e0 + per);
   int sum = 0;
   for (int e = e0; e < e1; ++e) sum += cnt_s[e];
   int total;
   int run = block_exclusive_scan(sum, scan_s, &total);
   for (int e = e0; e < e1; ++e) {
     const int c = cnt_s[e];
-    w.cnt[(int64_t)e * w.nwg + blockIdx.x] = c;
-    w.off[(int64_t)e * w.nwg + blockIdx.x] = run;
-    cnt_s[e] = run;
+    cnt_s[e] = run | (c << 16);
     run += c;
   }
+  __syncthreads();
+  uint32_t* runs = w.runs + (int64_t)blockIdx.x * nseg;
+  for (int e = tid; e < nseg; e += kBucketThreads) runs[e] = (uint32_t)cnt_s[e];
+  for (int e = tid; e < nseg; e += kBucketThreads) cnt_s[e] &= 0xFFFF;
   __syncthreads();
   const int64_t area = base;  // the workgroup's kBuildRows places
 #pragma unroll
@@ -508,15 +518,15 @@ __global__ __launch_bounds__(256) void hash_bucket_kernel(const CT* __restrict__
     if (seg[j] < 0) continue;
     const int64_t at = area + cnt_s[seg[j]] + rank[j];
     w.bkeys[at] = key[j];
-    w.brows[at] = (uint32_t)(base + j * 256 + tid);
+    w.brows[at] = (uint32_t)(base + j * kBucketThreads + tid);
   }
 }
 
 __global__ __launch_bounds__(256) void hash_segment_kernel(uint64_t* __restrict__ keys, uint32_t* __restrict__ vals,
                                                            uint32_t cap, uint32_t S, int fresh, BuildWs w,
                                                            int32_t* __restrict__ status) {
-  __shared__ unsigned long long k_s[kBuildMaxSlots];
-  __shared__ uint32_t v_s[kBuildMaxSlots];
+  __shared__ unsigned long long k_s[kBuildSlots];
+  __shared__ uint32_t v_s[kBuildSlots];
   __shared__ int rs_s[kBuildMaxWgs + 1];  // where workgroup w's run starts among the segment's rows
   __shared__ int ro_s[kBuildMaxWgs];      // that run's offset in w's area
   __shared__ int scan_s[8];
@@ -532,8 +542,9 @@ __global__ __launch_bounds__(256) void hash_segment_kernel(uint64_t* __restrict_
   const int per = (nwg + 255) / 256, q0 = tid * per, q1 = min(nwg, q0 + per);
   int sum = 0;
   for (int q = q0; q < q1; ++q) {
-    const int c = w.cnt[(int64_t)seg * nwg + q];
-    ro_s[q] = w.off[(int64_t)seg * nwg + q];
+    const uint32_t v = w.runs[(int64_t)q * gridDim.x + seg];
+    const int c = (int)(v >> 16);
+    ro_s[q] = (int)(v & 0xFFFFu);
     rs_s[q] = c;
     sum += c;
   }
@@ -547,33 +558,55 @@ __global__ __launch_bounds__(256) void hash_segment_kernel(uint64_t* __restrict_
   if (tid == 0) rs_s[nwg] = total;
   __syncthreads();
   int dup = 0;
-  for (int r = tid; r < total; r += 256) {
-    // the run holding row r: the last workgroup whose run starts at or before r
-    int lo = 0, hi = nwg - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (rs_s[mid] <= r)
-        lo = mid;
-      else
-        hi = mid - 1;
-    }
-    const int64_t at = (int64_t)lo * kBuildRows + ro_s[lo] + (r - rs_s[lo]);
-    const uint64_t key = w.bkeys[at];
-    const uint32_t row = w.brows[at];
-    bool placed = false;
-    for (uint32_t s = home_slot(key, cap) - s0; s < len; ++s) {
-      const unsigned long long old = atomicCAS(&k_s[s], (unsigned long long)ST_EMPTY_KEY, (unsigned long long)key);
-      if (old == ST_EMPTY_KEY || old == key) {
-        atomicMin(&v_s[s], row);
-        dup += old == key ? 1 : 0;
-        placed = true;
-        break;
+  // kSegBatch rows a thread at a time: their places found in LDS, then all their loads in
+  // flight together, then the inserts
+  constexpr int kSegBatch = 8;
+  for (int r0 = 0; r0 < total; r0 += 256 * kSegBatch) {
+    uint64_t key[kSegBatch];
+    uint32_t row[kSegBatch];
+    int64_t at[kSegBatch];
+#pragma unroll
+    for (int u = 0; u < kSegBatch; ++u) {
+      const int r = r0 + u * 256 + tid;
+      at[u] = -1;
+      if (r < total) {
+        // the run holding row r: the last workgroup whose run starts at or before r
+        int lo = 0, hi = nwg - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (rs_s[mid] <= r)
+            lo = mid;
+          else
+            hi = mid - 1;
+        }
+        at[u] = (int64_t)lo * kBuildRows + ro_s[lo] + (r - rs_s[lo]);
       }
     }
-    if (!placed) {
-      const int q = atomicAdd(w.spills, 1);
-      w.skeys[q] = key;
-      w.srows[q] = row;
+#pragma unroll
+    for (int u = 0; u < kSegBatch; ++u) {
+      key[u] = at[u] >= 0 ? w.bkeys[at[u]] : 0ull;
+      row[u] = at[u] >= 0 ? w.brows[at[u]] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kSegBatch; ++u) {
+      if (at[u] < 0) continue;
+      bool placed = false;
+      for (uint32_t s = home_slot(key[u], cap) - s0; s < len; ++s) {
+        const unsigned long long old =
+            atomicCAS(&k_s[s], (unsigned long long)ST_EMPTY_KEY, (unsigned long long)key[u]);
+        if (old == ST_EMPTY_KEY || old == key[u]) {
+          atomicMin(&v_s[s], row[u]);
+          dup += old == key[u] ? 1 : 0;
+          placed = true;
+          break;
+        }
+      }
+      if (!placed) {
+        const int q = atomicAdd(w.spills, 1);
+        w.skeys[q] = key[u];
+        w.srows[q] = row[u];
+        w.sfrom[q] = s0 + len == cap ? 0u : s0 + len;
+      }
     }
   }
   dup = wave_sum(dup);
@@ -585,16 +618,17 @@ __global__ __launch_bounds__(256) void hash_segment_kernel(uint64_t* __restrict_
   }
 }
 
-__global__ __launch_bounds__(1024) void hash_spill_kernel(uint64_t* __restrict__ keys, uint32_t* __restrict__ vals,
-                                                          uint32_t cap, BuildWs w, int32_t* __restrict__ status) {
+constexpr int kSpillGrid = 64;  // workgroups of the spill pass (a thread per spilled row, strided)
+__global__ __launch_bounds__(256) void hash_spill_kernel(uint64_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                                                         uint32_t cap, BuildWs w, int32_t* __restrict__ status) {
   const int ns = *w.spills;
   if (ns == 0) return;
   int sdup = 0, over = 0;
-  for (int q = threadIdx.x; q < ns; q += blockDim.x) {
+  for (int q = blockIdx.x * 256 + threadIdx.x; q < ns; q += gridDim.x * 256) {
     const uint64_t key = w.skeys[q];
     const uint32_t row = w.srows[q];
     bool was_new = false;
-    const uint32_t s = insert_slot_cas(keys, cap, key, was_new);
+    const uint32_t s = insert_slot_cas_from(keys, cap, key, w.sfrom[q], was_new);
     if (s == ST_NO_VAL) {
       ++over;
       continue;
@@ -608,8 +642,6 @@ __global__ __launch_bounds__(1024) void hash_spill_kernel(uint64_t* __restrict__
     if (sdup) atomicAdd(&status[ST_STATUS_DUPLICATE], sdup);
     if (over) atomicAdd(&status[ST_STATUS_OVERFLOW], over);
   }
-  __syncthreads();  // every thread has read the count
-  if (threadIdx.x == 0) *w.spills = 0;
 }
 
 }  // namespace st
@@ -640,14 +672,14 @@ int st_hash_build(const void* coords, int coord_dtype, int64_t n, int64_t scale,
   BuildWs w = build_ws(workspace, n, nseg);
   if (n > 0) {
     ST_DISPATCH_COORD(coord_dtype, CT,
-                      hash_bucket_kernel<CT><<<(unsigned)w.nwg, 256, 0, stream>>>(
+                      hash_bucket_kernel<CT><<<(unsigned)w.nwg, kBucketThreads, 0, stream>>>(
                           (const CT*)coords, n, scale, (uint32_t)capacity, (uint32_t)S, (int)nseg, w, status));
   } else {
     w.nwg = 0;  // a fresh empty table: every segment stored empty
   }
   hash_segment_kernel<<<(unsigned)nseg, 256, 0, stream>>>(keys, vals, (uint32_t)capacity, (uint32_t)S,
                                                            fresh ? 1 : 0, w, status);
-  if (n > 0) hash_spill_kernel<<<1, 1024, 0, stream>>>(keys, vals, (uint32_t)capacity, w, status);
+  if (n > 0) hash_spill_kernel<<<kSpillGrid, 256, 0, stream>>>(keys, vals, (uint32_t)capacity, w, status);
   ST_CHECK_LAUNCH();
   return ST_OK;
 }
