@@ -422,12 +422,16 @@ def measure_extra(name, steps, warmup, profile=False, fp32_precision="bf16x3", c
     Wd = W.detach()
     wt = weight_prep(Wd.contiguous(), _lib.W_TRANSPOSE)
     if algo == "hashfly":
-        from sparsetriton_amd.nn.functional.conv.funcs.implicit_hashfly_gemm import subm_fly_gemm
+        from sparsetriton_amd.nn.functional.conv.funcs.implicit_hashfly_gemm import fly_tile_order, subm_fly_gemm
         from sparsetriton_amd.nn.functional.conv.kmap import _offsets_i32, _target_offsets
 
         index = next(v for key, v in sp._cache.kmaps.items() if key[0] == "brick_index")
         offs = _offsets_i32(_target_offsets(k, 1, p, False, dev))
-        kern = {"gather_fly_fwd": _events_batch(torch, lambda: subm_fly_gemm(X, index, offs, wt), KR)}
+        order = fly_tile_order(index, offs, (k, 1, p))  # the step's cached order
+        Wc = Wd.contiguous()
+        kern = {"gather_fly_fwd": _events_batch(torch, lambda: subm_fly_gemm(X, index, offs, wt, order), KR),
+                "gather_fly_dgrad": _events_batch(
+                    torch, lambda: subm_fly_gemm(dY, index, offs, Wc, order, reverse_k=True), KR)}
         set_conv_algo(ConvAlgo.PrecomputedNeighborGEMM)  # an exact map of the same geometry: P and wgrad
         _, sp2 = fresh()
         sparse_conv3d(sp2, W, k, stride=s, padding=p, transposed=tr, submanifold=subm)

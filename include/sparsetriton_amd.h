@@ -184,6 +184,8 @@ int st_kmap_query(const void* out_coords, int coord_dtype, int64_t n_out, const 
  * st_kmap_subm = st_subm_index (the index alone, with the status counts) +
  * st_kmap_subm_query (the map from a built index; the index stays valid
  * while `workspace` and the coordinates are unchanged, for any offsets).
+ * st_kmap_subm_query with nbr = NULL writes row_masks only (then required):
+ * the input of st_kmap_sort_rows for a tile order of st_subm_fly_gemm.
  */
 int st_kmap_subm_workspace(int64_t n, int64_t batches, int64_t sx, int64_t sy, int64_t sz, int64_t* bytes);
 int st_kmap_subm(const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K, int64_t batches,
@@ -612,16 +614,22 @@ typedef struct st_lookup {
  * coordinates, stride 1, bounds = the index box), with the neighbours found
  * inside the GEMM in the coordinates' brick index (st_subm_index, same
  * geometry) instead of a hash table: no kernel map is stored.  Per 128-row
- * tile (rows in their given order) each row looks up its K neighbours
+ * tile (rows 128t .. 128t + 127 of `rows`, a permutation of 0 .. n-1, or of
+ * 0 .. n-1 itself when rows is NULL) each row looks up its K neighbours
  * (coords[r].xyz - offsets[k]; the lowest row of a repeated coordinate, as
  * the table holds), the tile's offset list is the union of its rows', and
  * out[r] = sum_k A[nbr(k, r)] Bt[k]^T (+ bias), Bt as st_gather_gemm's.
- * The input gradient of a submanifold map that is its own transpose (status
- * DUPLICATE and OUT_OF_BOX zero, offsets symmetric) is the same call with the
- * weights of st_weight_prep(ST_W_REVERSE).  Bitwise equal to st_hashfly_gemm
- * and st_gather_gemm_tiled on the same rows.  st_subm_fly_ok(n, Kd, Nd, K,
- * dtype) = 1 for the shapes built: Kd, Nd in {64, 128} (split fp32 not at
- * 128 x 128), K <= 27, dtype ST_BF16, ST_F16 or ST_F32_BF16X3, and n rows
+ * With rows = the st_kmap_sort_rows order of the offset masks
+ * (st_kmap_subm_query with nbr = NULL) a tile's rows share their offsets, so
+ * it loads fewer weight slices and runs fewer MFMAs; the sums do not change.
+ * flags: 0 or ST_GATHER_REVERSE_K (offset k takes Bt[K - 1 - k]): the input
+ * gradient of a submanifold map that is its own transpose (status DUPLICATE
+ * and OUT_OF_BOX zero, offsets symmetric) takes the weights as given
+ * (W (K, C_in, C_out) is then Bt) with no ST_W_REVERSE copy.  Bitwise
+ * equal to st_hashfly_gemm and st_gather_gemm_tiled on the same rows.
+ * st_subm_fly_ok(n, Kd, Nd, K, dtype) = 1 for the shapes built: Kd, Nd in
+ * {64, 128} (split fp32 not at 128 x 128), K <= 27, dtype ST_BF16, ST_F16
+ * or ST_F32_BF16X3, and n rows
  * of Kd elements under 2^31 - 64 bytes (the kernel addresses its operands
  * with 32-bit buffer offsets); others (and int64 coordinates) return
  * ST_ERR_UNSUPPORTED.  Host arithmetic only: it touches no device.
@@ -629,7 +637,8 @@ typedef struct st_lookup {
 int st_subm_fly_ok(int64_t n, int Kd, int Nd, int K, int dtype);
 int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
                      int64_t batches, int64_t sx, int64_t sy, int64_t sz, const void* index, int64_t index_bytes,
-                     const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype, st_stream_t stream);
+                     const int32_t* rows, const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype,
+                     int flags, st_stream_t stream);
 
 /*
  * Forward / input-gradient of ConvHashOnTheFlyImplicitGEMM

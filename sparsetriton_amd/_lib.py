@@ -73,7 +73,7 @@ _SIGNATURES = {
     "st_subm_index": [_P, _I, _L, _L, _L, _L, _L, _P, _L, _P, _P],
     "st_kmap_subm_query": [_P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _L, _P, _P, _P],
     "st_subm_fly_ok": [_L, _I, _I, _I, _I],
-    "st_subm_fly_gemm": [_P, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _L, _P, _P, _P, _I, _I, _I, _P],
+    "st_subm_fly_gemm": [_P, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "st_outcoords_sizes": [_L, ctypes.POINTER(OutGeom), _L, _L, ctypes.POINTER(_L), ctypes.POINTER(_L)],
     "st_outcoords_plan": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _L, _P, _L, _P, _P],
     "st_outcoords_emit": [_P, _I, _L, _P, ctypes.POINTER(OutGeom), _P, _P, _P, _L, _P, _L, _P, _P, _L, _P, _L,

@@ -23,8 +23,8 @@ int ops_wgrad_pairs_x3(const float* X, int64_t n_in, const float* dY, int64_t n_
                        int64_t max_chunks, int Cin, int Cout, float* partials, void* dW, int dw_dtype,
                        hipStream_t stream);
 int ops_gather_fly_x3(const float* A, int64_t n, const void* coords, int coord_dtype, const int32_t* offsets, int K,
-                      const SubmIndex& ix, const float* Bt, float* out, const float* bias, int Kd, int Nd,
-                      hipStream_t stream);
+                      const SubmIndex& ix, const int32_t* rows, int rev, const float* Bt, float* out,
+                      const float* bias, int Kd, int Nd, hipStream_t stream);
 }  // namespace st
 
 using namespace st;
@@ -364,9 +364,12 @@ int st_subm_fly_ok(int64_t n, int Kd, int Nd, int K, int dtype) {
 
 int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t n, const int32_t* offsets, int K,
                      int64_t batches, int64_t sx, int64_t sy, int64_t sz, const void* index, int64_t index_bytes,
-                     const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype, st_stream_t stream) {
+                     const int32_t* rows, const void* Bt, const void* bias, void* out, int Kd, int Nd, int dtype,
+                     int flags, st_stream_t stream) {
   const int64_t need = subm_workspace_bytes(n, batches, sx, sy, sz);
   if (need < 0 || index_bytes < need || K <= 0 || Kd <= 0 || Nd <= 0) return ST_ERR_ARG;
+  if (flags & ~ST_GATHER_REVERSE_K) return ST_ERR_ARG;
+  const int rev = (flags & ST_GATHER_REVERSE_K) ? 1 : 0;
   if (!st_subm_fly_ok(n, Kd, Nd, K, dtype)) return ST_ERR_UNSUPPORTED;
   if (n == 0) return ST_OK;
   if (!A || !coords || !offsets || !index || !Bt || !out) return ST_ERR_ARG;
@@ -374,13 +377,13 @@ int st_subm_fly_gemm(const void* A, const void* coords, int coord_dtype, int64_t
   subm_view(const_cast<void*>(index), n, batches, sx, sy, sz, &ix);
   switch (dtype) {
     case ST_F32_BF16X3:
-      return ops_gather_fly_x3((const float*)A, n, coords, coord_dtype, offsets, K, ix, (const float*)Bt, (float*)out,
-                               (const float*)bias, Kd, Nd, stream);
+      return ops_gather_fly_x3((const float*)A, n, coords, coord_dtype, offsets, K, ix, rows, rev, (const float*)Bt,
+                               (float*)out, (const float*)bias, Kd, Nd, stream);
     case ST_BF16:
-      return ops_gather_fly<__bf16>((const __bf16*)A, n, coords, coord_dtype, offsets, K, ix, (const __bf16*)Bt,
-                                    (__bf16*)out, (const __bf16*)bias, Kd, Nd, stream);
+      return ops_gather_fly<__bf16>((const __bf16*)A, n, coords, coord_dtype, offsets, K, ix, rows, rev,
+                                    (const __bf16*)Bt, (__bf16*)out, (const __bf16*)bias, Kd, Nd, stream);
     case ST_F16:
-      return ops_gather_fly<_Float16>((const _Float16*)A, n, coords, coord_dtype, offsets, K, ix,
+      return ops_gather_fly<_Float16>((const _Float16*)A, n, coords, coord_dtype, offsets, K, ix, rows, rev,
                                       (const _Float16*)Bt, (_Float16*)out, (const _Float16*)bias, Kd, Nd, stream);
     default:
       return ST_ERR_UNSUPPORTED;

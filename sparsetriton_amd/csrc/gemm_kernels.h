@@ -1775,17 +1775,18 @@ int ops_gather_hash(const T* A, int64_t n_src, const void* coords, int coord_dty
 // wide kernel (16-bit types; ST_ERR_UNSUPPORTED for shapes fly_ok rejects).
 template <typename T>
 int ops_gather_fly(const T* A, int64_t n, const void* coords, int coord_dtype, const int32_t* offsets, int K,
-                   const SubmIndex& ix, const T* Bt, T* out, const T* bias, int Kd, int Nd, hipStream_t stream) {
+                   const SubmIndex& ix, const int32_t* rows, int rev, const T* Bt, T* out, const T* bias, int Kd,
+                   int Nd, hipStream_t stream) {
   if constexpr (sizeof(T) != 2) {
     return ST_ERR_UNSUPPORTED;
   } else {
     if (!fly_ok(Kd, Nd, K, sizeof(T), false, n, A, Bt)) return ST_ERR_UNSUPPORTED;
     const BiasEpi<T> epi{bias};
     if (coord_dtype == ST_COORD_I16)
-      launch_wide<T, false>(A, n, FlySrc<int16_t>{(const int16_t*)coords, offsets, ix, K}, nullptr, Bt, out, epi, n,
+      launch_wide<T, false>(A, n, FlySrc<int16_t>{(const int16_t*)coords, offsets, ix, K, rows, rev}, nullptr, Bt, out, epi, n,
                             Kd, Nd, stream);
     else if (coord_dtype == ST_COORD_I32)
-      launch_wide<T, false>(A, n, FlySrc<int32_t>{(const int32_t*)coords, offsets, ix, K}, nullptr, Bt, out, epi, n,
+      launch_wide<T, false>(A, n, FlySrc<int32_t>{(const int32_t*)coords, offsets, ix, K, rows, rev}, nullptr, Bt, out, epi, n,
                             Kd, Nd, stream);
     else
       return ST_ERR_UNSUPPORTED;
@@ -1845,7 +1846,7 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
                                     hipStream_t);                                                                    \
   X template int ops_weight_prep<T>(const T*, T*, int, int, int, int, hipStream_t);                                  \
   X template int ops_gather_fly<T>(const T*, int64_t, const void*, int, const int32_t*, int, const SubmIndex&,       \
-                                   const T*, T*, const T*, int, int, hipStream_t);                                  \
+                                   const int32_t*, int, const T*, T*, const T*, int, int, hipStream_t);             \
   X template int ops_gather_tiled<T>(const T*, int64_t, const int32_t*, const int32_t*, const int16_t*,              \
                                      const int32_t*, const T*, T*, Epi<T>, int64_t, int, int, int, hipStream_t,    \
                                      int);                                                                         \

@@ -22,8 +22,8 @@
 // order of mfma_x3), exactly as the ring kernels do, so the two agree bitwise.
 // The tile's source rows (nk x 128) are copied to LDS first, so nk <= kWideMaxK.
 //
-// With a FlySrc (submanifold, no kernel map) the tile is 128 consecutive rows
-// and the prologue finds the sources itself: each thread looks its row's K
+// With a FlySrc (submanifold, no kernel map) the tile is 128 rows of the given
+// order (consecutive rows without one) and the prologue finds the sources itself: each thread looks its row's K
 // neighbours up in the coordinates' brick index (subm_index.h), the tile's
 // offset list is the union of its rows' (offsets no row of the tile has are
 // never loaded), and the main loop is the same.  A row with a neighbour
@@ -42,14 +42,20 @@ namespace st {
 constexpr int kWideMaxK = 27;  // offsets whose sources a wide workgroup holds (a 3x3x3 kernel)
 
 // Neighbours of destination row r looked up in a brick index (source rows are
-// the same coordinate set's rows: out = in, stride 1).
+// the same coordinate set's rows: out = in, stride 1).  rows (optional): the
+// destination rows in tile order, a permutation of 0 .. n-1 (e.g. sorted by
+// offset mask, so a tile's rows share their offsets); null = 0 .. n-1.
+// rev: offset k's B slice is Bt[K - 1 - k].
 template <typename CT>
 struct FlySrc {
   static constexpr bool kTiled = false;
+  static constexpr bool kRev = true;
   const CT* __restrict__ coords;
   const int32_t* __restrict__ offsets;  // K x 3
   SubmIndex ix;
   int K;
+  const int32_t* __restrict__ rows;
+  int rev;
 };
 
 // ST_GATHER_WIDE=0 keeps the four-wave kernels everywhere, =2 takes the wide one
@@ -146,11 +152,13 @@ __global__ __launch_bounds__(128 * TP) void gather_gemm_wide_kernel(const T* __r
     for (int j = tid; j < 3 * K; j += NT) off_s[j] = src.offsets[j];
     __syncthreads();
     const int64_t gr = th * kGemmBM + r;
-    drow_s[ht][r] = (tvalid && gr < n_dst) ? (int32_t)gr : -1;
+    const bool live = tvalid && gr < n_dst;
+    const int32_t d = live ? (src.rows ? src.rows[gr] : (int32_t)gr) : -1;
+    drow_s[ht][r] = d;
     uint32_t m = 0u;
-    if (tvalid && gr < n_dst) {
+    if (live) {
       int64_t b, x, y, z;
-      load_coord(src.coords, gr, b, x, y, z);
+      load_coord(src.coords, d, b, x, y, z);
       subm_neighbours(src.ix, b, x, y, z, off_s, K, subm_unit_offsets(off_s, K), [&](int k, int32_t v) {
         v = (int64_t)v >= n_src ? -1 : v;
         src_s[ht][k][r] = v;

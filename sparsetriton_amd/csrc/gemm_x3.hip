@@ -31,15 +31,15 @@ int ops_gather_tiled_x3(const float* A, int64_t n_src, const int32_t* perm, cons
 }
 
 int ops_gather_fly_x3(const float* A, int64_t n, const void* coords, int coord_dtype, const int32_t* offsets, int K,
-                      const SubmIndex& ix, const float* Bt, float* out, const float* bias, int Kd, int Nd,
-                      hipStream_t stream) {
+                      const SubmIndex& ix, const int32_t* rows, int rev, const float* Bt, float* out,
+                      const float* bias, int Kd, int Nd, hipStream_t stream) {
   if (!fly_ok(Kd, Nd, K, sizeof(float), true, n, A, Bt)) return ST_ERR_UNSUPPORTED;
   const BiasEpi<float> epi{bias};
   if (coord_dtype == ST_COORD_I16)
-    launch_wide<float, true>(A, n, FlySrc<int16_t>{(const int16_t*)coords, offsets, ix, K}, nullptr, Bt, out, epi, n,
+    launch_wide<float, true>(A, n, FlySrc<int16_t>{(const int16_t*)coords, offsets, ix, K, rows, rev}, nullptr, Bt, out, epi, n,
                              Kd, Nd, stream);
   else if (coord_dtype == ST_COORD_I32)
-    launch_wide<float, true>(A, n, FlySrc<int32_t>{(const int32_t*)coords, offsets, ix, K}, nullptr, Bt, out, epi, n,
+    launch_wide<float, true>(A, n, FlySrc<int32_t>{(const int32_t*)coords, offsets, ix, K, rows, rev}, nullptr, Bt, out, epi, n,
                              Kd, Nd, stream);
   else
     return ST_ERR_UNSUPPORTED;

@@ -341,8 +341,8 @@ struct QueryLds {
 static_assert(sizeof(QueryLds<>) >= sizeof(int32_t) * ST_MAX_KVOL * 3, "offsets fit the query's LDS");
 
 // nbr[k * n + o] = row of coords[o] - t_k (in the box, present), -1 otherwise,
-// and the row's mask words.
-template <typename CT>
+// and the row's mask words (NBR = false: the mask words only).
+template <typename CT, bool NBR>
 __global__ __launch_bounds__(kSubmThreads) void subm_query_kernel(const CT* __restrict__ coords, int64_t n,
                                                                   const int32_t* __restrict__ offsets, int K,
                                                                   SubmIndex ix, int32_t* __restrict__ nbr,
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kSubmThreads) void subm_query_kernel(const CT* __re
   const int W = (K + 31) >> 5;
   uint32_t mword = 0;
   auto emit = [&](int k, int32_t v) {
-    nbr[(int64_t)k * n + o] = v;
+    if constexpr (NBR) nbr[(int64_t)k * n + o] = v;
     if (v >= 0) mword |= 1u << (k & 31);
     if ((k & 31) == 31 || k == K - 1) {
       if (row_masks) row_masks[o * W + (k >> 5)] = mword;
@@ -898,12 +898,17 @@ int st_kmap_subm_query(const void* coords, int coord_dtype, int64_t n, const int
   if (need < 0 || workspace_bytes < need || K <= 0 || K > ST_MAX_KVOL) return ST_ERR_ARG;
   if (coord_dtype < ST_COORD_I16 || coord_dtype > ST_COORD_I64) return ST_ERR_UNSUPPORTED;
   if (n == 0) return ST_OK;
-  if (!coords || !offsets || !workspace || !nbr) return ST_ERR_ARG;
+  if (!coords || !offsets || !workspace || (!nbr && !row_masks)) return ST_ERR_ARG;
   SubmIndex ix;
   subm_view(const_cast<void*>(workspace), n, batches, sx, sy, sz, &ix);
+  const unsigned grid = st_blocks(n, kSubmThreads);
   ST_DISPATCH_COORD(coord_dtype, CT, {
-    subm_query_kernel<CT><<<st_blocks(n, kSubmThreads), kSubmThreads, 0, stream>>>((const CT*)coords, n, offsets, K,
-                                                                                 ix, nbr, row_masks);
+    if (nbr)
+      subm_query_kernel<CT, true><<<grid, kSubmThreads, 0, stream>>>((const CT*)coords, n, offsets, K, ix, nbr,
+                                                                     row_masks);
+    else
+      subm_query_kernel<CT, false><<<grid, kSubmThreads, 0, stream>>>((const CT*)coords, n, offsets, K, ix, nullptr,
+                                                                      row_masks);
   });
   ST_CHECK_LAUNCH();
   return ST_OK;

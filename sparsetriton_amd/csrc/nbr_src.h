@@ -24,6 +24,7 @@ namespace st {
 struct MapSrc {
   static constexpr bool kTiled = false;
   static constexpr bool kProbe = false;
+  static constexpr bool kRev = false;
   const int32_t* __restrict__ map;
   int64_t ks, rs;
   typedef int64_t RowCtx;
@@ -39,6 +40,7 @@ constexpr int kTileRows = 128;
 struct TiledSrc {
   static constexpr bool kTiled = true;
   static constexpr bool kProbe = false;
+  static constexpr bool kRev = true;
   const int32_t* __restrict__ nk;
   const int16_t* __restrict__ klist;
   const int32_t* __restrict__ tmap;
@@ -53,10 +55,11 @@ struct TiledSrc {
   }
 };
 
-// Index of the B slice that multiplies the sources of offset k.
+// Index of the B slice that multiplies the sources of offset k (sources with a
+// rev member: Bt[K - 1 - k] when it is set).
 template <typename Src>
 __device__ __forceinline__ int b_slice(const Src& src, int k) {
-  if constexpr (Src::kTiled)
+  if constexpr (Src::kRev)
     return src.rev ? src.K - 1 - k : k;
   else
     return k;
@@ -65,6 +68,7 @@ __device__ __forceinline__ int b_slice(const Src& src, int k) {
 template <typename CT>
 struct HashSrc {
   static constexpr bool kTiled = false;
+  static constexpr bool kRev = false;
   static constexpr bool kProbe = true;  // get() is a table probe: callers batch prep / home-slot loads / finish
   const CT* __restrict__ coords;
   const int32_t* __restrict__ offsets;

@@ -26,7 +26,8 @@ from sparsetriton_amd.config import ConvAlgo, MIN_TABLE_FACTOR, get_conv_algo, g
 from sparsetriton_amd.tensor import SparseTensor
 from sparsetriton_amd.utils.hash import HashTable
 
-from .funcs.implicit_hashfly_gemm import ConvHashOnTheFlyImplicitGEMM, ConvSubmFlyGEMM, InputGradLookup, subm_fly_ok
+from .funcs.implicit_hashfly_gemm import (ConvHashOnTheFlyImplicitGEMM, ConvSubmFlyGEMM, InputGradLookup, fly_tile_order,
+                                          subm_fly_ok)
 from .funcs.implicit_precomputed_gemm import ConvPrecomputedNeighborGEMM, conv_forward_epilogue
 from .kmap import (BrickIndex, KernelMap, _target_offsets, brick_out_coords_and_map, build_out_coords_and_map,
                    query_kernel_map, subm_kernel_map)
@@ -208,7 +209,8 @@ def _sparse_conv3d(tensor, weight, kernel_size, bias, stride, dilation, padding,
             _raise_table_errors(table_status, None)
             return _empty(tensor, C_out, new_shape)
         offsets = _target_offsets(k, d, p, False, device)
-        out_feats = ConvSubmFlyGEMM.apply(tensor.F, weight, index, offsets)
+        order = fly_tile_order(index, offsets, (k, d, p))
+        out_feats = ConvSubmFlyGEMM.apply(tensor.F, weight, index, offsets, order)
         if bias is not None:
             out_feats = out_feats + bias.to(out_feats.dtype)  # as the hash-probing branch below
     elif algo == ConvAlgo.ImplicitHashFlyGEMM:

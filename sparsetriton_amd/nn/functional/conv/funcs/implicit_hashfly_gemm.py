@@ -27,6 +27,8 @@ offsets none of the tile's rows has.
 """
 
 import ctypes
+import os
+from typing import Optional
 
 import torch
 
@@ -42,7 +44,7 @@ from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import 
 )
 from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex, KernelMap, row_representatives
 
-__all__ = ["ConvHashOnTheFlyImplicitGEMM", "ConvSubmFlyGEMM", "InputGradLookup", "subm_fly_ok"]
+__all__ = ["ConvHashOnTheFlyImplicitGEMM", "ConvSubmFlyGEMM", "InputGradLookup", "fly_tile_order", "subm_fly_ok"]
 
 
 def _lookup(K: int, sign: int, mul: int, div: int, bounds, row_bounds=(0, 0, 0)) -> _lib.Lookup:
@@ -198,14 +200,26 @@ def subm_fly_ok(n: int, C_in: int, C_out: int, K: int, dtype: torch.dtype) -> bo
     return bool(lib.st_subm_fly_ok(n, C_in, C_out, K, code)) and bool(lib.st_subm_fly_ok(n, C_out, C_in, K, code))
 
 
-def subm_fly_gemm(A: torch.Tensor, index: BrickIndex, offsets_i32: torch.Tensor, Bt: torch.Tensor) -> torch.Tensor:
-    """out[r] = sum_k A[nbr(k, r)] @ Bt[k]^T over the submanifold neighbours found in ``index``."""
+def subm_fly_gemm(A: torch.Tensor, index: BrickIndex, offsets_i32: torch.Tensor, Bt: torch.Tensor,
+                  order: Optional[torch.Tensor] = None, reverse_k: bool = False) -> torch.Tensor:
+    """out[r] = sum_k A[nbr(k, r)] @ Bt[k]^T over the submanifold neighbours found in ``index``
+    (``Bt[K-1-k]`` with ``reverse_k``), 128-row tiles taken in ``order`` (``index.tile_order``)
+    when given, else in row order; the sums are the same either way."""
     n, Kd, Nd = index.n, A.shape[1], Bt.shape[1]
     out = torch.empty((n, Nd), dtype=A.dtype, device=A.device)
     _lib.call("st_subm_fly_gemm", _lib.ptr(A), _lib.ptr(index.coords), _lib.coord_code(index.coords.dtype), n,
               _lib.ptr(offsets_i32), offsets_i32.shape[0], *index.geometry, _lib.ptr(index.work), index.nbytes,
-              _lib.ptr(Bt), None, _lib.ptr(out), Kd, Nd, _lib.compute_code(A.dtype), _lib.stream_of(A.device))
+              _lib.ptr(order) if order is not None else None, _lib.ptr(Bt), None, _lib.ptr(out), Kd, Nd,
+              _lib.compute_code(A.dtype), _lib.GATHER_REVERSE_K if reverse_k else 0, _lib.stream_of(A.device))
     return out
+
+
+def fly_tile_order(index: BrickIndex, kernel_offsets: torch.Tensor, key) -> Optional[torch.Tensor]:
+    """The index's mask-sorted tile order for the fly GEMMs (``BrickIndex.tile_order``);
+    ``ST_FLY_ORDER=0`` keeps the rows' own order (for timing the two against each other)."""
+    if os.environ.get("ST_FLY_ORDER", "1") == "0":
+        return None
+    return index.tile_order(kernel_offsets, key)
 
 
 class ConvSubmFlyGEMM(torch.autograd.Function):
@@ -213,12 +227,14 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
     and K-1-k) with no stored kernel map: every GEMM looks its neighbours up in ``index``.
 
     Forward and, when the map is its own transpose (unique coordinates inside the box), the input
-    gradient run ``st_subm_fly_gemm`` (the latter with the weights reversed); the weight gradient --
-    and the input gradient otherwise -- take a map queried from the index that lives only for
-    the backward call."""
+    gradient run ``st_subm_fly_gemm`` (the latter with the offsets' weight slices reversed), both
+    over ``order`` (the rows sorted by offset mask; a row of the transposed map has the reversed
+    mask, so rows that share one share the other) when given; the weight gradient -- and the input
+    gradient otherwise -- take a map queried from the index that lives only for the backward
+    call."""
 
     @staticmethod
-    def forward(ctx, features, weights, index: BrickIndex, kernel_offsets):
+    def forward(ctx, features, weights, index: BrickIndex, kernel_offsets, order=None):
         _lib.require_device(features, "features")
         K, C_in, C_out = weights.shape
         assert C_in == features.shape[1], f"weights C_in ({C_in}) != features C_in ({features.shape[1]})"
@@ -227,9 +243,9 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
         features = features.contiguous()
         offs = kernel_offsets.to(torch.int32).contiguous()
         wt = weight_prep(weights.to(features.dtype).contiguous(), _lib.W_TRANSPOSE)
-        out = subm_fly_gemm(features, index, offs, wt)
+        out = subm_fly_gemm(features, index, offs, wt, order)
         ctx.save_for_backward(features, weights, offs)
-        ctx.index = index
+        ctx.index, ctx.order = index, order
         return out
 
     @staticmethod
@@ -259,13 +275,13 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
             with torch.cuda.stream(side):
                 grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=pl, buffers=bufs)
             w = weights.to(features.dtype).contiguous()
-            grad_input = subm_fly_gemm(grad_output, index, offs, weight_prep(w, _lib.W_REVERSE))
+            grad_input = subm_fly_gemm(grad_output, index, offs, w, ctx.order, reverse_k=True)
             main.wait_stream(side)
-            return grad_input, grad_weights, None, None
+            return grad_input, grad_weights, None, None, None
         if ctx.needs_input_grad[0]:
             w = weights.to(features.dtype).contiguous()
             if index.transposable():
-                grad_input = subm_fly_gemm(grad_output, index, offs, weight_prep(w, _lib.W_REVERSE))
+                grad_input = subm_fly_gemm(grad_output, index, offs, w, ctx.order, reverse_k=True)
             else:
                 n = index.n
                 kmap = KernelMap(queried().nbr, n, n, K)
@@ -276,4 +292,4 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             kmap = queried()
             grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=kmap.pair_list(with_tiles=False))
-        return grad_input, grad_weights, None, None
+        return grad_input, grad_weights, None, None, None

@@ -657,6 +657,7 @@ class BrickIndex:
         self.coords = coords
         self.geometry = (int(batch_size),) + tuple(int(v) for v in spatial_shape)
         self.work, self.nbytes, self.status = work, int(nbytes), status
+        self._orders = {}
 
     @classmethod
     def build(cls, coords: torch.Tensor, batch_size: int, spatial_shape) -> Optional["BrickIndex"]:
@@ -699,6 +700,24 @@ class BrickIndex:
                   K, *self.geometry, _lib.ptr(self.work), self.nbytes, _lib.ptr(nbr), _lib.ptr(masks),
                   _lib.stream_of(dev))
         return KernelMap(nbr, n, n, K, out_masks=masks)
+
+    def tile_order(self, kernel_offsets: torch.Tensor, key) -> torch.Tensor:
+        """The rows sorted by their offset masks (``st_kmap_subm_query`` writing the masks only,
+        then ``st_kmap_sort_rows``): the tile order ``st_subm_fly_gemm`` takes, so a 128-row tile
+        holds rows that need the same offsets.  Built once per kernel geometry ``key`` and kept with
+        the index (n int32; no map is stored)."""
+        if key not in self._orders:
+            n = self.n
+            K = kernel_offsets.shape[0]
+            dev = self.coords.device
+            masks = torch.empty((n, _mask_words(K)), dtype=torch.int32, device=dev)
+            offs = _offsets_i32(kernel_offsets)
+            _lib.call("st_kmap_subm_query", _lib.ptr(self.coords), _lib.coord_code(self.coords.dtype), n,
+                      _lib.ptr(offs), K, *self.geometry, _lib.ptr(self.work), self.nbytes, None, _lib.ptr(masks),
+                      _lib.stream_of(dev))
+            self._orders[key] = TilePlan.build(n, K, masks).perm
+        return self._orders[key]
+
 
 class OutCoordTable:
     """Dedup table of a strided / transposed build: output coordinate -> output row."""

@@ -316,6 +316,52 @@ def test_brick_index_query_equals_subm_map(device):
         assert index.status.counters() == snap.counters()
         if shape == (24, 24, 24):  # (repeats outside a smaller box are not indexed, so not counted)
             assert snap.counters()["duplicate"] == 40 and snap.counters()["out_of_box"] == 0
+        # the masks-only query (nbr = NULL) behind the fly GEMMs' tile order
+        order = index.tile_order(offs, ("t", d))
+        n = coords.shape[0]
+        assert torch.equal(torch.sort(order.long())[0].cpu(), torch.arange(n))
+        key = km.out_masks[:, 0].long().cpu().numpy()
+        o = order.long().cpu().numpy()
+        runs = np.flatnonzero(np.diff(key[o])) + 1  # rows of one mask are contiguous in the order
+        assert len(np.unique(key)) == len(runs) + 1
+
+
+@pytest.mark.parametrize("cin,cout,dtype", [(64, 64, torch.bfloat16), (128, 128, torch.bfloat16),
+                                            (64, 128, torch.float32), (128, 64, torch.float16)])
+def test_subm_fly_tile_order_and_reversed_offsets(device, cin, cout, dtype):
+    """st_subm_fly_gemm over the index's mask-sorted tile order gives the row-order result bit for
+    bit (a row's sum does not depend on its tile), and its ST_GATHER_REVERSE_K input gradient with
+    the weights as given equals the same call with an ST_W_REVERSE copy, bit for bit."""
+    from sparsetriton_amd import _lib
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_hashfly_gemm import subm_fly_gemm
+    from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import weight_prep
+    from sparsetriton_amd.nn.functional.conv.kmap import BrickIndex, _target_offsets
+    rng = np.random.default_rng(39 + cin)
+    n, S = 7000, 22
+    c = _rand_coords(rng, n, S)
+    shape = (S, S, S)
+    coords = torch.as_tensor(c, device=device)
+    index = BrickIndex.build(coords, 2, shape)
+    assert index.transposable()
+    offs = _target_offsets(3, 1, 1, False, device)
+    order = index.tile_order(offs, (3, 1, 1))
+    assert index.tile_order(offs, (3, 1, 1)) is order  # kept with the index
+    X = torch.as_tensor(rng.standard_normal((n, cin)), device=device).to(dtype)
+    dY = torch.as_tensor(rng.standard_normal((n, cout)), device=device).to(dtype)
+    W = torch.as_tensor(rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cin), device=device).to(dtype)
+    wt = weight_prep(W.contiguous(), _lib.W_TRANSPOSE)
+    y0 = subm_fly_gemm(X, index, offs, wt)
+    y1 = subm_fly_gemm(X, index, offs, wt, order)
+    assert torch.equal(y0, y1)
+    g0 = subm_fly_gemm(dY, index, offs, weight_prep(W.contiguous(), _lib.W_REVERSE))
+    g1 = subm_fly_gemm(dY, index, offs, W.contiguous(), order, reverse_k=True)
+    g2 = subm_fly_gemm(dY, index, offs, W.contiguous(), None, reverse_k=True)
+    assert torch.equal(g0, g1) and torch.equal(g0, g2)
+    # against the float64 oracle's input gradient of the same map
+    Xq, Wq, dYq = X.float().cpu().numpy(), W.float().cpu().numpy(), dY.float().cpu().numpy()
+    y, gx, _ = _oracle(c, c, shape, Xq, Wq, dYq, 3, 1, 1, 1, False)
+    assert rel(y1.float().cpu(), y) < TOL[dtype]
+    assert rel(g1.float().cpu(), gx) < TOL[dtype]
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
 def test_probing_weight_gradient_entry(device, dtype, tol):
