@@ -568,14 +568,24 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_kernel(
       __syncthreads();
       return gn_s;
     } else {
-      for (int j = tid >> 7; j < ng; j += 2) {
-        int32_t v;
-        if constexpr (Src::kTiled)
-          v = src.get_tile(tile.rt, g0 + j, tid & (kGemmBM - 1));
-        else
-          v = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
-        if ((int64_t)v >= n_src) v = -1;
-        src_s[j][tid & (kGemmBM - 1)] = v;
+      // every load of the group in flight before the first is used
+      constexpr int PB = (SG + 1) / 2;
+      int32_t v[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int j = (tid >> 7) + 2 * u;  // uniform across the wave
+        v[u] = -1;
+        if (j < ng) {
+          if constexpr (Src::kTiled)
+            v[u] = src.get_tile(tile.rt, g0 + j, tid & (kGemmBM - 1));
+          else
+            v[u] = ld_row >= 0 ? src.get(rc, klist_s[g0 + j]) : -1;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int j = (tid >> 7) + 2 * u;
+        if (j < ng) src_s[j][tid & (kGemmBM - 1)] = (int64_t)v[u] >= n_src ? -1 : v[u];
       }
       return ng;
     }
