@@ -277,7 +277,7 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
             w = weights.to(features.dtype).contiguous()
             grad_input = subm_fly_gemm(grad_output, index, offs, w, ctx.order, reverse_k=True)
             main.wait_stream(side)
-            return grad_input, grad_weights, None, None, None
+            return (grad_input, grad_weights) + (None,) * (len(ctx.needs_input_grad) - 2)
         if ctx.needs_input_grad[0]:
             w = weights.to(features.dtype).contiguous()
             if index.transposable():
@@ -292,4 +292,5 @@ class ConvSubmFlyGEMM(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             kmap = queried()
             grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=kmap.pair_list(with_tiles=False))
-        return grad_input, grad_weights, None, None, None
+        # (index, offsets and, when given, the tile order take no gradient)
+        return (grad_input, grad_weights) + (None,) * (len(ctx.needs_input_grad) - 2)
