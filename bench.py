@@ -22,6 +22,11 @@ reference algorithm's CPU port (oracle/st_oracle.c: 31-bit hash with 128-probe
 cap, output-major map, output-stationary forward, scatter input gradient, weight
 gradient by row slabs x offsets as the reference's grid; fp32, OpenMP) on the same voxel set.
 
+``measured_peaks`` confirms the spec-sheet peaks on the box: a 1 GiB device-to-device copy and
+the dense bf16 MFMA rate of register-only MFMA chains (``st_mfma_peak``); every roofline also
+gives its achieved rate as ``frac_of_measured_peak`` of the measured rate for its bound (``frac``
+stays against the published peak).
+
 The default run also measures the other benchmark configurations -- config 2 in bf16, the
 strided (config 3) and transposed (config 4) convolutions, the 1M-voxel layer (config 5) with
 either algorithm -- into ``configs``: one record each with its step time, effective TFLOP/s, the
@@ -175,6 +180,63 @@ def gemm_roofline(kernel, kernel_ms, n_in, n_out, cin, cout, K, P, dts, fp32_pre
                 "frac": gbps / PEAK["hbm_GBps"], **common}
     return {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s", "frac": tflops / mfma_peak,
             **common}
+
+
+def measured_peaks(torch, dev):
+    """The chip's sustained rates, measured on the box beside the spec-sheet peaks the rooflines
+    use: HBM as a 1 GiB device-to-device copy (bytes read + written / time, 5 back-to-back copies
+    after 2 untimed), dense bf16 MFMA as `st_mfma_peak` (8 independent 16x16x32 chains per wave on
+    register operands, four workgroups of four waves per CU; 3 launches after 1 untimed)."""
+    import ctypes
+
+    from sparsetriton_amd import _lib
+
+    n = 1 << 28  # fp32 elements: 1 GiB
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    reps = 5
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    e1.synchronize()
+    copy_gbps = 2 * 4 * n * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks, iters, launches = 4 * cus, 500, 3
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flops = ctypes.c_int64()
+    stream = _lib.stream_of(dev)
+    _lib.call("st_mfma_peak", iters, blocks, _lib.ptr(out), ctypes.byref(flops), stream)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(launches):
+        _lib.call("st_mfma_peak", iters, blocks, _lib.ptr(out), ctypes.byref(flops), stream)
+    e1.record()
+    e1.synchronize()
+    bf16 = flops.value * launches / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    torch.cuda.empty_cache()
+    return {"hbm_copy_GBps": copy_gbps, "bf16_mfma_TFLOPs": bf16, "split_fp32_mfma_TFLOPs": bf16 / 3.0,
+            "spec": dict(PEAK), "copy": "1 GiB device-to-device, 2 x 1 GiB moved per copy",
+            "mfma": f"st_mfma_peak: {blocks} workgroups x 4 waves x {iters} x 8 chains of 16x16x32 bf16"}
+
+
+def with_measured_peak(roof, peaks):
+    """The roofline's achieved rate also as a fraction of the rate measured on the box for its
+    bound (copy bandwidth, or the MFMA rate scaled like the spec peak it uses)."""
+    if not roof or not peaks:
+        return roof
+    if roof["bound"] == "hbm":
+        m = peaks["hbm_copy_GBps"]
+    else:
+        m = peaks["bf16_mfma_TFLOPs"] * roof["mfma_peak_TFLOPs"] / PEAK["bf16_TFLOPs"]
+    roof["measured_peak"] = m
+    roof["frac_of_measured_peak"] = roof["achieved"] / m
+    return roof
 
 
 def _stats(t):
@@ -899,6 +961,15 @@ def main():
             f"{c1['all']['fwd_bwd_GFLOPs']['median']:.2f} GFLOP/s ({c1['all']['threads']} threads), "
             f"{c1['one']['fwd_bwd_GFLOPs']['median']:.2f} GFLOP/s (1 thread)")
 
+    peaks = None
+    if not args.profile:
+        peaks = measured_peaks(torch, dev)
+        log(f"measured peaks: copy {peaks['hbm_copy_GBps']:.0f} GB/s, bf16 MFMA {peaks['bf16_mfma_TFLOPs']:.0f} "
+            f"TFLOP/s (spec {PEAK['hbm_GBps']:.0f} GB/s, {PEAK['bf16_TFLOPs']:.0f} TFLOP/s)")
+        with_measured_peak(roofline, peaks)
+        for rec in (configs or {}).values():
+            with_measured_peak(rec.get("roofline"), peaks)
+
     line = {
         "metric": METRIC,
         "value": value,
@@ -923,6 +994,7 @@ def main():
         "cpu_baseline": cpu,
         "gpu_config1": cfg1_gpu,
         "configs": configs,
+        "measured_peaks": peaks,
     }
     print(json.dumps(line), flush=True)
 

@@ -505,6 +505,16 @@ int st_column_sum(const void* Y, int64_t n, int C, int dtype, float* partials, v
 int st_column_sum_noalloc(const void* Y, int64_t n, int C, int dtype, void* out, int out_dtype, st_stream_t stream);
 
 /*
+ * No counterpart in the reference: a measurement helper.  Runs `blocks`
+ * workgroups of 4 waves, each wave `iters` x 8 independent dense bf16 MFMAs
+ * (16 x 16 x 32) on register operands, and writes one float per thread to out
+ * (blocks * 256 floats); *flops receives the launch's floating-point operation
+ * count (set before the launch), so flops / duration is the chip's sustained
+ * bf16 MFMA rate.  The bench reports it beside the spec-sheet peak.
+ */
+int st_mfma_peak(int iters, int blocks, float* out, int64_t* flops, st_stream_t stream);
+
+/*
  * Output-stationary gather-GEMM, the forward of ConvPrecomputedNeighborGEMM
  * (precomputed_fwd_kernel, implicit_precomputed_gemm.py:64-126) and, with the
  * transposed map, its input-gradient (precomputed_bwd_feat_kernel :129-177,

@@ -60,6 +60,7 @@ _L = ctypes.c_int64
 # name -> argtypes (all functions return int unless listed in _RESTYPES)
 _SIGNATURES = {
     "st_version": [],
+    "st_mfma_peak": [_I, _I, _P, ctypes.POINTER(ctypes.c_int64), _P],
     "st_fill_u32": [_P, _L, ctypes.c_uint32, _P],
     "st_fill_u64": [_P, _L, ctypes.c_uint64, _P],
     "st_hash_probe_mode": [_I],
