@@ -316,7 +316,13 @@ def test_brick_index_query_equals_subm_map(device):
         assert index.status.counters() == snap.counters()
         if shape == (24, 24, 24):  # (repeats outside a smaller box are not indexed, so not counted)
             assert snap.counters()["duplicate"] == 40 and snap.counters()["out_of_box"] == 0
-        # the masks-only query (nbr = NULL) behind the fly GEMMs' tile order
+        # the masks-only query (nbr = NULL) behind the fly GEMMs' tile order: the same mask words
+        from sparsetriton_amd import _lib
+        mo = torch.full_like(q.out_masks, -7)
+        _lib.call("st_kmap_subm_query", _lib.ptr(coords), _lib.coord_code(coords.dtype), coords.shape[0],
+                  _lib.ptr(offs), offs.shape[0], *index.geometry, _lib.ptr(index.work), index.nbytes, None,
+                  _lib.ptr(mo), _lib.stream_of(coords.device))
+        assert torch.equal(mo, q.out_masks)
         order = index.tile_order(offs, ("t", d))
         n = coords.shape[0]
         assert torch.equal(torch.sort(order.long())[0].cpu(), torch.arange(n))

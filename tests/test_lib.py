@@ -4,6 +4,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import torch
+
 from sparsetriton_amd import _lib
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -80,3 +82,22 @@ def test_subm_fly_eligibility_is_size_aware():
     assert lib.st_subm_fly_ok(n_fwd_only, 64, 128, 27, 2) == 1
     assert not subm_fly_ok(n_fwd_only, 64, 128, 27, torch.bfloat16)
     assert subm_fly_ok((lim - 1) // (128 * 2), 64, 128, 27, torch.bfloat16)
+
+
+def test_fly_gemm_and_masks_query_argument_checks():
+    """Host-side checks of the brick-index entry points (no device memory is touched): the fly
+    GEMM takes only ST_GATHER_REVERSE_K as a flag, and a subm query needs a map or mask output."""
+    lib = _lib.lib()
+    nbytes = ctypes.c_int64()
+    assert lib.st_kmap_subm_workspace(0, 1, 8, 8, 8, ctypes.byref(nbytes)) == 0
+    bad_flags = _lib.GATHER_REVERSE_K << 1
+    # n = 0: returns before any launch once the arguments are valid
+    args = (None, None, _lib.coord_code(torch.int16), 0, None, 27, 1, 8, 8, 8, None, nbytes.value, None, None, None,
+            None, 64, 64, _lib.compute_code(torch.bfloat16))
+    assert lib.st_subm_fly_gemm(*args, 0, None) == 0
+    assert lib.st_subm_fly_gemm(*args, _lib.GATHER_REVERSE_K, None) == 0
+    assert lib.st_subm_fly_gemm(*args, bad_flags, None) == -1
+    # one row, neither nbr nor row_masks: rejected before the launch
+    assert lib.st_kmap_subm_workspace(1, 1, 8, 8, 8, ctypes.byref(nbytes)) == 0
+    assert lib.st_kmap_subm_query(ctypes.c_void_p(16), _lib.coord_code(torch.int16), 1, ctypes.c_void_p(16), 27, 1, 8, 8,
+                                  8, ctypes.c_void_p(16), nbytes.value, None, None, None) == -1
