@@ -179,7 +179,10 @@ class KernelMap:
             c = chk.counters()
             self._symmetric = c["duplicate"] == 0 and c["out_of_box"] == 0
             self._symmetry_check = None
-            if c["duplicate"] and self._out_coords is not None:
+            # repeated coordinates need their rows folded before the map is transposed (two rows of
+            # one coordinate reach the same (input, offset)); rows outside the box are not in the
+            # brick index, so its duplicate count cannot see repeats among them: look at every row
+            if (c["duplicate"] or c["out_of_box"]) and self._out_coords is not None:
                 self.set_row_representatives(row_representatives(self._out_coords))
             self._out_coords = None
         return self._symmetric

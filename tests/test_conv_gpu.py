@@ -143,7 +143,7 @@ def test_general_geometries(device, dtype, k, s, p, d, tr):
 
 
 @pytest.mark.parametrize("algo", list(ConvAlgo))
-@pytest.mark.parametrize("case", ["in_box", "out_of_box", "duplicates", "both"])
+@pytest.mark.parametrize("case", ["in_box", "out_of_box", "duplicates", "both", "repeats_outside"])
 def test_subm_rows_outside_shape_or_repeated(device, algo, case):
     """Submanifold fwd + dX + dW when rows lie outside spatial_shape or repeat a coordinate.
 
@@ -161,6 +161,16 @@ def test_subm_rows_outside_shape_or_repeated(device, algo, case):
     if case in ("duplicates", "both"):
         rows = rng.choice(n, 150, replace=False)
         c[rows[75:]] = c[rows[:75]]  # 75 rows repeat another row's coordinate
+    if case == "repeats_outside":
+        # repeats only among rows just past the box (z = 15): the brick index does not hold those
+        # rows, so its duplicate count cannot see them, yet two such rows reach the same
+        # (input, offset) -- the transposed map must fold them, as for repeats inside the box
+        shape = (20, 20, 15)
+        outside = np.flatnonzero(c[:, 3] == 15)
+        rows = rng.choice(outside, 40, replace=False)
+        c[rows[20:]] = c[rows[:20]]
+        nbr = O.exact_kmap(c, c, O.target_offsets(3, 1, 1, False), 1, shape)
+        assert any(len(v[v >= 0]) > len(np.unique(v[v >= 0])) for v in nbr.T)  # the case is exercised
     X = rng.standard_normal((n, 32)).astype(np.float32)
     W = (rng.standard_normal((27, 32, 24)) / np.sqrt(27 * 32)).astype(np.float32)
     dY = rng.standard_normal((n, 24)).astype(np.float32)

@@ -4,7 +4,8 @@ oracle: submanifold (odd kernel), strided and transposed convolutions; kernel 1-
 off the submanifold path), stride 1-3, dilation 1-2, padding within the reference's bounds;
 1-3 samples, boxes of 4-22 voxels a side with 1-1,500 rows, or (a quarter of the cases) up to
 53 a side with up to 20,000 rows; channel counts on and off the built
-MFMA widths; fp32 / bf16 / fp16; int16 / int32 coordinates; both algorithms.  Output
+MFMA widths; fp32 / bf16 / fp16; int16 / int32 coordinates; a fifth of the sets with repeated
+coordinates and some with rows past the box; both algorithms.  Output
 coordinates equal the oracle's in order; forward, input and weight gradients within the
 reference's tolerances (relative Frobenius error); an empty output is empty for the oracle too."""
 import numpy as np
@@ -49,12 +50,22 @@ def _case(seed: int):
     lin = np.sort(rng.choice(cells, n, replace=False))
     sx, sy, sz = shape
     c = np.stack([lin // (sx * sy * sz), (lin // (sy * sz)) % sx, (lin // sz) % sy, lin % sz], 1).astype(np.int32)
+    dup = bool(rng.random() < 0.2) and n >= 4
+    if dup:  # repeated coordinates: a later row takes an earlier row's coordinate
+        m = max(1, n // 10)
+        src, dst = rng.choice(n, m, replace=False), rng.choice(n, m, replace=False)
+        c[dst] = c[src]
+    oob = bool(rng.random() < 0.15) and n >= 4
+    if oob:  # rows past the box on one axis (the reference keeps them; no row finds them as neighbours)
+        rows = rng.choice(n, max(1, n // 20), replace=False)
+        ax = int(rng.integers(1, 4))
+        c[rows, ax] = shape[ax - 1] + rng.integers(0, 3, rows.shape[0])
     cin, cout = int(rng.choice(CHANNELS)), int(rng.choice(CHANNELS))
     dtype = DTYPES[int(rng.integers(0, 3))]
     cdt = torch.int16 if rng.random() < 0.5 else torch.int32
     algo = list(ConvAlgo)[int(rng.integers(0, 2))]
-    return dict(subm=subm, tr=tr, k=k, s=s, d=d, p=p, B=B, shape=shape, c=c, cin=cin, cout=cout, dtype=dtype,
-                cdt=cdt, algo=algo, rng=rng)
+    return dict(subm=subm, tr=tr, k=k, s=s, d=d, p=p, B=B, shape=shape, c=c, dup=dup, cin=cin, cout=cout,
+                dtype=dtype, cdt=cdt, algo=algo, oob=oob, rng=rng)
 
 
 @pytest.mark.parametrize("seed", range(160))
