@@ -4,8 +4,9 @@ oracle: submanifold (odd kernel), strided and transposed convolutions; kernel 1-
 off the submanifold path), stride 1-3, dilation 1-2, padding within the reference's bounds;
 1-3 samples, boxes of 4-22 voxels a side with 1-1,500 rows, or (a quarter of the cases) up to
 53 a side with up to 20,000 rows; channel counts on and off the built
-MFMA widths; fp32 / bf16 / fp16; int16 / int32 coordinates; a fifth of the sets with repeated
-coordinates and some with rows past the box; both algorithms.  Output
+MFMA widths; fp32 / bf16 / fp16; int16 / int32 / int64 coordinates; with and without bias; a
+fifth of the sets with repeated coordinates and some with rows past the box on either side; both
+algorithms.  Output
 coordinates equal the oracle's in order; forward, input and weight gradients within the
 reference's tolerances (relative Frobenius error); an empty output is empty for the oracle too."""
 import numpy as np
@@ -56,19 +57,21 @@ def _case(seed: int):
         src, dst = rng.choice(n, m, replace=False), rng.choice(n, m, replace=False)
         c[dst] = c[src]
     oob = bool(rng.random() < 0.15) and n >= 4
-    if oob:  # rows past the box on one axis (the reference keeps them; no row finds them as neighbours)
+    if oob:  # rows past the box on one axis, either side (the reference keeps them; no row finds them)
         rows = rng.choice(n, max(1, n // 20), replace=False)
         ax = int(rng.integers(1, 4))
-        c[rows, ax] = shape[ax - 1] + rng.integers(0, 3, rows.shape[0])
+        past = rng.integers(0, 3, rows.shape[0])
+        c[rows, ax] = np.where(rng.random(rows.shape[0]) < 0.5, shape[ax - 1] + past, -1 - past)
     cin, cout = int(rng.choice(CHANNELS)), int(rng.choice(CHANNELS))
     dtype = DTYPES[int(rng.integers(0, 3))]
-    cdt = torch.int16 if rng.random() < 0.5 else torch.int32
+    cdt = [torch.int16, torch.int32, torch.int64][int(rng.integers(0, 3))]
+    bias = bool(rng.random() < 0.3)
     algo = list(ConvAlgo)[int(rng.integers(0, 2))]
     return dict(subm=subm, tr=tr, k=k, s=s, d=d, p=p, B=B, shape=shape, c=c, dup=dup, cin=cin, cout=cout,
-                dtype=dtype, cdt=cdt, algo=algo, oob=oob, rng=rng)
+                dtype=dtype, cdt=cdt, algo=algo, oob=oob, bias=bias, rng=rng)
 
 
-@pytest.mark.parametrize("seed", range(160))
+@pytest.mark.parametrize("seed", range(400))
 def test_random_geometry_sweep(device, seed):
     cs = _case(seed)
     subm, tr, k, s, d, p, B, shape, c = (cs[x] for x in ("subm", "tr", "k", "s", "d", "p", "B", "shape", "c"))
@@ -83,8 +86,12 @@ def test_random_geometry_sweep(device, seed):
     try:
         feats = torch.as_tensor(X, device=device).to(dtype).requires_grad_(True)
         w = torch.as_tensor(W, device=device).to(dtype).requires_grad_(True)
+        bvec = None
+        if cs["bias"]:
+            bq = torch.as_tensor(rng.standard_normal(cout).astype(np.float32)).to(dtype).float().numpy()
+            bvec = torch.as_tensor(bq, device=device).to(dtype).requires_grad_(True)
         sp = SparseTensor(feats, torch.as_tensor(c, device=device).to(cs["cdt"]), spatial_shape=shape, batch_size=B)
-        out = sparse_conv3d(sp, w, k, stride=s, padding=p, dilation=d, transposed=tr, submanifold=subm)
+        out = sparse_conv3d(sp, w, k, bias=bvec, stride=s, padding=p, dilation=d, transposed=tr, submanifold=subm)
         oc = out.C.cpu().numpy().astype(np.int32)
         dY = torch.as_tensor(rng.standard_normal((oc.shape[0], cout)).astype(np.float32)).to(dtype).float().numpy()
         if oc.shape[0] == 0:
@@ -110,6 +117,9 @@ def test_random_geometry_sweep(device, seed):
         else:
             nbr = O.exact_kmap(c, oc, off, s, shape)
     y = O.fwd_f64_blas(X, W, nbr)
+    if bvec is not None:
+        y = y + bq[None, :].astype(np.float64)
+        assert _rel(bvec.grad.float().cpu().numpy(), dY.astype(np.float64).sum(0)) < TOL[dtype], label
     gx = O.dgrad_f64_blas(dY, W, nbr, n)
     gw = O.wgrad_f64_blas(X, dY, nbr, k ** 3)
     tol = TOL[dtype]
