@@ -399,8 +399,8 @@ def measure_extra(name, steps, warmup, profile=False, fp32_precision="bf16x3", c
     from sparsetriton_amd.nn.functional.conv.funcs.implicit_precomputed_gemm import (
         gather_gemm_dgrad,
         gather_gemm_fwd,
+        weight_gradient,
         weight_prep,
-        wgrad,
     )
 
     desc, Cin, Cout, k, s, p, tr, subm, dts, algo = EXTRA[name]
@@ -500,11 +500,11 @@ def measure_extra(name, steps, warmup, profile=False, fp32_precision="bf16x3", c
         km = next(iter(sp2._cache.neighbor_indices.values()))[1]
         km.prepare()
         P = km.num_pairs()
-        kern["wgrad(+reduce)"] = _events_batch(torch, lambda: wgrad(X, dY, km, Wd.dtype), KR)
+        kern["wgrad(+reduce)"] = _events_batch(torch, lambda: weight_gradient(X, dY, km, Wd.dtype), KR)
     else:
         kern = {"gather_gemm_fwd": _events_batch(torch, lambda: gather_gemm_fwd(X, km, wt), KR),
                 "gather_gemm_dgrad": _events_batch(torch, lambda: gather_gemm_dgrad(dY, km, Wd.contiguous()), KR),
-                "wgrad(+reduce)": _events_batch(torch, lambda: wgrad(X, dY, km, Wd.dtype), KR)}
+                "wgrad(+reduce)": _events_batch(torch, lambda: weight_gradient(X, dY, km, Wd.dtype), KR)}
     set_conv_algo(prev_algo)
     dom = max(kern, key=kern.get)
     # the input gradient reads dY (N_out x C_out) and writes dX: the same bytes as the forward

@@ -568,18 +568,28 @@ int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* p
 
 /*
  * Weight gradient of ConvPrecomputedNeighborGEMM (precomputed_bwd_weight_kernel,
- * implicit_precomputed_gemm.py:180-230):
+ * implicit_precomputed_gemm.py:180-230) over the map itself:
  *   dW[k] = sum over o with map(k, o) >= 0 of X[map(k, o)]^T @ dY[o]
- * Each (k, split) workgroup compacts its slice of map column k in LDS and
- * runs MFMA over the valid pairs only; partials (K * splits * C_in * C_out
- * fp32 workspace) are reduced in a fixed order, so dW is bit-identical run
- * to run.  X (n_in, C_in) and dY (n_out, C_out) are `dtype` (map entries
- * outside [0, n_in) add nothing); dW (K, C_in, C_out) is written in `dw_dtype`
- * (e.g. fp32 master weights under bf16 activations).
+ * The map's n_out columns are cut into `splits` windows per offset, each one
+ * workgroup's partial (partials: K * splits * C_in * C_out fp32 workspace),
+ * reduced in a fixed order, so dW is bit-identical run to run.  16-bit rows
+ * with C_in and C_out multiples of 128 run the window kernel: a workgroup
+ * takes two offsets of one window, its waves the offsets' 128 x 64 halves,
+ * each step's dY rows staged once for all four, steps in which an offset has
+ * no pair skipped.  `rows` (optional, window kernel only, else
+ * ST_ERR_UNSUPPORTED): the dY row of each map column, so that the caller can
+ * hand the columns over in another order -- map(k, p) pairs X row map(k, p)
+ * with dY row rows[p]; columns sorted by offset mask within slabs of the
+ * output order make most offset steps all pairs or none.  NULL: column p is
+ * dY row p.  Columns whose rows entry lies outside [0, n_out) add nothing.
+ * Other shapes compact each (k, window) slice of map column k in LDS.
+ * X (n_in, C_in) and dY (n_out, C_out) are `dtype` (map entries outside
+ * [0, n_in) add nothing); dW (K, C_in, C_out) is written in `dw_dtype` (e.g.
+ * fp32 master weights under bf16 activations).
  */
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,
-             int64_t map_r_stride, int64_t n_out, int K, int C_in, int C_out, int dtype, float* partials,
-             int64_t splits, void* dW, int dw_dtype, st_stream_t stream);
+             int64_t map_r_stride, const int32_t* rows, int64_t n_out, int K, int C_in, int C_out, int dtype,
+             float* partials, int64_t splits, void* dW, int dw_dtype, st_stream_t stream);
 
 /*
  * Weight gradient over a pair list from st_kmap_pairs: every chunk of

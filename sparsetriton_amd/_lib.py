@@ -102,7 +102,7 @@ _SIGNATURES = {
     "st_gather_gemm_tiled_epilogue": [_P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _L, _I, _I, _I, _I,
                                       _P],
     "st_gather_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P],
-    "st_wgrad": [_P, _L, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P, _L, _P, _I, _P],
+    "st_wgrad": [_P, _L, _P, _P, _L, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _I, _P],
     "st_hashfly_gemm": [_P, _L, _P, _I, _L, _P, ctypes.POINTER(Lookup), _P, _P, _L, _P, _P, _P, _I, _I, _I, _P],
     "st_to_dense": [_P, _L, _I, _I, _P, _I, _L, _L, _L, _L, _P, _P],
     "st_from_dense": [_P, _L, _L, _L, _L, _I, _I, _P, _I, _L, _P, _P],

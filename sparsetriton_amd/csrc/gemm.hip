@@ -326,14 +326,14 @@ int st_gather_gemm_tiled_epilogue(const void* A, int64_t n_src, const int32_t* p
 }
 
 int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, int64_t map_k_stride,
-             int64_t map_r_stride, int64_t n_out, int K, int C_in, int C_out, int dtype, float* partials,
-             int64_t splits, void* dW, int dw_dtype, st_stream_t stream) {
+             int64_t map_r_stride, const int32_t* rows, int64_t n_out, int K, int C_in, int C_out, int dtype,
+             float* partials, int64_t splits, void* dW, int dw_dtype, st_stream_t stream) {
   if (n_in < 0 || n_out < 0 || K <= 0 || K > ST_MAX_KVOL || C_in <= 0 || C_out <= 0 || splits < 1 || splits > 65535)
     return ST_ERR_ARG;
   if (n_out >= (1ll << 31)) return ST_ERR_ARG;
   if (!partials || !dW || (n_out > 0 && (!X || !dY || !map))) return ST_ERR_ARG;
   ST_DISPATCH_DTYPE(dtype, T,
-                    ops_wgrad_map<T>((const T*)X, n_in, (const T*)dY, map, map_k_stride, map_r_stride, n_out, K, C_in,
+                    ops_wgrad_map<T>((const T*)X, n_in, (const T*)dY, map, map_k_stride, map_r_stride, rows, n_out, K, C_in,
                                      C_out, partials, splits, dW, dw_dtype, stream));
 }
 

@@ -1600,15 +1600,233 @@ static int launch_wgrad_reduce(const float* partials, const int32_t* cstart_or_n
   return ST_OK;
 }
 
+// Weight gradient over windows of map columns for 16-bit rows whose C_in and
+// C_out are multiples of 128 (a workgroup covers one 128 x 128 channel tile):
+// column p of the map pairs X rows map(k, p) with dY row rows[p] (p itself
+// when rows is null), so a caller can hand the columns over in any order --
+// rows sorted by offset mask within slabs of their own order, with the map
+// permuted to match, lets the kernel skip most offset steps without pairs
+// while a slab's rows stay near each other.  A workgroup takes a window of
+// rows_per_split columns and two consecutive offsets; its four waves take
+// (offset, output-channel half) each, a 128 x 64 fp32 tile of dW[k] (two
+// workgroups per CU).  The window is walked in 32-column steps: a step's dY
+// rows are staged in LDS once for the four waves and each offset's X rows
+// once for its two waves (zeros where the map has no pair; two buffers, one
+// workgroup barrier a step); a wave adds X^T dY over the step, both operands
+// read as transpose fragments (tr_frag), skips the MFMAs of a step in which
+// its offset has no pair, and masks the dY elements of the columns without
+// one, so that a non-finite dY value reaches only the offsets that pair its
+// row, as in a sum over pairs.  Loads run two steps ahead: the map entries
+// and rows of step s + 3 are issued before the rows of step s + 2 (the
+// memory counter completes in order, so waiting on the former never waits on
+// the latter), with a register set per step parity (the loop body is two
+// steps, so no value still in flight is ever copied).  Against equal chunks
+// of the pair list a dY row is read once per two offsets instead of once per
+// pair, and the workgroups of one window run side by side on one XCD (work
+// item L = (window, channel tile, offset pair) runs on XCD L / ceil(items /
+// 8)), so the X rows that neighbouring offsets share come from that XCD's
+// L2.  Each wave stores its tile to partials[(k * splits + window) * C_in *
+// C_out ...] (the layout that wgrad_reduce_kernel sums).  Requires 16-byte
+// aligned rows and X and dY addressable by 32-bit buffer offsets.
+template <typename T>
+__global__ __launch_bounds__(256, 2) void wgrad_window_kernel(const T* __restrict__ X, const T* __restrict__ dY,
+                                                              const int32_t* __restrict__ map, int64_t ks, int64_t rs,
+                                                              const int32_t* __restrict__ rows, int64_t n_in,
+                                                              int64_t n_out, int K, int Cin, int Cout,
+                                                              int64_t rows_per_split, int splits,
+                                                              float* __restrict__ partials) {
+  using F = typename Frag<T>::type;
+  static_assert(Frag<T>::KSTEP == 32 && Frag<T>::VEC == 8, "16-bit MFMA fragments");
+  constexpr int P = wave_pitch(128);
+  constexpr int STAGE = 32 * P;  // 32 rows of 128 channels
+  __shared__ __attribute__((aligned(16))) T ys_s[2 * STAGE];      // dY, two buffers
+  __shared__ __attribute__((aligned(16))) T xs_s[2 * 2 * STAGE];  // X of the two offsets, two buffers
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int kpairs = (K + 1) / 2;
+  const int ntn = Cout / 128, ntiles = (Cin / 128) * ntn;
+  const int64_t items = (int64_t)splits * ntiles * kpairs;
+  const int64_t per = (items + 7) / 8;
+  const int64_t L = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (L >= items) return;  // uniform over the workgroup
+  const int grp = (int)(L % kpairs);
+  const int64_t wt = L / kpairs;
+  const int tile = (int)(wt % ntiles);
+  const int w = (int)(wt / ntiles);
+  const int cm0 = (tile / ntn) * 128, cn0 = (tile % ntn) * 128;
+  const int kw = wid >> 1, half = wid & 1;  // this wave's offset of the pair, output-channel half
+  const int k = grp * 2 + kw;
+  const bool kv = k < K;
+  const int64_t o0 = (int64_t)w * rows_per_split;
+  const int64_t o1 = min(o0 + rows_per_split, n_out);
+  const int nsteps = o1 > o0 ? (int)((o1 - o0 + 31) / 32) : 0;
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(X, n_in * Cin * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(dY, n_out * Cout * (int64_t)sizeof(T));
+  const int pt = half * 64 + lane;  // thread of this offset's pair of waves, 0..127
+
+  // column (lane mod 32) of step s: its dY row (-1 past the window, and for
+  // an entry of rows outside [0, n_out)) and its map entry through this
+  // wave's offset (-1: none)
+  auto load_row = [&](int s) -> int {
+    const int64_t p = o0 + 32 * (int64_t)s + (lane & 31);
+    const int r = (s < nsteps && p < o1) ? (rows ? rows[p] : (int)p) : -1;
+    return (r >= 0 && r < n_out) ? r : -1;
+  };
+  auto load_idx = [&](int s) -> int {
+    const int64_t p = o0 + 32 * (int64_t)s + (lane & 31);
+    return (kv && s < nsteps && p < o1) ? map[(int64_t)k * ks + p * rs] : -1;
+  };
+  // this offset's X rows of a step: load v takes 16 bytes (channel chunk
+  // pt mod 16) of step column pt / 16 + 8 v, whose map entry lane (column) holds
+  // (each lane taking 64 bytes of its own column's row instead, no exchange:
+  // 1.05 -> 1.23 ms on config 5, the loads less contiguous)
+  auto load_x = [&](int idx, int row, F* xr) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int col = (pt >> 4) + 8 * v;
+      const int ix = __shfl(row >= 0 ? idx : -1, col, 64);
+      xr[v] = load16<F>(x_rsrc, (ix >= 0 && ix < n_in) ? (ix * Cin + cm0 + (pt & 15) * 8) * (int)sizeof(T) : kOobOffset);
+    }
+  };
+  // the step's dY rows: 16 threads a row, step column tid / 16 + 16 v
+  auto load_y = [&](int row, F* yr) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int r = __shfl(row, (tid >> 4) + 16 * v, 64);
+      yr[v] = load16<F>(y_rsrc, r >= 0 ? (r * Cout + cn0 + (tid & 15) * 8) * (int)sizeof(T) : kOobOffset);
+    }
+  };
+
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // per step parity u: xr/yr[u] the rows of the next step s of parity u in
+  // flight and pmr[u] its pair mask; at step s, idx/row[u] hold the map
+  // entries and dY rows of step s + 2 (loaded at step s - 1)
+  F xr[2][4], yr[2][2];
+  int idx[2], row[2];
+  uint64_t pmr[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    idx[u] = load_idx(u);
+    row[u] = load_row(u);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    load_x(idx[u], row[u], xr[u]);
+    load_y(row[u], yr[u]);
+    pmr[u] = __ballot(row[u] >= 0 && idx[u] >= 0);
+  }
+  idx[0] = load_idx(2);
+  row[0] = load_row(2);
+  idx[1] = -1;  // (step 3's, loaded at step 0)
+  row[1] = -1;
+  // the steps rounded up to even: the extra step has no columns, so it adds
+  // nothing and skips its MFMAs
+  for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int s = s0 + u;
+      T* ys = ys_s + u * STAGE;
+      T* xs = xs_s + (u * 2 + kw) * STAGE;
+#pragma unroll
+      for (int v = 0; v < 2; ++v) *reinterpret_cast<F*>(&ys[((tid >> 4) + 16 * v) * P + (tid & 15) * 8]) = yr[u][v];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) *reinterpret_cast<F*>(&xs[((pt >> 4) + 8 * v) * P + (pt & 15) * 8]) = xr[u][v];
+      // the step's stages complete for every wave; the other buffers, read in
+      // the previous step, free for the next step's stores
+      __syncthreads();
+      const uint64_t pm = pmr[u];  // bit r (r < 32): step column r has a pair through this offset
+      // step s + 3's map entries and rows first, then step s + 2's rows
+      const int idx3 = load_idx(s + 3), row3 = load_row(s + 3);
+      load_x(idx[u], row[u], xr[u]);
+      load_y(row[u], yr[u]);
+      pmr[u] = __ballot(row[u] >= 0 && idx[u] >= 0);
+      // (each of idx / row[0 / 1] is set once per two steps, after its last
+      // use, so no value still in flight is copied)
+      idx[u ^ 1] = idx3;
+      row[u ^ 1] = row3;
+      if (pm) {  // uniform over the wave
+        // this lane's fragment elements hold columns 4g .. 4g+3 and 16+4g .. 16+4g+3
+        const uint32_t bits = (uint32_t)((pm >> (4 * g)) & 0xFu) | ((uint32_t)((pm >> (16 + 4 * g)) & 0xFu) << 4);
+        uint32_t mw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          mw[e] = (((bits >> (2 * e)) & 1u) ? 0x0000FFFFu : 0u) | (((bits >> (2 * e + 1)) & 1u) ? 0xFFFF0000u : 0u);
+        F b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint4 bw = __builtin_bit_cast(uint4, tr_frag<F, T, P>(ys, g, c, half * 64 + j * 16));
+          bw.x &= mw[0];
+          bw.y &= mw[1];
+          bw.z &= mw[2];
+          bw.w &= mw[3];
+          b[j] = __builtin_bit_cast(F, bw);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const F a = tr_frag<F, T, P>(xs, g, c, i * 16);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma(a, b[j], acc[i][j]);
+        }
+      }
+    }
+  }
+  if (kv) {
+    float* part = partials + ((int64_t)k * splits + w) * Cin * Cout;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part[(int64_t)(cm0 + i * 16 + g * 4 + r) * Cout + cn0 + half * 64 + j * 16 + c] = acc[i][j][r];
+  }
+}
+
+// Row arrays addressable by 32-bit buffer offsets.
+static bool rows_fit_buffer(int64_t n_in, int Cin, int64_t n_out, int Cout, size_t esz) {
+  return n_in * Cin * (int64_t)esz < (1ll << 31) - 64 && n_out * Cout * (int64_t)esz < (1ll << 31) - 64;
+}
+
+// Whether the window kernel above is taken for 16-bit maps with 128-multiple
+// channel counts (ST_WGRAD_WINDOW=0 turns it off).
+static bool wgrad_window_on() {
+  static int mode = -1;
+  if (mode < 0) {
+    const char* e = getenv("ST_WGRAD_WINDOW");
+    mode = (e && e[0] == '0') ? 0 : 1;
+  }
+  return mode == 1;
+}
+
 template <typename T, typename Src>
 static int launch_wgrad(const T* X, int64_t n_in, const T* dY, const Src& src, int64_t n_out, int K, int Cin,
-                        int Cout, float* partials, int64_t splits, void* dW, int dw_dtype, hipStream_t stream) {
+                        int Cout, float* partials, int64_t splits, void* dW, int dw_dtype, hipStream_t stream,
+                        const int32_t* rows = nullptr) {
   constexpr int VEC = Frag<T>::VEC;
   const int vec_x = (Cin % VEC == 0) && ((uintptr_t)X % 16 == 0);
   const int vec_y = (Cout % VEC == 0) && ((uintptr_t)dY % 16 == 0);
   const int64_t rows_per_split = (n_out + splits - 1) / splits;
   const int MB = (Cin + 15) / 16, NB = (Cout + 15) / 16;
   const unsigned gz = (unsigned)(((MB + kWgTileBlk - 1) / kWgTileBlk) * ((NB + kWgTileBlk - 1) / kWgTileBlk));
+  bool window = false;
+  if constexpr (sizeof(T) == 2 && !Src::kTiled && !Src::kProbe)
+    window = wgrad_window_on() && Cin % 128 == 0 && Cout % 128 == 0 && vec_x && vec_y &&
+             rows_fit_buffer(n_in, Cin, n_out, Cout, sizeof(T));
+  if (rows && !window) return ST_ERR_UNSUPPORTED;  // only the window kernel takes a column order
+  if constexpr (sizeof(T) == 2 && !Src::kTiled && !Src::kProbe) {
+    if (n_out > 0 && window) {
+      const int64_t items = splits * (int64_t)(Cin / 128) * (Cout / 128) * ((K + 1) / 2);
+      wgrad_window_kernel<T><<<(unsigned)(8 * ((items + 7) / 8)), 256, 0, stream>>>(
+          X, dY, src.map, src.ks, src.rs, rows, n_in, n_out, K, Cin, Cout, rows_per_split, (int)splits, partials);
+      ST_CHECK_LAUNCH();
+      return launch_wgrad_reduce(partials, nullptr, splits, K, Cin, Cout, dW, dw_dtype, stream);
+    }
+  }
   if (n_out > 0) {
     wgrad_kernel<T, Src><<<dim3((unsigned)splits, (unsigned)K, gz), 256, 0, stream>>>(
         X, dY, src, n_in, n_out, Cin, Cout, rows_per_split, (int)splits, partials, vec_x, vec_y);
@@ -1642,10 +1860,6 @@ static void launch_wgrad_pairs_f32(const float* X, const float* dY, const int2* 
 static int pow2_tile(int blocks) { return blocks >= 4 ? 4 : (blocks >= 2 ? 2 : 1); }
 
 
-// Row arrays addressable by 32-bit buffer offsets.
-static bool rows_fit_buffer(int64_t n_in, int Cin, int64_t n_out, int Cout, size_t esz) {
-  return n_in * Cin * (int64_t)esz < (1ll << 31) - 64 && n_out * Cout * (int64_t)esz < (1ll << 31) - 64;
-}
 
 // 16-bit weight-gradient kernel: 0 = per-wave steps (default), 1 = workgroup
 // LDS transpose (ST_WGRAD16=lds), 2 = per-wave steps with tiles of at most
@@ -1806,11 +2020,11 @@ int ops_gather_fly(const T* A, int64_t n, const void* coords, int coord_dtype, c
 }
 
 template <typename T>
-int ops_wgrad_map(const T* X, int64_t n_in, const T* dY, const int32_t* map, int64_t ks, int64_t rs, int64_t n_out,
-                  int K, int Cin, int Cout, float* partials, int64_t splits, void* dW, int dw_dtype,
-                  hipStream_t stream) {
+int ops_wgrad_map(const T* X, int64_t n_in, const T* dY, const int32_t* map, int64_t ks, int64_t rs,
+                  const int32_t* rows, int64_t n_out, int K, int Cin, int Cout, float* partials, int64_t splits,
+                  void* dW, int dw_dtype, hipStream_t stream) {
   MapSrc src{map, ks, rs};
-  return launch_wgrad<T>(X, n_in, dY, src, n_out, K, Cin, Cout, partials, splits, dW, dw_dtype, stream);
+  return launch_wgrad<T>(X, n_in, dY, src, n_out, K, Cin, Cout, partials, splits, dW, dw_dtype, stream, rows);
 }
 
 template <typename T>
@@ -1846,8 +2060,8 @@ int ops_weight_prep(const T* w, T* out, int K, int Cin, int Cout, int mode, hipS
                                     const uint64_t*, const uint32_t*, int64_t, const T*, T*, Epi<T>, int64_t, int, \
                                     int,                                                                             \
                                     hipStream_t);                                                                    \
-  X template int ops_wgrad_map<T>(const T*, int64_t, const T*, const int32_t*, int64_t, int64_t, int64_t, int, int,  \
-                                  int, float*, int64_t, void*, int, hipStream_t);                                    \
+  X template int ops_wgrad_map<T>(const T*, int64_t, const T*, const int32_t*, int64_t, int64_t, const int32_t*,   \
+                                  int64_t, int, int, int, float*, int64_t, void*, int, hipStream_t);               \
   X template int ops_wgrad_hash<T>(const T*, int64_t, const T*, const void*, int, int64_t, const int32_t*,           \
                                    const st_lookup*, const uint64_t*, const uint32_t*, int64_t, int, int, float*,    \
                                    int64_t, void*, int, hipStream_t);                                                \

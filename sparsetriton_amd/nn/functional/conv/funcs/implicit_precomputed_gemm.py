@@ -20,10 +20,13 @@ Kernels (``libsparsetriton_amd.so``):
             reversed, so dgrad gathers through the forward map, masks and tile
             order with the weights reversed along k (no inverse map is built);
   wgrad     st_wgrad_pairs over the (offset, out)-sorted pair list in
-            equal-size chunks, fixed-order reduce.
+            equal-size chunks, fixed-order reduce; for 16-bit rows with 128-multiple
+            channel counts over a dense map, st_wgrad over the map itself (windows of
+            output rows, four offsets a workgroup sharing each staged dY row).
 """
 
 import os
+from typing import Optional
 
 import torch
 
@@ -175,17 +178,82 @@ def wgrad(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dt
     return dW
 
 
-def wgrad_scan(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype) -> torch.Tensor:
-    """Weight gradient that compacts map columns on the fly (no pair list; st_wgrad)."""
+def window_splits(n_out: int, K: int, C_in: int, C_out: int) -> int:
+    """Output-row windows per offset for st_wgrad's window kernel (16-bit rows, C_in and C_out
+    multiples of 128): a workgroup per (window, 128 x 128 channel tile, pair of offsets), one
+    round of 512 workgroups (two per CU), windows of at least 1024 rows.
+    ST_WGRAD_WINDOW_ROUNDS=r asks for r rounds."""
+    items = (C_in // 128) * (C_out // 128) * ((K + 1) // 2)
+    rounds = max(1, int(os.environ.get("ST_WGRAD_WINDOW_ROUNDS", "1")))
+    return max(1, min((n_out + 1023) // 1024, max(1, (512 * rounds) // items)))
+
+
+def window_slab() -> int:
+    """Slab (rows) of ``KernelMap.window_order`` for the window weight gradient; 0 takes the map's
+    columns in their own order (ST_WGRAD_SLAB)."""
+    return int(os.environ.get("ST_WGRAD_SLAB", "4096"))
+
+
+def window_wgrad_ok(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap) -> bool:
+    """Whether the weight gradient runs over the map itself (st_wgrad's window kernel, the map's
+    columns in ``window_order``) instead of the pair list: only when ST_WGRAD_PATH=window asks
+    for it, for 16-bit rows with C_in and C_out multiples of 128.  On config 5 (1 M rows, 18
+    pairs a row) it moves half the fabric bytes of the pair-list kernel (2.5 vs 5.2 GB) at the
+    same time (1.05 vs 1.04 ms), so the pair list stays the default."""
+    if os.environ.get("ST_WGRAD_PATH", "pairs") != "window":
+        return False
+    return X.dtype in (torch.bfloat16, torch.float16) and X.shape[1] % 128 == 0 and dY.shape[1] % 128 == 0
+
+
+def scan_splits(X: torch.Tensor, dY: torch.Tensor, n_out: int, K: int) -> int:
+    """Row splits per offset for ``wgrad_scan``: ``window_splits`` where st_wgrad takes the window
+    kernel, else ``wgrad_splits``."""
+    C_in, C_out = X.shape[1], dY.shape[1]
+    if X.dtype in (torch.bfloat16, torch.float16) and C_in % 128 == 0 and C_out % 128 == 0:
+        return window_splits(n_out, K, C_in, C_out)
+    return wgrad_splits(n_out)
+
+
+def scan_buffers(X: torch.Tensor, dY: torch.Tensor, K: int, splits: int, dw_dtype: torch.dtype):
+    """(partials, dW) for ``wgrad_scan`` with ``splits`` row splits."""
+    C_in, C_out = X.shape[1], dY.shape[1]
+    return (torch.empty((K * splits * C_in * C_out,), dtype=torch.float32, device=X.device),
+            torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device))
+
+
+def wgrad_scan(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype,
+               splits: Optional[int] = None, buffers=None, order=None) -> torch.Tensor:
+    """Weight gradient over the map itself, no pair list (st_wgrad): for 16-bit rows with C_in and
+    C_out multiples of 128 the window kernel (over the map's columns in the order ``order`` =
+    ``KernelMap.window_order(slab)`` when given), else map columns compacted on the fly;
+    ``splits`` from ``scan_splits`` and ``buffers`` from ``scan_buffers`` unless given."""
     K, C_in, C_out = kmap.K, X.shape[1], dY.shape[1]
-    splits = wgrad_splits(kmap.n_out)
-    partials = torch.empty((K * splits * C_in * C_out,), dtype=torch.float32, device=X.device)
-    dW = torch.empty((K, C_in, C_out), dtype=dw_dtype, device=X.device)
-    _lib.call("st_wgrad", _lib.ptr(X), X.shape[0], _lib.ptr(dY), _lib.ptr(kmap.nbr), kmap.k_stride, kmap.r_stride,
-              kmap.n_out,
+    if splits is None:
+        splits = scan_splits(X, dY, kmap.n_out, K)
+    partials, dW = scan_buffers(X, dY, K, splits, dw_dtype) if buffers is None else buffers
+    if order is None:
+        m, ks, rs, rows = kmap.nbr, kmap.k_stride, kmap.r_stride, None
+    else:
+        rows, m = order
+        ks, rs = kmap.n_out, 1
+    _lib.call("st_wgrad", _lib.ptr(X), X.shape[0], _lib.ptr(dY), _lib.ptr(m), ks, rs,
+              None if rows is None else _lib.ptr(rows), kmap.n_out,
               K, C_in, C_out, _lib.feat_code(X.dtype), _lib.ptr(partials), splits, _lib.ptr(dW),
               _lib.feat_code(dw_dtype), _lib.stream_of(X.device))
     return dW
+
+
+def window_order(kmap: KernelMap):
+    slab = window_slab()
+    return kmap.window_order(slab) if slab > 0 else None
+
+
+def weight_gradient(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap, dw_dtype: torch.dtype) -> torch.Tensor:
+    """dW by the path the backward takes: the window kernel over the map where
+    ``window_wgrad_ok``, else the pair list."""
+    if window_wgrad_ok(X, dY, kmap):
+        return wgrad_scan(X, dY, kmap, dw_dtype, order=window_order(kmap))
+    return wgrad(X, dY, kmap, dw_dtype)
 
 
 _SIDE_STREAMS = {}
@@ -249,13 +317,20 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
             # The two gradients are independent: the weight gradient runs on a second stream beside
             # the input gradient (every buffer it touches is allocated on this stream first, and this
             # stream waits for it before returning).
-            pl = kmap.pair_list()
-            bufs = wgrad_buffers(features, grad_output, pl, kmap.K, weights.dtype)
+            if window_wgrad_ok(features, grad_output, kmap):
+                splits = scan_splits(features, grad_output, kmap.n_out, kmap.K)
+                bufs = scan_buffers(features, grad_output, kmap.K, splits, weights.dtype)
+                order = window_order(kmap)
+                run = lambda: wgrad_scan(features, grad_output, kmap, weights.dtype, splits, bufs, order)  # noqa: E731
+            else:
+                pl = kmap.pair_list()
+                bufs = wgrad_buffers(features, grad_output, pl, kmap.K, weights.dtype)
+                run = lambda: wgrad(features, grad_output, kmap, weights.dtype, pairs=pl, buffers=bufs)  # noqa: E731
             main = torch.cuda.current_stream(features.device)
             side = _side_stream(features.device)
             side.wait_stream(main)
             with torch.cuda.stream(side):
-                grad_weights = wgrad(features, grad_output, kmap, weights.dtype, pairs=pl, buffers=bufs)
+                grad_weights = run()
             w = weights.to(features.dtype).contiguous()
             grad_input = gather_gemm_dgrad(grad_output, kmap, w)
             main.wait_stream(side)
@@ -265,7 +340,7 @@ class ConvPrecomputedNeighborGEMM(torch.autograd.Function):
                 # dX[i] = sum_k dY[invnbr[k, i]] @ W[k]^T: W[k] (C_in, C_out) is already the (Nd, Kd) operand.
                 grad_input = gather_gemm_dgrad(grad_output, kmap, w)
             if ctx.needs_input_grad[1]:
-                grad_weights = wgrad(features, grad_output, kmap, weights.dtype)
+                grad_weights = weight_gradient(features, grad_output, kmap, weights.dtype)
         grad_bias = None
         if ctx.bias_dtype is not None and len(ctx.needs_input_grad) > 3 and ctx.needs_input_grad[3]:
             grad_bias = column_sum(grad_output, ctx.bias_dtype)

@@ -157,6 +157,7 @@ class KernelMap:
         self._fwd_tiles = None
         self._bwd_tiles = None
         self._pairs = {}
+        self._window_orders = {}
 
     @classmethod
     def from_neighbor_indices(cls, neighbor_indices: torch.Tensor, n_in: int) -> "KernelMap":
@@ -322,6 +323,24 @@ class KernelMap:
     def num_pairs(self) -> int:
         """Number of valid (input, output, offset) triples (synchronises)."""
         return int((self.neighbor_indices >= 0).sum().item())
+
+    def window_order(self, slab: int):
+        """(rows, map): the output rows sorted by offset mask (its first word) within consecutive
+        slabs of ``slab`` rows (int32, n_out) and the map's columns in that order ((K, n_out)
+        int32), kept per slab size -- the column order of the window weight gradient.  It skips
+        an offset's 32-column steps without pairs, and in this order most steps of an offset
+        have pairs in all columns or in none, while the rows of a slab stay near each other
+        (config 5: 1.04x the useful MFMA rows at 4,096-row slabs, 1.29x in row order)."""
+        got = self._window_orders.get(slab)
+        if got is None:
+            self.ensure_out_masks()
+            m = self.out_masks[:, 0].to(torch.int64) & 0xFFFFFFFF
+            pos = torch.arange(self.n_out, device=m.device, dtype=torch.int64)
+            order = torch.sort((pos // slab) * (1 << 32) + m, stable=True).indices
+            full = torch.as_strided(self.nbr, (self.K, self.n_out), (self.k_stride, self.r_stride))
+            got = (order.to(torch.int32), full.index_select(1, order).contiguous())
+            self._window_orders[slab] = got
+        return got
 
     def triples(self) -> torch.Tensor:
         """(P, 3) int64 rows (in, out, k) sorted -- the canonical parity form."""
