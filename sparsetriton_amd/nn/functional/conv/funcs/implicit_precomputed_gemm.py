@@ -198,7 +198,7 @@ def window_wgrad_ok(X: torch.Tensor, dY: torch.Tensor, kmap: KernelMap) -> bool:
     """Whether the weight gradient runs over the map itself (st_wgrad's window kernel, the map's
     columns in ``window_order``) instead of the pair list: only when ST_WGRAD_PATH=window asks
     for it, for 16-bit rows with C_in and C_out multiples of 128.  On config 5 (1 M rows, 18
-    pairs a row) it moves half the fabric bytes of the pair-list kernel (2.5 vs 5.2 GB) at the
+    pairs a row) it moves half the fabric bytes of the pair-list kernel (2.6 vs 5.2 GB) at the
     same time (1.05 vs 1.04 ms), so the pair list stays the default."""
     if os.environ.get("ST_WGRAD_PATH", "pairs") != "window":
         return False
