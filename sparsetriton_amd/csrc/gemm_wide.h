@@ -92,7 +92,13 @@ __global__ __launch_bounds__(128 * TP) void gather_gemm_wide_kernel(const T* __r
   static_assert(D >= 2 && D <= 3, "ring depth 2..3");
   using GV = typename std::conditional<X3, v4f, F16>::type;  // one 16-byte global load
 
-  __shared__ __attribute__((aligned(16))) L16 bt_s[2][PLANES][BN * KD];
+  // B, double-buffered; before the main loop a submanifold source's prologue
+  // keeps its unit_rows lookup tables (8 brick words and bases per thread)
+  // here too, so the buffer is sized for both
+  constexpr int BT_BYTES = 2 * PLANES * BN * KD * (int)sizeof(L16);
+  constexpr int LK_BYTES = S::kTiled ? 0 : 8 * NT * (int)(sizeof(unsigned long long) + sizeof(int32_t));
+  __shared__ __attribute__((aligned(16))) unsigned char bt_raw[BT_BYTES > LK_BYTES ? BT_BYTES : LK_BYTES];
+  auto bt_s = reinterpret_cast<L16 (*)[PLANES][BN * KD]>(bt_raw);
   __shared__ int32_t src_s[TP][kWideMaxK][kGemmBM];  // per tile: sources by list position (tiled) or offset (fly)
   __shared__ int32_t drow_s[TP][kGemmBM];
   __shared__ int16_t klist_s[TP][kWideMaxK];  // per tile's offset list (tiled)
@@ -159,11 +165,16 @@ __global__ __launch_bounds__(128 * TP) void gather_gemm_wide_kernel(const T* __r
     if (live) {
       int64_t b, x, y, z;
       load_coord(src.coords, d, b, x, y, z);
-      subm_neighbours(src.ix, b, x, y, z, off_s, K, subm_unit_offsets(off_s, K), [&](int k, int32_t v) {
+      auto found = [&](int k, int32_t v) {
         v = (int64_t)v >= n_src ? -1 : v;
         src_s[ht][k][r] = v;
         m |= (v >= 0 ? 1u : 0u) << k;
-      });
+      };
+      if (unit_offsets(src.offsets, K))  // (uniform) the 3x3x3 kernel: 32-bit lookups, words in LDS
+        unit_rows<NT>(src.ix, b, x, y, z, src.offsets, K, reinterpret_cast<unsigned long long*>(bt_raw),
+                      reinterpret_cast<int32_t*>(bt_raw + 8 * NT * sizeof(unsigned long long)), found);
+      else
+        subm_neighbours(src.ix, b, x, y, z, off_s, K, found);
     } else {
       for (int k = 0; k < K; ++k) src_s[ht][k][r] = -1;
     }

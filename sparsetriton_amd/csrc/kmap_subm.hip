@@ -245,92 +245,6 @@ __global__ __launch_bounds__(kSubmThreads) void subm_rowmap_kernel(const CT* __r
   if (prev != 0x7FFFFFFF && status) atomicAdd(&status[ST_STATUS_DUPLICATE], 1);
 }
 
-// Whether every offset component lies in [-1, 1] (uniform scalar loads).
-__device__ __forceinline__ bool unit_offsets(const int32_t* __restrict__ offsets, int K) {
-  bool unit = true;
-  for (int t = 0; t < 3 * K; ++t) unit = unit && offsets[t] >= -1 && offsets[t] <= 1;
-  return unit;
-}
-
-// The rows of (b, x, y, z) - t_k for unit offsets, k = 0 .. K-1, passed to
-// emit(k, row) in ascending k (row -1: outside the box or absent) -- the
-// submanifold lookup in 32-bit arithmetic.  One word per axis holds, for
-// t = -1, 0, 1, the neighbour coordinate's in-box bit, which of the two bricks
-// the row's neighbours span on that axis it lies in, and its position in that
-// brick; the up to 8 bricks' level-2 words and bases sit in LDS (bits_s /
-// pre_s, 8 x 256 per workgroup, this thread's column only); offsets are
-// uniform scalar loads.  Per offset: three field extracts, an LDS read, a bit
-// test and a popcount.  subm_neighbours spends ~95 VALU instructions per
-// offset (64-bit coordinates, an 8-way select), which bounded the query.
-template <typename Emit>
-__device__ __forceinline__ void unit_rows(const SubmIndex& ix, int64_t b, int64_t x, int64_t y, int64_t z,
-                                          const int32_t* __restrict__ offsets, int K,
-                                          unsigned long long* __restrict__ bits_s, int32_t* __restrict__ pre_s,
-                                          Emit&& emit) {
-  const int tid = threadIdx.x;
-  // a row more than one voxel outside the box has no neighbour in it
-  const bool near = b >= 0 && b < ix.nb && x >= -1 && x <= ix.sx && y >= -1 && y <= ix.sy && z >= -1 && z <= ix.sz;
-  uint32_t A[3] = {0u, 0u, 0u};
-  int bb[3] = {0, 0, 0};
-  if (near) {
-    const int c3[3] = {(int)x, (int)y, (int)z};
-    const int S3[3] = {ix.sx, ix.sy, ix.sz};
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      bb[a] = (c3[a] - 1) >> 2;  // brick of the lowest neighbour coordinate
-#pragma unroll
-      for (int ti = 0; ti < 3; ++ti) {  // t = ti - 1, neighbour coordinate c - t
-        const int q = c3[a] - (ti - 1);
-        const uint32_t f = ((q >= 0 && q < S3[a]) ? 8u : 0u) | ((uint32_t)((q >> 2) - bb[a]) << 2) | (uint32_t)(q & 3);
-        A[a] |= f << (4 * ti);
-      }
-    }
-  }
-  {
-    int64_t brk[8];
-    bool in[8];
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {
-      const int cx = bb[0] + (s8 >> 2), cy = bb[1] + ((s8 >> 1) & 1), cz = bb[2] + (s8 & 1);
-      in[s8] = near && cx >= 0 && cx < ix.bx && cy >= 0 && cy < ix.by && cz >= 0 && cz < ix.bz;
-      brk[s8] = in[s8] ? ((b * ix.bx + cx) * ix.by + cy) * ix.bz + cz : 0;
-    }
-    SubmL1 e1[8];
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) e1[s8] = in[s8] ? ix.l1[brk[s8] >> 6] : SubmL1{0ull, 0, 0};
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {
-      const bool occ = in[s8] && ((e1[s8].bits >> (brk[s8] & 63)) & 1ull);
-      const int r = occ ? subm_brick_rank(e1[s8], brk[s8]) : 0;
-      bits_s[s8 * kSubmThreads + tid] = occ ? ix.l2bits[r] : 0ull;
-      pre_s[s8 * kSubmThreads + tid] = occ ? ix.l2pre[r] : 0;
-    }
-  }
-  for (int k0 = 0; k0 < K; k0 += kSubmGroup) {
-    int idx[kSubmGroup];
-    // branch-free, so a group's scalar and LDS loads issue together
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) {
-      const int k = k0 + j < K ? k0 + j : K - 1;
-      const uint32_t fx = (A[0] >> (4 * (offsets[3 * k] + 1))) & 15u;
-      const uint32_t fy = (A[1] >> (4 * (offsets[3 * k + 1] + 1))) & 15u;
-      const uint32_t fz = (A[2] >> (4 * (offsets[3 * k + 2] + 1))) & 15u;
-      const int s8 = (int)((fx & 4u) | ((fy & 4u) >> 1) | ((fz & 4u) >> 2));
-      const int vb = (int)(((fx & 3u) << 4) | ((fy & 3u) << 2) | (fz & 3u));
-      const unsigned long long w = bits_s[s8 * kSubmThreads + tid];
-      const int base = pre_s[s8 * kSubmThreads + tid];
-      const bool has = (fx & fy & fz & 8u) && ((w >> vb) & 1ull);
-      idx[j] = has ? base + (int)__popcll(w & below(vb)) : -1;
-    }
-    int32_t rr[kSubmGroup];
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j) rr[j] = idx[j] >= 0 ? ix.rowmap[idx[j]] : -1;
-#pragma unroll
-    for (int j = 0; j < kSubmGroup; ++j)
-      if (k0 + j < K) emit(k0 + j, rr[j]);
-  }
-}
-
 // LDS of a query workgroup: the unit path's brick words and bases, or the
 // general path's offsets (NONE: a kernel that uses neither).
 template <bool NONE = false>
@@ -371,7 +285,7 @@ __global__ __launch_bounds__(kSubmThreads) void subm_query_kernel(const CT* __re
   if (unit)
     unit_rows(ix, b, x, y, z, offsets, K, lds.bits, lds.pre, emit);
   else  // (small lookup groups: this path's registers set the kernel's occupancy)
-    subm_neighbours<3>(ix, b, x, y, z, off_s, K, false, emit);
+    subm_neighbours<3>(ix, b, x, y, z, off_s, K, emit);
 }
 
 // ------------------------------------- strided / transposed output coordinates
@@ -647,7 +561,7 @@ __global__ __launch_bounds__(256) void strided_query_kernel(const CT* __restrict
     if (unit)
       unit_rows(ix, b, x * g.s, y * g.s, z * g.s, offsets, K, lds.bits, lds.pre, emit);
     else
-      subm_neighbours<3>(ix, b, x * g.s, y * g.s, z * g.s, off_s, K, false, emit);
+      subm_neighbours<3>(ix, b, x * g.s, y * g.s, z * g.s, off_s, K, emit);
     return;
   }
   // (o - t_k) / s: s divides it when o and t_k agree mod s on every axis, and then it is

@@ -75,13 +75,6 @@ __device__ __forceinline__ int subm_brick_rank(const SubmL1& e, int64_t br) {
   return e.bpre + (int)__popcll(e.bits & below((int)(br & 63)));
 }
 
-// Whether every offset component (off_s: K x 3) lies in [-1, 1].
-__device__ __forceinline__ bool subm_unit_offsets(const int32_t* off_s, int K) {
-  bool unit = true;
-  for (int t = 0; t < 3 * K; ++t) unit = unit && off_s[t] >= -1 && off_s[t] <= 1;
-  return unit;
-}
-
 // The rows of the coordinates (b, q) that q_of(k, qx, qy, qz) yields (false:
 // none), passed to emit(k, row) in ascending k = 0 .. K-1 (row -1: no
 // coordinate, outside the box or absent).  kSubmGroup lookups are in flight at
@@ -131,70 +124,11 @@ __device__ __forceinline__ void subm_lookup(const SubmIndex& ix, int64_t b, int 
 }
 
 // The rows of (b, x, y, z) - off_s[k] for k = 0 .. K-1, passed to emit(k, row)
-// in ascending k (row -1: outside the box or absent).  kSubmGroup lookups are
-// in flight at a time, each three dependent loads (level-1 entry; level-2
-// bits and base; rowmap), all L2-resident.  With unit offsets (the 3x3x3
-// kernel) the neighbours lie in the at most 2 x 2 x 2 bricks around the row,
-// each looked up once.
+// in ascending k (row -1: outside the box or absent): subm_lookup over the
+// offsets (any size; unit offsets take unit_rows).
 template <int G = kSubmGroup, typename Emit>
 __device__ __forceinline__ void subm_neighbours(const SubmIndex& ix, int64_t b, int64_t x, int64_t y, int64_t z,
-                                                const int32_t* off_s, int K, bool unit, Emit&& emit) {
-  if (unit) {
-    // bricks [bx + lo, bx + hi] per axis, lo = -1 when the row sits on the brick's low face
-    const int64_t bx = x >> 2, by = y >> 2, bz = z >> 2;
-    const int lx = (x & 3) == 0 ? -1 : 0, ly = (y & 3) == 0 ? -1 : 0, lz = (z & 3) == 0 ? -1 : 0;
-    const int hx = (x & 3) == 3 ? 1 : 0, hy = (y & 3) == 3 ? 1 : 0, hz = (z & 3) == 3 ? 1 : 0;
-    int64_t brk[8];
-    bool in[8];
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {
-      const int dx = lx + (s8 >> 2), dy = ly + ((s8 >> 1) & 1), dz = lz + (s8 & 1);
-      const int64_t cx = bx + dx, cy = by + dy, cz = bz + dz;
-      in[s8] = dx <= hx && dy <= hy && dz <= hz && b >= 0 && b < ix.nb && cx >= 0 && cx < ix.bx && cy >= 0 &&
-               cy < ix.by && cz >= 0 && cz < ix.bz;
-      brk[s8] = in[s8] ? ((b * ix.bx + cx) * ix.by + cy) * ix.bz + cz : 0;
-    }
-    SubmL1 e1[8];
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) e1[s8] = in[s8] ? ix.l1[brk[s8] >> 6] : SubmL1{0ull, 0, 0};
-    unsigned long long bits[8];
-    int32_t pre[8];
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {
-      const bool occ = in[s8] && ((e1[s8].bits >> (brk[s8] & 63)) & 1ull);
-      const int r = occ ? subm_brick_rank(e1[s8], brk[s8]) : 0;
-      bits[s8] = occ ? ix.l2bits[r] : 0ull;
-      pre[s8] = occ ? ix.l2pre[r] : 0;
-    }
-    for (int k0 = 0; k0 < K; k0 += kSubmGroup) {
-      int32_t rr[kSubmGroup];
-#pragma unroll
-      for (int j = 0; j < kSubmGroup; ++j) {
-        const int k = k0 + j;
-        rr[j] = -1;
-        if (k < K) {
-          const int64_t qx = x - off_s[3 * k], qy = y - off_s[3 * k + 1], qz = z - off_s[3 * k + 2];
-          if (subm_in_box(ix, b, qx, qy, qz)) {
-            const int s8 = ((int)((qx >> 2) - bx - lx) << 2) | ((int)((qy >> 2) - by - ly) << 1) |
-                           (int)((qz >> 2) - bz - lz);
-            unsigned long long w = 0ull;
-            int p = 0;
-#pragma unroll
-            for (int t8 = 0; t8 < 8; ++t8) {
-              w = s8 == t8 ? bits[t8] : w;
-              p = s8 == t8 ? pre[t8] : p;
-            }
-            const int vb = subm_vbit(qx, qy, qz);
-            if ((w >> vb) & 1ull) rr[j] = ix.rowmap[p + (int)__popcll(w & below(vb))];
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kSubmGroup; ++j)
-        if (k0 + j < K) emit(k0 + j, rr[j]);
-    }
-    return;
-  }
+                                                const int32_t* off_s, int K, Emit&& emit) {
   subm_lookup<G>(ix, b, K,
               [&](int k, int64_t& qx, int64_t& qy, int64_t& qz) {
                 qx = x - off_s[3 * k];
@@ -203,6 +137,119 @@ __device__ __forceinline__ void subm_neighbours(const SubmIndex& ix, int64_t b, 
                 return true;
               },
               emit);
+}
+
+// Whether every offset component lies in [-1, 1] (uniform scalar loads).
+__device__ __forceinline__ bool unit_offsets(const int32_t* __restrict__ offsets, int K) {
+  bool unit = true;
+  for (int t = 0; t < 3 * K; ++t) unit = unit && offsets[t] >= -1 && offsets[t] <= 1;
+  return unit;
+}
+
+// The rows of (b, x, y, z) - t_k for unit offsets, k = 0 .. K-1, passed to
+// emit(k, row) in ascending k (row -1: outside the box or absent) -- the
+// submanifold lookup in 32-bit arithmetic.  One word per axis holds, for
+// t = -1, 0, 1, the neighbour coordinate's in-box bit, which of the two bricks
+// the row's neighbours span on that axis it lies in, and its position in that
+// brick; the up to 8 bricks' level-2 words and bases sit in LDS (bits_s /
+// pre_s, 8 x NT per workgroup of NT threads, this thread's column only); offsets are
+// uniform scalar loads.  Per offset: three field extracts, an LDS read, a bit
+// test and a popcount.  subm_neighbours spends ~95 VALU instructions per
+// offset (64-bit coordinates, an 8-way select), which bounded the query.
+template <int NT = kSubmThreads, typename Emit>
+__device__ __forceinline__ void unit_rows(const SubmIndex& ix, int64_t b, int64_t x, int64_t y, int64_t z,
+                                          const int32_t* __restrict__ offsets, int K,
+                                          unsigned long long* __restrict__ bits_s, int32_t* __restrict__ pre_s,
+                                          Emit&& emit) {
+  const int tid = threadIdx.x;
+  // a row more than one voxel outside the box has no neighbour in it
+  const bool near = b >= 0 && b < ix.nb && x >= -1 && x <= ix.sx && y >= -1 && y <= ix.sy && z >= -1 && z <= ix.sz;
+  uint32_t A[3] = {0u, 0u, 0u};
+  int bb[3] = {0, 0, 0};
+  if (near) {
+    const int c3[3] = {(int)x, (int)y, (int)z};
+    const int S3[3] = {ix.sx, ix.sy, ix.sz};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      bb[a] = (c3[a] - 1) >> 2;  // brick of the lowest neighbour coordinate
+#pragma unroll
+      for (int ti = 0; ti < 3; ++ti) {  // t = ti - 1, neighbour coordinate c - t
+        const int q = c3[a] - (ti - 1);
+        const uint32_t f = ((q >= 0 && q < S3[a]) ? 8u : 0u) | ((uint32_t)((q >> 2) - bb[a]) << 2) | (uint32_t)(q & 3);
+        A[a] |= f << (4 * ti);
+      }
+    }
+  }
+  {
+    int64_t brk[8];
+    bool in[8];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      const int cx = bb[0] + (s8 >> 2), cy = bb[1] + ((s8 >> 1) & 1), cz = bb[2] + (s8 & 1);
+      in[s8] = near && cx >= 0 && cx < ix.bx && cy >= 0 && cy < ix.by && cz >= 0 && cz < ix.bz;
+      brk[s8] = in[s8] ? ((b * ix.bx + cx) * ix.by + cy) * ix.bz + cz : 0;
+    }
+    // All 8 level-1 entries, then all 8 level-2 words and bases, in flight
+    // together: the loads are unconditional (index 0 for a brick outside the
+    // box or unoccupied, its value then dropped), and the table is stored only
+    // after the last of them -- a store right after each load waited for it,
+    // one round trip per brick.  An index without occupied bricks (cap2 = 0:
+    // no level-2 entry to read) leaves every word 0.
+    unsigned long long w2[8];
+    int32_t p2[8];
+    bool occ[8];
+    if (ix.cap2 > 0) {  // (uniform)
+      SubmL1 e1[8];
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) e1[s8] = ix.l1[in[s8] ? brk[s8] >> 6 : 0];
+      int r8[8];
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        occ[s8] = in[s8] && ((e1[s8].bits >> (brk[s8] & 63)) & 1ull);
+        r8[s8] = occ[s8] ? subm_brick_rank(e1[s8], brk[s8]) : 0;
+      }
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        w2[s8] = ix.l2bits[r8[s8]];
+        p2[s8] = ix.l2pre[r8[s8]];
+      }
+    } else {
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        occ[s8] = false;
+        w2[s8] = 0ull;
+        p2[s8] = 0;
+      }
+    }
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      bits_s[s8 * NT + tid] = occ[s8] ? w2[s8] : 0ull;
+      pre_s[s8 * NT + tid] = occ[s8] ? p2[s8] : 0;
+    }
+  }
+  for (int k0 = 0; k0 < K; k0 += kSubmGroup) {
+    int idx[kSubmGroup];
+    // branch-free, so a group's scalar and LDS loads issue together
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j) {
+      const int k = k0 + j < K ? k0 + j : K - 1;
+      const uint32_t fx = (A[0] >> (4 * (offsets[3 * k] + 1))) & 15u;
+      const uint32_t fy = (A[1] >> (4 * (offsets[3 * k + 1] + 1))) & 15u;
+      const uint32_t fz = (A[2] >> (4 * (offsets[3 * k + 2] + 1))) & 15u;
+      const int s8 = (int)((fx & 4u) | ((fy & 4u) >> 1) | ((fz & 4u) >> 2));
+      const int vb = (int)(((fx & 3u) << 4) | ((fy & 3u) << 2) | (fz & 3u));
+      const unsigned long long w = bits_s[s8 * NT + tid];
+      const int base = pre_s[s8 * NT + tid];
+      const bool has = (fx & fy & fz & 8u) && ((w >> vb) & 1ull);
+      idx[j] = has ? base + (int)__popcll(w & below(vb)) : -1;
+    }
+    int32_t rr[kSubmGroup];
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j) rr[j] = idx[j] >= 0 ? ix.rowmap[idx[j]] : -1;
+#pragma unroll
+    for (int j = 0; j < kSubmGroup; ++j)
+      if (k0 + j < K) emit(k0 + j, rr[j]);
+  }
 }
 
 // Geometry of the index of n rows over [0, batches) x [0, sx) x [0, sy) x [0, sz);
