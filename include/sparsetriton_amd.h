@@ -72,10 +72,12 @@ enum st_weight_mode {
 
 /* ------------------------------------------------------------- utilities */
 
-/* Library version string, e.g. "sparsetriton_amd 0.1 gfx950". */
+/* Library version string, e.g. "sparsetriton_amd 0.1 gfx950" (a utility of
+ * this library: no counterpart in the reference). */
 const char* st_version(void);
 
-/* Fill n 32-bit / 64-bit words with `value` (table clears, -1 map fills). */
+/* Fill n 32-bit / 64-bit words with `value` (table clears, -1 map fills; the
+ * reference's torch.full calls around its kernels, utils/hash.py:428-429, 568). */
 int st_fill_u32(uint32_t* dst, int64_t n, uint32_t value, st_stream_t stream);
 int st_fill_u64(uint64_t* dst, int64_t n, uint64_t value, st_stream_t stream);
 
@@ -407,7 +409,9 @@ int st_kmap_pairs(const int32_t* map, int64_t map_k_stride, int64_t map_r_stride
  * c >= the chunk count.  Stably sorting chunk ids by these keys
  * (st_kmap_sort_rows with K = 9, one key word per row: one radix pass) gives
  * the chunk order st_wgrad_pairs walks: chunks of every offset that touch the
- * same output rows -- and hence nearby input rows -- run together.
+ * same output rows -- and hence nearby input rows -- run together.  No
+ * counterpart in the reference, whose weight-gradient grid walks
+ * (N_out / BN, K, channel tiles) directly (implicit_precomputed_gemm.py:180-230).
  */
 int st_kmap_pairs_chunk_keys(const int32_t* pairs, const int32_t* kstart, const int32_t* cstart, int K, int chunk,
                              int64_t max_chunks, int64_t n_out, uint32_t* keys, st_stream_t stream);
@@ -535,7 +539,8 @@ int st_gather_gemm(const void* A, int64_t n_src, const int32_t* map, int64_t map
                    void* out, int64_t n_dst, int K, int Kd, int Nd, int dtype, st_stream_t stream);
 
 /*
- * st_gather_gemm over a tile plan (st_tile_plan built with the same perm):
+ * st_gather_gemm over a tile plan (st_tile_plan built with the same perm) --
+ * the same reference kernels (implicit_precomputed_gemm.py:64-177) --:
  * the workgroup reads its tile's offsets and source rows contiguously
  * instead of gathering map entries and masks row by row.  Same result as
  * st_gather_gemm with that map.  Reductions wider than 128 (16-bit and
@@ -592,7 +597,8 @@ int st_wgrad(const void* X, int64_t n_in, const void* dY, const int32_t* map, in
              float* partials, int64_t splits, void* dW, int dw_dtype, st_stream_t stream);
 
 /*
- * Weight gradient over a pair list from st_kmap_pairs: every chunk of
+ * Weight gradient (precomputed_bwd_weight_kernel,
+ * implicit_precomputed_gemm.py:180-230) over a pair list from st_kmap_pairs: every chunk of
  * `chunk` pairs is one equal-sized task (the centre offset of a submanifold
  * map has N pairs, the others far fewer), its C_in x C_out partial goes to
  * partials[chunk] (max_chunks * C_in * C_out fp32; max_chunks >= P / chunk + K,
