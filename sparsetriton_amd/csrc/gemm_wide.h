@@ -248,11 +248,7 @@ __global__ __launch_bounds__(128 * TP) void gather_gemm_wide_kernel(const T* __r
       const int nr = idx / GCH, cv = idx - nr * GCH;
       if constexpr (X3) {
         v4bf hi, lo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          hi[e] = (__bf16)b_reg[jb][e];
-          lo[e] = (__bf16)(b_reg[jb][e] - (float)hi[e]);
-        }
+        split4(b_reg[jb], hi, lo);
         const int o = bpos(nr, cv >> 1) + (cv & 1) * 4;
         *reinterpret_cast<v4bf*>(&bt_s[buf][0][o]) = hi;
         *reinterpret_cast<v4bf*>(&bt_s[buf][1][o]) = lo;

@@ -137,11 +137,7 @@ __global__ __launch_bounds__(256) void gather_gemm_x3_kernel(
       const int nr = idx / CV, cv = idx - nr * CV;
       if (idx < BN * CV) {
         v4bf hi, lo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          hi[e] = (__bf16)b[j][e];
-          lo[e] = (__bf16)(b[j][e] - (float)hi[e]);
-        }
+        split4(b[j], hi, lo);
         *reinterpret_cast<v4bf*>(&bt_s[buf][0][nr * PITCH + cv * 4]) = hi;
         *reinterpret_cast<v4bf*>(&bt_s[buf][1][nr * PITCH + cv * 4]) = lo;
       }
@@ -429,11 +425,7 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
       const int nr = idx / CV, cv = idx - nr * CV;
       if (idx < BN * CV) {
         v4bf hi, lo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          hi[e] = (__bf16)b_ring[SL][jb][e];
-          lo[e] = (__bf16)(b_ring[SL][jb][e] - (float)hi[e]);
-        }
+        split4_each(b_ring[SL][jb], hi, lo);
         const int o = bpos(nr, cv >> 1) + (cv & 1) * 4;
         *reinterpret_cast<v4bf*>(&bt_s[buf][0][o]) = hi;
         *reinterpret_cast<v4bf*>(&bt_s[buf][1][o]) = lo;
@@ -456,6 +448,15 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
       }
 #pragma unroll
       for (int jj = 0; jj < KS; ++jj) {
+        // B fragments first: their LDS reads are then in flight while A is split
+        v8bf bh[NBLK], bl[NBLK];
+#pragma unroll
+        for (int nb = 0; nb < NBLK; ++nb) {
+          const int off = bpos(nb * 16 + c, jj * 4 + g);
+          bh[nb] = *reinterpret_cast<const v8bf*>(&bt_s[buf][0][off]);
+          bl[nb] = *reinterpret_cast<const v8bf*>(&bt_s[buf][1][off]);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from sinking them to the MFMAs
         v8bf ah[2], al[2];
         if constexpr (LINES) {
           const int q = jj * 8 + g * 2;
@@ -473,13 +474,6 @@ __global__ __launch_bounds__(256) void gather_gemm_ring_x3_kernel(
         // the three products in three rounds over all 2 * NBLK accumulators, so that
         // consecutive MFMAs never feed each other (one round per product keeps
         // 2 * NBLK independent accumulations between dependent ones)
-        v8bf bh[NBLK], bl[NBLK];
-#pragma unroll
-        for (int nb = 0; nb < NBLK; ++nb) {
-          const int off = bpos(nb * 16 + c, jj * 4 + g);
-          bh[nb] = *reinterpret_cast<const v8bf*>(&bt_s[buf][0][off]);
-          bl[nb] = *reinterpret_cast<const v8bf*>(&bt_s[buf][1][off]);
-        }
 #pragma unroll
         for (int nb = 0; nb < NBLK; ++nb) {
           acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[0], bh[nb], acc[0][nb], 0, 0, 0);
@@ -687,18 +681,10 @@ __global__ __launch_bounds__(256, 2) void wgrad_pairs_x3_kernel(const float* __r
         // split once per element as it is staged: hi = bf16(x), lo = bf16(x - hi)
         v4bf h, l;
         const int at = pl_at(v * 4 + lr, lc * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          h[e] = (__bf16)xr[v][e];
-          l[e] = (__bf16)(xr[v][e] - (float)h[e]);
-        }
+        split4(xr[v], h, l);
         *reinterpret_cast<v4bf*>(&xh[at]) = h;
         *reinterpret_cast<v4bf*>(&xl[at]) = l;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          h[e] = (__bf16)yr[v][e];
-          l[e] = (__bf16)(yr[v][e] - (float)h[e]);
-        }
+        split4(yr[v], h, l);
         *reinterpret_cast<v4bf*>(&yh[at]) = h;
         *reinterpret_cast<v4bf*>(&yl[at]) = l;
       }

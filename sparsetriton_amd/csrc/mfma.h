@@ -58,20 +58,52 @@ __device__ __forceinline__ v4f mfma(const v8bf& a, const v8bf& b, v4f acc) {
 
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
-// hi/lo bf16 split of 8 consecutive fp32 values (the split-operand fp32
-// products: x = hi + lo + d, |d| <= 2^-18 |x|).
+// hi/lo bf16 split of fp32 values (the split-operand fp32 products:
+// x = hi + lo + d, |d| <= 2^-18 |x|), hi = bf16(x) and lo = bf16(x - hi),
+// both rounded to nearest even.  A pair is converted by one packed
+// conversion; each hi comes back to fp32 exactly as a shift (low half) or a
+// mask (high half) of the packed word, so a value costs three VALU operations
+// (half a conversion, the shift or mask, the subtraction, half a conversion)
+// instead of four with a second conversion of each hi.
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){a, b}, v2bf));
+}
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16(a, b);
+  lo = pack_bf16(a - __builtin_bit_cast(float, hi << 16), b - __builtin_bit_cast(float, hi & 0xFFFF0000u));
+}
+__device__ __forceinline__ void split4(const v4f& x, v4bf& hi, v4bf& lo) {
+  uint32_t h[2], l[2];
+  split_pair(x[0], x[1], h[0], l[0]);
+  split_pair(x[2], x[3], h[1], l[1]);
+  hi = __builtin_bit_cast(v4bf, h);
+  lo = __builtin_bit_cast(v4bf, l);
+}
+// 8 consecutive values: x0 gives elements 0..3, x1 elements 4..7
 __device__ __forceinline__ void split8(const v4f& x0, const v4f& x1, v8bf& hi, v8bf& lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const __bf16 h0 = (__bf16)x0[e];
-    const __bf16 h1 = (__bf16)x1[e];
-    hi[e] = h0;
-    hi[e + 4] = h1;
-    lo[e] = (__bf16)(x0[e] - (float)h0);
-    lo[e + 4] = (__bf16)(x1[e] - (float)h1);
-  }
+  uint32_t h[4], l[4];
+  split_pair(x0[0], x0[1], h[0], l[0]);
+  split_pair(x0[2], x0[3], h[1], l[1]);
+  split_pair(x1[0], x1[1], h[2], l[2]);
+  split_pair(x1[2], x1[3], h[3], l[3]);
+  hi = __builtin_bit_cast(v8bf, h);
+  lo = __builtin_bit_cast(v8bf, l);
 }
 
+// The same split of 4 values with a conversion per element (four operations
+// a value).  It measured faster than split4 in the fp32 ring gather's B stage
+// (config 2 forward 140 -> 123 us), where the stage overlaps the previous
+// offset's MFMAs.
+__device__ __forceinline__ void split4_each(const v4f& x, v4bf& hi, v4bf& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (__bf16)x[e];
+    lo[e] = (__bf16)(x[e] - (float)hi[e]);
+  }
+}
 // a*b ~= al*bh + ah*bl + ah*bh, in that order (every kernel that must agree
 // bitwise with another adds the three products in this order)
 __device__ __forceinline__ v4f mfma_x3(const v8bf& ah, const v8bf& al, const v8bf& bh, const v8bf& bl, v4f acc) {
