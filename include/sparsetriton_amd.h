@@ -116,7 +116,7 @@ int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale
  * 516-544), partitioned: the same insert as st_hash_insert (same keys, values,
  * lowest row of a repeated coordinate, status counts) built segment by
  * segment in LDS.  Rows are grouped by the segment of their home slot (per
- * workgroup of 8192 rows, in LDS), then one workgroup per segment of 2048
+ * workgroup of 4096 rows, in LDS), then one workgroup per segment of 2048
  * slots gathers its rows, inserts them by LDS CAS and stores the segment
  * with coalesced writes; rows whose probe runs past their segment are
  * inserted by global CAS, from the next segment on, after every segment is
@@ -126,7 +126,7 @@ int st_hash_insert(const void* coords, int coord_dtype, int64_t n, int64_t scale
  * inserts into the table's current contents, as st_hash_insert does.
  * workspace (st_hash_build_workspace bytes) must be zeroed before its first
  * use; every call leaves it reusable as is.  Calls that share a workspace
- * must not overlap.  ST_ERR_UNSUPPORTED above 16.7M slots or 16.7M rows and
+ * must not overlap.  ST_ERR_UNSUPPORTED above 16.7M slots or 8.4M rows and
  * while the 16-lane probe mode is on (st_hash_probe_mode): use
  * st_hash_insert there.
  */

@@ -396,7 +396,7 @@ static unsigned group_blocks(int64_t rows) { return (unsigned)((rows * kGroup + 
 // end, spills, and the global probe finds the key.  The table's key -> row
 // mapping is the CAS build's; slot positions may differ (they depend on the
 // insertion order in either build).
-constexpr int kBuildRows = 8192;      // rows per bucketing workgroup (32 per thread)
+constexpr int kBuildRows = 4096;      // rows per bucketing workgroup (4 per thread)
 constexpr int kBuildMaxSegs = 8192;   // the bucketing pass's LDS count table
 constexpr int kBuildSlots = 2048;     // slots per segment (24 KB of LDS)
 constexpr int kBuildMaxWgs = 2048;    // bucketing workgroups a segment gathers from
